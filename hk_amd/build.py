@@ -1,0 +1,70 @@
+"""Builds the HIP engine library hk_amd/libhkhip.so for gfx950 (hipcc, in-tree).
+
+Every translation unit is compiled with hipcc and linked into one shared library exporting the
+C ABI of include/hkhip.h. Flags that matter for the arithmetic:
+  -ffp-contract=off   no implicit FMA contraction: the dequantizer is bit-exact with hk's
+                      decoders and every fused multiply-add in the kernels is written as fmaf
+  -Xclang -target-feature -Xclang -packed-fp32-ops
+                      no packed-FP32 instructions
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+OUT = os.path.join(HERE, "libhkhip.so")
+BUILD_DIR = os.path.join(HERE, "_build")
+SOURCES = ["engine.hip", "weights.hip", "qact.hip", "mmvq.hip", "mm.hip"]
+ARCH = "gfx950"
+
+
+def hipcc() -> str:
+    for c in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if c and os.path.exists(c):
+            return c
+    raise RuntimeError("hipcc not found: the HIP engine cannot be built")
+
+
+def cflags() -> list[str]:
+    return [
+        "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-ffp-contract=off",
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-Wall", "-Wno-unused-result", "-Wno-unused-command-line-argument",
+    ]
+
+
+def _compile(src: str) -> str:
+    obj = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + ".o")
+    cmd = [hipcc(), *cflags(), "-c", os.path.join(CSRC, src), "-o", obj]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {src}:\n{r.stderr}")
+    noise = "warning: unknown target feature" if "packed-fp32-ops" in r.stderr else None
+    for line in r.stderr.splitlines():
+        if "error" in line or ("warning" in line and not (noise and noise in line)):
+            print(line, file=sys.stderr)
+    return obj
+
+
+def build(jobs: int | None = None) -> str:
+    """Compile every source and link libhkhip.so. Always rebuilds."""
+    os.makedirs(BUILD_DIR, exist_ok=True)
+    jobs = jobs or min(len(SOURCES), os.cpu_count() or 4)
+    with cf.ThreadPoolExecutor(jobs) as ex:
+        objs = list(ex.map(_compile, SOURCES))
+    tmp = OUT + ".tmp"
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed:\n{r.stderr}")
+    os.replace(tmp, OUT)
+    return OUT
+
+
+if __name__ == "__main__":
+    print(build())

@@ -1,0 +1,143 @@
+// Shared definitions of the HIP engine: device layouts of weights and activations, small
+// device helpers, and the launchers each kernel file provides to engine.cpp.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/hkhip.h"
+
+namespace hkhip {
+
+constexpr uint32_t QK_K = 256;
+
+inline uint64_t align256(uint64_t x) { return (x + 255) & ~uint64_t(255); }
+
+// Block geometry in hk's file layout (src/quant/blocks.zig:17-34).
+inline int block_elems(int t) {
+    switch (t) {
+    case HKHIP_Q8_0: case HKHIP_IQ4_NL: return 32;
+    case HKHIP_Q4_K: case HKHIP_Q6_K: return 256;
+    default: return 0;
+    }
+}
+inline int block_bytes(int t) {
+    switch (t) {
+    case HKHIP_Q8_0: return 34;
+    case HKHIP_IQ4_NL: return 18;
+    case HKHIP_Q4_K: return 144;
+    case HKHIP_Q6_K: return 210;
+    default: return 0;
+    }
+}
+// vecdot.zig:185-191
+inline int act_kind(int t) { return (t == HKHIP_Q8_0 || t == HKHIP_IQ4_NL) ? HKHIP_ACT_A8 : HKHIP_ACT_Q8K; }
+
+// Device layout of a weight matrix. Q4_K keeps the 144-byte file blocks (already 16-byte
+// aligned). The 2-byte-aligned formats are split at upload into a quant plane whose blocks
+// are 16-byte aligned and a plane of f16 scales, one per block, in block order:
+//   Q8_0   quant plane: 32 B per block (qs)        scale plane: d
+//   IQ4_NL quant plane: 16 B per block (qs)        scale plane: d
+//   Q6_K   quant plane: 208 B per block (ql qh sc) scale plane: d
+struct WLayout {
+    uint64_t quant_bytes;  // bytes of the quant plane (or of the whole Q4_K matrix)
+    uint64_t scale_off;    // offset of the scale plane
+    uint64_t total;
+    uint32_t qblock;       // bytes per block in the quant plane
+};
+
+inline WLayout weight_layout(int t, uint32_t rows, uint32_t cols) {
+    WLayout L{};
+    uint64_t nb = uint64_t(rows) * (cols / block_elems(t));
+    switch (t) {
+    case HKHIP_Q4_K: L.qblock = 144; break;
+    case HKHIP_Q8_0: L.qblock = 32; break;
+    case HKHIP_IQ4_NL: L.qblock = 16; break;
+    case HKHIP_Q6_K: L.qblock = 208; break;
+    }
+    L.quant_bytes = nb * L.qblock;
+    if (t == HKHIP_Q4_K) {
+        L.scale_off = L.quant_bytes;
+        L.total = L.quant_bytes;
+    } else {
+        L.scale_off = align256(L.quant_bytes);
+        L.total = L.scale_off + nb * 2;
+    }
+    return L;
+}
+
+// Activation-quant buffer for n tokens of k values. Both kinds live side by side so one
+// input serves Q8_0 / IQ4_NL (A8) and Q4_K / Q6_K (Q8K) products alike:
+//   a8_qs [n][k] i8, a8_d [n][k/32] f32, a8_s [n][k/32] i32,
+//   k_qs  [n][k] i8, k_d  [n][k/256] f32, k_bs [n][k/16] i16
+struct ActLayout {
+    uint64_t a8_qs, a8_d, a8_s, k_qs, k_d, k_bs, total;
+};
+
+inline ActLayout act_layout(uint32_t n, uint32_t k) {
+    ActLayout L{};
+    uint64_t nk = uint64_t(n) * k;
+    uint64_t o = 0;
+    L.a8_qs = o; o = align256(o + nk);
+    L.a8_d = o;  o = align256(o + nk / 32 * 4);
+    L.a8_s = o;  o = align256(o + nk / 32 * 4);
+    L.k_qs = o;  o = align256(o + (k % QK_K == 0 ? nk : 0));
+    L.k_d = o;   o = align256(o + (k % QK_K == 0 ? nk / QK_K * 4 : 0));
+    L.k_bs = o;  o = align256(o + (k % QK_K == 0 ? nk / 16 * 2 : 0));
+    L.total = o;
+    return L;
+}
+
+struct ActA8 {
+    const int8_t *qs;
+    const float *d;
+};
+struct ActQ8K {
+    const int8_t *qs;
+    const float *d;
+    const int16_t *bs;
+};
+
+// ---- device helpers ----
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t bits) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
+}
+
+// hk's IQ4_NL codebook (src/quant/tables.zig:13), packed four entries per word, entry 0 in
+// the lowest byte, for byte-permute lookups.
+constexpr int8_t kvalues_iq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+constexpr uint32_t iq4nl_word(int w) {
+    return uint32_t(uint8_t(kvalues_iq4nl[4 * w])) | (uint32_t(uint8_t(kvalues_iq4nl[4 * w + 1])) << 8) |
+           (uint32_t(uint8_t(kvalues_iq4nl[4 * w + 2])) << 16) | (uint32_t(uint8_t(kvalues_iq4nl[4 * w + 3])) << 24);
+}
+constexpr uint32_t IQ4NL_T0 = iq4nl_word(0), IQ4NL_T1 = iq4nl_word(1), IQ4NL_T2 = iq4nl_word(2),
+                   IQ4NL_T3 = iq4nl_word(3);
+static_assert(IQ4NL_T0 == 0xBFAD9881u && IQ4NL_T3 == 0x71594535u, "codebook packing");
+
+// Four 4-bit indices (one per byte, each < 16) to four signed codebook bytes.
+__device__ __forceinline__ uint32_t iq4nl_lookup4(uint32_t idx) {
+    uint32_t sel = idx & 0x07070707u;
+    uint32_t lo = __builtin_amdgcn_perm(IQ4NL_T1, IQ4NL_T0, sel);
+    uint32_t hi = __builtin_amdgcn_perm(IQ4NL_T3, IQ4NL_T2, sel);
+    uint32_t m = ((idx >> 3) & 0x01010101u) * 0xFFu; // 0xFF in bytes whose index is >= 8
+    return (hi & m) | (lo & ~m);
+}
+
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// ---- launchers (defined in the kernel files) ----
+
+hipError_t launch_repack(int t, const uint8_t *src, uint8_t *dst, uint32_t rows, uint32_t cols, hipStream_t s);
+hipError_t launch_dequant(int t, const uint8_t *w, uint32_t rows, uint32_t cols, uint32_t row0, uint32_t nrows,
+                          float *out, hipStream_t s);
+hipError_t launch_qact(const float *x, uint32_t n, uint32_t k, int kind, uint8_t *xq, hipStream_t s);
+hipError_t launch_act_pack(const uint8_t *xq, uint32_t n, uint32_t k, int kind, uint8_t *out, hipStream_t s);
+hipError_t launch_mmvq(int t, const uint8_t *w, uint32_t rows, uint32_t cols, const uint8_t *xq, uint32_t n,
+                       float *y, const float *bias, int mode, hipStream_t s);
+hipError_t launch_mm(int t, const uint8_t *w, uint32_t rows, uint32_t cols, const uint8_t *xq, uint32_t n,
+                     float *y, const float *bias, int mode, hipStream_t s);
+
+} // namespace hkhip

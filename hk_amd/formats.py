@@ -1,0 +1,54 @@
+"""hk's block formats on the quantized-linear path: StorageType codes and block geometry.
+
+Codes are hk's StorageType bytes (reference src/format.zig:26-84); geometry is
+src/quant/blocks.zig:17-34 and the size table `info` / `byteSize` (blocks.zig:84-127).
+"""
+from __future__ import annotations
+
+Q8_0 = 0x16
+Q4_K = 0x42
+Q6_K = 0x44
+IQ4_NL = 0x55
+
+NAMES = {Q8_0: "q8_0", Q4_K: "q4_k", Q6_K: "q6_k", IQ4_NL: "iq4_nl"}
+BY_NAME = {v: k for k, v in NAMES.items()}
+
+# weights per block, bytes per block (blocks.zig:49-72 size asserts)
+INFO = {Q8_0: (32, 34), IQ4_NL: (32, 18), Q4_K: (256, 144), Q6_K: (256, 210)}
+
+# Activation kind each format is dotted against (vecdot.zig:185-191).
+ACT_A8, ACT_Q8K = 0, 1
+ACT_KIND = {Q8_0: ACT_A8, IQ4_NL: ACT_A8, Q4_K: ACT_Q8K, Q6_K: ACT_Q8K}
+
+# Bits per weight in the file layout (the numerator of the bandwidth roofline).
+BPW = {t: 8.0 * b / e for t, (e, b) in INFO.items()}
+
+# hk's IQ4_NL codebook (src/quant/tables.zig:13).
+KVALUES_IQ4NL = (-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113)
+
+
+class UnsupportedType(ValueError):
+    pass
+
+
+class NotBlockAligned(ValueError):
+    pass
+
+
+def byte_size(t: int, n_elems: int) -> int:
+    """Exact bytes of n_elems weights of type t; refuses partial blocks (blocks.zig:123-127)."""
+    if t not in INFO:
+        raise UnsupportedType(f"storage type 0x{t:02x} is not on the HIP path")
+    elems, nbytes = INFO[t]
+    if n_elems % elems:
+        raise NotBlockAligned(f"{n_elems} weights is not a whole number of {elems}-weight blocks")
+    return n_elems // elems * nbytes
+
+
+def matrix_bytes(t: int, rows: int, cols: int) -> int:
+    """Bytes of a rows x cols matrix (abi_ops.zig:56-62)."""
+    if t not in INFO:
+        raise UnsupportedType(f"storage type 0x{t:02x} is not on the HIP path")
+    if cols % INFO[t][0]:
+        raise NotBlockAligned(f"cols {cols} is not a whole number of blocks")
+    return rows * byte_size(t, cols)

@@ -1,0 +1,84 @@
+"""Synthetic weights and activations of the shapes the benchmarks and tests use.
+
+Blocks are random but valid: quant bytes are uniform; scale fields are finite f16 drawn as
+SURVEY-style |N(0, 0.02)| magnitudes (per format below); activations are N(0, 1) f32, with an
+optional fraction of outliers at +-20. The same generator runs on NumPy (host, tests and the
+CPU baseline) or torch (device, for multi-GB benchmark matrices).
+
+  Q8_0   qs uniform in [-127, 127];           d = |N(0,0.02)| / 127 * 4
+  Q4_K   qs and the 12 scale bytes uniform;   d = dmin = |N(0,0.02)| / 63
+  Q6_K   ql / qh uniform, scales in [-32,31]; d = |N(0,0.02)| / 127
+  IQ4_NL indices uniform;                     d = |N(0,0.02)|
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from . import formats
+
+SEED_BASE = 20261201
+
+
+def seed_for(config: int, tensor: int) -> int:
+    """seed = 20261201 + config * 1000 + tensor index."""
+    return SEED_BASE + config * 1000 + tensor
+
+
+def _f16_scales_np(rng, nb: int, div: float) -> np.ndarray:
+    return (np.abs(rng.normal(0.0, 0.02, nb)) / div).astype(np.float16)
+
+
+def weights_np(t: int, rows: int, cols: int, seed: int) -> np.ndarray:
+    """Random valid blocks in hk's file layout, as a [rows, row_bytes] uint8 array."""
+    elems, bb = formats.INFO[t]
+    nb = rows * (cols // elems)
+    rng = np.random.default_rng(seed)
+    raw = rng.integers(0, 256, size=(nb, bb), dtype=np.uint8)
+    if t == formats.Q8_0:
+        raw[:, 2:34] = rng.integers(-127, 128, size=(nb, 32)).astype(np.int8).view(np.uint8)
+        raw[:, 0:2] = _f16_scales_np(rng, nb, 127.0 / 4.0).view(np.uint8).reshape(nb, 2)
+    elif t == formats.Q4_K:
+        raw[:, 0:2] = _f16_scales_np(rng, nb, 63.0).view(np.uint8).reshape(nb, 2)
+        raw[:, 2:4] = _f16_scales_np(rng, nb, 63.0).view(np.uint8).reshape(nb, 2)
+    elif t == formats.Q6_K:
+        raw[:, 192:208] = rng.integers(-32, 32, size=(nb, 16)).astype(np.int8).view(np.uint8)
+        raw[:, 208:210] = _f16_scales_np(rng, nb, 127.0).view(np.uint8).reshape(nb, 2)
+    elif t == formats.IQ4_NL:
+        raw[:, 0:2] = _f16_scales_np(rng, nb, 1.0).view(np.uint8).reshape(nb, 2)
+    return raw.reshape(rows, -1)
+
+
+def activations_np(n: int, k: int, seed: int, outliers: float = 0.0) -> np.ndarray:
+    rng = np.random.default_rng(seed)
+    x = rng.normal(0.0, 1.0, size=(n, k)).astype(np.float32)
+    if outliers > 0:
+        mask = rng.random((n, k)) < outliers
+        x[mask] = np.where(rng.random(int(mask.sum())) < 0.5, -20.0, 20.0).astype(np.float32)
+    return x
+
+
+def weights_torch(t: int, rows: int, cols: int, seed: int, device="cuda"):
+    """Same distribution as weights_np, generated on the device (for multi-GB matrices)."""
+    import torch
+
+    elems, bb = formats.INFO[t]
+    nb = rows * (cols // elems)
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    raw = torch.randint(0, 256, (nb, bb), dtype=torch.uint8, device=device, generator=g)
+
+    def scales(div):
+        return (torch.randn(nb, device=device, generator=g) * 0.02).abs().div_(div).half().view(torch.uint8).view(nb, 2)
+
+    if t == formats.Q8_0:
+        raw[:, 2:34] = torch.randint(-127, 128, (nb, 32), device=device, generator=g).to(torch.int8).view(torch.uint8)
+        raw[:, 0:2] = scales(127.0 / 4.0)
+    elif t == formats.Q4_K:
+        raw[:, 0:2] = scales(63.0)
+        raw[:, 2:4] = scales(63.0)
+    elif t == formats.Q6_K:
+        raw[:, 192:208] = torch.randint(-32, 32, (nb, 16), device=device, generator=g).to(torch.int8).view(torch.uint8)
+        raw[:, 208:210] = scales(127.0)
+    elif t == formats.IQ4_NL:
+        raw[:, 0:2] = scales(1.0)
+    return raw.view(rows, -1)

@@ -1,0 +1,144 @@
+/* hkhip.h — C ABI of the MI355X (gfx950) quantized-linear engine for hk.
+ *
+ * This is the drop-in boundary a HIP backend of hk binds: hk's Zig host side would
+ * @cImport this header the way src/cuda.zig loads libcuda, and a `hip` arm is added to
+ * backend.Device (reference src/backend/backend.zig:27,128-209). Every entry point takes
+ * plain pointers, sizes and hk's own StorageType byte codes (src/format.zig:26-84).
+ *
+ * Shapes follow hk's engine: W is `rows` x `cols` (M x K) in one of the block formats,
+ * activations x are token major [n][K] f32, outputs y are token major [n][M] f32
+ * (src/engine/matmul.zig:5, src/kernels_impl.zig:27).
+ *
+ * Error convention: entry points return 0 on success or a negative HKHIP_E_* code and
+ * set a thread-local message readable with hkhip_last_error(). The codes mirror the CUDA
+ * engine's error set (src/cuda/engine.zig:31-40). The host-pointer products
+ * (hkhip_gemv_*, hkhip_gemm_host) additionally fill y with NaN on failure, as hk's C ABI
+ * does (src/c_api.zig:16-18).
+ *
+ * Threading: one engine = one device + one stream. Calls on one engine are serialised by
+ * the caller (hk's Model does this); every entry point makes the engine's device current,
+ * so an engine may be used from a thread other than the one that created it.
+ */
+#ifndef HKHIP_H
+#define HKHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* hk StorageType codes handled by the HIP kernels (src/format.zig:52,75,84). */
+#define HKHIP_Q8_0 0x16
+#define HKHIP_Q4_K 0x42
+#define HKHIP_Q6_K 0x44
+#define HKHIP_IQ4_NL 0x55
+
+/* Activation kinds (src/quant/vecdot.zig:183-191 ActKind). */
+#define HKHIP_ACT_A8 0  /* per 32: d = amax/127, round half away, s = sum q */
+#define HKHIP_ACT_Q8K 1 /* per 256: signed-max scale, clamp 127, 16 bsums   */
+
+/* Output modes of the products. */
+#define HKHIP_STORE 0      /* y  = W x + bias */
+#define HKHIP_ACCUMULATE 1 /* y += W x + bias (residual add fused into the product) */
+
+/* Error codes (src/cuda/engine.zig:31-40). */
+#define HKHIP_OK 0
+#define HKHIP_E_UNSUPPORTED_TYPE -1
+#define HKHIP_E_UNSUPPORTED_SHAPE -2
+#define HKHIP_E_OUT_OF_DEVICE_MEMORY -3
+#define HKHIP_E_DEVICE_FAILED -4
+#define HKHIP_E_BAD_ARGUMENT -5
+#define HKHIP_E_NO_DEVICE -6
+
+typedef struct hkhip_engine hkhip_engine;
+
+/* A weight matrix resident on the device. The device layout is private to the engine
+ * (Q4_K is kept in file layout; Q8_0, Q6_K and IQ4_NL are split into an aligned quant plane
+ * and a scale plane); `file_bytes` is the size of the same matrix in hk's file layout.
+ * Mirrors DevMat{mem, t, rows, cols} (src/cuda/engine.zig:111-116). */
+typedef struct hkhip_mat {
+    void *mem;
+    uint64_t file_bytes;
+    uint64_t dev_bytes;
+    uint32_t rows;
+    uint32_t cols;
+    uint8_t t;
+    uint8_t owned;
+    uint8_t pad[6];
+} hkhip_mat;
+
+/* ---- engine lifetime (probeCuda / Engine.init / deinit: src/backend/backend.zig:92-126) ---- */
+int hkhip_device_count(void);
+int hkhip_init(int device, hkhip_engine **out);
+void hkhip_destroy(hkhip_engine *eng);
+/* Runs the engine's work on `stream` (a hipStream_t) instead of its own stream; NULL restores it. */
+int hkhip_set_stream(hkhip_engine *eng, void *stream);
+void *hkhip_stream(hkhip_engine *eng);
+int hkhip_sync(hkhip_engine *eng);
+const char *hkhip_last_error(void);
+const char *hkhip_device_name(hkhip_engine *eng);
+
+/* ---- capability and sizing (src/cuda/engine.zig:106-108 supports, abi_ops.zig:56-62) ---- */
+int hkhip_supports(uint8_t t);
+/* Bytes of rows x cols weights of type t in hk's file layout, or a negative error. */
+int64_t hkhip_matrix_bytes(uint8_t t, uint32_t rows, uint32_t cols);
+/* Bytes of the activation-quant buffer for n tokens of k values (both kinds). */
+uint64_t hkhip_act_bytes(uint32_t n, uint32_t k);
+
+/* ---- device memory (the thin shim over hipMalloc / hipMemcpyAsync, src/cuda.zig) ---- */
+int hkhip_alloc(hkhip_engine *eng, uint64_t bytes, void **out);
+void hkhip_dev_free(hkhip_engine *eng, void *p);
+int hkhip_copy_h2d(hkhip_engine *eng, void *dst, const void *src, uint64_t bytes);
+int hkhip_copy_d2h(hkhip_engine *eng, void *dst, const void *src, uint64_t bytes);
+
+/* ---- weights (Engine.upload, src/cuda/engine.zig:493-506) ----
+ * Copies `bytes` of hk-file-layout weights from `src` (host memory, e.g. the mmap'd .hk
+ * tensor, or device memory when src_on_device != 0) to the device and repacks them into the
+ * device layout. Refuses cols % 32 != 0 or cols not a whole number of blocks
+ * (UNSUPPORTED_SHAPE), unknown types (UNSUPPORTED_TYPE) and bytes != matrix_bytes. */
+int hkhip_upload(hkhip_engine *eng, const void *src, uint64_t bytes, uint8_t t, uint32_t rows,
+                 uint32_t cols, int src_on_device, hkhip_mat *out);
+void hkhip_free(hkhip_engine *eng, hkhip_mat *m);
+
+/* Decodes rows [row0, row0 + nrows) of a device matrix to f32 [nrows][cols] in device memory,
+ * bit-for-bit as dequantizeRow (src/quant/dequant.zig:550-591). */
+int hkhip_dequantize(hkhip_engine *eng, const hkhip_mat *m, uint32_t row0, uint32_t nrows, float *out_dev);
+
+/* ---- activations (prepare: src/cuda/engine.zig:614-630; CPU arithmetic vecdot.zig:134-180) ----
+ * Quantizes x_dev [n][k] f32 into xq_dev (hkhip_act_bytes(n, k) bytes) as `kind`. The buffer
+ * holds both kinds side by side, so one input prepared once serves every product reading it. */
+int hkhip_qact(hkhip_engine *eng, const float *x_dev, uint32_t n, uint32_t k, int kind, void *xq_dev);
+/* Reads one kind back in hk's block structs: A8 as {f32 d, i32 s, i8 qs[32]} (40 B) per 32,
+ * Q8K as {f32 d, i8 qs[256], i16 bsums[16]} (292 B) per 256 (vecdot.zig:22-26, blocks.zig:25). */
+int hkhip_act_export(hkhip_engine *eng, const void *xq_dev, uint32_t n, uint32_t k, int kind, void *host_out);
+
+/* ---- products (mm: src/cuda/engine.zig:581-611) ----
+ * y_dev[t][r] (=|+=) dot(W[r], x[t]) + bias[r] for t < n, from activations already prepared
+ * with hkhip_qact for the matrix's kind (A8: Q8_0, IQ4_NL; Q8K: Q4_K, Q6_K). bias may be NULL.
+ * hkhip_matvec: decode kernels, 1 <= n <= 8 (src/kernels_impl.zig:14-33 rows).
+ * hkhip_gemm:   prefill MFMA kernels, any n >= 1 (src/quant/gemm.zig tiles).
+ * hkhip_mm:     picks matvec for n < 8 and gemm otherwise (matmul.zig:18 min_tiled_tokens). */
+int hkhip_matvec(hkhip_engine *eng, const hkhip_mat *m, const void *xq_dev, float *y_dev, uint32_t n,
+                 const float *bias_dev, int mode);
+int hkhip_gemm(hkhip_engine *eng, const hkhip_mat *m, const void *xq_dev, float *y_dev, uint32_t n,
+               const float *bias_dev, int mode);
+int hkhip_mm(hkhip_engine *eng, const hkhip_mat *m, const void *xq_dev, float *y_dev, uint32_t n,
+             const float *bias_dev, int mode);
+
+/* ---- host-pointer products (secondary boundary: src/c_api.zig:1380-1400, hk.h:451-453,
+ * src/engine/abi_ops.zig:65-107) ----
+ * y[t*m + r] = dot(W[r], x[t]) + bias[r] with W, x, bias, y in host memory, on the process's
+ * default engine (device 0). On failure y is filled with NaN and a negative code returned. */
+int hkhip_gemm_host(uint8_t t, const void *w, const float *x, const float *bias, float *y, uint64_t m,
+                    uint64_t k, uint64_t n);
+int hkhip_gemv_q8_0(const void *w, const float *x, const float *bias, float *y, uint64_t m, uint64_t k);
+int hkhip_gemv_q4_k(const void *w, const float *x, const float *bias, float *y, uint64_t m, uint64_t k);
+int hkhip_gemv_q6_k(const void *w, const float *x, const float *bias, float *y, uint64_t m, uint64_t k);
+int hkhip_gemv_iq4_nl(const void *w, const float *x, const float *bias, float *y, uint64_t m, uint64_t k);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* HKHIP_H */

@@ -1,0 +1,236 @@
+"""GPU parity: the HIP kernels, called through the C ABI, against the CPU oracle.
+
+Bars: dequantized weights and quantized activations bit-identical to hk's CPU arithmetic;
+matvec / GEMM outputs within max relative error 1e-3 (helpers.parity_err) of the oracle's
+restatement of hk's CPU kernels on the same seeded inputs. Shapes follow the reference's own
+GPU parity tests (tests/test_cuda.zig:287-389: M = 21, K = 512, n in {1, 19, 150}) plus ragged
+rows, the smallest legal K, bias, accumulate mode and the BASELINE shapes.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from hk_amd import formats as F
+from hk_amd import synth
+from oracle import oracle as O
+from tests.helpers import PARITY_TOL, load_fixture, parity_err
+
+pytestmark = pytest.mark.gpu
+
+FMTS = [F.Q8_0, F.Q4_K, F.Q6_K, F.IQ4_NL]
+FIXTURES = {F.Q8_0: "q8_0", F.Q4_K: "q4_k", F.Q6_K: "q6_k", F.IQ4_NL: "iq4_nl"}
+
+
+@pytest.fixture(scope="module")
+def torch_cuda():
+    import torch
+
+    assert torch.cuda.is_available(), "GPU tests need a visible MI355X"
+    return torch
+
+
+@pytest.fixture(scope="module")
+def eng(torch_cuda):
+    from hk_amd import Engine
+
+    e = Engine(0)
+    e.set_stream(torch_cuda.cuda.current_stream().cuda_stream)
+    yield e
+    e.close()
+
+
+def run(eng, torch, t, raw, m, k, x, path="mm", bias=None, mode=0, y0=None):
+    n = x.shape[0]
+    w = eng.upload(raw, t, m, k)
+    xd = torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    xq = torch.empty(eng.act_bytes(n, k), dtype=torch.uint8, device="cuda")
+    eng.qact(xd, n, k, F.ACT_KIND[t], xq)
+    y = torch.from_numpy(y0.copy()).cuda() if y0 is not None else torch.full((n, m), float("nan"), device="cuda")
+    bd = torch.from_numpy(bias).cuda() if bias is not None else None
+    getattr(eng, path)(w, xq, y, n, bd, mode)
+    torch.cuda.synchronize()
+    out = y.cpu().numpy()
+    eng.free(w)
+    return out
+
+
+# ---------------------------------------------------------------------------------------- dequant
+
+@pytest.mark.parametrize("t", FMTS)
+def test_dequant_fixture_bit_exact(eng, torch_cuda, t):
+    fx = load_fixture(FIXTURES[t])
+    rows, k = fx["rows"], fx["blocks_per_row"] * fx["block_elems"]
+    w = eng.upload(fx["raw"], t, rows, k)
+    out = torch_cuda.empty((rows, k), dtype=torch_cuda.float32, device="cuda")
+    eng.dequantize(w, out)
+    got = out.cpu().numpy()
+    want = np.stack([O.dequantize(t, fx["raw"][r], k) for r in range(rows)])
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(got, fx["expected"])  # gguf's values (equal up to the sign of zero)
+    eng.free(w)
+
+
+@pytest.mark.parametrize("t", FMTS)
+def test_dequant_random_bit_exact(eng, torch_cuda, t):
+    rows, k = 13, 1024
+    raw = synth.weights_np(t, rows, k, seed=7 + t)
+    w = eng.upload(raw, t, rows, k)
+    out = torch_cuda.empty((rows - 3, k), dtype=torch_cuda.float32, device="cuda")
+    eng.dequantize(w, out, row0=3, nrows=rows - 3)
+    got = out.cpu().numpy()
+    want = np.stack([O.dequantize(t, raw[r], k) for r in range(3, rows)])
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    eng.free(w)
+
+
+# ---------------------------------------------------------------------------------------- qact
+
+def _act_cases():
+    rng = np.random.default_rng(11)
+    x = rng.normal(0, 1, (5, 1024)).astype(np.float32)
+    x[1, :256] = 0.0                      # an all-zero super-block and eight zero A8 blocks
+    x[2, 3] = 7.5
+    x[2, 200] = -7.5                      # tie on |x|: the first one sets the sign of d
+    x[3] *= 1e-30                         # tiny (denormal-range) values
+    x[4] = synth.activations_np(1, 1024, 3, outliers=0.01)[0]
+    return x
+
+
+@pytest.mark.parametrize("kind", [F.ACT_A8, F.ACT_Q8K])
+def test_qact_bit_exact(eng, torch_cuda, kind):
+    x = _act_cases()
+    n, k = x.shape
+    xd = torch_cuda.from_numpy(x).cuda()
+    xq = torch_cuda.empty(eng.act_bytes(n, k), dtype=torch_cuda.uint8, device="cuda")
+    eng.qact(xd, n, k, kind, xq)
+    got = eng.act_export(xq, n, k, kind)
+    want = np.concatenate([(O.quantize_a8 if kind == F.ACT_A8 else O.quantize_q8k)(x[i]) for i in range(n)])
+    assert np.array_equal(got, want.view(np.uint8))
+
+
+# ---------------------------------------------------------------------------------------- products
+
+MATVEC_SHAPES = [(21, 512), (300, 1024), (64, 256), (1, 4096), (37, 3072)]
+
+
+@pytest.mark.parametrize("t", FMTS)
+@pytest.mark.parametrize("n", [1, 2, 3, 4, 8])
+@pytest.mark.parametrize("shape", MATVEC_SHAPES)
+def test_matvec_parity(eng, torch_cuda, t, n, shape):
+    m, k = shape
+    raw = synth.weights_np(t, m, k, seed=100 + m + t)
+    x = synth.activations_np(n, k, seed=200 + n)
+    got = run(eng, torch_cuda, t, raw, m, k, x, path="matvec")
+    want = O.matmul(t, raw, m, k, x, n, tiled=False)
+    assert parity_err(got, want) <= PARITY_TOL
+
+
+GEMM_SHAPES = [(21, 512), (37, 256), (130, 1024), (64, 3072)]
+
+
+@pytest.mark.parametrize("t", FMTS)
+@pytest.mark.parametrize("n", [1, 8, 11, 19, 150])
+@pytest.mark.parametrize("shape", GEMM_SHAPES)
+def test_gemm_parity(eng, torch_cuda, t, n, shape):
+    m, k = shape
+    raw = synth.weights_np(t, m, k, seed=300 + m + t)
+    x = synth.activations_np(n, k, seed=400 + n, outliers=0.01)
+    got = run(eng, torch_cuda, t, raw, m, k, x, path="gemm")
+    want = O.matmul(t, raw, m, k, x, n, tiled=True)
+    assert parity_err(got, want) <= PARITY_TOL
+
+
+@pytest.mark.parametrize("t", FMTS)
+def test_fixture_rows_gemm(eng, torch_cuda, t):
+    """The reference's tiled-GEMM test shape (test_quant.zig:281-359): 37 rows tiled from the
+    fixture rows, 11 tokens, bias i % 5."""
+    fx = load_fixture(FIXTURES[t])
+    k = fx["blocks_per_row"] * fx["block_elems"]
+    raw = np.stack([fx["raw"][r % fx["rows"]] for r in range(37)])
+    x = np.random.default_rng(0x6E33).uniform(-1, 1, (11, k)).astype(np.float32)
+    bias = (np.arange(37) % 5).astype(np.float32)
+    got = run(eng, torch_cuda, t, raw, 37, k, x, path="mm", bias=bias)
+    want = O.matmul(t, raw, 37, k, x, 11, bias=bias)
+    assert parity_err(got, want) <= PARITY_TOL
+
+
+@pytest.mark.parametrize("t", FMTS)
+@pytest.mark.parametrize("n", [7, 8])
+def test_mm_dispatch_bias_accumulate(eng, torch_cuda, t, n):
+    m, k = 45, 512
+    raw = synth.weights_np(t, m, k, seed=500 + t)
+    x = synth.activations_np(n, k, seed=501)
+    bias = np.linspace(-2, 2, m).astype(np.float32)
+    y0 = synth.activations_np(n, m, seed=502)
+    got = run(eng, torch_cuda, t, raw, m, k, x, path="mm", bias=bias, mode=1, y0=y0)
+    want = O.matmul(t, raw, m, k, x, n, bias=bias) + y0
+    assert parity_err(got, want) <= PARITY_TOL
+
+
+def test_host_gemv_entry_points(torch_cuda):
+    from hk_amd import gemm, gemv
+
+    m, k = 33, 1024
+    for t in FMTS:
+        raw = synth.weights_np(t, m, k, seed=600 + t)
+        x = synth.activations_np(1, k, seed=601)
+        bias = np.arange(m, dtype=np.float32)
+        got = gemv(t, raw, x[0], bias, m, k)
+        want = O.matmul(t, raw, m, k, x, 1, bias=bias)[0]
+        assert parity_err(got, want) <= PARITY_TOL
+        xs = synth.activations_np(12, k, seed=602)
+        got = gemm(t, raw, xs, None, m, k, 12)
+        assert parity_err(got, O.matmul(t, raw, m, k, xs, 12)) <= PARITY_TOL
+
+
+def test_errors(eng, torch_cuda):
+    from hk_amd import HipError
+    from hk_amd import gemm as host_gemm
+
+    with pytest.raises(HipError) as e:
+        eng.upload(np.zeros(100 * 34 // 32, np.uint8), F.Q8_0, 1, 100)
+    assert e.value.code == -2  # UNSUPPORTED_SHAPE: cols not a multiple of 32
+    with pytest.raises(HipError) as e:
+        eng.upload(np.zeros(18, np.uint8), 0x15, 1, 32)  # Q4_0: not on this path
+    assert e.value.code == -1
+    raw = synth.weights_np(F.Q4_K, 4, 256, seed=1)
+    w = eng.upload(raw, F.Q4_K, 4, 256)
+    xq = torch_cuda.zeros(eng.act_bytes(9, 256), dtype=torch_cuda.uint8, device="cuda")
+    y = torch_cuda.zeros((9, 4), device="cuda")
+    with pytest.raises(HipError):
+        eng.matvec(w, xq, y, 9)  # decode kernels take at most 8 tokens
+    with pytest.raises(HipError):
+        eng.mm(w, xq, y, 2, None, 7)  # unknown mode
+    eng.free(w)
+    with pytest.raises(HipError) as e:
+        host_gemm(F.Q4_K, np.zeros(144, np.uint8), np.zeros(100, np.float32), None, 1, 100, 1)
+    assert np.isnan(e.value.y).all()  # hk's C ABI poisons the output (c_api.zig:16-18)
+
+
+# ---------------------------------------------------------------------------------------- BASELINE shapes
+
+@pytest.mark.parametrize("t,m,k,n", [
+    (F.Q8_0, 3072, 1024, 1),        # config 1
+    (F.Q4_K, 14336, 4096, 1),       # config 4 gate/up
+    (F.Q4_K, 4096, 14336, 8),       # config 4 down, batch 8
+    (F.IQ4_NL, 14336, 4096, 1),     # config 5
+    (F.Q6_K, 4096, 14336, 1),       # config 5 down
+])
+def test_baseline_matvec_shapes(eng, torch_cuda, t, m, k, n):
+    raw = synth.weights_np(t, m, k, seed=synth.seed_for(4, t))
+    x = synth.activations_np(n, k, seed=synth.seed_for(4, 99), outliers=0.01 if t == F.IQ4_NL else 0.0)
+    got = run(eng, torch_cuda, t, raw, m, k, x, path="mm")
+    want = O.matmul(t, raw, m, k, x, n, threads=16)
+    assert parity_err(got, want) <= PARITY_TOL
+
+
+@pytest.mark.parametrize("t,m,k", [(F.Q4_K, 3072, 1024), (F.Q4_K, 1024, 3072), (F.Q6_K, 1024, 3072),
+                                   (F.IQ4_NL, 3072, 1024)])
+def test_baseline_prefill_shapes(eng, torch_cuda, t, m, k):
+    n = 512  # config 3
+    raw = synth.weights_np(t, m, k, seed=synth.seed_for(3, t))
+    x = synth.activations_np(n, k, seed=synth.seed_for(3, 99))
+    got = run(eng, torch_cuda, t, raw, m, k, x, path="mm")
+    want = O.matmul(t, raw, m, k, x, n, threads=16)
+    assert parity_err(got, want) <= PARITY_TOL
