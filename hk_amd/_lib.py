@@ -45,6 +45,7 @@ SIGNATURES = {
     "hkhip_init": (_I, [_I, ctypes.POINTER(_P)]),
     "hkhip_destroy": (None, [_P]),
     "hkhip_set_stream": (_I, [_P, _P]),
+    "hkhip_use_own_stream": (_I, [_P]),
     "hkhip_stream": (_P, [_P]),
     "hkhip_sync": (_I, [_P]),
     "hkhip_last_error": (ctypes.c_char_p, []),
@@ -62,6 +63,7 @@ SIGNATURES = {
     "hkhip_qact": (_I, [_P, _P, _U32, _U32, _I, _P]),
     "hkhip_act_export": (_I, [_P, _P, _U32, _U32, _I, _P]),
     "hkhip_matvec": (_I, [_P, _MP, _P, _P, _U32, _P, _I]),
+    "hkhip_matvec_parts": (_I, [_P, _MP, _U32, _P, _P, _U32, _P, _P, _I]),
     "hkhip_gemm": (_I, [_P, _MP, _P, _P, _U32, _P, _I]),
     "hkhip_mm": (_I, [_P, _MP, _P, _P, _U32, _P, _I]),
     "hkhip_gemm_host": (_I, [_U8, _P, _P, _P, _P, _U64, _U64, _U64]),

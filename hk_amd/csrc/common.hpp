@@ -135,6 +135,15 @@ hipError_t launch_dequant(int t, const uint8_t *w, uint32_t rows, uint32_t cols,
                           float *out, hipStream_t s);
 hipError_t launch_qact(const float *x, uint32_t n, uint32_t k, int kind, uint8_t *xq, hipStream_t s);
 hipError_t launch_act_pack(const uint8_t *xq, uint32_t n, uint32_t k, int kind, uint8_t *out, hipStream_t s);
+// One matrix of a fused decode launch (all parts share cols and the input).
+struct MvPartDesc {
+    const uint8_t *w;
+    float *y;
+    const float *bias;
+    uint32_t rows;
+};
+hipError_t launch_mmvq_parts(int t, const MvPartDesc *parts, int nparts, uint32_t K, const float *x,
+                             const uint8_t *xq, uint32_t n, int mode, hipStream_t s);
 hipError_t launch_mmvq(int t, const uint8_t *w, uint32_t rows, uint32_t cols, const uint8_t *xq, uint32_t n,
                        float *y, const float *bias, int mode, hipStream_t s);
 hipError_t launch_mm(int t, const uint8_t *w, uint32_t rows, uint32_t cols, const uint8_t *xq, uint32_t n,

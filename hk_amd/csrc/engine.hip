@@ -95,7 +95,14 @@ void hkhip_destroy(hkhip_engine *eng) {
 int hkhip_set_stream(hkhip_engine *eng, void *stream) {
     int rc = enter(eng);
     if (rc) return rc;
-    eng->cur = stream ? reinterpret_cast<hipStream_t>(stream) : eng->own;
+    eng->cur = reinterpret_cast<hipStream_t>(stream);
+    return HKHIP_OK;
+}
+
+int hkhip_use_own_stream(hkhip_engine *eng) {
+    int rc = enter(eng);
+    if (rc) return rc;
+    eng->cur = eng->own;
     return HKHIP_OK;
 }
 
@@ -273,6 +280,27 @@ int hkhip_matvec(hkhip_engine *eng, const hkhip_mat *m, const void *xq_dev, floa
     if (n == 0) return HKHIP_OK;
     HIP_TRY(launch_mmvq(m->t, reinterpret_cast<const uint8_t *>(m->mem), m->rows, m->cols,
                         reinterpret_cast<const uint8_t *>(xq_dev), n, y_dev, bias_dev, mode, eng->cur), "mmvq launch");
+    return HKHIP_OK;
+}
+
+int hkhip_matvec_parts(hkhip_engine *eng, const hkhip_mat *mats, uint32_t nparts, const float *x_dev,
+                       const void *xq_dev, uint32_t n, float *const *ys, const float *const *biases, int mode) {
+    int rc = enter(eng);
+    if (rc) return rc;
+    if (!mats || !ys || nparts < 1 || nparts > 4) return fail(HKHIP_E_BAD_ARGUMENT, "need 1..4 parts, got %u", nparts);
+    if ((x_dev == nullptr) == (xq_dev == nullptr)) return fail(HKHIP_E_BAD_ARGUMENT, "give exactly one of x and xq");
+    MvPartDesc parts[4];
+    for (uint32_t i = 0; i < nparts; i++) {
+        if ((rc = check_product(&mats[i], x_dev ? (const void *)x_dev : xq_dev, ys[i], n, mode))) return rc;
+        if (mats[i].t != mats[0].t || mats[i].cols != mats[0].cols)
+            return fail(HKHIP_E_BAD_ARGUMENT, "fused parts must share type and cols");
+        parts[i] = MvPartDesc{reinterpret_cast<const uint8_t *>(mats[i].mem), ys[i], biases ? biases[i] : nullptr,
+                              mats[i].rows};
+    }
+    if (n > 8) return fail(HKHIP_E_UNSUPPORTED_SHAPE, "matvec takes at most 8 tokens, got %u", n);
+    if (n == 0) return HKHIP_OK;
+    HIP_TRY(launch_mmvq_parts(mats[0].t, parts, int(nparts), mats[0].cols, x_dev,
+                              reinterpret_cast<const uint8_t *>(xq_dev), n, mode, eng->cur), "mmvq launch");
     return HKHIP_OK;
 }
 

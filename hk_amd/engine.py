@@ -85,8 +85,12 @@ class Engine:
         return lib().hkhip_device_name(self._h).decode()
 
     def set_stream(self, stream: int | None) -> None:
-        """Run on an existing hipStream_t (e.g. torch.cuda.current_stream().cuda_stream)."""
-        check(lib().hkhip_set_stream(self._h, stream))
+        """Run on an existing hipStream_t, e.g. torch.cuda.current_stream().cuda_stream
+        (0 / None is the null stream); use_own_stream() goes back to the engine's stream."""
+        check(lib().hkhip_set_stream(self._h, stream or None))
+
+    def use_own_stream(self) -> None:
+        check(lib().hkhip_use_own_stream(self._h))
 
     @property
     def stream(self) -> int:
@@ -147,6 +151,15 @@ class Engine:
     # -- products ------------------------------------------------------------------------
     def matvec(self, m: DevMat, xq, y, n: int, bias=None, mode: int = STORE) -> None:
         check(lib().hkhip_matvec(self._h, ctypes.byref(m.raw), _ptr(xq), _ptr(y), n, _ptr(bias), mode))
+
+    def matvec_parts(self, mats, ys, n: int, x=None, xq=None, biases=None, mode: int = STORE) -> None:
+        """Up to four matrices sharing one input in one launch (matmul.runParts). Pass the f32
+        input `x` (quantized inside the kernel) or a prepared `xq`."""
+        k = len(mats)
+        arr = (HkhipMat * k)(*[m.raw for m in mats])
+        yp = (ctypes.c_void_p * k)(*[_ptr(y) for y in ys])
+        bp = None if biases is None else (ctypes.c_void_p * k)(*[_ptr(b) for b in biases])
+        check(lib().hkhip_matvec_parts(self._h, arr, k, _ptr(x), _ptr(xq), n, yp, bp, mode))
 
     def gemm(self, m: DevMat, xq, y, n: int, bias=None, mode: int = STORE) -> None:
         check(lib().hkhip_gemm(self._h, ctypes.byref(m.raw), _ptr(xq), _ptr(y), n, _ptr(bias), mode))

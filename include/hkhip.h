@@ -73,8 +73,10 @@ typedef struct hkhip_mat {
 int hkhip_device_count(void);
 int hkhip_init(int device, hkhip_engine **out);
 void hkhip_destroy(hkhip_engine *eng);
-/* Runs the engine's work on `stream` (a hipStream_t) instead of its own stream; NULL restores it. */
+/* Runs the engine's work on `stream` (a hipStream_t; NULL is the device's null stream). */
 int hkhip_set_stream(hkhip_engine *eng, void *stream);
+/* Returns the engine to the stream it created at init. */
+int hkhip_use_own_stream(hkhip_engine *eng);
 void *hkhip_stream(hkhip_engine *eng);
 int hkhip_sync(hkhip_engine *eng);
 const char *hkhip_last_error(void);
@@ -126,6 +128,15 @@ int hkhip_gemm(hkhip_engine *eng, const hkhip_mat *m, const void *xq_dev, float 
                const float *bias_dev, int mode);
 int hkhip_mm(hkhip_engine *eng, const hkhip_mat *m, const void *xq_dev, float *y_dev, uint32_t n,
              const float *bias_dev, int mode);
+
+/* Fused decode products: up to 4 matrices that read the same input (q/k/v; gate/up) in one
+ * launch, as matmul.runParts fuses them on the CPU (src/engine/matmul.zig:96-144). All parts
+ * share type and cols. Give the input either as f32 x_dev [n][cols], which the kernel quantizes
+ * itself with the qact arithmetic (no separate hkhip_qact launch), or as xq_dev prepared by
+ * hkhip_qact (x_dev NULL). ys[i] / biases[i] belong to mats[i]; biases may be NULL or hold
+ * NULLs. 1 <= n <= 8. */
+int hkhip_matvec_parts(hkhip_engine *eng, const hkhip_mat *mats, uint32_t nparts, const float *x_dev,
+                       const void *xq_dev, uint32_t n, float *const *ys, const float *const *biases, int mode);
 
 /* ---- host-pointer products (secondary boundary: src/c_api.zig:1380-1400, hk.h:451-453,
  * src/engine/abi_ops.zig:65-107) ----

@@ -1,0 +1,94 @@
+"""The C-ABI library without a GPU: it loads, exports exactly what include/hkhip.h declares,
+and its host-side logic (sizes, validation, error codes, NaN poisoning) behaves as the
+reference's C ABI does. No compute call reaches a device here."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from hk_amd import _lib, formats as F
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions() -> set[str]:
+    text = open(os.path.join(ROOT, "include", "hkhip.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(hkhip_\w+)\s*\(", text))
+
+
+def test_library_builds_and_loads():
+    assert os.path.exists(_lib.LIB_PATH), "run __graft_entry__.build() first"
+    _lib.lib()
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    declared = header_functions()
+    assert len(declared) >= 25
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    for name in sorted(declared):
+        assert hasattr(lib, name), f"{name} declared in hkhip.h but not exported"
+    assert declared == set(_lib.SIGNATURES), "Python binding and header disagree"
+
+
+def test_missing_library_fails_loudly(monkeypatch):
+    monkeypatch.setattr(_lib, "LIB_PATH", "/nonexistent/libhkhip.so")
+    monkeypatch.setattr(_lib, "_lib", None)
+    with pytest.raises(RuntimeError, match="missing"):
+        _lib.lib()
+
+
+def test_sizes_match_the_block_table():
+    L = _lib.lib()
+    for t, (elems, nbytes) in F.INFO.items():
+        assert L.hkhip_supports(t) == 1
+        assert L.hkhip_matrix_bytes(t, 7, elems * 3) == 7 * 3 * nbytes
+        assert F.matrix_bytes(t, 7, elems * 3) == 7 * 3 * nbytes
+    assert L.hkhip_matrix_bytes(F.Q4_K, 14336, 4096) == 33030144
+    assert L.hkhip_matrix_bytes(F.Q6_K, 128256, 4096) == 430940160
+    assert L.hkhip_supports(0x15) == 0  # Q4_0 is not on this path
+    assert L.hkhip_matrix_bytes(0x15, 1, 32) == -1  # UNSUPPORTED_TYPE
+    assert L.hkhip_matrix_bytes(F.Q4_K, 1, 100) == -2  # UNSUPPORTED_SHAPE
+    assert b"whole number" in L.hkhip_last_error()
+
+
+def test_byte_size_rejects_partial_blocks():
+    """blocks.zig:129-134 ('block size table matches the reference')."""
+    with pytest.raises(F.NotBlockAligned):
+        F.byte_size(F.Q4_K, 100)
+    with pytest.raises(F.UnsupportedType):
+        F.byte_size(0x22, 256)
+    assert F.BPW[F.Q4_K] == 4.5 and F.BPW[F.Q6_K] == 6.5625 and F.BPW[F.Q8_0] == 8.5
+
+
+def test_act_bytes_holds_both_kinds():
+    L = _lib.lib()
+    n, k = 3, 4096
+    need = n * k * 2 + n * k // 32 * 8 + n * k // 256 * 4 + n * k // 16 * 2
+    assert L.hkhip_act_bytes(n, k) >= need
+    assert L.hkhip_act_bytes(n, k) % 256 == 0
+
+
+def test_host_product_poisons_output_on_failure():
+    """A failing hkhip_gemv_* fills y with NaN (c_api.zig:16-18) and returns a negative code.
+    Here it fails either on the bad shape or, on a machine without a GPU, on the device."""
+    L = _lib.lib()
+    y = np.zeros(4, np.float32)
+    w = np.zeros(4 * 144, np.uint8)
+    x = np.zeros(100, np.float32)
+    rc = L.hkhip_gemv_q4_k(w.ctypes.data, x.ctypes.data, None, y.ctypes.data, 4, 100)
+    assert rc == -2 and np.isnan(y).all()
+
+
+def test_engine_init_reports_missing_device():
+    """Without a HIP device, init fails with NO_DEVICE and a message (probeCuda's 'no device')."""
+    L = _lib.lib()
+    if L.hkhip_device_count() > 0:
+        pytest.skip("a device is present")
+    h = ctypes.c_void_p()
+    assert L.hkhip_init(0, ctypes.byref(h)) == -6
+    assert L.hkhip_last_error()

@@ -234,3 +234,51 @@ def test_baseline_prefill_shapes(eng, torch_cuda, t, m, k):
     got = run(eng, torch_cuda, t, raw, m, k, x, path="mm")
     want = O.matmul(t, raw, m, k, x, n, threads=16)
     assert parity_err(got, want) <= PARITY_TOL
+
+
+# ---------------------------------------------------------------------------------------- fused parts
+
+@pytest.mark.parametrize("t", FMTS)
+@pytest.mark.parametrize("n", [1, 3, 8])
+@pytest.mark.parametrize("prepared", [False, True])
+def test_matvec_parts_parity(eng, torch_cuda, t, n, prepared):
+    """q/k/v-style fusion: three matrices of different heights sharing one input, in one launch,
+    with the input quantized inside the kernel (or prepared by qact). Each part is checked
+    against the oracle on its own."""
+    torch = torch_cuda
+    k = 1024
+    heights = [96, 32, 40]
+    raws = [synth.weights_np(t, m, k, seed=700 + i + t) for i, m in enumerate(heights)]
+    x = synth.activations_np(n, k, seed=701 + n, outliers=0.01)
+    mats = [eng.upload(r, t, m, k) for r, m in zip(raws, heights)]
+    ys = [torch.full((n, m), float("nan"), device="cuda") for m in heights]
+    biases = [torch.from_numpy(np.arange(m, dtype=np.float32) * 0.5).cuda() for m in heights]
+    xd = torch.from_numpy(x).cuda()
+    if prepared:
+        xq = torch.empty(eng.act_bytes(n, k), dtype=torch.uint8, device="cuda")
+        eng.qact(xd, n, k, F.ACT_KIND[t], xq)
+        eng.matvec_parts(mats, ys, n, xq=xq, biases=biases)
+    else:
+        eng.matvec_parts(mats, ys, n, x=xd, biases=biases)
+    torch.cuda.synchronize()
+    for r, m, y, b in zip(raws, heights, ys, biases):
+        want = O.matmul(t, r, m, k, x, n, bias=b.cpu().numpy(), tiled=False)
+        assert parity_err(y.cpu().numpy(), want) <= PARITY_TOL
+    for w in mats:
+        eng.free(w)
+
+
+@pytest.mark.parametrize("t,k,n", [(F.Q4_K, 14336, 8), (F.Q8_0, 20480, 8), (F.Q6_K, 4096, 8)])
+def test_matvec_parts_large_k(eng, torch_cuda, t, k, n):
+    """The largest decode inputs: 8 tokens of the 8B down projection (~130 KB of activations in
+    LDS) and, for Q8_0, more than the LDS holds (the launch splits the tokens)."""
+    torch = torch_cuda
+    m = 300
+    raw = synth.weights_np(t, m, k, seed=800 + t)
+    x = synth.activations_np(n, k, seed=801)
+    w = eng.upload(raw, t, m, k)
+    y = torch.full((n, m), float("nan"), device="cuda")
+    eng.matvec_parts([w], [y], n, x=torch.from_numpy(x).cuda())
+    torch.cuda.synchronize()
+    assert parity_err(y.cpu().numpy(), O.matmul(t, raw, m, k, x, n, tiled=False)) <= PARITY_TOL
+    eng.free(w)

@@ -1,0 +1,259 @@
+"""Pins of the CPU oracle (CPU only; no GPU).
+
+The oracle restates hk's CPU kernels in C. Each part is pinned by something other than its own
+formula:
+  decoders     hk's fixtures, written by the gguf reference decoder (tools/gen_quant_fixtures.py),
+               bit for bit up to the sign of zero
+  scale unpack the word trick of vecdot.zig:461-474 against scaleMinK4 (dequant.zig:166-175) on
+               every possible byte pattern of each scale position
+  quantizers   closed-form invariants (|q| <= 127, the extreme element hits +-127, d*q within
+               d/2 of x, s / bsums are the sums of q, the all-zero block, first-index ties)
+  dots         an independent float64 restatement from the decoded weights and the dequantized
+               activations (d * q), which is algebraically the integer dot, to 1e-5 of the terms;
+               and hk's own bound against the float decode-dot (test_quant.zig:161)
+  GEMM path    equal to the row dots within 1e-4 (test_quant.zig:326), 37 rows x 11 tokens
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from hk_amd import formats as F
+from hk_amd import synth
+from oracle import oracle as O
+from tests.helpers import load_fixture
+
+FMTS = [F.Q8_0, F.Q4_K, F.Q6_K, F.IQ4_NL]
+FIXTURES = {F.Q8_0: "q8_0", F.Q4_K: "q4_k", F.Q6_K: "q6_k", F.IQ4_NL: "iq4_nl"}
+GGML_TYPE = {F.Q8_0: 8, F.Q4_K: 12, F.Q6_K: 14, F.IQ4_NL: 20}
+
+
+@pytest.fixture(scope="module", autouse=True)
+def built():
+    O.build()
+
+
+# ------------------------------------------------------------------------------------ decoders
+
+@pytest.mark.parametrize("t", FMTS)
+def test_fixture_geometry(t):
+    fx = load_fixture(FIXTURES[t])
+    assert fx["ggml_type"] == GGML_TYPE[t]
+    assert (fx["block_elems"], fx["block_bytes"]) == F.INFO[t]
+    assert (O.block_elems(t), O.block_bytes(t)) == F.INFO[t]
+
+
+@pytest.mark.parametrize("t", FMTS)
+def test_decoders_match_reference_fixtures(t):
+    fx = load_fixture(FIXTURES[t])
+    k = fx["blocks_per_row"] * fx["block_elems"]
+    got = np.stack([O.dequantize(t, fx["raw"][r], k) for r in range(fx["rows"])])
+    want = fx["expected"]
+    assert np.array_equal(got, want)  # exact values (0.0 == -0.0)
+    diff = got.view(np.uint32) != want.view(np.uint32)
+    # hk's q6_k decoder computes d * f32(scale * q), which is -0.0 for a negative d and q = 0;
+    # gguf writes +0.0 there. Every other bit agrees.
+    assert np.all(got[diff] == 0.0)
+    if t != F.Q6_K:
+        assert not diff.any()
+
+
+def test_dequantize_rejects_wrong_lengths():
+    """dequantizeRow refuses partial blocks (test_quant.zig 'decoding rejects wrong lengths')."""
+    with pytest.raises(ValueError):
+        O.dequantize(F.Q8_0, np.zeros(33, np.uint8), 32)
+    with pytest.raises(ValueError):
+        O.dequantize(F.Q8_0, np.zeros(34, np.uint8), 31)
+    with pytest.raises(ValueError):
+        O.dequantize(0x22, np.zeros(34, np.uint8), 32)
+
+
+@pytest.mark.parametrize("t", FMTS)
+def test_decode_closed_forms_on_constructed_blocks(t):
+    """Hand-built blocks whose values follow from the format definition alone."""
+    if t == F.Q8_0:
+        b = np.zeros(34, np.uint8)
+        b[0:2] = np.array([0.5], np.float16).view(np.uint8)
+        b[2:34] = np.arange(-16, 16, dtype=np.int8).view(np.uint8)
+        assert np.array_equal(O.dequantize(t, b, 32), np.arange(-16, 16) * 0.5)
+    elif t == F.IQ4_NL:
+        b = np.zeros(18, np.uint8)
+        b[0:2] = np.array([2.0], np.float16).view(np.uint8)
+        b[2:18] = (np.arange(16) | ((15 - np.arange(16)) << 4)).astype(np.uint8)
+        want = 2.0 * np.array(F.KVALUES_IQ4NL + F.KVALUES_IQ4NL[::-1], np.float32)
+        assert np.array_equal(O.dequantize(t, b, 32), want)
+    elif t == F.Q4_K:
+        b = np.zeros(144, np.uint8)
+        b[0:2] = np.array([1.0], np.float16).view(np.uint8)   # d
+        b[2:4] = np.array([0.25], np.float16).view(np.uint8)  # dmin
+        # sub-block j: scale j + 1, min 2j (all below 16, so only the low 4 bits are used)
+        for j in range(8):
+            sc, mn = j + 1, 2 * j
+            if j < 4:
+                b[4 + j] = sc
+                b[8 + j] = mn
+            else:
+                b[8 + j] = sc | (mn << 4)
+        b[16:144] = 0x53  # low nibble 3, high nibble 5
+        got = O.dequantize(t, b, 256)
+        for j in range(8):
+            nib = 3 if j % 2 == 0 else 5
+            want = (j + 1) * 1.0 * nib - 0.25 * (2 * j)
+            assert np.all(got[32 * j:32 * j + 32] == np.float32(want))
+    else:  # Q6_K
+        b = np.zeros(210, np.uint8)
+        b[208:210] = np.array([0.5], np.float16).view(np.uint8)
+        b[192:208] = np.arange(-8, 8, dtype=np.int8).view(np.uint8)  # scale per 16
+        b[0:128] = 0x21   # low 4 bits: 1 (ql low nibble), 2 (ql high nibble)
+        b[128:192] = 0xE4  # high 2 bits per quarter: 0, 1, 2, 3
+        got = O.dequantize(t, b, 256)
+        for half in range(2):
+            for part, (low, hi2) in enumerate([(1, 0), (1, 1), (2, 2), (2, 3)]):
+                q = (low | (hi2 << 4)) - 32
+                for l in range(32):
+                    g = 8 * half + 2 * part + l // 16
+                    assert got[128 * half + 32 * part + l] == np.float32(0.5 * ((g - 8) * q))
+
+
+def test_scale_unpack_word_trick_matches_scale_min_k4():
+    """scalesMinsK4 (vecdot.zig:461-474) and scaleMinK4 (dequant.zig:166-175) agree on every
+    byte value at every one of the 12 positions, with the other bytes random."""
+    rng = np.random.default_rng(5)
+    for pos in range(12):
+        for v in range(256):
+            p = rng.integers(0, 256, 12, dtype=np.uint8)
+            p[pos] = v
+            sc, mn = O.scales_mins_words(p)
+            for j in range(8):
+                assert (sc[j], mn[j]) == O.scale_min_k4(j, p)
+
+
+# ------------------------------------------------------------------------------------ quantizers
+
+def _round_half_away(v):
+    a = np.abs(v.astype(np.float64))
+    f = np.floor(a)
+    return np.sign(v) * (f + (a - f >= 0.5))
+
+
+def test_quantize_a8_invariants():
+    rng = np.random.default_rng(1)
+    x = rng.normal(0, 1, 32 * 64).astype(np.float32)
+    x[32:64] = 0.0                        # zero block
+    x[64:96] = rng.normal(0, 1e-30, 32)   # denormal-range block
+    x[96:128] *= 1e4
+    blocks = O.quantize_a8(x)
+    for b, blk in enumerate(blocks):
+        v = x[32 * b:32 * b + 32]
+        q = blk["qs"].astype(np.int64)
+        amax = np.max(np.abs(v))
+        assert blk["d"] == np.float32(amax) / np.float32(127.0)
+        assert blk["s"] == q.sum()
+        assert np.all(np.abs(q) <= 127)
+        if amax == 0:
+            assert np.all(q == 0) and blk["d"] == 0
+            continue
+        i = int(np.argmax(np.abs(v)))
+        assert abs(q[i]) == 127 and np.sign(q[i]) == np.sign(v[i])
+        # q = round_half_away(x * (1/d)) in f32 arithmetic
+        idv = np.float32(1.0) / np.float32(blk["d"])
+        assert np.array_equal(q, _round_half_away(v * idv))
+        assert np.all(np.abs(v - blk["d"] * q) <= blk["d"] * 0.5 * (1 + 1e-5) + 1e-37)
+
+
+def test_quantize_q8k_invariants():
+    rng = np.random.default_rng(2)
+    x = rng.normal(0, 1, 256 * 16).astype(np.float32)
+    x[256:512] = 0.0
+    x[512 + 10], x[512 + 200] = -9.0, 9.0   # tie on |x|: the first (negative) one wins
+    x[768 + 10], x[768 + 200] = 9.0, -9.0
+    x[1024:1280] *= 1e-30
+    blocks = O.quantize_q8k(x)
+    for b, blk in enumerate(blocks):
+        v = x[256 * b:256 * b + 256]
+        q = blk["qs"].astype(np.int64)
+        assert np.array_equal(blk["bsums"], q.reshape(16, 16).sum(axis=1))
+        if np.max(np.abs(v)) == 0:
+            assert np.all(q == 0) and blk["d"] == 0 and np.all(blk["bsums"] == 0)
+            continue
+        i = int(np.argmax(np.abs(v)))  # numpy's argmax returns the first maximum
+        assert q[i] == -127            # iscale * max = -127
+        assert np.sign(blk["d"]) == -np.sign(v[i])
+        assert np.all(q <= 127) and np.all(q >= -128)
+        err = np.abs(v - blk["d"] * q)
+        clamped = q == 127
+        assert np.all(err[~clamped] <= abs(blk["d"]) * 0.5 * (1 + 1e-5) + 1e-37)
+    assert blocks[2]["d"] > 0 and blocks[3]["d"] < 0  # the tie rule: first index sets the sign
+
+
+# ------------------------------------------------------------------------------------ dots
+
+def _decoded_act(t, x):
+    """Dequantized activations d * q, the value the integer dot multiplies by."""
+    if F.ACT_KIND[t] == F.ACT_A8:
+        a = O.quantize_a8(x)
+        return (a["d"][:, None].astype(np.float64) * a["qs"].astype(np.float64)).ravel(), a
+    a = O.quantize_q8k(x)
+    return (a["d"][:, None].astype(np.float64) * a["qs"].astype(np.float64)).ravel(), a
+
+
+@pytest.mark.parametrize("t", FMTS)
+def test_dot_equals_float64_restatement(t):
+    """The integer dot equals sum_k w_k * (d_a q_k) (exact algebra) up to f32 rounding."""
+    rng = np.random.default_rng(0xD07)
+    k = 1024
+    raw = synth.weights_np(t, 6, k, seed=9 + t)
+    for trial in range(4):
+        x = rng.normal(0, 1, k).astype(np.float32)
+        if trial == 3:
+            x[rng.random(k) < 0.01] = 20.0
+        xa, act = _decoded_act(t, x)
+        for r in range(raw.shape[0]):
+            w = O.dequantize(t, raw[r], k).astype(np.float64)
+            want = float(np.sum(w * xa))
+            terms = float(np.sum(np.abs(w * xa)))
+            got = O.dot_row(t, raw[r], act)
+            assert abs(got - want) <= 1e-5 * terms + 1e-6
+
+
+@pytest.mark.parametrize("t", FMTS)
+def test_dot_within_reference_bound_on_fixtures(t):
+    """hk's own check (test_quant.zig:121-194): integer dot vs float64 decode-dot of the f32
+    activations, within 0.01 * sum|terms| + 1e-4."""
+    fx = load_fixture(FIXTURES[t])
+    k = fx["blocks_per_row"] * fx["block_elems"]
+    rng = np.random.default_rng(0xD07)
+    for _ in range(8):
+        x = (rng.random(k) * 2 - 1).astype(np.float32)
+        _, act = _decoded_act(t, x)
+        for r in range(fx["rows"]):
+            w = O.dequantize(t, fx["raw"][r], k).astype(np.float64)
+            want = float(np.sum(w * x))
+            tol = 0.01 * float(np.sum(np.abs(w * x))) + 1e-4
+            assert abs(O.dot_row(t, fx["raw"][r], act) - want) <= tol
+
+
+@pytest.mark.parametrize("t", FMTS)
+def test_gemm_path_equals_row_dots(t):
+    """gemm.tiles equals vecdot single dots (test_quant.zig:281-359): 37 rows from the fixture
+    rows, 11 tokens, bias i % 5, within 1e-4 * max(1, |want|)."""
+    fx = load_fixture(FIXTURES[t])
+    k = fx["blocks_per_row"] * fx["block_elems"]
+    raw = np.stack([fx["raw"][r % fx["rows"]] for r in range(37)])
+    x = np.random.default_rng(0x6E33).uniform(-1, 1, (11, k)).astype(np.float32)
+    bias = (np.arange(37) % 5).astype(np.float32)
+    tiled = O.matmul(t, raw, 37, k, x, 11, bias=bias, tiled=True)
+    rows = O.matmul(t, raw, 37, k, x, 11, bias=bias, tiled=False)
+    assert np.all(np.abs(tiled - rows) <= 1e-4 * np.maximum(1.0, np.abs(rows)))
+
+
+def test_matmul_dispatch_and_threads():
+    """n >= 8 takes the tiled path (matmul.zig:18); threads do not change results."""
+    t, m, k = F.Q4_K, 40, 512
+    raw = synth.weights_np(t, m, k, seed=3)
+    for n in (7, 8):
+        x = synth.activations_np(n, k, seed=4)
+        y1 = O.matmul(t, raw, m, k, x, n, threads=1)
+        y4 = O.matmul(t, raw, m, k, x, n, threads=4)
+        assert np.array_equal(y1, y4)
+        assert np.array_equal(y1, O.matmul(t, raw, m, k, x, n, tiled=(n >= 8)))
