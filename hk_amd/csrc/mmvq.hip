@@ -3,20 +3,25 @@
 // k4Block/dotQ4K 482-522, dotQ6K 533-570); only the order of the f32 scale accumulation differs.
 //
 // One launch computes up to four matrices that read the same input (q/k/v, gate/up), the way
-// matmul.runParts fuses them on the CPU (src/engine/matmul.zig:96-144). Each workgroup stages
-// the quantized activations in LDS: either it quantizes the f32 input itself with the qact
-// arithmetic (quant.hpp; every workgroup produces the same bytes), or it copies an input already
-// quantized by hkhip_qact. A wave issues the weight loads of its first rows before that staging,
-// so the activation work hides under the HBM latency instead of adding to it.
+// matmul.runParts fuses them on the CPU (src/engine/matmul.zig:96-144).
 //
-// Mapping: a row is owned by `lpr` lanes of one wave, chosen so each lane holds up to four work
-// units of the row (a 4096-wide Q4_K row: 16 lanes x 4 units, four rows per wave). A unit is the
-// slice of a row a lane handles, chosen so every lane issues 16-byte loads:
+// Work unit: a slice of a row that one lane reads with 16-byte loads:
 //   Q4_K   a quarter super-block: 32 B of nibbles (two sub-blocks of 32) + the 16-B header
 //   Q6_K   a quarter super-block: 16 B of each of ql-low, ql-high, qh (64 weights, 4 groups)
 //   Q8_0   one block: 32 B of int8
 //   IQ4_NL one block: 16 B of nibbles, looked up in the codebook with byte permutes
-// Products use sdot4 (v_dot4_i32_i8); lane partials are reduced with cross-lane shuffles.
+// Products use sdot4 (v_dot4_i32_i8); lane partials are reduced with DPP lane moves.
+//
+// Two kernels:
+//  * mmvr_kernel (the decode path): lane l of a wave owns units l, l+64, ... of every row and
+//    holds their activations in registers; a wave streams a contiguous range of whole rows, so
+//    each activation register serves every row. Used when the activations fit the registers
+//    (rows of up to 256-512 units, depending on format and token count).
+//  * mmvq_kernel (everything else): a row is shared by 2^k lanes that step through it, and the
+//    activations stay in LDS.
+// Both are persistent (about one wave set per SIMD) with double-buffered weight loads, and both
+// quantize an f32 input themselves, once per workgroup, with the qact arithmetic (quant.hpp), so
+// that a decode step needs no separate quantization launch.
 #include <map>
 #include <mutex>
 #include <stdlib.h>
@@ -26,8 +31,7 @@
 namespace hkhip {
 
 constexpr int MV_PARTS = 4;
-constexpr int MV_UNROLL = 4;                 // units per lane loaded before use
-constexpr uint32_t MV_LDS_MAX = 160 * 1024;  // LDS per workgroup on gfx950
+constexpr uint32_t MV_LDS_MAX = 160 * 1024; // LDS per workgroup on gfx950
 
 struct MvPart {
     const uint8_t *w;
@@ -35,25 +39,32 @@ struct MvPart {
     float *y;
     const float *bias;
     uint32_t rows;
-    uint32_t row0; // first row of this part in the fused row space
+    uint32_t gstart; // first row group of this part (parts start on a group boundary)
 };
 
 struct MvArgs {
     MvPart p[MV_PARTS];
-    uint32_t nparts, total_rows, K;
-    const float *x;       // f32 input [NT][K], quantized in the prologue; or null
-    const int8_t *gqs;    // pre-quantized input (engine activation buffer) when x is null
+    uint32_t nparts, ngroups, K;
+    const float *x;    // f32 input [NT][K], quantized in the prologue; or null
+    const int8_t *gqs; // pre-quantized input (engine activation buffer) when x is null
     const float *gd;
     const int16_t *gbs;
     int mode;
     int lpr_log2;
+    uint32_t ntok; // tokens actually present (register kernel; at most its NT)
 };
 
 __device__ __forceinline__ uint4 ldw(const void *p) { return *reinterpret_cast<const uint4 *>(p); }
 
 // LDS layout for NT tokens of K: qs [NT][K] i8 | bsums [NT][K/16] i16 (Q8K) | d [NT][K/blk] f32.
+// Within a token, 16-byte chunks are permuted inside aligned groups of four (K-quants; two for
+// A8) so that the chunks consecutive lanes read in one instruction fall in different banks.
 __host__ __device__ inline uint32_t mv_lds_bytes(int nt, uint32_t K, bool kq) {
     return nt * K + (kq ? nt * K / 8 : 0) + nt * (K / (kq ? 256 : 32)) * 4;
+}
+
+template <uint32_t MASK> __device__ __forceinline__ uint32_t swz(uint32_t c) {
+    return c ^ (((c >> 3) ^ (c >> 4)) & MASK);
 }
 
 // Activations staged in LDS.
@@ -71,7 +82,9 @@ struct RowRef {
 };
 
 // ---------------------------------------------------------------------------------------------
-// Per-format unit load and unit dot. units(K) = work units per row.
+// Per-format pieces. units(K): work units per row. lds_chunk / bs_index: LDS position of the
+// natural 16-B activation chunk / bsum within a token. W: one unit of weights, AU: the matching
+// activations. dot: one unit against one token.
 // ---------------------------------------------------------------------------------------------
 
 template <int T> struct MvFmt;
@@ -79,63 +92,113 @@ template <int T> struct MvFmt;
 template <> struct MvFmt<HKHIP_Q4_K> {
     static constexpr bool kq = true;
     __device__ static uint32_t units(uint32_t K) { return K / 64; }
+    __device__ static uint32_t lds_chunk(uint32_t c) { return swz<3>(c); }
+    __device__ static uint32_t bs_index(uint32_t g) { return g; }
     struct W {
         uint4 h, q0, q1;
     };
+    struct AU {
+        uint32_t q[16];
+        int b01, b23;
+        float d;
+    };
     __device__ static RowRef row(const uint8_t *w, const uint16_t *, uint32_t r, uint32_t K) {
         return RowRef{w + uint64_t(r) * (K / 256) * 144, nullptr};
+    }
+    // Offset in the token of the j-th 16-value chunk of unit u (natural order; chunks ascend in j).
+    __device__ static uint32_t chunk_off(uint32_t u, uint32_t j) { return 64 * u + 16 * j; }
+    __device__ static AU make(const uint32_t *q, const int *bs, float d) {
+        AU a;
+#pragma unroll
+        for (int i = 0; i < 16; i++) a.q[i] = q[i];
+        a.b01 = bs[0] + bs[1];
+        a.b23 = bs[2] + bs[3];
+        a.d = d;
+        return a;
     }
     __device__ static W load(const RowRef &R, uint32_t u) {
         const uint8_t *blk = R.w + (u >> 2) * 144;
         return W{ldw(blk), ldw(blk + 16 + 32 * (u & 3)), ldw(blk + 32 + 32 * (u & 3))};
     }
-    template <int NT>
-    __device__ static void dot(const W &w, uint32_t u, const ActL &A, float *acc, float *corr) {
-        const uint32_t sb = u >> 2, q = u & 3, K = A.K, nsb = K / 256;
+    // Unit u = quarter q of super-block sb: activation bytes 64q..64q+63, bsums 4q..4q+3.
+    __device__ static AU act(const ActL &A, uint32_t t, uint32_t u) {
+        const uint32_t base = t * (A.K / 16);
+        AU a;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint4 v = ldw(A.qs + 16 * (base + swz<3>(4 * u + j)));
+            a.q[4 * j] = v.x; a.q[4 * j + 1] = v.y; a.q[4 * j + 2] = v.z; a.q[4 * j + 3] = v.w;
+        }
+        const uint2 b = *reinterpret_cast<const uint2 *>(A.bs + base + 4 * u);
+        a.b01 = int(int16_t(b.x & 0xFFFF)) + int(int16_t(b.x >> 16));
+        a.b23 = int(int16_t(b.y & 0xFFFF)) + int(int16_t(b.y >> 16));
+        a.d = A.d[t * (A.K / 256) + (u >> 2)];
+        return a;
+    }
+    __device__ static void dot(const W &w, uint32_t u, const AU &a, float &acc, float &corr) {
+        const uint32_t q = u & 3;
         const uint4 h = w.h;
         // scalesMinsK4 word unpack (vecdot.zig:461-474), then sub-blocks 2q and 2q+1.
         const uint32_t k1 = 0x3f3f3f3fu, k2 = 0x0f0f0f0fu, k3 = 0x03030303u;
-        const uint32_t mn_hi = ((h.w >> 4) & k2) | (((h.z >> 6) & k3) << 4);
-        const uint32_t mn_lo = h.z & k1;
-        const uint32_t sc_hi = (h.w & k2) | (((h.y >> 6) & k3) << 4);
-        const uint32_t sc_lo = h.y & k1;
         const uint32_t sh = 16 * (q & 1);
-        const uint32_t scw = ((q < 2) ? sc_lo : sc_hi) >> sh, mnw = ((q < 2) ? mn_lo : mn_hi) >> sh;
-        const int sc0 = scw & 0xFF, sc1 = (scw >> 8) & 0xFF, mn0 = mnw & 0xFF, mn1 = (mnw >> 8) & 0xFF;
-        const float d = f16_bits_to_f32(h.x & 0xFFFF), dmin = f16_bits_to_f32(h.x >> 16);
-        const uint32_t qw[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
-#pragma unroll
-        for (int t = 0; t < NT; t++) {
-            const int8_t *aq = A.qs + t * K + sb * 256 + 64 * q;
-            const uint4 a0 = ldw(aq), a1 = ldw(aq + 16), a2 = ldw(aq + 32), a3 = ldw(aq + 48);
-            const uint32_t aw[16] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w,
-                                     a2.x, a2.y, a2.z, a2.w, a3.x, a3.y, a3.z, a3.w};
-            int slo = 0, shi = 0;
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                slo = sdot4(qw[i] & 0x0F0F0F0Fu, aw[i], slo);
-                shi = sdot4((qw[i] >> 4) & 0x0F0F0F0Fu, aw[8 + i], shi);
-            }
-            const uint2 bsw = *reinterpret_cast<const uint2 *>(A.bs + t * (K / 16) + sb * 16 + 4 * q);
-            const int b01 = int(int16_t(bsw.x & 0xFFFF)) + int(int16_t(bsw.x >> 16));
-            const int b23 = int(int16_t(bsw.y & 0xFFFF)) + int(int16_t(bsw.y >> 16));
-            const float ad = A.d[t * nsb + sb];
-            acc[t] = fmaf((float)(slo * sc0 + shi * sc1), d * ad, acc[t]);
-            corr[t] = fmaf((float)(mn0 * b01 + mn1 * b23), dmin * ad, corr[t]);
+        uint32_t scw, mnw;
+        if (q < 2) {
+            scw = (h.y & k1) >> sh;
+            mnw = (h.z & k1) >> sh;
+        } else {
+            scw = ((h.w & k2) | (((h.y >> 6) & k3) << 4)) >> sh;
+            mnw = (((h.w >> 4) & k2) | (((h.z >> 6) & k3) << 4)) >> sh;
         }
+        const int sc0 = scw & 0xFF, sc1 = (scw >> 8) & 0xFF, mn0 = mnw & 0xFF, mn1 = (mnw >> 8) & 0xFF;
+        const uint32_t qw[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
+        int slo = 0, shi = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            slo = sdot4(qw[i] & 0x0F0F0F0Fu, a.q[i], slo);
+            shi = sdot4((qw[i] >> 4) & 0x0F0F0F0Fu, a.q[8 + i], shi);
+        }
+        const float d = f16_bits_to_f32(h.x & 0xFFFF), dmin = f16_bits_to_f32(h.x >> 16);
+        acc = fmaf((float)(slo * sc0 + shi * sc1), d * a.d, acc);
+        corr = fmaf((float)(mn0 * a.b01 + mn1 * a.b23), dmin * a.d, corr);
     }
 };
 
 template <> struct MvFmt<HKHIP_Q6_K> {
     static constexpr bool kq = true;
     __device__ static uint32_t units(uint32_t K) { return K / 64; }
+    // Unit-major within a super-block: the 64 bytes (and 4 bsums) one unit reads are contiguous.
+    // Natural chunk m (values 16m..16m+15) is segment p = (m >> 1) & 3 of unit (n = m >> 3,
+    // lc = m & 1), unit index 2n + lc.
+    __device__ static uint32_t unit_major(uint32_t c) {
+        const uint32_t m = c & 15;
+        return (c & ~15u) + 4 * (2 * (m >> 3) + (m & 1)) + ((m >> 1) & 3);
+    }
+    __device__ static uint32_t lds_chunk(uint32_t c) { return swz<3>(unit_major(c)); }
+    __device__ static uint32_t bs_index(uint32_t g) { return unit_major(g); }
     struct W {
         uint4 l0, l1, hh;
         uint2 sc;
         uint32_t d;
     };
+    struct AU {
+        uint32_t q[16];
+        int bs[4];
+        float d;
+    };
     __device__ static RowRef row(const uint8_t *w, const uint16_t *ws, uint32_t r, uint32_t K) {
         return RowRef{w + uint64_t(r) * (K / 256) * 208, ws + uint64_t(r) * (K / 256)};
+    }
+    __device__ static uint32_t chunk_off(uint32_t u, uint32_t j) {
+        return 256 * (u >> 2) + 128 * ((u >> 1) & 1) + 16 * (u & 1) + 32 * j;
+    }
+    __device__ static AU make(const uint32_t *q, const int *bs, float d) {
+        AU a;
+#pragma unroll
+        for (int i = 0; i < 16; i++) a.q[i] = q[i];
+#pragma unroll
+        for (int i = 0; i < 4; i++) a.bs[i] = bs[i];
+        a.d = d;
+        return a;
     }
     __device__ static W load(const RowRef &R, uint32_t u) {
         const uint32_t n = (u >> 1) & 1, lc = u & 1;
@@ -148,41 +211,45 @@ template <> struct MvFmt<HKHIP_Q6_K> {
         w.d = R.ws[u >> 2];
         return w;
     }
-    template <int NT>
-    __device__ static void dot(const W &w, uint32_t u, const ActL &A, float *acc, float *) {
-        const uint32_t sb = u >> 2, n = (u >> 1) & 1, lc = u & 1, K = A.K, nsb = K / 256;
+    // Unit u = (sb, n, lc): activations 128n + 32p + 16lc + i (p < 4, i < 16), groups 8n + 2p + lc.
+    __device__ static AU act(const ActL &A, uint32_t t, uint32_t u) {
+        const uint32_t base = t * (A.K / 16);
+        AU a;
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const uint4 v = ldw(A.qs + 16 * (base + swz<3>(4 * u + p)));
+            a.q[4 * p] = v.x; a.q[4 * p + 1] = v.y; a.q[4 * p + 2] = v.z; a.q[4 * p + 3] = v.w;
+        }
+        const uint2 b = *reinterpret_cast<const uint2 *>(A.bs + base + 4 * u);
+        a.bs[0] = int16_t(b.x & 0xFFFF);
+        a.bs[1] = int16_t(b.x >> 16);
+        a.bs[2] = int16_t(b.y & 0xFFFF);
+        a.bs[3] = int16_t(b.y >> 16);
+        a.d = A.d[t * (A.K / 256) + (u >> 2)];
+        return a;
+    }
+    __device__ static void dot(const W &w, uint32_t u, const AU &a, float &acc, float &) {
+        const uint32_t lc = u & 1;
         const int sc[4] = {int8_t(w.sc.x >> (8 * lc)), int8_t(w.sc.x >> (8 * lc + 16)),
                            int8_t(w.sc.y >> (8 * lc)), int8_t(w.sc.y >> (8 * lc + 16))};
         const uint32_t L0[4] = {w.l0.x, w.l0.y, w.l0.z, w.l0.w};
         const uint32_t L1[4] = {w.l1.x, w.l1.y, w.l1.z, w.l1.w};
         const uint32_t H[4] = {w.hh.x, w.hh.y, w.hh.z, w.hh.w};
-        uint32_t qv[4][4];
+        int s[4] = {0, 0, 0, 0};
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            qv[0][i] = (L0[i] & 0x0F0F0F0Fu) | ((H[i] & 0x03030303u) << 4);
-            qv[1][i] = (L1[i] & 0x0F0F0F0Fu) | (((H[i] >> 2) & 0x03030303u) << 4);
-            qv[2][i] = ((L0[i] >> 4) & 0x0F0F0F0Fu) | (((H[i] >> 4) & 0x03030303u) << 4);
-            qv[3][i] = ((L1[i] >> 4) & 0x0F0F0F0Fu) | (((H[i] >> 6) & 0x03030303u) << 4);
+            s[0] = sdot4((L0[i] & 0x0F0F0F0Fu) | ((H[i] & 0x03030303u) << 4), a.q[i], s[0]);
+            s[1] = sdot4((L1[i] & 0x0F0F0F0Fu) | (((H[i] >> 2) & 0x03030303u) << 4), a.q[4 + i], s[1]);
+            s[2] = sdot4(((L0[i] >> 4) & 0x0F0F0F0Fu) | (((H[i] >> 4) & 0x03030303u) << 4), a.q[8 + i], s[2]);
+            s[3] = sdot4(((L1[i] >> 4) & 0x0F0F0F0Fu) | (((H[i] >> 6) & 0x03030303u) << 4), a.q[12 + i], s[3]);
         }
-        const float d = f16_bits_to_f32(w.d);
+        int isum = 0, bias = 0;
 #pragma unroll
-        for (int t = 0; t < NT; t++) {
-            const int8_t *aq = A.qs + t * K + sb * 256 + 128 * n + 16 * lc;
-            const uint4 bsv = ldw(A.bs + t * (K / 16) + sb * 16 + 8 * n);
-            const uint32_t bw[4] = {bsv.x, bsv.y, bsv.z, bsv.w};
-            int isum = 0, bias = 0;
-#pragma unroll
-            for (int g = 0; g < 4; g++) {
-                const uint4 av = ldw(aq + 32 * g);
-                int s = sdot4(qv[g][0], av.x, 0);
-                s = sdot4(qv[g][1], av.y, s);
-                s = sdot4(qv[g][2], av.z, s);
-                s = sdot4(qv[g][3], av.w, s);
-                isum += s * sc[g];
-                bias += sc[g] * int(int16_t(bw[g] >> (16 * lc)));
-            }
-            acc[t] = fmaf((float)(isum - 32 * bias), d * A.d[t * nsb + sb], acc[t]);
+        for (int g = 0; g < 4; g++) {
+            isum += s[g] * sc[g];
+            bias += sc[g] * a.bs[g];
         }
+        acc = fmaf((float)(isum - 32 * bias), f16_bits_to_f32(w.d) * a.d, acc);
     }
 };
 
@@ -191,9 +258,15 @@ template <int T> struct MvLegacy {
     static constexpr bool kq = false;
     static constexpr uint32_t QB = (T == HKHIP_Q8_0) ? 32 : 16; // quant-plane bytes per block
     __device__ static uint32_t units(uint32_t K) { return K / 32; }
+    __device__ static uint32_t lds_chunk(uint32_t c) { return swz<1>(c); }
+    __device__ static uint32_t bs_index(uint32_t g) { return g; }
     struct W {
         uint4 x0, x1;
         uint32_t d;
+    };
+    struct AU {
+        uint32_t q[8];
+        float d;
     };
     __device__ static RowRef row(const uint8_t *w, const uint16_t *ws, uint32_t r, uint32_t K) {
         return RowRef{w + uint64_t(r) * (K / 32) * QB, ws + uint64_t(r) * (K / 32)};
@@ -205,8 +278,17 @@ template <int T> struct MvLegacy {
         w.d = R.ws[u];
         return w;
     }
-    template <int NT>
-    __device__ static void dot(const W &w, uint32_t u, const ActL &A, float *acc, float *) {
+    __device__ static AU act(const ActL &A, uint32_t t, uint32_t u) {
+        const uint32_t base = t * (A.K / 16);
+        const uint4 v0 = ldw(A.qs + 16 * (base + swz<1>(2 * u)));
+        const uint4 v1 = ldw(A.qs + 16 * (base + swz<1>(2 * u + 1)));
+        AU a;
+        a.q[0] = v0.x; a.q[1] = v0.y; a.q[2] = v0.z; a.q[3] = v0.w;
+        a.q[4] = v1.x; a.q[5] = v1.y; a.q[6] = v1.z; a.q[7] = v1.w;
+        a.d = A.d[t * (A.K / 32) + u];
+        return a;
+    }
+    __device__ static void dot(const W &w, uint32_t, const AU &a, float &acc, float &) {
         uint32_t qw[8];
         if constexpr (T == HKHIP_Q8_0) {
             qw[0] = w.x0.x; qw[1] = w.x0.y; qw[2] = w.x0.z; qw[3] = w.x0.w;
@@ -219,242 +301,522 @@ template <int T> struct MvLegacy {
                 qw[4 + i] = iq4nl_lookup4((n4[i] >> 4) & 0x0F0F0F0Fu);
             }
         }
-        const float d = f16_bits_to_f32(w.d);
-        const uint32_t K = A.K, U = K / 32;
+        int s = 0;
 #pragma unroll
-        for (int t = 0; t < NT; t++) {
-            const int8_t *aq = A.qs + t * K + 32 * u;
-            const uint4 a0 = ldw(aq), a1 = ldw(aq + 16);
-            int s = sdot4(qw[0], a0.x, 0);
-            s = sdot4(qw[1], a0.y, s);
-            s = sdot4(qw[2], a0.z, s);
-            s = sdot4(qw[3], a0.w, s);
-            s = sdot4(qw[4], a1.x, s);
-            s = sdot4(qw[5], a1.y, s);
-            s = sdot4(qw[6], a1.z, s);
-            s = sdot4(qw[7], a1.w, s);
-            acc[t] = fmaf((float)s, d * A.d[t * U + u], acc[t]);
-        }
+        for (int i = 0; i < 8; i++) s = sdot4(qw[i], a.q[i], s);
+        acc = fmaf((float)s, f16_bits_to_f32(w.d) * a.d, acc);
     }
 };
 template <> struct MvFmt<HKHIP_Q8_0> : MvLegacy<HKHIP_Q8_0> {};
 template <> struct MvFmt<HKHIP_IQ4_NL> : MvLegacy<HKHIP_IQ4_NL> {};
 
 // ---------------------------------------------------------------------------------------------
-// Kernel
+// Shared pieces of the kernels
 // ---------------------------------------------------------------------------------------------
 
-template <int T, int NT>
-__global__ __launch_bounds__(256) void mmvq_kernel(MvArgs a) {
+
+// Sum over each aligned group of 2^lg lanes; every lane of the group gets the sum.
+__device__ __forceinline__ float group_sum(float v, uint32_t lg) {
+    if (lg >= 1) v += dpp_f<DPP_XOR1>(v);
+    if (lg >= 2) v += dpp_f<DPP_XOR2>(v);
+    if (lg >= 3) v += dpp_f<DPP_HALF_MIRROR>(v);
+    if (lg >= 4) v += dpp_f<DPP_MIRROR>(v);
+    if (lg == 5) v += __shfl_xor(v, 16);
+    if (lg == 6) v = (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
+    return v;
+}
+
+// Quantizes (or copies) the NT-token input into LDS. All NW waves take part; ends with a barrier.
+template <typename F, int NT, int NW>
+__device__ __forceinline__ void stage_acts(const MvArgs &a, int8_t *sqs, int16_t *sbs, float *sd) {
+    constexpr bool kq = F::kq;
+    constexpr uint32_t NTH = NW * 64;
+    const uint32_t K = a.K, kc = K / 16;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (a.x) {
+        if constexpr (kq) {
+            const uint32_t kb = K / 256, nblk = NT * kb;
+            // Every load of the first blocks first, then the reductions.
+            constexpr int PB = 2;
+            float4 xv[PB];
+#pragma unroll
+            for (int j = 0; j < PB; j++) {
+                const uint32_t b = wave + NW * j;
+                if (b < nblk) xv[j] = reinterpret_cast<const float4 *>(a.x + uint64_t(b) * 256)[lane];
+            }
+            auto put = [&](uint32_t b, const Q8KQ &qr) {
+                const uint32_t t = NT == 1 ? 0 : b / kb, sb = b - t * kb;
+                const uint32_t c = 16 * sb + (lane >> 2);
+                *reinterpret_cast<uint32_t *>(sqs + 16 * (t * kc + F::lds_chunk(c)) + 4 * (lane & 3)) = qr.packed;
+                if ((lane & 3) == 0) sbs[t * kc + F::bs_index(16 * sb + lane / 4)] = (int16_t)qr.bsum;
+                if (lane == 0) sd[b] = qr.d;
+            };
+#pragma unroll
+            for (int j = 0; j < PB; j++) {
+                const uint32_t b = wave + NW * j;
+                if (b < nblk) put(b, quant_q8k_wave(xv[j], lane));
+            }
+            for (uint32_t b = wave + NW * PB; b < nblk; b += NW)
+                put(b, quant_q8k_wave(reinterpret_cast<const float4 *>(a.x + uint64_t(b) * 256)[lane], lane));
+        } else {
+            const uint32_t ka = K / 32, nblk = NT * ka, hw = tid >> 5, hl = tid & 31;
+            // Both half-waves run every iteration (the quantizer needs the whole wave).
+            const uint32_t nb2 = (nblk + 2 * NW - 1) / (2 * NW) * (2 * NW);
+            constexpr int PB = 2;
+            float xs[PB];
+#pragma unroll
+            for (int j = 0; j < PB; j++) {
+                const uint32_t b = hw + 2 * NW * j;
+                xs[j] = b < nblk ? a.x[uint64_t(b) * 32 + hl] : 0.0f;
+            }
+            auto put = [&](uint32_t b, const A8Q &qr) {
+                const uint32_t t = NT == 1 ? 0 : b / ka, blk = b - t * ka;
+                sqs[16 * (t * kc + F::lds_chunk(2 * blk + (hl >> 4))) + (hl & 15)] = (int8_t)qr.q;
+                if (hl == 0) sd[b] = qr.d;
+            };
+#pragma unroll
+            for (int j = 0; j < PB; j++) {
+                if (2 * NW * j < nb2) {
+                    const A8Q qr = quant_a8_halfwave(xs[j]);
+                    const uint32_t b = hw + 2 * NW * j;
+                    if (b < nblk) put(b, qr);
+                }
+            }
+            for (uint32_t b0 = 2 * NW * PB; b0 < nb2; b0 += 2 * NW) {
+                const uint32_t b = b0 + hw;
+                const A8Q qr = quant_a8_halfwave(b < nblk ? a.x[uint64_t(b) * 32 + hl] : 0.0f);
+                if (b < nblk) put(b, qr);
+            }
+        }
+    } else {
+        for (uint32_t i = tid; i < NT * kc; i += NTH) {
+            const uint32_t t = NT == 1 ? 0 : i / kc, c = i - t * kc;
+            reinterpret_cast<uint4 *>(sqs)[t * kc + F::lds_chunk(c)] = reinterpret_cast<const uint4 *>(a.gqs)[i];
+        }
+        const uint32_t nd = NT * (K / (kq ? 256 : 32));
+        for (uint32_t i = tid; i < nd; i += NTH) sd[i] = a.gd[i];
+        if constexpr (kq) {
+            for (uint32_t i = tid; i < NT * kc; i += NTH) {
+                const uint32_t t = NT == 1 ? 0 : i / kc, g = i - t * kc;
+                sbs[t * kc + F::bs_index(g)] = a.gbs[i];
+            }
+        }
+    }
+    __syncthreads();
+}
+
+#define MV_SEL(f) (p == 0 ? a.p[0].f : p == 1 ? a.p[1].f : p == 2 ? a.p[2].f : a.p[3].f)
+
+// The row group g of a wave: its part (the same for every lane), local row and row pointers.
+template <typename F>
+__device__ __forceinline__ RowRef mv_locate(const MvArgs &a, uint32_t g, uint32_t sub, uint32_t rpw, uint32_t &p,
+                                            uint32_t &r, bool &active) {
+    p = 0;
+#pragma unroll
+    for (int i = 1; i < MV_PARTS; i++)
+        if (i < int(a.nparts) && g >= a.p[i].gstart) p = i;
+    r = (g - MV_SEL(gstart)) * rpw + sub;
+    active = r < MV_SEL(rows);
+    return F::row(MV_SEL(w), MV_SEL(ws), active ? r : 0, a.K);
+}
+
+template <int NT>
+__device__ __forceinline__ void mv_store(const MvArgs &a, uint32_t p, uint32_t r, const float *acc) {
+    float *y = MV_SEL(y);
+    const float *bias = MV_SEL(bias);
+    const uint32_t rows = MV_SEL(rows);
+    const float b = bias ? bias[r] : 0.0f;
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        float *dst = y + uint64_t(t) * rows + r;
+        if (a.mode == HKHIP_ACCUMULATE)
+            *dst += acc[t] + b;
+        else
+            *dst = acc[t] + b;
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// General kernel: NT tokens, rows of any length (steps of UNR units per lane), activations from
+// LDS.
+// ---------------------------------------------------------------------------------------------
+
+template <int T, int NT, int NW, int UNR>
+__global__ __launch_bounds__(NW * 64) void mmvq_kernel(MvArgs a) {
     using F = MvFmt<T>;
+    using W = typename F::W;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     constexpr bool kq = F::kq;
     const uint32_t K = a.K;
     int8_t *sqs = reinterpret_cast<int8_t *>(smem);
     int16_t *sbs = reinterpret_cast<int16_t *>(smem + NT * K);
     float *sd = reinterpret_cast<float *>(smem + NT * K + (kq ? NT * K / 8 : 0));
-    const ActL act{sqs, sbs, sd, K};
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t lg = a.lpr_log2, lpr = 1u << lg, rpw = 64u >> lg;
     const uint32_t sub = lane >> lg, ul = lane & (lpr - 1);
-    const uint32_t groups = (a.total_rows + rpw - 1) / rpw;
     const uint32_t U = F::units(K);
-    const uint32_t stride = gridDim.x * 4;
+    const uint32_t step_units = UNR * lpr;
+    const uint32_t nch = (U + step_units - 1) / step_units; // steps per row
+    const uint32_t nwaves = gridDim.x * NW, wid = blockIdx.x * NW + wave;
+    const uint32_t g0 = uint32_t(uint64_t(a.ngroups) * wid / nwaves);
+    const uint32_t g1 = uint32_t(uint64_t(a.ngroups) * (wid + 1) / nwaves);
 
-    // Row of this lane in group g: its part, local row and row pointers.
-    auto locate = [&](uint32_t g, uint32_t &p, uint32_t &r, bool &active) -> RowRef {
-        const uint32_t grow = g * rpw + sub;
-        active = g < groups && grow < a.total_rows;
-        p = 0;
-#pragma unroll
-        for (int i = 1; i < MV_PARTS; i++)
-            if (i < int(a.nparts) && grow >= a.p[i].row0) p = i;
-#define SEL(f) (p == 0 ? a.p[0].f : p == 1 ? a.p[1].f : p == 2 ? a.p[2].f : a.p[3].f)
-        r = active ? grow - SEL(row0) : 0;
-        return F::row(SEL(w), SEL(ws), r, K);
-#undef SEL
-    };
+    stage_acts<F, NT, NW>(a, sqs, sbs, sd);
+    const ActL act{sqs, sbs, sd, K};
 
-    typename F::W wv[MV_UNROLL];
-    auto load_chunk = [&](const RowRef &R, bool active, uint32_t base) {
+    float acc[NT], corr[NT];
 #pragma unroll
-        for (int c = 0; c < MV_UNROLL; c++) {
+    for (int t = 0; t < NT; t++) acc[t] = corr[t] = 0.0f;
+    W wa[UNR], wb[UNR];
+    auto load = [&](W *w, uint32_t g, uint32_t ch) {
+        uint32_t p, r;
+        bool active;
+        const RowRef R = mv_locate<F>(a, g, sub, rpw, p, r, active);
+        const uint32_t base = ul + ch * step_units;
+#pragma unroll
+        for (int c = 0; c < UNR; c++) {
             const uint32_t u = base + c * lpr;
-            if (active && u < U) wv[c] = F::load(R, u);
+            if (active && u < U) w[c] = F::load(R, u);
         }
     };
-
-    const uint32_t g0 = blockIdx.x * 4 + wave;
-    uint32_t p, r;
-    bool active;
-    RowRef R = locate(g0, p, r, active);
-
-    // Order of the memory traffic: the first batch of activation loads, then this wave's first
-    // weight loads, then the activation work. Loads complete in issue order, so the activation
-    // data can be used while the weight bytes are still in flight.
-    constexpr int PB = 4; // activation loads per lane in the first batch
-    float4 xv[PB];        // Q8K: one float4 of a block per lane
-    float xs[PB];         // A8:  one value of a block per lane
-    uint4 qv[PB];         // prepared input: 16 B of qs per thread
-    if (a.x) {
-        if constexpr (kq) {
-            const uint32_t nblk = NT * K / 256;
+    auto compute = [&](const W *w, uint32_t g, uint32_t ch) {
+        uint32_t p, r;
+        bool active;
+        (void)mv_locate<F>(a, g, sub, rpw, p, r, active);
+        const uint32_t base = ul + ch * step_units;
+        if (active) {
 #pragma unroll
-            for (int j = 0; j < PB; j++) {
-                const uint32_t b = wave + 4 * j;
-                if (b < nblk) xv[j] = reinterpret_cast<const float4 *>(a.x + uint64_t(b) * 256)[lane];
-            }
-        } else {
-            const uint32_t nblk = NT * K / 32, hw = tid >> 5, hl = tid & 31;
-#pragma unroll
-            for (int j = 0; j < PB; j++) {
-                const uint32_t b = hw + 8 * j;
-                xs[j] = b < nblk ? a.x[uint64_t(b) * 32 + hl] : 0.0f;
-            }
-        }
-    } else {
-#pragma unroll
-        for (int j = 0; j < PB; j++) {
-            const uint32_t i = tid + 256 * j;
-            if (i < NT * K / 16) qv[j] = reinterpret_cast<const uint4 *>(a.gqs)[i];
-        }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    load_chunk(R, active, ul);
-    __builtin_amdgcn_sched_barrier(0);
-
-    // ---- activations into LDS ----
-#ifdef HKHIP_MV_PROBE_NO_PROLOGUE
-    if (false) {
-#else
-    if (a.x) {
-#endif
-        if constexpr (kq) {
-            const uint32_t nblk = NT * K / 256;
-#pragma unroll
-            for (int j = 0; j < PB; j++) {
-                const uint32_t b = wave + 4 * j;
-                if (b < nblk) {
-                    const Q8KQ qr = quant_q8k_wave(xv[j], lane);
-                    reinterpret_cast<uint32_t *>(sqs + b * 256)[lane] = qr.packed;
-                    if ((lane & 3) == 0) sbs[b * 16 + lane / 4] = (int16_t)qr.bsum;
-                    if (lane == 0) sd[b] = qr.d;
-                }
-            }
-            for (uint32_t b = wave + 4 * PB; b < nblk; b += 4) {
-                const Q8KQ qr = quant_q8k_wave(reinterpret_cast<const float4 *>(a.x + uint64_t(b) * 256)[lane], lane);
-                reinterpret_cast<uint32_t *>(sqs + b * 256)[lane] = qr.packed;
-                if ((lane & 3) == 0) sbs[b * 16 + lane / 4] = (int16_t)qr.bsum;
-                if (lane == 0) sd[b] = qr.d;
-            }
-        } else {
-            const uint32_t nblk = NT * K / 32, hw = tid >> 5, hl = tid & 31;
-            // Both half-waves run every iteration (the quantizer needs the whole wave).
-            const uint32_t nb2 = (nblk + 7) / 8 * 8;
-#pragma unroll
-            for (int j = 0; j < PB; j++) {
-                const uint32_t b = hw + 8 * j;
-                if (8 * j < nb2) {
-                    const A8Q qr = quant_a8_halfwave(xs[j]);
-                    if (b < nblk) {
-                        sqs[b * 32 + hl] = (int8_t)qr.q;
-                        if (hl == 0) sd[b] = qr.d;
-                    }
-                }
-            }
-            for (uint32_t b0 = 8 * PB; b0 < nb2; b0 += 8) {
-                const uint32_t b = b0 + hw;
-                const A8Q qr = quant_a8_halfwave(b < nblk ? a.x[uint64_t(b) * 32 + hl] : 0.0f);
-                if (b < nblk) {
-                    sqs[b * 32 + hl] = (int8_t)qr.q;
-                    if (hl == 0) sd[b] = qr.d;
-                }
-            }
-        }
-    } else
-#ifdef HKHIP_MV_PROBE_NO_PROLOGUE
-    if (false)
-#endif
-    {
-#pragma unroll
-        for (int j = 0; j < PB; j++) {
-            const uint32_t i = tid + 256 * j;
-            if (i < NT * K / 16) reinterpret_cast<uint4 *>(sqs)[i] = qv[j];
-        }
-        for (uint32_t i = tid + 256 * PB; i < NT * K / 16; i += 256)
-            reinterpret_cast<uint4 *>(sqs)[i] = reinterpret_cast<const uint4 *>(a.gqs)[i];
-        const uint32_t nd = NT * (K / (kq ? 256 : 32));
-        for (uint32_t i = tid; i < nd; i += 256) sd[i] = a.gd[i];
-        if constexpr (kq)
-            for (uint32_t i = tid; i < NT * K / 32; i += 256)
-                reinterpret_cast<uint32_t *>(sbs)[i] = reinterpret_cast<const uint32_t *>(a.gbs)[i];
-    }
-#ifndef HKHIP_MV_PROBE_NO_PROLOGUE
-    __syncthreads();
-#endif
-
-    // ---- rows ----
-    for (uint32_t g = g0; g < groups; g += stride) {
-        if (g != g0) {
-            R = locate(g, p, r, active);
-            load_chunk(R, active, ul);
-        }
-        float acc[NT], corr[NT];
-#pragma unroll
-        for (int t = 0; t < NT; t++) acc[t] = corr[t] = 0.0f;
-        for (uint32_t base = ul; active && base < U;) {
-#pragma unroll
-            for (int c = 0; c < MV_UNROLL; c++) {
+            for (int c = 0; c < UNR; c++) {
                 const uint32_t u = base + c * lpr;
-#ifdef HKHIP_MV_PROBE_LOADS_ONLY
                 if (u < U) {
-                    uint32_t xr = 0;
-                    for (uint32_t i = 0; i < sizeof(wv[c]) / 4; i++) xr ^= reinterpret_cast<const uint32_t *>(&wv[c])[i];
-                    acc[0] += __builtin_bit_cast(float, xr & 1u);
+#pragma unroll
+                    for (int t = 0; t < NT; t++) F::dot(w[c], u, F::act(act, t, u), acc[t], corr[t]);
                 }
-#else
-                if (u < U) F::template dot<NT>(wv[c], u, act, acc, corr);
-#endif
             }
-            base += MV_UNROLL * lpr;
-            if (base < U) load_chunk(R, active, base);
         }
+        if (ch + 1 < nch) return;
+        float v[NT];
 #pragma unroll
         for (int t = 0; t < NT; t++) {
-            float v = acc[t] - corr[t];
-            for (uint32_t off = lpr >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off);
-            acc[t] = v;
+            v[t] = group_sum(acc[t] - corr[t], lg);
+            acc[t] = corr[t] = 0.0f;
         }
-        if (active && ul == 0) {
-            float *y = p == 0 ? a.p[0].y : p == 1 ? a.p[1].y : p == 2 ? a.p[2].y : a.p[3].y;
-            const float *bias = p == 0 ? a.p[0].bias : p == 1 ? a.p[1].bias : p == 2 ? a.p[2].bias : a.p[3].bias;
-            const uint32_t rows = p == 0 ? a.p[0].rows : p == 1 ? a.p[1].rows : p == 2 ? a.p[2].rows : a.p[3].rows;
-            const float b = bias ? bias[r] : 0.0f;
+        if (active && ul == 0) mv_store<NT>(a, p, r, v);
+    };
+    // Steps in order (g, ch); the next step's weights load while this one computes.
+    uint32_t g = g0, ch = 0;
+    if (g < g1) load(wa, g, ch);
+    while (g < g1) {
+        uint32_t gn = g, cn = ch + 1;
+        if (cn == nch) {
+            gn++;
+            cn = 0;
+        }
+        if (gn < g1) load(wb, gn, cn);
+        compute(wa, g, ch);
+        if (gn >= g1) break;
+        uint32_t g2 = gn, c2 = cn + 1;
+        if (c2 == nch) {
+            g2++;
+            c2 = 0;
+        }
+        if (g2 < g1) load(wa, g2, c2);
+        compute(wb, gn, cn);
+        g = g2;
+        ch = c2;
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Register kernel: lane l of every wave owns units l, l+64, ... (C of them) of every row, and
+// keeps their activations for all NT tokens in registers. A wave streams a contiguous range of
+// whole rows, R rows per step, so row addresses are wave-uniform (scalar) and each activation
+// register is reused for every row. There is no LDS and no barrier: the first step's weight
+// loads are issued before the activations are read, and an f32 input is quantized by the lanes
+// themselves (a Q8K super-block is four consecutive units, i.e. four neighbouring lanes).
+// ---------------------------------------------------------------------------------------------
+
+// Unit u of token t from quantized activations in the engine's layout (global memory or LDS):
+// qs [n][K] int8, bs [n][K/16] int16 (Q8K), d [n][K/256] (Q8K) or [n][K/32] (A8) f32.
+template <typename F>
+__device__ __forceinline__ typename F::AU load_unit(const int8_t *gqs, const int16_t *gbs, const float *gd, uint32_t K,
+                                                    uint32_t t, uint32_t u) {
+    typename F::AU au;
+    if constexpr (F::kq) {
+        const int8_t *qs = gqs + uint64_t(t) * K;
+        uint32_t q[16];
+        int bs[4];
 #pragma unroll
-            for (int t = 0; t < NT; t++) {
-                float *dst = y + uint64_t(t) * rows + r;
-                if (a.mode == HKHIP_ACCUMULATE)
-                    *dst += acc[t] + b;
-                else
-                    *dst = acc[t] + b;
-            }
+        for (int j = 0; j < 4; j++) {
+            const uint32_t off = F::chunk_off(u, j);
+            const uint4 v = ldw(qs + off);
+            q[4 * j] = v.x; q[4 * j + 1] = v.y; q[4 * j + 2] = v.z; q[4 * j + 3] = v.w;
+            bs[j] = gbs[uint64_t(t) * (K / 16) + off / 16];
+        }
+        au = F::make(q, bs, gd[t * (K / 256) + (u >> 2)]);
+    } else {
+        const int8_t *qs = gqs + uint64_t(t) * K + 32 * u;
+        const uint4 v0 = ldw(qs), v1 = ldw(qs + 16);
+        au.q[0] = v0.x; au.q[1] = v0.y; au.q[2] = v0.z; au.q[3] = v0.w;
+        au.q[4] = v1.x; au.q[5] = v1.y; au.q[6] = v1.z; au.q[7] = v1.w;
+        au.d = gd[t * (K / 32) + u];
+    }
+    return au;
+}
+
+// A8 quantization of 256 values per wave, four consecutive values per lane (lane l holds
+// 4l..4l+3, so one block of 32 is eight lanes). Returns this lane's four bytes; d is the block's.
+__device__ __forceinline__ uint32_t quant_a8_oct(float4 v4, float &d) {
+    const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+    float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    m = fmaxf(m, dpp_f<DPP_XOR1>(m));
+    m = fmaxf(m, dpp_f<DPP_XOR2>(m));
+    m = fmaxf(m, dpp_f<DPP_HALF_MIRROR>(m));
+    d = __fdiv_rn(m, 127.0f);
+    const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+    uint32_t pk = 0;
+#pragma unroll
+    for (int b = 0; b < 4; b++) pk |= uint32_t(uint8_t((int)roundf(v[b] * id))) << (8 * b);
+    return pk;
+}
+
+// Bytes of LDS the register kernel uses to stage an f32 input of nt tokens.
+__host__ __device__ inline uint32_t mvr_lds_bytes(int nt, uint32_t K, bool kq) {
+    return nt * K + (kq ? nt * K / 8 + nt * (K / 256) * 4 : nt * (K / 32) * 4);
+}
+
+// Quantizes one 256-value block b (of token-major input x) with a whole wave and writes it to
+// the LDS staging area in the engine's activation layout.
+template <typename F>
+__device__ __forceinline__ void mvr_stage_block(float4 v, uint32_t b, bool valid, int8_t *sqs, int16_t *sbs,
+                                                float *sd) {
+    const uint32_t lane = __lane_id();
+    if constexpr (F::kq) {
+        const Q8KQ qr = quant_q8k_wave(v, lane);
+        *reinterpret_cast<uint32_t *>(sqs + 256 * b + 4 * lane) = qr.packed;
+        if ((lane & 3) == 0) sbs[16 * b + lane / 4] = (int16_t)qr.bsum;
+        if (lane == 0) sd[b] = qr.d;
+    } else {
+        float d;
+        const uint32_t pk = quant_a8_oct(v, d);
+        if (valid) {
+            *reinterpret_cast<uint32_t *>(sqs + 256 * b + 4 * lane) = pk;
+            if ((lane & 7) == 0) sd[8 * b + lane / 8] = d;
         }
     }
 }
 
+#ifndef MVR_MINW
+#define MVR_MINW 1
+#endif
+template <int T, int NT, int C, int R, int NW>
+__global__ __launch_bounds__(NW * 64, MVR_MINW) void mmvr_kernel(MvArgs a) {
+    using F = MvFmt<T>;
+    using W = typename F::W;
+    using AU = typename F::AU;
+    const uint32_t K = a.K;
+    const uint32_t lane = __lane_id();
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t U = F::units(K);
+    const uint32_t nwaves = gridDim.x * NW, wid = blockIdx.x * NW + wave;
+    const uint32_t total = a.ngroups; // rows of all parts
+    const uint32_t r0 = uint32_t(uint64_t(total) * wid / nwaves);
+    const uint32_t r1 = uint32_t(uint64_t(total) * (wid + 1) / nwaves);
+    // A wave without rows still helps stage the input (and reaches the barrier).
+    const uint32_t rlast = r0 < r1 ? r1 - 1 : 0;
+
+    // Row r of the concatenated parts: its part. Fields are copied member by member so the
+    // argument block is never indexed dynamically (which would move it to scratch).
+    auto locate = [&](uint32_t r) -> MvPart {
+        MvPart q = a.p[0];
+#pragma unroll
+        for (int i = 1; i < MV_PARTS; i++) {
+            if (i < int(a.nparts) && r >= a.p[i].gstart) {
+                q.w = a.p[i].w;
+                q.ws = a.p[i].ws;
+                q.y = a.p[i].y;
+                q.bias = a.p[i].bias;
+                q.rows = a.p[i].rows;
+                q.gstart = a.p[i].gstart;
+            }
+        }
+        return q;
+    };
+    // Every step issues the same loads, with rows past the range and units past the row clamped
+    // to valid ones, and no other global load happens until the final stores: the compiler can
+    // then wait for exactly the older step while the newer one stays in flight (the memory
+    // counter is in order, so any later load that is waited on would drain the prefetch too).
+    W wa[R][C], wb[R][C];
+    auto load = [&](W (*w)[C], uint32_t rb) {
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            const uint32_t r = rb + i < r1 ? rb + i : rlast;
+            const MvPart q = locate(r);
+            const RowRef RR = F::row(q.w, q.ws, r - q.gstart, K);
+#pragma unroll
+            for (int c = 0; c < C; c++) {
+                const uint32_t u = lane + 64 * c;
+                w[i][c] = F::load(RR, u < U ? u : U - 1);
+            }
+        }
+    };
+    // Activations. An f32 input is quantized once per workgroup into LDS: its first blocks are
+    // loaded before any weight, so quantizing them waits only for them (the memory counter is
+    // in order), and the weights of the first two steps stream in meanwhile. A quantized input
+    // is read by each lane directly, also ahead of the weights.
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    constexpr int PB = 2;
+    const uint32_t ntok = NT == 1 ? 1u : a.ntok;
+    const uint32_t nflat = ntok * K, nblk = (nflat + 255) / 256;
+    float4 xv[PB];
+    AU au[NT][C];
+    if (a.x) {
+#pragma unroll
+        for (int j = 0; j < PB; j++) {
+            const uint32_t b = wave + NW * j, e = 256 * b + 4 * lane;
+            xv[j] = (b < nblk && e < nflat) ? *reinterpret_cast<const float4 *>(a.x + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    } else {
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            if (NT > 1 && uint32_t(t) >= a.ntok) break;
+#pragma unroll
+            for (int c = 0; c < C; c++) {
+                const uint32_t u = lane + 64 * c;
+                au[t][c] = load_unit<F>(a.gqs, a.gbs, a.gd, K, t, u < U ? u : U - 1);
+            }
+        }
+    }
+    load(wa, r0);
+    load(wb, r0 + R);
+    if (a.x) {
+        int8_t *sqs = reinterpret_cast<int8_t *>(smem);
+        int16_t *sbs = reinterpret_cast<int16_t *>(smem + nflat);
+        float *sd = reinterpret_cast<float *>(smem + nflat + (F::kq ? nflat / 8 : 0));
+#pragma unroll
+        for (int j = 0; j < PB; j++) {
+            const uint32_t b = wave + NW * j;
+            if (b < nblk) mvr_stage_block<F>(xv[j], b, 256 * b + 4 * lane < nflat, sqs, sbs, sd);
+        }
+        for (uint32_t b = wave + NW * PB; b < nblk; b += NW) {
+            const uint32_t e = 256 * b + 4 * lane;
+            const float4 v = e < nflat ? *reinterpret_cast<const float4 *>(a.x + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+            mvr_stage_block<F>(v, b, e < nflat, sqs, sbs, sd);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            if (NT > 1 && uint32_t(t) >= a.ntok) break;
+#pragma unroll
+            for (int c = 0; c < C; c++) {
+                const uint32_t u = lane + 64 * c;
+                au[t][c] = load_unit<F>(sqs, sbs, sd, K, t, u < U ? u : U - 1);
+            }
+        }
+    }
+
+    // Activation loads were issued after the first two steps of weights; waiting for all of
+    // them here (the first step is needed next anyway) leaves nothing older than a prefetch
+    // pending inside the loop. 0x0F70 = vmcnt(0), expcnt and lgkmcnt unconstrained.
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+
+    // Lane j keeps the results of row fbase + j until they are stored, 64 rows at a time.
+    float res[NT];
+    uint32_t fbase = r0;
+    auto flush = [&](uint32_t n) {
+        if (lane < n) {
+            const uint32_t r = fbase + lane;
+            MvPart q = a.p[0];
+#pragma unroll
+            for (int i = 1; i < MV_PARTS; i++) {
+                if (i < int(a.nparts) && r >= a.p[i].gstart) {
+                    q.y = a.p[i].y;
+                    q.bias = a.p[i].bias;
+                    q.rows = a.p[i].rows;
+                    q.gstart = a.p[i].gstart;
+                }
+            }
+            const uint32_t lr = r - q.gstart;
+            const float b = q.bias ? q.bias[lr] : 0.0f;
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                if (NT > 1 && uint32_t(t) >= a.ntok) break;
+                float *y = q.y + uint64_t(t) * q.rows + lr;
+                if (a.mode == HKHIP_ACCUMULATE)
+                    *y += res[t] + b;
+                else
+                    *y = res[t] + b;
+            }
+        }
+        fbase += n;
+    };
+    auto compute = [&](const W (*w)[C], uint32_t rb) {
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            if (rb + i >= r1) break;
+            float acc[NT], corr[NT];
+#pragma unroll
+            for (int t = 0; t < NT; t++) acc[t] = corr[t] = 0.0f;
+#pragma unroll
+            for (int c = 0; c < C; c++) {
+                const uint32_t u = lane + 64 * c;
+                if (u < U) {
+#pragma unroll
+                    for (int t = 0; t < NT; t++) {
+                        if (NT == 1 || uint32_t(t) < a.ntok) {
+#ifdef HKHIP_MV_PROBE_LOADS_ONLY
+                            uint32_t xr = 0;
+                            for (uint32_t k = 0; k < sizeof(W) / 4; k++) xr ^= reinterpret_cast<const uint32_t *>(&w[i][c])[k];
+                            acc[t] += __builtin_bit_cast(float, xr & 1u) + au[t][c].d;
+#else
+                            F::dot(w[i][c], u, au[t][c], acc[t], corr[t]);
+#endif
+                        }
+                    }
+                }
+            }
+            const uint32_t slot = rb + i - fbase;
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                const float v = group_sum(acc[t] - corr[t], 6);
+                if (lane == slot) res[t] = v;
+            }
+        }
+    };
+    const uint32_t ns = (r1 - r0 + R - 1) / R;
+    for (uint32_t s = 0; s < ns; s += 2) {
+        if (r0 + s * R - fbase == 64) flush(64);
+        compute(wa, r0 + s * R);
+        load(wa, r0 + (s + 2) * R);
+        if (s + 1 >= ns) break;
+        if (r0 + (s + 1) * R - fbase == 64) flush(64);
+        compute(wb, r0 + (s + 1) * R);
+        load(wb, r0 + (s + 3) * R);
+    }
+    flush(r1 - fbase);
+}
+
+#undef MV_SEL
+
+// ---------------------------------------------------------------------------------------------
+// Launch
+// ---------------------------------------------------------------------------------------------
+
 typedef void (*mv_kernel_t)(MvArgs);
+
+constexpr int MV_NW = 8, MV_UNR = 2;   // general kernel: 8 waves, 2 units per lane per step
 
 template <int T>
 static mv_kernel_t pick(int nt) {
     switch (nt) {
-    case 1: return mmvq_kernel<T, 1>;
-    case 2: return mmvq_kernel<T, 2>;
-    case 3: return mmvq_kernel<T, 3>;
-    case 4: return mmvq_kernel<T, 4>;
-    case 5: return mmvq_kernel<T, 5>;
-    case 6: return mmvq_kernel<T, 6>;
-    case 7: return mmvq_kernel<T, 7>;
-    case 8: return mmvq_kernel<T, 8>;
+    case 1: return mmvq_kernel<T, 1, MV_NW, MV_UNR>;
+    case 2: return mmvq_kernel<T, 2, MV_NW, MV_UNR>;
+    case 3: return mmvq_kernel<T, 3, MV_NW, MV_UNR>;
+    case 4: return mmvq_kernel<T, 4, MV_NW, MV_UNR>;
+    case 5: return mmvq_kernel<T, 5, MV_NW, MV_UNR>;
+    case 6: return mmvq_kernel<T, 6, MV_NW, MV_UNR>;
+    case 7: return mmvq_kernel<T, 7, MV_NW, MV_UNR>;
+    case 8: return mmvq_kernel<T, 8, MV_NW, MV_UNR>;
     default: return nullptr;
     }
 }
@@ -469,9 +831,74 @@ static mv_kernel_t kernel_for(int t, int nt) {
     }
 }
 
+
+// Register kernel variants: NT in {1, 2, 4, 8} (a launch of n tokens uses the smallest NT >= n),
+// C = units per lane (rows of at most 64*C units), R = rows per step. The activations of NT*C
+// units must fit the register file next to two steps of weights: NT*C <= 8 for Q4_K/Q6_K and
+// <= 16 for Q8_0/IQ4_NL; larger shapes use the LDS kernel.
+#ifndef MVR_NWAVES
+#define MVR_NWAVES 8
+#endif
+#ifndef MVR_R1
+#define MVR_R1 2
+#endif
+__host__ __device__ constexpr int mvr_rows(int nt, int c) { return nt == 1 ? (c >= MVR_R1 ? 1 : MVR_R1 / c) : (c >= 2 ? 1 : 2); }
+// Largest C per (format, NT): the activations of NT*C units must fit the register file next to
+// two steps of weights.
+__host__ __device__ constexpr int mvr_cmax(int t, int nt) {
+    return t == HKHIP_Q4_K ? (nt == 1 ? 4 : nt == 8 ? 1 : 2)
+         : t == HKHIP_Q6_K ? (nt == 1 ? 4 : nt == 2 ? 2 : 1)
+                           : (nt == 1 ? 8 : nt == 8 ? 2 : 4);
+}
+// Waves per workgroup: MVR_NWAVES (a budget of 256 registers per lane), or 4 (512) for the
+// variants that need more.
+__host__ __device__ constexpr int mvr_nw(int t, int nt, int c) {
+    return (t == HKHIP_Q6_K && nt * c >= 4) || (t == HKHIP_Q4_K && nt * c >= 8 && nt < 8) ? 4 : MVR_NWAVES;
+}
+
+template <int T, int NT, int C>
+static mv_kernel_t mvr_if_fits() {
+    if constexpr (C <= mvr_cmax(T, NT))
+        return mmvr_kernel<T, NT, C, mvr_rows(NT, C), mvr_nw(T, NT, C)>;
+    else
+        return nullptr;
+}
+
+template <int T, int NT>
+static mv_kernel_t mvr_pick_c(int c) {
+    switch (c) {
+    case 1: return mvr_if_fits<T, NT, 1>();
+    case 2: return mvr_if_fits<T, NT, 2>();
+    case 4: return mvr_if_fits<T, NT, 4>();
+    case 8: return mvr_if_fits<T, NT, 8>();
+    default: return nullptr;
+    }
+}
+
+template <int T>
+static mv_kernel_t mvr_pick(int nt, int c) {
+    switch (nt) {
+    case 1: return mvr_pick_c<T, 1>(c);
+    case 2: return mvr_pick_c<T, 2>(c);
+    case 4: return mvr_pick_c<T, 4>(c);
+    case 8: return mvr_pick_c<T, 8>(c);
+    default: return nullptr;
+    }
+}
+
+static mv_kernel_t kernelr_for(int t, int nt, int c) {
+    switch (t) {
+    case HKHIP_Q4_K: return mvr_pick<HKHIP_Q4_K>(nt, c);
+    case HKHIP_Q6_K: return mvr_pick<HKHIP_Q6_K>(nt, c);
+    case HKHIP_Q8_0: return mvr_pick<HKHIP_Q8_0>(nt, c);
+    case HKHIP_IQ4_NL: return mvr_pick<HKHIP_IQ4_NL>(nt, c);
+    default: return nullptr;
+    }
+}
+
 // Resident workgroups per CU for a kernel at an LDS size (cached; the first call per kernel also
 // raises its dynamic-LDS limit to the full 160 KB).
-static int resident_per_cu(mv_kernel_t k, uint32_t lds) {
+static int resident_per_cu(mv_kernel_t k, int threads, uint32_t lds) {
     static std::mutex mu;
     static std::map<std::pair<void *, uint32_t>, int> cache;
     std::lock_guard<std::mutex> lock(mu);
@@ -481,7 +908,7 @@ static int resident_per_cu(mv_kernel_t k, uint32_t lds) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
                               int(MV_LDS_MAX));
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, 256, lds) != hipSuccess || n < 1) n = 1;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, threads, lds) != hipSuccess || n < 1) n = 1;
     cache[key] = n;
     return n;
 }
@@ -505,26 +932,71 @@ hipError_t launch_mmvq_parts(int t, const MvPartDesc *parts, int nparts, uint32_
                              const uint8_t *xq, uint32_t n, int mode, hipStream_t s) {
     if (n < 1 || n > 8 || nparts < 1 || nparts > MV_PARTS) return hipErrorInvalidValue;
     const bool kq = (t == HKHIP_Q4_K || t == HKHIP_Q6_K);
+    static const int force_general = env_int("HKHIP_MV_GENERAL", 0);
+    {
+        // Register kernel when the shape fits it.
+        const uint32_t units = kq ? K / 64 : K / 32;
+        const int nt = n == 1 ? 1 : n == 2 ? 2 : n <= 4 ? 4 : 8;
+        int c = 1;
+        while (c < 8 && 64u * c < units) c *= 2;
+        mv_kernel_t k = (64u * c >= units && !force_general) ? kernelr_for(t, nt, c) : nullptr;
+        if (k) {
+            MvArgs a{};
+            uint32_t rows = 0;
+            for (int i = 0; i < nparts; i++) {
+                const WLayout W = weight_layout(t, parts[i].rows, K);
+                a.p[i].w = parts[i].w;
+                a.p[i].ws = reinterpret_cast<const uint16_t *>(parts[i].w + W.scale_off);
+                a.p[i].y = parts[i].y;
+                a.p[i].bias = parts[i].bias;
+                a.p[i].rows = parts[i].rows;
+                a.p[i].gstart = rows;
+                rows += parts[i].rows;
+            }
+            for (int i = nparts; i < MV_PARTS; i++) a.p[i].gstart = 0xffffffffu;
+            a.nparts = uint32_t(nparts);
+            a.ngroups = rows;
+            a.K = K;
+            a.mode = mode;
+            a.ntok = n;
+            if (x) {
+                a.x = x;
+            } else {
+                const ActLayout A = act_layout(n, K);
+                a.gqs = reinterpret_cast<const int8_t *>(xq + (kq ? A.k_qs : A.a8_qs));
+                a.gd = reinterpret_cast<const float *>(xq + (kq ? A.k_d : A.a8_d));
+                a.gbs = reinterpret_cast<const int16_t *>(xq + A.k_bs);
+            }
+            if (rows == 0) return hipSuccess;
+            const int R = mvr_rows(nt, c);
+            const uint32_t lds = x ? mvr_lds_bytes(int(n), K, kq) : 0;
+            if (lds > MV_LDS_MAX) return hipErrorInvalidValue;
+            const int nw = mvr_nw(t, nt, c);
+            const uint32_t cap = uint32_t(cu_count() * resident_per_cu(k, nw * 64, lds));
+            const uint32_t want = (rows + nw * R - 1) / (nw * R);
+            const uint32_t grid = want < cap ? want : cap;
+            hipLaunchKernelGGL(k, dim3(grid), dim3(nw * 64), lds, s, a);
+            return hipGetLastError();
+        }
+    }
     // Tokens per launch: as many as the LDS holds (all 8 at every BASELINE shape).
     int per = int(n);
     while (per > 1 && mv_lds_bytes(per, K, kq) > MV_LDS_MAX) per--;
     if (mv_lds_bytes(per, K, kq) > MV_LDS_MAX) return hipErrorInvalidValue;
-    // Lanes per row: enough that each lane has MV_UNROLL units of the row in flight at once.
     const uint32_t units = kq ? K / 64 : K / 32;
-    const uint32_t want_lanes = (units + MV_UNROLL - 1) / MV_UNROLL;
+    // Lanes per row: enough that a row takes one step of UNR units per lane when it can.
+    const uint32_t unr = MV_UNR;
+    const uint32_t want_lanes = (units + unr - 1) / unr;
     int lg = 0;
     while ((1u << lg) < want_lanes && lg < 6) lg++;
-    // Tuning overrides (experiments only): lanes-per-row log2, and the workgroup cap
-    // (0 = one workgroup per 4 row groups, no persistence).
-    static const int env_lg = env_int("HKHIP_MV_LPR", -1);
-    static const int env_cap = env_int("HKHIP_MV_CAP", -1);
-    if (env_lg >= 0 && env_lg <= 6) lg = env_lg;
+    const uint32_t rpw = 64u >> lg;
+    const int nw = MV_NW;
     const ActLayout A = act_layout(n, K);
     const uint32_t dblk = kq ? 256 : 32;
     for (uint32_t t0 = 0; t0 < n; t0 += per) {
         const int nt = int(n - t0 < uint32_t(per) ? n - t0 : uint32_t(per));
         MvArgs a{};
-        uint32_t total = 0;
+        uint32_t groups = 0;
         for (int i = 0; i < nparts; i++) {
             const WLayout W = weight_layout(t, parts[i].rows, K);
             a.p[i].w = parts[i].w;
@@ -532,12 +1004,12 @@ hipError_t launch_mmvq_parts(int t, const MvPartDesc *parts, int nparts, uint32_
             a.p[i].y = parts[i].y + uint64_t(t0) * parts[i].rows;
             a.p[i].bias = parts[i].bias;
             a.p[i].rows = parts[i].rows;
-            a.p[i].row0 = total;
-            total += parts[i].rows;
+            a.p[i].gstart = groups;
+            groups += (parts[i].rows + rpw - 1) / rpw;
         }
-        for (int i = nparts; i < MV_PARTS; i++) a.p[i].row0 = 0xffffffffu;
+        for (int i = nparts; i < MV_PARTS; i++) a.p[i].gstart = 0xffffffffu;
         a.nparts = uint32_t(nparts);
-        a.total_rows = total;
+        a.ngroups = groups;
         a.K = K;
         a.mode = mode;
         a.lpr_log2 = lg;
@@ -548,17 +1020,18 @@ hipError_t launch_mmvq_parts(int t, const MvPartDesc *parts, int nparts, uint32_
             a.gd = reinterpret_cast<const float *>(xq + (kq ? A.k_d : A.a8_d)) + uint64_t(t0) * (K / dblk);
             a.gbs = reinterpret_cast<const int16_t *>(xq + A.k_bs) + uint64_t(t0) * (K / 16);
         }
-        if (total == 0) continue;
+        if (groups == 0) continue;
         mv_kernel_t k = kernel_for(t, nt);
         if (!k) return hipErrorInvalidValue;
         const uint32_t lds = mv_lds_bytes(nt, K, kq);
-        const uint32_t groups = (total + (64u >> lg) - 1) / (64u >> lg);
-        const uint32_t want = (groups + 3) / 4;
-        uint32_t cap = uint32_t(cu_count() * resident_per_cu(k, lds));
-        if (env_cap == 0) cap = 0xffffffffu;
-        else if (env_cap > 0) cap = uint32_t(env_cap);
+        // Enough workgroups for every row group, and at least one per CU while there are row
+        // groups to give them (small matrices still spread their bytes over every CU).
+        const uint32_t ncu = uint32_t(cu_count());
+        uint32_t want = (groups + nw - 1) / nw;
+        if (want < ncu) want = groups < ncu ? groups : ncu;
+        const uint32_t cap = uint32_t(cu_count() * resident_per_cu(k, nw * 64, lds));
         const uint32_t grid = want < cap ? want : cap;
-        hipLaunchKernelGGL(k, dim3(grid), dim3(256), lds, s, a);
+        hipLaunchKernelGGL(k, dim3(grid), dim3(nw * 64), lds, s, a);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }

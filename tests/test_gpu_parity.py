@@ -13,6 +13,7 @@ import pytest
 
 from hk_amd import formats as F
 from hk_amd import synth
+from hk_amd.engine import ACCUMULATE
 from oracle import oracle as O
 from tests.helpers import PARITY_TOL, load_fixture, parity_err
 
@@ -282,3 +283,70 @@ def test_matvec_parts_large_k(eng, torch_cuda, t, k, n):
     torch.cuda.synchronize()
     assert parity_err(y.cpu().numpy(), O.matmul(t, raw, m, k, x, n, tiled=False)) <= PARITY_TOL
     eng.free(w)
+
+
+# ---------------------------------------------------------------------------------------- kernel variants
+
+@pytest.mark.parametrize("t,k,n", [
+    (F.Q4_K, 4096, 1), (F.Q4_K, 8192, 1), (F.Q4_K, 16384, 1), (F.Q4_K, 16640, 1),   # C=1,2,4, LDS kernel
+    (F.Q4_K, 8192, 2), (F.Q4_K, 16384, 2), (F.Q4_K, 8192, 4), (F.Q4_K, 4096, 5), (F.Q4_K, 8192, 8),
+    (F.Q6_K, 8192, 1), (F.Q6_K, 16384, 1), (F.Q6_K, 8192, 2), (F.Q6_K, 4096, 4), (F.Q6_K, 4096, 7),
+    (F.Q8_0, 2048, 1), (F.Q8_0, 16384, 1), (F.Q8_0, 16416, 1), (F.Q8_0, 8192, 2), (F.Q8_0, 4096, 6),
+    (F.IQ4_NL, 8192, 1), (F.IQ4_NL, 16384, 2), (F.IQ4_NL, 4096, 8), (F.IQ4_NL, 96, 3),
+])
+@pytest.mark.parametrize("prepared", [False, True])
+def test_matvec_kernel_variants(eng, torch_cuda, t, k, n, prepared):
+    """Every register-kernel variant (units per lane 1-8, token counts padded up to 1/2/4/8) and
+    the shapes just past it, which fall back to the LDS kernel; f32 input and prepared input."""
+    torch = torch_cuda
+    m = 333
+    raw = synth.weights_np(t, m, k, seed=900 + t + k)
+    x = synth.activations_np(n, k, seed=901 + n, outliers=0.01)
+    w = eng.upload(raw, t, m, k)
+    y = torch.full((n, m), float("nan"), device="cuda")
+    xd = torch.from_numpy(x).cuda()
+    if prepared:
+        xq = torch.empty(eng.act_bytes(n, k), dtype=torch.uint8, device="cuda")
+        eng.qact(xd, n, k, F.ACT_KIND[t], xq)
+        eng.matvec_parts([w], [y], n, xq=xq)
+    else:
+        eng.matvec_parts([w], [y], n, x=xd)
+    torch.cuda.synchronize()
+    assert parity_err(y.cpu().numpy(), O.matmul(t, raw, m, k, x, n, tiled=False)) <= PARITY_TOL
+    eng.free(w)
+
+
+def test_matvec_many_rows_per_wave(eng, torch_cuda):
+    """More rows than a wave keeps results for (64), so results are stored in several batches;
+    accumulate mode and a bias on top."""
+    torch = torch_cuda
+    t, m, k, n = F.Q8_0, 140000, 256, 2
+    raw = synth.weights_np(t, m, k, seed=950)
+    x = synth.activations_np(n, k, seed=951)
+    w = eng.upload(raw, t, m, k)
+    y0 = np.random.default_rng(952).standard_normal((n, m)).astype(np.float32)
+    y = torch.from_numpy(y0).cuda()
+    b = torch.from_numpy(np.linspace(-1, 1, m, dtype=np.float32)).cuda()
+    eng.matvec_parts([w], [y], n, x=torch.from_numpy(x).cuda(), biases=[b], mode=ACCUMULATE)
+    torch.cuda.synchronize()
+    want = y0 + O.matmul(t, raw, m, k, x, n, bias=b.cpu().numpy(), tiled=False)
+    assert parity_err(y.cpu().numpy(), want) <= PARITY_TOL
+    eng.free(w)
+
+
+@pytest.mark.parametrize("t", FMTS)
+def test_matvec_parts_straddling_waves(eng, torch_cuda, t):
+    """Parts large enough that some waves' row ranges cross from one part into the next."""
+    torch = torch_cuda
+    k, n = 512, 1
+    heights = [3001, 999, 1203, 77]
+    raws = [synth.weights_np(t, m, k, seed=960 + i) for i, m in enumerate(heights)]
+    x = synth.activations_np(n, k, seed=965)
+    mats = [eng.upload(r, t, m, k) for r, m in zip(raws, heights)]
+    ys = [torch.full((n, m), float("nan"), device="cuda") for m in heights]
+    eng.matvec_parts(mats, ys, n, x=torch.from_numpy(x).cuda())
+    torch.cuda.synchronize()
+    for r, m, y in zip(raws, heights, ys):
+        assert parity_err(y.cpu().numpy(), O.matmul(t, r, m, k, x, n, tiled=False)) <= PARITY_TOL
+    for w in mats:
+        eng.free(w)
