@@ -117,6 +117,10 @@ template <> struct MvFmt<HKHIP_Q4_K> {
         return a;
     }
     __device__ static W load(const RowRef &R, uint32_t u) {
+#ifdef HKHIP_MV_PROBE_CONTIG
+        { const uint32_t base = (u & ~63u) * 36, l = u & 63;
+        return W{ldw(R.w + base + 16 * l), ldw(R.w + base + 1024 + 16 * l), ldw(R.w + base + 2048 + 16 * (l & 15))}; }
+#endif
         const uint8_t *blk = R.w + (u >> 2) * 144;
         return W{ldw(blk), ldw(blk + 16 + 32 * (u & 3)), ldw(blk + 32 + 32 * (u & 3))};
     }
@@ -606,6 +610,16 @@ __device__ __forceinline__ void mvr_stage_block(float4 v, uint32_t b, bool valid
     }
 }
 
+#ifdef HKHIP_MV_PROBE_TS
+__device__ uint64_t *g_ts;
+#define MV_TS(i)                                                                                  \
+    do {                                                                                          \
+        const uint64_t t_ = __builtin_amdgcn_s_memrealtime();                                     \
+        if (__lane_id() == 0) g_ts[(blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6)) * 5 + i] = t_; \
+    } while (0)
+#else
+#define MV_TS(i)
+#endif
 #ifndef MVR_MINW
 #define MVR_MINW 1
 #endif
@@ -665,17 +679,21 @@ __global__ __launch_bounds__(NW * 64, MVR_MINW) void mmvr_kernel(MvArgs a) {
     // in order), and the weights of the first two steps stream in meanwhile. A quantized input
     // is read by each lane directly, also ahead of the weights.
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    constexpr int PB = 2;
     const uint32_t ntok = NT == 1 ? 1u : a.ntok;
     const uint32_t nflat = ntok * K, nblk = (nflat + 255) / 256;
+    // Blocks of 256 inputs per wave: at most NT*K/256/NW, i.e. NT*2C (Q8K) or NT*C (A8) * 8/NW.
+    // Up to 8 are loaded up front, with clamped (always issued) loads.
+    constexpr int PBW = (F::kq ? 2 : 1) * C * NT * 8 / NW;
+    constexpr int PB = PBW < 8 ? PBW : 8;
     float4 xv[PB];
     AU au[NT][C];
+    auto xload = [&](uint32_t b) -> float4 {
+        const uint32_t e = 256 * (b < nblk ? b : nblk - 1) + 4 * lane;
+        return *reinterpret_cast<const float4 *>(a.x + (e < nflat ? e : nflat - 4));
+    };
     if (a.x) {
 #pragma unroll
-        for (int j = 0; j < PB; j++) {
-            const uint32_t b = wave + NW * j, e = 256 * b + 4 * lane;
-            xv[j] = (b < nblk && e < nflat) ? *reinterpret_cast<const float4 *>(a.x + e) : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
+        for (int j = 0; j < PB; j++) xv[j] = xload(wave + NW * j);
     } else {
 #pragma unroll
         for (int t = 0; t < NT; t++) {
@@ -687,8 +705,10 @@ __global__ __launch_bounds__(NW * 64, MVR_MINW) void mmvr_kernel(MvArgs a) {
             }
         }
     }
+    MV_TS(0);
+    const uint32_t ns = (r1 - r0 + R - 1) / R; // steps of this wave
     load(wa, r0);
-    load(wb, r0 + R);
+    MV_TS(1);
     if (a.x) {
         int8_t *sqs = reinterpret_cast<int8_t *>(smem);
         int16_t *sbs = reinterpret_cast<int16_t *>(smem + nflat);
@@ -698,10 +718,15 @@ __global__ __launch_bounds__(NW * 64, MVR_MINW) void mmvr_kernel(MvArgs a) {
             const uint32_t b = wave + NW * j;
             if (b < nblk) mvr_stage_block<F>(xv[j], b, 256 * b + 4 * lane < nflat, sqs, sbs, sd);
         }
-        for (uint32_t b = wave + NW * PB; b < nblk; b += NW) {
-            const uint32_t e = 256 * b + 4 * lane;
-            const float4 v = e < nflat ? *reinterpret_cast<const float4 *>(a.x + e) : make_float4(0.f, 0.f, 0.f, 0.f);
-            mvr_stage_block<F>(v, b, e < nflat, sqs, sbs, sd);
+        // Rare (more than 8 blocks per wave): the rest, PB blocks at a time.
+        for (uint32_t b0 = wave + NW * PB; b0 < nblk; b0 += NW * PB) {
+#pragma unroll
+            for (int j = 0; j < PB; j++) xv[j] = xload(b0 + NW * j);
+#pragma unroll
+            for (int j = 0; j < PB; j++) {
+                const uint32_t b = b0 + NW * j;
+                if (b < nblk) mvr_stage_block<F>(xv[j], b, 256 * b + 4 * lane < nflat, sqs, sbs, sd);
+            }
         }
         __syncthreads();
 #pragma unroll
@@ -714,15 +739,16 @@ __global__ __launch_bounds__(NW * 64, MVR_MINW) void mmvr_kernel(MvArgs a) {
             }
         }
     }
+    // The second step is issued only now, so that the barrier does not wait for every wave to get
+    // two steps of loads past a busy memory pipeline.
+    if (ns > 1) load(wb, r0 + R);
 
-    // Activation loads were issued after the first two steps of weights; waiting for all of
-    // them here (the first step is needed next anyway) leaves nothing older than a prefetch
-    // pending inside the loop. 0x0F70 = vmcnt(0), expcnt and lgkmcnt unconstrained.
-    __builtin_amdgcn_s_waitcnt(0x0F70);
+    MV_TS(2);
 
-    // Lane j keeps the results of row fbase + j until they are stored, 64 rows at a time.
+    // Lane j keeps the result of row r0 + j; the launch gives no wave more than 64 rows, so the
+    // results are stored once, at the end, and the loop issues no load but weights.
     float res[NT];
-    uint32_t fbase = r0;
+    const uint32_t fbase = r0;
     auto flush = [&](uint32_t n) {
         if (lane < n) {
             const uint32_t r = fbase + lane;
@@ -748,7 +774,6 @@ __global__ __launch_bounds__(NW * 64, MVR_MINW) void mmvr_kernel(MvArgs a) {
                     *y = res[t] + b;
             }
         }
-        fbase += n;
     };
     auto compute = [&](const W (*w)[C], uint32_t rb) {
 #pragma unroll
@@ -783,17 +808,31 @@ __global__ __launch_bounds__(NW * 64, MVR_MINW) void mmvr_kernel(MvArgs a) {
             }
         }
     };
-    const uint32_t ns = (r1 - r0 + R - 1) / R;
-    for (uint32_t s = 0; s < ns; s += 2) {
-        if (r0 + s * R - fbase == 64) flush(64);
+    // Steady state: every step's loads are valid, so each load is issued unconditionally and the
+    // wait before a compute covers exactly the older buffer. The last (up to three) steps are
+    // peeled so that nothing is loaded past the range.
+    uint32_t s = 0;
+    for (; s + 3 < ns; s += 2) {
         compute(wa, r0 + s * R);
         load(wa, r0 + (s + 2) * R);
-        if (s + 1 >= ns) break;
-        if (r0 + (s + 1) * R - fbase == 64) flush(64);
         compute(wb, r0 + (s + 1) * R);
         load(wb, r0 + (s + 3) * R);
     }
-    flush(r1 - fbase);
+    MV_TS(3);
+    auto step = [&](const W (*w)[C], uint32_t st) { compute(w, r0 + st * R); };
+    if (s + 2 < ns) {
+        step(wa, s);
+        load(wa, r0 + (s + 2) * R);
+        step(wb, s + 1);
+        step(wa, s + 2);
+    } else if (s + 1 < ns) {
+        step(wa, s);
+        step(wb, s + 1);
+    } else if (s < ns) {
+        step(wa, s);
+    }
+    flush(r1 - r0);
+    MV_TS(4);
 }
 
 #undef MV_SEL
@@ -852,8 +891,15 @@ __host__ __device__ constexpr int mvr_cmax(int t, int nt) {
 }
 // Waves per workgroup: MVR_NWAVES (a budget of 256 registers per lane), or 4 (512) for the
 // variants that need more.
+#ifndef MVR_NW_Q4C4
+#define MVR_NW_Q4C4 MVR_NWAVES
+#endif
 __host__ __device__ constexpr int mvr_nw(int t, int nt, int c) {
-    return (t == HKHIP_Q6_K && nt * c >= 4) || (t == HKHIP_Q4_K && nt * c >= 8 && nt < 8) ? 4 : MVR_NWAVES;
+    if (t == HKHIP_Q4_K && nt == 1 && c == 4) return MVR_NW_Q4C4;
+    return (t == HKHIP_Q6_K && nt * c >= 4) || (t == HKHIP_Q4_K && nt * c >= 8 && nt < 8) ||
+                   ((t == HKHIP_Q8_0 || t == HKHIP_IQ4_NL) && c >= 4 && nt * c >= 8)
+               ? 4
+               : MVR_NWAVES;
 }
 
 template <int T, int NT, int C>
@@ -974,7 +1020,12 @@ hipError_t launch_mmvq_parts(int t, const MvPartDesc *parts, int nparts, uint32_
             const int nw = mvr_nw(t, nt, c);
             const uint32_t cap = uint32_t(cu_count() * resident_per_cu(k, nw * 64, lds));
             const uint32_t want = (rows + nw * R - 1) / (nw * R);
-            const uint32_t grid = want < cap ? want : cap;
+            uint32_t grid = want < cap ? want : cap;
+            static const int grid_cap = env_int("HKHIP_MV_GRID_CAP", 0); // experiments only
+            if (grid_cap > 0 && grid > uint32_t(grid_cap)) grid = grid_cap;
+            // At most 64 rows per wave (each lane keeps one row's result); extra workgroups queue.
+            const uint32_t need = (rows + 64u * nw - 1) / (64u * nw);
+            if (grid < need) grid = need;
             hipLaunchKernelGGL(k, dim3(grid), dim3(nw * 64), lds, s, a);
             return hipGetLastError();
         }
