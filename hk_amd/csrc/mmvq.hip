@@ -117,10 +117,6 @@ template <> struct MvFmt<HKHIP_Q4_K> {
         return a;
     }
     __device__ static W load(const RowRef &R, uint32_t u) {
-#ifdef HKHIP_MV_PROBE_CONTIG
-        { const uint32_t base = (u & ~63u) * 36, l = u & 63;
-        return W{ldw(R.w + base + 16 * l), ldw(R.w + base + 1024 + 16 * l), ldw(R.w + base + 2048 + 16 * (l & 15))}; }
-#endif
         const uint8_t *blk = R.w + (u >> 2) * 144;
         return W{ldw(blk), ldw(blk + 16 + 32 * (u & 3)), ldw(blk + 32 + 32 * (u & 3))};
     }
@@ -568,44 +564,79 @@ __device__ __forceinline__ typename F::AU load_unit(const int8_t *gqs, const int
     return au;
 }
 
-// A8 quantization of 256 values per wave, four consecutive values per lane (lane l holds
-// 4l..4l+3, so one block of 32 is eight lanes). Returns this lane's four bytes; d is the block's.
-__device__ __forceinline__ uint32_t quant_a8_oct(float4 v4, float &d) {
-    const float v[4] = {v4.x, v4.y, v4.z, v4.w};
-    float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    m = fmaxf(m, dpp_f<DPP_XOR1>(m));
-    m = fmaxf(m, dpp_f<DPP_XOR2>(m));
-    m = fmaxf(m, dpp_f<DPP_HALF_MIRROR>(m));
-    d = __fdiv_rn(m, 127.0f);
-    const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
-    uint32_t pk = 0;
-#pragma unroll
-    for (int b = 0; b < 4; b++) pk |= uint32_t(uint8_t((int)roundf(v[b] * id))) << (8 * b);
-    return pk;
-}
-
 // Bytes of LDS the register kernel uses to stage an f32 input of nt tokens.
 __host__ __device__ inline uint32_t mvr_lds_bytes(int nt, uint32_t K, bool kq) {
     return nt * K + (kq ? nt * K / 8 + nt * (K / 256) * 4 : nt * (K / 32) * 4);
 }
 
-// Quantizes one 256-value block b (of token-major input x) with a whole wave and writes it to
-// the LDS staging area in the engine's activation layout.
+// Quantizes 1024 consecutive inputs per wave (lane l holds values 16l..16l+15 of the chunk) with
+// the qact arithmetic and writes them to the LDS staging area in the engine's activation layout.
+// Q8K: a block of 256 is one row of 16 lanes, so every reduction stays inside a DPP row and a
+// wave quantizes four blocks at once. A8: a block of 32 is two lanes. `valid` is false for lanes
+// past the input (whole blocks). All 64 lanes must execute this.
 template <typename F>
-__device__ __forceinline__ void mvr_stage_block(float4 v, uint32_t b, bool valid, int8_t *sqs, int16_t *sbs,
-                                                float *sd) {
+__device__ __forceinline__ void mvr_stage_chunk(const float4 *xv, uint32_t c, bool valid, int8_t *sqs,
+                                                int16_t *sbs, float *sd) {
     const uint32_t lane = __lane_id();
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        v[4 * i] = xv[i].x; v[4 * i + 1] = xv[i].y; v[4 * i + 2] = xv[i].z; v[4 * i + 3] = xv[i].w;
+    }
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) m = fmaxf(m, fabsf(v[i]));
+    const uint32_t e = 1024 * c + 16 * lane; // first input of this lane
+    uint32_t pk[4];
     if constexpr (F::kq) {
-        const Q8KQ qr = quant_q8k_wave(v, lane);
-        *reinterpret_cast<uint32_t *>(sqs + 256 * b + 4 * lane) = qr.packed;
-        if ((lane & 3) == 0) sbs[16 * b + lane / 4] = (int16_t)qr.bsum;
-        if (lane == 0) sd[b] = qr.d;
-    } else {
-        float d;
-        const uint32_t pk = quant_a8_oct(v, d);
+        const float amax = row_max(m);
+        // Signed value of the first element with |x| == amax (lowest index wins, as the
+        // reference's strict '>' scan does): this lane's first hit, then the row's lowest lane.
+        float first = 0.0f;
+        bool hit = false;
+#pragma unroll
+        for (int i = 15; i >= 0; i--) {
+            if (fabsf(v[i]) == amax) {
+                first = v[i];
+                hit = true;
+            }
+        }
+        const uint64_t mask = __ballot(hit);
+        const uint32_t rbits = uint32_t(mask >> (lane & 48)) & 0xFFFFu;
+        const float mx = __shfl(first, int((lane & 48) + (rbits ? __builtin_ctz(rbits) : 0)));
+        const bool zero = amax == 0.0f || rbits == 0;
+        const float iscale = zero ? 0.0f : __fdiv_rn(-127.0f, mx);
+        int bsum = 0;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            uint32_t p = 0;
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const int t = (int)roundf(iscale * v[4 * w + b]);
+                p |= uint32_t(uint8_t(t < 127 ? t : 127)) << (8 * b);
+            }
+            pk[w] = p;
+            bsum = sdot4(p, 0x01010101u, bsum);
+        }
         if (valid) {
-            *reinterpret_cast<uint32_t *>(sqs + 256 * b + 4 * lane) = pk;
-            if ((lane & 7) == 0) sd[8 * b + lane / 8] = d;
+            *reinterpret_cast<uint4 *>(sqs + e) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+            sbs[e / 16] = (int16_t)bsum;
+            if ((lane & 15) == 0) sd[e / 256] = zero ? 0.0f : __fdiv_rn(1.0f, iscale);
+        }
+    } else {
+        const float amax = fmaxf(m, dpp_f<DPP_XOR1>(m));
+        const float d = __fdiv_rn(amax, 127.0f);
+        const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            uint32_t p = 0;
+#pragma unroll
+            for (int b = 0; b < 4; b++) p |= uint32_t(uint8_t((int)roundf(v[4 * w + b] * id))) << (8 * b);
+            pk[w] = p;
+        }
+        if (valid) {
+            *reinterpret_cast<uint4 *>(sqs + e) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+            if ((lane & 1) == 0) sd[e / 32] = d;
         }
     }
 }
@@ -680,20 +711,23 @@ __global__ __launch_bounds__(NW * 64, MVR_MINW) void mmvr_kernel(MvArgs a) {
     // is read by each lane directly, also ahead of the weights.
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const uint32_t ntok = NT == 1 ? 1u : a.ntok;
-    const uint32_t nflat = ntok * K, nblk = (nflat + 255) / 256;
-    // Blocks of 256 inputs per wave: at most NT*K/256/NW, i.e. NT*2C (Q8K) or NT*C (A8) * 8/NW.
-    // Up to 8 are loaded up front, with clamped (always issued) loads.
-    constexpr int PBW = (F::kq ? 2 : 1) * C * NT * 8 / NW;
-    constexpr int PB = PBW < 8 ? PBW : 8;
-    float4 xv[PB];
+    const uint32_t nflat = ntok * K;
+    // Chunks of 1024 inputs per wave: at most NT*K/1024/NW = (4 or 2)*NT*C/NW. Up to 4 are
+    // loaded up front (clamped, always issued).
+    constexpr int CPW = (F::kq ? 4 : 2) * NT * C / NW;
+    constexpr int PB = CPW < 1 ? 1 : CPW > 4 ? 4 : CPW;
+    const uint32_t nchunk = (nflat + 1023) / 1024;
+    float4 xv[PB][4];
     AU au[NT][C];
-    auto xload = [&](uint32_t b) -> float4 {
-        const uint32_t e = 256 * (b < nblk ? b : nblk - 1) + 4 * lane;
-        return *reinterpret_cast<const float4 *>(a.x + (e < nflat ? e : nflat - 4));
+    auto xload = [&](uint32_t cidx, float4 *dst) {
+        const uint32_t e = 1024 * (cidx < nchunk ? cidx : nchunk - 1) + 16 * lane;
+        const float4 *src = reinterpret_cast<const float4 *>(a.x + (e < nflat ? e : nflat - 16));
+#pragma unroll
+        for (int i = 0; i < 4; i++) dst[i] = src[i];
     };
     if (a.x) {
 #pragma unroll
-        for (int j = 0; j < PB; j++) xv[j] = xload(wave + NW * j);
+        for (int j = 0; j < PB; j++) xload(wave + NW * j, xv[j]);
     } else {
 #pragma unroll
         for (int t = 0; t < NT; t++) {
@@ -708,26 +742,26 @@ __global__ __launch_bounds__(NW * 64, MVR_MINW) void mmvr_kernel(MvArgs a) {
     MV_TS(0);
     const uint32_t ns = (r1 - r0 + R - 1) / R; // steps of this wave
     load(wa, r0);
-    MV_TS(1);
     if (a.x) {
         int8_t *sqs = reinterpret_cast<int8_t *>(smem);
         int16_t *sbs = reinterpret_cast<int16_t *>(smem + nflat);
         float *sd = reinterpret_cast<float *>(smem + nflat + (F::kq ? nflat / 8 : 0));
 #pragma unroll
         for (int j = 0; j < PB; j++) {
-            const uint32_t b = wave + NW * j;
-            if (b < nblk) mvr_stage_block<F>(xv[j], b, 256 * b + 4 * lane < nflat, sqs, sbs, sd);
+            const uint32_t cidx = wave + NW * j;
+            if (cidx < nchunk) mvr_stage_chunk<F>(xv[j], cidx, 1024 * cidx + 16 * lane < nflat, sqs, sbs, sd);
         }
-        // Rare (more than 8 blocks per wave): the rest, PB blocks at a time.
-        for (uint32_t b0 = wave + NW * PB; b0 < nblk; b0 += NW * PB) {
+        // Rare (more than PB chunks per wave): the rest, PB chunks at a time.
+        for (uint32_t c0 = wave + NW * PB; c0 < nchunk; c0 += NW * PB) {
 #pragma unroll
-            for (int j = 0; j < PB; j++) xv[j] = xload(b0 + NW * j);
+            for (int j = 0; j < PB; j++) xload(c0 + NW * j, xv[j]);
 #pragma unroll
             for (int j = 0; j < PB; j++) {
-                const uint32_t b = b0 + NW * j;
-                if (b < nblk) mvr_stage_block<F>(xv[j], b, 256 * b + 4 * lane < nflat, sqs, sbs, sd);
+                const uint32_t cidx = c0 + NW * j;
+                if (cidx < nchunk) mvr_stage_chunk<F>(xv[j], cidx, 1024 * cidx + 16 * lane < nflat, sqs, sbs, sd);
             }
         }
+        MV_TS(1);
         __syncthreads();
 #pragma unroll
         for (int t = 0; t < NT; t++) {
