@@ -42,8 +42,9 @@ def parse():
     p.add_argument("--layers", type=int, default=LLAMA8B["layers"])
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
-    p.add_argument("--only", choices=["all", "decode", "kernel", "prefill"], default="all",
-                   help="run one part only (profiling)")
+    p.add_argument("--only", choices=["all", "decode", "kernel", "prefill", "copy"], default="all",
+                   help="run one part only (profiling); 'copy' runs a plain 256 MiB device copy 20 times, "
+                        "the calibration for the HBM traffic counters")
     return p.parse_args()
 
 
@@ -60,6 +61,14 @@ def main():
 
     torch.cuda.init()
     dev = torch.device("cuda:0")
+    if args.only == "copy":
+        src = torch.ones(64 << 20, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(20):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": src.numel() * 4, "launches": 20}))
+        return
     eng = Engine(0)
     stream = torch.cuda.Stream()
     torch.cuda.set_stream(stream)
@@ -165,7 +174,8 @@ def main():
         torch.cuda.synchronize()
         us = 1e3 * e0.elapsed_time(e1) / (reps * len(pairs))
         kbytes = 2 * pairs[0][0].file_bytes + 4 * H + 2 * 4 * FF
-        result["kernel"] = dict(name="mmvq_kernel<Q4_K,1> (gate+up fused, qact in prologue)", shape="2x14336x4096",
+        result["kernel"] = dict(name="mmvr_kernel<Q4_K, NT=1, C=1> (gate+up fused, f32 input quantized in-kernel)",
+                                shape="2x14336x4096",
                                 launches=reps * len(pairs), avg_us=us, bytes_per_launch=kbytes,
                                 gbs=kbytes / (us * 1e-6) / 1e9)
 
@@ -216,7 +226,8 @@ def main():
                    "frac_hbm_peak": round(dec.get("gbs", 0.0) / HBM_PEAK_GBS, 4),
                    "graph": "one HIP graph per step"},
         "roofline": {"bound": "hbm", "achieved": round(ker.get("gbs", 0.0), 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(ker.get("gbs", 0.0) / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(ker.get("gbs", 0.0) / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(),
                      "kernel": ker.get("name"), "shape": ker.get("shape"), "avg_us": ker.get("avg_us"),
                      "bytes_per_launch": ker.get("bytes_per_launch")},
         "prefill": result.get("prefill"),
@@ -224,6 +235,18 @@ def main():
     }
     print(json.dumps(line), flush=True)
     eng.close()
+
+
+def measured_traffic():
+    """HBM bytes per launch of the roofline kernel, as measured with rocprofv3 PMC counters
+    (FETCH_SIZE + WRITE_SIZE, each scaled by what the counter reads for a plain copy of known
+    size) and recorded in profiles/; None when no measurement is recorded."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "mmvr_q4k_gate_up_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get("traffic_bytes")
+    except (OSError, ValueError):
+        return None
 
 
 def time_graph(torch, eng, stream, fn, reps: int) -> float:
