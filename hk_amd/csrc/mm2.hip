@@ -1,0 +1,358 @@
+// Prefill GEMM for Q4_K on the int8 MFMA units, split-plane form.
+//
+// Per row r, token t and super-block b, hk's CPU kernel (src/quant/gemm.zig kernelK 180-236,
+// with the scale unpack of unpack.zig) computes
+//     y[t][r] += d[r,b]*da[t,b] * sum_s sc[r,b,s] * sum_{k in s} q[r,k]*a[t,k]
+//              - dmin[r,b]*da[t,b] * sum_s mn[r,b,s] * bsum32[t,b,s]
+// with exact integer inner sums. Here:
+//  * main term: the 6-bit sub-block scale is folded into the weights as two int8 planes: with
+//    sc = 8*sh + sl (sh, sl in [0,7]), sc*q = 8*(sh*q) + (sl*q) and both products are at most
+//    105, so one packed 16-bit multiply makes a plane for four weights without carries between
+//    bytes. Two int32 MFMA chains over the super-block's 256 weights give sum(sh*q*a) and
+//    sum(sl*q*a), combined exactly as (h << 3) + l -- the same integer as the reference's -- and
+//    applied with one f32 update per super-block.
+//  * min term: a small product over sub-blocks with the float scales folded into the operands,
+//    (-dmin*mn) x (da*bsum32), on the bf16 MFMA with each fp32 operand split into bf16 hi + lo
+//    (three products: hi*hi + hi*lo + lo*hi, ~2^-16 relative error), accumulated in f32 straight
+//    into the output tile.
+// Only the f32 summation order differs from the reference.
+//
+// Tiling: a workgroup of 8 waves (two per SIMD, so one wave's VALU work and LDS waits overlap
+// the other's MFMAs) owns 256 rows x 128 tokens; a wave owns 32 rows (its lanes' rows, so a
+// row's scales are per-lane scalars) x 128 tokens (4 MFMA tiles of 32x32). Weights are private
+// to a wave: each lane loads and unpacks its row's half of every super-block straight from HBM
+// into MFMA operand registers. Activations are shared: the workgroup stages each super-block's
+// 128 tokens x 256 int8 (+ the scales and the min-term operand) in LDS, double buffered, one
+// barrier per super-block.
+//
+// MFMA roles: A = activations (tokens as M), B = weights (rows as N). Output lane l holds row
+// l%32 and tokens 8*(v/4) + 4*(l/32) + v%4 for v < 16.
+#include "common.hpp"
+
+namespace hkhip {
+
+
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+
+// Shapes: NW waves per workgroup (32 rows each), TT token tiles of 32 per wave; the workgroup
+// covers 32*NW rows x 32*TT tokens. The large configuration (8, 4) amortizes the weight unpack
+// over 128 tokens; smaller ones keep small matrices spread over the 256 CUs.
+// LDS: a super-block of a token is 256 bytes = 16 chunks of 16; chunk c sits at c ^ (token & 15)
+// so that the 32 tokens one MFMA operand read covers hit distinct banks.
+template <int TOK> struct Q2Smem {
+    int8_t a[2][TOK * 256];
+    uint32_t mb[2][TOK][8]; // per token: 8 bf16 hi (words 0-3), 8 bf16 lo (words 4-7)
+    float da[2][TOK];
+};
+
+struct Mm2Args {
+    const uint8_t *w;
+    uint32_t rows, cols, n;
+    const int8_t *aqs;
+    const float *ad;
+    const int16_t *abs;
+    float *y;
+    const float *bias;
+    int mode;
+    uint32_t rblocks, tblocks;
+};
+
+__device__ __forceinline__ uint4 ldg16(const void *p) { return *reinterpret_cast<const uint4 *>(p); }
+
+// 16 bytes per lane global -> LDS (lane L writes at lds + 16*L). A non-template function: used
+// directly in the kernel template, the builtin keeps the host side from emitting its stub.
+__device__ __forceinline__ void load_lds16(const void *g, void *lds) {
+    __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
+}
+
+// fp32 -> bf16 bits, round to nearest even (finite inputs).
+__device__ __forceinline__ uint32_t bf16_rne(float x) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, x);
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+// x as bf16 hi + bf16 lo (x - hi), packed: hi in bits 0-15, lo in 16-31.
+__device__ __forceinline__ uint32_t bf16_split(float x) {
+    const uint32_t hi = bf16_rne(x);
+    const float r = x - __builtin_bit_cast(float, hi << 16);
+    return hi | (bf16_rne(r) << 16);
+}
+
+// Four nibble bytes (values 0..15) times a 3-bit scale factor: each byte product is at most
+// 105, so a packed 16-bit multiply of the word keeps every byte separate.
+__device__ __forceinline__ uint32_t mul_bytes(uint32_t nib, uint32_t f2) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(us2, nib) * __builtin_bit_cast(us2, f2));
+}
+
+template <int Q2_NW, int Q2_TT>
+__global__ __launch_bounds__(Q2_NW * 64, 2) void mm2_q4k_kernel(Mm2Args a) {
+    constexpr int Q2_ROWS = 32 * Q2_NW, Q2_TOK = 32 * Q2_TT;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
+    Q2Smem<Q2_TOK> &S = *reinterpret_cast<Q2Smem<Q2_TOK> *>(smem_raw);
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t h = lane >> 5, j = lane & 31;
+    const uint32_t K = a.cols, nsb = K / 256;
+
+    // Workgroup -> (row block, token block). The token blocks of one row block are consecutive
+    // workgroups on the same XCD (workgroups go round-robin over the 8 XCDs), so the rows they
+    // share are read from HBM once and then served by that XCD's L2.
+    uint32_t rb, tb;
+    {
+        const uint32_t i = blockIdx.x;
+        if (a.rblocks % 8 == 0) {
+            const uint32_t xcd = i % 8, k = i / 8;
+            rb = xcd * (a.rblocks / 8) + k / a.tblocks;
+            tb = k % a.tblocks;
+        } else {
+            rb = i / a.tblocks;
+            tb = i % a.tblocks;
+        }
+    }
+    const uint32_t r0 = rb * Q2_ROWS, t0 = tb * Q2_TOK;
+    const uint32_t myrow = r0 + 32 * wave + j;
+    const uint32_t wrow = myrow < a.rows ? myrow : a.rows - 1;
+    const uint8_t *wbase = a.w + uint64_t(wrow) * nsb * 144;
+
+    // ---- staging of one super-block of activations ----
+    // The int8 values go global -> LDS directly (global_load_lds_dwordx4: lane L of a wave writes
+    // 16 bytes at the wave's LDS pointer + 16*L), 4 x 1 KB per wave = 16 token rows; the
+    // swizzle is applied on the global side. Threads below 128 load token tid's scale and bsums
+    // into registers and write the min-term operand after the compute.
+    float sda = 0.0f;
+    uint4 sbs0 = make_uint4(0, 0, 0, 0), sbs1 = sbs0;
+    const bool tok_thread = tid < Q2_TOK;
+    auto stage_load = [&](uint32_t sb, uint32_t buf) {
+        // Each wave moves TPW token rows, 4 per 1-KB direct load.
+        constexpr uint32_t TPW = Q2_TOK / Q2_NW;
+        static_assert(TPW % 4 == 0, "token rows per wave");
+#pragma unroll
+        for (uint32_t i = 0; i < TPW / 4; i++) {
+            const uint32_t tl = TPW * wave + 4 * i + lane / 16; // token row in the workgroup
+            const uint32_t c = (lane % 16) ^ (tl & 15);         // chunk this lane's 16 bytes hold
+            const uint32_t tok = t0 + tl, tk = tok < a.n ? tok : a.n - 1;
+            load_lds16(a.aqs + uint64_t(tk) * K + 256 * sb + 16 * c, &S.a[buf][(TPW * wave + 4 * i) * 256]);
+        }
+        if (tok_thread) {
+            const uint32_t tok = t0 + tid, tk = tok < a.n ? tok : a.n - 1;
+            sda = a.ad[uint64_t(tk) * nsb + sb];
+            const int16_t *bs = a.abs + uint64_t(tk) * (K / 16) + 16 * sb;
+            sbs0 = ldg16(bs);
+            sbs1 = ldg16(bs + 8);
+        }
+    };
+    auto stage_store = [&](uint32_t buf) {
+        if (tok_thread) {
+            const bool ok = t0 + tid < a.n;
+            const uint32_t bw[8] = {sbs0.x, sbs0.y, sbs0.z, sbs0.w, sbs1.x, sbs1.y, sbs1.z, sbs1.w};
+            uint32_t hw[4], lw[4];
+#pragma unroll
+            for (int s = 0; s < 8; s++) {
+                const int b32 = int(int16_t(bw[s] & 0xFFFF)) + int(int16_t(bw[s] >> 16));
+                const uint32_t sp = ok ? bf16_split(sda * (float)b32) : 0u;
+                if (s & 1) {
+                    hw[s / 2] |= sp << 16;
+                    lw[s / 2] |= sp & 0xFFFF0000u;
+                } else {
+                    hw[s / 2] = sp & 0xFFFFu;
+                    lw[s / 2] = sp >> 16;
+                }
+            }
+            uint4 *mb = reinterpret_cast<uint4 *>(S.mb[buf][tid]);
+            mb[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+            mb[1] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+            S.da[buf][tid] = ok ? sda : 0.0f;
+        }
+    };
+
+    // ---- this lane's weights: its row's half (h) of a super-block ----
+    uint4 wh, wq[4];
+    auto wload = [&](uint32_t sb) {
+        const uint8_t *blk = wbase + uint64_t(sb) * 144;
+        wh = ldg16(blk);
+#pragma unroll
+        for (int p = 0; p < 4; p++) wq[p] = ldg16(blk + 16 + 32 * p + 16 * h);
+    };
+
+    v16f acc[Q2_TT];
+#pragma unroll
+    for (int t = 0; t < Q2_TT; t++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[t][v] = 0.0f;
+
+    stage_load(0, 0);
+    wload(0);
+    stage_store(0);
+    __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): the direct-to-LDS loads have landed
+    __syncthreads();
+
+    for (uint32_t sb = 0; sb < nsb; sb++) {
+        const uint32_t buf = sb & 1;
+        const uint4 ch = wh, c0 = wq[0], c1 = wq[1], c2 = wq[2], c3 = wq[3];
+        const uint32_t nx = sb + 1 < nsb ? sb + 1 : sb;
+        stage_load(nx, buf ^ 1);
+
+        // Unpack: scales (vecdot.zig:461-474 word form), then both planes of the 8 sub-blocks.
+        const uint32_t k1 = 0x3f3f3f3fu, k2 = 0x0f0f0f0fu, k3 = 0x03030303u;
+        const uint32_t scl = ch.y & k1, mnl = ch.z & k1;
+        const uint32_t sch = (ch.w & k2) | (((ch.y >> 6) & k3) << 4);
+        const uint32_t mnh = ((ch.w >> 4) & k2) | (((ch.z >> 6) & k3) << 4);
+        const float d = f16_bits_to_f32(ch.x & 0xFFFF), dmin = f16_bits_to_f32(ch.x >> 16);
+        v4i bhi[8], blo[8];
+        const uint4 cq[4] = {c0, c1, c2, c3};
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const uint32_t se = (p < 2 ? scl >> (16 * p) : sch >> (16 * (p - 2))) & 0xFF;
+            const uint32_t so = (p < 2 ? scl >> (16 * p + 8) : sch >> (16 * (p - 2) + 8)) & 0xFF;
+            const uint32_t she = (se >> 3) * 0x00010001u, sle = (se & 7) * 0x00010001u;
+            const uint32_t sho = (so >> 3) * 0x00010001u, slo = (so & 7) * 0x00010001u;
+            const uint32_t qw[4] = {cq[p].x, cq[p].y, cq[p].z, cq[p].w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t ne = qw[i] & 0x0F0F0F0Fu, no = (qw[i] >> 4) & 0x0F0F0F0Fu;
+                bhi[2 * p][i] = int(mul_bytes(ne, she));
+                blo[2 * p][i] = int(mul_bytes(ne, sle));
+                bhi[2 * p + 1][i] = int(mul_bytes(no, sho));
+                blo[2 * p + 1][i] = int(mul_bytes(no, slo));
+            }
+        }
+        // Min-term operand of this lane's row: -dmin*mn for sub-blocks 4h..4h+3, bf16 hi / lo.
+        v4s mhi, mlo;
+        {
+            const uint32_t mw = h ? mnh : mnl;
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                const uint32_t sp = bf16_split(-dmin * (float)((mw >> (8 * s)) & 0xFF));
+                mhi[s] = short(sp & 0xFFFF);
+                mlo[s] = short(sp >> 16);
+            }
+        }
+
+        // A operand of tile t, sub-block s: token 32t + j, chunk 2s + h (swizzled).
+        const int8_t *abase = &S.a[buf][j * 256];
+        const uint32_t sw = j & 15;
+        v4i av[8];
+        auto load_a = [&](int t) {
+#pragma unroll
+            for (int s = 0; s < 8; s++)
+                av[s] = *reinterpret_cast<const v4i *>(abase + 32 * t * 256 + 16 * ((2 * s + h) ^ sw));
+        };
+#ifndef MM2_NO_PREFETCH
+        load_a(0);
+#endif
+#pragma unroll
+        for (int t = 0; t < Q2_TT; t++) {
+            // One accumulator: the sh-plane chain, times 8, then the sl-plane chain on top.
+            v16i sacc = {};
+#ifdef MM2_NO_PREFETCH
+            load_a(t);
+#endif
+#pragma unroll
+            for (int s = 0; s < 8; s++) sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[s], bhi[s], sacc, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 16; v++) sacc[v] <<= 3;
+#pragma unroll
+            for (int s = 0; s < 8; s++) sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[s], blo[s], sacc, 0, 0, 0);
+#ifndef MM2_NO_PREFETCH
+            if (t + 1 < Q2_TT) load_a(t + 1);
+#endif
+            if (t == (Q2_TT > 1 ? 1 : 0)) wload(nx); // next super-block's weights, once this one's raw words are dead
+            // Token scales of this lane's 16 outputs: tokens 32t + 8g + 4h + (0..3).
+            const float4 *dap = reinterpret_cast<const float4 *>(&S.da[buf][32 * t + 4 * h]);
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const float4 dv = dap[2 * g];
+                const float ds[4] = {dv.x, dv.y, dv.z, dv.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int v = 4 * g + e;
+                    acc[t][v] = fmaf((float)sacc[v], d * ds[e], acc[t][v]);
+                }
+            }
+            // Min term: tokens' da*bsum32 (A) x rows' -dmin*mn (B), bf16 hi/lo split.
+            const uint32_t *mbp = S.mb[buf][32 * t + j];
+            const uint2 ahi = *reinterpret_cast<const uint2 *>(mbp + 2 * h);
+            const uint2 alo = *reinterpret_cast<const uint2 *>(mbp + 4 + 2 * h);
+            const v4s ah = __builtin_bit_cast(v4s, ahi), al = __builtin_bit_cast(v4s, alo);
+            acc[t] = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(ah, mhi, acc[t], 0, 0, 0);
+            acc[t] = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(ah, mlo, acc[t], 0, 0, 0);
+            acc[t] = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(al, mhi, acc[t], 0, 0, 0);
+        }
+
+        stage_store(buf ^ 1);
+        __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): next super-block's activations are in LDS
+        __syncthreads();
+    }
+
+    // ---- store: y[token][row], bias, accumulate ----
+    if (myrow < a.rows) {
+        const float b = a.bias ? a.bias[myrow] : 0.0f;
+#pragma unroll
+        for (int t = 0; t < Q2_TT; t++) {
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const uint32_t tok = t0 + 32 * t + 8 * (v / 4) + 4 * h + (v % 4);
+                if (tok < a.n) {
+                    float *dst = a.y + uint64_t(tok) * a.rows + myrow;
+                    if (a.mode == HKHIP_ACCUMULATE)
+                        *dst += acc[t][v] + b;
+                    else
+                        *dst = acc[t][v] + b;
+                }
+            }
+        }
+    }
+}
+
+
+
+bool mm2_supports(int t, uint32_t rows, uint32_t cols, uint32_t n) {
+    return t == HKHIP_Q4_K && cols % 256 == 0 && rows > 0 && n > 0;
+}
+
+typedef void (*mm2_kernel_t)(Mm2Args);
+
+template <int NW, int TT>
+static hipError_t launch_mm2_cfg(const Mm2Args &a0, hipStream_t s) {
+    const mm2_kernel_t k = mm2_q4k_kernel<NW, TT>;
+    static bool attr = false;
+    if (!attr) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  int(sizeof(Q2Smem<32 * TT>)));
+        attr = true;
+    }
+    Mm2Args a = a0;
+    a.rblocks = (a.rows + 32 * NW - 1) / (32 * NW);
+    a.tblocks = (a.n + 32 * TT - 1) / (32 * TT);
+    hipLaunchKernelGGL(k, dim3(a.rblocks * a.tblocks), dim3(NW * 64), sizeof(Q2Smem<32 * TT>), s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_mm2(int t, const uint8_t *w, uint32_t rows, uint32_t cols, const uint8_t *xq, uint32_t n, float *y,
+                      const float *bias, int mode, hipStream_t s) {
+    if (!mm2_supports(t, rows, cols, n)) return hipErrorInvalidValue;
+    const ActLayout A = act_layout(n, cols);
+    Mm2Args a{};
+    a.w = w;
+    a.rows = rows;
+    a.cols = cols;
+    a.n = n;
+    a.aqs = reinterpret_cast<const int8_t *>(xq + A.k_qs);
+    a.ad = reinterpret_cast<const float *>(xq + A.k_d);
+    a.abs = reinterpret_cast<const int16_t *>(xq + A.k_bs);
+    a.y = y;
+    a.bias = bias;
+    a.mode = mode;
+    // The largest tile that still gives most of the 256 CUs a workgroup.
+    auto blocks = [&](uint32_t nw, uint32_t tt) {
+        return ((rows + 32 * nw - 1) / (32 * nw)) * ((n + 32 * tt - 1) / (32 * tt));
+    };
+    if (blocks(8, 4) >= 192) return launch_mm2_cfg<8, 4>(a, s);
+    if (blocks(4, 2) >= 160) return launch_mm2_cfg<4, 2>(a, s);
+    return launch_mm2_cfg<4, 1>(a, s);
+}
+
+} // namespace hkhip
