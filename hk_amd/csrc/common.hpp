@@ -69,9 +69,11 @@ inline WLayout weight_layout(int t, uint32_t rows, uint32_t cols) {
 // Activation-quant buffer for n tokens of k values. Both kinds live side by side so one
 // input serves Q8_0 / IQ4_NL (A8) and Q4_K / Q6_K (Q8K) products alike:
 //   a8_qs [n][k] i8, a8_d [n][k/32] f32, a8_s [n][k/32] i32,
-//   k_qs  [n][k] i8, k_d  [n][k/256] f32, k_bs [n][k/16] i16
+//   k_qs  [n][k] i8, k_d  [n][k/256] f32, k_bs [n][k/16] i16,
+//   k_mb  [n][k/256][16] bf16: per super-block, d*bsum32 of its 8 sub-blocks split in bf16 hi (8)
+//         then lo (8) -- the token-side operand of the GEMM's min term, precomputed once
 struct ActLayout {
-    uint64_t a8_qs, a8_d, a8_s, k_qs, k_d, k_bs, total;
+    uint64_t a8_qs, a8_d, a8_s, k_qs, k_d, k_bs, k_mb, total;
 };
 
 inline ActLayout act_layout(uint32_t n, uint32_t k) {
@@ -84,6 +86,7 @@ inline ActLayout act_layout(uint32_t n, uint32_t k) {
     L.k_qs = o;  o = align256(o + (k % QK_K == 0 ? nk : 0));
     L.k_d = o;   o = align256(o + (k % QK_K == 0 ? nk / QK_K * 4 : 0));
     L.k_bs = o;  o = align256(o + (k % QK_K == 0 ? nk / 16 * 2 : 0));
+    L.k_mb = o;  o = align256(o + (k % QK_K == 0 ? nk / QK_K * 32 : 0));
     L.total = o;
     return L;
 }

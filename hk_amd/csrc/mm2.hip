@@ -27,6 +27,8 @@
 //
 // MFMA roles: A = activations (tokens as M), B = weights (rows as N). Output lane l holds row
 // l%32 and tokens 8*(v/4) + 4*(l/32) + v%4 for v < 16.
+#include <stdlib.h>
+
 #include "common.hpp"
 
 namespace hkhip {
@@ -38,15 +40,22 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef short v4s __attribute__((ext_vector_type(4)));
 typedef unsigned short us2 __attribute__((ext_vector_type(2)));
 
-// Shapes: NW waves per workgroup (32 rows each), TT token tiles of 32 per wave; the workgroup
-// covers 32*NW rows x 32*TT tokens. The large configuration (8, 4) amortizes the weight unpack
-// over 128 tokens; smaller ones keep small matrices spread over the 256 CUs.
-// LDS: a super-block of a token is 256 bytes = 16 chunks of 16; chunk c sits at c ^ (token & 15)
-// so that the 32 tokens one MFMA operand read covers hit distinct banks.
-template <int TOK> struct Q2Smem {
-    int8_t a[2][TOK * 256];
-    uint32_t mb[2][TOK][8]; // per token: 8 bf16 hi (words 0-3), 8 bf16 lo (words 4-7)
-    float da[2][TOK];
+// Shapes: NW waves per workgroup (32 rows each), TT token tiles of 32 per wave, NB super-blocks
+// in flight; the workgroup covers 32*NW rows x 32*TT tokens. The large configuration amortizes
+// the weight unpack over 128 tokens; smaller ones keep small matrices spread over the CUs.
+// Everything a super-block needs arrives by direct global -> LDS loads into a ring of NB slots:
+//   a   token rows, 256 int8 each; 16-byte chunk c of token t sits at c ^ (t & 15) so the 32
+//       tokens one MFMA operand read covers hit distinct banks
+//   w   per wave, its 32 rows' 144-byte blocks back to back
+//   mb  per token, the min-term operand (k_mb of the activation buffer, 32 bytes)
+//   da  per token, the Q8K scale
+// Every wave issues the same loads (waves past the tokens load duplicates into their own spare
+// entries), so the in-order memory counter can be waited on with a constant.
+template <int TOK, int NW> struct Q2Slot {
+    int8_t a[TOK * 256];
+    uint8_t w[NW][4608];
+    uint32_t mb[NW * 32][8]; // token t at mb[t]; wave m's load fills tokens 32m..32m+31
+    float da[NW * 64];       // token t at da[t]; wave m's load fills tokens 64m..64m+63
 };
 
 struct Mm2Args {
@@ -55,6 +64,7 @@ struct Mm2Args {
     const int8_t *aqs;
     const float *ad;
     const int16_t *abs;
+    const uint8_t *amb; // k_mb: per token and super-block, 32 bytes
     float *y;
     const float *bias;
     int mode;
@@ -67,6 +77,10 @@ __device__ __forceinline__ uint4 ldg16(const void *p) { return *reinterpret_cast
 // directly in the kernel template, the builtin keeps the host side from emitting its stub.
 __device__ __forceinline__ void load_lds16(const void *g, void *lds) {
     __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
+}
+
+__device__ __forceinline__ void load_lds4(const void *g, void *lds) {
+    __builtin_amdgcn_global_load_lds(g, lds, 4, 0, 0);
 }
 
 // fp32 -> bf16 bits, round to nearest even (finite inputs).
@@ -87,8 +101,17 @@ __device__ __forceinline__ uint32_t mul_bytes(uint32_t nib, uint32_t f2) {
     return __builtin_bit_cast(uint32_t, __builtin_bit_cast(us2, nib) * __builtin_bit_cast(us2, f2));
 }
 
+template <int TOK> struct Q2Smem {
+    int8_t a[2][TOK * 256];
+    uint32_t mb[2][TOK][8]; // per token: 8 bf16 hi (words 0-3), 8 bf16 lo (words 4-7)
+    float da[2][TOK];
+};
+
+// Large-tile variant: weights go global -> registers (each lane its own row half), loaded
+// while the previous super-block computes; activations and token data through LDS, double
+// buffered. Measured faster than staging the weights in LDS for this tile.
 template <int Q2_NW, int Q2_TT>
-__global__ __launch_bounds__(Q2_NW * 64, 2) void mm2_q4k_kernel(Mm2Args a) {
+__global__ __launch_bounds__(Q2_NW * 64, 2) void mm2_q4k_reg_kernel(Mm2Args a) {
     constexpr int Q2_ROWS = 32 * Q2_NW, Q2_TOK = 32 * Q2_TT;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
     Q2Smem<Q2_TOK> &S = *reinterpret_cast<Q2Smem<Q2_TOK> *>(smem_raw);
@@ -309,6 +332,209 @@ __global__ __launch_bounds__(Q2_NW * 64, 2) void mm2_q4k_kernel(Mm2Args a) {
 
 
 
+template <int NW, int TT, int NB>
+__global__ __launch_bounds__(NW * 64, 2) void mm2_q4k_kernel(Mm2Args a) {
+    constexpr int ROWS = 32 * NW, TOK = 32 * TT;
+    using Slot = Q2Slot<TOK, NW>;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
+    Slot *ring = reinterpret_cast<Slot *>(smem_raw);
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t h = lane >> 5, j = lane & 31;
+    const uint32_t K = a.cols, nsb = K / 256;
+
+    // Workgroup -> (row block, token block). The token blocks of one row block are consecutive
+    // workgroups on the same XCD (workgroups go round-robin over the 8 XCDs), so the rows they
+    // share are read from HBM once and then served by that XCD's L2.
+    uint32_t rb, tb;
+    {
+        const uint32_t i = blockIdx.x;
+        if (a.rblocks % 8 == 0) {
+            const uint32_t xcd = i % 8, k = i / 8;
+            rb = xcd * (a.rblocks / 8) + k / a.tblocks;
+            tb = k % a.tblocks;
+        } else {
+            rb = i / a.tblocks;
+            tb = i % a.tblocks;
+        }
+    }
+    const uint32_t r0 = rb * ROWS, t0 = tb * TOK;
+    const uint32_t myrow = r0 + 32 * wave + j;
+
+    // ---- the direct loads of one super-block into a slot (CPW per wave) ----
+    constexpr uint32_t TPW = TOK / NW; // token rows per wave
+    static_assert(TPW % 4 == 0, "token rows per wave");
+    constexpr uint32_t CPW = TPW / 4 + 6 + 1 + 1; // a + w + mb + da
+    // Weight bytes of this wave: 16-byte piece P (64*i + lane, i < 4) is byte 16*(P%9) of row
+    // P/9's block; the last 512 bytes (pieces 256..287) go as 4-byte words 1024 + 64*i + lane.
+    const uint8_t *wsrc[6];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t P = 64 * i + lane;
+        const uint32_t row = r0 + 32 * wave + P / 9, rr = row < a.rows ? row : a.rows - 1;
+        wsrc[i] = a.w + uint64_t(rr) * nsb * 144 + 16 * (P % 9);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const uint32_t Wd = 1024 + 64 * i + lane; // 4-byte word index in the wave's area
+        const uint32_t row = r0 + 32 * wave + Wd / 36, rr = row < a.rows ? row : a.rows - 1;
+        wsrc[4 + i] = a.w + uint64_t(rr) * nsb * 144 + 4 * (Wd % 36);
+    }
+    auto issue = [&](uint32_t sb, uint32_t slot) {
+        Slot &S = ring[slot];
+#pragma unroll
+        for (uint32_t i = 0; i < TPW / 4; i++) {
+            const uint32_t tl = TPW * wave + 4 * i + lane / 16;
+            const uint32_t c = (lane % 16) ^ (tl & 15);
+            const uint32_t tok = t0 + tl, tk = tok < a.n ? tok : a.n - 1;
+            load_lds16(a.aqs + uint64_t(tk) * K + 256 * sb + 16 * c, &S.a[(TPW * wave + 4 * i) * 256]);
+        }
+        const uint64_t wo = uint64_t(sb) * 144;
+#pragma unroll
+        for (int i = 0; i < 4; i++) load_lds16(wsrc[i] + wo, &S.w[wave][1024 * i]);
+#pragma unroll
+        for (int i = 0; i < 2; i++) load_lds4(wsrc[4 + i] + wo, &S.w[wave][4096 + 256 * i]);
+        {
+            const uint32_t tl = 32 * wave + lane / 2, tok = t0 + (tl < TOK ? tl : 0);
+            const uint32_t tk = tok < a.n ? tok : a.n - 1;
+            load_lds16(a.amb + (uint64_t(tk) * nsb + sb) * 32 + 16 * (lane & 1), &S.mb[32 * wave][0]);
+        }
+        {
+            const uint32_t tl = 64 * wave + lane, tok = t0 + (tl < TOK ? tl : 0);
+            const uint32_t tk = tok < a.n ? tok : a.n - 1;
+            load_lds4(a.ad + uint64_t(tk) * nsb + sb, &S.da[64 * wave]);
+        }
+    };
+
+    v16f acc[TT];
+#pragma unroll
+    for (int t = 0; t < TT; t++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[t][v] = 0.0f;
+
+    // Prologue: NB-1 super-blocks in flight.
+#pragma unroll
+    for (int p = 0; p < NB - 1; p++) issue(p < int(nsb) ? p : nsb - 1, p);
+    // Wait for slot 0 (the loads of NB-2 later super-blocks may stay in flight).
+    __builtin_amdgcn_s_waitcnt(0x0F70 & ~0xF | ((CPW * (NB - 2)) & 0xF) | (((CPW * (NB - 2)) >> 4) << 14));
+    __syncthreads();
+
+    for (uint32_t sb = 0; sb < nsb; sb++) {
+        const uint32_t slot = sb % NB;
+        {
+            const uint32_t ahead = sb + NB - 1;
+            issue(ahead < nsb ? ahead : nsb - 1, ahead % NB);
+        }
+        Slot &S = ring[slot];
+
+        // Unpack this lane's row half (h) from LDS: header, then both planes of 8 sub-blocks.
+        const uint8_t *blk = &S.w[wave][144 * j];
+        const uint4 ch = *reinterpret_cast<const uint4 *>(blk);
+        uint4 cq[4];
+#pragma unroll
+        for (int p = 0; p < 4; p++) cq[p] = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * p + 16 * h);
+        // Scales: vecdot.zig:461-474 word form.
+        const uint32_t k1 = 0x3f3f3f3fu, k2 = 0x0f0f0f0fu, k3 = 0x03030303u;
+        const uint32_t scl = ch.y & k1, mnl = ch.z & k1;
+        const uint32_t sch = (ch.w & k2) | (((ch.y >> 6) & k3) << 4);
+        const uint32_t mnh = ((ch.w >> 4) & k2) | (((ch.z >> 6) & k3) << 4);
+        const float d = f16_bits_to_f32(ch.x & 0xFFFF), dmin = f16_bits_to_f32(ch.x >> 16);
+        v4i bhi[8], blo[8];
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const uint32_t se = (p < 2 ? scl >> (16 * p) : sch >> (16 * (p - 2))) & 0xFF;
+            const uint32_t so = (p < 2 ? scl >> (16 * p + 8) : sch >> (16 * (p - 2) + 8)) & 0xFF;
+            const uint32_t she = (se >> 3) * 0x00010001u, sle = (se & 7) * 0x00010001u;
+            const uint32_t sho = (so >> 3) * 0x00010001u, slo = (so & 7) * 0x00010001u;
+            const uint32_t qw[4] = {cq[p].x, cq[p].y, cq[p].z, cq[p].w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t ne = qw[i] & 0x0F0F0F0Fu, no = (qw[i] >> 4) & 0x0F0F0F0Fu;
+                bhi[2 * p][i] = int(mul_bytes(ne, she));
+                blo[2 * p][i] = int(mul_bytes(ne, sle));
+                bhi[2 * p + 1][i] = int(mul_bytes(no, sho));
+                blo[2 * p + 1][i] = int(mul_bytes(no, slo));
+            }
+        }
+        // Min-term operand of this lane's row: -dmin*mn for sub-blocks 4h..4h+3, bf16 hi / lo.
+        v4s mhi, mlo;
+        {
+            const uint32_t mw = h ? mnh : mnl;
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                const uint32_t sp = bf16_split(-dmin * (float)((mw >> (8 * s)) & 0xFF));
+                mhi[s] = short(sp & 0xFFFF);
+                mlo[s] = short(sp >> 16);
+            }
+        }
+
+        // A operand of tile t, sub-block s: token 32t + j, chunk 2s + h (swizzled).
+        const int8_t *abase = &S.a[j * 256];
+        const uint32_t sw = j & 15;
+        v4i av[8];
+        auto load_a = [&](int t) {
+#pragma unroll
+            for (int s = 0; s < 8; s++)
+                av[s] = *reinterpret_cast<const v4i *>(abase + 32 * t * 256 + 16 * ((2 * s + h) ^ sw));
+        };
+        load_a(0);
+#pragma unroll
+        for (int t = 0; t < TT; t++) {
+            // One accumulator: the sh-plane chain, times 8, then the sl-plane chain on top.
+            v16i sacc = {};
+#pragma unroll
+            for (int s = 0; s < 8; s++) sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[s], bhi[s], sacc, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 16; v++) sacc[v] <<= 3;
+#pragma unroll
+            for (int s = 0; s < 8; s++) sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[s], blo[s], sacc, 0, 0, 0);
+            if (t + 1 < TT) load_a(t + 1);
+            // Token scales of this lane's 16 outputs: tokens 32t + 8g + 4h + (0..3).
+            const float4 *dap = reinterpret_cast<const float4 *>(&S.da[32 * t + 4 * h]);
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const float4 dv = dap[2 * g];
+                const float ds[4] = {dv.x, dv.y, dv.z, dv.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int v = 4 * g + e;
+                    acc[t][v] = fmaf((float)sacc[v], d * ds[e], acc[t][v]);
+                }
+            }
+            // Min term: tokens' da*bsum32 (A) x rows' -dmin*mn (B), bf16 hi/lo split.
+            const uint32_t *mbp = S.mb[32 * t + j];
+            const uint2 ahi = *reinterpret_cast<const uint2 *>(mbp + 2 * h);
+            const uint2 alo = *reinterpret_cast<const uint2 *>(mbp + 4 + 2 * h);
+            const v4s ah = __builtin_bit_cast(v4s, ahi), al = __builtin_bit_cast(v4s, alo);
+            acc[t] = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(ah, mhi, acc[t], 0, 0, 0);
+            acc[t] = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(ah, mlo, acc[t], 0, 0, 0);
+            acc[t] = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(al, mhi, acc[t], 0, 0, 0);
+        }
+        // The next super-block's slot has landed once at most NB-2 later issues are pending.
+        __builtin_amdgcn_s_waitcnt(0x0F70 & ~0xF | ((CPW * (NB - 2)) & 0xF) | (((CPW * (NB - 2)) >> 4) << 14));
+        __syncthreads();
+    }
+
+    // ---- store: y[token][row], bias, accumulate ----
+    if (myrow < a.rows) {
+        const float b = a.bias ? a.bias[myrow] : 0.0f;
+#pragma unroll
+        for (int t = 0; t < TT; t++) {
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const uint32_t tok = t0 + 32 * t + 8 * (v / 4) + 4 * h + (v % 4);
+                if (tok < a.n) {
+                    float *dst = a.y + uint64_t(tok) * a.rows + myrow;
+                    if (a.mode == HKHIP_ACCUMULATE)
+                        *dst += acc[t][v] + b;
+                    else
+                        *dst = acc[t][v] + b;
+                }
+            }
+        }
+    }
+}
+
 bool mm2_supports(int t, uint32_t rows, uint32_t cols, uint32_t n) {
     return t == HKHIP_Q4_K && cols % 256 == 0 && rows > 0 && n > 0;
 }
@@ -316,18 +542,35 @@ bool mm2_supports(int t, uint32_t rows, uint32_t cols, uint32_t n) {
 typedef void (*mm2_kernel_t)(Mm2Args);
 
 template <int NW, int TT>
-static hipError_t launch_mm2_cfg(const Mm2Args &a0, hipStream_t s) {
-    const mm2_kernel_t k = mm2_q4k_kernel<NW, TT>;
+static hipError_t launch_mm2_reg(const Mm2Args &a0, hipStream_t s) {
+    const mm2_kernel_t k = mm2_q4k_reg_kernel<NW, TT>;
+    constexpr size_t lds = sizeof(Q2Smem<32 * TT>);
     static bool attr = false;
     if (!attr) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  int(sizeof(Q2Smem<32 * TT>)));
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k), hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
         attr = true;
     }
     Mm2Args a = a0;
     a.rblocks = (a.rows + 32 * NW - 1) / (32 * NW);
     a.tblocks = (a.n + 32 * TT - 1) / (32 * TT);
-    hipLaunchKernelGGL(k, dim3(a.rblocks * a.tblocks), dim3(NW * 64), sizeof(Q2Smem<32 * TT>), s, a);
+    hipLaunchKernelGGL(k, dim3(a.rblocks * a.tblocks), dim3(NW * 64), lds, s, a);
+    return hipGetLastError();
+}
+
+template <int NW, int TT, int NB>
+static hipError_t launch_mm2_cfg(const Mm2Args &a0, hipStream_t s) {
+    const mm2_kernel_t k = mm2_q4k_kernel<NW, TT, NB>;
+    constexpr size_t lds = NB * sizeof(Q2Slot<32 * TT, NW>);
+    static_assert(lds <= 160 * 1024, "LDS");
+    static bool attr = false;
+    if (!attr) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k), hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+        attr = true;
+    }
+    Mm2Args a = a0;
+    a.rblocks = (a.rows + 32 * NW - 1) / (32 * NW);
+    a.tblocks = (a.n + 32 * TT - 1) / (32 * TT);
+    hipLaunchKernelGGL(k, dim3(a.rblocks * a.tblocks), dim3(NW * 64), lds, s, a);
     return hipGetLastError();
 }
 
@@ -343,6 +586,7 @@ hipError_t launch_mm2(int t, const uint8_t *w, uint32_t rows, uint32_t cols, con
     a.aqs = reinterpret_cast<const int8_t *>(xq + A.k_qs);
     a.ad = reinterpret_cast<const float *>(xq + A.k_d);
     a.abs = reinterpret_cast<const int16_t *>(xq + A.k_bs);
+    a.amb = xq + A.k_mb;
     a.y = y;
     a.bias = bias;
     a.mode = mode;
@@ -350,9 +594,18 @@ hipError_t launch_mm2(int t, const uint8_t *w, uint32_t rows, uint32_t cols, con
     auto blocks = [&](uint32_t nw, uint32_t tt) {
         return ((rows + 32 * nw - 1) / (32 * nw)) * ((n + 32 * tt - 1) / (32 * tt));
     };
-    if (blocks(8, 4) >= 192) return launch_mm2_cfg<8, 4>(a, s);
-    if (blocks(4, 2) >= 160) return launch_mm2_cfg<4, 2>(a, s);
-    return launch_mm2_cfg<4, 1>(a, s);
+    static const int force = getenv("HKHIP_MM2_CFG") ? atoi(getenv("HKHIP_MM2_CFG")) : 0; // experiments only
+    if (force == 84) return launch_mm2_cfg<8, 4, 2>(a, s);
+    if (force == 840) return launch_mm2_reg<8, 4>(a, s);
+    if (force == 42) return launch_mm2_cfg<4, 2, 2>(a, s);
+    if (force == 41) return launch_mm2_cfg<4, 1, 2>(a, s);
+    if (force == 21) return launch_mm2_cfg<2, 1, 3>(a, s);
+    if (force == 11) return launch_mm2_cfg<1, 1, 3>(a, s);
+    if (blocks(8, 4) >= 192) return launch_mm2_reg<8, 4>(a, s);
+    if (blocks(4, 2) >= 160) return launch_mm2_cfg<4, 2, 2>(a, s);
+    if (blocks(4, 1) >= 256) return launch_mm2_cfg<4, 1, 2>(a, s);
+    if (blocks(2, 1) >= 256) return launch_mm2_cfg<2, 1, 3>(a, s);
+    return launch_mm2_cfg<1, 1, 3>(a, s);
 }
 
 } // namespace hkhip

@@ -19,8 +19,14 @@ __global__ void qact_a8_kernel(const float *__restrict__ x, uint64_t total, int8
 }
 
 // Q8K: one wave per 256-value block, four consecutive values per lane.
+// fp32 -> bf16 bits, round to nearest even (finite inputs).
+__device__ __forceinline__ uint32_t bf16_bits_rne(float x) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, x);
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
 __global__ void qact_q8k_kernel(const float *__restrict__ x, uint64_t nblocks, int8_t *__restrict__ qs,
-                                float *__restrict__ dout, int16_t *__restrict__ bsout) {
+                                float *__restrict__ dout, int16_t *__restrict__ bsout, uint16_t *__restrict__ mbout) {
     const uint32_t lane = threadIdx.x & 63;
     const uint64_t b = (uint64_t(blockIdx.x) * blockDim.x + threadIdx.x) / 64;
     if (b >= nblocks) return; // whole waves exit together
@@ -28,6 +34,16 @@ __global__ void qact_q8k_kernel(const float *__restrict__ x, uint64_t nblocks, i
     reinterpret_cast<uint32_t *>(qs + b * QK_K)[lane] = r.packed;
     if ((lane & 3) == 0) bsout[b * 16 + lane / 4] = (int16_t)r.bsum;
     if (lane == 0) dout[b] = r.d;
+    // GEMM min-term operand: d * (sum over the 32 values of sub-block s) as bf16 hi + lo. The
+    // 16-value sums sit in lanes 4g; sub-block s = groups 2s and 2s+1 (lanes 8s and 8s+4).
+    const int b32 = r.bsum + __shfl_down(r.bsum, 4);
+    if ((lane & 7) == 0) {
+        const float v = r.d * (float)b32;
+        const uint32_t hi = bf16_bits_rne(v);
+        const uint32_t lo = bf16_bits_rne(v - __builtin_bit_cast(float, hi << 16));
+        mbout[b * 16 + lane / 8] = uint16_t(hi);
+        mbout[b * 16 + 8 + lane / 8] = uint16_t(lo);
+    }
 }
 
 hipError_t launch_qact(const float *x, uint32_t n, uint32_t k, int kind, uint8_t *xq, hipStream_t s) {
@@ -44,7 +60,8 @@ hipError_t launch_qact(const float *x, uint32_t n, uint32_t k, int kind, uint8_t
         uint64_t grid = (nb + 3) / 4; // 4 waves per workgroup
         qact_q8k_kernel<<<uint32_t(grid), 256, 0, s>>>(x, nb, reinterpret_cast<int8_t *>(xq + L.k_qs),
                                                        reinterpret_cast<float *>(xq + L.k_d),
-                                                       reinterpret_cast<int16_t *>(xq + L.k_bs));
+                                                       reinterpret_cast<int16_t *>(xq + L.k_bs),
+                                                       reinterpret_cast<uint16_t *>(xq + L.k_mb));
     }
     return hipGetLastError();
 }
