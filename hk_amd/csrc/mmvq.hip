@@ -135,10 +135,16 @@ template <> struct MvFmt<HKHIP_Q4_K> {
         a.d = A.d[t * (A.K / 256) + (u >> 2)];
         return a;
     }
-    __device__ static void dot(const W &w, uint32_t u, const AU &a, float &acc, float &corr) {
+    // Weight-side work of a unit, done once for all tokens: the two sub-block scales and mins
+    // (scalesMinsK4 word unpack, vecdot.zig:461-474) and the unpacked nibbles.
+    struct P {
+        uint32_t lo[8], hi[8];
+        int sc0, sc1, mn0, mn1;
+        float d, dmin;
+    };
+    __device__ static P prep(const W &w, uint32_t u) {
         const uint32_t q = u & 3;
         const uint4 h = w.h;
-        // scalesMinsK4 word unpack (vecdot.zig:461-474), then sub-blocks 2q and 2q+1.
         const uint32_t k1 = 0x3f3f3f3fu, k2 = 0x0f0f0f0fu, k3 = 0x03030303u;
         const uint32_t sh = 16 * (q & 1);
         uint32_t scw, mnw;
@@ -149,17 +155,31 @@ template <> struct MvFmt<HKHIP_Q4_K> {
             scw = ((h.w & k2) | (((h.y >> 6) & k3) << 4)) >> sh;
             mnw = (((h.w >> 4) & k2) | (((h.z >> 6) & k3) << 4)) >> sh;
         }
-        const int sc0 = scw & 0xFF, sc1 = (scw >> 8) & 0xFF, mn0 = mnw & 0xFF, mn1 = (mnw >> 8) & 0xFF;
+        P p;
+        p.sc0 = scw & 0xFF; p.sc1 = (scw >> 8) & 0xFF; p.mn0 = mnw & 0xFF; p.mn1 = (mnw >> 8) & 0xFF;
         const uint32_t qw[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            p.lo[i] = qw[i] & 0x0F0F0F0Fu;
+            p.hi[i] = (qw[i] >> 4) & 0x0F0F0F0Fu;
+        }
+        p.d = f16_bits_to_f32(h.x & 0xFFFF);
+        p.dmin = f16_bits_to_f32(h.x >> 16);
+        return p;
+    }
+    // One token: sub-blocks 2q and 2q+1 of the super-block (k4Block, vecdot.zig:482-522).
+    __device__ static void dotp(const P &p, const AU &a, float &acc, float &corr) {
         int slo = 0, shi = 0;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            slo = sdot4(qw[i] & 0x0F0F0F0Fu, a.q[i], slo);
-            shi = sdot4((qw[i] >> 4) & 0x0F0F0F0Fu, a.q[8 + i], shi);
+            slo = sdot4(p.lo[i], a.q[i], slo);
+            shi = sdot4(p.hi[i], a.q[8 + i], shi);
         }
-        const float d = f16_bits_to_f32(h.x & 0xFFFF), dmin = f16_bits_to_f32(h.x >> 16);
-        acc = fmaf((float)(slo * sc0 + shi * sc1), d * a.d, acc);
-        corr = fmaf((float)(mn0 * a.b01 + mn1 * a.b23), dmin * a.d, corr);
+        acc = fmaf((float)(slo * p.sc0 + shi * p.sc1), p.d * a.d, acc);
+        corr = fmaf((float)(p.mn0 * a.b01 + p.mn1 * a.b23), p.dmin * a.d, corr);
+    }
+    __device__ static void dot(const W &w, uint32_t u, const AU &a, float &acc, float &corr) {
+        dotp(prep(w, u), a, acc, corr);
     }
 };
 
@@ -228,28 +248,48 @@ template <> struct MvFmt<HKHIP_Q6_K> {
         a.d = A.d[t * (A.K / 256) + (u >> 2)];
         return a;
     }
-    __device__ static void dot(const W &w, uint32_t u, const AU &a, float &acc, float &) {
+    // Weight-side work of a unit: the 6-bit values of its 4 groups of 16 (stored as q, the -32
+    // goes through bsums) and their scales.
+    struct P {
+        uint32_t q[16];
+        int sc[4];
+        float d;
+    };
+    __device__ static P prep(const W &w, uint32_t u) {
         const uint32_t lc = u & 1;
-        const int sc[4] = {int8_t(w.sc.x >> (8 * lc)), int8_t(w.sc.x >> (8 * lc + 16)),
-                           int8_t(w.sc.y >> (8 * lc)), int8_t(w.sc.y >> (8 * lc + 16))};
+        P p;
+        p.sc[0] = int8_t(w.sc.x >> (8 * lc));
+        p.sc[1] = int8_t(w.sc.x >> (8 * lc + 16));
+        p.sc[2] = int8_t(w.sc.y >> (8 * lc));
+        p.sc[3] = int8_t(w.sc.y >> (8 * lc + 16));
         const uint32_t L0[4] = {w.l0.x, w.l0.y, w.l0.z, w.l0.w};
         const uint32_t L1[4] = {w.l1.x, w.l1.y, w.l1.z, w.l1.w};
         const uint32_t H[4] = {w.hh.x, w.hh.y, w.hh.z, w.hh.w};
-        int s[4] = {0, 0, 0, 0};
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            s[0] = sdot4((L0[i] & 0x0F0F0F0Fu) | ((H[i] & 0x03030303u) << 4), a.q[i], s[0]);
-            s[1] = sdot4((L1[i] & 0x0F0F0F0Fu) | (((H[i] >> 2) & 0x03030303u) << 4), a.q[4 + i], s[1]);
-            s[2] = sdot4(((L0[i] >> 4) & 0x0F0F0F0Fu) | (((H[i] >> 4) & 0x03030303u) << 4), a.q[8 + i], s[2]);
-            s[3] = sdot4(((L1[i] >> 4) & 0x0F0F0F0Fu) | (((H[i] >> 6) & 0x03030303u) << 4), a.q[12 + i], s[3]);
+            p.q[i] = (L0[i] & 0x0F0F0F0Fu) | ((H[i] & 0x03030303u) << 4);
+            p.q[4 + i] = (L1[i] & 0x0F0F0F0Fu) | (((H[i] >> 2) & 0x03030303u) << 4);
+            p.q[8 + i] = ((L0[i] >> 4) & 0x0F0F0F0Fu) | (((H[i] >> 4) & 0x03030303u) << 4);
+            p.q[12 + i] = ((L1[i] >> 4) & 0x0F0F0F0Fu) | (((H[i] >> 6) & 0x03030303u) << 4);
         }
+        p.d = f16_bits_to_f32(w.d);
+        return p;
+    }
+    // One token (dotQ6K, vecdot.zig:533-570).
+    __device__ static void dotp(const P &p, const AU &a, float &acc, float &) {
         int isum = 0, bias = 0;
 #pragma unroll
         for (int g = 0; g < 4; g++) {
-            isum += s[g] * sc[g];
-            bias += sc[g] * a.bs[g];
+            int sg = 0;
+#pragma unroll
+            for (int i = 0; i < 4; i++) sg = sdot4(p.q[4 * g + i], a.q[4 * g + i], sg);
+            isum += sg * p.sc[g];
+            bias += p.sc[g] * a.bs[g];
         }
-        acc = fmaf((float)(isum - 32 * bias), f16_bits_to_f32(w.d) * a.d, acc);
+        acc = fmaf((float)(isum - 32 * bias), p.d * a.d, acc);
+    }
+    __device__ static void dot(const W &w, uint32_t u, const AU &a, float &acc, float &corr) {
+        dotp(prep(w, u), a, acc, corr);
     }
 };
 
@@ -288,23 +328,35 @@ template <int T> struct MvLegacy {
         a.d = A.d[t * (A.K / 32) + u];
         return a;
     }
-    __device__ static void dot(const W &w, uint32_t, const AU &a, float &acc, float &) {
-        uint32_t qw[8];
+    // Weight-side work of a unit: its 32 int8 weights (codebook lookups for IQ4_NL) and scale.
+    struct P {
+        uint32_t q[8];
+        float d;
+    };
+    __device__ static P prep(const W &w, uint32_t) {
+        P p;
         if constexpr (T == HKHIP_Q8_0) {
-            qw[0] = w.x0.x; qw[1] = w.x0.y; qw[2] = w.x0.z; qw[3] = w.x0.w;
-            qw[4] = w.x1.x; qw[5] = w.x1.y; qw[6] = w.x1.z; qw[7] = w.x1.w;
+            p.q[0] = w.x0.x; p.q[1] = w.x0.y; p.q[2] = w.x0.z; p.q[3] = w.x0.w;
+            p.q[4] = w.x1.x; p.q[5] = w.x1.y; p.q[6] = w.x1.z; p.q[7] = w.x1.w;
         } else {
             const uint32_t n4[4] = {w.x0.x, w.x0.y, w.x0.z, w.x0.w};
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                qw[i] = iq4nl_lookup4(n4[i] & 0x0F0F0F0Fu);
-                qw[4 + i] = iq4nl_lookup4((n4[i] >> 4) & 0x0F0F0F0Fu);
+                p.q[i] = iq4nl_lookup4(n4[i] & 0x0F0F0F0Fu);
+                p.q[4 + i] = iq4nl_lookup4((n4[i] >> 4) & 0x0F0F0F0Fu);
             }
         }
+        p.d = f16_bits_to_f32(w.d);
+        return p;
+    }
+    __device__ static void dotp(const P &p, const AU &a, float &acc, float &) {
         int s = 0;
 #pragma unroll
-        for (int i = 0; i < 8; i++) s = sdot4(qw[i], a.q[i], s);
-        acc = fmaf((float)s, f16_bits_to_f32(w.d) * a.d, acc);
+        for (int i = 0; i < 8; i++) s = sdot4(p.q[i], a.q[i], s);
+        acc = fmaf((float)s, p.d * a.d, acc);
+    }
+    __device__ static void dot(const W &w, uint32_t u, const AU &a, float &acc, float &corr) {
+        dotp(prep(w, u), a, acc, corr);
     }
 };
 template <> struct MvFmt<HKHIP_Q8_0> : MvLegacy<HKHIP_Q8_0> {};
@@ -820,18 +872,10 @@ __global__ __launch_bounds__(NW * 64, MVR_MINW) void mmvr_kernel(MvArgs a) {
             for (int c = 0; c < C; c++) {
                 const uint32_t u = lane + 64 * c;
                 if (u < U) {
+                    const typename F::P pw = F::prep(w[i][c], u);
 #pragma unroll
-                    for (int t = 0; t < NT; t++) {
-                        if (NT == 1 || uint32_t(t) < a.ntok) {
-#ifdef HKHIP_MV_PROBE_LOADS_ONLY
-                            uint32_t xr = 0;
-                            for (uint32_t k = 0; k < sizeof(W) / 4; k++) xr ^= reinterpret_cast<const uint32_t *>(&w[i][c])[k];
-                            acc[t] += __builtin_bit_cast(float, xr & 1u) + au[t][c].d;
-#else
-                            F::dot(w[i][c], u, au[t][c], acc[t], corr[t]);
-#endif
-                        }
-                    }
+                    for (int t = 0; t < NT; t++)
+                        if (NT == 1 || uint32_t(t) < a.ntok) F::dotp(pw, au[t][c], acc[t], corr[t]);
                 }
             }
             const uint32_t slot = rb + i - fbase;
@@ -915,7 +959,7 @@ static mv_kernel_t kernel_for(int t, int nt) {
 #ifndef MVR_R1
 #define MVR_R1 2
 #endif
-__host__ __device__ constexpr int mvr_rows(int nt, int c) { return nt == 1 ? (c >= MVR_R1 ? 1 : MVR_R1 / c) : (c >= 2 ? 1 : 2); }
+__host__ __device__ constexpr int mvr_rows(int nt, int c) { return nt == 1 ? (c >= MVR_R1 ? 1 : MVR_R1 / c) : (c >= 2 || nt >= 8 ? 1 : 2); }
 // Largest C per (format, NT): the activations of NT*C units must fit the register file next to
 // two steps of weights.
 __host__ __device__ constexpr int mvr_cmax(int t, int nt) {
