@@ -416,7 +416,7 @@ __global__ __launch_bounds__(NW * 64, 2) void mm2_q4k_kernel(Mm2Args a) {
 #pragma unroll
     for (int p = 0; p < NB - 1; p++) issue(p < int(nsb) ? p : nsb - 1, p);
     // Wait for slot 0 (the loads of NB-2 later super-blocks may stay in flight).
-    __builtin_amdgcn_s_waitcnt(0x0F70 & ~0xF | ((CPW * (NB - 2)) & 0xF) | (((CPW * (NB - 2)) >> 4) << 14));
+    __builtin_amdgcn_s_waitcnt((0x0F70 & ~0xF) | ((CPW * (NB - 2)) & 0xF) | (((CPW * (NB - 2)) >> 4) << 14));
     __syncthreads();
 
     for (uint32_t sb = 0; sb < nsb; sb++) {
@@ -511,7 +511,7 @@ __global__ __launch_bounds__(NW * 64, 2) void mm2_q4k_kernel(Mm2Args a) {
             acc[t] = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(al, mhi, acc[t], 0, 0, 0);
         }
         // The next super-block's slot has landed once at most NB-2 later issues are pending.
-        __builtin_amdgcn_s_waitcnt(0x0F70 & ~0xF | ((CPW * (NB - 2)) & 0xF) | (((CPW * (NB - 2)) >> 4) << 14));
+        __builtin_amdgcn_s_waitcnt((0x0F70 & ~0xF) | ((CPW * (NB - 2)) & 0xF) | (((CPW * (NB - 2)) >> 4) << 14));
         __syncthreads();
     }
 
