@@ -10,7 +10,6 @@
 // to int8 (nibbles, 6-bit values with the -32 offset folded in, codebook lookups), in LDS.
 // MFMA operand A = activations (tokens as M), B = weights (rows as N), so each lane's 16
 // results share one weight row and its scales.
-#include <stdlib.h>
 
 #include "common.hpp"
 
@@ -285,8 +284,7 @@ __global__ __launch_bounds__(256) void mm_kernel(MmArgs a) {
 hipError_t launch_mm(int t, const uint8_t *w, uint32_t rows, uint32_t cols, const uint8_t *xq, uint32_t n,
                      float *y, const float *bias, int mode, hipStream_t s) {
     if (rows == 0 || n == 0) return hipSuccess;
-    static const bool force_v1 = getenv("HKHIP_MM_V1") != nullptr; // experiments only
-    if (!force_v1 && mm2_supports(t, rows, cols, n)) return launch_mm2(t, w, rows, cols, xq, n, y, bias, mode, s);
+    if (mm2_supports(t, rows, cols, n)) return launch_mm2(t, w, rows, cols, xq, n, y, bias, mode, s);
     WLayout W = weight_layout(t, rows, cols);
     ActLayout A = act_layout(n, cols);
     const bool kq = (t == HKHIP_Q4_K || t == HKHIP_Q6_K);

@@ -27,7 +27,6 @@
 //
 // MFMA roles: A = activations (tokens as M), B = weights (rows as N). Output lane l holds row
 // l%32 and tokens 8*(v/4) + 4*(l/32) + v%4 for v < 16.
-#include <stdlib.h>
 
 #include "common.hpp"
 
@@ -594,13 +593,6 @@ hipError_t launch_mm2(int t, const uint8_t *w, uint32_t rows, uint32_t cols, con
     auto blocks = [&](uint32_t nw, uint32_t tt) {
         return ((rows + 32 * nw - 1) / (32 * nw)) * ((n + 32 * tt - 1) / (32 * tt));
     };
-    static const int force = getenv("HKHIP_MM2_CFG") ? atoi(getenv("HKHIP_MM2_CFG")) : 0; // experiments only
-    if (force == 84) return launch_mm2_cfg<8, 4, 2>(a, s);
-    if (force == 840) return launch_mm2_reg<8, 4>(a, s);
-    if (force == 42) return launch_mm2_cfg<4, 2, 2>(a, s);
-    if (force == 41) return launch_mm2_cfg<4, 1, 2>(a, s);
-    if (force == 21) return launch_mm2_cfg<2, 1, 3>(a, s);
-    if (force == 11) return launch_mm2_cfg<1, 1, 3>(a, s);
     if (blocks(8, 4) >= 192) return launch_mm2_reg<8, 4>(a, s);
     if (blocks(4, 2) >= 160) return launch_mm2_cfg<4, 2, 2>(a, s);
     if (blocks(4, 1) >= 256) return launch_mm2_cfg<4, 1, 2>(a, s);

@@ -24,7 +24,6 @@
 // that a decode step needs no separate quantization launch.
 #include <map>
 #include <mutex>
-#include <stdlib.h>
 
 #include "quant.hpp"
 
@@ -693,21 +692,8 @@ __device__ __forceinline__ void mvr_stage_chunk(const float4 *xv, uint32_t c, bo
     }
 }
 
-#ifdef HKHIP_MV_PROBE_TS
-__device__ uint64_t *g_ts;
-#define MV_TS(i)                                                                                  \
-    do {                                                                                          \
-        const uint64_t t_ = __builtin_amdgcn_s_memrealtime();                                     \
-        if (__lane_id() == 0) g_ts[(blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6)) * 5 + i] = t_; \
-    } while (0)
-#else
-#define MV_TS(i)
-#endif
-#ifndef MVR_MINW
-#define MVR_MINW 1
-#endif
 template <int T, int NT, int C, int R, int NW>
-__global__ __launch_bounds__(NW * 64, MVR_MINW) void mmvr_kernel(MvArgs a) {
+__global__ __launch_bounds__(NW * 64) void mmvr_kernel(MvArgs a) {
     using F = MvFmt<T>;
     using W = typename F::W;
     using AU = typename F::AU;
@@ -791,7 +777,6 @@ __global__ __launch_bounds__(NW * 64, MVR_MINW) void mmvr_kernel(MvArgs a) {
             }
         }
     }
-    MV_TS(0);
     const uint32_t ns = (r1 - r0 + R - 1) / R; // steps of this wave
     load(wa, r0);
     if (a.x) {
@@ -813,7 +798,6 @@ __global__ __launch_bounds__(NW * 64, MVR_MINW) void mmvr_kernel(MvArgs a) {
                 if (cidx < nchunk) mvr_stage_chunk<F>(xv[j], cidx, 1024 * cidx + 16 * lane < nflat, sqs, sbs, sd);
             }
         }
-        MV_TS(1);
         __syncthreads();
 #pragma unroll
         for (int t = 0; t < NT; t++) {
@@ -828,8 +812,6 @@ __global__ __launch_bounds__(NW * 64, MVR_MINW) void mmvr_kernel(MvArgs a) {
     // The second step is issued only now, so that the barrier does not wait for every wave to get
     // two steps of loads past a busy memory pipeline.
     if (ns > 1) load(wb, r0 + R);
-
-    MV_TS(2);
 
     // Lane j keeps the result of row r0 + j; the launch gives no wave more than 64 rows, so the
     // results are stored once, at the end, and the loop issues no load but weights.
@@ -896,7 +878,6 @@ __global__ __launch_bounds__(NW * 64, MVR_MINW) void mmvr_kernel(MvArgs a) {
         compute(wb, r0 + (s + 1) * R);
         load(wb, r0 + (s + 3) * R);
     }
-    MV_TS(3);
     auto step = [&](const W (*w)[C], uint32_t st) { compute(w, r0 + st * R); };
     if (s + 2 < ns) {
         step(wa, s);
@@ -910,7 +891,6 @@ __global__ __launch_bounds__(NW * 64, MVR_MINW) void mmvr_kernel(MvArgs a) {
         step(wa, s);
     }
     flush(r1 - r0);
-    MV_TS(4);
 }
 
 #undef MV_SEL
@@ -953,12 +933,8 @@ static mv_kernel_t kernel_for(int t, int nt) {
 // C = units per lane (rows of at most 64*C units), R = rows per step. The activations of NT*C
 // units must fit the register file next to two steps of weights: NT*C <= 8 for Q4_K/Q6_K and
 // <= 16 for Q8_0/IQ4_NL; larger shapes use the LDS kernel.
-#ifndef MVR_NWAVES
-#define MVR_NWAVES 8
-#endif
-#ifndef MVR_R1
-#define MVR_R1 2
-#endif
+constexpr int MVR_NWAVES = 8; // waves per workgroup (a budget of 256 registers per lane)
+constexpr int MVR_R1 = 2;     // rows per step at one token and C = 1
 __host__ __device__ constexpr int mvr_rows(int nt, int c) { return nt == 1 ? (c >= MVR_R1 ? 1 : MVR_R1 / c) : (c >= 2 || nt >= 8 ? 1 : 2); }
 // Largest C per (format, NT): the activations of NT*C units must fit the register file next to
 // two steps of weights.
@@ -969,11 +945,7 @@ __host__ __device__ constexpr int mvr_cmax(int t, int nt) {
 }
 // Waves per workgroup: MVR_NWAVES (a budget of 256 registers per lane), or 4 (512) for the
 // variants that need more.
-#ifndef MVR_NW_Q4C4
-#define MVR_NW_Q4C4 MVR_NWAVES
-#endif
 __host__ __device__ constexpr int mvr_nw(int t, int nt, int c) {
-    if (t == HKHIP_Q4_K && nt == 1 && c == 4) return MVR_NW_Q4C4;
     return (t == HKHIP_Q6_K && nt * c >= 4) || (t == HKHIP_Q4_K && nt * c >= 8 && nt < 8) ||
                    ((t == HKHIP_Q8_0 || t == HKHIP_IQ4_NL) && c >= 4 && nt * c >= 8)
                ? 4
@@ -1047,23 +1019,18 @@ static int cu_count() {
     return n;
 }
 
-static int env_int(const char *name, int dflt) {
-    const char *v = getenv(name);
-    return v ? atoi(v) : dflt;
-}
 
 hipError_t launch_mmvq_parts(int t, const MvPartDesc *parts, int nparts, uint32_t K, const float *x,
                              const uint8_t *xq, uint32_t n, int mode, hipStream_t s) {
     if (n < 1 || n > 8 || nparts < 1 || nparts > MV_PARTS) return hipErrorInvalidValue;
     const bool kq = (t == HKHIP_Q4_K || t == HKHIP_Q6_K);
-    static const int force_general = env_int("HKHIP_MV_GENERAL", 0);
     {
         // Register kernel when the shape fits it.
         const uint32_t units = kq ? K / 64 : K / 32;
         const int nt = n == 1 ? 1 : n == 2 ? 2 : n <= 4 ? 4 : 8;
         int c = 1;
         while (c < 8 && 64u * c < units) c *= 2;
-        mv_kernel_t k = (64u * c >= units && !force_general) ? kernelr_for(t, nt, c) : nullptr;
+        mv_kernel_t k = 64u * c >= units ? kernelr_for(t, nt, c) : nullptr;
         if (k) {
             MvArgs a{};
             uint32_t rows = 0;
@@ -1099,8 +1066,6 @@ hipError_t launch_mmvq_parts(int t, const MvPartDesc *parts, int nparts, uint32_
             const uint32_t cap = uint32_t(cu_count() * resident_per_cu(k, nw * 64, lds));
             const uint32_t want = (rows + nw * R - 1) / (nw * R);
             uint32_t grid = want < cap ? want : cap;
-            static const int grid_cap = env_int("HKHIP_MV_GRID_CAP", 0); // experiments only
-            if (grid_cap > 0 && grid > uint32_t(grid_cap)) grid = grid_cap;
             // At most 64 rows per wave (each lane keeps one row's result); extra workgroups queue.
             const uint32_t need = (rows + 64u * nw - 1) / (64u * nw);
             if (grid < need) grid = need;
