@@ -692,19 +692,26 @@ __device__ __forceinline__ void mvr_stage_chunk(const float4 *xv, uint32_t c, bo
     }
 }
 
-template <int T, int NT, int C, int R, int NW>
+// KS > 1 splits each row's units over KS waves of a workgroup (for rows whose activations would
+// not fit one wave's registers): wave w is slice w % KS of row group w / KS; the slices' partial
+// results meet in LDS at the end.
+template <int T, int NT, int C, int R, int NW, int KS>
 __global__ __launch_bounds__(NW * 64) void mmvr_kernel(MvArgs a) {
     using F = MvFmt<T>;
     using W = typename F::W;
     using AU = typename F::AU;
+    static_assert(NW % KS == 0, "slices per workgroup");
+    constexpr int NRG = NW / KS; // row groups per workgroup
     const uint32_t K = a.K;
     const uint32_t lane = __lane_id();
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t rg = wave / KS, ks = wave % KS;
     const uint32_t U = F::units(K);
-    const uint32_t nwaves = gridDim.x * NW, wid = blockIdx.x * NW + wave;
+    const uint32_t u0 = ks * 64 * C; // first unit of this wave's slice
+    const uint32_t ngroups = gridDim.x * NRG, gid = blockIdx.x * NRG + rg;
     const uint32_t total = a.ngroups; // rows of all parts
-    const uint32_t r0 = uint32_t(uint64_t(total) * wid / nwaves);
-    const uint32_t r1 = uint32_t(uint64_t(total) * (wid + 1) / nwaves);
+    const uint32_t r0 = uint32_t(uint64_t(total) * gid / ngroups);
+    const uint32_t r1 = uint32_t(uint64_t(total) * (gid + 1) / ngroups);
     // A wave without rows still helps stage the input (and reaches the barrier).
     const uint32_t rlast = r0 < r1 ? r1 - 1 : 0;
 
@@ -738,7 +745,7 @@ __global__ __launch_bounds__(NW * 64) void mmvr_kernel(MvArgs a) {
             const RowRef RR = F::row(q.w, q.ws, r - q.gstart, K);
 #pragma unroll
             for (int c = 0; c < C; c++) {
-                const uint32_t u = lane + 64 * c;
+                const uint32_t u = u0 + lane + 64 * c;
                 w[i][c] = F::load(RR, u < U ? u : U - 1);
             }
         }
@@ -772,7 +779,7 @@ __global__ __launch_bounds__(NW * 64) void mmvr_kernel(MvArgs a) {
             if (NT > 1 && uint32_t(t) >= a.ntok) break;
 #pragma unroll
             for (int c = 0; c < C; c++) {
-                const uint32_t u = lane + 64 * c;
+                const uint32_t u = u0 + lane + 64 * c;
                 au[t][c] = load_unit<F>(a.gqs, a.gbs, a.gd, K, t, u < U ? u : U - 1);
             }
         }
@@ -804,7 +811,7 @@ __global__ __launch_bounds__(NW * 64) void mmvr_kernel(MvArgs a) {
             if (NT > 1 && uint32_t(t) >= a.ntok) break;
 #pragma unroll
             for (int c = 0; c < C; c++) {
-                const uint32_t u = lane + 64 * c;
+                const uint32_t u = u0 + lane + 64 * c;
                 au[t][c] = load_unit<F>(sqs, sbs, sd, K, t, u < U ? u : U - 1);
             }
         }
@@ -852,7 +859,7 @@ __global__ __launch_bounds__(NW * 64) void mmvr_kernel(MvArgs a) {
             for (int t = 0; t < NT; t++) acc[t] = corr[t] = 0.0f;
 #pragma unroll
             for (int c = 0; c < C; c++) {
-                const uint32_t u = lane + 64 * c;
+                const uint32_t u = u0 + lane + 64 * c;
                 if (u < U) {
                     const typename F::P pw = F::prep(w[i][c], u);
 #pragma unroll
@@ -890,7 +897,25 @@ __global__ __launch_bounds__(NW * 64) void mmvr_kernel(MvArgs a) {
     } else if (s < ns) {
         step(wa, s);
     }
-    flush(r1 - r0);
+    if constexpr (KS > 1) {
+        // Slices 1.. leave their partials in LDS (after the staging area); slice 0 adds and stores.
+        const uint32_t cofs = a.x ? (mvr_lds_bytes(int(NT == 1 ? 1u : a.ntok), K, F::kq) + 15) & ~15u : 0u;
+        float *cb = reinterpret_cast<float *>(smem + cofs) + (rg * KS) * 64 * NT;
+        if (ks > 0) {
+#pragma unroll
+            for (int t = 0; t < NT; t++) cb[(ks * 64 + lane) * NT + t] = res[t];
+        }
+        __syncthreads();
+        if (ks == 0) {
+#pragma unroll
+            for (int k = 1; k < KS; k++)
+#pragma unroll
+                for (int t = 0; t < NT; t++) res[t] += cb[(k * 64 + lane) * NT + t];
+            flush(r1 - r0);
+        }
+    } else {
+        flush(r1 - r0);
+    }
 }
 
 #undef MV_SEL
@@ -952,42 +977,54 @@ __host__ __device__ constexpr int mvr_nw(int t, int nt, int c) {
                : MVR_NWAVES;
 }
 
-template <int T, int NT, int C>
+template <int T, int NT, int C, int KS>
 static mv_kernel_t mvr_if_fits() {
-    if constexpr (C <= mvr_cmax(T, NT))
-        return mmvr_kernel<T, NT, C, mvr_rows(NT, C), mvr_nw(T, NT, C)>;
+    if constexpr (C <= mvr_cmax(T, NT) && KS <= mvr_nw(T, NT, C))
+        return mmvr_kernel<T, NT, C, mvr_rows(NT, C), mvr_nw(T, NT, C), KS>;
     else
         return nullptr;
 }
 
+// Units per lane c and slices ks: one slice for c <= cmax; beyond that, the largest c (cmax) in
+// 2, 4 or 8 slices.
 template <int T, int NT>
-static mv_kernel_t mvr_pick_c(int c) {
-    switch (c) {
-    case 1: return mvr_if_fits<T, NT, 1>();
-    case 2: return mvr_if_fits<T, NT, 2>();
-    case 4: return mvr_if_fits<T, NT, 4>();
-    case 8: return mvr_if_fits<T, NT, 8>();
+static mv_kernel_t mvr_pick_c(int c, int ks) {
+    constexpr int CM = mvr_cmax(T, NT);
+    if (ks == 1) {
+        switch (c) {
+        case 1: return mvr_if_fits<T, NT, 1, 1>();
+        case 2: return mvr_if_fits<T, NT, 2, 1>();
+        case 4: return mvr_if_fits<T, NT, 4, 1>();
+        case 8: return mvr_if_fits<T, NT, 8, 1>();
+        default: return nullptr;
+        }
+    }
+    if (c != CM) return nullptr;
+    switch (ks) {
+    case 2: return mvr_if_fits<T, NT, CM, 2>();
+    case 4: return mvr_if_fits<T, NT, CM, 4>();
+    case 8: return mvr_if_fits<T, NT, CM, 8>();
     default: return nullptr;
     }
 }
 
 template <int T>
-static mv_kernel_t mvr_pick(int nt, int c) {
+static mv_kernel_t mvr_pick(int nt, int c, int ks) {
     switch (nt) {
-    case 1: return mvr_pick_c<T, 1>(c);
-    case 2: return mvr_pick_c<T, 2>(c);
-    case 4: return mvr_pick_c<T, 4>(c);
-    case 8: return mvr_pick_c<T, 8>(c);
+    case 1: return mvr_pick_c<T, 1>(c, ks);
+    case 2: return mvr_pick_c<T, 2>(c, ks);
+    case 4: return mvr_pick_c<T, 4>(c, ks);
+    case 8: return mvr_pick_c<T, 8>(c, ks);
     default: return nullptr;
     }
 }
 
-static mv_kernel_t kernelr_for(int t, int nt, int c) {
+static mv_kernel_t kernelr_for(int t, int nt, int c, int ks) {
     switch (t) {
-    case HKHIP_Q4_K: return mvr_pick<HKHIP_Q4_K>(nt, c);
-    case HKHIP_Q6_K: return mvr_pick<HKHIP_Q6_K>(nt, c);
-    case HKHIP_Q8_0: return mvr_pick<HKHIP_Q8_0>(nt, c);
-    case HKHIP_IQ4_NL: return mvr_pick<HKHIP_IQ4_NL>(nt, c);
+    case HKHIP_Q4_K: return mvr_pick<HKHIP_Q4_K>(nt, c, ks);
+    case HKHIP_Q6_K: return mvr_pick<HKHIP_Q6_K>(nt, c, ks);
+    case HKHIP_Q8_0: return mvr_pick<HKHIP_Q8_0>(nt, c, ks);
+    case HKHIP_IQ4_NL: return mvr_pick<HKHIP_IQ4_NL>(nt, c, ks);
     default: return nullptr;
     }
 }
@@ -1028,9 +1065,21 @@ hipError_t launch_mmvq_parts(int t, const MvPartDesc *parts, int nparts, uint32_
         // Register kernel when the shape fits it.
         const uint32_t units = kq ? K / 64 : K / 32;
         const int nt = n == 1 ? 1 : n == 2 ? 2 : n <= 4 ? 4 : 8;
-        int c = 1;
+        int c = 1, ks = 1;
         while (c < 8 && 64u * c < units) c *= 2;
-        mv_kernel_t k = 64u * c >= units ? kernelr_for(t, nt, c) : nullptr;
+        if (64u * c < units || c > mvr_cmax(t, nt)) {
+            // Rows too long for one wave's registers: slices of cmax units per lane.
+            c = mvr_cmax(t, nt);
+            while (ks < 8 && 64u * c * ks < units) ks *= 2;
+        }
+        mv_kernel_t k = 64u * c * ks >= units ? kernelr_for(t, nt, c, ks) : nullptr;
+        if (k && x) {
+            // An f32 input is staged whole in LDS; when it does not fit, the LDS kernel splits the
+            // tokens over launches.
+            uint32_t need = mvr_lds_bytes(int(n), K, kq);
+            if (ks > 1) need = ((need + 15) & ~15u) + uint32_t(mvr_nw(t, nt, c)) * 64 * nt * 4;
+            if (need > MV_LDS_MAX) k = nullptr;
+        }
         if (k) {
             MvArgs a{};
             uint32_t rows = 0;
@@ -1060,14 +1109,16 @@ hipError_t launch_mmvq_parts(int t, const MvPartDesc *parts, int nparts, uint32_
             }
             if (rows == 0) return hipSuccess;
             const int R = mvr_rows(nt, c);
-            const uint32_t lds = x ? mvr_lds_bytes(int(n), K, kq) : 0;
+            const int nw = mvr_nw(t, nt, c), nrg = nw / ks;
+            uint32_t lds = x ? mvr_lds_bytes(int(n), K, kq) : 0;
+            if (ks > 1) lds = ((lds + 15) & ~15u) + uint32_t(nw) * 64 * nt * 4; // partials
             if (lds > MV_LDS_MAX) return hipErrorInvalidValue;
-            const int nw = mvr_nw(t, nt, c);
             const uint32_t cap = uint32_t(cu_count() * resident_per_cu(k, nw * 64, lds));
-            const uint32_t want = (rows + nw * R - 1) / (nw * R);
+            const uint32_t want = (rows + nrg * R - 1) / (nrg * R);
             uint32_t grid = want < cap ? want : cap;
-            // At most 64 rows per wave (each lane keeps one row's result); extra workgroups queue.
-            const uint32_t need = (rows + 64u * nw - 1) / (64u * nw);
+            // At most 64 rows per row group (each lane keeps one row's result); extra workgroups
+            // queue.
+            const uint32_t need = (rows + 64u * nrg - 1) / (64u * nrg);
             if (grid < need) grid = need;
             hipLaunchKernelGGL(k, dim3(grid), dim3(nw * 64), lds, s, a);
             return hipGetLastError();

@@ -293,11 +293,14 @@ def test_matvec_parts_large_k(eng, torch_cuda, t, k, n):
     (F.Q6_K, 8192, 1), (F.Q6_K, 16384, 1), (F.Q6_K, 8192, 2), (F.Q6_K, 4096, 4), (F.Q6_K, 4096, 7),
     (F.Q8_0, 2048, 1), (F.Q8_0, 16384, 1), (F.Q8_0, 16416, 1), (F.Q8_0, 8192, 2), (F.Q8_0, 4096, 6),
     (F.IQ4_NL, 8192, 1), (F.IQ4_NL, 16384, 2), (F.IQ4_NL, 4096, 8), (F.IQ4_NL, 96, 3),
+    # rows split over 2-8 waves (K slices), partials combined in LDS
+    (F.Q4_K, 14336, 8), (F.Q4_K, 14336, 2), (F.Q4_K, 14336, 3), (F.Q4_K, 28672, 1),
+    (F.Q6_K, 14336, 8), (F.Q6_K, 20480, 1), (F.Q8_0, 20480, 8), (F.IQ4_NL, 14336, 4),
 ])
 @pytest.mark.parametrize("prepared", [False, True])
 def test_matvec_kernel_variants(eng, torch_cuda, t, k, n, prepared):
-    """Every register-kernel variant (units per lane 1-8, token counts padded up to 1/2/4/8) and
-    the shapes just past it, which fall back to the LDS kernel; f32 input and prepared input."""
+    """Every register-kernel variant (units per lane 1-8, token counts padded up to 1/2/4/8, rows
+    split over 2-8 waves) and the shapes past it; f32 input and prepared input."""
     torch = torch_cuda
     m = 333
     raw = synth.weights_np(t, m, k, seed=900 + t + k)
