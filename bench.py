@@ -191,7 +191,7 @@ def main():
             xq = torch.empty(eng.act_bytes(n, k_), dtype=torch.uint8, device=dev)
             yy = torch.empty(n, m_, device=dev)
             eng.qact(x, n, k_, F.ACT_Q8K, xq)
-            us = time_graph(torch, eng, stream, lambda: eng.gemm(w, xq, yy, n), 20)
+            us = time_graph(torch, eng, stream, lambda: eng.gemm(w, xq, yy, n), 5)
             tops = 2.0 * m_ * n * k_ / (us * 1e-6) / 1e12
             pre.append(dict(shape=f"{m_}x{k_}x{n}", fmt="q4_k", avg_us=round(us, 2), tops=round(tops, 2),
                             frac_int8_peak=round(tops / INT8_PEAK_TOPS, 4)))
@@ -249,8 +249,10 @@ def measured_traffic():
         return None
 
 
-def time_graph(torch, eng, stream, fn, reps: int) -> float:
-    """Average microseconds of fn's GPU work, captured once in a HIP graph and replayed."""
+def time_graph(torch, eng, stream, fn, reps: int, per_graph: int = 10) -> float:
+    """Average microseconds of one call of fn's GPU work: per_graph calls are captured back to back
+    in one HIP graph (so the graph's own launch cost is spread over them) and the graph is
+    replayed reps times."""
     fn()
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
@@ -258,7 +260,8 @@ def time_graph(torch, eng, stream, fn, reps: int) -> float:
     cap.wait_stream(stream)
     with torch.cuda.graph(g, stream=cap):
         eng.set_stream(cap.cuda_stream)
-        fn()
+        for _ in range(per_graph):
+            fn()
     eng.set_stream(stream.cuda_stream)
     g.replay()
     torch.cuda.synchronize()
@@ -268,7 +271,7 @@ def time_graph(torch, eng, stream, fn, reps: int) -> float:
         g.replay()
     e1.record(stream)
     torch.cuda.synchronize()
-    return 1e3 * e0.elapsed_time(e1) / reps
+    return 1e3 * e0.elapsed_time(e1) / (reps * per_graph)
 
 
 def cpu_baseline(seconds: float):
