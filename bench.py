@@ -7,7 +7,8 @@ TOPS (% of dense int8 MFMA peak).
 A step is one batch-1 decode token through every linear layer of a Llama-3-8B-shaped decoder
 32 layers x {q 4096x4096, k 1024x4096, v 1024x4096, o 4096x4096,
 gate 14336x4096, up 14336x4096, down 4096x14336} in Q4_K, plus the 128256x4096 Q6_K lm_head.
-Each layer quantizes its inputs once per input vector (qact) and runs the seven matvecs;
+Each layer runs four fused matvec launches (q/k/v, o, gate/up, down) on f32 inputs, which the
+kernels quantize as they stage them;
 weights are random-init (synthetic, 4.36 GB resident, so the 256 MB Infinity Cache cannot
 serve them). The step is captured once as a HIP graph and replayed. `value` is the step's
 algorithmic bytes (file-layout weight bytes + f32 activations in + f32 outputs) / step time.

@@ -70,8 +70,9 @@ inline WLayout weight_layout(int t, uint32_t rows, uint32_t cols) {
 // input serves Q8_0 / IQ4_NL (A8) and Q4_K / Q6_K (Q8K) products alike:
 //   a8_qs [n][k] i8, a8_d [n][k/32] f32, a8_s [n][k/32] i32,
 //   k_qs  [n][k] i8, k_d  [n][k/256] f32, k_bs [n][k/16] i16,
-//   k_mb  [n][k/256][16] bf16: per super-block, d*bsum32 of its 8 sub-blocks split in bf16 hi (8)
-//         then lo (8) -- the token-side operand of the GEMM's min term, precomputed once
+//   k_mb  [n][k/256][16] bf16: per super-block, its 8 sub-blocks' 32-value sums as exact bf16
+//         integers, bsum32 = 64*u + v with v in [0, 63]: 64*u for the 8 sub-blocks, then v --
+//         the token-side operand of the GEMM's integer min term, precomputed once
 struct ActLayout {
     uint64_t a8_qs, a8_d, a8_s, k_qs, k_d, k_bs, k_mb, total;
 };

@@ -11,10 +11,16 @@
 //    bytes. Two int32 MFMA chains over the super-block's 256 weights give sum(sh*q*a) and
 //    sum(sl*q*a), combined exactly as (h << 3) + l -- the same integer as the reference's -- and
 //    applied with one f32 update per super-block.
-//  * min term: a small product over sub-blocks with the float scales folded into the operands,
-//    (-dmin*mn) x (da*bsum32), on the bf16 MFMA with each fp32 operand split into bf16 hi + lo
-//    (three products: hi*hi + hi*lo + lo*hi, ~2^-16 relative error), accumulated in f32 straight
-//    into the output tile.
+//  * min term: J = sum_s mn[s]*bsum32[s] is an integer below 2^22, and both factors are exact
+//    bf16 integers once bsum32 is written as 64*u + v (v in [0, 63]). The staged kernels run one
+//    32x32x16 bf16 MFMA with 64*u in its first 8 k and v in the other 8 (against mn in both),
+//    which yields J exactly in f32, and apply both terms in one update: y += da*(d*I - dmin*J).
+//    The large-tile kernel has no registers left for J's tile, so it folds the float scales into
+//    the operands instead, (-dmin*mn) x (da*bsum32), each split into three bf16 parts (their sum
+//    is the fp32 value to within 2^-24): a 32x32x16 MFMA pairs 8 sub-blocks of one token part
+//    (first 8 k) and another (last 8 k) with a row part, so three of them, (hi|mid) x h,
+//    (hi|mid) x m, (hi|lo) x (l|h), form every partial product down to 2^-24, accumulated in f32
+//    straight into the output tile.
 // Only the f32 summation order differs from the reference.
 //
 // Tiling: a workgroup of 8 waves (two per SIMD, so one wave's VALU work and LDS waits overlap
@@ -36,7 +42,7 @@ namespace hkhip {
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
-typedef short v4s __attribute__((ext_vector_type(4)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef unsigned short us2 __attribute__((ext_vector_type(2)));
 
 // Shapes: NW waves per workgroup (32 rows each), TT token tiles of 32 per wave, NB super-blocks
@@ -63,7 +69,7 @@ struct Mm2Args {
     const int8_t *aqs;
     const float *ad;
     const int16_t *abs;
-    const uint8_t *amb; // k_mb: per token and super-block, 32 bytes
+    const uint8_t *amb; // k_mb: per token and super-block, 32 bytes (64*u, then v, as bf16)
     float *y;
     const float *bias;
     int mode;
@@ -87,11 +93,74 @@ __device__ __forceinline__ uint32_t bf16_rne(float x) {
     const uint32_t u = __builtin_bit_cast(uint32_t, x);
     return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
 }
-// x as bf16 hi + bf16 lo (x - hi), packed: hi in bits 0-15, lo in 16-31.
-__device__ __forceinline__ uint32_t bf16_split(float x) {
-    const uint32_t hi = bf16_rne(x);
-    const float r = x - __builtin_bit_cast(float, hi << 16);
-    return hi | (bf16_rne(r) << 16);
+// x as three bf16 parts p[0] + p[1] + p[2] (each the rounding of what the previous ones leave;
+// their sum is x to within 2^-24 relative).
+__device__ __forceinline__ void bf16_split3(float x, uint32_t p[3]) {
+    p[0] = bf16_rne(x);
+    const float r1 = x - __builtin_bit_cast(float, p[0] << 16);
+    p[1] = bf16_rne(r1);
+    p[2] = bf16_rne(r1 - __builtin_bit_cast(float, p[1] << 16));
+}
+
+// Row-side min-term operands of one super-block: -dmin*mn of the 8 sub-blocks (6-bit mins in
+// the bytes of mnl, mnh) in three bf16 parts, as the B operands of the three 32x32x16 MFMAs:
+// hi and mid in both lane halves, then lo in half 0 and hi in half 1.
+struct MinB {
+    v8bf b1, b2, b3;
+};
+__device__ __forceinline__ MinB min_operands(uint32_t mnl, uint32_t mnh, float dmin, uint32_t h) {
+    uint32_t w[3][4];
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+        uint32_t p[3];
+        bf16_split3(-dmin * (float)(((s < 4 ? mnl : mnh) >> (8 * (s & 3))) & 0xFF), p);
+#pragma unroll
+        for (int q = 0; q < 3; q++) {
+            if (s & 1)
+                w[q][s / 2] |= p[q] << 16;
+            else
+                w[q][s / 2] = p[q];
+        }
+    }
+    MinB m;
+    m.b1 = __builtin_bit_cast(v8bf, make_uint4(w[0][0], w[0][1], w[0][2], w[0][3]));
+    m.b2 = __builtin_bit_cast(v8bf, make_uint4(w[1][0], w[1][1], w[1][2], w[1][3]));
+    const uint32_t q = h ? 0 : 2;
+    m.b3 = __builtin_bit_cast(v8bf, make_uint4(w[q][0], w[q][1], w[q][2], w[q][3]));
+    return m;
+}
+
+// Adds the min term of one 32x32 tile: tm = the 12 words (hi, mid, lo: 8 bf16 each) of this
+// lane's token, B = the row side.
+__device__ __forceinline__ void min_term(v16f &acc, const uint32_t *tm, const MinB &B, uint32_t h) {
+    const v8bf a12 = __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4 *>(tm + 4 * h)); // hi | mid
+    const v8bf a3 = __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4 *>(tm + 8 * h));  // hi | lo
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a12, B.b1, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a12, B.b2, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a3, B.b3, acc, 0, 0, 0);
+}
+
+// Row-side operand of the min term: the 8 sub-blocks' 6-bit mins (bytes of mnl, mnh) as bf16
+// integers, the same 8 values in both lane halves.
+__device__ __forceinline__ v8bf min_b(uint32_t mnl, uint32_t mnh) {
+    uint32_t w[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const uint32_t src = q < 2 ? mnl : mnh, sh = 16 * (q & 1);
+        const float e = (float)((src >> sh) & 0xFF), o = (float)((src >> (sh + 8)) & 0xFF);
+        w[q] = (__builtin_bit_cast(uint32_t, e) >> 16) | (__builtin_bit_cast(uint32_t, o) & 0xFFFF0000u);
+    }
+    return __builtin_bit_cast(v8bf, make_uint4(w[0], w[1], w[2], w[3]));
+}
+
+// J = sum_s mn[s] * bsum32[s] of a 32x32 tile, exact: tm holds this lane's token's 8 words
+// (64*u of the 8 sub-blocks in words 0-3, v in 4-7); lane half h supplies its half. `after` is
+// a value the caller computes just before: the operand is tied to it so that the MFMA is not
+// hoisted (with its result registers) ahead of the tile's other work.
+__device__ __forceinline__ v16f min_j(const uint32_t *tm, v8bf mn, uint32_t h, float after) {
+    uint4 w = *reinterpret_cast<const uint4 *>(tm + 4 * h);
+    asm volatile("" : "+v"(w.x) : "v"(after));
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, w), mn, v16f{}, 0, 0, 0);
 }
 
 // Four nibble bytes (values 0..15) times a 3-bit scale factor: each byte product is at most
@@ -102,7 +171,7 @@ __device__ __forceinline__ uint32_t mul_bytes(uint32_t nib, uint32_t f2) {
 
 template <int TOK> struct Q2Smem {
     int8_t a[2][TOK * 256];
-    uint32_t mb[2][TOK][8]; // per token: 8 bf16 hi (words 0-3), 8 bf16 lo (words 4-7)
+    uint32_t mb[2][TOK][12]; // per token: 8 bf16 hi (words 0-3), mid (4-7), lo (8-11)
     float da[2][TOK];
 };
 
@@ -170,22 +239,23 @@ __global__ __launch_bounds__(Q2_NW * 64, 2) void mm2_q4k_reg_kernel(Mm2Args a) {
         if (tok_thread) {
             const bool ok = t0 + tid < a.n;
             const uint32_t bw[8] = {sbs0.x, sbs0.y, sbs0.z, sbs0.w, sbs1.x, sbs1.y, sbs1.z, sbs1.w};
-            uint32_t hw[4], lw[4];
+            uint32_t w[3][4];
 #pragma unroll
             for (int s = 0; s < 8; s++) {
                 const int b32 = int(int16_t(bw[s] & 0xFFFF)) + int(int16_t(bw[s] >> 16));
-                const uint32_t sp = ok ? bf16_split(sda * (float)b32) : 0u;
-                if (s & 1) {
-                    hw[s / 2] |= sp << 16;
-                    lw[s / 2] |= sp & 0xFFFF0000u;
-                } else {
-                    hw[s / 2] = sp & 0xFFFFu;
-                    lw[s / 2] = sp >> 16;
+                uint32_t p[3];
+                bf16_split3(ok ? sda * (float)b32 : 0.0f, p);
+#pragma unroll
+                for (int q = 0; q < 3; q++) {
+                    if (s & 1)
+                        w[q][s / 2] |= p[q] << 16;
+                    else
+                        w[q][s / 2] = p[q];
                 }
             }
             uint4 *mb = reinterpret_cast<uint4 *>(S.mb[buf][tid]);
-            mb[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-            mb[1] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+#pragma unroll
+            for (int q = 0; q < 3; q++) mb[q] = make_uint4(w[q][0], w[q][1], w[q][2], w[q][3]);
             S.da[buf][tid] = ok ? sda : 0.0f;
         }
     };
@@ -241,17 +311,8 @@ __global__ __launch_bounds__(Q2_NW * 64, 2) void mm2_q4k_reg_kernel(Mm2Args a) {
                 blo[2 * p + 1][i] = int(mul_bytes(no, slo));
             }
         }
-        // Min-term operand of this lane's row: -dmin*mn for sub-blocks 4h..4h+3, bf16 hi / lo.
-        v4s mhi, mlo;
-        {
-            const uint32_t mw = h ? mnh : mnl;
-#pragma unroll
-            for (int s = 0; s < 4; s++) {
-                const uint32_t sp = bf16_split(-dmin * (float)((mw >> (8 * s)) & 0xFF));
-                mhi[s] = short(sp & 0xFFFF);
-                mlo[s] = short(sp >> 16);
-            }
-        }
+        // Min-term operands of this lane's row.
+        const MinB mB = min_operands(mnl, mnh, dmin, h);
 
         // A operand of tile t, sub-block s: token 32t + j, chunk 2s + h (swizzled).
         const int8_t *abase = &S.a[buf][j * 256];
@@ -295,13 +356,7 @@ __global__ __launch_bounds__(Q2_NW * 64, 2) void mm2_q4k_reg_kernel(Mm2Args a) {
                 }
             }
             // Min term: tokens' da*bsum32 (A) x rows' -dmin*mn (B), bf16 hi/lo split.
-            const uint32_t *mbp = S.mb[buf][32 * t + j];
-            const uint2 ahi = *reinterpret_cast<const uint2 *>(mbp + 2 * h);
-            const uint2 alo = *reinterpret_cast<const uint2 *>(mbp + 4 + 2 * h);
-            const v4s ah = __builtin_bit_cast(v4s, ahi), al = __builtin_bit_cast(v4s, alo);
-            acc[t] = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(ah, mhi, acc[t], 0, 0, 0);
-            acc[t] = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(ah, mlo, acc[t], 0, 0, 0);
-            acc[t] = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(al, mhi, acc[t], 0, 0, 0);
+            min_term(acc[t], S.mb[buf][32 * t + j], mB, h);
         }
 
         stage_store(buf ^ 1);
@@ -366,33 +421,38 @@ __global__ __launch_bounds__(NW * 64, 2) void mm2_q4k_kernel(Mm2Args a) {
     constexpr uint32_t CPW = TPW / 4 + 6 + 1 + 1; // a + w + mb + da
     // Weight bytes of this wave: 16-byte piece P (64*i + lane, i < 4) is byte 16*(P%9) of row
     // P/9's block; the last 512 bytes (pieces 256..287) go as 4-byte words 1024 + 64*i + lane.
-    const uint8_t *wsrc[6];
+    // Per-lane 32-bit byte offsets from uniform bases (mm2_supports checks that they fit).
+    uint32_t woff[6];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const uint32_t P = 64 * i + lane;
         const uint32_t row = r0 + 32 * wave + P / 9, rr = row < a.rows ? row : a.rows - 1;
-        wsrc[i] = a.w + uint64_t(rr) * nsb * 144 + 16 * (P % 9);
+        woff[i] = rr * nsb * 144 + 16 * (P % 9);
     }
 #pragma unroll
     for (int i = 0; i < 2; i++) {
         const uint32_t Wd = 1024 + 64 * i + lane; // 4-byte word index in the wave's area
         const uint32_t row = r0 + 32 * wave + Wd / 36, rr = row < a.rows ? row : a.rows - 1;
-        wsrc[4 + i] = a.w + uint64_t(rr) * nsb * 144 + 4 * (Wd % 36);
+        woff[4 + i] = rr * nsb * 144 + 4 * (Wd % 36);
+    }
+    uint32_t aoff[TPW / 4];
+#pragma unroll
+    for (uint32_t i = 0; i < TPW / 4; i++) {
+        const uint32_t tl = TPW * wave + 4 * i + lane / 16;
+        const uint32_t c = (lane % 16) ^ (tl & 15);
+        const uint32_t tok = t0 + tl, tk = tok < a.n ? tok : a.n - 1;
+        aoff[i] = tk * K + 16 * c;
     }
     auto issue = [&](uint32_t sb, uint32_t slot) {
         Slot &S = ring[slot];
+        const int8_t *ga = a.aqs + 256 * sb;
 #pragma unroll
-        for (uint32_t i = 0; i < TPW / 4; i++) {
-            const uint32_t tl = TPW * wave + 4 * i + lane / 16;
-            const uint32_t c = (lane % 16) ^ (tl & 15);
-            const uint32_t tok = t0 + tl, tk = tok < a.n ? tok : a.n - 1;
-            load_lds16(a.aqs + uint64_t(tk) * K + 256 * sb + 16 * c, &S.a[(TPW * wave + 4 * i) * 256]);
-        }
-        const uint64_t wo = uint64_t(sb) * 144;
+        for (uint32_t i = 0; i < TPW / 4; i++) load_lds16(ga + aoff[i], &S.a[(TPW * wave + 4 * i) * 256]);
+        const uint8_t *gw = a.w + uint64_t(sb) * 144;
 #pragma unroll
-        for (int i = 0; i < 4; i++) load_lds16(wsrc[i] + wo, &S.w[wave][1024 * i]);
+        for (int i = 0; i < 4; i++) load_lds16(gw + woff[i], &S.w[wave][1024 * i]);
 #pragma unroll
-        for (int i = 0; i < 2; i++) load_lds4(wsrc[4 + i] + wo, &S.w[wave][4096 + 256 * i]);
+        for (int i = 0; i < 2; i++) load_lds4(gw + woff[4 + i], &S.w[wave][4096 + 256 * i]);
         {
             const uint32_t tl = 32 * wave + lane / 2, tok = t0 + (tl < TOK ? tl : 0);
             const uint32_t tk = tok < a.n ? tok : a.n - 1;
@@ -455,17 +515,9 @@ __global__ __launch_bounds__(NW * 64, 2) void mm2_q4k_kernel(Mm2Args a) {
                 blo[2 * p + 1][i] = int(mul_bytes(no, slo));
             }
         }
-        // Min-term operand of this lane's row: -dmin*mn for sub-blocks 4h..4h+3, bf16 hi / lo.
-        v4s mhi, mlo;
-        {
-            const uint32_t mw = h ? mnh : mnl;
-#pragma unroll
-            for (int s = 0; s < 4; s++) {
-                const uint32_t sp = bf16_split(-dmin * (float)((mw >> (8 * s)) & 0xFF));
-                mhi[s] = short(sp & 0xFFFF);
-                mlo[s] = short(sp >> 16);
-            }
-        }
+        // Min-term operand of this lane's row.
+        const v8bf mB = min_b(mnl, mnh);
+        const float ndmin = -dmin;
 
         // A operand of tile t, sub-block s: token 32t + j, chunk 2s + h (swizzled).
         const int8_t *abase = &S.a[j * 256];
@@ -479,6 +531,7 @@ __global__ __launch_bounds__(NW * 64, 2) void mm2_q4k_kernel(Mm2Args a) {
         load_a(0);
 #pragma unroll
         for (int t = 0; t < TT; t++) {
+            const v16f jt = min_j(S.mb[32 * t + j], mB, h, acc[t][15]);
             // One accumulator: the sh-plane chain, times 8, then the sl-plane chain on top.
             v16i sacc = {};
 #pragma unroll
@@ -497,17 +550,9 @@ __global__ __launch_bounds__(NW * 64, 2) void mm2_q4k_kernel(Mm2Args a) {
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     const int v = 4 * g + e;
-                    acc[t][v] = fmaf((float)sacc[v], d * ds[e], acc[t][v]);
+                    acc[t][v] = fmaf(fmaf((float)sacc[v], d, ndmin * jt[v]), ds[e], acc[t][v]);
                 }
             }
-            // Min term: tokens' da*bsum32 (A) x rows' -dmin*mn (B), bf16 hi/lo split.
-            const uint32_t *mbp = S.mb[32 * t + j];
-            const uint2 ahi = *reinterpret_cast<const uint2 *>(mbp + 2 * h);
-            const uint2 alo = *reinterpret_cast<const uint2 *>(mbp + 4 + 2 * h);
-            const v4s ah = __builtin_bit_cast(v4s, ahi), al = __builtin_bit_cast(v4s, alo);
-            acc[t] = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(ah, mhi, acc[t], 0, 0, 0);
-            acc[t] = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(ah, mlo, acc[t], 0, 0, 0);
-            acc[t] = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(al, mhi, acc[t], 0, 0, 0);
         }
         // The next super-block's slot has landed once at most NB-2 later issues are pending.
         __builtin_amdgcn_s_waitcnt((0x0F70 & ~0xF) | ((CPW * (NB - 2)) & 0xF) | (((CPW * (NB - 2)) >> 4) << 14));
@@ -535,7 +580,10 @@ __global__ __launch_bounds__(NW * 64, 2) void mm2_q4k_kernel(Mm2Args a) {
 }
 
 bool mm2_supports(int t, uint32_t rows, uint32_t cols, uint32_t n) {
-    return t == HKHIP_Q4_K && cols % 256 == 0 && rows > 0 && n > 0;
+    // The kernels' per-lane byte offsets are 32-bit: weights rows*cols*9/16 bytes, activations
+    // n*cols bytes.
+    return t == HKHIP_Q4_K && cols % 256 == 0 && rows > 0 && n > 0 &&
+           uint64_t(rows) * (cols / 256) * 144 < (1ull << 32) && uint64_t(n) * cols < (1ull << 32);
 }
 
 typedef void (*mm2_kernel_t)(Mm2Args);

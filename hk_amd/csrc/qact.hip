@@ -34,15 +34,14 @@ __global__ void qact_q8k_kernel(const float *__restrict__ x, uint64_t nblocks, i
     reinterpret_cast<uint32_t *>(qs + b * QK_K)[lane] = r.packed;
     if ((lane & 3) == 0) bsout[b * 16 + lane / 4] = (int16_t)r.bsum;
     if (lane == 0) dout[b] = r.d;
-    // GEMM min-term operand: d * (sum over the 32 values of sub-block s) as bf16 hi + lo. The
-    // 16-value sums sit in lanes 4g; sub-block s = groups 2s and 2s+1 (lanes 8s and 8s+4).
+    // GEMM min-term operand: the sum over the 32 values of sub-block s, bsum32 = 64*u + v
+    // (v in [0, 63], u in [-64, 63]), as the exact bf16 integers 64*u and v. The 16-value sums
+    // sit in lanes 4g; sub-block s = groups 2s and 2s+1 (lanes 8s and 8s+4).
     const int b32 = r.bsum + __shfl_down(r.bsum, 4);
     if ((lane & 7) == 0) {
-        const float v = r.d * (float)b32;
-        const uint32_t hi = bf16_bits_rne(v);
-        const uint32_t lo = bf16_bits_rne(v - __builtin_bit_cast(float, hi << 16));
-        mbout[b * 16 + lane / 8] = uint16_t(hi);
-        mbout[b * 16 + 8 + lane / 8] = uint16_t(lo);
+        const int v = b32 & 63;
+        mbout[b * 16 + lane / 8] = uint16_t(bf16_bits_rne((float)(b32 - v)));
+        mbout[b * 16 + 8 + lane / 8] = uint16_t(bf16_bits_rne((float)v));
     }
 }
 

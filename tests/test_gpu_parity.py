@@ -237,6 +237,22 @@ def test_baseline_prefill_shapes(eng, torch_cuda, t, m, k):
     assert parity_err(got, want) <= PARITY_TOL
 
 
+@pytest.mark.parametrize("m,k,n,mode", [(12288, 256, 512, 0), (12000, 512, 520, 1)])
+def test_gemm_large_tile(eng, torch_cuda, m, k, n, mode):
+    """Shapes that select the Q4_K GEMM's 256-row x 128-token tile (at least 192 tiles): one
+    exact fit, one with ragged rows and tokens, bias and accumulate."""
+    t = F.Q4_K
+    raw = synth.weights_np(t, m, k, seed=600 + m)
+    x = synth.activations_np(n, k, seed=601, outliers=0.01)
+    bias = np.linspace(-1, 1, m).astype(np.float32) if mode else None
+    y0 = synth.activations_np(n, m, seed=602) if mode else None
+    got = run(eng, torch_cuda, t, raw, m, k, x, path="mm", bias=bias, mode=mode, y0=y0)
+    want = O.matmul(t, raw, m, k, x, n, bias=bias, threads=16)
+    if mode:
+        want = want + y0
+    assert parity_err(got, want) <= PARITY_TOL
+
+
 # ---------------------------------------------------------------------------------------- fused parts
 
 @pytest.mark.parametrize("t", FMTS)
