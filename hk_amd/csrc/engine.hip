@@ -315,11 +315,29 @@ int hkhip_gemm(hkhip_engine *eng, const hkhip_mat *m, const void *xq_dev, float 
     return HKHIP_OK;
 }
 
+// Fewest tokens for which the GEMM beats 8-token matvec passes (measured on MI355X at the
+// Llama-3-8B FFN shapes: a GEMM pass costs about as much at 16 tokens as at 64, while each
+// matvec pass of 8 tokens streams the weights once more).
+static uint32_t gemm_min_tokens(int t) {
+    switch (t) {
+    case HKHIP_Q6_K: return 65;
+    case HKHIP_Q8_0:
+    case HKHIP_IQ4_NL: return 25;
+    default: return 9;
+    }
+}
+
 int hkhip_mm(hkhip_engine *eng, const hkhip_mat *m, const void *xq_dev, float *y_dev, uint32_t n,
              const float *bias_dev, int mode) {
-    // matmul.zig:18 min_tiled_tokens = 8
-    return n < 8 ? hkhip_matvec(eng, m, xq_dev, y_dev, n, bias_dev, mode)
-                 : hkhip_gemm(eng, m, xq_dev, y_dev, n, bias_dev, mode);
+    // The CPU engine tiles from min_tiled_tokens = 8 (matmul.zig:18); here the register matvec
+    // covers up to 8 tokens and, below the GEMM's break-even, runs in passes of 8.
+    if (n <= 8) return hkhip_matvec(eng, m, xq_dev, y_dev, n, bias_dev, mode);
+    if (n >= gemm_min_tokens(m->t)) return hkhip_gemm(eng, m, xq_dev, y_dev, n, bias_dev, mode);
+    int rc = enter(eng);
+    if (rc || (rc = check_product(m, xq_dev, y_dev, n, mode))) return rc;
+    HIP_TRY(launch_mmvq(m->t, reinterpret_cast<const uint8_t *>(m->mem), m->rows, m->cols,
+                        reinterpret_cast<const uint8_t *>(xq_dev), n, y_dev, bias_dev, mode, eng->cur), "mmvq launch");
+    return HKHIP_OK;
 }
 
 // ---- host-pointer products on a process-wide default engine ----

@@ -1057,8 +1057,31 @@ static int cu_count() {
 }
 
 
-hipError_t launch_mmvq_parts(int t, const MvPartDesc *parts, int nparts, uint32_t K, const float *x,
-                             const uint8_t *xq, uint32_t n, int mode, hipStream_t s) {
+// Where a launch finds its input: an f32 array, or the planes of a prepared activation buffer.
+struct MvAct {
+    const float *x;
+    const int8_t *qs;
+    const float *d;
+    const int16_t *bs;
+};
+
+// The input of tokens t0.. of `a`.
+static MvAct mv_act_at(const MvAct &a, bool kq, uint32_t K, uint32_t t0) {
+    MvAct r{};
+    if (a.x) {
+        r.x = a.x + uint64_t(t0) * K;
+    } else {
+        r.qs = a.qs + uint64_t(t0) * K;
+        r.d = a.d + uint64_t(t0) * (K / (kq ? 256 : 32));
+        r.bs = a.bs + uint64_t(t0) * (K / 16);
+    }
+    return r;
+}
+
+// One launch (register kernel) or a few (LDS kernel) for at most 8 tokens.
+static hipError_t launch_mv_chunk(int t, const MvPartDesc *parts, int nparts, uint32_t K, const MvAct &act,
+                                  uint32_t n, int mode, hipStream_t s) {
+    const float *x = act.x;
     if (n < 1 || n > 8 || nparts < 1 || nparts > MV_PARTS) return hipErrorInvalidValue;
     const bool kq = (t == HKHIP_Q4_K || t == HKHIP_Q6_K);
     {
@@ -1099,14 +1122,10 @@ hipError_t launch_mmvq_parts(int t, const MvPartDesc *parts, int nparts, uint32_
             a.K = K;
             a.mode = mode;
             a.ntok = n;
-            if (x) {
-                a.x = x;
-            } else {
-                const ActLayout A = act_layout(n, K);
-                a.gqs = reinterpret_cast<const int8_t *>(xq + (kq ? A.k_qs : A.a8_qs));
-                a.gd = reinterpret_cast<const float *>(xq + (kq ? A.k_d : A.a8_d));
-                a.gbs = reinterpret_cast<const int16_t *>(xq + A.k_bs);
-            }
+            a.x = act.x;
+            a.gqs = act.qs;
+            a.gd = act.d;
+            a.gbs = act.bs;
             if (rows == 0) return hipSuccess;
             const int R = mvr_rows(nt, c);
             const int nw = mvr_nw(t, nt, c), nrg = nw / ks;
@@ -1136,8 +1155,6 @@ hipError_t launch_mmvq_parts(int t, const MvPartDesc *parts, int nparts, uint32_
     while ((1u << lg) < want_lanes && lg < 6) lg++;
     const uint32_t rpw = 64u >> lg;
     const int nw = MV_NW;
-    const ActLayout A = act_layout(n, K);
-    const uint32_t dblk = kq ? 256 : 32;
     for (uint32_t t0 = 0; t0 < n; t0 += per) {
         const int nt = int(n - t0 < uint32_t(per) ? n - t0 : uint32_t(per));
         MvArgs a{};
@@ -1158,13 +1175,11 @@ hipError_t launch_mmvq_parts(int t, const MvPartDesc *parts, int nparts, uint32_
         a.K = K;
         a.mode = mode;
         a.lpr_log2 = lg;
-        if (x) {
-            a.x = x + uint64_t(t0) * K;
-        } else {
-            a.gqs = reinterpret_cast<const int8_t *>(xq + (kq ? A.k_qs : A.a8_qs)) + uint64_t(t0) * K;
-            a.gd = reinterpret_cast<const float *>(xq + (kq ? A.k_d : A.a8_d)) + uint64_t(t0) * (K / dblk);
-            a.gbs = reinterpret_cast<const int16_t *>(xq + A.k_bs) + uint64_t(t0) * (K / 16);
-        }
+        const MvAct at = mv_act_at(act, kq, K, t0);
+        a.x = at.x;
+        a.gqs = at.qs;
+        a.gd = at.d;
+        a.gbs = at.bs;
         if (groups == 0) continue;
         mv_kernel_t k = kernel_for(t, nt);
         if (!k) return hipErrorInvalidValue;
@@ -1178,6 +1193,33 @@ hipError_t launch_mmvq_parts(int t, const MvPartDesc *parts, int nparts, uint32_
         const uint32_t grid = want < cap ? want : cap;
         hipLaunchKernelGGL(k, dim3(grid), dim3(nw * 64), lds, s, a);
         hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+hipError_t launch_mmvq_parts(int t, const MvPartDesc *parts, int nparts, uint32_t K, const float *x,
+                             const uint8_t *xq, uint32_t n, int mode, hipStream_t s) {
+    if (n < 1 || nparts < 1 || nparts > MV_PARTS) return hipErrorInvalidValue;
+    const bool kq = (t == HKHIP_Q4_K || t == HKHIP_Q6_K);
+    MvAct act{};
+    if (x) {
+        act.x = x;
+    } else {
+        const ActLayout A = act_layout(n, K);
+        act.qs = reinterpret_cast<const int8_t *>(xq + (kq ? A.k_qs : A.a8_qs));
+        act.d = reinterpret_cast<const float *>(xq + (kq ? A.k_d : A.a8_d));
+        act.bs = reinterpret_cast<const int16_t *>(xq + A.k_bs);
+    }
+    // Up to 8 tokens per launch; more run as consecutive chunks of 8.
+    for (uint32_t t0 = 0; t0 < n; t0 += 8) {
+        const uint32_t nc = n - t0 < 8 ? n - t0 : 8;
+        MvPartDesc pc[MV_PARTS];
+        for (int i = 0; i < nparts; i++) {
+            pc[i] = parts[i];
+            pc[i].y = parts[i].y + uint64_t(t0) * parts[i].rows;
+        }
+        const hipError_t e = launch_mv_chunk(t, pc, nparts, K, t0 ? mv_act_at(act, kq, K, t0) : act, nc, mode, s);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;

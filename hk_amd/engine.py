@@ -165,7 +165,8 @@ class Engine:
         check(lib().hkhip_gemm(self._h, ctypes.byref(m.raw), _ptr(xq), _ptr(y), n, _ptr(bias), mode))
 
     def mm(self, m: DevMat, xq, y, n: int, bias=None, mode: int = STORE) -> None:
-        """y[t][r] = dot(W[r], x[t]) + bias[r]: decode kernel below 8 tokens, MFMA GEMM from 8
+        """y[t][r] = dot(W[r], x[t]) + bias[r]: decode kernel up to 8 tokens, 8-token decode passes
+        up to the GEMM's break-even (Q6_K 64, Q8_0 / IQ4_NL 24 tokens), MFMA GEMM beyond
         (mm: cuda/engine.zig:581-611; matmul.zig:18,107)."""
         check(lib().hkhip_mm(self._h, ctypes.byref(m.raw), _ptr(xq), _ptr(y), n, _ptr(bias), mode))
 

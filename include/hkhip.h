@@ -121,7 +121,9 @@ int hkhip_act_export(hkhip_engine *eng, const void *xq_dev, uint32_t n, uint32_t
  * with hkhip_qact for the matrix's kind (A8: Q8_0, IQ4_NL; Q8K: Q4_K, Q6_K). bias may be NULL.
  * hkhip_matvec: decode kernels, 1 <= n <= 8 (src/kernels_impl.zig:14-33 rows).
  * hkhip_gemm:   prefill MFMA kernels, any n >= 1 (src/quant/gemm.zig tiles).
- * hkhip_mm:     picks matvec for n < 8 and gemm otherwise (matmul.zig:18 min_tiled_tokens). */
+ * hkhip_mm:     picks matvec for n <= 8, then 8-token matvec passes up to the GEMM's break-even
+ *               (Q6_K: 64 tokens, Q8_0 / IQ4_NL: 24), then gemm (the CPU engine's switch is
+ *               matmul.zig:18 min_tiled_tokens = 8). */
 int hkhip_matvec(hkhip_engine *eng, const hkhip_mat *m, const void *xq_dev, float *y_dev, uint32_t n,
                  const float *bias_dev, int mode);
 int hkhip_gemm(hkhip_engine *eng, const hkhip_mat *m, const void *xq_dev, float *y_dev, uint32_t n,

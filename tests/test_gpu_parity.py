@@ -169,6 +169,21 @@ def test_mm_dispatch_bias_accumulate(eng, torch_cuda, t, n):
     assert parity_err(got, want) <= PARITY_TOL
 
 
+
+@pytest.mark.parametrize("t", FMTS)
+@pytest.mark.parametrize("n", [9, 17, 24, 40])
+def test_mm_chunked_matvec(eng, torch_cuda, t, n):
+    """hkhip_mm between 8 tokens and the GEMM's break-even runs 8-token matvec passes (a ragged
+    last one); bias and accumulate apply once per token."""
+    m, k = 300, 1024
+    raw = synth.weights_np(t, m, k, seed=700 + t)
+    x = synth.activations_np(n, k, seed=701 + n)
+    bias = np.linspace(-1, 1, m).astype(np.float32)
+    y0 = synth.activations_np(n, m, seed=702)
+    got = run(eng, torch_cuda, t, raw, m, k, x, path="mm", bias=bias, mode=1, y0=y0)
+    want = O.matmul(t, raw, m, k, x, n, bias=bias) + y0
+    assert parity_err(got, want) <= PARITY_TOL
+
 def test_host_gemv_entry_points(torch_cuda):
     from hk_amd import gemm, gemv
 
