@@ -151,6 +151,10 @@ hipError_t launch_mmvq_parts(int t, const MvPartDesc *parts, int nparts, uint32_
 hipError_t launch_mmvq(int t, const uint8_t *w, uint32_t rows, uint32_t cols, const uint8_t *xq, uint32_t n,
                        float *y, const float *bias, int mode, hipStream_t s);
 bool mm2_supports(int t, uint32_t rows, uint32_t cols, uint32_t n);
+// Small-batch MFMA product (Q4_K, 1..32 tokens): weights streamed like the decode kernels.
+bool mmsk_supports(int t, uint32_t rows, uint32_t cols, uint32_t n);
+hipError_t launch_mmsk(int t, const uint8_t *w, uint32_t rows, uint32_t cols, const uint8_t *xq, uint32_t n,
+                       float *y, const float *bias, int mode, hipStream_t s);
 hipError_t launch_mm2(int t, const uint8_t *w, uint32_t rows, uint32_t cols, const uint8_t *xq, uint32_t n, float *y,
                       const float *bias, int mode, hipStream_t s);
 hipError_t launch_mm(int t, const uint8_t *w, uint32_t rows, uint32_t cols, const uint8_t *xq, uint32_t n,

@@ -36,6 +36,8 @@
 
 #include "common.hpp"
 
+#include <type_traits>
+
 namespace hkhip {
 
 
@@ -78,14 +80,18 @@ struct Mm2Args {
 
 __device__ __forceinline__ uint4 ldg16(const void *p) { return *reinterpret_cast<const uint4 *>(p); }
 
-// 16 bytes per lane global -> LDS (lane L writes at lds + 16*L). A non-template function: used
-// directly in the kernel template, the builtin keeps the host side from emitting its stub.
-__device__ __forceinline__ void load_lds16(const void *g, void *lds) {
-    __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
+// 16 (4) bytes per lane global -> LDS: lane L writes at the wave-uniform LDS address + 16*L
+// (4*L). Issued as inline assembly: the compiler then keeps no books on these loads (the kernels
+// wait for them with explicit counts), where for the builtin it would wait for all of them before
+// an LDS read it cannot prove independent -- which drains the prefetch ring every step.
+__device__ __forceinline__ uint32_t lds_addr(const void *lds) {
+    return uint32_t((uintptr_t)(const __attribute__((address_space(3))) void *)lds);
 }
-
+__device__ __forceinline__ void load_lds16(const void *g, void *lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(lds_addr(lds)) : "memory", "m0");
+}
 __device__ __forceinline__ void load_lds4(const void *g, void *lds) {
-    __builtin_amdgcn_global_load_lds(g, lds, 4, 0, 0);
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" : : "v"(g), "s"(lds_addr(lds)) : "memory", "m0");
 }
 
 // fp32 -> bf16 bits, round to nearest even (finite inputs).
@@ -390,8 +396,22 @@ template <int NW, int TT, int NB>
 __global__ __launch_bounds__(NW * 64, 2) void mm2_q4k_kernel(Mm2Args a) {
     constexpr int ROWS = 32 * NW, TOK = 32 * TT;
     using Slot = Q2Slot<TOK, NW>;
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
-    Slot *ring = reinterpret_cast<Slot *>(smem_raw);
+    static_assert(NB == 2 || NB == 3, "ring depth");
+    // The ring's slots are LDS objects of their own, and the loop below is unrolled over them, so
+    // the compiler can tell that reading one slot does not alias the direct loads into another
+    // (with one array it would wait for every load in flight before the first read).
+    __shared__ __attribute__((aligned(16))) Slot ring0;
+    __shared__ __attribute__((aligned(16))) Slot ring1;
+    __shared__ __attribute__((aligned(16))) Slot ring2;
+    auto slot_at = [&](auto ic) -> Slot & {
+        constexpr int i = decltype(ic)::value;
+        if constexpr (i == 0)
+            return ring0;
+        else if constexpr (i == 1)
+            return ring1;
+        else
+            return ring2;
+    };
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t h = lane >> 5, j = lane & 31;
@@ -443,8 +463,7 @@ __global__ __launch_bounds__(NW * 64, 2) void mm2_q4k_kernel(Mm2Args a) {
         const uint32_t tok = t0 + tl, tk = tok < a.n ? tok : a.n - 1;
         aoff[i] = tk * K + 16 * c;
     }
-    auto issue = [&](uint32_t sb, uint32_t slot) {
-        Slot &S = ring[slot];
+    auto issue = [&](uint32_t sb, Slot &S) {
         const int8_t *ga = a.aqs + 256 * sb;
 #pragma unroll
         for (uint32_t i = 0; i < TPW / 4; i++) load_lds16(ga + aoff[i], &S.a[(TPW * wave + 4 * i) * 256]);
@@ -472,19 +491,20 @@ __global__ __launch_bounds__(NW * 64, 2) void mm2_q4k_kernel(Mm2Args a) {
         for (int v = 0; v < 16; v++) acc[t][v] = 0.0f;
 
     // Prologue: NB-1 super-blocks in flight.
-#pragma unroll
-    for (int p = 0; p < NB - 1; p++) issue(p < int(nsb) ? p : nsb - 1, p);
+    issue(0, ring0);
+    if constexpr (NB == 3) issue(1 < nsb ? 1 : nsb - 1, ring1);
     // Wait for slot 0 (the loads of NB-2 later super-blocks may stay in flight).
     __builtin_amdgcn_s_waitcnt((0x0F70 & ~0xF) | ((CPW * (NB - 2)) & 0xF) | (((CPW * (NB - 2)) >> 4) << 14));
     __syncthreads();
 
-    for (uint32_t sb = 0; sb < nsb; sb++) {
-        const uint32_t slot = sb % NB;
+    // One super-block from slot IC while the one NB-1 ahead goes into slot (IC + NB-1) % NB.
+    auto step = [&](auto ic, uint32_t sb) {
+        constexpr int I = decltype(ic)::value;
         {
             const uint32_t ahead = sb + NB - 1;
-            issue(ahead < nsb ? ahead : nsb - 1, ahead % NB);
+            issue(ahead < nsb ? ahead : nsb - 1, slot_at(std::integral_constant<int, (I + NB - 1) % NB>{}));
         }
-        Slot &S = ring[slot];
+        Slot &S = slot_at(ic);
 
         // Unpack this lane's row half (h) from LDS: header, then both planes of 8 sub-blocks.
         const uint8_t *blk = &S.w[wave][144 * j];
@@ -557,6 +577,12 @@ __global__ __launch_bounds__(NW * 64, 2) void mm2_q4k_kernel(Mm2Args a) {
         // The next super-block's slot has landed once at most NB-2 later issues are pending.
         __builtin_amdgcn_s_waitcnt((0x0F70 & ~0xF) | ((CPW * (NB - 2)) & 0xF) | (((CPW * (NB - 2)) >> 4) << 14));
         __syncthreads();
+    };
+    for (uint32_t sb = 0; sb < nsb; sb += NB) {
+        step(std::integral_constant<int, 0>{}, sb);
+        if (sb + 1 < nsb) step(std::integral_constant<int, 1>{}, sb + 1);
+        if constexpr (NB == 3)
+            if (sb + 2 < nsb) step(std::integral_constant<int, 2>{}, sb + 2);
     }
 
     // ---- store: y[token][row], bias, accumulate ----
@@ -607,13 +633,8 @@ static hipError_t launch_mm2_reg(const Mm2Args &a0, hipStream_t s) {
 template <int NW, int TT, int NB>
 static hipError_t launch_mm2_cfg(const Mm2Args &a0, hipStream_t s) {
     const mm2_kernel_t k = mm2_q4k_kernel<NW, TT, NB>;
-    constexpr size_t lds = NB * sizeof(Q2Slot<32 * TT, NW>);
-    static_assert(lds <= 160 * 1024, "LDS");
-    static bool attr = false;
-    if (!attr) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k), hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
-        attr = true;
-    }
+    static_assert(NB * sizeof(Q2Slot<32 * TT, NW>) <= 160 * 1024, "LDS");
+    constexpr size_t lds = 0; // the ring is static
     Mm2Args a = a0;
     a.rblocks = (a.rows + 32 * NW - 1) / (32 * NW);
     a.tblocks = (a.n + 32 * TT - 1) / (32 * TT);
