@@ -16,8 +16,11 @@ algorithmic bytes (file-layout weight bytes + f32 activations in + f32 outputs) 
 Also reported:
   roofline      the dominant kernel (Q4_K matvec, 14336x4096, batch 1), timed with HIP events
                 over back-to-back launches that rotate through the 64 distinct gate/up matrices
-  prefill       Q4_K GEMM, 512 tokens, at the 8B FFN shape (14336x4096) and Qwen3-0.6B FFN-up
-                (3072x1024), in TOPS against the 5.0 POPS dense int8 MFMA peak
+  prefill       GEMM at 512 tokens, in TOPS against the 5.0 POPS dense int8 MFMA peak: Q4_K at the
+                8B FFN shapes (14336x4096, 4096x14336) and the Qwen3-0.6B FFN shapes (3072x1024,
+                1024x3072), IQ4_NL 14336x4096 and Q6_K 4096x14336
+  extra         the decode step at batch 8 (config 4), and config 5's batch-1 matvecs (IQ4_NL
+                14336x4096, Q6_K 4096x14336) rotating over 12 matrices each
   cpu_baseline  the oracle's restatement of hk's CPU kernels on the host cores, on a bounded
                 sample (the 14336x4096 Q4_K matvec, repeated for ~10 s)
 """
@@ -43,7 +46,7 @@ def parse():
     p.add_argument("--layers", type=int, default=LLAMA8B["layers"])
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
-    p.add_argument("--only", choices=["all", "decode", "kernel", "prefill", "copy"], default="all",
+    p.add_argument("--only", choices=["all", "decode", "kernel", "prefill", "extra", "copy"], default="all",
                    help="run one part only (profiling); 'copy' runs a plain 256 MiB device copy 20 times, "
                         "the calibration for the HBM traffic counters")
     return p.parse_args()
@@ -59,6 +62,7 @@ def main():
     import torch
 
     from hk_amd import Engine, formats as F, synth
+    FMT_NAME = {F.Q4_K: "q4_k", F.Q6_K: "q6_k", F.Q8_0: "q8_0", F.IQ4_NL: "iq4_nl"}
 
     torch.cuda.init()
     dev = torch.device("cuda:0")
@@ -183,22 +187,68 @@ def main():
     # ---- prefill GEMM, 512 tokens ----
     if args.only in ("all", "prefill"):
         pre = []
+        # The headline shape first, then BASELINE configs 3 (Qwen3-0.6B FFN) and 5 (8B FFN in the
+        # mixed formats), and the 8B down projection.
         for (name, t, m_, k_) in [("llama8b-ffn-up", F.Q4_K, FF, H), ("qwen3-0.6b-ffn-up", F.Q4_K, 3072, 1024),
-                                  ("qwen3-0.6b-ffn-down", F.Q4_K, 1024, 3072)]:
+                                  ("qwen3-0.6b-ffn-down", F.Q4_K, 1024, 3072),
+                                  ("llama8b-ffn-down", F.Q4_K, H, FF),
+                                  ("llama8b-ffn-up", F.IQ4_NL, FF, H), ("llama8b-ffn-down", F.Q6_K, H, FF)]:
             n = 512
-            reuse = layers[0]["gate"] if (m_, k_) == (FF, H) else None
-            w = reuse or upload_synth(t, m_, k_, synth.seed_for(3, m_ + k_))
+            reuse = layers[0]["gate"] if (t, m_, k_) == (F.Q4_K, FF, H) else None
+            w = reuse or upload_synth(t, m_, k_, synth.seed_for(3, m_ + k_ + t))
             x = torch.randn(n, k_, device=dev)
             xq = torch.empty(eng.act_bytes(n, k_), dtype=torch.uint8, device=dev)
             yy = torch.empty(n, m_, device=dev)
-            eng.qact(x, n, k_, F.ACT_Q8K, xq)
+            eng.qact(x, n, k_, F.ACT_KIND[t], xq)
             us = time_graph(torch, eng, stream, lambda: eng.gemm(w, xq, yy, n), 5)
             tops = 2.0 * m_ * n * k_ / (us * 1e-6) / 1e12
-            pre.append(dict(shape=f"{m_}x{k_}x{n}", fmt="q4_k", avg_us=round(us, 2), tops=round(tops, 2),
-                            frac_int8_peak=round(tops / INT8_PEAK_TOPS, 4)))
+            pre.append(dict(shape=f"{m_}x{k_}x{n}", fmt=FMT_NAME[t], workload=name, avg_us=round(us, 2),
+                            tops=round(tops, 2), frac_int8_peak=round(tops / INT8_PEAK_TOPS, 4)))
             if reuse is None:
                 eng.free(w)
         result["prefill"] = pre
+
+    # ---- BASELINE config 4 at batch 8 (the decode step for 8 tokens) and config 5's batch-1
+    # matvecs (IQ4_NL gate/up, Q6_K down), each rotating over 12 distinct matrices so that the
+    # 256 MB Infinity Cache cannot serve them.
+    if args.only in ("all", "extra"):
+        extra = {}
+        x_h8 = torch.randn(8, H, device=dev)
+        x_f8 = torch.randn(8, FF, device=dev)
+        outs8 = {name: torch.empty(8, r, device=dev) for name, r, _ in shapes}
+        logits8 = torch.empty(8, V, device=dev)
+
+        def step8():
+            for lw in layers:
+                eng.matvec_parts([lw["q"], lw["k"], lw["v"]], [outs8["q"], outs8["k"], outs8["v"]], 8, x=x_h8)
+                eng.matvec_parts([lw["o"]], [outs8["o"]], 8, x=x_h8)
+                eng.matvec_parts([lw["gate"], lw["up"]], [outs8["gate"], outs8["up"]], 8, x=x_h8)
+                eng.matvec_parts([lw["down"]], [outs8["down"]], 8, x=x_f8)
+            eng.matvec_parts([lm_head], [logits8], 8, x=x_h8)
+
+        us8 = time_graph(torch, eng, stream, step8, max(3, args.steps // 5), per_graph=1)
+        b8_bytes = weight_bytes + 8 * act_bytes
+        extra["decode_batch8"] = dict(ms_per_step=round(us8 / 1e3, 4), tokens_per_s=round(8e6 / us8, 1),
+                                      gbs=round(b8_bytes / (us8 * 1e-6) / 1e9, 1),
+                                      frac_hbm_peak=round(b8_bytes / (us8 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4))
+        mv = []
+        for (name, t, m_, k_) in [("llama8b-ffn-up", F.IQ4_NL, FF, H), ("llama8b-ffn-down", F.Q6_K, H, FF)]:
+            ws = [upload_synth(t, m_, k_, synth.seed_for(5, 100 * t + i)) for i in range(12)]
+            xv = torch.randn(1, k_, device=dev)
+            yv = torch.empty(1, m_, device=dev)
+
+            def rot():
+                for w_ in ws:
+                    eng.matvec_parts([w_], [yv], 1, x=xv)
+
+            us = time_graph(torch, eng, stream, rot, 5, per_graph=1) / len(ws)
+            mv.append(dict(shape=f"{m_}x{k_}", fmt=FMT_NAME[t], workload=name, avg_us=round(us, 2),
+                           gbs=round(ws[0].file_bytes / (us * 1e-6) / 1e9, 1),
+                           frac_hbm_peak=round(ws[0].file_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)))
+            for w_ in ws:
+                eng.free(w_)
+        extra["matvec_batch1"] = mv
+        result["extra"] = extra
 
     # ---- CPU baseline: the oracle on the host cores, bounded sample ----
     cpu = None
@@ -232,6 +282,7 @@ def main():
                      "kernel": ker.get("name"), "shape": ker.get("shape"), "avg_us": ker.get("avg_us"),
                      "bytes_per_launch": ker.get("bytes_per_launch")},
         "prefill": result.get("prefill"),
+        "extra": result.get("extra"),
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
