@@ -218,7 +218,26 @@ def main():
         outs8 = {name: torch.empty(8, r, device=dev) for name, r, _ in shapes}
         logits8 = torch.empty(8, V, device=dev)
 
+        xq_h8 = torch.empty(eng.act_bytes(8, H), dtype=torch.uint8, device=dev)
+        xq_f8 = torch.empty(eng.act_bytes(8, FF), dtype=torch.uint8, device=dev)
+
         def step8():
+            # Each product quantizes its own input (a decoder's four projections read four
+            # different vectors), then runs on the prepared activations: the Q4_K layers on the
+            # small-batch MFMA kernel, the Q6_K lm_head on the decode kernel.
+            for lw in layers:
+                eng.qact(x_h8, 8, H, F.ACT_Q8K, xq_h8)
+                eng.matvec_parts([lw["q"], lw["k"], lw["v"]], [outs8["q"], outs8["k"], outs8["v"]], 8, xq=xq_h8)
+                eng.qact(x_h8, 8, H, F.ACT_Q8K, xq_h8)
+                eng.matvec_parts([lw["o"]], [outs8["o"]], 8, xq=xq_h8)
+                eng.qact(x_h8, 8, H, F.ACT_Q8K, xq_h8)
+                eng.matvec_parts([lw["gate"], lw["up"]], [outs8["gate"], outs8["up"]], 8, xq=xq_h8)
+                eng.qact(x_f8, 8, FF, F.ACT_Q8K, xq_f8)
+                eng.matvec_parts([lw["down"]], [outs8["down"]], 8, xq=xq_f8)
+            eng.qact(x_h8, 8, H, F.ACT_Q8K, xq_h8)
+            eng.matvec_parts([lm_head], [logits8], 8, xq=xq_h8)
+
+        def step8_f32():
             for lw in layers:
                 eng.matvec_parts([lw["q"], lw["k"], lw["v"]], [outs8["q"], outs8["k"], outs8["v"]], 8, x=x_h8)
                 eng.matvec_parts([lw["o"]], [outs8["o"]], 8, x=x_h8)
@@ -227,6 +246,8 @@ def main():
             eng.matvec_parts([lm_head], [logits8], 8, x=x_h8)
 
         us8 = time_graph(torch, eng, stream, step8, max(3, args.steps // 5), per_graph=1)
+        us8f = time_graph(torch, eng, stream, step8_f32, max(3, args.steps // 5), per_graph=1)
+        extra["decode_batch8_f32_inputs_ms"] = round(us8f / 1e3, 4)
         b8_bytes = weight_bytes + 8 * act_bytes
         extra["decode_batch8"] = dict(ms_per_step=round(us8 / 1e3, 4), tokens_per_s=round(8e6 / us8, 1),
                                       gbs=round(b8_bytes / (us8 * 1e-6) / 1e9, 1),

@@ -73,8 +73,18 @@ inline WLayout weight_layout(int t, uint32_t rows, uint32_t cols) {
 //   k_mb  [n][k/256][16] bf16: per super-block, its 8 sub-blocks' 32-value sums as exact bf16
 //         integers, bsum32 = 64*u + v with v in [0, 63]: 64*u for the 8 sub-blocks, then v --
 //         the token-side operand of the GEMM's integer min term, precomputed once
+//   For at most SK_MAX_TOKENS tokens, token-interleaved copies of the Q8K planes for the
+//   small-batch kernel, tokens in tiles of 16 (the last one padded with the last token):
+//   k_il   [k/64][tiles][64][16 B]: entry 16g + p holds token 16*tile + p's values
+//          64c + 16g .. 64c + 16g + 15 -- one 16-token tile's 64-value chunk is 1 KB in the
+//          order of the MFMA lanes that use it
+//   k_ilmb [k/256][tiles][2][16][16 B]: k_mb's two 16-byte halves, token-interleaved
+//   k_ild  [k/256][tiles][16] f32: k_d, token-interleaved
+constexpr uint32_t SK_MAX_TOKENS = 32;
+constexpr uint32_t SK_MIN_TOKENS = 4; // below, the decode kernels are faster
 struct ActLayout {
-    uint64_t a8_qs, a8_d, a8_s, k_qs, k_d, k_bs, k_mb, total;
+    uint64_t a8_qs, a8_d, a8_s, k_qs, k_d, k_bs, k_mb, k_il, k_ilmb, k_ild, total;
+    uint32_t tiles; // 16-token tiles of the interleaved planes (0: none)
 };
 
 inline ActLayout act_layout(uint32_t n, uint32_t k) {
@@ -88,6 +98,11 @@ inline ActLayout act_layout(uint32_t n, uint32_t k) {
     L.k_d = o;   o = align256(o + (k % QK_K == 0 ? nk / QK_K * 4 : 0));
     L.k_bs = o;  o = align256(o + (k % QK_K == 0 ? nk / 16 * 2 : 0));
     L.k_mb = o;  o = align256(o + (k % QK_K == 0 ? nk / QK_K * 32 : 0));
+    L.tiles = (k % QK_K == 0 && n >= 1 && n <= SK_MAX_TOKENS) ? (n + 15) / 16 : 0;
+    const uint64_t tk = uint64_t(L.tiles) * 16 * k; // interleaved entries (padded tokens)
+    L.k_il = o;   o = align256(o + tk);
+    L.k_ilmb = o; o = align256(o + tk / QK_K * 32);
+    L.k_ild = o;  o = align256(o + tk / QK_K * 4);
     L.total = o;
     return L;
 }
@@ -155,6 +170,8 @@ bool mm2_supports(int t, uint32_t rows, uint32_t cols, uint32_t n);
 bool mmsk_supports(int t, uint32_t rows, uint32_t cols, uint32_t n);
 hipError_t launch_mmsk(int t, const uint8_t *w, uint32_t rows, uint32_t cols, const uint8_t *xq, uint32_t n,
                        float *y, const float *bias, int mode, hipStream_t s);
+hipError_t launch_mmsk_parts(int t, const MvPartDesc *parts, int nparts, uint32_t cols, const uint8_t *xq,
+                             uint32_t n, int mode, hipStream_t s);
 hipError_t launch_mm2(int t, const uint8_t *w, uint32_t rows, uint32_t cols, const uint8_t *xq, uint32_t n, float *y,
                       const float *bias, int mode, hipStream_t s);
 hipError_t launch_mm(int t, const uint8_t *w, uint32_t rows, uint32_t cols, const uint8_t *xq, uint32_t n,

@@ -286,7 +286,7 @@ hipError_t launch_mm(int t, const uint8_t *w, uint32_t rows, uint32_t cols, cons
     if (rows == 0 || n == 0) return hipSuccess;
     // Few tokens: the weights dominate, so the kernel that streams them (small-batch MFMA); many:
     // the tiled GEMM.
-    if (mmsk_supports(t, rows, cols, n)) return launch_mmsk(t, w, rows, cols, xq, n, y, bias, mode, s);
+    if (n >= SK_MIN_TOKENS && mmsk_supports(t, rows, cols, n)) return launch_mmsk(t, w, rows, cols, xq, n, y, bias, mode, s);
     if (mm2_supports(t, rows, cols, n)) return launch_mm2(t, w, rows, cols, xq, n, y, bias, mode, s);
     WLayout W = weight_layout(t, rows, cols);
     ActLayout A = act_layout(n, cols);

@@ -1,10 +1,9 @@
 // Small-batch product for Q4_K (2..32 tokens) on the int8 MFMA units.
 //
-// Between single-token decode and prefill, the weights still dominate the bytes (each is used by
-// a handful of tokens), so this kernel streams them like the decode kernels -- every wave loads
-// its rows' blocks straight from HBM into registers, two super-blocks in flight -- but
-// multiplies them against the tokens on v_mfma_i32_16x16x64_i8 instead of per-token dot
-// products, so the per-weight VALU work no longer grows with the token count.
+// Between single-token decode and prefill the weights still dominate the bytes (each is used by
+// a handful of tokens), so this kernel streams them like the decode kernels, but multiplies them
+// against the tokens on v_mfma_i32_16x16x64_i8 instead of per-token dot products: the per-weight
+// VALU work no longer grows with the token count.
 //
 // Arithmetic (hk's CPU kernel, src/quant/gemm.zig kernelK 180-236, per row r, token t,
 // super-block b):  y += da*(d*I - dmin*J),  I = sum_s sc_s * sum_{k in s} q*a,
@@ -13,15 +12,22 @@
 //    product at most 105 (one packed 16-bit multiply per four weights); the MFMA chain runs the
 //    sh plane, the result is multiplied by 8, then the sl plane is added on top.
 //  * J: one v_mfma_f32_16x16x32_bf16 over exact bf16 integers: the mins against the tokens'
-//    bsum32 = 64*u + v (the activation buffer's k_mb plane), exact in f32 (|J| < 2^22).
+//    bsum32 = 64*u + v (the activation buffer's k_ilmb plane), exact in f32 (|J| < 2^22).
 //
-// Layout. A workgroup owns 16 rows; its KS waves split the super-blocks (KS is picked so that
-// the launch has about 2048 waves) and add their partial sums in LDS at the end. Each wave keeps
-// PF super-blocks in flight. MFMA roles: A = weights (row = lane % 16), B = activations (token =
-// lane % 16); lane group g = lane / 16 supplies k = 16g..16g+15 of each 64-value chunk, so the
-// four groups read a token's chunk as one contiguous 64-byte piece and a row's chunk as two
-// 16-byte pieces (groups g and g+2 read the same bytes: low and high nibbles are sub-blocks 2c
-// and 2c+1 of chunk c). Output lane l holds rows 4*(l/16) + i (i < 4) of token l % 16.
+// Layout. A workgroup owns 16 rows of one part (fused products: up to 4 matrices reading the
+// same input, their row tiles numbered in sequence); its KS waves split the super-blocks and add
+// their partial sums in LDS at the end. MFMA roles: A = weights (row = lane % 16), B =
+// activations (token = lane % 16); lane group g = lane / 16 supplies values 16g..16g+15 of each
+// 64-value chunk. Output lane l holds rows 4*(l/16) + i (i < 4) of token l % 16.
+//
+// Memory. Every global access is a contiguous piece of 1 KB (or 512 / 64 bytes): the weights of
+// a super-block (16 rows x 144 bytes) go global -> LDS by direct loads into a per-wave ring of PF
+// slots and are read back from there; the activations come from the token-interleaved planes
+// the quantizer writes for small batches (k_il: a tile's 64-value chunk is 1 KB in lane order).
+// The direct loads are issued as inline assembly (the compiler would otherwise wait for all of
+// them before any LDS read it cannot prove independent) and waited for with an explicit count;
+// the activation loads are ordinary, and the compiler's waits for them, which do not count the
+// direct loads, keep about one super-block less in flight: PF = 4 leaves two ahead.
 
 #include "common.hpp"
 
@@ -34,75 +40,121 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef unsigned short us2 __attribute__((ext_vector_type(2)));
 
-struct SkArgs {
+constexpr int SK_PARTS = 4;
+constexpr uint32_t SK_SLOT = 3072; // 16 x 144 weight bytes, padded to three 1-KB loads
+
+struct SkPart {
     const uint8_t *w;
-    uint32_t rows, K, n;
-    const int8_t *aqs;  // k_qs [n][K]
-    const float *ad;    // k_d [n][K/256]
-    const uint8_t *amb; // k_mb [n][K/256] x 32 bytes
     float *y;
     const float *bias;
-    int mode;
+    uint32_t rows, tile0; // tile0: first row tile of the part in the launch
 };
 
-__device__ __forceinline__ uint4 ld16(const void *p) { return *reinterpret_cast<const uint4 *>(p); }
+struct SkArgs {
+    SkPart p[SK_PARTS];
+    uint32_t nparts, K, n, tiles; // tiles: 16-token tiles of the interleaved planes
+    const uint8_t *il;
+    const uint8_t *ilmb;
+    const float *ild;
+    int mode;
+};
 
 __device__ __forceinline__ uint32_t mul_bytes(uint32_t nib, uint32_t f2) {
     return __builtin_bit_cast(uint32_t, __builtin_bit_cast(us2, nib) * __builtin_bit_cast(us2, f2));
 }
 
-// One super-block's operands of this lane: its row's block header and the 16-byte pieces of
-// the four chunks, and per token tile the activations, the min-term words and the scale.
-template <int NTT> struct SkBuf {
-    uint4 hdr;
-    uint4 q[4];
-    uint4 a[NTT][4];
-    uint4 mb[NTT];
+// A direct global -> LDS load the compiler does not track (see the header): lane L writes 16
+// bytes at the wave-uniform LDS address + 16*L.
+__device__ __forceinline__ uint32_t lds_addr(const void *lds) {
+    return uint32_t((uintptr_t)(const __attribute__((address_space(3))) void *)lds);
+}
+__device__ __forceinline__ void dma16(const void *g, void *lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(lds_addr(lds)) : "memory", "m0");
+}
+__device__ __forceinline__ v4i ld16(const void *g) { return *reinterpret_cast<const v4i *>(g); }
+// s_waitcnt vmcnt(N), as assembly with a memory clobber so that no memory access (the LDS
+// reads of the slot just waited for, in particular) moves across it.
+template <int N> __device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+// The activation operands of one super-block, per token tile.
+template <int NTT> struct SkAct {
+    v4i a[NTT][4];
+    v4i mb[NTT];
     float da[NTT];
 };
 
 template <int NTT, int KS, int PF>
 __global__ __launch_bounds__(KS * 64) void mmsk_q4k_kernel(SkArgs a) {
+    constexpr int OPS = 3 + NTT * 6; // loads per super-block and wave
+    __shared__ __attribute__((aligned(16))) uint8_t ring[KS][PF][SK_SLOT];
+    __shared__ v4f part[KS > 1 ? KS - 1 : 1][NTT][64];
+
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t g = lane >> 4, p = lane & 15;
     const uint32_t nsb = a.K / 256;
-    const uint32_t r0 = blockIdx.x * 16;
-    // This wave's super-blocks.
+
+    // Part and row tile of this workgroup (uniform). Fields are copied member by member so the
+    // argument block is never indexed dynamically.
+    uint32_t pi = 0;
+#pragma unroll
+    for (int i = 1; i < SK_PARTS; i++)
+        if (i < int(a.nparts) && blockIdx.x >= a.p[i].tile0) pi = i;
+    const uint8_t *W = a.p[0].w;
+    float *Y = a.p[0].y;
+    const float *B = a.p[0].bias;
+    uint32_t rows = a.p[0].rows, tile0 = a.p[0].tile0;
+#pragma unroll
+    for (int i = 1; i < SK_PARTS; i++) {
+        if (pi == uint32_t(i)) {
+            W = a.p[i].w;
+            Y = a.p[i].y;
+            B = a.p[i].bias;
+            rows = a.p[i].rows;
+            tile0 = a.p[i].tile0;
+        }
+    }
+    const uint32_t r0 = (blockIdx.x - tile0) * 16;
     const uint32_t sb0 = nsb * wave / KS, sb1 = nsb * (wave + 1) / KS;
 
-    const uint32_t row = r0 + p < a.rows ? r0 + p : a.rows - 1;
-    const uint8_t *wrow = a.w + uint64_t(row) * nsb * 144;
-    uint32_t tokn[NTT]; // token (tile*16 + p), clamped to the last one
+    // Weight piece P = 64i + lane (16 bytes) of a super-block: byte 16*(P % 9) of row P / 9's
+    // block; pieces past the 144 repeat the last (they land in the slot's padding).
+    uint32_t woff[3];
 #pragma unroll
-    for (int tt = 0; tt < NTT; tt++) {
-        const uint32_t tok = 16 * tt + p < a.n ? 16 * tt + p : a.n - 1;
-        tokn[tt] = tok;
+    for (int i = 0; i < 3; i++) {
+        const uint32_t P = 64 * i + lane < 144 ? 64 * i + lane : 143;
+        const uint32_t row = r0 + P / 9 < rows ? r0 + P / 9 : rows - 1;
+        woff[i] = row * nsb * 144 + 16 * (P % 9);
     }
+    uint8_t (*const myring)[SK_SLOT] = ring[wave];
 
-    auto load = [&](SkBuf<NTT> &b, uint32_t sb) {
-        const uint8_t *blk = wrow + uint64_t(sb) * 144;
-        b.hdr = ld16(blk);
+    auto issue = [&](uint32_t sb, uint8_t *slot, SkAct<NTT> &x) {
+        const uint8_t *gw = W + uint64_t(sb) * 144;
 #pragma unroll
-        for (int c = 0; c < 4; c++) b.q[c] = ld16(blk + 16 + 32 * c + 16 * (g & 1));
+        for (int i = 0; i < 3; i++) dma16(gw + woff[i], slot + 1024 * i);
 #pragma unroll
         for (int tt = 0; tt < NTT; tt++) {
-            const int8_t *ta = a.aqs + uint64_t(tokn[tt]) * a.K + 256 * sb + 16 * g;
+            const uint8_t *ga = a.il + ((uint64_t(4 * sb) * a.tiles + tt) * 64 + lane) * 16;
 #pragma unroll
-            for (int c = 0; c < 4; c++) b.a[tt][c] = ld16(ta + 64 * c);
-            b.mb[tt] = ld16(a.amb + (uint64_t(tokn[tt]) * nsb + sb) * 32 + 16 * (g & 1));
-            b.da[tt] = a.ad[uint64_t(tokn[tt]) * nsb + sb];
+            for (int c = 0; c < 4; c++) x.a[tt][c] = ld16(ga + uint64_t(c) * a.tiles * 1024);
+            x.mb[tt] = ld16(a.ilmb + ((uint64_t(sb) * a.tiles + tt) * 2 + (g & 1)) * 256 + 16 * p);
+            x.da[tt] = a.ild[(uint64_t(sb) * a.tiles + tt) * 16 + p];
         }
-        // A buffer's loads stay together and in order behind the previous buffer's.
-        __builtin_amdgcn_sched_barrier(0);
     };
 
     v4f acc[NTT];
 #pragma unroll
     for (int tt = 0; tt < NTT; tt++) acc[tt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
-    auto compute = [&](const SkBuf<NTT> &b, float keep) {
-        const uint4 h = b.hdr;
+    auto compute = [&](const uint8_t *slot, const SkAct<NTT> &x, float keep) {
+        const uint8_t *blk = slot + 144 * p;
+        const uint4 h = *reinterpret_cast<const uint4 *>(blk);
+        uint4 q[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) q[c] = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * c + 16 * (g & 1));
         const uint32_t k1 = 0x3f3f3f3fu, k2 = 0x0f0f0f0fu, k3 = 0x03030303u;
         const uint32_t scl = h.y & k1, mnl = h.z & k1;
         const uint32_t sch = (h.w & k2) | (((h.y >> 6) & k3) << 4);
@@ -116,7 +168,7 @@ __global__ __launch_bounds__(KS * 64) void mmsk_q4k_kernel(SkArgs a) {
             const uint32_t sc = ((c < 2 ? scl : sch) >> (8 * (2 * (c & 1) + (g >> 1)))) & 0xFF;
             const uint32_t fh = (sc >> 3) * 0x00010001u, fl = (sc & 7) * 0x00010001u;
             const uint32_t sh = 4 * (g >> 1);
-            const uint32_t w4[4] = {b.q[c].x, b.q[c].y, b.q[c].z, b.q[c].w};
+            const uint32_t w4[4] = {q[c].x, q[c].y, q[c].z, q[c].w};
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const uint32_t nib = (w4[i] >> sh) & 0x0F0F0F0Fu;
@@ -125,18 +177,15 @@ __global__ __launch_bounds__(KS * 64) void mmsk_q4k_kernel(SkArgs a) {
             }
         }
         // Min-term A operand: the 8 mins as bf16 integers in lane groups 0 and 1, zero in 2, 3.
-        v8bf am;
-        {
-            uint32_t mw[4];
+        uint32_t mw[4];
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const uint32_t src = q < 2 ? mnl : mnh, s = 16 * (q & 1);
-                const float e = (float)((src >> s) & 0xFF), o = (float)((src >> (s + 8)) & 0xFF);
-                mw[q] = g < 2 ? (__builtin_bit_cast(uint32_t, e) >> 16) | (__builtin_bit_cast(uint32_t, o) & 0xFFFF0000u) : 0u;
-            }
-            am = __builtin_bit_cast(v8bf, make_uint4(mw[0], mw[1], mw[2], mw[3]));
+        for (int i = 0; i < 4; i++) {
+            const uint32_t src = i < 2 ? mnl : mnh, s = 16 * (i & 1);
+            const float e = (float)((src >> s) & 0xFF), o = (float)((src >> (s + 8)) & 0xFF);
+            mw[i] = g < 2 ? (__builtin_bit_cast(uint32_t, e) >> 16) | (__builtin_bit_cast(uint32_t, o) & 0xFFFF0000u) : 0u;
         }
-        // Scales of this lane's output rows 4*(lane/16) + i: from the lanes that loaded them.
+        const v8bf am = __builtin_bit_cast(v8bf, make_uint4(mw[0], mw[1], mw[2], mw[3]));
+        // Scales of this lane's output rows 4*(lane/16) + i, from the lanes that read them.
         float dr[4], mr[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -148,42 +197,40 @@ __global__ __launch_bounds__(KS * 64) void mmsk_q4k_kernel(SkArgs a) {
             v4i s = {0, 0, 0, 0};
 #pragma unroll
             for (int c = 0; c < 4; c++)
-                s = __builtin_amdgcn_mfma_i32_16x16x64_i8(ph[c], __builtin_bit_cast(v4i, b.a[tt][c]), s, 0, 0, 0);
+                s = __builtin_amdgcn_mfma_i32_16x16x64_i8(ph[c], x.a[tt][c], s, 0, 0, 0);
 #pragma unroll
             for (int i = 0; i < 4; i++) s[i] <<= 3;
 #pragma unroll
             for (int c = 0; c < 4; c++)
-                s = __builtin_amdgcn_mfma_i32_16x16x64_i8(pl[c], __builtin_bit_cast(v4i, b.a[tt][c]), s, 0, 0, 0);
-            const uint4 mbw = g < 2 ? b.mb[tt] : make_uint4(0, 0, 0, 0);
+                s = __builtin_amdgcn_mfma_i32_16x16x64_i8(pl[c], x.a[tt][c], s, 0, 0, 0);
+            const v4i mbw = g < 2 ? x.mb[tt] : v4i{0, 0, 0, 0};
             const v4f j = __builtin_amdgcn_mfma_f32_16x16x32_bf16(am, __builtin_bit_cast(v8bf, mbw), v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
 #pragma unroll
-            for (int i = 0; i < 4; i++) acc[tt][i] = fmaf(fmaf((float)s[i], dr[i], mr[i] * j[i]), b.da[tt] * keep, acc[tt][i]);
+            for (int i = 0; i < 4; i++) acc[tt][i] = fmaf(fmaf((float)s[i], dr[i], mr[i] * j[i]), x.da[tt] * keep, acc[tt][i]);
         }
     };
 
-    // PF super-blocks in flight. Every step issues the same loads and runs the same arithmetic
-    // (past the wave's range on repeats of its last super-block, scaled by zero): no branch in the
-    // loop, so the in-order memory counter covers exactly the buffer about to be used.
     if (sb0 < sb1) {
-        SkBuf<NTT> b[PF];
+        SkAct<NTT> x[PF];
         const uint32_t last = sb1 - 1;
+        // PF-1 super-blocks in flight ahead of the one computed. Every step issues the same loads
+        // (past the wave's range, repeats of its last super-block, multiplied by zero), so one
+        // wait count fits all.
 #pragma unroll
-        for (int i = 0; i < PF; i++) load(b[i], sb0 + i < last ? sb0 + i : last);
+        for (int i = 0; i < PF - 1; i++) issue(sb0 + i < last ? sb0 + i : last, myring[i], x[i]);
         for (uint32_t sb = sb0; sb <= last; sb += PF) {
 #pragma unroll
             for (int i = 0; i < PF; i++) {
-                compute(b[i], sb + i <= last ? 1.0f : 0.0f);
-                // Keep the refill behind the compute: hoisted above it, its loads would sit in the
-                // in-order memory counter ahead of the wait for this buffer.
-                __builtin_amdgcn_sched_barrier(0);
-                const uint32_t nx = sb + i + PF;
-                load(b[i], nx < last ? nx : last);
+                const uint32_t nx = sb + i + PF - 1;
+                issue(nx < last ? nx : last, myring[(i + PF - 1) % PF], x[(i + PF - 1) % PF]);
+                wait_vm<OPS * (PF - 1)>();
+                compute(myring[i], x[i], sb + i <= last ? 1.0f : 0.0f);
             }
         }
+        wait_vm<0>(); // nothing in flight past the loop
     }
 
     // Partial sums of the waves meet in LDS; wave 0 finishes the rows.
-    __shared__ v4f part[KS > 1 ? KS - 1 : 1][NTT][64];
     if (wave > 0) {
 #pragma unroll
         for (int tt = 0; tt < NTT; tt++) part[wave - 1][tt][lane] = acc[tt];
@@ -199,9 +246,9 @@ __global__ __launch_bounds__(KS * 64) void mmsk_q4k_kernel(SkArgs a) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const uint32_t r = r0 + 4 * g + i;
-                    if (r < a.rows) {
-                        float *dst = a.y + uint64_t(tok) * a.rows + r;
-                        const float v = acc[tt][i] + (a.bias ? a.bias[r] : 0.0f);
+                    if (r < rows) {
+                        float *dst = Y + uint64_t(tok) * rows + r;
+                        const float v = acc[tt][i] + (B ? B[r] : 0.0f);
                         if (a.mode == HKHIP_ACCUMULATE)
                             *dst += v;
                         else
@@ -213,41 +260,58 @@ __global__ __launch_bounds__(KS * 64) void mmsk_q4k_kernel(SkArgs a) {
     }
 }
 
+typedef void (*sk_kernel_t)(SkArgs);
+
+template <int NTT, int PF> sk_kernel_t sk_pick(uint32_t ks) {
+    return ks == 1 ? mmsk_q4k_kernel<NTT, 1, PF>
+         : ks == 2 ? mmsk_q4k_kernel<NTT, 2, PF>
+         : ks == 4 ? mmsk_q4k_kernel<NTT, 4, PF>
+                   : mmsk_q4k_kernel<NTT, 8, PF>;
+}
+
 } // namespace
 
 bool mmsk_supports(int t, uint32_t rows, uint32_t cols, uint32_t n) {
-    return t == HKHIP_Q4_K && cols % 256 == 0 && rows > 0 && n >= 1 && n <= 32;
+    return t == HKHIP_Q4_K && cols % 256 == 0 && rows > 0 && n >= 1 && n <= SK_MAX_TOKENS &&
+           uint64_t(rows) * (cols / 256) * 144 < (1ull << 32);
+}
+
+hipError_t launch_mmsk_parts(int t, const MvPartDesc *parts, int nparts, uint32_t cols, const uint8_t *xq,
+                             uint32_t n, int mode, hipStream_t s) {
+    if (nparts < 1 || nparts > SK_PARTS) return hipErrorInvalidValue;
+    for (int i = 0; i < nparts; i++)
+        if (!mmsk_supports(t, parts[i].rows, cols, n)) return hipErrorInvalidValue;
+    const ActLayout A = act_layout(n, cols);
+    if (A.tiles == 0) return hipErrorInvalidValue;
+    SkArgs a{};
+    uint32_t tiles = 0;
+    for (int i = 0; i < nparts; i++) {
+        a.p[i] = SkPart{parts[i].w, parts[i].y, parts[i].bias, parts[i].rows, tiles};
+        tiles += (parts[i].rows + 15) / 16;
+    }
+    for (int i = nparts; i < SK_PARTS; i++) a.p[i].tile0 = 0xffffffffu;
+    a.nparts = uint32_t(nparts);
+    a.K = cols;
+    a.n = n;
+    a.tiles = A.tiles;
+    a.il = xq + A.k_il;
+    a.ilmb = xq + A.k_ilmb;
+    a.ild = reinterpret_cast<const float *>(xq + A.k_ild);
+    a.mode = mode;
+    // K slices: enough waves for ~2048 in the launch, each with at least 4 super-blocks when
+    // the matrix has them.
+    const uint32_t nsb = cols / 256;
+    uint32_t ks = 1;
+    while (ks < 8 && tiles * ks * 2 <= 2048 && nsb / (2 * ks) >= 4) ks *= 2;
+    const sk_kernel_t k = A.tiles == 1 ? sk_pick<1, 4>(ks) : sk_pick<2, 3>(ks);
+    hipLaunchKernelGGL(k, dim3(tiles), dim3(ks * 64), 0, s, a);
+    return hipGetLastError();
 }
 
 hipError_t launch_mmsk(int t, const uint8_t *w, uint32_t rows, uint32_t cols, const uint8_t *xq, uint32_t n,
                        float *y, const float *bias, int mode, hipStream_t s) {
-    if (!mmsk_supports(t, rows, cols, n)) return hipErrorInvalidValue;
-    const ActLayout A = act_layout(n, cols);
-    SkArgs a{};
-    a.w = w;
-    a.rows = rows;
-    a.K = cols;
-    a.n = n;
-    a.aqs = reinterpret_cast<const int8_t *>(xq + A.k_qs);
-    a.ad = reinterpret_cast<const float *>(xq + A.k_d);
-    a.amb = xq + A.k_mb;
-    a.y = y;
-    a.bias = bias;
-    a.mode = mode;
-    // K slices: enough waves for ~2048 in the launch, each with at least 4 super-blocks when
-    // the matrix has them.
-    const uint32_t tiles = (rows + 15) / 16, nsb = cols / 256;
-    uint32_t ks = 1;
-    while (ks < 8 && tiles * ks * 2 <= 2048 && nsb / (2 * ks) >= 4) ks *= 2;
-    const dim3 grid(tiles);
-    typedef void (*sk_kernel_t)(SkArgs);
-    sk_kernel_t k;
-    if (n <= 16)
-        k = ks == 1 ? mmsk_q4k_kernel<1, 1, 4> : ks == 2 ? mmsk_q4k_kernel<1, 2, 4> : ks == 4 ? mmsk_q4k_kernel<1, 4, 4> : mmsk_q4k_kernel<1, 8, 4>;
-    else
-        k = ks == 1 ? mmsk_q4k_kernel<2, 1, 2> : ks == 2 ? mmsk_q4k_kernel<2, 2, 2> : ks == 4 ? mmsk_q4k_kernel<2, 4, 2> : mmsk_q4k_kernel<2, 8, 2>;
-    hipLaunchKernelGGL(k, grid, dim3(ks * 64), 0, s, a);
-    return hipGetLastError();
+    const MvPartDesc p{w, y, bias, rows};
+    return launch_mmsk_parts(t, &p, 1, cols, xq, n, mode, s);
 }
 
 } // namespace hkhip

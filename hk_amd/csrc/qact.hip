@@ -25,8 +25,18 @@ __device__ __forceinline__ uint32_t bf16_bits_rne(float x) {
     return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
 }
 
+// Token-interleaved copies for the small-batch kernel (tiles > 0; layout in common.hpp): token
+// t's entries, and for the last token also those of the padding tokens of its tile.
+struct QactIl {
+    uint8_t *qs;
+    uint16_t *mb;
+    float *d;
+    uint32_t tiles, n, nsb;
+};
+
 __global__ void qact_q8k_kernel(const float *__restrict__ x, uint64_t nblocks, int8_t *__restrict__ qs,
-                                float *__restrict__ dout, int16_t *__restrict__ bsout, uint16_t *__restrict__ mbout) {
+                                float *__restrict__ dout, int16_t *__restrict__ bsout, uint16_t *__restrict__ mbout,
+                                QactIl il) {
     const uint32_t lane = threadIdx.x & 63;
     const uint64_t b = (uint64_t(blockIdx.x) * blockDim.x + threadIdx.x) / 64;
     if (b >= nblocks) return; // whole waves exit together
@@ -38,10 +48,27 @@ __global__ void qact_q8k_kernel(const float *__restrict__ x, uint64_t nblocks, i
     // (v in [0, 63], u in [-64, 63]), as the exact bf16 integers 64*u and v. The 16-value sums
     // sit in lanes 4g; sub-block s = groups 2s and 2s+1 (lanes 8s and 8s+4).
     const int b32 = r.bsum + __shfl_down(r.bsum, 4);
+    const int bv = b32 & 63;
+    const uint16_t mu = uint16_t(bf16_bits_rne((float)(b32 - bv))), mv = uint16_t(bf16_bits_rne((float)bv));
     if ((lane & 7) == 0) {
-        const int v = b32 & 63;
-        mbout[b * 16 + lane / 8] = uint16_t(bf16_bits_rne((float)(b32 - v)));
-        mbout[b * 16 + 8 + lane / 8] = uint16_t(bf16_bits_rne((float)v));
+        mbout[b * 16 + lane / 8] = mu;
+        mbout[b * 16 + 8 + lane / 8] = mv;
+    }
+    if (il.tiles) {
+        const uint32_t t = uint32_t(b / il.nsb), sb = uint32_t(b % il.nsb);
+        const uint32_t tile = t / 16, p0 = t % 16;
+        const uint32_t p1 = t + 1 == il.n ? 16 : p0 + 1; // the last token also fills its tile's padding
+        const uint32_t c64 = 4 * sb + lane / 16, g = (lane % 16) / 4;
+        for (uint32_t p = p0; p < p1; p++) {
+            uint8_t *e = il.qs + ((uint64_t(c64) * il.tiles + tile) * 64 + 16 * g + p) * 16 + 4 * (lane % 4);
+            *reinterpret_cast<uint32_t *>(e) = r.packed;
+            const uint64_t mbase = (uint64_t(sb) * il.tiles + tile) * 256; // in uint16: 2 halves x 16 x 8
+            if ((lane & 7) == 0) {
+                il.mb[mbase + p * 8 + lane / 8] = mu;
+                il.mb[mbase + 128 + p * 8 + lane / 8] = mv;
+            }
+            if (lane == 0) il.d[(uint64_t(sb) * il.tiles + tile) * 16 + p] = r.d;
+        }
     }
 }
 
@@ -60,7 +87,10 @@ hipError_t launch_qact(const float *x, uint32_t n, uint32_t k, int kind, uint8_t
         qact_q8k_kernel<<<uint32_t(grid), 256, 0, s>>>(x, nb, reinterpret_cast<int8_t *>(xq + L.k_qs),
                                                        reinterpret_cast<float *>(xq + L.k_d),
                                                        reinterpret_cast<int16_t *>(xq + L.k_bs),
-                                                       reinterpret_cast<uint16_t *>(xq + L.k_mb));
+                                                       reinterpret_cast<uint16_t *>(xq + L.k_mb),
+                                                       QactIl{xq + L.k_il, reinterpret_cast<uint16_t *>(xq + L.k_ilmb),
+                                                              reinterpret_cast<float *>(xq + L.k_ild), L.tiles, n,
+                                                              k / QK_K});
     }
     return hipGetLastError();
 }
