@@ -33,7 +33,8 @@
 
 namespace hkhip {
 
-namespace {
+// Helpers and the kernel live in a named namespace so that profiles show the kernel's name.
+namespace sk {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
@@ -41,7 +42,9 @@ typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef unsigned short us2 __attribute__((ext_vector_type(2)));
 
 constexpr int SK_PARTS = 4;
-constexpr uint32_t SK_SLOT = 3072; // 16 x 144 weight bytes, padded to three 1-KB loads
+// Weight bytes of a super-block for RT row tiles of 16 (144 bytes a row), padded to whole 1-KB
+// direct loads.
+template <int RT> constexpr uint32_t sk_dma() { return (144 * 16 * RT + 1023) / 1024; }
 
 struct SkPart {
     const uint8_t *w;
@@ -86,11 +89,12 @@ template <int NTT> struct SkAct {
     float da[NTT];
 };
 
-template <int NTT, int KS, int PF>
+template <int NTT, int KS, int PF, int RT>
 __global__ __launch_bounds__(KS * 64) void mmsk_q4k_kernel(SkArgs a) {
-    constexpr int OPS = 3 + NTT * 6; // loads per super-block and wave
-    __shared__ __attribute__((aligned(16))) uint8_t ring[KS][PF][SK_SLOT];
-    __shared__ v4f part[KS > 1 ? KS - 1 : 1][NTT][64];
+    constexpr uint32_t NDMA = sk_dma<RT>(), SLOT = 1024 * NDMA;
+    constexpr int OPS = NDMA + NTT * 6; // loads per super-block and wave
+    __shared__ __attribute__((aligned(16))) uint8_t ring[KS][PF][SLOT];
+    __shared__ v4f part[KS > 1 ? KS - 1 : 1][RT][NTT][64];
 
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -117,40 +121,50 @@ __global__ __launch_bounds__(KS * 64) void mmsk_q4k_kernel(SkArgs a) {
             tile0 = a.p[i].tile0;
         }
     }
-    const uint32_t r0 = (blockIdx.x - tile0) * 16;
+    const uint32_t r0 = (blockIdx.x - tile0) * 16 * RT;
     const uint32_t sb0 = nsb * wave / KS, sb1 = nsb * (wave + 1) / KS;
 
     // Weight piece P = 64i + lane (16 bytes) of a super-block: byte 16*(P % 9) of row P / 9's
-    // block; pieces past the 144 repeat the last (they land in the slot's padding).
-    uint32_t woff[3];
+    // block; pieces past the last repeat it (they land in the slot's padding).
+    constexpr uint32_t NP = 144 * RT;
+    uint32_t woff[NDMA];
 #pragma unroll
-    for (int i = 0; i < 3; i++) {
-        const uint32_t P = 64 * i + lane < 144 ? 64 * i + lane : 143;
+    for (uint32_t i = 0; i < NDMA; i++) {
+        const uint32_t P = 64 * i + lane < NP ? 64 * i + lane : NP - 1;
         const uint32_t row = r0 + P / 9 < rows ? r0 + P / 9 : rows - 1;
         woff[i] = row * nsb * 144 + 16 * (P % 9);
     }
-    uint8_t (*const myring)[SK_SLOT] = ring[wave];
+    uint8_t (*const myring)[SLOT] = ring[wave];
 
+    // Lanes of tokens past n read the last token's entries: the same addresses as its own lanes,
+    // so a load brings in only the real tokens' bytes.
+    uint32_t tp[NTT];
+#pragma unroll
+    for (int tt = 0; tt < NTT; tt++) tp[tt] = 16 * tt + p < a.n ? p : a.n - 1 - 16 * tt;
     auto issue = [&](uint32_t sb, uint8_t *slot, SkAct<NTT> &x) {
         const uint8_t *gw = W + uint64_t(sb) * 144;
 #pragma unroll
-        for (int i = 0; i < 3; i++) dma16(gw + woff[i], slot + 1024 * i);
+        for (uint32_t i = 0; i < NDMA; i++) dma16(gw + woff[i], slot + 1024 * i);
 #pragma unroll
         for (int tt = 0; tt < NTT; tt++) {
-            const uint8_t *ga = a.il + ((uint64_t(4 * sb) * a.tiles + tt) * 64 + lane) * 16;
+            const uint8_t *ga = a.il + ((uint64_t(4 * sb) * a.tiles + tt) * 64 + 16 * g + tp[tt]) * 16;
 #pragma unroll
             for (int c = 0; c < 4; c++) x.a[tt][c] = ld16(ga + uint64_t(c) * a.tiles * 1024);
-            x.mb[tt] = ld16(a.ilmb + ((uint64_t(sb) * a.tiles + tt) * 2 + (g & 1)) * 256 + 16 * p);
-            x.da[tt] = a.ild[(uint64_t(sb) * a.tiles + tt) * 16 + p];
+            x.mb[tt] = ld16(a.ilmb + ((uint64_t(sb) * a.tiles + tt) * 2 + (g & 1)) * 256 + 16 * tp[tt]);
+            x.da[tt] = a.ild[(uint64_t(sb) * a.tiles + tt) * 16 + tp[tt]];
         }
     };
 
-    v4f acc[NTT];
+    v4f acc[RT][NTT];
 #pragma unroll
-    for (int tt = 0; tt < NTT; tt++) acc[tt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (int tt = 0; tt < NTT; tt++) acc[rt][tt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
     auto compute = [&](const uint8_t *slot, const SkAct<NTT> &x, float keep) {
-        const uint8_t *blk = slot + 144 * p;
+#pragma unroll
+      for (int rt = 0; rt < RT; rt++) {
+        const uint8_t *blk = slot + 144 * (16 * rt + p);
         const uint4 h = *reinterpret_cast<const uint4 *>(blk);
         uint4 q[4];
 #pragma unroll
@@ -206,8 +220,9 @@ __global__ __launch_bounds__(KS * 64) void mmsk_q4k_kernel(SkArgs a) {
             const v4i mbw = g < 2 ? x.mb[tt] : v4i{0, 0, 0, 0};
             const v4f j = __builtin_amdgcn_mfma_f32_16x16x32_bf16(am, __builtin_bit_cast(v8bf, mbw), v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
 #pragma unroll
-            for (int i = 0; i < 4; i++) acc[tt][i] = fmaf(fmaf((float)s[i], dr[i], mr[i] * j[i]), x.da[tt] * keep, acc[tt][i]);
+            for (int i = 0; i < 4; i++) acc[rt][tt][i] = fmaf(fmaf((float)s[i], dr[i], mr[i] * j[i]), x.da[tt] * keep, acc[rt][tt][i]);
         }
+      }
     };
 
     if (sb0 < sb1) {
@@ -233,26 +248,31 @@ __global__ __launch_bounds__(KS * 64) void mmsk_q4k_kernel(SkArgs a) {
     // Partial sums of the waves meet in LDS; wave 0 finishes the rows.
     if (wave > 0) {
 #pragma unroll
-        for (int tt = 0; tt < NTT; tt++) part[wave - 1][tt][lane] = acc[tt];
+        for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+            for (int tt = 0; tt < NTT; tt++) part[wave - 1][rt][tt][lane] = acc[rt][tt];
     }
     if (KS > 1) __syncthreads();
     if (wave == 0) {
 #pragma unroll
-        for (int tt = 0; tt < NTT; tt++) {
+        for (int rt = 0; rt < RT; rt++) {
 #pragma unroll
-            for (int w = 0; w < KS - 1; w++) acc[tt] += part[w][tt][lane];
-            const uint32_t tok = 16 * tt + p;
-            if (tok < a.n) {
+            for (int tt = 0; tt < NTT; tt++) {
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const uint32_t r = r0 + 4 * g + i;
-                    if (r < rows) {
-                        float *dst = Y + uint64_t(tok) * rows + r;
-                        const float v = acc[tt][i] + (B ? B[r] : 0.0f);
-                        if (a.mode == HKHIP_ACCUMULATE)
-                            *dst += v;
-                        else
-                            *dst = v;
+                for (int w = 0; w < KS - 1; w++) acc[rt][tt] += part[w][rt][tt][lane];
+                const uint32_t tok = 16 * tt + p;
+                if (tok < a.n) {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const uint32_t r = r0 + 16 * rt + 4 * g + i;
+                        if (r < rows) {
+                            float *dst = Y + uint64_t(tok) * rows + r;
+                            const float v = acc[rt][tt][i] + (B ? B[r] : 0.0f);
+                            if (a.mode == HKHIP_ACCUMULATE)
+                                *dst += v;
+                            else
+                                *dst = v;
+                        }
                     }
                 }
             }
@@ -262,14 +282,23 @@ __global__ __launch_bounds__(KS * 64) void mmsk_q4k_kernel(SkArgs a) {
 
 typedef void (*sk_kernel_t)(SkArgs);
 
-template <int NTT, int PF> sk_kernel_t sk_pick(uint32_t ks) {
-    return ks == 1 ? mmsk_q4k_kernel<NTT, 1, PF>
-         : ks == 2 ? mmsk_q4k_kernel<NTT, 2, PF>
-         : ks == 4 ? mmsk_q4k_kernel<NTT, 4, PF>
-                   : mmsk_q4k_kernel<NTT, 8, PF>;
+// At most 4 waves with two row tiles each (the LDS ring of 8 would not fit).
+template <int RT> constexpr uint32_t sk_max_ks() { return RT > 1 ? 4 : 8; }
+template <int NTT, int PF, int RT> sk_kernel_t sk_pick(uint32_t ks) {
+    if constexpr (sk_max_ks<RT>() >= 8)
+        if (ks == 8) return mmsk_q4k_kernel<NTT, 8, PF, RT>;
+    return ks == 1 ? mmsk_q4k_kernel<NTT, 1, PF, RT>
+         : ks == 2 ? mmsk_q4k_kernel<NTT, 2, PF, RT>
+                   : mmsk_q4k_kernel<NTT, 4, PF, RT>;
 }
 
-} // namespace
+} // namespace sk
+
+using sk::SkArgs;
+using sk::SkPart;
+using sk::sk_kernel_t;
+using sk::sk_pick;
+using sk::SK_PARTS;
 
 bool mmsk_supports(int t, uint32_t rows, uint32_t cols, uint32_t n) {
     return t == HKHIP_Q4_K && cols % 256 == 0 && rows > 0 && n >= 1 && n <= SK_MAX_TOKENS &&
@@ -283,11 +312,14 @@ hipError_t launch_mmsk_parts(int t, const MvPartDesc *parts, int nparts, uint32_
         if (!mmsk_supports(t, parts[i].rows, cols, n)) return hipErrorInvalidValue;
     const ActLayout A = act_layout(n, cols);
     if (A.tiles == 0) return hipErrorInvalidValue;
+    // Row tiles of 16 per wave: 1 (two share the activation loads, but need 320 VGPRs and
+    // measured slower).
+    constexpr uint32_t RT = 1;
     SkArgs a{};
     uint32_t tiles = 0;
     for (int i = 0; i < nparts; i++) {
         a.p[i] = SkPart{parts[i].w, parts[i].y, parts[i].bias, parts[i].rows, tiles};
-        tiles += (parts[i].rows + 15) / 16;
+        tiles += (parts[i].rows + 16 * RT - 1) / (16 * RT);
     }
     for (int i = nparts; i < SK_PARTS; i++) a.p[i].tile0 = 0xffffffffu;
     a.nparts = uint32_t(nparts);
@@ -302,8 +334,8 @@ hipError_t launch_mmsk_parts(int t, const MvPartDesc *parts, int nparts, uint32_
     // the matrix has them.
     const uint32_t nsb = cols / 256;
     uint32_t ks = 1;
-    while (ks < 8 && tiles * ks * 2 <= 2048 && nsb / (2 * ks) >= 4) ks *= 2;
-    const sk_kernel_t k = A.tiles == 1 ? sk_pick<1, 4>(ks) : sk_pick<2, 3>(ks);
+    while (ks < sk_max_ks<RT>() && tiles * ks * 2 <= 2048 && nsb / (2 * ks) >= 4) ks *= 2;
+    const sk_kernel_t k = A.tiles == 1 ? sk_pick<1, 4, RT>(ks) : sk_pick<2, 3, RT>(ks);
     hipLaunchKernelGGL(k, dim3(tiles), dim3(ks * 64), 0, s, a);
     return hipGetLastError();
 }

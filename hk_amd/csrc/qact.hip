@@ -55,7 +55,8 @@ __global__ void qact_q8k_kernel(const float *__restrict__ x, uint64_t nblocks, i
         mbout[b * 16 + 8 + lane / 8] = mv;
     }
     if (il.tiles) {
-        const uint32_t t = uint32_t(b / il.nsb), sb = uint32_t(b % il.nsb);
+        const uint32_t b32i = uint32_t(b); // tokens <= SK_MAX_TOKENS: a small index
+        const uint32_t t = b32i / il.nsb, sb = b32i - t * il.nsb;
         const uint32_t tile = t / 16, p0 = t % 16;
         const uint32_t p1 = t + 1 == il.n ? 16 : p0 + 1; // the last token also fills its tile's padding
         const uint32_t c64 = 4 * sb + lane / 16, g = (lane % 16) / 4;
