@@ -298,6 +298,7 @@ using sk::SkArgs;
 using sk::SkPart;
 using sk::sk_kernel_t;
 using sk::sk_pick;
+using sk::sk_max_ks;
 using sk::SK_PARTS;
 
 bool mmsk_supports(int t, uint32_t rows, uint32_t cols, uint32_t n) {
