@@ -19,7 +19,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libhkhip.so")
 BUILD_DIR = os.path.join(HERE, "_build")
-SOURCES = ["engine.hip", "weights.hip", "qact.hip", "mmvq.hip", "mm.hip", "mm2.hip", "mmsk.hip"]
+SOURCES = ["engine.hip", "weights.hip", "qact.hip", "mmvq.hip", "mm.hip", "mm2.hip", "mmsk.hip", "mmx.hip"]
 ARCH = "gfx950"
 
 

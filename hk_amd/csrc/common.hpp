@@ -143,6 +143,20 @@ __device__ __forceinline__ uint32_t iq4nl_lookup4(uint32_t idx) {
     return (hi & m) | (lo & ~m);
 }
 
+// 16 (4) bytes per lane global -> LDS: lane L writes at the wave-uniform LDS address + 16*L
+// (4*L). Issued as inline assembly: the compiler then keeps no books on these loads (the kernels
+// wait for them with explicit counts), where for the builtin it would wait for all of them before
+// an LDS read it cannot prove independent -- which drains the prefetch ring every step.
+__device__ __forceinline__ uint32_t lds_addr(const void *lds) {
+    return uint32_t((uintptr_t)(const __attribute__((address_space(3))) void *)lds);
+}
+__device__ __forceinline__ void load_lds16(const void *g, void *lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(lds_addr(lds)) : "memory", "m0");
+}
+__device__ __forceinline__ void load_lds4(const void *g, void *lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" : : "v"(g), "s"(lds_addr(lds)) : "memory", "m0");
+}
+
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
@@ -172,6 +186,10 @@ hipError_t launch_mmsk(int t, const uint8_t *w, uint32_t rows, uint32_t cols, co
                        float *y, const float *bias, int mode, hipStream_t s);
 hipError_t launch_mmsk_parts(int t, const MvPartDesc *parts, int nparts, uint32_t cols, const uint8_t *xq,
                              uint32_t n, int mode, hipStream_t s);
+// Prefill GEMM for Q6_K, Q8_0 and IQ4_NL (cols a multiple of 256).
+bool mmx_supports(int t, uint32_t rows, uint32_t cols, uint32_t n);
+hipError_t launch_mmx(int t, const uint8_t *w, uint32_t rows, uint32_t cols, const uint8_t *xq, uint32_t n, float *y,
+                      const float *bias, int mode, hipStream_t s);
 hipError_t launch_mm2(int t, const uint8_t *w, uint32_t rows, uint32_t cols, const uint8_t *xq, uint32_t n, float *y,
                       const float *bias, int mode, hipStream_t s);
 hipError_t launch_mm(int t, const uint8_t *w, uint32_t rows, uint32_t cols, const uint8_t *xq, uint32_t n,

@@ -80,20 +80,6 @@ struct Mm2Args {
 
 __device__ __forceinline__ uint4 ldg16(const void *p) { return *reinterpret_cast<const uint4 *>(p); }
 
-// 16 (4) bytes per lane global -> LDS: lane L writes at the wave-uniform LDS address + 16*L
-// (4*L). Issued as inline assembly: the compiler then keeps no books on these loads (the kernels
-// wait for them with explicit counts), where for the builtin it would wait for all of them before
-// an LDS read it cannot prove independent -- which drains the prefetch ring every step.
-__device__ __forceinline__ uint32_t lds_addr(const void *lds) {
-    return uint32_t((uintptr_t)(const __attribute__((address_space(3))) void *)lds);
-}
-__device__ __forceinline__ void load_lds16(const void *g, void *lds) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(lds_addr(lds)) : "memory", "m0");
-}
-__device__ __forceinline__ void load_lds4(const void *g, void *lds) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" : : "v"(g), "s"(lds_addr(lds)) : "memory", "m0");
-}
-
 // fp32 -> bf16 bits, round to nearest even (finite inputs).
 __device__ __forceinline__ uint32_t bf16_rne(float x) {
     const uint32_t u = __builtin_bit_cast(uint32_t, x);

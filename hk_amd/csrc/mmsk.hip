@@ -66,14 +66,6 @@ __device__ __forceinline__ uint32_t mul_bytes(uint32_t nib, uint32_t f2) {
     return __builtin_bit_cast(uint32_t, __builtin_bit_cast(us2, nib) * __builtin_bit_cast(us2, f2));
 }
 
-// A direct global -> LDS load the compiler does not track (see the header): lane L writes 16
-// bytes at the wave-uniform LDS address + 16*L.
-__device__ __forceinline__ uint32_t lds_addr(const void *lds) {
-    return uint32_t((uintptr_t)(const __attribute__((address_space(3))) void *)lds);
-}
-__device__ __forceinline__ void dma16(const void *g, void *lds) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(lds_addr(lds)) : "memory", "m0");
-}
 __device__ __forceinline__ v4i ld16(const void *g) { return *reinterpret_cast<const v4i *>(g); }
 // s_waitcnt vmcnt(N), as assembly with a memory clobber so that no memory access (the LDS
 // reads of the slot just waited for, in particular) moves across it.
@@ -144,7 +136,7 @@ __global__ __launch_bounds__(KS * 64) void mmsk_q4k_kernel(SkArgs a) {
     auto issue = [&](uint32_t sb, uint8_t *slot, SkAct<NTT> &x) {
         const uint8_t *gw = W + uint64_t(sb) * 144;
 #pragma unroll
-        for (uint32_t i = 0; i < NDMA; i++) dma16(gw + woff[i], slot + 1024 * i);
+        for (uint32_t i = 0; i < NDMA; i++) load_lds16(gw + woff[i], slot + 1024 * i);
 #pragma unroll
         for (int tt = 0; tt < NTT; tt++) {
             const uint8_t *ga = a.il + ((uint64_t(4 * sb) * a.tiles + tt) * 64 + 16 * g + tp[tt]) * 16;

@@ -1,0 +1,419 @@
+// Prefill GEMM for Q6_K, Q8_0 and IQ4_NL on the int8 MFMA units (K a multiple of 256).
+//
+// Integer arithmetic as in hk's CPU kernels (src/quant/gemm.zig kernelK 180-236 for Q6_K,
+// kernelLegacy 131-176 for the 32-weight blocks):
+//  * Q6_K: per row r, token t and super-block b, y += d[r,b]*da[t,b] * I with the exact integer
+//    I = sum_g sc[r,b,g] * sum_{k in g} (q[r,k] - 32) * a[t,k] over the 16 groups of 16. The
+//    signed 8-bit group scale is folded into the weights as three int8 planes: sc = 64*e2 +
+//    8*e1 + e0 with digits in [-3, 4], so every plane value (q - 32)*e lies in [-128, 124].
+//    Each MFMA lane holds 16 weights of one group, so a lane's plane bytes share one digit. One
+//    int32 chain per tile gives ((P2 << 3) + P1 << 3) + P0 = I, the reference's integer.
+//  * Q8_0 / IQ4_NL: y += (dw[r,c]*da[t,c]) * I_c per 32-weight block c (I_c exact). One
+//    32x32x32 int8 MFMA yields the tile's I_c; then per output one multiply (dw*da), one
+//    convert and one fma.
+// Only the f32 summation order differs from the reference.
+//
+// Structure (as the Q4_K ring kernel): a workgroup of NW waves owns 32*NW rows x 32*TT tokens;
+// every operand of a super-block (256 weights) goes global -> LDS by direct loads into a ring of
+// NB slots, NB-1 super-blocks ahead of the compute; each lane builds its row's MFMA operands
+// from LDS. MFMA roles: A = activations (tokens as M), B = weights (rows as N); output lane l
+// holds row l%32 and tokens 8*(v/4) + 4*(l/32) + v%4.
+
+#include "common.hpp"
+
+#include <type_traits>
+
+namespace hkhip {
+namespace mx {
+
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+
+// Per-format geometry of one super-block step (256 weights of 32 rows = one wave's share).
+template <int T> struct Fmt;
+template <> struct Fmt<HKHIP_Q6_K> {
+    static constexpr uint32_t RB = 208;  // quant-plane bytes per row and step
+    static constexpr uint32_t W16 = 6;   // 1-KB direct loads per wave
+    static constexpr uint32_t W4 = 2;    // 256-B direct loads (the rest)
+    static constexpr uint32_t WSB = 256; // scale bytes per wave (one dword per lane)
+    static constexpr uint32_t DAB = 4;   // activation-scale bytes per token and step
+};
+template <> struct Fmt<HKHIP_Q8_0> {
+    static constexpr uint32_t RB = 256, W16 = 8, W4 = 0, WSB = 1024, DAB = 32;
+};
+template <> struct Fmt<HKHIP_IQ4_NL> {
+    static constexpr uint32_t RB = 128, W16 = 4, W4 = 0, WSB = 1024, DAB = 32;
+};
+
+template <int T, int TOK, int NW> struct MxSlot {
+    int8_t a[TOK * 256];                     // chunk c of token t at c ^ (t & 15)
+    uint8_t w[NW][32 * Fmt<T>::RB];          // per wave, its 32 rows' bytes of the step
+    uint8_t ws[NW][Fmt<T>::WSB];             // per wave, the rows' f16 scales of the step
+    // Activation scales: Q6_K per token (wave m fills tokens 64m..64m+63); A8 per block and token,
+    // block-major ([8][TOK]), so that four consecutive tokens' scales are one 16-byte read.
+    float da[T == HKHIP_Q6_K ? 64 * NW : 8 * TOK];
+};
+
+struct MxArgs {
+    const uint8_t *w;
+    const uint8_t *ws; // f16 scale plane
+    uint32_t rows, cols, n;
+    const int8_t *aqs;
+    const float *ad;
+    float *y;
+    const float *bias;
+    int mode;
+    uint32_t rblocks, tblocks;
+};
+
+// Bytes q (each in [0, 63]) times a digit e in [-3, 4], minus 32*e: per byte (q - 32)*e as a
+// two's-complement byte. Even and odd bytes go through packed 16-bit multiply-adds (the low
+// byte of each 16-bit product is the wanted byte) and are interleaved back by a byte permute.
+__device__ __forceinline__ uint32_t plane4(uint32_t ev, uint32_t od, uint32_t m, uint32_t c) {
+    const us2 pe = __builtin_bit_cast(us2, ev) * __builtin_bit_cast(us2, m) + __builtin_bit_cast(us2, c);
+    const us2 po = __builtin_bit_cast(us2, od) * __builtin_bit_cast(us2, m) + __builtin_bit_cast(us2, c);
+    return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, po), __builtin_bit_cast(uint32_t, pe), 0x06020400u);
+}
+
+// sc = 64*e2 + 8*e1 + e0, digits in [-3, 4] (e2 in [-2, 2] for sc in [-128, 127]).
+__device__ __forceinline__ void digits(int sc, int e[3]) {
+    e[0] = ((sc + 3) & 7) - 3;
+    const int r = (sc - e[0]) >> 3;
+    e[1] = ((r + 3) & 7) - 3;
+    e[2] = (r - e[1]) >> 3;
+}
+
+__device__ __forceinline__ uint32_t lo16x2(int v) { return (uint32_t(v) & 0xFFFFu) * 0x00010001u; }
+
+template <int T, int NW, int TT, int NB>
+__global__ __launch_bounds__(NW * 64, 1) void mmx_kernel(MxArgs a) {
+    constexpr int TOK = 32 * TT;
+    using F = Fmt<T>;
+    using Slot = MxSlot<T, TOK, NW>;
+    constexpr bool q6 = (T == HKHIP_Q6_K);
+    static_assert(NB == 2 || NB == 3, "ring depth");
+    static_assert(q6 ? TOK <= 64 * NW : (8 * TOK) % (64 * NW) == 0, "token scales per wave");
+    __shared__ __attribute__((aligned(16))) Slot ring0;
+    __shared__ __attribute__((aligned(16))) Slot ring1;
+    __shared__ __attribute__((aligned(16))) Slot ring2;
+    auto slot_at = [&](auto ic) -> Slot & {
+        constexpr int i = decltype(ic)::value;
+        if constexpr (i == 0)
+            return ring0;
+        else if constexpr (i == 1)
+            return ring1;
+        else
+            return ring2;
+    };
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t h = lane >> 5, j = lane & 31;
+    const uint32_t K = a.cols, nsb = K / 256;
+
+    // Workgroup -> (row block, token block); the token blocks of a row block run on one XCD so
+    // its L2 serves the repeated weight reads (workgroups go round-robin over the 8 XCDs).
+    uint32_t rb, tb;
+    {
+        const uint32_t i = blockIdx.x;
+        if (a.rblocks % 8 == 0) {
+            const uint32_t xcd = i % 8, k = i / 8;
+            rb = xcd * (a.rblocks / 8) + k / a.tblocks;
+            tb = k % a.tblocks;
+        } else {
+            rb = i / a.tblocks;
+            tb = i % a.tblocks;
+        }
+    }
+    const uint32_t r0 = rb * 32 * NW, t0 = tb * TOK;
+    const uint32_t myrow = r0 + 32 * wave + j;
+    auto clamp_row = [&](uint32_t r) { return r < a.rows ? r : a.rows - 1; };
+    auto clamp_tok = [&](uint32_t t) { return t < a.n ? t : a.n - 1; };
+
+    // ---- per-lane 32-bit offsets of the direct loads (mmx_supports checks that they fit) ----
+    constexpr uint32_t TPW = TOK / NW; // token rows per wave
+    static_assert(TPW % 4 == 0, "token rows per wave");
+    constexpr uint32_t DAL = q6 ? 1 : 8 * TOK / (64 * NW);         // token-scale loads per wave
+    constexpr uint32_t CPW = TPW / 4 + F::W16 + F::W4 + 1 + DAL; // loads per wave and step
+    // Weights: 16-byte piece P = 64*i + lane of the wave's area is row P/(RB/16), piece P%(RB/16);
+    // rows of 256 or 128 bytes are swizzled (piece c of row r at c ^ (r & 15), resp. r & 7) so
+    // the 32 rows one operand read covers hit distinct banks. Q6_K's 208-byte rows need no
+    // swizzle; its last 512 bytes go as words.
+    constexpr uint32_t PPR = F::RB / 16;
+    uint32_t woff[F::W16 + F::W4];
+#pragma unroll
+    for (uint32_t i = 0; i < F::W16; i++) {
+        const uint32_t P = 64 * i + lane, lr = P / PPR, pc = P % PPR;
+        const uint32_t rr = clamp_row(r0 + 32 * wave + lr);
+        const uint32_t c = q6 ? pc : (pc ^ (lr & (PPR - 1)));
+        woff[i] = rr * nsb * F::RB + 16 * c;
+    }
+    if constexpr (q6) {
+#pragma unroll
+        for (uint32_t i = 0; i < F::W4; i++) {
+            const uint32_t Wd = 64 * 4 * F::W16 + 64 * i + lane; // 4-byte word of the wave's area
+            const uint32_t rr = clamp_row(r0 + 32 * wave + Wd / (F::RB / 4));
+            woff[F::W16 + i] = rr * nsb * F::RB + 4 * (Wd % (F::RB / 4));
+        }
+    }
+    // Scales: Q6_K one f16 per row and step (the aligned dword holding it); the blocks' eight
+    // f16 (16 bytes) per row and step otherwise. Lanes 32-63 repeat lanes 0-31.
+    const uint32_t srow = clamp_row(r0 + 32 * wave + j);
+    const uint32_t sbase = q6 ? srow * nsb : srow * (K / 32) * 2;
+    // Token data: activation int8 rows, swizzled like the weights; token scales.
+    uint32_t aoff[TPW / 4];
+#pragma unroll
+    for (uint32_t i = 0; i < TPW / 4; i++) {
+        const uint32_t tl = TPW * wave + 4 * i + lane / 16;
+        const uint32_t c = (lane % 16) ^ (tl & 15);
+        aoff[i] = clamp_tok(t0 + tl) * K + 16 * c;
+    }
+    // Token scales: Q6_K lane L of wave m loads token 64m + L's; A8 load i of wave m covers the
+    // 64 entries 64*(DAL*m + i) .. of the [8][TOK] array: block e / TOK, token e % TOK.
+    uint32_t doff[DAL];
+#pragma unroll
+    for (uint32_t i = 0; i < DAL; i++) {
+        if constexpr (q6) {
+            const uint32_t tl = 64 * wave + lane;
+            doff[i] = clamp_tok(t0 + (tl < TOK ? tl : 0)) * nsb * 4;
+        } else {
+            const uint32_t e = 64 * (DAL * wave + i) + lane;
+            doff[i] = clamp_tok(t0 + e % TOK) * (K / 32) * 4 + 4 * (e / TOK);
+        }
+    }
+
+    auto issue = [&](uint32_t sb, Slot &S) {
+        const int8_t *ga = a.aqs + 256 * sb;
+#pragma unroll
+        for (uint32_t i = 0; i < TPW / 4; i++) load_lds16(ga + aoff[i], &S.a[(TPW * wave + 4 * i) * 256]);
+        const uint8_t *gw = a.w + uint64_t(sb) * F::RB;
+#pragma unroll
+        for (uint32_t i = 0; i < F::W16; i++) load_lds16(gw + woff[i], &S.w[wave][1024 * i]);
+#pragma unroll
+        for (uint32_t i = 0; i < F::W4; i++) load_lds4(gw + woff[F::W16 + i], &S.w[wave][1024 * F::W16 + 256 * i]);
+        const uint8_t *gd = reinterpret_cast<const uint8_t *>(a.ad);
+        if constexpr (q6) {
+            load_lds4(a.ws + (((sbase + sb) >> 1) << 2), &S.ws[wave][0]);
+            load_lds4(gd + doff[0] + 4 * sb, &S.da[64 * wave]);
+        } else {
+            load_lds16(a.ws + sbase + 16 * sb, &S.ws[wave][0]);
+#pragma unroll
+            for (uint32_t i = 0; i < DAL; i++) load_lds4(gd + doff[i] + 32 * sb, &S.da[64 * (DAL * wave + i)]);
+        }
+    };
+
+    v16f acc[TT];
+#pragma unroll
+    for (int t = 0; t < TT; t++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[t][v] = 0.0f;
+
+    issue(0, ring0);
+    if constexpr (NB == 3) issue(1 < nsb ? 1 : nsb - 1, ring1);
+    __builtin_amdgcn_s_waitcnt((0x0F70 & ~0xF) | ((CPW * (NB - 2)) & 0xF) | (((CPW * (NB - 2)) >> 4) << 14));
+    __syncthreads();
+
+    const uint32_t sw = j & 15;
+    auto step = [&](auto ic, uint32_t sb) {
+        constexpr int I = decltype(ic)::value;
+        {
+            const uint32_t ahead = sb + NB - 1;
+            issue(ahead < nsb ? ahead : nsb - 1, slot_at(std::integral_constant<int, (I + NB - 1) % NB>{}));
+        }
+        Slot &S = slot_at(ic);
+        const int8_t *abase = &S.a[j * 256];
+        v4i av[8];
+        auto load_a = [&](int t) {
+#pragma unroll
+            for (int c = 0; c < 8; c++)
+                av[c] = *reinterpret_cast<const v4i *>(abase + 32 * t * 256 + 16 * ((2 * c + h) ^ sw));
+        };
+
+        if constexpr (q6) {
+            // This lane's row half: group 2c + h of chunk c = 4n + p is ql bytes 64n + 32(p&1) +
+            // 16h.. (nibble p>>1), qh bytes 128 + 32n + 16h.. (bits 2p), scale byte 192 + 8n + 2p + h
+            // (dequant.zig's Q6_K order).
+            const uint8_t *blk = &S.w[wave][208 * j];
+            uint4 ql[2][2], qh[2];
+#pragma unroll
+            for (int n = 0; n < 2; n++) {
+#pragma unroll
+                for (int pp = 0; pp < 2; pp++) ql[n][pp] = *reinterpret_cast<const uint4 *>(blk + 64 * n + 32 * pp + 16 * h);
+                qh[n] = *reinterpret_cast<const uint4 *>(blk + 128 + 32 * n + 16 * h);
+            }
+            const uint4 scw = *reinterpret_cast<const uint4 *>(blk + 192);
+            const uint32_t scs[4] = {scw.x, scw.y, scw.z, scw.w};
+            const uint32_t dword = *reinterpret_cast<const uint32_t *>(&S.ws[wave][4 * j]);
+            const float d = f16_bits_to_f32(((sbase + sb) & 1) ? dword >> 16 : dword & 0xFFFF);
+            v4i P[3][8];
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                const int n = c / 4, p = c % 4;
+                const uint32_t sbyte = 8 * n + 2 * p + h;
+                const int sc = int(int8_t((scs[sbyte / 4] >> (8 * (sbyte % 4))) & 0xFF));
+                int e[3];
+                digits(sc, e);
+                const uint32_t qlw[4] = {ql[n][p & 1].x, ql[n][p & 1].y, ql[n][p & 1].z, ql[n][p & 1].w};
+                const uint32_t qhw[4] = {qh[n].x, qh[n].y, qh[n].z, qh[n].w};
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const uint32_t q = ((qlw[i] >> (4 * (p >> 1))) & 0x0F0F0F0Fu) | (((qhw[i] >> (2 * p)) & 0x03030303u) << 4);
+                    const uint32_t ev = q & 0x00FF00FFu, od = (q >> 8) & 0x00FF00FFu;
+#pragma unroll
+                    for (int k = 0; k < 3; k++) P[k][c][i] = int(plane4(ev, od, lo16x2(e[k]), lo16x2(-32 * e[k])));
+                }
+            }
+            load_a(0);
+#pragma unroll
+            for (int t = 0; t < TT; t++) {
+                v16i sacc = {};
+#pragma unroll
+                for (int c = 0; c < 8; c++) sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[c], P[2][c], sacc, 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < 16; v++) sacc[v] <<= 3;
+#pragma unroll
+                for (int c = 0; c < 8; c++) sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[c], P[1][c], sacc, 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < 16; v++) sacc[v] <<= 3;
+#pragma unroll
+                for (int c = 0; c < 8; c++) sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[c], P[0][c], sacc, 0, 0, 0);
+                if (t + 1 < TT) load_a(t + 1);
+                const float4 *dap = reinterpret_cast<const float4 *>(&S.da[32 * t + 4 * h]);
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    const float4 dv = dap[2 * g];
+                    const float ds[4] = {dv.x, dv.y, dv.z, dv.w};
+#pragma unroll
+                    for (int e = 0; e < 4; e++) acc[t][4 * g + e] = fmaf((float)sacc[4 * g + e], d * ds[e], acc[t][4 * g + e]);
+                }
+            }
+        } else {
+            // Block c of this lane's row: its 16-byte piece (Q8_0: bytes 16h.. of the block;
+            // IQ4_NL: the block's 16 bytes, low nibbles for h = 0, high for h = 1).
+            const uint8_t *blk = &S.w[wave][F::RB * j];
+            v4i wv[8];
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                if constexpr (T == HKHIP_Q8_0) {
+                    wv[c] = *reinterpret_cast<const v4i *>(blk + 16 * ((2 * c + h) ^ sw));
+                } else {
+                    const uint4 x = *reinterpret_cast<const uint4 *>(blk + 16 * (c ^ (j & 7)));
+                    const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+                    for (int i = 0; i < 4; i++) wv[c][i] = int(iq4nl_lookup4((xs[i] >> (4 * h)) & 0x0F0F0F0Fu));
+                }
+            }
+            const uint4 s16 = *reinterpret_cast<const uint4 *>(&S.ws[wave][16 * j]);
+            const uint32_t sw4[4] = {s16.x, s16.y, s16.z, s16.w};
+            float dw[8];
+#pragma unroll
+            for (int c = 0; c < 8; c++) dw[c] = f16_bits_to_f32((sw4[c / 2] >> (16 * (c & 1))) & 0xFFFF);
+            load_a(0);
+#pragma unroll
+            for (int t = 0; t < TT; t++) {
+#pragma unroll
+                for (int c = 0; c < 8; c++) {
+                    const v16i p = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[c], wv[c], v16i{}, 0, 0, 0);
+                    // Scales of this lane's 16 outputs: tokens 32t + 8g + 4h + (0..3).
+                    const float4 *dap = reinterpret_cast<const float4 *>(&S.da[c * TOK + 32 * t + 4 * h]);
+#pragma unroll
+                    for (int g = 0; g < 4; g++) {
+                        const float4 dv = dap[2 * g];
+                        const float ds[4] = {dv.x, dv.y, dv.z, dv.w};
+#pragma unroll
+                        for (int e = 0; e < 4; e++)
+                            acc[t][4 * g + e] = fmaf((float)p[4 * g + e], dw[c] * ds[e], acc[t][4 * g + e]);
+                    }
+                }
+                if (t + 1 < TT) load_a(t + 1);
+            }
+        }
+        __builtin_amdgcn_s_waitcnt((0x0F70 & ~0xF) | ((CPW * (NB - 2)) & 0xF) | (((CPW * (NB - 2)) >> 4) << 14));
+        __syncthreads();
+    };
+    for (uint32_t sb = 0; sb < nsb; sb += NB) {
+        step(std::integral_constant<int, 0>{}, sb);
+        if (sb + 1 < nsb) step(std::integral_constant<int, 1>{}, sb + 1);
+        if constexpr (NB == 3)
+            if (sb + 2 < nsb) step(std::integral_constant<int, 2>{}, sb + 2);
+    }
+
+    // ---- store: y[token][row], bias, accumulate ----
+    if (myrow < a.rows) {
+        const float b = a.bias ? a.bias[myrow] : 0.0f;
+#pragma unroll
+        for (int t = 0; t < TT; t++) {
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const uint32_t tok = t0 + 32 * t + 8 * (v / 4) + 4 * h + (v % 4);
+                if (tok < a.n) {
+                    float *dst = a.y + uint64_t(tok) * a.rows + myrow;
+                    if (a.mode == HKHIP_ACCUMULATE)
+                        *dst += acc[t][v] + b;
+                    else
+                        *dst = acc[t][v] + b;
+                }
+            }
+        }
+    }
+}
+
+typedef void (*mx_kernel_t)(MxArgs);
+
+template <int T, int NW, int TT, int NB>
+hipError_t launch_cfg(const MxArgs &a0, hipStream_t s) {
+    static_assert(NB * sizeof(MxSlot<T, 32 * TT, NW>) <= 160 * 1024, "LDS");
+    MxArgs a = a0;
+    a.rblocks = (a.rows + 32 * NW - 1) / (32 * NW);
+    a.tblocks = (a.n + 32 * TT - 1) / (32 * TT);
+    hipLaunchKernelGGL((mmx_kernel<T, NW, TT, NB>), dim3(a.rblocks * a.tblocks), dim3(NW * 64), 0, s, a);
+    return hipGetLastError();
+}
+
+} // namespace mx
+
+bool mmx_supports(int t, uint32_t rows, uint32_t cols, uint32_t n) {
+    if (t != HKHIP_Q6_K && t != HKHIP_Q8_0 && t != HKHIP_IQ4_NL) return false;
+    if (cols % 256 != 0 || rows == 0 || n == 0) return false;
+    // 32-bit per-lane byte offsets: quant plane, scale plane and activations.
+    const WLayout W = weight_layout(t, rows, cols);
+    return W.total < (1ull << 32) && uint64_t(n) * cols < (1ull << 32);
+}
+
+hipError_t launch_mmx(int t, const uint8_t *w, uint32_t rows, uint32_t cols, const uint8_t *xq, uint32_t n, float *y,
+                      const float *bias, int mode, hipStream_t s) {
+    if (!mmx_supports(t, rows, cols, n)) return hipErrorInvalidValue;
+    const WLayout W = weight_layout(t, rows, cols);
+    const ActLayout A = act_layout(n, cols);
+    const bool q6 = t == HKHIP_Q6_K;
+    mx::MxArgs a{};
+    a.w = w;
+    a.ws = w + W.scale_off;
+    a.rows = rows;
+    a.cols = cols;
+    a.n = n;
+    a.aqs = reinterpret_cast<const int8_t *>(xq + (q6 ? A.k_qs : A.a8_qs));
+    a.ad = reinterpret_cast<const float *>(xq + (q6 ? A.k_d : A.a8_d));
+    a.y = y;
+    a.bias = bias;
+    a.mode = mode;
+    // Tile choice (measured at the 8B FFN shapes, 512 tokens): the largest tile that still gives
+    // most CUs a workgroup.
+    auto blocks = [&](uint32_t nw, uint32_t tt) {
+        return ((rows + 32 * nw - 1) / (32 * nw)) * ((n + 32 * tt - 1) / (32 * tt));
+    };
+    switch (t) {
+    case HKHIP_Q6_K:
+        if (blocks(4, 2) >= 192) return mx::launch_cfg<HKHIP_Q6_K, 4, 2, 2>(a, s);
+        return mx::launch_cfg<HKHIP_Q6_K, 4, 1, 2>(a, s);
+    case HKHIP_Q8_0:
+        return mx::launch_cfg<HKHIP_Q8_0, 4, 1, 2>(a, s);
+    case HKHIP_IQ4_NL:
+        if (blocks(8, 2) >= 224) return mx::launch_cfg<HKHIP_IQ4_NL, 8, 2, 2>(a, s);
+        return mx::launch_cfg<HKHIP_IQ4_NL, 4, 1, 2>(a, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+} // namespace hkhip
