@@ -6,4 +6,4 @@ include/hkhip.h (libhkhip.so).
 """
 from . import formats  # noqa: F401
 from ._lib import HipError, lib  # noqa: F401
-from .engine import ACCUMULATE, STORE, DevMat, Engine, gemm, gemv  # noqa: F401
+from .engine import ACCUMULATE, SILU_MUL, STORE, DevMat, Engine, gemm, gemv  # noqa: F401

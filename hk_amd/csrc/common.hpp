@@ -74,7 +74,8 @@ inline WLayout weight_layout(int t, uint32_t rows, uint32_t cols) {
 //         integers, bsum32 = 64*u + v with v in [0, 63]: 64*u for the 8 sub-blocks, then v --
 //         the token-side operand of the GEMM's integer min term, precomputed once
 //   For at most SK_MAX_TOKENS tokens, token-interleaved copies of the Q8K planes for the
-//   small-batch kernel, tokens in tiles of 16 (the last one padded with the last token):
+//   small-batch kernel, tokens in tiles of 16 (the last tile's padding positions are left
+//   unwritten; the kernel's padding lanes read the last token's entries instead):
 //   k_il   [k/64][tiles][64][16 B]: entry 16g + p holds token 16*tile + p's values
 //          64c + 16g .. 64c + 16g + 15 -- one 16-token tile's 64-value chunk is 1 KB in the
 //          order of the MFMA lanes that use it
@@ -156,6 +157,10 @@ __device__ __forceinline__ void load_lds16(const void *g, void *lds) {
 __device__ __forceinline__ void load_lds4(const void *g, void *lds) {
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" : : "v"(g), "s"(lds_addr(lds)) : "memory", "m0");
 }
+
+// Output mode HKHIP_SILU_MUL: output i of gate g (row 2i) and up u (row 2i + 1), as
+// shaders/mmvq.comp:186 computes it.
+__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);

@@ -266,7 +266,10 @@ int hkhip_act_export(hkhip_engine *eng, const void *xq_dev, uint32_t n, uint32_t
 static int check_product(const hkhip_mat *m, const void *xq, float *y, uint32_t n, int mode) {
     int rc = check_mat(m);
     if (rc) return rc;
-    if (mode != HKHIP_STORE && mode != HKHIP_ACCUMULATE) return fail(HKHIP_E_BAD_ARGUMENT, "unknown mode %d", mode);
+    if (mode != HKHIP_STORE && mode != HKHIP_ACCUMULATE && mode != HKHIP_SILU_MUL)
+        return fail(HKHIP_E_BAD_ARGUMENT, "unknown mode %d", mode);
+    if (mode == HKHIP_SILU_MUL && (m->rows % 2 || n > 8))
+        return fail(HKHIP_E_BAD_ARGUMENT, "silu(gate)*up needs interleaved gate/up rows (even count) and n <= 8");
     if (act_kind(m->t) == HKHIP_ACT_Q8K && m->cols % QK_K) return fail(HKHIP_E_UNSUPPORTED_SHAPE, "bad cols");
     if (n && (!xq || !y)) return fail(HKHIP_E_BAD_ARGUMENT, "null buffer");
     return HKHIP_OK;
@@ -277,6 +280,7 @@ int hkhip_matvec(hkhip_engine *eng, const hkhip_mat *m, const void *xq_dev, floa
     int rc = enter(eng);
     if (rc || (rc = check_product(m, xq_dev, y_dev, n, mode))) return rc;
     if (n > 8) return fail(HKHIP_E_UNSUPPORTED_SHAPE, "matvec takes at most 8 tokens, got %u", n);
+    if (mode == HKHIP_SILU_MUL && bias_dev) return fail(HKHIP_E_BAD_ARGUMENT, "silu(gate)*up takes no bias");
     if (n == 0) return HKHIP_OK;
     HIP_TRY(launch_mmvq(m->t, reinterpret_cast<const uint8_t *>(m->mem), m->rows, m->cols,
                         reinterpret_cast<const uint8_t *>(xq_dev), n, y_dev, bias_dev, mode, eng->cur), "mmvq launch");
@@ -292,6 +296,8 @@ int hkhip_matvec_parts(hkhip_engine *eng, const hkhip_mat *mats, uint32_t nparts
     MvPartDesc parts[4];
     for (uint32_t i = 0; i < nparts; i++) {
         if ((rc = check_product(&mats[i], x_dev ? (const void *)x_dev : xq_dev, ys[i], n, mode))) return rc;
+        if (mode == HKHIP_SILU_MUL && biases && biases[i])
+            return fail(HKHIP_E_BAD_ARGUMENT, "silu(gate)*up takes no bias");
         if (mats[i].t != mats[0].t || mats[i].cols != mats[0].cols)
             return fail(HKHIP_E_BAD_ARGUMENT, "fused parts must share type and cols");
         parts[i] = MvPartDesc{reinterpret_cast<const uint8_t *>(mats[i].mem), ys[i], biases ? biases[i] : nullptr,
@@ -308,6 +314,7 @@ int hkhip_gemm(hkhip_engine *eng, const hkhip_mat *m, const void *xq_dev, float 
                const float *bias_dev, int mode) {
     int rc = enter(eng);
     if (rc || (rc = check_product(m, xq_dev, y_dev, n, mode))) return rc;
+    if (mode == HKHIP_SILU_MUL) return fail(HKHIP_E_BAD_ARGUMENT, "silu(gate)*up is a decode mode (hkhip_matvec)");
     if (n == 0) return HKHIP_OK;
     if ((n + 63) / 64 > 65535u) return fail(HKHIP_E_UNSUPPORTED_SHAPE, "too many tokens: %u", n);
     HIP_TRY(launch_mm(m->t, reinterpret_cast<const uint8_t *>(m->mem), m->rows, m->cols,
@@ -320,8 +327,8 @@ int hkhip_gemm(hkhip_engine *eng, const hkhip_mat *m, const void *xq_dev, float 
 // matvec pass of 8 tokens streams the weights once more).
 static uint32_t gemm_min_tokens(int t) {
     switch (t) {
-    case HKHIP_Q6_K: return 65;
-    case HKHIP_Q8_0:
+    case HKHIP_Q6_K:
+    case HKHIP_Q8_0: return 33;
     case HKHIP_IQ4_NL: return 25;
     default: return 9;
     }

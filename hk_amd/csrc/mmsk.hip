@@ -253,7 +253,14 @@ __global__ __launch_bounds__(KS * 64) void mmsk_q4k_kernel(SkArgs a) {
 #pragma unroll
                 for (int w = 0; w < KS - 1; w++) acc[rt][tt] += part[w][rt][tt][lane];
                 const uint32_t tok = 16 * tt + p;
-                if (tok < a.n) {
+                if (tok < a.n && a.mode == HKHIP_SILU_MUL) {
+                    // Rows 4g + i of the tile: gate/up pairs (i = 0, 1) and (2, 3).
+#pragma unroll
+                    for (int i = 0; i < 4; i += 2) {
+                        const uint32_t r = r0 + 16 * rt + 4 * g + i;
+                        if (r < rows) Y[uint64_t(tok) * (rows / 2) + r / 2] = silu_mul(acc[rt][tt][i], acc[rt][tt][i + 1]);
+                    }
+                } else if (tok < a.n) {
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
                         const uint32_t r = r0 + 16 * rt + 4 * g + i;

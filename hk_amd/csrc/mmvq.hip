@@ -552,7 +552,21 @@ __global__ __launch_bounds__(NW * 64) void mmvq_kernel(MvArgs a) {
             v[t] = group_sum(acc[t] - corr[t], lg);
             acc[t] = corr[t] = 0.0f;
         }
-        if (active && ul == 0) mv_store<NT>(a, p, r, v);
+        if (a.mode == HKHIP_SILU_MUL) {
+            // Row r's lanes are sub-group `sub`; the up row of an even r is the next sub-group
+            // (the launch keeps at least two rows per wave in this mode).
+            float up[NT];
+#pragma unroll
+            for (int t = 0; t < NT; t++) up[t] = __shfl_down(v[t], lpr);
+            if (active && ul == 0 && (r & 1) == 0) {
+                float *y = MV_SEL(y);
+                const uint32_t rows = MV_SEL(rows);
+#pragma unroll
+                for (int t = 0; t < NT; t++) y[uint64_t(t) * (rows / 2) + r / 2] = silu_mul(v[t], up[t]);
+            }
+        } else if (active && ul == 0) {
+            mv_store<NT>(a, p, r, v);
+        }
     };
     // Steps in order (g, ch); the next step's weights load while this one computes.
     uint32_t g = g0, ch = 0;
@@ -710,8 +724,10 @@ __global__ __launch_bounds__(NW * 64) void mmvr_kernel(MvArgs a) {
     const uint32_t u0 = ks * 64 * C; // first unit of this wave's slice
     const uint32_t ngroups = gridDim.x * NRG, gid = blockIdx.x * NRG + rg;
     const uint32_t total = a.ngroups; // rows of all parts
-    const uint32_t r0 = uint32_t(uint64_t(total) * gid / ngroups);
-    const uint32_t r1 = uint32_t(uint64_t(total) * (gid + 1) / ngroups);
+    // Mode HKHIP_SILU_MUL splits the rows in gate/up pairs, so that a pair stays in one wave.
+    const uint32_t pr = a.mode == HKHIP_SILU_MUL ? 2u : 1u;
+    const uint32_t r0 = pr * uint32_t(uint64_t(total / pr) * gid / ngroups);
+    const uint32_t r1 = pr * uint32_t(uint64_t(total / pr) * (gid + 1) / ngroups);
     // A wave without rows still helps stage the input (and reaches the barrier).
     const uint32_t rlast = r0 < r1 ? r1 - 1 : 0;
 
@@ -825,6 +841,22 @@ __global__ __launch_bounds__(NW * 64) void mmvr_kernel(MvArgs a) {
     float res[NT];
     const uint32_t fbase = r0;
     auto flush = [&](uint32_t n) {
+        if (a.mode == HKHIP_SILU_MUL) {
+            // Lane 2i holds gate row r0 + 2i, lane 2i + 1 its up row (r0 is even).
+            float up[NT];
+#pragma unroll
+            for (int t = 0; t < NT; t++) up[t] = __shfl_down(res[t], 1);
+            if (lane < n && (lane & 1) == 0) {
+                const MvPart q = locate(fbase + lane);
+                const uint32_t o = (fbase + lane - q.gstart) / 2;
+#pragma unroll
+                for (int t = 0; t < NT; t++) {
+                    if (NT > 1 && uint32_t(t) >= a.ntok) break;
+                    q.y[uint64_t(t) * (q.rows / 2) + o] = silu_mul(res[t], up[t]);
+                }
+            }
+            return;
+        }
         if (lane < n) {
             const uint32_t r = fbase + lane;
             MvPart q = a.p[0];
@@ -1153,6 +1185,7 @@ static hipError_t launch_mv_chunk(int t, const MvPartDesc *parts, int nparts, ui
     const uint32_t want_lanes = (units + unr - 1) / unr;
     int lg = 0;
     while ((1u << lg) < want_lanes && lg < 6) lg++;
+    if (mode == HKHIP_SILU_MUL && lg > 5) lg = 5; // a gate/up pair within one wave
     const uint32_t rpw = 64u >> lg;
     const int nw = MV_NW;
     for (uint32_t t0 = 0; t0 < n; t0 += per) {
@@ -1163,7 +1196,7 @@ static hipError_t launch_mv_chunk(int t, const MvPartDesc *parts, int nparts, ui
             const WLayout W = weight_layout(t, parts[i].rows, K);
             a.p[i].w = parts[i].w;
             a.p[i].ws = reinterpret_cast<const uint16_t *>(parts[i].w + W.scale_off);
-            a.p[i].y = parts[i].y + uint64_t(t0) * parts[i].rows;
+            a.p[i].y = parts[i].y + uint64_t(t0) * (mode == HKHIP_SILU_MUL ? parts[i].rows / 2 : parts[i].rows);
             a.p[i].bias = parts[i].bias;
             a.p[i].rows = parts[i].rows;
             a.p[i].gstart = groups;
@@ -1224,7 +1257,7 @@ hipError_t launch_mmvq_parts(int t, const MvPartDesc *parts, int nparts, uint32_
         MvPartDesc pc[MV_PARTS];
         for (int i = 0; i < nparts; i++) {
             pc[i] = parts[i];
-            pc[i].y = parts[i].y + uint64_t(t0) * parts[i].rows;
+            pc[i].y = parts[i].y + uint64_t(t0) * (mode == HKHIP_SILU_MUL ? parts[i].rows / 2 : parts[i].rows);
         }
         const hipError_t e = launch_mv_chunk(t, pc, nparts, K, t0 ? mv_act_at(act, kq, K, t0) : act, nc, mode, s);
         if (e != hipSuccess) return e;

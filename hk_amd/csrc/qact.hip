@@ -26,7 +26,8 @@ __device__ __forceinline__ uint32_t bf16_bits_rne(float x) {
 }
 
 // Token-interleaved copies for the small-batch kernel (tiles > 0; layout in common.hpp): token
-// t's entries, and for the last token also those of the padding tokens of its tile.
+// t's entries. The padding positions of the last tile are not written: the reader takes the last
+// token's entries for them.
 struct QactIl {
     uint8_t *qs;
     uint16_t *mb;
@@ -57,19 +58,16 @@ __global__ void qact_q8k_kernel(const float *__restrict__ x, uint64_t nblocks, i
     if (il.tiles) {
         const uint32_t b32i = uint32_t(b); // tokens <= SK_MAX_TOKENS: a small index
         const uint32_t t = b32i / il.nsb, sb = b32i - t * il.nsb;
-        const uint32_t tile = t / 16, p0 = t % 16;
-        const uint32_t p1 = t + 1 == il.n ? 16 : p0 + 1; // the last token also fills its tile's padding
+        const uint32_t tile = t / 16, p = t % 16;
         const uint32_t c64 = 4 * sb + lane / 16, g = (lane % 16) / 4;
-        for (uint32_t p = p0; p < p1; p++) {
-            uint8_t *e = il.qs + ((uint64_t(c64) * il.tiles + tile) * 64 + 16 * g + p) * 16 + 4 * (lane % 4);
-            *reinterpret_cast<uint32_t *>(e) = r.packed;
-            const uint64_t mbase = (uint64_t(sb) * il.tiles + tile) * 256; // in uint16: 2 halves x 16 x 8
-            if ((lane & 7) == 0) {
-                il.mb[mbase + p * 8 + lane / 8] = mu;
-                il.mb[mbase + 128 + p * 8 + lane / 8] = mv;
-            }
-            if (lane == 0) il.d[(uint64_t(sb) * il.tiles + tile) * 16 + p] = r.d;
+        uint8_t *e = il.qs + ((uint64_t(c64) * il.tiles + tile) * 64 + 16 * g + p) * 16 + 4 * (lane % 4);
+        *reinterpret_cast<uint32_t *>(e) = r.packed;
+        const uint64_t mbase = (uint64_t(sb) * il.tiles + tile) * 256; // in uint16: 2 halves x 16 x 8
+        if ((lane & 7) == 0) {
+            il.mb[mbase + p * 8 + lane / 8] = mu;
+            il.mb[mbase + 128 + p * 8 + lane / 8] = mv;
         }
+        if (lane == 0) il.d[(uint64_t(sb) * il.tiles + tile) * 16 + p] = r.d;
     }
 }
 

@@ -19,7 +19,7 @@ import numpy as np
 from . import formats
 from ._lib import HipError, HkhipMat, check, lib
 
-STORE, ACCUMULATE = 0, 1
+STORE, ACCUMULATE, SILU_MUL = 0, 1, 2  # output modes (hkhip.h HKHIP_STORE / ACCUMULATE / SILU_MUL)
 MIN_TILED_TOKENS = 8  # matmul.zig:18
 
 
@@ -166,7 +166,7 @@ class Engine:
 
     def mm(self, m: DevMat, xq, y, n: int, bias=None, mode: int = STORE) -> None:
         """y[t][r] = dot(W[r], x[t]) + bias[r]: decode kernel up to 8 tokens, 8-token decode passes
-        up to the GEMM's break-even (Q6_K 64, Q8_0 / IQ4_NL 24 tokens), MFMA GEMM beyond
+        up to the GEMM's break-even (Q6_K / Q8_0 32, IQ4_NL 24 tokens), MFMA GEMM beyond
         (mm: cuda/engine.zig:581-611; matmul.zig:18,107)."""
         check(lib().hkhip_mm(self._h, ctypes.byref(m.raw), _ptr(xq), _ptr(y), n, _ptr(bias), mode))
 

@@ -13,7 +13,7 @@ import pytest
 
 from hk_amd import formats as F
 from hk_amd import synth
-from hk_amd.engine import ACCUMULATE
+from hk_amd.engine import ACCUMULATE, SILU_MUL
 from oracle import oracle as O
 from tests.helpers import PARITY_TOL, load_fixture, parity_err
 
@@ -384,3 +384,84 @@ def test_matvec_parts_straddling_waves(eng, torch_cuda, t):
         assert parity_err(y.cpu().numpy(), O.matmul(t, r, m, k, x, n, tiled=False)) <= PARITY_TOL
     for w in mats:
         eng.free(w)
+
+
+# ---------------------------------------------------------------------------------------- silu(gate) * up
+
+def silu_mul_ref(y):
+    """shaders/mmvq.comp:186 on the oracle's product of interleaved gate/up rows."""
+    g, u = y[:, 0::2].astype(np.float32), y[:, 1::2].astype(np.float32)
+    with np.errstate(over="ignore"):  # exp(-g) = inf for very negative g: silu -> -0, as on the GPU
+        return g / (np.float32(1) + np.exp(-g)) * u
+
+
+@pytest.mark.parametrize("t", FMTS)
+@pytest.mark.parametrize("n", [1, 3, 5, 8])
+@pytest.mark.parametrize("prepared", [False, True])
+def test_silu_mul_parts(eng, torch_cuda, t, n, prepared):
+    """Mode 2 (the Vulkan mmvq's fused gate/up): two interleaved gate/up matrices in one launch,
+    each output silu(gate) * up; f32 input (decode kernel) or prepared (Q4_K from 4 tokens: the
+    small-batch kernel)."""
+    torch = torch_cuda
+    k = 1024
+    heights = [2 * 48, 2 * 21]
+    raws = [synth.weights_np(t, m, k, seed=1100 + i + t) for i, m in enumerate(heights)]
+    x = synth.activations_np(n, k, seed=1101 + n, outliers=0.01)
+    mats = [eng.upload(r, t, m, k) for r, m in zip(raws, heights)]
+    ys = [torch.full((n, m // 2), float("nan"), device="cuda") for m in heights]
+    xd = torch.from_numpy(x).cuda()
+    if prepared:
+        xq = torch.empty(eng.act_bytes(n, k), dtype=torch.uint8, device="cuda")
+        eng.qact(xd, n, k, F.ACT_KIND[t], xq)
+        eng.matvec_parts(mats, ys, n, xq=xq, mode=SILU_MUL)
+    else:
+        eng.matvec_parts(mats, ys, n, x=xd, mode=SILU_MUL)
+    torch.cuda.synchronize()
+    for r, m, y in zip(raws, heights, ys):
+        want = silu_mul_ref(O.matmul(t, r, m, k, x, n, tiled=False))
+        assert parity_err(y.cpu().numpy(), want) <= PARITY_TOL
+    for w in mats:
+        eng.free(w)
+
+
+@pytest.mark.parametrize("t,k,n", [(F.Q4_K, 14336, 8), (F.Q4_K, 16640, 1), (F.Q8_0, 16416, 2),
+                                   (F.Q6_K, 20480, 1), (F.IQ4_NL, 4096, 8)])
+def test_silu_mul_kernel_variants(eng, torch_cuda, t, k, n):
+    """Mode 2 where rows are split over K-slice waves and where the LDS kernel runs (rows longer
+    than the register kernel takes)."""
+    torch = torch_cuda
+    m = 2 * 150
+    raw = synth.weights_np(t, m, k, seed=1200 + t + k)
+    x = synth.activations_np(n, k, seed=1201 + n)
+    w = eng.upload(raw, t, m, k)
+    y = torch.full((n, m // 2), float("nan"), device="cuda")
+    eng.matvec_parts([w], [y], n, x=torch.from_numpy(x).cuda(), mode=SILU_MUL)
+    torch.cuda.synchronize()
+    want = silu_mul_ref(O.matmul(t, raw, m, k, x, n, tiled=False))
+    assert parity_err(y.cpu().numpy(), want) <= PARITY_TOL
+    eng.free(w)
+
+
+def test_silu_mul_rejects(eng, torch_cuda):
+    """Mode 2 takes an even row count, no bias, at most 8 tokens, and no GEMM."""
+    from hk_amd import HipError
+
+    torch = torch_cuda
+    t, k = F.Q4_K, 256
+    odd = eng.upload(synth.weights_np(t, 7, k, seed=1300), t, 7, k)
+    even = eng.upload(synth.weights_np(t, 8, k, seed=1301), t, 8, k)
+    xq = torch.zeros(eng.act_bytes(16, k), dtype=torch.uint8, device="cuda")
+    y = torch.zeros(16, 8, device="cuda")
+    b = torch.zeros(8, device="cuda")
+    with pytest.raises(HipError):
+        eng.matvec(odd, xq, y, 1, mode=SILU_MUL)
+    with pytest.raises(HipError):
+        eng.matvec(even, xq, y, 1, bias=b, mode=SILU_MUL)
+    with pytest.raises(HipError):
+        eng.gemm(even, xq, y, 1, mode=SILU_MUL)
+    with pytest.raises(HipError):
+        eng.mm(even, xq, y, 16, mode=SILU_MUL)
+    eng.matvec(even, xq, y, 1, mode=SILU_MUL)
+    torch.cuda.synchronize()
+    eng.free(odd)
+    eng.free(even)
