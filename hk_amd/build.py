@@ -1,4 +1,5 @@
-"""Builds the HIP engine library hk_amd/libhkhip.so for gfx950 (hipcc, in-tree).
+"""Builds the HIP engine library hk_amd/libhkhip.so (and the benchmark's peak probes,
+hk_amd/libhkpeak.so) for gfx950 (hipcc, in-tree).
 
 Every translation unit is compiled with hipcc and linked into one shared library exporting the
 C ABI of include/hkhip.h. Flags that matter for the arithmetic:
@@ -63,7 +64,24 @@ def build(jobs: int | None = None) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
     os.replace(tmp, OUT)
+    build_peak()
     return OUT
+
+
+PEAK_SRC = "peak.hip"
+PEAK_OUT = os.path.join(HERE, "libhkpeak.so")
+
+
+def build_peak() -> str:
+    """The benchmark's peak probes (MFMA rate, HBM read rate): a library of their own."""
+    obj = _compile(PEAK_SRC)
+    tmp = PEAK_OUT + ".tmp"
+    r = subprocess.run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, obj],
+                       capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed:\n{r.stderr}")
+    os.replace(tmp, PEAK_OUT)
+    return PEAK_OUT
 
 
 if __name__ == "__main__":
