@@ -378,28 +378,30 @@ __global__ __launch_bounds__(Q2_NW * 64, 2) void mm2_q4k_reg_kernel(Mm2Args a) {
 
 
 
-template <int NW, int TT, int NB>
-__global__ __launch_bounds__(NW * 64, 2) void mm2_q4k_kernel(Mm2Args a) {
+// KS > 1 splits K: the workgroup's waves form KS slices of NW waves; slice k takes super-blocks
+// k, k + KS, ... through a ring of its own, and the slices' partial tiles are added in LDS (in
+// slice order) at the end. For matrices too small to give every SIMD two waves otherwise.
+template <int NW, int TT, int NB, int KS = 1>
+__global__ __launch_bounds__(NW * KS * 64, 2) void mm2_q4k_kernel(Mm2Args a) {
     constexpr int ROWS = 32 * NW, TOK = 32 * TT;
     using Slot = Q2Slot<TOK, NW>;
     static_assert(NB == 2 || NB == 3, "ring depth");
-    // The ring's slots are LDS objects of their own, and the loop below is unrolled over them, so
-    // the compiler can tell that reading one slot does not alias the direct loads into another
-    // (with one array it would wait for every load in flight before the first read).
-    __shared__ __attribute__((aligned(16))) Slot ring0;
-    __shared__ __attribute__((aligned(16))) Slot ring1;
-    __shared__ __attribute__((aligned(16))) Slot ring2;
+    // The ring's slots are LDS objects of their own, and the loop below is unrolled over them.
+    __shared__ __attribute__((aligned(16))) Slot ring0[KS];
+    __shared__ __attribute__((aligned(16))) Slot ring1[KS];
+    __shared__ __attribute__((aligned(16))) Slot ring2[KS];
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wall = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t ks = wall / NW, wave = wall % NW; // K slice, row wave within the slice
     auto slot_at = [&](auto ic) -> Slot & {
         constexpr int i = decltype(ic)::value;
         if constexpr (i == 0)
-            return ring0;
+            return ring0[ks];
         else if constexpr (i == 1)
-            return ring1;
+            return ring1[ks];
         else
-            return ring2;
+            return ring2[ks];
     };
-    const uint32_t tid = threadIdx.x, lane = tid & 63;
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t h = lane >> 5, j = lane & 31;
     const uint32_t K = a.cols, nsb = K / 256;
 
@@ -476,87 +478,92 @@ __global__ __launch_bounds__(NW * 64, 2) void mm2_q4k_kernel(Mm2Args a) {
 #pragma unroll
         for (int v = 0; v < 16; v++) acc[t][v] = 0.0f;
 
+    // Step j of slice ks is super-block ks + KS*j (loads past the end repeat the last one).
+    const uint32_t nst = (nsb + KS - 1) / KS;
+    auto sb_of = [&](uint32_t st) {
+        const uint32_t sb = ks + KS * st;
+        return sb < nsb ? sb : nsb - 1;
+    };
+
     // Prologue: NB-1 super-blocks in flight.
-    issue(0, ring0);
-    if constexpr (NB == 3) issue(1 < nsb ? 1 : nsb - 1, ring1);
+    issue(sb_of(0), slot_at(std::integral_constant<int, 0>{}));
+    if constexpr (NB == 3) issue(sb_of(1), slot_at(std::integral_constant<int, 1>{}));
     // Wait for slot 0 (the loads of NB-2 later super-blocks may stay in flight).
     __builtin_amdgcn_s_waitcnt((0x0F70 & ~0xF) | ((CPW * (NB - 2)) & 0xF) | (((CPW * (NB - 2)) >> 4) << 14));
     __syncthreads();
 
     // One super-block from slot IC while the one NB-1 ahead goes into slot (IC + NB-1) % NB.
-    auto step = [&](auto ic, uint32_t sb) {
+    auto step = [&](auto ic, uint32_t st) {
         constexpr int I = decltype(ic)::value;
-        {
-            const uint32_t ahead = sb + NB - 1;
-            issue(ahead < nsb ? ahead : nsb - 1, slot_at(std::integral_constant<int, (I + NB - 1) % NB>{}));
-        }
+        issue(sb_of(st + NB - 1), slot_at(std::integral_constant<int, (I + NB - 1) % NB>{}));
         Slot &S = slot_at(ic);
-
-        // Unpack this lane's row half (h) from LDS: header, then both planes of 8 sub-blocks.
-        const uint8_t *blk = &S.w[wave][144 * j];
-        const uint4 ch = *reinterpret_cast<const uint4 *>(blk);
-        uint4 cq[4];
+        if (KS == 1 || ks + KS * st < nsb) {
+            // Unpack this lane's row half (h) from LDS: header, then both planes of 8 sub-blocks.
+            const uint8_t *blk = &S.w[wave][144 * j];
+            const uint4 ch = *reinterpret_cast<const uint4 *>(blk);
+            uint4 cq[4];
 #pragma unroll
-        for (int p = 0; p < 4; p++) cq[p] = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * p + 16 * h);
-        // Scales: vecdot.zig:461-474 word form.
-        const uint32_t k1 = 0x3f3f3f3fu, k2 = 0x0f0f0f0fu, k3 = 0x03030303u;
-        const uint32_t scl = ch.y & k1, mnl = ch.z & k1;
-        const uint32_t sch = (ch.w & k2) | (((ch.y >> 6) & k3) << 4);
-        const uint32_t mnh = ((ch.w >> 4) & k2) | (((ch.z >> 6) & k3) << 4);
-        const float d = f16_bits_to_f32(ch.x & 0xFFFF), dmin = f16_bits_to_f32(ch.x >> 16);
-        v4i bhi[8], blo[8];
+            for (int p = 0; p < 4; p++) cq[p] = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * p + 16 * h);
+            // Scales: vecdot.zig:461-474 word form.
+            const uint32_t k1 = 0x3f3f3f3fu, k2 = 0x0f0f0f0fu, k3 = 0x03030303u;
+            const uint32_t scl = ch.y & k1, mnl = ch.z & k1;
+            const uint32_t sch = (ch.w & k2) | (((ch.y >> 6) & k3) << 4);
+            const uint32_t mnh = ((ch.w >> 4) & k2) | (((ch.z >> 6) & k3) << 4);
+            const float d = f16_bits_to_f32(ch.x & 0xFFFF), dmin = f16_bits_to_f32(ch.x >> 16);
+            v4i bhi[8], blo[8];
 #pragma unroll
-        for (int p = 0; p < 4; p++) {
-            const uint32_t se = (p < 2 ? scl >> (16 * p) : sch >> (16 * (p - 2))) & 0xFF;
-            const uint32_t so = (p < 2 ? scl >> (16 * p + 8) : sch >> (16 * (p - 2) + 8)) & 0xFF;
-            const uint32_t she = (se >> 3) * 0x00010001u, sle = (se & 7) * 0x00010001u;
-            const uint32_t sho = (so >> 3) * 0x00010001u, slo = (so & 7) * 0x00010001u;
-            const uint32_t qw[4] = {cq[p].x, cq[p].y, cq[p].z, cq[p].w};
+            for (int p = 0; p < 4; p++) {
+                const uint32_t se = (p < 2 ? scl >> (16 * p) : sch >> (16 * (p - 2))) & 0xFF;
+                const uint32_t so = (p < 2 ? scl >> (16 * p + 8) : sch >> (16 * (p - 2) + 8)) & 0xFF;
+                const uint32_t she = (se >> 3) * 0x00010001u, sle = (se & 7) * 0x00010001u;
+                const uint32_t sho = (so >> 3) * 0x00010001u, slo = (so & 7) * 0x00010001u;
+                const uint32_t qw[4] = {cq[p].x, cq[p].y, cq[p].z, cq[p].w};
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t ne = qw[i] & 0x0F0F0F0Fu, no = (qw[i] >> 4) & 0x0F0F0F0Fu;
-                bhi[2 * p][i] = int(mul_bytes(ne, she));
-                blo[2 * p][i] = int(mul_bytes(ne, sle));
-                bhi[2 * p + 1][i] = int(mul_bytes(no, sho));
-                blo[2 * p + 1][i] = int(mul_bytes(no, slo));
+                for (int i = 0; i < 4; i++) {
+                    const uint32_t ne = qw[i] & 0x0F0F0F0Fu, no = (qw[i] >> 4) & 0x0F0F0F0Fu;
+                    bhi[2 * p][i] = int(mul_bytes(ne, she));
+                    blo[2 * p][i] = int(mul_bytes(ne, sle));
+                    bhi[2 * p + 1][i] = int(mul_bytes(no, sho));
+                    blo[2 * p + 1][i] = int(mul_bytes(no, slo));
+                }
             }
-        }
-        // Min-term operand of this lane's row.
-        const v8bf mB = min_b(mnl, mnh);
-        const float ndmin = -dmin;
+            // Min-term operand of this lane's row.
+            const v8bf mB = min_b(mnl, mnh);
+            const float ndmin = -dmin;
 
-        // A operand of tile t, sub-block s: token 32t + j, chunk 2s + h (swizzled).
-        const int8_t *abase = &S.a[j * 256];
-        const uint32_t sw = j & 15;
-        v4i av[8];
-        auto load_a = [&](int t) {
+            // A operand of tile t, sub-block s: token 32t + j, chunk 2s + h (swizzled).
+            const int8_t *abase = &S.a[j * 256];
+            const uint32_t sw = j & 15;
+            v4i av[8];
+            auto load_a = [&](int t) {
 #pragma unroll
-            for (int s = 0; s < 8; s++)
-                av[s] = *reinterpret_cast<const v4i *>(abase + 32 * t * 256 + 16 * ((2 * s + h) ^ sw));
-        };
-        load_a(0);
+                for (int s = 0; s < 8; s++)
+                    av[s] = *reinterpret_cast<const v4i *>(abase + 32 * t * 256 + 16 * ((2 * s + h) ^ sw));
+            };
+            load_a(0);
 #pragma unroll
-        for (int t = 0; t < TT; t++) {
-            const v16f jt = min_j(S.mb[32 * t + j], mB, h, acc[t][15]);
-            // One accumulator: the sh-plane chain, times 8, then the sl-plane chain on top.
-            v16i sacc = {};
+            for (int t = 0; t < TT; t++) {
+                const v16f jt = min_j(S.mb[32 * t + j], mB, h, acc[t][15]);
+                // One accumulator: the sh-plane chain, times 8, then the sl-plane chain on top.
+                v16i sacc = {};
 #pragma unroll
-            for (int s = 0; s < 8; s++) sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[s], bhi[s], sacc, 0, 0, 0);
+                for (int s = 0; s < 8; s++) sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[s], bhi[s], sacc, 0, 0, 0);
 #pragma unroll
-            for (int v = 0; v < 16; v++) sacc[v] <<= 3;
+                for (int v = 0; v < 16; v++) sacc[v] <<= 3;
 #pragma unroll
-            for (int s = 0; s < 8; s++) sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[s], blo[s], sacc, 0, 0, 0);
-            if (t + 1 < TT) load_a(t + 1);
-            // Token scales of this lane's 16 outputs: tokens 32t + 8g + 4h + (0..3).
-            const float4 *dap = reinterpret_cast<const float4 *>(&S.da[32 * t + 4 * h]);
+                for (int s = 0; s < 8; s++) sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[s], blo[s], sacc, 0, 0, 0);
+                if (t + 1 < TT) load_a(t + 1);
+                // Token scales of this lane's 16 outputs: tokens 32t + 8g + 4h + (0..3).
+                const float4 *dap = reinterpret_cast<const float4 *>(&S.da[32 * t + 4 * h]);
 #pragma unroll
-            for (int g = 0; g < 4; g++) {
-                const float4 dv = dap[2 * g];
-                const float ds[4] = {dv.x, dv.y, dv.z, dv.w};
+                for (int g = 0; g < 4; g++) {
+                    const float4 dv = dap[2 * g];
+                    const float ds[4] = {dv.x, dv.y, dv.z, dv.w};
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const int v = 4 * g + e;
-                    acc[t][v] = fmaf(fmaf((float)sacc[v], d, ndmin * jt[v]), ds[e], acc[t][v]);
+                    for (int e = 0; e < 4; e++) {
+                        const int v = 4 * g + e;
+                        acc[t][v] = fmaf(fmaf((float)sacc[v], d, ndmin * jt[v]), ds[e], acc[t][v]);
+                    }
                 }
             }
         }
@@ -564,11 +571,33 @@ __global__ __launch_bounds__(NW * 64, 2) void mm2_q4k_kernel(Mm2Args a) {
         __builtin_amdgcn_s_waitcnt((0x0F70 & ~0xF) | ((CPW * (NB - 2)) & 0xF) | (((CPW * (NB - 2)) >> 4) << 14));
         __syncthreads();
     };
-    for (uint32_t sb = 0; sb < nsb; sb += NB) {
-        step(std::integral_constant<int, 0>{}, sb);
-        if (sb + 1 < nsb) step(std::integral_constant<int, 1>{}, sb + 1);
+    for (uint32_t st = 0; st < nst; st += NB) {
+        step(std::integral_constant<int, 0>{}, st);
+        if (st + 1 < nst) step(std::integral_constant<int, 1>{}, st + 1);
         if constexpr (NB == 3)
-            if (sb + 2 < nsb) step(std::integral_constant<int, 2>{}, sb + 2);
+            if (st + 2 < nst) step(std::integral_constant<int, 2>{}, st + 2);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): no direct load still writing the ring
+
+    if constexpr (KS > 1) {
+        // Slices 1.. leave their tiles in the (now idle) ring; slice 0 adds them in order.
+        float *red = reinterpret_cast<float *>(&ring0[0]);
+        static_assert((KS - 1) * NW * TT * 16 * 64 * 4 <= KS * sizeof(Slot), "reduction space");
+        __syncthreads();
+        if (ks > 0) {
+#pragma unroll
+            for (int t = 0; t < TT; t++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) red[((((ks - 1) * NW + wave) * TT + t) * 16 + v) * 64 + lane] = acc[t][v];
+        }
+        __syncthreads();
+        if (ks > 0) return;
+#pragma unroll
+        for (int k = 1; k < KS; k++)
+#pragma unroll
+            for (int t = 0; t < TT; t++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) acc[t][v] += red[((((k - 1) * NW + wave) * TT + t) * 16 + v) * 64 + lane];
     }
 
     // ---- store: y[token][row], bias, accumulate ----
@@ -616,15 +645,15 @@ static hipError_t launch_mm2_reg(const Mm2Args &a0, hipStream_t s) {
     return hipGetLastError();
 }
 
-template <int NW, int TT, int NB>
+template <int NW, int TT, int NB, int KS = 1>
 static hipError_t launch_mm2_cfg(const Mm2Args &a0, hipStream_t s) {
-    const mm2_kernel_t k = mm2_q4k_kernel<NW, TT, NB>;
-    static_assert(NB * sizeof(Q2Slot<32 * TT, NW>) <= 160 * 1024, "LDS");
+    const mm2_kernel_t k = mm2_q4k_kernel<NW, TT, NB, KS>;
+    static_assert(NB * KS * sizeof(Q2Slot<32 * TT, NW>) <= 160 * 1024, "LDS");
     constexpr size_t lds = 0; // the ring is static
     Mm2Args a = a0;
     a.rblocks = (a.rows + 32 * NW - 1) / (32 * NW);
     a.tblocks = (a.n + 32 * TT - 1) / (32 * TT);
-    hipLaunchKernelGGL(k, dim3(a.rblocks * a.tblocks), dim3(NW * 64), lds, s, a);
+    hipLaunchKernelGGL(k, dim3(a.rblocks * a.tblocks), dim3(NW * KS * 64), lds, s, a);
     return hipGetLastError();
 }
 
@@ -648,10 +677,16 @@ hipError_t launch_mm2(int t, const uint8_t *w, uint32_t rows, uint32_t cols, con
     auto blocks = [&](uint32_t nw, uint32_t tt) {
         return ((rows + 32 * nw - 1) / (32 * nw)) * ((n + 32 * tt - 1) / (32 * tt));
     };
+    // Below that, K slices give the SIMDs a second wave (measured at 512 tokens: 4096x14336
+    // 104 -> 87 us with two slices, 1024x3072 16.8 -> 10.7 us with four).
+    const uint32_t nsb = cols / 256;
     if (blocks(8, 4) >= 192) return launch_mm2_reg<8, 4>(a, s);
-    if (blocks(4, 2) >= 160) return launch_mm2_cfg<4, 2, 2>(a, s);
-    if (blocks(4, 1) >= 256) return launch_mm2_cfg<4, 1, 2>(a, s);
-    if (blocks(2, 1) >= 256) return launch_mm2_cfg<2, 1, 3>(a, s);
+    if (blocks(4, 2) >= 160) return nsb >= 4 ? launch_mm2_cfg<4, 2, 2, 2>(a, s) : launch_mm2_cfg<4, 2, 2>(a, s);
+    if (blocks(2, 1) >= 128) {
+        if (nsb >= 8) return launch_mm2_cfg<2, 1, 2, 4>(a, s);
+        if (nsb >= 2) return launch_mm2_cfg<2, 1, 2, 2>(a, s);
+        return launch_mm2_cfg<2, 1, 3>(a, s);
+    }
     return launch_mm2_cfg<1, 1, 3>(a, s);
 }
 

@@ -252,10 +252,13 @@ def test_baseline_prefill_shapes(eng, torch_cuda, t, m, k):
     assert parity_err(got, want) <= PARITY_TOL
 
 
-@pytest.mark.parametrize("m,k,n,mode", [(12288, 256, 512, 0), (12000, 512, 520, 1)])
+@pytest.mark.parametrize("m,k,n,mode", [(12288, 256, 512, 0), (12000, 512, 520, 1),
+                                        (2000, 2304, 130, 1), (2048, 512, 128, 0), (2600, 1280, 520, 1)])
 def test_gemm_large_tile(eng, torch_cuda, m, k, n, mode):
-    """Shapes that select the Q4_K GEMM's 256-row x 128-token tile (at least 192 tiles): one
-    exact fit, one with ragged rows and tokens, bias and accumulate."""
+    """Shapes that select each Q4_K GEMM configuration: the 256-row x 128-token register tile (at
+    least 192 tiles), and the ring kernel split over 4 and 2 K slices (9 and 5 super-blocks, so
+    slices get unequal counts; 2 super-blocks over 2 slices); exact fits and ragged rows and
+    tokens with bias and accumulate."""
     t = F.Q4_K
     raw = synth.weights_np(t, m, k, seed=600 + m)
     x = synth.activations_np(n, k, seed=601, outliers=0.01)
