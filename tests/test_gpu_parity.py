@@ -252,6 +252,22 @@ def test_baseline_prefill_shapes(eng, torch_cuda, t, m, k):
     assert parity_err(got, want) <= PARITY_TOL
 
 
+@pytest.mark.parametrize("t,m,k,n,mode", [(F.IQ4_NL, 4000, 1280, 300, 1), (F.IQ4_NL, 9000, 512, 260, 0),
+                                          (F.Q6_K, 4100, 768, 100, 1), (F.Q8_0, 3000, 1024, 70, 1)])
+def test_gemm_configs_other_formats(eng, torch_cuda, t, m, k, n, mode):
+    """The Q6_K / Q8_0 / IQ4_NL GEMM's configurations: IQ4_NL split over two K slices (5
+    super-blocks) and its 256-row tile; ragged rows and tokens, bias, accumulate."""
+    raw = synth.weights_np(t, m, k, seed=1400 + m)
+    x = synth.activations_np(n, k, seed=1401, outliers=0.01)
+    bias = np.linspace(-1, 1, m).astype(np.float32) if mode else None
+    y0 = synth.activations_np(n, m, seed=1402) if mode else None
+    got = run(eng, torch_cuda, t, raw, m, k, x, path="gemm", bias=bias, mode=mode, y0=y0)
+    want = O.matmul(t, raw, m, k, x, n, bias=bias, threads=16)
+    if mode:
+        want = want + y0
+    assert parity_err(got, want) <= PARITY_TOL
+
+
 @pytest.mark.parametrize("m,k,n,mode", [(12288, 256, 512, 0), (12000, 512, 520, 1),
                                         (2000, 2304, 130, 1), (2048, 512, 128, 0), (2600, 1280, 520, 1)])
 def test_gemm_large_tile(eng, torch_cuda, m, k, n, mode):
