@@ -19,8 +19,10 @@ Also reported:
   prefill       GEMM at 512 tokens, in TOPS against the 5.0 POPS dense int8 MFMA peak: Q4_K at the
                 8B FFN shapes (14336x4096, 4096x14336) and the Qwen3-0.6B FFN shapes (3072x1024,
                 1024x3072), IQ4_NL 14336x4096 and Q6_K 4096x14336
-  extra         the decode step at batch 8 (config 4), and config 5's batch-1 matvecs (IQ4_NL
-                14336x4096, Q6_K 4096x14336) rotating over 12 matrices each
+  extra         the decode step at batch 8 (config 4); config 5's batch-1 matvecs (IQ4_NL
+                14336x4096, Q6_K 4096x14336) rotating over 12 matrices each; config 1 (the Q8_0
+                3072x1024 matvec, rotating over 160 copies); config 2 (a batch-1 decode step of a
+                Qwen3-0.6B-shaped decoder, tokens/s)
   measured_peaks  this GPU's dense int8 MFMA rate and HBM read rate from probe kernels
                 (hk_amd/csrc/peak.hip), quoted beside the published peaks the fractions use
   cpu_baseline  the oracle's restatement of hk's CPU kernels on the host cores, on a bounded
@@ -271,6 +273,55 @@ def main():
             for w_ in ws:
                 eng.free(w_)
         extra["matvec_batch1"] = mv
+
+        # Config 1: the Q8_0 3072x1024 matvec at batch 1 (f32 input quantized in-kernel), rotating
+        # over 160 copies (535 MB, past the Infinity Cache).
+        ws = [upload_synth(F.Q8_0, 3072, 1024, synth.seed_for(1, i)) for i in range(160)]
+        xv = torch.randn(1, 1024, device=dev)
+        yv = torch.empty(1, 3072, device=dev)
+
+        def rot1():
+            for w_ in ws:
+                eng.matvec_parts([w_], [yv], 1, x=xv)
+
+        us = time_graph(torch, eng, stream, rot1, 5, per_graph=1) / len(ws)
+        b1 = ws[0].file_bytes + 4 * 1024 + 4 * 3072
+        extra["config1_q8_0_matvec"] = dict(shape="3072x1024", avg_us=round(us, 2), gbs=round(b1 / (us * 1e-6) / 1e9, 1),
+                                            frac_hbm_peak=round(b1 / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4))
+        for w_ in ws:
+            eng.free(w_)
+
+        # Config 2: a batch-1 decode step through every linear layer of a Qwen3-0.6B-shaped decoder
+        # (28 x {q 2048x1024, k/v 1024x1024, o 1024x2048, gate/up 3072x1024, down 1024x3072} Q4_K +
+        # the 151936x1024 Q6_K lm_head), four fused launches per layer as in the 8B step.
+        qshapes = [("q", 2048, 1024), ("k", 1024, 1024), ("v", 1024, 1024), ("o", 1024, 2048),
+                   ("gate", 3072, 1024), ("up", 3072, 1024), ("down", 1024, 3072)]
+        qlayers = [{nm: upload_synth(F.Q4_K, r, c, synth.seed_for(2, li * 10 + i)) for i, (nm, r, c) in enumerate(qshapes)}
+                   for li in range(28)]
+        qhead = upload_synth(F.Q6_K, 151936, 1024, synth.seed_for(2, 999))
+        qx = {c: torch.randn(1, c, device=dev) for c in (1024, 2048, 3072)}
+        qo = {nm: torch.empty(1, r, device=dev) for nm, r, _ in qshapes}
+        qlog = torch.empty(1, 151936, device=dev)
+
+        def qstep():
+            for lw in qlayers:
+                eng.matvec_parts([lw["q"], lw["k"], lw["v"]], [qo["q"], qo["k"], qo["v"]], 1, x=qx[1024])
+                eng.matvec_parts([lw["o"]], [qo["o"]], 1, x=qx[2048])
+                eng.matvec_parts([lw["gate"], lw["up"]], [qo["gate"], qo["up"]], 1, x=qx[1024])
+                eng.matvec_parts([lw["down"]], [qo["down"]], 1, x=qx[3072])
+            eng.matvec_parts([qhead], [qlog], 1, x=qx[1024])
+
+        usq = time_graph(torch, eng, stream, qstep, max(5, args.steps // 2), per_graph=1)
+        qbytes = sum(m.file_bytes for lw in qlayers for m in lw.values()) + qhead.file_bytes
+        qbytes += 28 * 4 * (1024 + 2048 + 1024 + 3072 + sum(r for _, r, _ in qshapes)) + 4 * (1024 + 151936)
+        extra["config2_qwen3_0_6b_decode"] = dict(ms_per_step=round(usq / 1e3, 4), tokens_per_s=round(1e6 / usq, 1),
+                                                  step_bytes=qbytes, gbs=round(qbytes / (usq * 1e-6) / 1e9, 1),
+                                                  frac_hbm_peak=round(qbytes / (usq * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                                                  launches=4 * 28 + 1)
+        for lw in qlayers:
+            for m in lw.values():
+                eng.free(m)
+        eng.free(qhead)
         result["extra"] = extra
 
     # ---- this GPU's measured peaks, quoted beside the published ones (the fractions use those) ----
