@@ -1,4 +1,4 @@
-// Small-batch product for Q4_K (2..32 tokens) on the int8 MFMA units.
+// Small-batch product for Q4_K and Q6_K (4..32 tokens) on the int8 MFMA units.
 //
 // Between single-token decode and prefill the weights still dominate the bytes (each is used by
 // a handful of tokens), so this kernel streams them like the decode kernels, but multiplies them
@@ -13,6 +13,10 @@
 //    sh plane, the result is multiplied by 8, then the sl plane is added on top.
 //  * J: one v_mfma_f32_16x16x32_bf16 over exact bf16 integers: the mins against the tokens'
 //    bsum32 = 64*u + v (the activation buffer's k_ilmb plane), exact in f32 (|J| < 2^22).
+// Q6_K (kernelK with the 16-weight groups): y += da*d*I, I = sum_g sc_g * sum_{k in g} (q - 32)*a.
+// A lane's 16 weights of a chunk are one group, so the signed 8-bit scale folds into them as
+// three int8 digit planes, sc = 64*e2 + 8*e1 + e0 with digits in [-3, 4] (each (q - 32)*e in
+// [-128, 124]); one int32 chain ((P2 << 3) + P1 << 3) + P0 gives I exactly (as the prefill GEMM).
 //
 // Layout. A workgroup owns 16 rows of one part (fused products: up to 4 matrices reading the
 // same input, their row tiles numbered in sequence); its KS waves split the super-blocks and add
@@ -42,12 +46,15 @@ typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef unsigned short us2 __attribute__((ext_vector_type(2)));
 
 constexpr int SK_PARTS = 4;
-// Weight bytes of a super-block for RT row tiles of 16 (144 bytes a row), padded to whole 1-KB
-// direct loads.
-template <int RT> constexpr uint32_t sk_dma() { return (144 * 16 * RT + 1023) / 1024; }
+// Quant-plane bytes of a row's super-block, and the 1-KB direct loads of a super-block for RT row
+// tiles of 16 (Q6_K: 4 KB, of which 3328 bytes are the rows and 256 bytes after them the rows'
+// scale words).
+template <int T> constexpr uint32_t sk_rb() { return T == HKHIP_Q6_K ? 208 : 144; }
+template <int T, int RT> constexpr uint32_t sk_dma() { return T == HKHIP_Q6_K ? 4 : (144 * 16 * RT + 1023) / 1024; }
 
 struct SkPart {
     const uint8_t *w;
+    const uint8_t *ws; // Q6_K: the f16 scale plane
     float *y;
     const float *bias;
     uint32_t rows, tile0; // tile0: first row tile of the part in the launch
@@ -67,6 +74,22 @@ __device__ __forceinline__ uint32_t mul_bytes(uint32_t nib, uint32_t f2) {
 }
 
 __device__ __forceinline__ v4i ld16(const void *g) { return *reinterpret_cast<const v4i *>(g); }
+
+// Q6_K: bytes q (each in [0, 63]) times a digit e in [-3, 4], minus 32*e, per byte as a
+// two's-complement byte (even and odd bytes through packed 16-bit multiply-adds, interleaved back
+// by a byte permute); sc = 64*e2 + 8*e1 + e0 with digits in [-3, 4].
+__device__ __forceinline__ uint32_t plane4(uint32_t ev, uint32_t od, uint32_t m, uint32_t c) {
+    const us2 pe = __builtin_bit_cast(us2, ev) * __builtin_bit_cast(us2, m) + __builtin_bit_cast(us2, c);
+    const us2 po = __builtin_bit_cast(us2, od) * __builtin_bit_cast(us2, m) + __builtin_bit_cast(us2, c);
+    return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, po), __builtin_bit_cast(uint32_t, pe), 0x06020400u);
+}
+__device__ __forceinline__ void digits(int sc, int e[3]) {
+    e[0] = ((sc + 3) & 7) - 3;
+    const int r = (sc - e[0]) >> 3;
+    e[1] = ((r + 3) & 7) - 3;
+    e[2] = (r - e[1]) >> 3;
+}
+__device__ __forceinline__ uint32_t lo16x2(int v) { return (uint32_t(v) & 0xFFFFu) * 0x00010001u; }
 // s_waitcnt vmcnt(N), as assembly with a memory clobber so that no memory access (the LDS
 // reads of the slot just waited for, in particular) moves across it.
 template <int N> __device__ __forceinline__ void wait_vm() {
@@ -81,10 +104,12 @@ template <int NTT> struct SkAct {
     float da[NTT];
 };
 
-template <int NTT, int KS, int PF, int RT>
-__global__ __launch_bounds__(KS * 64) void mmsk_q4k_kernel(SkArgs a) {
-    constexpr uint32_t NDMA = sk_dma<RT>(), SLOT = 1024 * NDMA;
-    constexpr int OPS = NDMA + NTT * 6; // loads per super-block and wave
+template <int T, int NTT, int KS, int PF, int RT>
+__global__ __launch_bounds__(KS * 64) void mmsk_kernel(SkArgs a) {
+    constexpr bool q6 = T == HKHIP_Q6_K;
+    static_assert(!q6 || RT == 1, "Q6_K: one row tile per wave");
+    constexpr uint32_t RB = sk_rb<T>(), NDMA = sk_dma<T, RT>(), SLOT = 1024 * NDMA;
+    constexpr int OPS = NDMA + (q6 ? 1 : 0) + NTT * (q6 ? 5 : 6); // loads per super-block and wave
     __shared__ __attribute__((aligned(16))) uint8_t ring[KS][PF][SLOT];
     __shared__ v4f part[KS > 1 ? KS - 1 : 1][RT][NTT][64];
 
@@ -100,6 +125,7 @@ __global__ __launch_bounds__(KS * 64) void mmsk_q4k_kernel(SkArgs a) {
     for (int i = 1; i < SK_PARTS; i++)
         if (i < int(a.nparts) && blockIdx.x >= a.p[i].tile0) pi = i;
     const uint8_t *W = a.p[0].w;
+    const uint8_t *WS = a.p[0].ws;
     float *Y = a.p[0].y;
     const float *B = a.p[0].bias;
     uint32_t rows = a.p[0].rows, tile0 = a.p[0].tile0;
@@ -107,6 +133,7 @@ __global__ __launch_bounds__(KS * 64) void mmsk_q4k_kernel(SkArgs a) {
     for (int i = 1; i < SK_PARTS; i++) {
         if (pi == uint32_t(i)) {
             W = a.p[i].w;
+            WS = a.p[i].ws;
             Y = a.p[i].y;
             B = a.p[i].bias;
             rows = a.p[i].rows;
@@ -116,16 +143,19 @@ __global__ __launch_bounds__(KS * 64) void mmsk_q4k_kernel(SkArgs a) {
     const uint32_t r0 = (blockIdx.x - tile0) * 16 * RT;
     const uint32_t sb0 = nsb * wave / KS, sb1 = nsb * (wave + 1) / KS;
 
-    // Weight piece P = 64i + lane (16 bytes) of a super-block: byte 16*(P % 9) of row P / 9's
+    // Weight piece P = 64i + lane (16 bytes) of a super-block: byte 16*(P % PPR) of row P / PPR's
     // block; pieces past the last repeat it (they land in the slot's padding).
-    constexpr uint32_t NP = 144 * RT;
+    constexpr uint32_t PPR = RB / 16, NP = PPR * 16 * RT;
     uint32_t woff[NDMA];
 #pragma unroll
     for (uint32_t i = 0; i < NDMA; i++) {
         const uint32_t P = 64 * i + lane < NP ? 64 * i + lane : NP - 1;
-        const uint32_t row = r0 + P / 9 < rows ? r0 + P / 9 : rows - 1;
-        woff[i] = row * nsb * 144 + 16 * (P % 9);
+        const uint32_t row = r0 + P / PPR < rows ? r0 + P / PPR : rows - 1;
+        woff[i] = row * nsb * RB + 16 * (P % PPR);
     }
+    // Q6_K scales: lane L loads the aligned word holding row r0 + L % 16's f16 for the super-block.
+    const uint32_t srow = r0 + (lane & 15) < rows ? r0 + (lane & 15) : rows - 1;
+    const uint32_t sbase = srow * nsb;
     uint8_t (*const myring)[SLOT] = ring[wave];
 
     // Lanes of tokens past n read the last token's entries: the same addresses as its own lanes,
@@ -134,15 +164,16 @@ __global__ __launch_bounds__(KS * 64) void mmsk_q4k_kernel(SkArgs a) {
 #pragma unroll
     for (int tt = 0; tt < NTT; tt++) tp[tt] = 16 * tt + p < a.n ? p : a.n - 1 - 16 * tt;
     auto issue = [&](uint32_t sb, uint8_t *slot, SkAct<NTT> &x) {
-        const uint8_t *gw = W + uint64_t(sb) * 144;
+        const uint8_t *gw = W + uint64_t(sb) * RB;
 #pragma unroll
         for (uint32_t i = 0; i < NDMA; i++) load_lds16(gw + woff[i], slot + 1024 * i);
+        if constexpr (q6) load_lds4(WS + (((sbase + sb) >> 1) << 2), slot + 16 * RB);
 #pragma unroll
         for (int tt = 0; tt < NTT; tt++) {
             const uint8_t *ga = a.il + ((uint64_t(4 * sb) * a.tiles + tt) * 64 + 16 * g + tp[tt]) * 16;
 #pragma unroll
             for (int c = 0; c < 4; c++) x.a[tt][c] = ld16(ga + uint64_t(c) * a.tiles * 1024);
-            x.mb[tt] = ld16(a.ilmb + ((uint64_t(sb) * a.tiles + tt) * 2 + (g & 1)) * 256 + 16 * tp[tt]);
+            if constexpr (!q6) x.mb[tt] = ld16(a.ilmb + ((uint64_t(sb) * a.tiles + tt) * 2 + (g & 1)) * 256 + 16 * tp[tt]);
             x.da[tt] = a.ild[(uint64_t(sb) * a.tiles + tt) * 16 + tp[tt]];
         }
     };
@@ -153,6 +184,60 @@ __global__ __launch_bounds__(KS * 64) void mmsk_q4k_kernel(SkArgs a) {
 #pragma unroll
         for (int tt = 0; tt < NTT; tt++) acc[rt][tt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
+    auto compute6 = [&](const uint8_t *slot, const SkAct<NTT> &x, float keep, uint32_t sb) {
+        // Lane (row p, group g), chunk c: values 64c + 16g.. = group 4c + g of the super-block,
+        // i.e. ql bytes 64n + 32(g>>1) + 16(g&1).. (nibble c&1), qh bytes 128 + 32n + 16(g&1)..
+        // (bits 2(2(c&1) + (g>>1))), scale byte 192 + 8n + 4(c&1) + 2(g>>1) + (g&1), n = c >> 1.
+        const uint8_t *blk = slot + RB * p;
+        uint4 ql[2], qh[2];
+#pragma unroll
+        for (int n = 0; n < 2; n++) {
+            ql[n] = *reinterpret_cast<const uint4 *>(blk + 64 * n + 32 * (g >> 1) + 16 * (g & 1));
+            qh[n] = *reinterpret_cast<const uint4 *>(blk + 128 + 32 * n + 16 * (g & 1));
+        }
+        const uint4 scw = *reinterpret_cast<const uint4 *>(blk + 192);
+        const uint32_t scs[4] = {scw.x, scw.y, scw.z, scw.w};
+        const uint32_t dword = *reinterpret_cast<const uint32_t *>(slot + 16 * RB + 4 * p);
+        const float d = f16_bits_to_f32(((sbase + sb) & 1) ? dword >> 16 : dword & 0xFFFF);
+        v4i P[3][4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int n = c >> 1;
+            const uint32_t sidx = 8 * n + 4 * (c & 1) + 2 * (g >> 1) + (g & 1);
+            const int sc = int(int8_t((scs[sidx / 4] >> (8 * (sidx % 4))) & 0xFF));
+            int e[3];
+            digits(sc, e);
+            const uint32_t qs = 2 * (2 * (c & 1) + (g >> 1));
+            const uint32_t lw[4] = {ql[n].x, ql[n].y, ql[n].z, ql[n].w};
+            const uint32_t hw[4] = {qh[n].x, qh[n].y, qh[n].z, qh[n].w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t q = ((lw[i] >> (4 * (c & 1))) & 0x0F0F0F0Fu) | (((hw[i] >> qs) & 0x03030303u) << 4);
+                const uint32_t ev = q & 0x00FF00FFu, od = (q >> 8) & 0x00FF00FFu;
+#pragma unroll
+                for (int k = 0; k < 3; k++) P[k][c][i] = int(plane4(ev, od, lo16x2(e[k]), lo16x2(-32 * e[k])));
+            }
+        }
+        float dr[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) dr[i] = __shfl(d, int(4 * g + i));
+#pragma unroll
+        for (int tt = 0; tt < NTT; tt++) {
+            v4i s = {0, 0, 0, 0};
+#pragma unroll
+            for (int c = 0; c < 4; c++) s = __builtin_amdgcn_mfma_i32_16x16x64_i8(P[2][c], x.a[tt][c], s, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++) s[i] <<= 3;
+#pragma unroll
+            for (int c = 0; c < 4; c++) s = __builtin_amdgcn_mfma_i32_16x16x64_i8(P[1][c], x.a[tt][c], s, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++) s[i] <<= 3;
+#pragma unroll
+            for (int c = 0; c < 4; c++) s = __builtin_amdgcn_mfma_i32_16x16x64_i8(P[0][c], x.a[tt][c], s, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[0][tt][i] = fmaf((float)s[i], dr[i] * (x.da[tt] * keep), acc[0][tt][i]);
+        }
+    };
     auto compute = [&](const uint8_t *slot, const SkAct<NTT> &x, float keep) {
 #pragma unroll
       for (int rt = 0; rt < RT; rt++) {
@@ -231,7 +316,10 @@ __global__ __launch_bounds__(KS * 64) void mmsk_q4k_kernel(SkArgs a) {
                 const uint32_t nx = sb + i + PF - 1;
                 issue(nx < last ? nx : last, myring[(i + PF - 1) % PF], x[(i + PF - 1) % PF]);
                 wait_vm<OPS * (PF - 1)>();
-                compute(myring[i], x[i], sb + i <= last ? 1.0f : 0.0f);
+                if constexpr (q6)
+                    compute6(myring[i], x[i], sb + i <= last ? 1.0f : 0.0f, sb + i <= last ? sb + i : last);
+                else
+                    compute(myring[i], x[i], sb + i <= last ? 1.0f : 0.0f);
             }
         }
         wait_vm<0>(); // nothing in flight past the loop
@@ -283,12 +371,12 @@ typedef void (*sk_kernel_t)(SkArgs);
 
 // At most 4 waves with two row tiles each (the LDS ring of 8 would not fit).
 template <int RT> constexpr uint32_t sk_max_ks() { return RT > 1 ? 4 : 8; }
-template <int NTT, int PF, int RT> sk_kernel_t sk_pick(uint32_t ks) {
+template <int T, int NTT, int PF, int RT> sk_kernel_t sk_pick(uint32_t ks) {
     if constexpr (sk_max_ks<RT>() >= 8)
-        if (ks == 8) return mmsk_q4k_kernel<NTT, 8, PF, RT>;
-    return ks == 1 ? mmsk_q4k_kernel<NTT, 1, PF, RT>
-         : ks == 2 ? mmsk_q4k_kernel<NTT, 2, PF, RT>
-                   : mmsk_q4k_kernel<NTT, 4, PF, RT>;
+        if (ks == 8) return mmsk_kernel<T, NTT, 8, PF, RT>;
+    return ks == 1 ? mmsk_kernel<T, NTT, 1, PF, RT>
+         : ks == 2 ? mmsk_kernel<T, NTT, 2, PF, RT>
+                   : mmsk_kernel<T, NTT, 4, PF, RT>;
 }
 
 } // namespace sk
@@ -301,8 +389,9 @@ using sk::sk_max_ks;
 using sk::SK_PARTS;
 
 bool mmsk_supports(int t, uint32_t rows, uint32_t cols, uint32_t n) {
-    return t == HKHIP_Q4_K && cols % 256 == 0 && rows > 0 && n >= 1 && n <= SK_MAX_TOKENS &&
-           uint64_t(rows) * (cols / 256) * 144 < (1ull << 32);
+    // 32-bit per-lane offsets into the quant plane (and, Q6_K, the scale plane after it).
+    return (t == HKHIP_Q4_K || t == HKHIP_Q6_K) && cols % 256 == 0 && rows > 0 && n >= 1 && n <= SK_MAX_TOKENS &&
+           weight_layout(t, rows, cols).total < (1ull << 32);
 }
 
 hipError_t launch_mmsk_parts(int t, const MvPartDesc *parts, int nparts, uint32_t cols, const uint8_t *xq,
@@ -318,7 +407,8 @@ hipError_t launch_mmsk_parts(int t, const MvPartDesc *parts, int nparts, uint32_
     SkArgs a{};
     uint32_t tiles = 0;
     for (int i = 0; i < nparts; i++) {
-        a.p[i] = SkPart{parts[i].w, parts[i].y, parts[i].bias, parts[i].rows, tiles};
+        a.p[i] = SkPart{parts[i].w, parts[i].w + weight_layout(t, parts[i].rows, cols).scale_off, parts[i].y,
+                        parts[i].bias, parts[i].rows, tiles};
         tiles += (parts[i].rows + 16 * RT - 1) / (16 * RT);
     }
     for (int i = nparts; i < SK_PARTS; i++) a.p[i].tile0 = 0xffffffffu;
@@ -335,7 +425,8 @@ hipError_t launch_mmsk_parts(int t, const MvPartDesc *parts, int nparts, uint32_
     const uint32_t nsb = cols / 256;
     uint32_t ks = 1;
     while (ks < sk_max_ks<RT>() && tiles * ks * 2 <= 2048 && nsb / (2 * ks) >= 4) ks *= 2;
-    const sk_kernel_t k = A.tiles == 1 ? sk_pick<1, 4, RT>(ks) : sk_pick<2, 3, RT>(ks);
+    const sk_kernel_t k = t == HKHIP_Q6_K ? (A.tiles == 1 ? sk_pick<HKHIP_Q6_K, 1, 4, RT>(ks) : sk_pick<HKHIP_Q6_K, 2, 3, RT>(ks))
+                                          : (A.tiles == 1 ? sk_pick<HKHIP_Q4_K, 1, 4, RT>(ks) : sk_pick<HKHIP_Q4_K, 2, 3, RT>(ks));
     hipLaunchKernelGGL(k, dim3(tiles), dim3(ks * 64), 0, s, a);
     return hipGetLastError();
 }

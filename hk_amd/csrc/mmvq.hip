@@ -1235,7 +1235,7 @@ hipError_t launch_mmvq_parts(int t, const MvPartDesc *parts, int nparts, uint32_
                              const uint8_t *xq, uint32_t n, int mode, hipStream_t s) {
     if (n < 1 || nparts < 1 || nparts > MV_PARTS) return hipErrorInvalidValue;
     const bool kq = (t == HKHIP_Q4_K || t == HKHIP_Q6_K);
-    // Q4_K from 4 tokens with a prepared input: the small-batch MFMA kernel (it needs the
+    // Q4_K and Q6_K from 4 tokens with a prepared input: the small-batch MFMA kernel (it needs the
     // quantizer's token-interleaved planes, so not for an f32 input).
     if (!x && n >= SK_MIN_TOKENS) {
         bool sk = true;
