@@ -484,3 +484,47 @@ def test_silu_mul_rejects(eng, torch_cuda):
     torch.cuda.synchronize()
     eng.free(odd)
     eng.free(even)
+
+
+# ---------------------------------------------------------------------------------------- full-size prefill
+
+@pytest.mark.parametrize("t,m,k", [(F.Q4_K, 14336, 4096), (F.Q4_K, 4096, 14336), (F.IQ4_NL, 14336, 4096),
+                                   (F.Q6_K, 4096, 14336), (F.Q8_0, 14336, 4096)])
+def test_full_size_prefill_rows(eng, torch_cuda, t, m, k):
+    """The BASELINE 8B FFN prefill GEMMs (512 tokens) at full size. Each output row depends only
+    on its weight row, so the oracle is run on a sample of rows -- the first and last, rows at the
+    kernels' 16/32/128/256-row tile edges and random ones -- against all 512 tokens."""
+    n = 512
+    raw = synth.weights_np(t, m, k, seed=1500 + t)
+    x = synth.activations_np(n, k, seed=1501, outliers=0.01)
+    got = run(eng, torch_cuda, t, raw, m, k, x, path="mm")
+    rng = np.random.default_rng(1502)
+    edges = [0, 1, 15, 16, 31, 32, 127, 128, 255, 256, m // 2, m - 257, m - 33, m - 2, m - 1]
+    rows = np.unique(np.concatenate([np.array(edges), rng.integers(0, m, 33)]))
+    want = O.matmul(t, raw[rows], len(rows), k, x, n, threads=16)
+    assert parity_err(got[:, rows], want) <= PARITY_TOL
+
+
+@pytest.mark.parametrize("t,m,k", [(F.Q4_K, 14336, 4096), (F.Q4_K, 4096, 14336), (F.Q6_K, 128256, 4096)])
+def test_full_size_batch8_rows(eng, torch_cuda, t, m, k):
+    """The batch-8 decode products of config 4 at full size (the small-batch kernel on a prepared
+    input), the 128256-row Q6_K lm_head included; a sample of rows against the oracle."""
+    torch = torch_cuda
+    n = 8
+    raw = synth.weights_np(t, m, k, seed=1600 + t)
+    x = synth.activations_np(n, k, seed=1601)
+    w = eng.upload(raw, t, m, k)
+    xd = torch.from_numpy(x).cuda()
+    xq = torch.empty(eng.act_bytes(n, k), dtype=torch.uint8, device="cuda")
+    eng.qact(xd, n, k, F.ACT_KIND[t], xq)
+    y = torch.full((n, m), float("nan"), device="cuda")
+    eng.matvec_parts([w], [y], n, xq=xq)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    eng.free(w)
+    rng = np.random.default_rng(1602)
+    rows = np.unique(np.concatenate([np.array([0, 1, 15, 16, 17, m // 2, m - 17, m - 16, m - 1]),
+                                     rng.integers(0, m, 55)]))
+    want = O.matmul(t, raw[rows], len(rows), k, x, n, threads=16)
+    assert parity_err(got[:, rows], want) <= PARITY_TOL
+    assert np.isfinite(got).all()
