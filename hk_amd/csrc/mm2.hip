@@ -315,25 +315,18 @@ __global__ __launch_bounds__(Q2_NW * 64, 2) void mm2_q4k_reg_kernel(Mm2Args a) {
             for (int s = 0; s < 8; s++)
                 av[s] = *reinterpret_cast<const v4i *>(abase + 32 * t * 256 + 16 * ((2 * s + h) ^ sw));
         };
-#ifndef MM2_NO_PREFETCH
         load_a(0);
-#endif
 #pragma unroll
         for (int t = 0; t < Q2_TT; t++) {
             // One accumulator: the sh-plane chain, times 8, then the sl-plane chain on top.
             v16i sacc = {};
-#ifdef MM2_NO_PREFETCH
-            load_a(t);
-#endif
 #pragma unroll
             for (int s = 0; s < 8; s++) sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[s], bhi[s], sacc, 0, 0, 0);
 #pragma unroll
             for (int v = 0; v < 16; v++) sacc[v] <<= 3;
 #pragma unroll
             for (int s = 0; s < 8; s++) sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[s], blo[s], sacc, 0, 0, 0);
-#ifndef MM2_NO_PREFETCH
             if (t + 1 < Q2_TT) load_a(t + 1);
-#endif
             if (t == (Q2_TT > 1 ? 1 : 0)) wload(nx); // next super-block's weights, once this one's raw words are dead
             // Token scales of this lane's 16 outputs: tokens 32t + 8g + 4h + (0..3).
             const float4 *dap = reinterpret_cast<const float4 *>(&S.da[buf][32 * t + 4 * h]);
