@@ -61,7 +61,7 @@ inline WLayout weight_layout(int t, uint32_t rows, uint32_t cols) {
         L.total = L.quant_bytes;
     } else {
         L.scale_off = align256(L.quant_bytes);
-        L.total = L.scale_off + nb * 2;
+        L.total = align256(L.scale_off + nb * 2); // the kernels read the scales as aligned words
     }
     return L;
 }
