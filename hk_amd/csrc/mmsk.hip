@@ -104,6 +104,168 @@ template <int NTT> struct SkAct {
     float da[NTT];
 };
 
+// One super-block of a 16-row tile against the token tiles of x (Q6_K). `slot` holds the rows'
+// 208-byte blocks and, 3328 bytes in, the aligned words of their f16 scales; dodd picks the word's
+// half.
+template <int NTT>
+__device__ __forceinline__ void sk_step_q6k(const uint8_t *slot, const SkAct<NTT> &x, float keep, uint32_t g,
+                                            uint32_t p, uint32_t dodd, v4f (&acc)[1][NTT]) {
+    // Lane (row p, group g), chunk c: values 64c + 16g.. = group 4c + g of the super-block,
+    // i.e. ql bytes 64n + 32(g>>1) + 16(g&1).. (nibble c&1), qh bytes 128 + 32n + 16(g&1)..
+    // (bits 2(2(c&1) + (g>>1))), scale byte 192 + 8n + 4(c&1) + 2(g>>1) + (g&1), n = c >> 1.
+    const uint8_t *blk = slot + 208 * p;
+    uint4 ql[2], qh[2];
+#pragma unroll
+    for (int n = 0; n < 2; n++) {
+        ql[n] = *reinterpret_cast<const uint4 *>(blk + 64 * n + 32 * (g >> 1) + 16 * (g & 1));
+        qh[n] = *reinterpret_cast<const uint4 *>(blk + 128 + 32 * n + 16 * (g & 1));
+    }
+    const uint4 scw = *reinterpret_cast<const uint4 *>(blk + 192);
+    const uint32_t scs[4] = {scw.x, scw.y, scw.z, scw.w};
+    const uint32_t dword = *reinterpret_cast<const uint32_t *>(slot + 16 * 208 + 4 * p);
+    const float d = f16_bits_to_f32(dodd ? dword >> 16 : dword & 0xFFFF);
+    v4i P[3][4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const int n = c >> 1;
+        const uint32_t sidx = 8 * n + 4 * (c & 1) + 2 * (g >> 1) + (g & 1);
+        const int sc = int(int8_t((scs[sidx / 4] >> (8 * (sidx % 4))) & 0xFF));
+        int e[3];
+        digits(sc, e);
+        const uint32_t qs = 2 * (2 * (c & 1) + (g >> 1));
+        const uint32_t lw[4] = {ql[n].x, ql[n].y, ql[n].z, ql[n].w};
+        const uint32_t hw[4] = {qh[n].x, qh[n].y, qh[n].z, qh[n].w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t q = ((lw[i] >> (4 * (c & 1))) & 0x0F0F0F0Fu) | (((hw[i] >> qs) & 0x03030303u) << 4);
+            const uint32_t ev = q & 0x00FF00FFu, od = (q >> 8) & 0x00FF00FFu;
+#pragma unroll
+            for (int k = 0; k < 3; k++) P[k][c][i] = int(plane4(ev, od, lo16x2(e[k]), lo16x2(-32 * e[k])));
+        }
+    }
+    float dr[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) dr[i] = __shfl(d, int(4 * g + i));
+#pragma unroll
+    for (int tt = 0; tt < NTT; tt++) {
+        v4i s = {0, 0, 0, 0};
+#pragma unroll
+        for (int c = 0; c < 4; c++) s = __builtin_amdgcn_mfma_i32_16x16x64_i8(P[2][c], x.a[tt][c], s, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) s[i] <<= 3;
+#pragma unroll
+        for (int c = 0; c < 4; c++) s = __builtin_amdgcn_mfma_i32_16x16x64_i8(P[1][c], x.a[tt][c], s, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) s[i] <<= 3;
+#pragma unroll
+        for (int c = 0; c < 4; c++) s = __builtin_amdgcn_mfma_i32_16x16x64_i8(P[0][c], x.a[tt][c], s, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[0][tt][i] = fmaf((float)s[i], dr[i] * (x.da[tt] * keep), acc[0][tt][i]);
+    }
+}
+
+// One super-block of RT 16-row tiles against the token tiles of x (Q4_K); `slot` holds the rows'
+// 144-byte blocks.
+template <int NTT, int RT>
+__device__ __forceinline__ void sk_step_q4k(const uint8_t *slot, const SkAct<NTT> &x, float keep, uint32_t g,
+                                            uint32_t p, v4f (&acc)[RT][NTT]) {
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) {
+        const uint8_t *blk = slot + 144 * (16 * rt + p);
+        const uint4 h = *reinterpret_cast<const uint4 *>(blk);
+        uint4 q[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) q[c] = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * c + 16 * (g & 1));
+        const uint32_t k1 = 0x3f3f3f3fu, k2 = 0x0f0f0f0fu, k3 = 0x03030303u;
+        const uint32_t scl = h.y & k1, mnl = h.z & k1;
+        const uint32_t sch = (h.w & k2) | (((h.y >> 6) & k3) << 4);
+        const uint32_t mnh = ((h.w >> 4) & k2) | (((h.z >> 6) & k3) << 4);
+        const float d = f16_bits_to_f32(h.x & 0xFFFF), ndmin = -f16_bits_to_f32(h.x >> 16);
+        // Planes of the four chunks: chunk c, lane group g is sub-block 2c + g/2 (low nibbles for
+        // g < 2, high for g >= 2).
+        v4i ph[4], pl[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const uint32_t sc = ((c < 2 ? scl : sch) >> (8 * (2 * (c & 1) + (g >> 1)))) & 0xFF;
+            const uint32_t fh = (sc >> 3) * 0x00010001u, fl = (sc & 7) * 0x00010001u;
+            const uint32_t sh = 4 * (g >> 1);
+            const uint32_t w4[4] = {q[c].x, q[c].y, q[c].z, q[c].w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t nib = (w4[i] >> sh) & 0x0F0F0F0Fu;
+                ph[c][i] = int(mul_bytes(nib, fh));
+                pl[c][i] = int(mul_bytes(nib, fl));
+            }
+        }
+        // Min-term A operand: the 8 mins as bf16 integers in lane groups 0 and 1, zero in 2, 3.
+        uint32_t mw[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t src = i < 2 ? mnl : mnh, s = 16 * (i & 1);
+            const float e = (float)((src >> s) & 0xFF), o = (float)((src >> (s + 8)) & 0xFF);
+            mw[i] = g < 2 ? (__builtin_bit_cast(uint32_t, e) >> 16) | (__builtin_bit_cast(uint32_t, o) & 0xFFFF0000u) : 0u;
+        }
+        const v8bf am = __builtin_bit_cast(v8bf, make_uint4(mw[0], mw[1], mw[2], mw[3]));
+        // Scales of this lane's output rows 4*(lane/16) + i, from the lanes that read them.
+        float dr[4], mr[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            dr[i] = __shfl(d, int(4 * g + i));
+            mr[i] = __shfl(ndmin, int(4 * g + i));
+        }
+#pragma unroll
+        for (int tt = 0; tt < NTT; tt++) {
+            v4i s = {0, 0, 0, 0};
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                s = __builtin_amdgcn_mfma_i32_16x16x64_i8(ph[c], x.a[tt][c], s, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++) s[i] <<= 3;
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                s = __builtin_amdgcn_mfma_i32_16x16x64_i8(pl[c], x.a[tt][c], s, 0, 0, 0);
+            const v4i mbw = g < 2 ? x.mb[tt] : v4i{0, 0, 0, 0};
+            const v4f j = __builtin_amdgcn_mfma_f32_16x16x32_bf16(am, __builtin_bit_cast(v8bf, mbw), v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[rt][tt][i] = fmaf(fmaf((float)s[i], dr[i], mr[i] * j[i]), x.da[tt] * keep, acc[rt][tt][i]);
+        }
+    }
+}
+
+// Stores the tiles of one wave: output lane l holds rows 4*(l/16) + i of token l % 16.
+template <int NTT, int RT>
+__device__ __forceinline__ void sk_store(const v4f (&acc)[RT][NTT], uint32_t n, int mode, uint32_t r0, uint32_t rows,
+                                         float *Y, const float *B, uint32_t g, uint32_t p) {
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) {
+#pragma unroll
+        for (int tt = 0; tt < NTT; tt++) {
+            const uint32_t tok = 16 * tt + p;
+            if (tok < n && mode == HKHIP_SILU_MUL) {
+                // Rows 4g + i of the tile: gate/up pairs (i = 0, 1) and (2, 3).
+#pragma unroll
+                for (int i = 0; i < 4; i += 2) {
+                    const uint32_t r = r0 + 16 * rt + 4 * g + i;
+                    if (r < rows) Y[uint64_t(tok) * (rows / 2) + r / 2] = silu_mul(acc[rt][tt][i], acc[rt][tt][i + 1]);
+                }
+            } else if (tok < n) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const uint32_t r = r0 + 16 * rt + 4 * g + i;
+                    if (r < rows) {
+                        float *dst = Y + uint64_t(tok) * rows + r;
+                        const float v = acc[rt][tt][i] + (B ? B[r] : 0.0f);
+                        if (mode == HKHIP_ACCUMULATE)
+                            *dst += v;
+                        else
+                            *dst = v;
+                    }
+                }
+            }
+        }
+    }
+}
+
 template <int T, int NTT, int KS, int PF, int RT>
 __global__ __launch_bounds__(KS * 64) void mmsk_kernel(SkArgs a) {
     constexpr bool q6 = T == HKHIP_Q6_K;
@@ -184,124 +346,6 @@ __global__ __launch_bounds__(KS * 64) void mmsk_kernel(SkArgs a) {
 #pragma unroll
         for (int tt = 0; tt < NTT; tt++) acc[rt][tt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
-    auto compute6 = [&](const uint8_t *slot, const SkAct<NTT> &x, float keep, uint32_t sb) {
-        // Lane (row p, group g), chunk c: values 64c + 16g.. = group 4c + g of the super-block,
-        // i.e. ql bytes 64n + 32(g>>1) + 16(g&1).. (nibble c&1), qh bytes 128 + 32n + 16(g&1)..
-        // (bits 2(2(c&1) + (g>>1))), scale byte 192 + 8n + 4(c&1) + 2(g>>1) + (g&1), n = c >> 1.
-        const uint8_t *blk = slot + RB * p;
-        uint4 ql[2], qh[2];
-#pragma unroll
-        for (int n = 0; n < 2; n++) {
-            ql[n] = *reinterpret_cast<const uint4 *>(blk + 64 * n + 32 * (g >> 1) + 16 * (g & 1));
-            qh[n] = *reinterpret_cast<const uint4 *>(blk + 128 + 32 * n + 16 * (g & 1));
-        }
-        const uint4 scw = *reinterpret_cast<const uint4 *>(blk + 192);
-        const uint32_t scs[4] = {scw.x, scw.y, scw.z, scw.w};
-        const uint32_t dword = *reinterpret_cast<const uint32_t *>(slot + 16 * RB + 4 * p);
-        const float d = f16_bits_to_f32(((sbase + sb) & 1) ? dword >> 16 : dword & 0xFFFF);
-        v4i P[3][4];
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const int n = c >> 1;
-            const uint32_t sidx = 8 * n + 4 * (c & 1) + 2 * (g >> 1) + (g & 1);
-            const int sc = int(int8_t((scs[sidx / 4] >> (8 * (sidx % 4))) & 0xFF));
-            int e[3];
-            digits(sc, e);
-            const uint32_t qs = 2 * (2 * (c & 1) + (g >> 1));
-            const uint32_t lw[4] = {ql[n].x, ql[n].y, ql[n].z, ql[n].w};
-            const uint32_t hw[4] = {qh[n].x, qh[n].y, qh[n].z, qh[n].w};
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t q = ((lw[i] >> (4 * (c & 1))) & 0x0F0F0F0Fu) | (((hw[i] >> qs) & 0x03030303u) << 4);
-                const uint32_t ev = q & 0x00FF00FFu, od = (q >> 8) & 0x00FF00FFu;
-#pragma unroll
-                for (int k = 0; k < 3; k++) P[k][c][i] = int(plane4(ev, od, lo16x2(e[k]), lo16x2(-32 * e[k])));
-            }
-        }
-        float dr[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) dr[i] = __shfl(d, int(4 * g + i));
-#pragma unroll
-        for (int tt = 0; tt < NTT; tt++) {
-            v4i s = {0, 0, 0, 0};
-#pragma unroll
-            for (int c = 0; c < 4; c++) s = __builtin_amdgcn_mfma_i32_16x16x64_i8(P[2][c], x.a[tt][c], s, 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 4; i++) s[i] <<= 3;
-#pragma unroll
-            for (int c = 0; c < 4; c++) s = __builtin_amdgcn_mfma_i32_16x16x64_i8(P[1][c], x.a[tt][c], s, 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 4; i++) s[i] <<= 3;
-#pragma unroll
-            for (int c = 0; c < 4; c++) s = __builtin_amdgcn_mfma_i32_16x16x64_i8(P[0][c], x.a[tt][c], s, 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 4; i++) acc[0][tt][i] = fmaf((float)s[i], dr[i] * (x.da[tt] * keep), acc[0][tt][i]);
-        }
-    };
-    auto compute = [&](const uint8_t *slot, const SkAct<NTT> &x, float keep) {
-#pragma unroll
-      for (int rt = 0; rt < RT; rt++) {
-        const uint8_t *blk = slot + 144 * (16 * rt + p);
-        const uint4 h = *reinterpret_cast<const uint4 *>(blk);
-        uint4 q[4];
-#pragma unroll
-        for (int c = 0; c < 4; c++) q[c] = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * c + 16 * (g & 1));
-        const uint32_t k1 = 0x3f3f3f3fu, k2 = 0x0f0f0f0fu, k3 = 0x03030303u;
-        const uint32_t scl = h.y & k1, mnl = h.z & k1;
-        const uint32_t sch = (h.w & k2) | (((h.y >> 6) & k3) << 4);
-        const uint32_t mnh = ((h.w >> 4) & k2) | (((h.z >> 6) & k3) << 4);
-        const float d = f16_bits_to_f32(h.x & 0xFFFF), ndmin = -f16_bits_to_f32(h.x >> 16);
-        // Planes of the four chunks: chunk c, lane group g is sub-block 2c + g/2 (low nibbles for
-        // g < 2, high for g >= 2).
-        v4i ph[4], pl[4];
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const uint32_t sc = ((c < 2 ? scl : sch) >> (8 * (2 * (c & 1) + (g >> 1)))) & 0xFF;
-            const uint32_t fh = (sc >> 3) * 0x00010001u, fl = (sc & 7) * 0x00010001u;
-            const uint32_t sh = 4 * (g >> 1);
-            const uint32_t w4[4] = {q[c].x, q[c].y, q[c].z, q[c].w};
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t nib = (w4[i] >> sh) & 0x0F0F0F0Fu;
-                ph[c][i] = int(mul_bytes(nib, fh));
-                pl[c][i] = int(mul_bytes(nib, fl));
-            }
-        }
-        // Min-term A operand: the 8 mins as bf16 integers in lane groups 0 and 1, zero in 2, 3.
-        uint32_t mw[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t src = i < 2 ? mnl : mnh, s = 16 * (i & 1);
-            const float e = (float)((src >> s) & 0xFF), o = (float)((src >> (s + 8)) & 0xFF);
-            mw[i] = g < 2 ? (__builtin_bit_cast(uint32_t, e) >> 16) | (__builtin_bit_cast(uint32_t, o) & 0xFFFF0000u) : 0u;
-        }
-        const v8bf am = __builtin_bit_cast(v8bf, make_uint4(mw[0], mw[1], mw[2], mw[3]));
-        // Scales of this lane's output rows 4*(lane/16) + i, from the lanes that read them.
-        float dr[4], mr[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            dr[i] = __shfl(d, int(4 * g + i));
-            mr[i] = __shfl(ndmin, int(4 * g + i));
-        }
-#pragma unroll
-        for (int tt = 0; tt < NTT; tt++) {
-            v4i s = {0, 0, 0, 0};
-#pragma unroll
-            for (int c = 0; c < 4; c++)
-                s = __builtin_amdgcn_mfma_i32_16x16x64_i8(ph[c], x.a[tt][c], s, 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 4; i++) s[i] <<= 3;
-#pragma unroll
-            for (int c = 0; c < 4; c++)
-                s = __builtin_amdgcn_mfma_i32_16x16x64_i8(pl[c], x.a[tt][c], s, 0, 0, 0);
-            const v4i mbw = g < 2 ? x.mb[tt] : v4i{0, 0, 0, 0};
-            const v4f j = __builtin_amdgcn_mfma_f32_16x16x32_bf16(am, __builtin_bit_cast(v8bf, mbw), v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 4; i++) acc[rt][tt][i] = fmaf(fmaf((float)s[i], dr[i], mr[i] * j[i]), x.da[tt] * keep, acc[rt][tt][i]);
-        }
-      }
-    };
-
     if (sb0 < sb1) {
         SkAct<NTT> x[PF];
         const uint32_t last = sb1 - 1;
@@ -316,10 +360,11 @@ __global__ __launch_bounds__(KS * 64) void mmsk_kernel(SkArgs a) {
                 const uint32_t nx = sb + i + PF - 1;
                 issue(nx < last ? nx : last, myring[(i + PF - 1) % PF], x[(i + PF - 1) % PF]);
                 wait_vm<OPS * (PF - 1)>();
+                const float keep = sb + i <= last ? 1.0f : 0.0f;
                 if constexpr (q6)
-                    compute6(myring[i], x[i], sb + i <= last ? 1.0f : 0.0f, sb + i <= last ? sb + i : last);
+                    sk_step_q6k<NTT>(myring[i], x[i], keep, g, p, (sbase + (sb + i <= last ? sb + i : last)) & 1, acc);
                 else
-                    compute(myring[i], x[i], sb + i <= last ? 1.0f : 0.0f);
+                    sk_step_q4k<NTT, RT>(myring[i], x[i], keep, g, p, acc);
             }
         }
         wait_vm<0>(); // nothing in flight past the loop
@@ -335,35 +380,12 @@ __global__ __launch_bounds__(KS * 64) void mmsk_kernel(SkArgs a) {
     if (KS > 1) __syncthreads();
     if (wave == 0) {
 #pragma unroll
-        for (int rt = 0; rt < RT; rt++) {
+        for (int rt = 0; rt < RT; rt++)
 #pragma unroll
-            for (int tt = 0; tt < NTT; tt++) {
+            for (int tt = 0; tt < NTT; tt++)
 #pragma unroll
                 for (int w = 0; w < KS - 1; w++) acc[rt][tt] += part[w][rt][tt][lane];
-                const uint32_t tok = 16 * tt + p;
-                if (tok < a.n && a.mode == HKHIP_SILU_MUL) {
-                    // Rows 4g + i of the tile: gate/up pairs (i = 0, 1) and (2, 3).
-#pragma unroll
-                    for (int i = 0; i < 4; i += 2) {
-                        const uint32_t r = r0 + 16 * rt + 4 * g + i;
-                        if (r < rows) Y[uint64_t(tok) * (rows / 2) + r / 2] = silu_mul(acc[rt][tt][i], acc[rt][tt][i + 1]);
-                    }
-                } else if (tok < a.n) {
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const uint32_t r = r0 + 16 * rt + 4 * g + i;
-                        if (r < rows) {
-                            float *dst = Y + uint64_t(tok) * rows + r;
-                            const float v = acc[rt][tt][i] + (B ? B[r] : 0.0f);
-                            if (a.mode == HKHIP_ACCUMULATE)
-                                *dst += v;
-                            else
-                                *dst = v;
-                        }
-                    }
-                }
-            }
-        }
+        sk_store<NTT, RT>(acc, a.n, a.mode, r0, rows, Y, B, g, p);
     }
 }
 

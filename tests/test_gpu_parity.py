@@ -528,3 +528,39 @@ def test_full_size_batch8_rows(eng, torch_cuda, t, m, k):
     want = O.matmul(t, raw[rows], len(rows), k, x, n, threads=16)
     assert parity_err(got[:, rows], want) <= PARITY_TOL
     assert np.isfinite(got).all()
+
+
+@pytest.mark.parametrize("t", [F.Q4_K, F.Q6_K])
+@pytest.mark.parametrize("n,mode", [(5, 0), (20, 1), (8, 2)])
+def test_small_batch_many_tiles(eng, torch_cuda, t, n, mode):
+    """The small-batch kernel over two fused parts with ragged heights (over 1000 row tiles), one
+    or two token tiles, bias and accumulate, and silu(gate)*up."""
+    torch = torch_cuda
+    k = 512
+    heights = [9000, 7778] if mode == 2 else [9000, 7777]
+    raws = [synth.weights_np(t, m, k, seed=1700 + i + t) for i, m in enumerate(heights)]
+    x = synth.activations_np(n, k, seed=1701 + n, outliers=0.01)
+    mats = [eng.upload(r, t, m, k) for r, m in zip(raws, heights)]
+    cols = [m // 2 if mode == 2 else m for m in heights]
+    y0s = [synth.activations_np(n, c, seed=1702 + c) for c in cols]
+    ys = [torch.from_numpy(y0.copy()).cuda() if mode == 1 else torch.full((n, c), float("nan"), device="cuda")
+          for y0, c in zip(y0s, cols)]
+    biases = [torch.from_numpy(np.linspace(-1, 1, m).astype(np.float32)).cuda() for m in heights] if mode != 2 else None
+    xq = torch.empty(eng.act_bytes(n, k), dtype=torch.uint8, device="cuda")
+    eng.qact(torch.from_numpy(x).cuda(), n, k, F.ACT_KIND[t], xq)
+    if n <= 8:
+        eng.matvec_parts(mats, ys, n, xq=xq, biases=biases, mode=mode)
+    else:
+        for w, y, b in zip(mats, ys, biases):
+            eng.mm(w, xq, y, n, bias=b, mode=mode)
+    torch.cuda.synchronize()
+    for i, (r, m) in enumerate(zip(raws, heights)):
+        b = biases[i].cpu().numpy() if biases else None
+        want = O.matmul(t, r, m, k, x, n, bias=b, tiled=False)
+        if mode == 1:
+            want = want + y0s[i]
+        if mode == 2:
+            want = silu_mul_ref(want)
+        assert parity_err(ys[i].cpu().numpy(), want) <= PARITY_TOL
+    for w in mats:
+        eng.free(w)
