@@ -448,8 +448,24 @@ def cpu_baseline(seconds: float):
         reps += 1
     dt = (time.perf_counter() - t0) / reps
     nbytes = raw.nbytes + 4 * k + 4 * m
+    # The same product on one thread, for a figure comparable to hk-kernels' single-thread runs.
+    reps1, t1 = 0, time.perf_counter()
+    while time.perf_counter() - t1 < max(1.0, seconds / 4):
+        O.matmul(F.Q4_K, raw, m, k, x, 1, threads=1)
+        reps1 += 1
+    dt1 = (time.perf_counter() - t1) / reps1
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
     return {"value": round(nbytes / dt / 1e9, 2), "unit": "GB/s", "cores": cores, "kind": "port",
-            "sample": f"Q4_K 14336x4096 matvec, batch 1, {reps} reps in {seconds:.0f} s (OpenMP, scalar C)"}
+            "sample": f"Q4_K 14336x4096 matvec, batch 1, {reps} reps in {seconds:.0f} s (OpenMP, scalar C)",
+            "single_thread_value": round(nbytes / dt1 / 1e9, 2), "cpu_model": model}
 
 
 if __name__ == "__main__":
