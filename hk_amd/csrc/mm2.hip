@@ -35,6 +35,7 @@
 // l%32 and tokens 8*(v/4) + 4*(l/32) + v%4 for v < 16.
 
 #include "common.hpp"
+#include "gemm_store.hpp"
 
 #include <type_traits>
 
@@ -75,6 +76,7 @@ struct Mm2Args {
     float *y;
     const float *bias;
     int mode;
+    int wide; // y 16-byte aligned and rows a multiple of 4: whole tiles go out as 16-byte stores
     uint32_t rblocks, tblocks;
 };
 
@@ -349,22 +351,18 @@ __global__ __launch_bounds__(Q2_NW * 64, 2) void mm2_q4k_reg_kernel(Mm2Args a) {
         __syncthreads();
     }
 
-    // ---- store: y[token][row], bias, accumulate ----
-    if (myrow < a.rows) {
-        const float b = a.bias ? a.bias[myrow] : 0.0f;
+    // ---- store: y[token][row], bias, accumulate (the last step's barrier freed the LDS) ----
+    {
+        float *st = reinterpret_cast<float *>(smem_raw) + 1024 * wave;
+        const float b = (a.bias && myrow < a.rows) ? a.bias[myrow] : 0.0f;
+        const uint32_t rw0 = r0 + 32 * wave;
 #pragma unroll
         for (int t = 0; t < Q2_TT; t++) {
-#pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const uint32_t tok = t0 + 32 * t + 8 * (v / 4) + 4 * h + (v % 4);
-                if (tok < a.n) {
-                    float *dst = a.y + uint64_t(tok) * a.rows + myrow;
-                    if (a.mode == HKHIP_ACCUMULATE)
-                        *dst += acc[t][v] + b;
-                    else
-                        *dst = acc[t][v] + b;
-                }
-            }
+            const uint32_t tk0 = t0 + 32 * t;
+            if (a.wide && rw0 + 32 <= a.rows && tk0 + 32 <= a.n)
+                gemm_store_tile_wide(st, acc[t], b, a.y, a.rows, rw0, tk0, a.mode);
+            else
+                gemm_store_tile(acc[t], b, a.y, a.rows, a.n, myrow, tk0, a.mode);
         }
     }
 }
@@ -571,12 +569,12 @@ __global__ __launch_bounds__(NW * KS * 64, 2) void mm2_q4k_kernel(Mm2Args a) {
             if (st + 2 < nst) step(std::integral_constant<int, 2>{}, st + 2);
     }
     __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): no direct load still writing the ring
+    __syncthreads();                   // in any wave: the ring is free from here
 
     if constexpr (KS > 1) {
-        // Slices 1.. leave their tiles in the (now idle) ring; slice 0 adds them in order.
+        // Slices 1.. leave their tiles in the ring; slice 0 adds them in order.
         float *red = reinterpret_cast<float *>(&ring0[0]);
         static_assert((KS - 1) * NW * TT * 16 * 64 * 4 <= KS * sizeof(Slot), "reduction space");
-        __syncthreads();
         if (ks > 0) {
 #pragma unroll
             for (int t = 0; t < TT; t++)
@@ -584,31 +582,31 @@ __global__ __launch_bounds__(NW * KS * 64, 2) void mm2_q4k_kernel(Mm2Args a) {
                 for (int v = 0; v < 16; v++) red[((((ks - 1) * NW + wave) * TT + t) * 16 + v) * 64 + lane] = acc[t][v];
         }
         __syncthreads();
+        if (ks == 0) {
+#pragma unroll
+            for (int k = 1; k < KS; k++)
+#pragma unroll
+                for (int t = 0; t < TT; t++)
+#pragma unroll
+                    for (int v = 0; v < 16; v++) acc[t][v] += red[((((k - 1) * NW + wave) * TT + t) * 16 + v) * 64 + lane];
+        }
+        __syncthreads(); // the reduction area is read: the ring takes the output staging
         if (ks > 0) return;
-#pragma unroll
-        for (int k = 1; k < KS; k++)
-#pragma unroll
-            for (int t = 0; t < TT; t++)
-#pragma unroll
-                for (int v = 0; v < 16; v++) acc[t][v] += red[((((k - 1) * NW + wave) * TT + t) * 16 + v) * 64 + lane];
     }
 
     // ---- store: y[token][row], bias, accumulate ----
-    if (myrow < a.rows) {
-        const float b = a.bias ? a.bias[myrow] : 0.0f;
+    {
+        static_assert(NW * 4096 <= KS * sizeof(Slot), "output staging space");
+        float *st = reinterpret_cast<float *>(&ring0[0]) + 1024 * wave;
+        const float b = (a.bias && myrow < a.rows) ? a.bias[myrow] : 0.0f;
+        const uint32_t rw0 = r0 + 32 * wave;
 #pragma unroll
         for (int t = 0; t < TT; t++) {
-#pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const uint32_t tok = t0 + 32 * t + 8 * (v / 4) + 4 * h + (v % 4);
-                if (tok < a.n) {
-                    float *dst = a.y + uint64_t(tok) * a.rows + myrow;
-                    if (a.mode == HKHIP_ACCUMULATE)
-                        *dst += acc[t][v] + b;
-                    else
-                        *dst = acc[t][v] + b;
-                }
-            }
+            const uint32_t tk0 = t0 + 32 * t;
+            if (a.wide && rw0 + 32 <= a.rows && tk0 + 32 <= a.n)
+                gemm_store_tile_wide(st, acc[t], b, a.y, a.rows, rw0, tk0, a.mode);
+            else
+                gemm_store_tile(acc[t], b, a.y, a.rows, a.n, myrow, tk0, a.mode);
         }
     }
 }
@@ -666,6 +664,7 @@ hipError_t launch_mm2(int t, const uint8_t *w, uint32_t rows, uint32_t cols, con
     a.y = y;
     a.bias = bias;
     a.mode = mode;
+    a.wide = (reinterpret_cast<uintptr_t>(y) % 16 == 0 && rows % 4 == 0) ? 1 : 0;
     // The largest tile that still gives most of the 256 CUs a workgroup.
     auto blocks = [&](uint32_t nw, uint32_t tt) {
         return ((rows + 32 * nw - 1) / (32 * nw)) * ((n + 32 * tt - 1) / (32 * tt));

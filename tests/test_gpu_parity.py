@@ -564,3 +564,25 @@ def test_small_batch_many_tiles(eng, torch_cuda, t, n, mode):
         assert parity_err(ys[i].cpu().numpy(), want) <= PARITY_TOL
     for w in mats:
         eng.free(w)
+
+
+@pytest.mark.parametrize("t", FMTS)
+def test_gemm_unaligned_output(eng, torch_cuda, t):
+    """Outputs that are not 16-byte aligned (here one float past an aligned buffer) take the
+    per-lane stores of the GEMM's epilogue; the aligned case takes the staged 16-byte stores."""
+    torch = torch_cuda
+    m, k, n = 1024, 512, 96
+    raw = synth.weights_np(t, m, k, seed=1800 + t)
+    x = synth.activations_np(n, k, seed=1801)
+    w = eng.upload(raw, t, m, k)
+    xq = torch.empty(eng.act_bytes(n, k), dtype=torch.uint8, device="cuda")
+    eng.qact(torch.from_numpy(x).cuda(), n, k, F.ACT_KIND[t], xq)
+    want = O.matmul(t, raw, m, k, x, n, threads=16)
+    for off in (0, 1):
+        buf = torch.full((n * m + 4,), float("nan"), device="cuda")
+        y = buf[off:off + n * m]
+        eng.gemm(w, xq, y, n)
+        torch.cuda.synchronize()
+        assert parity_err(y.view(n, m).cpu().numpy(), want) <= PARITY_TOL
+        assert torch.isnan(buf[:off]).all() and torch.isnan(buf[off + n * m:]).all()
+    eng.free(w)
