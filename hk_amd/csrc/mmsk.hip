@@ -248,6 +248,26 @@ __device__ __forceinline__ void sk_store(const v4f (&acc)[RT][NTT], uint32_t n, 
                     const uint32_t r = r0 + 16 * rt + 4 * g + i;
                     if (r < rows) Y[uint64_t(tok) * (rows / 2) + r / 2] = silu_mul(acc[rt][tt][i], acc[rt][tt][i + 1]);
                 }
+            } else if (tok < n && (rows % 4) == 0 && (reinterpret_cast<uintptr_t>(Y) % 16) == 0 &&
+                       r0 + 16 * rt + 4 * g + 3 < rows) {
+                // The lane's four consecutive rows as one 16-byte store.
+                const uint32_t r = r0 + 16 * rt + 4 * g;
+                float4 *dst = reinterpret_cast<float4 *>(Y + uint64_t(tok) * rows + r);
+                float4 v = make_float4(acc[rt][tt][0], acc[rt][tt][1], acc[rt][tt][2], acc[rt][tt][3]);
+                if (B) {
+                    v.x += B[r];
+                    v.y += B[r + 1];
+                    v.z += B[r + 2];
+                    v.w += B[r + 3];
+                }
+                if (mode == HKHIP_ACCUMULATE) {
+                    const float4 o = *dst;
+                    v.x += o.x;
+                    v.y += o.y;
+                    v.z += o.z;
+                    v.w += o.w;
+                }
+                *dst = v;
             } else if (tok < n) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
