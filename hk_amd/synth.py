@@ -9,6 +9,8 @@ CPU baseline) or torch (device, for multi-GB benchmark matrices).
   Q4_K   qs and the 12 scale bytes uniform;   d = dmin = |N(0,0.02)| / 63
   Q6_K   ql / qh uniform, scales in [-32,31]; d = |N(0,0.02)| / 127
   IQ4_NL indices uniform;                     d = |N(0,0.02)|
+  Q4_0 / Q5_0  quants uniform;                d = |N(0,0.02)| / 8 (/ 16)
+  Q4_1 / Q5_1  quants uniform;                d = |N(0,0.02)| / 16 (/ 32), m = -|N(0,0.02)|
 """
 from __future__ import annotations
 
@@ -45,7 +47,17 @@ def weights_np(t: int, rows: int, cols: int, seed: int) -> np.ndarray:
         raw[:, 208:210] = _f16_scales_np(rng, nb, 127.0).view(np.uint8).reshape(nb, 2)
     elif t == formats.IQ4_NL:
         raw[:, 0:2] = _f16_scales_np(rng, nb, 1.0).view(np.uint8).reshape(nb, 2)
+    elif t in _LOW_BIT:
+        div, has_m = _LOW_BIT[t]
+        raw[:, 0:2] = _f16_scales_np(rng, nb, div).view(np.uint8).reshape(nb, 2)
+        if has_m:
+            raw[:, 2:4] = (-_f16_scales_np(rng, nb, 1.0)).view(np.uint8).reshape(nb, 2)
     return raw.reshape(rows, -1)
+
+
+# Q4_0 / Q4_1 / Q5_0 / Q5_1: scale divisor, has an offset m (f16 at bytes 2..3).
+_LOW_BIT = {formats.Q4_0: (8.0, False), formats.Q4_1: (16.0, True), formats.Q5_0: (16.0, False),
+            formats.Q5_1: (32.0, True)}
 
 
 def activations_np(n: int, k: int, seed: int, outliers: float = 0.0) -> np.ndarray:
@@ -81,4 +93,9 @@ def weights_torch(t: int, rows: int, cols: int, seed: int, device="cuda"):
         raw[:, 208:210] = scales(127.0)
     elif t == formats.IQ4_NL:
         raw[:, 0:2] = scales(1.0)
+    elif t in _LOW_BIT:
+        div, has_m = _LOW_BIT[t]
+        raw[:, 0:2] = scales(div)
+        if has_m:
+            raw[:, 2:4] = (-(torch.randn(nb, device=device, generator=g) * 0.02).abs()).half().view(torch.uint8).view(nb, 2)
     return raw.view(rows, -1)

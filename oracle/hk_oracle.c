@@ -1,10 +1,10 @@
 /* CPU oracle for hk's quantized-linear hot path. TEST INFRASTRUCTURE ONLY.
  *
  * Restates, in plain C, the arithmetic of the reference CPU kernels:
- *   - block decoders           src/quant/dequant.zig:74-78, 166-202, 237-267, 430-437, 550-591
+ *   - block decoders           src/quant/dequant.zig:24-78, 166-202, 237-267, 430-437, 550-591
  *   - activation quantizers    src/quant/vecdot.zig:134-180
- *   - single-row dots          src/quant/vecdot.zig:235-250, 369-384, 459-570, 725-771
- *   - register-tiled GEMM      src/quant/gemm.zig:131-236, 281-313, 504-520
+ *   - single-row dots          src/quant/vecdot.zig:235-384, 459-570, 725-771
+ *   - register-tiled GEMM      src/quant/gemm.zig:131-236, 262-313, 504-520
  *   - canonical unpack         src/quant/unpack.zig:29-76, 81-160
  *   - matmul dispatch          src/engine/matmul.zig:18, 96-153 (n >= 8 -> tiles)
  *
@@ -55,7 +55,7 @@ static inline float h16(const uint8_t *p) { return hko_f16_to_f32(rd16(p)); }
 
 int hko_block_elems(int t) {
     switch (t) {
-    case HKO_Q8_0: case HKO_IQ4_NL: return 32;
+    case HKO_Q8_0: case HKO_IQ4_NL: case HKO_Q4_0: case HKO_Q4_1: case HKO_Q5_0: case HKO_Q5_1: return 32;
     case HKO_Q4_K: case HKO_Q6_K: return QK_K;
     default: return 0;
     }
@@ -67,13 +67,18 @@ int hko_block_bytes(int t) {
     case HKO_IQ4_NL: return 18; /* blocks.zig:34 */
     case HKO_Q4_K: return 144;  /* blocks.zig:21 */
     case HKO_Q6_K: return 210;  /* blocks.zig:23 */
+    case HKO_Q4_0: return 18;   /* blocks.zig:13 */
+    case HKO_Q4_1: return 20;   /* blocks.zig:14 */
+    case HKO_Q5_0: return 22;   /* blocks.zig:15 */
+    case HKO_Q5_1: return 24;   /* blocks.zig:16 */
     default: return 0;
     }
 }
 
 int hko_act_kind(int t) {
     switch (t) {
-    case HKO_Q8_0: case HKO_IQ4_NL: return 0; /* vecdot.zig:187 */
+    case HKO_Q8_0: case HKO_IQ4_NL: case HKO_Q4_0: case HKO_Q4_1: case HKO_Q5_0: case HKO_Q5_1:
+        return 0; /* vecdot.zig:187 */
     case HKO_Q4_K: case HKO_Q6_K: return 1;   /* vecdot.zig:188 */
     default: return -1;
     }
@@ -111,6 +116,43 @@ void hko_scales_mins_k4_words(const uint8_t p[12], uint8_t sc[8], uint8_t mn[8])
         sc[4 + i] = (uint8_t)(u[1] >> (8 * i));
         mn[i] = (uint8_t)(u[2] >> (8 * i));
         mn[4 + i] = (uint8_t)(u[3] >> (8 * i));
+    }
+}
+
+/* The unsigned quants of a Q4_0 / Q4_1 / Q5_0 / Q5_1 block, weight order: byte j's low nibble is
+ * weight j, its high nibble weight j + 16 (dequant.zig:24-70); Q5 adds bit j of the little-endian
+ * qh word as bit 4 of weight j. Returns the block's quant bytes' offset. */
+static int low_bit_quants(int t, const uint8_t *b, int32_t u[32]) {
+    int qs = (t == HKO_Q4_0) ? 2 : 4;
+    uint32_t qh = 0;
+    if (t == HKO_Q5_0) { qh = (uint32_t)b[2] | ((uint32_t)b[3] << 8) | ((uint32_t)b[4] << 16) | ((uint32_t)b[5] << 24); qs = 6; }
+    if (t == HKO_Q5_1) { qh = (uint32_t)b[4] | ((uint32_t)b[5] << 8) | ((uint32_t)b[6] << 16) | ((uint32_t)b[7] << 24); qs = 8; }
+    for (int j = 0; j < 16; j++) {
+        u[j] = b[qs + j] & 0x0F;
+        u[j + 16] = b[qs + j] >> 4;
+        if (t == HKO_Q5_0 || t == HKO_Q5_1) {
+            u[j] |= (int32_t)(((qh >> j) << 4) & 0x10);
+            u[j + 16] |= (int32_t)((qh >> (j + 12)) & 0x10);
+        }
+    }
+    return qs;
+}
+
+/* Zero point (gemm.zig:262-270 legacyZeroPoint) and whether a block has an offset m. */
+static int low_bit_zp(int t) { return t == HKO_Q4_0 ? 8 : t == HKO_Q5_0 ? 16 : 0; }
+static int low_bit_has_m(int t) { return t == HKO_Q4_1 || t == HKO_Q5_1; }
+
+/* dequant.zig:24-70: d * (u - zp), or d * u + m. */
+static void deq_low_bit(int t, const uint8_t *b, float *out) {
+    int32_t u[32];
+    low_bit_quants(t, b, u);
+    float d = h16(b);
+    if (low_bit_has_m(t)) {
+        float m = h16(b + 2);
+        for (int j = 0; j < 32; j++) out[j] = (float)u[j] * d + m;
+    } else {
+        int zp = low_bit_zp(t);
+        for (int j = 0; j < 32; j++) out[j] = (float)(u[j] - zp) * d;
     }
 }
 
@@ -193,6 +235,7 @@ int hko_dequantize_row(int t, const uint8_t *src, size_t src_len, float *dst, si
         case HKO_Q4_K: deq_q4_k(b, o); break;
         case HKO_Q6_K: deq_q6_k(b, o); break;
         case HKO_IQ4_NL: deq_iq4_nl(b, o); break;
+        case HKO_Q4_0: case HKO_Q4_1: case HKO_Q5_0: case HKO_Q5_1: deq_low_bit(t, b, o); break;
         }
     }
     return 0;
@@ -293,6 +336,29 @@ static float dot_legacy(int t, const uint8_t *row, size_t nb, const hko_block_a8
     return reduce8(accf);
 }
 
+/* vecdot.zig:293-367 (dotQ4_0, dotQ4_1, dotQ5_0, dotQ5_1): unsigned quants against A8. The zero
+ * point comes off lane 0 only (lane0(zp * s)); the offset term m * (d_a * s) is added to every
+ * lane, so the eight lanes' sum is scaled back by 1/8. */
+static float dot_low_bit(int t, const uint8_t *row, size_t nb, const hko_block_a8 *a) {
+    float accf[8] = {0}, extra[8] = {0};
+    int32_t u[32], di[8];
+    const int zp = low_bit_zp(t), has_m = low_bit_has_m(t);
+    for (size_t i = 0; i < nb; i++) {
+        const uint8_t *b = row + i * (size_t)hko_block_bytes(t);
+        low_bit_quants(t, b, u);
+        float dv = h16(b);
+        dp32(di, u, a[i].qs);
+        di[0] -= zp * a[i].s;
+        float s = dv * a[i].d;
+        for (int L = 0; L < 8; L++) accf[L] = fmaf((float)di[L], s, accf[L]);
+        if (has_m) {
+            float mv = h16(b + 2), ds = a[i].d * (float)a[i].s;
+            for (int L = 0; L < 8; L++) extra[L] = fmaf(mv, ds, extra[L]);
+        }
+    }
+    return has_m ? reduce8(accf) + reduce8(extra) * (1.0f / 8.0f) : reduce8(accf);
+}
+
 /* vecdot.zig:482-522 k4Block / dotQ4K */
 static float dot_q4_k(const uint8_t *row, size_t nsb, const hko_block_q8k *a) {
     float accf[8] = {0}, corr[8] = {0};
@@ -357,6 +423,7 @@ static float dot_q6_k(const uint8_t *row, size_t nsb, const hko_block_q8k *a) {
 float hko_dot_row(int t, const uint8_t *row, size_t k, const hko_block_a8 *a8, const hko_block_q8k *q8k) {
     switch (t) {
     case HKO_Q8_0: case HKO_IQ4_NL: return dot_legacy(t, row, k / 32, a8);
+    case HKO_Q4_0: case HKO_Q4_1: case HKO_Q5_0: case HKO_Q5_1: return dot_low_bit(t, row, k / 32, a8);
     case HKO_Q4_K: return dot_q4_k(row, k / QK_K, q8k);
     case HKO_Q6_K: return dot_q6_k(row, k / QK_K, q8k);
     default: return NAN;
@@ -430,8 +497,27 @@ static float tile_k(int t, const uint8_t *row, size_t nsb, const hko_block_q8k *
     return accf;
 }
 
+/* gemm.zig:131-176 kernelLegacy for one row and token: integer block sum of the unsigned quants,
+ * minus zp * s, times d * d_a; plus m * (d_a * s) for the formats with an offset. */
+static float tile_low_bit(int t, const uint8_t *row, size_t nb, const hko_block_a8 *a) {
+    float accf = 0.0f;
+    int32_t u[32];
+    const int zp = low_bit_zp(t), has_m = low_bit_has_m(t);
+    for (size_t i = 0; i < nb; i++) {
+        const uint8_t *b = row + i * (size_t)hko_block_bytes(t);
+        low_bit_quants(t, b, u);
+        int32_t acci = 0;
+        for (int j = 0; j < 32; j++) acci += u[j] * a[i].qs[j];
+        acci -= zp * a[i].s;
+        accf = fmaf((float)acci, h16(b) * a[i].d, accf);
+        if (has_m) accf = fmaf(h16(b + 2), a[i].d * (float)a[i].s, accf);
+    }
+    return accf;
+}
+
 /* gemm.zig:131-176 kernelLegacy (signed, no zero point, no offset) for one row and token. */
 static float tile_legacy(int t, const uint8_t *row, size_t nb, const hko_block_a8 *a) {
+    if (t != HKO_Q8_0 && t != HKO_IQ4_NL) return tile_low_bit(t, row, nb, a);
     float accf = 0.0f;
     for (size_t i = 0; i < nb; i++) {
         const uint8_t *b = row + i * (size_t)hko_block_bytes(t);

@@ -20,7 +20,11 @@ extern "C" {
 #endif
 
 /* hk StorageType codes (reference src/format.zig:26-84). */
+#define HKO_Q4_0 0x15
 #define HKO_Q8_0 0x16
+#define HKO_Q4_1 0x17
+#define HKO_Q5_0 0x18
+#define HKO_Q5_1 0x19
 #define HKO_Q4_K 0x42
 #define HKO_Q6_K 0x44
 #define HKO_IQ4_NL 0x55

@@ -23,9 +23,9 @@ from hk_amd import synth
 from oracle import oracle as O
 from tests.helpers import load_fixture
 
-FMTS = [F.Q8_0, F.Q4_K, F.Q6_K, F.IQ4_NL]
-FIXTURES = {F.Q8_0: "q8_0", F.Q4_K: "q4_k", F.Q6_K: "q6_k", F.IQ4_NL: "iq4_nl"}
-GGML_TYPE = {F.Q8_0: 8, F.Q4_K: 12, F.Q6_K: 14, F.IQ4_NL: 20}
+FMTS = [F.Q8_0, F.Q4_K, F.Q6_K, F.IQ4_NL, F.Q4_0, F.Q4_1, F.Q5_0, F.Q5_1]
+FIXTURES = F.NAMES
+GGML_TYPE = {F.Q8_0: 8, F.Q4_K: 12, F.Q6_K: 14, F.IQ4_NL: 20, F.Q4_0: 2, F.Q4_1: 3, F.Q5_0: 6, F.Q5_1: 7}
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -100,6 +100,29 @@ def test_decode_closed_forms_on_constructed_blocks(t):
             nib = 3 if j % 2 == 0 else 5
             want = (j + 1) * 1.0 * nib - 0.25 * (2 * j)
             assert np.all(got[32 * j:32 * j + 32] == np.float32(want))
+    elif t in (F.Q4_0, F.Q4_1, F.Q5_0, F.Q5_1):
+        # ggml's block definitions: byte j holds weight j (low nibble) and j + 16 (high nibble);
+        # Q5 takes bit j of the little-endian qh word as weight j's fifth bit.
+        five, has_m = t in (F.Q5_0, F.Q5_1), t in (F.Q4_1, F.Q5_1)
+        nb = F.INFO[t][1]
+        b = np.zeros(nb, np.uint8)
+        b[0:2] = np.array([0.5], np.float16).view(np.uint8)
+        off = 2
+        if has_m:
+            b[2:4] = np.array([-1.25], np.float16).view(np.uint8)
+            off = 4
+        qh = 0xA5C3F00F
+        if five:
+            b[off:off + 4] = np.array([qh], "<u4").view(np.uint8)
+            off += 4
+        b[off:off + 16] = (np.arange(16) | ((15 - np.arange(16)) << 4)).astype(np.uint8)
+        u = [j if j < 16 else 31 - j for j in range(32)]
+        if five:
+            u = [u[j] + 16 * ((qh >> j) & 1) for j in range(32)]
+        zp = {F.Q4_0: 8, F.Q5_0: 16}.get(t, 0)
+        want = [np.float32(uj) * np.float32(0.5) + np.float32(-1.25) if has_m else np.float32(uj - zp) * np.float32(0.5)
+                for uj in u]
+        assert np.array_equal(O.dequantize(t, b, 32), np.array(want, np.float32))
     else:  # Q6_K
         b = np.zeros(210, np.uint8)
         b[208:210] = np.array([0.5], np.float16).view(np.uint8)
