@@ -68,6 +68,7 @@ SIGNATURES = {
     "hkhip_mm": (_I, [_P, _MP, _P, _P, _U32, _P, _I]),
     "hkhip_gemm_host": (_I, [_U8, _P, _P, _P, _P, _U64, _U64, _U64]),
     "hkhip_gemv_q8_0": (_I, [_P, _P, _P, _P, _U64, _U64]),
+    "hkhip_gemv_q4_0": (_I, [_P, _P, _P, _P, _U64, _U64]),
     "hkhip_gemv_q4_k": (_I, [_P, _P, _P, _P, _U64, _U64]),
     "hkhip_gemv_q6_k": (_I, [_P, _P, _P, _P, _U64, _U64]),
     "hkhip_gemv_iq4_nl": (_I, [_P, _P, _P, _P, _U64, _U64]),

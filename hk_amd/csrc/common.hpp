@@ -16,10 +16,14 @@ inline uint64_t align256(uint64_t x) { return (x + 255) & ~uint64_t(255); }
 // Block geometry in hk's file layout (src/quant/blocks.zig:17-34).
 inline int block_elems(int t) {
     switch (t) {
-    case HKHIP_Q8_0: case HKHIP_IQ4_NL: return 32;
+    case HKHIP_Q8_0: case HKHIP_IQ4_NL: case HKHIP_Q4_0: case HKHIP_Q4_1: case HKHIP_Q5_0: case HKHIP_Q5_1:
+        return 32;
     case HKHIP_Q4_K: case HKHIP_Q6_K: return 256;
     default: return 0;
     }
+}
+__host__ __device__ inline int block_bytes_dev(int t) {
+    return t == HKHIP_Q4_0 ? 18 : t == HKHIP_Q4_1 ? 20 : t == HKHIP_Q5_0 ? 22 : t == HKHIP_Q5_1 ? 24 : 0;
 }
 inline int block_bytes(int t) {
     switch (t) {
@@ -27,11 +31,33 @@ inline int block_bytes(int t) {
     case HKHIP_IQ4_NL: return 18;
     case HKHIP_Q4_K: return 144;
     case HKHIP_Q6_K: return 210;
+    case HKHIP_Q4_0: return 18;
+    case HKHIP_Q4_1: return 20;
+    case HKHIP_Q5_0: return 22;
+    case HKHIP_Q5_1: return 24;
     default: return 0;
     }
 }
 // vecdot.zig:185-191
-inline int act_kind(int t) { return (t == HKHIP_Q8_0 || t == HKHIP_IQ4_NL) ? HKHIP_ACT_A8 : HKHIP_ACT_Q8K; }
+inline int act_kind(int t) { return block_elems(t) == 32 ? HKHIP_ACT_A8 : HKHIP_ACT_Q8K; }
+// The 32-weight formats (A8 activations).
+__host__ __device__ constexpr bool legacy32(int t) {
+    return t == HKHIP_Q8_0 || t == HKHIP_IQ4_NL || t == HKHIP_Q4_0 || t == HKHIP_Q4_1 || t == HKHIP_Q5_0 ||
+           t == HKHIP_Q5_1;
+}
+// The 4/5-bit 32-weight formats: zero point (gemm.zig:262-270), offset m, fifth bit.
+__host__ __device__ constexpr bool has_m(int t) { return t == HKHIP_Q4_1 || t == HKHIP_Q5_1; }
+__host__ __device__ constexpr bool has_qh(int t) { return t == HKHIP_Q5_0 || t == HKHIP_Q5_1; }
+__host__ __device__ constexpr int zero_point(int t) { return t == HKHIP_Q4_0 ? 8 : t == HKHIP_Q5_0 ? 16 : 0; }
+// Geometry of one row's record in the side plane (see WLayout), in bytes: the offsets m and qh
+// start at, and the record stride. The fifth-bit words start 4-byte aligned.
+struct SideGeom {
+    uint32_t m_off, qh_off, stride;
+};
+__host__ __device__ constexpr SideGeom side_geom(int t, uint32_t nbr) {
+    return SideGeom{2 * nbr, ((has_m(t) ? 4 : 2) * nbr + 3) & ~3u,
+                    has_qh(t) ? (((has_m(t) ? 4 : 2) * nbr + 3) & ~3u) + 4 * nbr : (has_m(t) ? 4 : 2) * nbr};
+}
 
 // Device layout of a weight matrix. Q4_K keeps the 144-byte file blocks (already 16-byte
 // aligned). The 2-byte-aligned formats are split at upload into a quant plane whose blocks
@@ -39,6 +65,11 @@ inline int act_kind(int t) { return (t == HKHIP_Q8_0 || t == HKHIP_IQ4_NL) ? HKH
 //   Q8_0   quant plane: 32 B per block (qs)        scale plane: d
 //   IQ4_NL quant plane: 16 B per block (qs)        scale plane: d
 //   Q6_K   quant plane: 208 B per block (ql qh sc) scale plane: d
+//   Q4_0 / Q4_1 / Q5_0 / Q5_1  quant plane: 16 B per block (qs, file nibble order)
+//          side plane, one record per row of nbr = cols/32 blocks: d[nbr] f16, then m[nbr] f16
+//          (Q4_1, Q5_1), then, from the next 4-byte boundary, qh[nbr] u32 (Q5_0, Q5_1; bit j =
+//          weight j's fifth bit) -- side_geom(). For the other formats the side plane is the
+//          scale plane alone (d per block, block order).
 struct WLayout {
     uint64_t quant_bytes;  // bytes of the quant plane (or of the whole Q4_K matrix)
     uint64_t scale_off;    // offset of the scale plane
@@ -52,7 +83,7 @@ inline WLayout weight_layout(int t, uint32_t rows, uint32_t cols) {
     switch (t) {
     case HKHIP_Q4_K: L.qblock = 144; break;
     case HKHIP_Q8_0: L.qblock = 32; break;
-    case HKHIP_IQ4_NL: L.qblock = 16; break;
+    case HKHIP_IQ4_NL: case HKHIP_Q4_0: case HKHIP_Q4_1: case HKHIP_Q5_0: case HKHIP_Q5_1: L.qblock = 16; break;
     case HKHIP_Q6_K: L.qblock = 208; break;
     }
     L.quant_bytes = nb * L.qblock;
@@ -61,7 +92,8 @@ inline WLayout weight_layout(int t, uint32_t rows, uint32_t cols) {
         L.total = L.quant_bytes;
     } else {
         L.scale_off = align256(L.quant_bytes);
-        L.total = align256(L.scale_off + nb * 2); // the kernels read the scales as aligned words
+        const uint64_t side = block_elems(t) == 32 ? uint64_t(rows) * side_geom(t, cols / 32).stride : nb * 2;
+        L.total = align256(L.scale_off + side); // the kernels read the scales as aligned words
     }
     return L;
 }
@@ -142,6 +174,24 @@ __device__ __forceinline__ uint32_t iq4nl_lookup4(uint32_t idx) {
     uint32_t hi = __builtin_amdgcn_perm(IQ4NL_T3, IQ4NL_T2, sel);
     uint32_t m = ((idx >> 3) & 0x01010101u) * 0xFFu; // 0xFF in bytes whose index is >= 8
     return (hi & m) | (lo & ~m);
+}
+
+// Four unsigned quants (one per byte, each < 128) minus a zero point z4 = z * 0x01010101 (z <
+// 128), as two's-complement bytes: the 0x80 bias keeps the byte subtractions from borrowing.
+__device__ __forceinline__ uint32_t sub_zp4(uint32_t u, uint32_t z4) { return ((u | 0x80808080u) - z4) ^ 0x80808080u; }
+// Bits 0-3 of b to bit 4 of bytes 0-3 (the shifted copies of b do not overlap: no carries).
+__device__ __forceinline__ uint32_t bits_to_b4(uint32_t b) { return ((b & 0xFu) * 0x02040810u) & 0x10101010u; }
+
+// Signed int8 weights of a 32-weight 4/5-bit block, four per word: word i of half hh (hh = 0
+// the low nibbles of the block's 16 bytes, weights 4i..4i+3; hh = 1 the high nibbles, weights
+// 16 + 4i..), from the block's quant word x (bytes 4i..4i+3) and fifth-bit word qh. Q4_1 and
+// Q5_1 stay unsigned (their offset is a separate term); IQ4_NL goes through the codebook.
+template <int T> __device__ __forceinline__ uint32_t low_bit_word(uint32_t x, uint32_t qh, uint32_t hh, uint32_t i) {
+    uint32_t n = (x >> (4 * hh)) & 0x0F0F0F0Fu;
+    if constexpr (T == HKHIP_IQ4_NL) return iq4nl_lookup4(n);
+    if constexpr (has_qh(T)) n |= bits_to_b4(qh >> (16 * hh + 4 * i));
+    if constexpr (zero_point(T) != 0) n = sub_zp4(n, uint32_t(zero_point(T)) * 0x01010101u);
+    return n;
 }
 
 // 16 (4) bytes per lane global -> LDS: lane L writes at the wave-uniform LDS address + 16*L

@@ -329,7 +329,8 @@ static uint32_t gemm_min_tokens(int t) {
     switch (t) {
     case HKHIP_Q6_K:
     case HKHIP_Q8_0: return 33;
-    case HKHIP_IQ4_NL: return 25;
+    case HKHIP_IQ4_NL:
+    case HKHIP_Q4_0: case HKHIP_Q4_1: case HKHIP_Q5_0: case HKHIP_Q5_1: return 25; // IQ4_NL's (same quant bytes)
     default: return 9;
     }
 }
@@ -402,6 +403,9 @@ int hkhip_gemm_host(uint8_t t, const void *w, const float *x, const float *bias,
 
 int hkhip_gemv_q8_0(const void *w, const float *x, const float *bias, float *y, uint64_t m, uint64_t k) {
     return hkhip_gemm_host(HKHIP_Q8_0, w, x, bias, y, m, k, 1);
+}
+int hkhip_gemv_q4_0(const void *w, const float *x, const float *bias, float *y, uint64_t m, uint64_t k) {
+    return hkhip_gemm_host(HKHIP_Q4_0, w, x, bias, y, m, k, 1);
 }
 int hkhip_gemv_q4_k(const void *w, const float *x, const float *bias, float *y, uint64_t m, uint64_t k) {
     return hkhip_gemm_host(HKHIP_Q4_K, w, x, bias, y, m, k, 1);

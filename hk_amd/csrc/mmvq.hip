@@ -10,6 +10,7 @@
 //   Q6_K   a quarter super-block: 16 B of each of ql-low, ql-high, qh (64 weights, 4 groups)
 //   Q8_0   one block: 32 B of int8
 //   IQ4_NL one block: 16 B of nibbles, looked up in the codebook with byte permutes
+//   Q4_0, Q4_1, Q5_0, Q5_1  one block: 16 B of nibbles + side-plane d (m, fifth bits)
 // Products use sdot4 (v_dot4_i32_i8); lane partials are reduced with DPP lane moves.
 //
 // Two kernels:
@@ -77,7 +78,9 @@ struct ActL {
 // Where one lane's row lives.
 struct RowRef {
     const uint8_t *w;   // first byte of the row in the quant plane
-    const uint16_t *ws; // first scale of the row in the scale plane
+    const uint16_t *ws; // first scale of the row in the scale (side) plane
+    const uint16_t *wm; // Q4_1 / Q5_1: the row's offsets m
+    const uint32_t *wh; // Q5_0 / Q5_1: the row's fifth-bit words
 };
 
 // ---------------------------------------------------------------------------------------------
@@ -292,7 +295,10 @@ template <> struct MvFmt<HKHIP_Q6_K> {
     }
 };
 
-// Q8_0 and IQ4_NL: one 32-weight block per unit, against A8.
+// The 32-weight formats, one block per unit, against A8: Q8_0 and IQ4_NL (vecdot.zig:235-250,
+// 369-384) signed; Q4_0 / Q5_0 with their zero point subtracted per weight (so the block sum is
+// dotQ4_0's dpu - 8*s, dotQ5_0's - 16*s); Q4_1 / Q5_1 unsigned plus m * (d_a * s), with s the
+// block's activation sum (dotQ4_1 / dotQ5_1, 311-367).
 template <int T> struct MvLegacy {
     static constexpr bool kq = false;
     static constexpr uint32_t QB = (T == HKHIP_Q8_0) ? 32 : 16; // quant-plane bytes per block
@@ -301,20 +307,26 @@ template <int T> struct MvLegacy {
     __device__ static uint32_t bs_index(uint32_t g) { return g; }
     struct W {
         uint4 x0, x1;
-        uint32_t d;
+        uint32_t d, m, qh;
     };
     struct AU {
         uint32_t q[8];
         float d;
     };
     __device__ static RowRef row(const uint8_t *w, const uint16_t *ws, uint32_t r, uint32_t K) {
-        return RowRef{w + uint64_t(r) * (K / 32) * QB, ws + uint64_t(r) * (K / 32)};
+        const uint32_t nbr = K / 32;
+        const SideGeom G = side_geom(T, nbr);
+        const uint8_t *side = reinterpret_cast<const uint8_t *>(ws) + uint64_t(r) * G.stride;
+        return RowRef{w + uint64_t(r) * nbr * QB, reinterpret_cast<const uint16_t *>(side),
+                      reinterpret_cast<const uint16_t *>(side + G.m_off), reinterpret_cast<const uint32_t *>(side + G.qh_off)};
     }
     __device__ static W load(const RowRef &R, uint32_t u) {
         W w;
         w.x0 = ldw(R.w + u * QB);
         if constexpr (T == HKHIP_Q8_0) w.x1 = ldw(R.w + u * QB + 16);
         w.d = R.ws[u];
+        if constexpr (has_m(T)) w.m = R.wm[u];
+        if constexpr (has_qh(T)) w.qh = R.wh[u];
         return w;
     }
     __device__ static AU act(const ActL &A, uint32_t t, uint32_t u) {
@@ -327,10 +339,11 @@ template <int T> struct MvLegacy {
         a.d = A.d[t * (A.K / 32) + u];
         return a;
     }
-    // Weight-side work of a unit: its 32 int8 weights (codebook lookups for IQ4_NL) and scale.
+    // Weight-side work of a unit: its 32 int8 weights (codebook lookups for IQ4_NL, zero point
+    // and fifth bits for Q4_0..Q5_1), scale and offset.
     struct P {
         uint32_t q[8];
-        float d;
+        float d, m;
     };
     __device__ static P prep(const W &w, uint32_t) {
         P p;
@@ -339,13 +352,15 @@ template <int T> struct MvLegacy {
             p.q[4] = w.x1.x; p.q[5] = w.x1.y; p.q[6] = w.x1.z; p.q[7] = w.x1.w;
         } else {
             const uint32_t n4[4] = {w.x0.x, w.x0.y, w.x0.z, w.x0.w};
+            const uint32_t qh = has_qh(T) ? w.qh : 0u;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                p.q[i] = iq4nl_lookup4(n4[i] & 0x0F0F0F0Fu);
-                p.q[4 + i] = iq4nl_lookup4((n4[i] >> 4) & 0x0F0F0F0Fu);
+                p.q[i] = low_bit_word<T>(n4[i], qh, 0, i);
+                p.q[4 + i] = low_bit_word<T>(n4[i], qh, 1, i);
             }
         }
         p.d = f16_bits_to_f32(w.d);
+        p.m = has_m(T) ? f16_bits_to_f32(w.m) : 0.0f;
         return p;
     }
     __device__ static void dotp(const P &p, const AU &a, float &acc, float &) {
@@ -353,6 +368,12 @@ template <int T> struct MvLegacy {
 #pragma unroll
         for (int i = 0; i < 8; i++) s = sdot4(p.q[i], a.q[i], s);
         acc = fmaf((float)s, p.d * a.d, acc);
+        if constexpr (has_m(T)) {
+            int as = 0;
+#pragma unroll
+            for (int i = 0; i < 8; i++) as = sdot4(0x01010101, a.q[i], as);
+            acc = fmaf(p.m, a.d * (float)as, acc);
+        }
     }
     __device__ static void dot(const W &w, uint32_t u, const AU &a, float &acc, float &corr) {
         dotp(prep(w, u), a, acc, corr);
@@ -360,6 +381,10 @@ template <int T> struct MvLegacy {
 };
 template <> struct MvFmt<HKHIP_Q8_0> : MvLegacy<HKHIP_Q8_0> {};
 template <> struct MvFmt<HKHIP_IQ4_NL> : MvLegacy<HKHIP_IQ4_NL> {};
+template <> struct MvFmt<HKHIP_Q4_0> : MvLegacy<HKHIP_Q4_0> {};
+template <> struct MvFmt<HKHIP_Q4_1> : MvLegacy<HKHIP_Q4_1> {};
+template <> struct MvFmt<HKHIP_Q5_0> : MvLegacy<HKHIP_Q5_0> {};
+template <> struct MvFmt<HKHIP_Q5_1> : MvLegacy<HKHIP_Q5_1> {};
 
 // ---------------------------------------------------------------------------------------------
 // Shared pieces of the kernels
@@ -981,6 +1006,10 @@ static mv_kernel_t kernel_for(int t, int nt) {
     case HKHIP_Q6_K: return pick<HKHIP_Q6_K>(nt);
     case HKHIP_Q8_0: return pick<HKHIP_Q8_0>(nt);
     case HKHIP_IQ4_NL: return pick<HKHIP_IQ4_NL>(nt);
+    case HKHIP_Q4_0: return pick<HKHIP_Q4_0>(nt);
+    case HKHIP_Q4_1: return pick<HKHIP_Q4_1>(nt);
+    case HKHIP_Q5_0: return pick<HKHIP_Q5_0>(nt);
+    case HKHIP_Q5_1: return pick<HKHIP_Q5_1>(nt);
     default: return nullptr;
     }
 }
@@ -989,7 +1018,7 @@ static mv_kernel_t kernel_for(int t, int nt) {
 // Register kernel variants: NT in {1, 2, 4, 8} (a launch of n tokens uses the smallest NT >= n),
 // C = units per lane (rows of at most 64*C units), R = rows per step. The activations of NT*C
 // units must fit the register file next to two steps of weights: NT*C <= 8 for Q4_K/Q6_K and
-// <= 16 for Q8_0/IQ4_NL; larger shapes use the LDS kernel.
+// <= 16 for the 32-weight formats; larger shapes use the LDS kernel.
 constexpr int MVR_NWAVES = 8; // waves per workgroup (a budget of 256 registers per lane)
 constexpr int MVR_R1 = 2;     // rows per step at one token and C = 1
 __host__ __device__ constexpr int mvr_rows(int nt, int c) { return nt == 1 ? (c >= MVR_R1 ? 1 : MVR_R1 / c) : (c >= 2 || nt >= 8 ? 1 : 2); }
@@ -1004,7 +1033,7 @@ __host__ __device__ constexpr int mvr_cmax(int t, int nt) {
 // variants that need more.
 __host__ __device__ constexpr int mvr_nw(int t, int nt, int c) {
     return (t == HKHIP_Q6_K && nt * c >= 4) || (t == HKHIP_Q4_K && nt * c >= 8 && nt < 8) ||
-                   ((t == HKHIP_Q8_0 || t == HKHIP_IQ4_NL) && c >= 4 && nt * c >= 8)
+                   (legacy32(t) && c >= 4 && nt * c >= 8)
                ? 4
                : MVR_NWAVES;
 }
@@ -1057,6 +1086,10 @@ static mv_kernel_t kernelr_for(int t, int nt, int c, int ks) {
     case HKHIP_Q6_K: return mvr_pick<HKHIP_Q6_K>(nt, c, ks);
     case HKHIP_Q8_0: return mvr_pick<HKHIP_Q8_0>(nt, c, ks);
     case HKHIP_IQ4_NL: return mvr_pick<HKHIP_IQ4_NL>(nt, c, ks);
+    case HKHIP_Q4_0: return mvr_pick<HKHIP_Q4_0>(nt, c, ks);
+    case HKHIP_Q4_1: return mvr_pick<HKHIP_Q4_1>(nt, c, ks);
+    case HKHIP_Q5_0: return mvr_pick<HKHIP_Q5_0>(nt, c, ks);
+    case HKHIP_Q5_1: return mvr_pick<HKHIP_Q5_1>(nt, c, ks);
     default: return nullptr;
     }
 }

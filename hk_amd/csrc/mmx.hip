@@ -1,4 +1,5 @@
-// Prefill GEMM for Q6_K, Q8_0 and IQ4_NL on the int8 MFMA units (K a multiple of 256).
+// Prefill GEMM for Q6_K and the 32-weight formats (Q8_0, IQ4_NL, Q4_0, Q4_1, Q5_0, Q5_1) on the
+// int8 MFMA units (K a multiple of 256).
 //
 // Integer arithmetic as in hk's CPU kernels (src/quant/gemm.zig kernelK 180-236 for Q6_K,
 // kernelLegacy 131-176 for the 32-weight blocks):
@@ -8,9 +9,10 @@
 //    8*e1 + e0 with digits in [-3, 4], so every plane value (q - 32)*e lies in [-128, 124].
 //    Each MFMA lane holds 16 weights of one group, so a lane's plane bytes share one digit. One
 //    int32 chain per tile gives ((P2 << 3) + P1 << 3) + P0 = I, the reference's integer.
-//  * Q8_0 / IQ4_NL: y += (dw[r,c]*da[t,c]) * I_c per 32-weight block c (I_c exact). One
-//    32x32x32 int8 MFMA yields the tile's I_c; then per output one multiply (dw*da), one
-//    convert and one fma.
+//  * 32-weight formats: y += (dw[r,c]*da[t,c]) * I_c per block c (I_c exact). One 32x32x32
+//    int8 MFMA yields the tile's I_c; then per output one multiply (dw*da), one convert and one
+//    fma. Q4_0 / Q5_0 weights enter as u - zp (kernelLegacy's acci - zp*s); Q4_1 / Q5_1 as u,
+//    plus m[r,c] * (da[t,c] * s[t,c]) per output (kernelLegacy's has_m term).
 // Only the f32 summation order differs from the reference.
 //
 // Structure (as the Q4_K ring kernel): a workgroup of NW waves owns 32*NW rows x 32*TT tokens;
@@ -47,6 +49,15 @@ template <> struct Fmt<HKHIP_Q8_0> {
 template <> struct Fmt<HKHIP_IQ4_NL> {
     static constexpr uint32_t RB = 128, W16 = 4, W4 = 0, WSB = 1024, DAB = 32;
 };
+// Q4_0..Q5_1: side data per row and step: d (16 B) and m (16 B) as one 1-KB load per wave (lanes
+// 32-63 take m), the fifth-bit words (32 B) as a second.
+template <int T> struct Fmt4 {
+    static constexpr uint32_t RB = 128, W16 = 4, W4 = 0, WSB = has_qh(T) ? 2048 : 1024, DAB = 32;
+};
+template <> struct Fmt<HKHIP_Q4_0> : Fmt4<HKHIP_Q4_0> {};
+template <> struct Fmt<HKHIP_Q4_1> : Fmt4<HKHIP_Q4_1> {};
+template <> struct Fmt<HKHIP_Q5_0> : Fmt4<HKHIP_Q5_0> {};
+template <> struct Fmt<HKHIP_Q5_1> : Fmt4<HKHIP_Q5_1> {};
 
 template <int T, int TOK, int NW> struct MxSlot {
     int8_t a[TOK * 256];                     // chunk c of token t at c ^ (t & 15)
@@ -55,6 +66,7 @@ template <int T, int TOK, int NW> struct MxSlot {
     // Activation scales: Q6_K per token (wave m fills tokens 64m..64m+63); A8 per block and token,
     // block-major ([8][TOK]), so that four consecutive tokens' scales are one 16-byte read.
     float da[T == HKHIP_Q6_K ? 64 * NW : 8 * TOK];
+    int sa[has_m(T) ? 8 * TOK : 1]; // Q4_1 / Q5_1: the blocks' activation sums s, as da
 };
 
 struct MxArgs {
@@ -63,6 +75,7 @@ struct MxArgs {
     uint32_t rows, cols, n;
     const int8_t *aqs;
     const float *ad;
+    const int32_t *as; // A8 block sums (Q4_1, Q5_1)
     float *y;
     const float *bias;
     int mode;
@@ -140,7 +153,7 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
     constexpr uint32_t TPW = TOK / NW; // token rows per wave
     static_assert(TPW % 4 == 0, "token rows per wave");
     constexpr uint32_t DAL = q6 ? 1 : 8 * TOK / (64 * NW);         // token-scale loads per wave
-    constexpr uint32_t CPW = TPW / 4 + F::W16 + F::W4 + 1 + DAL; // loads per wave and step
+    constexpr uint32_t CPW = TPW / 4 + F::W16 + F::W4 + 1 + DAL + (has_qh(T) ? 1 : 0) + (has_m(T) ? DAL : 0);
     // Weights: 16-byte piece P = 64*i + lane of the wave's area is row P/(RB/16), piece P%(RB/16);
     // rows of 256 or 128 bytes are swizzled (piece c of row r at c ^ (r & 15), resp. r & 7) so
     // the 32 rows one operand read covers hit distinct banks. Q6_K's 208-byte rows need no
@@ -164,8 +177,14 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
     }
     // Scales: Q6_K one f16 per row and step (the aligned dword holding it); the blocks' eight
     // f16 (16 bytes) per row and step otherwise. Lanes 32-63 repeat lanes 0-31.
+    // Q4_0..Q5_1 (side plane per row: d[nbr], m[nbr], qh[nbr]): lanes 32-63 load m, and the
+    // fifth-bit words of blocks 0-3 (lanes 0-31) and 4-7 (lanes 32-63) go as a second load.
     const uint32_t srow = clamp_row(r0 + 32 * wave + j);
-    const uint32_t sbase = q6 ? srow * nsb : srow * (K / 32) * 2;
+    constexpr bool low4 = has_m(T) || has_qh(T) || zero_point(T) != 0;
+    const SideGeom G = side_geom(T, K / 32);
+    const uint32_t sidebase = srow * G.stride;
+    const uint32_t sbase = q6 ? srow * nsb : !low4 ? srow * G.stride : sidebase + (h && has_m(T) ? G.m_off : 0);
+    const uint32_t qhbase = sidebase + G.qh_off + 16 * h;
     // Token data: activation int8 rows, swizzled like the weights; token scales.
     uint32_t aoff[TPW / 4];
 #pragma unroll
@@ -203,8 +222,14 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
             load_lds4(gd + doff[0] + 4 * sb, &S.da[64 * wave]);
         } else {
             load_lds16(a.ws + sbase + 16 * sb, &S.ws[wave][0]);
+            if constexpr (has_qh(T)) load_lds16(a.ws + qhbase + 32 * sb, &S.ws[wave][1024]);
 #pragma unroll
             for (uint32_t i = 0; i < DAL; i++) load_lds4(gd + doff[i] + 32 * sb, &S.da[64 * (DAL * wave + i)]);
+            if constexpr (has_m(T)) {
+                const uint8_t *gs = reinterpret_cast<const uint8_t *>(a.as);
+#pragma unroll
+                for (uint32_t i = 0; i < DAL; i++) load_lds4(gs + doff[i] + 32 * sb, &S.sa[64 * (DAL * wave + i)]);
+            }
         }
     };
 
@@ -314,9 +339,19 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
                 } else {
                     const uint4 x = *reinterpret_cast<const uint4 *>(blk + 16 * (c ^ (j & 7)));
                     const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
+                    uint32_t qh = 0;
+                    if constexpr (has_qh(T))
+                        qh = *reinterpret_cast<const uint32_t *>(&S.ws[wave][1024 + 16 * (32 * (c / 4) + j) + 4 * (c % 4)]);
 #pragma unroll
-                    for (int i = 0; i < 4; i++) wv[c][i] = int(iq4nl_lookup4((xs[i] >> (4 * h)) & 0x0F0F0F0Fu));
+                    for (int i = 0; i < 4; i++) wv[c][i] = int(low_bit_word<T>(xs[i], qh, h, i));
                 }
+            }
+            float mw[8];
+            if constexpr (has_m(T)) {
+                const uint4 m16 = *reinterpret_cast<const uint4 *>(&S.ws[wave][16 * (32 + j)]);
+                const uint32_t mw4[4] = {m16.x, m16.y, m16.z, m16.w};
+#pragma unroll
+                for (int c = 0; c < 8; c++) mw[c] = f16_bits_to_f32((mw4[c / 2] >> (16 * (c & 1))) & 0xFFFF);
             }
             const uint4 s16 = *reinterpret_cast<const uint4 *>(&S.ws[wave][16 * j]);
             const uint32_t sw4[4] = {s16.x, s16.y, s16.z, s16.w};
@@ -338,6 +373,13 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
 #pragma unroll
                         for (int e = 0; e < 4; e++)
                             acc[t][4 * g + e] = fmaf((float)p[4 * g + e], dw[c] * ds[e], acc[t][4 * g + e]);
+                        if constexpr (has_m(T)) {
+                            const int4 sv = *reinterpret_cast<const int4 *>(&S.sa[c * TOK + 32 * t + 4 * h + 8 * g]);
+                            const int ss[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+                            for (int e = 0; e < 4; e++)
+                                acc[t][4 * g + e] = fmaf(mw[c], ds[e] * (float)ss[e], acc[t][4 * g + e]);
+                        }
                     }
                 }
                 if (t + 1 < TT) load_a(t + 1);
@@ -407,10 +449,21 @@ hipError_t launch_cfg(const MxArgs &a0, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Q4_0..Q5_1: IQ4_NL's tile choice (same quant bytes per block).
+template <int T> hipError_t launch_low4(const MxArgs &a, hipStream_t s, uint32_t b82, uint32_t b42) {
+    if (b82 >= 224) return launch_cfg<T, 8, 2, 2>(a, s);
+    if constexpr (has_qh(T)) { // two K slices would not fit the LDS with the fifth-bit words
+        if (b42 >= 128) return launch_cfg<T, 4, 2, 2>(a, s);
+    } else {
+        if (b42 >= 128 && a.cols >= 1024) return launch_cfg<T, 4, 2, 2, 2>(a, s);
+    }
+    return launch_cfg<T, 4, 1, 2>(a, s);
+}
+
 } // namespace mx
 
 bool mmx_supports(int t, uint32_t rows, uint32_t cols, uint32_t n) {
-    if (t != HKHIP_Q6_K && t != HKHIP_Q8_0 && t != HKHIP_IQ4_NL) return false;
+    if (t != HKHIP_Q6_K && !legacy32(t)) return false;
     if (cols % 256 != 0 || rows == 0 || n == 0) return false;
     // 32-bit per-lane byte offsets: quant plane, scale plane and activations.
     const WLayout W = weight_layout(t, rows, cols);
@@ -431,6 +484,7 @@ hipError_t launch_mmx(int t, const uint8_t *w, uint32_t rows, uint32_t cols, con
     a.n = n;
     a.aqs = reinterpret_cast<const int8_t *>(xq + (q6 ? A.k_qs : A.a8_qs));
     a.ad = reinterpret_cast<const float *>(xq + (q6 ? A.k_d : A.a8_d));
+    a.as = reinterpret_cast<const int32_t *>(xq + A.a8_s);
     a.y = y;
     a.bias = bias;
     a.mode = mode;
@@ -451,6 +505,10 @@ hipError_t launch_mmx(int t, const uint8_t *w, uint32_t rows, uint32_t cols, con
         if (blocks(8, 2) >= 224) return mx::launch_cfg<HKHIP_IQ4_NL, 8, 2, 2>(a, s);
         if (blocks(4, 2) >= 128 && cols >= 1024) return mx::launch_cfg<HKHIP_IQ4_NL, 4, 2, 2, 2>(a, s);
         return mx::launch_cfg<HKHIP_IQ4_NL, 4, 1, 2>(a, s);
+    case HKHIP_Q4_0: return mx::launch_low4<HKHIP_Q4_0>(a, s, blocks(8, 2), blocks(4, 2));
+    case HKHIP_Q4_1: return mx::launch_low4<HKHIP_Q4_1>(a, s, blocks(8, 2), blocks(4, 2));
+    case HKHIP_Q5_0: return mx::launch_low4<HKHIP_Q5_0>(a, s, blocks(8, 2), blocks(4, 2));
+    case HKHIP_Q5_1: return mx::launch_low4<HKHIP_Q5_1>(a, s, blocks(8, 2), blocks(4, 2));
     default: return hipErrorInvalidValue;
     }
 }

@@ -1,20 +1,50 @@
 // Weight upload repack (file layout -> device layout) and the bit-exact dequantizer.
 //
-// The decoders restate src/quant/dequant.zig (q8_0 74-78, scaleMinK4 166-175, q4_k 177-202,
-// q6_k 237-267, iq4_nl 430-437). The library is built with -ffp-contract=off, so every
-// multiply and subtract below rounds separately, as in the Zig source, and the f32 results
-// are bit-identical to hk's CPU decoders.
+// The decoders restate src/quant/dequant.zig (q4_0 24-31, q4_1 33-41, q5_0 43-56, q5_1 58-72,
+// q8_0 74-78, scaleMinK4 166-175, q4_k 177-202, q6_k 237-267, iq4_nl 430-437). The library is
+// built with -ffp-contract=off, so every multiply and add below rounds separately, as in the Zig
+// source, and the f32 results are bit-identical to hk's CPU decoders.
 #include "common.hpp"
 
 namespace hkhip {
 
-// One thread per block: file block b -> quant plane block b (16-byte aligned) + scale plane[b].
+// Side-plane addresses of block b (row b / nbr, column block b % nbr) of a 4/5-bit format.
+struct SideRef {
+    uint64_t d, m, qh; // byte offsets from the side plane
+};
+__host__ __device__ inline SideRef side_ref(int t, uint64_t b, uint32_t nbr) {
+    const SideGeom G = side_geom(t, nbr);
+    const uint64_t r = b / nbr, c = b % nbr, base = r * G.stride;
+    return SideRef{base + 2 * c, base + G.m_off + 2 * c, base + G.qh_off + 4 * c};
+}
+
+// One thread per block: file block b -> quant plane block b (16-byte aligned) + its side-plane
+// entries.
 __global__ void repack_kernel(int t, const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, uint64_t nblocks,
-                              uint64_t scale_off) {
+                              uint64_t scale_off, uint32_t nbr) {
     uint64_t b = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     if (b >= nblocks) return;
     uint16_t *scales = reinterpret_cast<uint16_t *>(dst + scale_off);
-    if (t == HKHIP_Q8_0) {
+    if (t == HKHIP_Q4_0 || t == HKHIP_Q4_1 || t == HKHIP_Q5_0 || t == HKHIP_Q5_1) {
+        // blocks.zig:13-16: d, [m], [qh[4]], qs[16]
+        const uint8_t *s = src + b * block_bytes_dev(t);
+        uint8_t *side = dst + scale_off;
+        const SideRef R = side_ref(t, b, nbr);
+        side[R.d] = s[0];
+        side[R.d + 1] = s[1];
+        uint32_t o = 2;
+        if (has_m(t)) {
+            side[R.m] = s[2];
+            side[R.m + 1] = s[3];
+            o = 4;
+        }
+        if (has_qh(t)) {
+            for (int k = 0; k < 4; k++) side[R.qh + k] = s[o + k];
+            o += 4;
+        }
+        uint8_t *q = dst + b * 16;
+        for (int j = 0; j < 16; j++) q[j] = s[o + j];
+    } else if (t == HKHIP_Q8_0) {
         const uint8_t *s = src + b * 34;
         scales[b] = uint16_t(s[0] | (s[1] << 8));
         uint8_t *q = dst + b * 32;
@@ -38,7 +68,7 @@ hipError_t launch_repack(int t, const uint8_t *src, uint8_t *dst, uint32_t rows,
     if (t == HKHIP_Q4_K) return hipMemcpyAsync(dst, src, L.total, hipMemcpyDeviceToDevice, s);
     if (nb == 0) return hipSuccess;
     uint32_t grid = uint32_t((nb + 255) / 256);
-    repack_kernel<<<grid, 256, 0, s>>>(t, src, dst, nb, L.scale_off);
+    repack_kernel<<<grid, 256, 0, s>>>(t, src, dst, nb, L.scale_off, cols / 32);
     return hipGetLastError();
 }
 
@@ -62,7 +92,23 @@ __global__ void dequant_kernel(int t, const uint8_t *__restrict__ w, uint32_t co
     uint32_t c = uint32_t(i % cols);
     const uint16_t *scales = reinterpret_cast<const uint16_t *>(w + scale_off);
     float v;
-    if (t == HKHIP_Q8_0) {
+    if (t == HKHIP_Q4_0 || t == HKHIP_Q4_1 || t == HKHIP_Q5_0 || t == HKHIP_Q5_1) {
+        const uint64_t b = r * (cols / 32) + c / 32;
+        const uint8_t *side = w + scale_off;
+        const SideRef R = side_ref(t, b, cols / 32);
+        const float d = f16_bits_to_f32(side[R.d] | (side[R.d + 1] << 8));
+        const uint32_t j = c % 32;
+        const uint8_t byte = w[b * 16 + (j & 15)];
+        uint32_t u = j < 16 ? (byte & 0x0F) : (byte >> 4);
+        if (has_qh(t)) {
+            const uint32_t qh = side[R.qh] | (side[R.qh + 1] << 8) | (side[R.qh + 2] << 16) | (uint32_t(side[R.qh + 3]) << 24);
+            u |= ((qh >> j) & 1u) << 4;
+        }
+        if (has_m(t))
+            v = (float)u * d + f16_bits_to_f32(side[R.m] | (side[R.m + 1] << 8));
+        else
+            v = (float)(int(u) - zero_point(t)) * d;
+    } else if (t == HKHIP_Q8_0) {
         uint64_t b = r * (cols / 32) + c / 32;
         float d = f16_bits_to_f32(scales[b]);
         v = (float)(int8_t)w[b * 32 + (c % 32)] * d;

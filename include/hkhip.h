@@ -29,8 +29,12 @@
 extern "C" {
 #endif
 
-/* hk StorageType codes handled by the HIP kernels (src/format.zig:52,75,84). */
+/* hk StorageType codes handled by the HIP kernels (src/format.zig:49-53,75,77,84). */
+#define HKHIP_Q4_0 0x15
 #define HKHIP_Q8_0 0x16
+#define HKHIP_Q4_1 0x17
+#define HKHIP_Q5_0 0x18
+#define HKHIP_Q5_1 0x19
 #define HKHIP_Q4_K 0x42
 #define HKHIP_Q6_K 0x44
 #define HKHIP_IQ4_NL 0x55
@@ -153,6 +157,7 @@ int hkhip_matvec_parts(hkhip_engine *eng, const hkhip_mat *mats, uint32_t nparts
 int hkhip_gemm_host(uint8_t t, const void *w, const float *x, const float *bias, float *y, uint64_t m,
                     uint64_t k, uint64_t n);
 int hkhip_gemv_q8_0(const void *w, const float *x, const float *bias, float *y, uint64_t m, uint64_t k);
+int hkhip_gemv_q4_0(const void *w, const float *x, const float *bias, float *y, uint64_t m, uint64_t k); /* hk.h:452 */
 int hkhip_gemv_q4_k(const void *w, const float *x, const float *bias, float *y, uint64_t m, uint64_t k);
 int hkhip_gemv_q6_k(const void *w, const float *x, const float *bias, float *y, uint64_t m, uint64_t k);
 int hkhip_gemv_iq4_nl(const void *w, const float *x, const float *bias, float *y, uint64_t m, uint64_t k);

@@ -19,8 +19,9 @@ from tests.helpers import PARITY_TOL, load_fixture, parity_err
 
 pytestmark = pytest.mark.gpu
 
-FMTS = [F.Q8_0, F.Q4_K, F.Q6_K, F.IQ4_NL]
-FIXTURES = {F.Q8_0: "q8_0", F.Q4_K: "q4_k", F.Q6_K: "q6_k", F.IQ4_NL: "iq4_nl"}
+FMTS = [F.Q8_0, F.Q4_K, F.Q6_K, F.IQ4_NL, F.Q4_0, F.Q4_1, F.Q5_0, F.Q5_1]
+FIXTURES = F.NAMES
+LOW4 = [F.Q4_0, F.Q4_1, F.Q5_0, F.Q5_1]
 
 
 @pytest.fixture(scope="module")
@@ -184,6 +185,40 @@ def test_mm_chunked_matvec(eng, torch_cuda, t, n):
     want = O.matmul(t, raw, m, k, x, n, bias=bias) + y0
     assert parity_err(got, want) <= PARITY_TOL
 
+@pytest.mark.parametrize("t", LOW4)
+@pytest.mark.parametrize("n", [9, 30, 40])
+def test_low4_rows_not_whole_super_blocks(eng, torch_cuda, t, n):
+    """Q4_0..Q5_1 with K = 96 (three blocks, no whole super-block): the GEMM entry points run
+    decode passes; bias and accumulate."""
+    m, k = 45, 96
+    raw = synth.weights_np(t, m, k, seed=1500 + t)
+    x = synth.activations_np(n, k, seed=1501)
+    bias = np.arange(m, dtype=np.float32)
+    y0 = synth.activations_np(n, m, seed=1502)
+    for path in ("mm", "gemm"):
+        got = run(eng, torch_cuda, t, raw, m, k, x, path=path, bias=bias, mode=1, y0=y0)
+        want = O.matmul(t, raw, m, k, x, n, bias=bias) + y0
+        assert parity_err(got, want) <= PARITY_TOL
+
+
+def test_host_gemv_q4_0_symbol(torch_cuda):
+    """hkhip_gemv_q4_0 stands in for hk_gemv_q4_0 (hk.h:452): host pointers, bias."""
+    import ctypes
+    from hk_amd import _lib
+
+    m, k = 19, 512
+    raw = np.ascontiguousarray(synth.weights_np(F.Q4_0, m, k, seed=1600))
+    x = synth.activations_np(1, k, seed=1601)[0]
+    bias = np.linspace(-2, 2, m).astype(np.float32)
+    y = np.full(m, np.nan, np.float32)
+    P = ctypes.c_void_p
+    rc = _lib.lib().hkhip_gemv_q4_0(raw.ctypes.data_as(P), x.ctypes.data_as(P), bias.ctypes.data_as(P),
+                                    y.ctypes.data_as(P), m, k)
+    assert rc == 0
+    want = O.matmul(F.Q4_0, raw, m, k, x[None], 1, bias=bias)[0]
+    assert parity_err(y, want) <= PARITY_TOL
+
+
 def test_host_gemv_entry_points(torch_cuda):
     from hk_amd import gemm, gemv
 
@@ -208,7 +243,7 @@ def test_errors(eng, torch_cuda):
         eng.upload(np.zeros(100 * 34 // 32, np.uint8), F.Q8_0, 1, 100)
     assert e.value.code == -2  # UNSUPPORTED_SHAPE: cols not a multiple of 32
     with pytest.raises(HipError) as e:
-        eng.upload(np.zeros(18, np.uint8), 0x15, 1, 32)  # Q4_0: not on this path
+        eng.upload(np.zeros(176, np.uint8), 0x43, 1, 256)  # Q5_K: not on this path
     assert e.value.code == -1
     raw = synth.weights_np(F.Q4_K, 4, 256, seed=1)
     w = eng.upload(raw, F.Q4_K, 4, 256)
@@ -253,7 +288,8 @@ def test_baseline_prefill_shapes(eng, torch_cuda, t, m, k):
 
 
 @pytest.mark.parametrize("t,m,k,n,mode", [(F.IQ4_NL, 4000, 1280, 300, 1), (F.IQ4_NL, 9000, 512, 260, 0),
-                                          (F.Q6_K, 4100, 768, 100, 1), (F.Q8_0, 3000, 1024, 70, 1)])
+                                          (F.Q6_K, 4100, 768, 100, 1), (F.Q8_0, 3000, 1024, 70, 1)] +
+                         [(t, 4000, 1280, 300, 1) for t in LOW4] + [(t, 9000, 512, 260, 0) for t in LOW4])
 def test_gemm_configs_other_formats(eng, torch_cuda, t, m, k, n, mode):
     """The Q6_K / Q8_0 / IQ4_NL GEMM's configurations: IQ4_NL split over two K slices (5
     super-blocks) and its 256-row tile; ragged rows and tokens, bias, accumulate."""
@@ -346,6 +382,9 @@ def test_matvec_parts_large_k(eng, torch_cuda, t, k, n):
     # rows split over 2-8 waves (K slices), partials combined in LDS
     (F.Q4_K, 14336, 8), (F.Q4_K, 14336, 2), (F.Q4_K, 14336, 3), (F.Q4_K, 28672, 1),
     (F.Q6_K, 14336, 8), (F.Q6_K, 20480, 1), (F.Q8_0, 20480, 8), (F.IQ4_NL, 14336, 4),
+    # the 4/5-bit formats: register kernel C = 8, LDS kernel, K slices
+    (F.Q4_0, 16384, 1), (F.Q4_1, 16416, 1), (F.Q5_0, 8192, 2), (F.Q5_1, 4096, 8),
+    (F.Q4_0, 14336, 4), (F.Q4_1, 14336, 8), (F.Q5_0, 20480, 1), (F.Q5_1, 16384, 2),
 ])
 @pytest.mark.parametrize("prepared", [False, True])
 def test_matvec_kernel_variants(eng, torch_cuda, t, k, n, prepared):
