@@ -66,7 +66,7 @@ def main():
     import torch
 
     from hk_amd import Engine, formats as F, synth
-    FMT_NAME = {F.Q4_K: "q4_k", F.Q6_K: "q6_k", F.Q8_0: "q8_0", F.IQ4_NL: "iq4_nl"}
+    FMT_NAME = F.NAMES
 
     torch.cuda.init()
     dev = torch.device("cuda:0")
@@ -196,7 +196,8 @@ def main():
         for (name, t, m_, k_) in [("llama8b-ffn-up", F.Q4_K, FF, H), ("qwen3-0.6b-ffn-up", F.Q4_K, 3072, 1024),
                                   ("qwen3-0.6b-ffn-down", F.Q4_K, 1024, 3072),
                                   ("llama8b-ffn-down", F.Q4_K, H, FF),
-                                  ("llama8b-ffn-up", F.IQ4_NL, FF, H), ("llama8b-ffn-down", F.Q6_K, H, FF)]:
+                                  ("llama8b-ffn-up", F.IQ4_NL, FF, H), ("llama8b-ffn-down", F.Q6_K, H, FF)] + \
+                                 [("llama8b-ffn-up", t, FF, H) for t in (F.Q4_0, F.Q4_1, F.Q5_0, F.Q5_1)]:
             n = 512
             reuse = layers[0]["gate"] if (t, m_, k_) == (F.Q4_K, FF, H) else None
             w = reuse or upload_synth(t, m_, k_, synth.seed_for(3, m_ + k_ + t))
@@ -257,7 +258,8 @@ def main():
                                       gbs=round(b8_bytes / (us8 * 1e-6) / 1e9, 1),
                                       frac_hbm_peak=round(b8_bytes / (us8 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4))
         mv = []
-        for (name, t, m_, k_) in [("llama8b-ffn-up", F.IQ4_NL, FF, H), ("llama8b-ffn-down", F.Q6_K, H, FF)]:
+        for (name, t, m_, k_) in [("llama8b-ffn-up", F.IQ4_NL, FF, H), ("llama8b-ffn-down", F.Q6_K, H, FF)] + \
+                                 [("llama8b-ffn-up", t, FF, H) for t in (F.Q4_0, F.Q4_1, F.Q5_0, F.Q5_1)]:
             ws = [upload_synth(t, m_, k_, synth.seed_for(5, 100 * t + i)) for i in range(12)]
             xv = torch.randn(1, k_, device=dev)
             yv = torch.empty(1, m_, device=dev)
