@@ -11,23 +11,25 @@ Q4_1 = 0x17
 Q5_0 = 0x18
 Q5_1 = 0x19
 Q4_K = 0x42
+Q5_K = 0x43
 Q6_K = 0x44
 IQ4_NL = 0x55
+IQ4_XS = 0x56
 
 NAMES = {Q8_0: "q8_0", Q4_K: "q4_k", Q6_K: "q6_k", IQ4_NL: "iq4_nl",
-         Q4_0: "q4_0", Q4_1: "q4_1", Q5_0: "q5_0", Q5_1: "q5_1"}
+         Q4_0: "q4_0", Q4_1: "q4_1", Q5_0: "q5_0", Q5_1: "q5_1", Q5_K: "q5_k", IQ4_XS: "iq4_xs"}
 BY_NAME = {v: k for k, v in NAMES.items()}
 
 # weights per block, bytes per block (blocks.zig:49-72 size asserts)
 INFO = {Q8_0: (32, 34), IQ4_NL: (32, 18), Q4_K: (256, 144), Q6_K: (256, 210),
-        Q4_0: (32, 18), Q4_1: (32, 20), Q5_0: (32, 22), Q5_1: (32, 24)}
+        Q4_0: (32, 18), Q4_1: (32, 20), Q5_0: (32, 22), Q5_1: (32, 24), Q5_K: (256, 176), IQ4_XS: (256, 136)}
 # The 32-weight formats (A8 activations), and those of them with an offset m per block.
 LEGACY = (Q8_0, IQ4_NL, Q4_0, Q4_1, Q5_0, Q5_1)
 WITH_M = (Q4_1, Q5_1)
 
 # Activation kind each format is dotted against (vecdot.zig:185-191).
 ACT_A8, ACT_Q8K = 0, 1
-ACT_KIND = {Q4_K: ACT_Q8K, Q6_K: ACT_Q8K, **{t: ACT_A8 for t in LEGACY}}
+ACT_KIND = {Q4_K: ACT_Q8K, Q5_K: ACT_Q8K, Q6_K: ACT_Q8K, IQ4_XS: ACT_Q8K, **{t: ACT_A8 for t in LEGACY}}
 
 # Bits per weight in the file layout (the numerator of the bandwidth roofline).
 BPW = {t: 8.0 * b / e for t, (e, b) in INFO.items()}

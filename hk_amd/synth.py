@@ -11,6 +11,8 @@ CPU baseline) or torch (device, for multi-GB benchmark matrices).
   IQ4_NL indices uniform;                     d = |N(0,0.02)|
   Q4_0 / Q5_0  quants uniform;                d = |N(0,0.02)| / 8 (/ 16)
   Q4_1 / Q5_1  quants uniform;                d = |N(0,0.02)| / 16 (/ 32), m = -|N(0,0.02)|
+  Q5_K   as Q4_K (qh uniform);                d = dmin = |N(0,0.02)| / 63
+  IQ4_XS indices and scale bits uniform;      d = |N(0,0.02)| / 1024
 """
 from __future__ import annotations
 
@@ -39,9 +41,11 @@ def weights_np(t: int, rows: int, cols: int, seed: int) -> np.ndarray:
     if t == formats.Q8_0:
         raw[:, 2:34] = rng.integers(-127, 128, size=(nb, 32)).astype(np.int8).view(np.uint8)
         raw[:, 0:2] = _f16_scales_np(rng, nb, 127.0 / 4.0).view(np.uint8).reshape(nb, 2)
-    elif t == formats.Q4_K:
+    elif t in (formats.Q4_K, formats.Q5_K):
         raw[:, 0:2] = _f16_scales_np(rng, nb, 63.0).view(np.uint8).reshape(nb, 2)
         raw[:, 2:4] = _f16_scales_np(rng, nb, 63.0).view(np.uint8).reshape(nb, 2)
+    elif t == formats.IQ4_XS:
+        raw[:, 0:2] = _f16_scales_np(rng, nb, 1024.0).view(np.uint8).reshape(nb, 2)
     elif t == formats.Q6_K:
         raw[:, 192:208] = rng.integers(-32, 32, size=(nb, 16)).astype(np.int8).view(np.uint8)
         raw[:, 208:210] = _f16_scales_np(rng, nb, 127.0).view(np.uint8).reshape(nb, 2)
@@ -85,9 +89,11 @@ def weights_torch(t: int, rows: int, cols: int, seed: int, device="cuda"):
     if t == formats.Q8_0:
         raw[:, 2:34] = torch.randint(-127, 128, (nb, 32), device=device, generator=g).to(torch.int8).view(torch.uint8)
         raw[:, 0:2] = scales(127.0 / 4.0)
-    elif t == formats.Q4_K:
+    elif t in (formats.Q4_K, formats.Q5_K):
         raw[:, 0:2] = scales(63.0)
         raw[:, 2:4] = scales(63.0)
+    elif t == formats.IQ4_XS:
+        raw[:, 0:2] = scales(1024.0)
     elif t == formats.Q6_K:
         raw[:, 192:208] = torch.randint(-32, 32, (nb, 16), device=device, generator=g).to(torch.int8).view(torch.uint8)
         raw[:, 208:210] = scales(127.0)

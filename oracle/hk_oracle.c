@@ -56,7 +56,7 @@ static inline float h16(const uint8_t *p) { return hko_f16_to_f32(rd16(p)); }
 int hko_block_elems(int t) {
     switch (t) {
     case HKO_Q8_0: case HKO_IQ4_NL: case HKO_Q4_0: case HKO_Q4_1: case HKO_Q5_0: case HKO_Q5_1: return 32;
-    case HKO_Q4_K: case HKO_Q6_K: return QK_K;
+    case HKO_Q4_K: case HKO_Q5_K: case HKO_Q6_K: case HKO_IQ4_XS: return QK_K;
     default: return 0;
     }
 }
@@ -67,6 +67,8 @@ int hko_block_bytes(int t) {
     case HKO_IQ4_NL: return 18; /* blocks.zig:34 */
     case HKO_Q4_K: return 144;  /* blocks.zig:21 */
     case HKO_Q6_K: return 210;  /* blocks.zig:23 */
+    case HKO_Q5_K: return 176;  /* blocks.zig:22 */
+    case HKO_IQ4_XS: return 136; /* blocks.zig:35 */
     case HKO_Q4_0: return 18;   /* blocks.zig:13 */
     case HKO_Q4_1: return 20;   /* blocks.zig:14 */
     case HKO_Q5_0: return 22;   /* blocks.zig:15 */
@@ -79,7 +81,7 @@ int hko_act_kind(int t) {
     switch (t) {
     case HKO_Q8_0: case HKO_IQ4_NL: case HKO_Q4_0: case HKO_Q4_1: case HKO_Q5_0: case HKO_Q5_1:
         return 0; /* vecdot.zig:187 */
-    case HKO_Q4_K: case HKO_Q6_K: return 1;   /* vecdot.zig:188 */
+    case HKO_Q4_K: case HKO_Q5_K: case HKO_Q6_K: case HKO_IQ4_XS: return 1; /* vecdot.zig:188 */
     default: return -1;
     }
 }
@@ -211,6 +213,46 @@ static void deq_q6_k(const uint8_t *b, float *out) {
     }
 }
 
+/* dequant.zig:204-235: Q4_K's decode with the fifth bit of weight l of chunk c's low (high) half
+ * at bit 2c (2c + 1) of qh[l]. */
+static void deq_q5_k(const uint8_t *b, float *out) {
+    float d = h16(b), min = h16(b + 2);
+    const uint8_t *qh = b + 16, *qs = b + 48;
+    for (int c = 0; c < 4; c++) {
+        uint8_t sc, mn;
+        hko_scale_min_k4(2 * c, b + 4, &sc, &mn);
+        float d1 = d * (float)sc, m1 = min * (float)mn;
+        hko_scale_min_k4(2 * c + 1, b + 4, &sc, &mn);
+        float d2 = d * (float)sc, m2 = min * (float)mn;
+        for (int l = 0; l < 32; l++) {
+            uint32_t lo = (qs[32 * c + l] & 0x0F) + ((qh[l] >> (2 * c)) & 1 ? 16 : 0);
+            uint32_t hi = (qs[32 * c + l] >> 4) + ((qh[l] >> (2 * c + 1)) & 1 ? 16 : 0);
+            out[64 * c + l] = d1 * (float)lo - m1;
+            out[64 * c + 32 + l] = d2 * (float)hi - m2;
+        }
+    }
+}
+
+/* IQ4_XS sub-block scale ls = (6-bit scale) - 32 (dequant.zig:443-447, vecdot.zig:577-582). */
+static int32_t iq4xs_ls(const uint8_t *b, int ib) {
+    uint32_t scales_h = (uint32_t)b[2] | ((uint32_t)b[3] << 8);
+    uint32_t lo = (b[4 + ib / 2] >> (4 * (ib % 2))) & 0x0F, hi = (scales_h >> (2 * ib)) & 3;
+    return (int32_t)(lo | (hi << 4)) - 32;
+}
+
+/* dequant.zig:439-455 */
+static void deq_iq4_xs(const uint8_t *b, float *out) {
+    float d = h16(b);
+    for (int ib = 0; ib < 8; ib++) {
+        float dl = d * (float)iq4xs_ls(b, ib);
+        const uint8_t *qs = b + 8 + 16 * ib;
+        for (int j = 0; j < 16; j++) {
+            out[32 * ib + j] = dl * (float)kvalues_iq4nl[qs[j] & 0x0F];
+            out[32 * ib + j + 16] = dl * (float)kvalues_iq4nl[qs[j] >> 4];
+        }
+    }
+}
+
 /* dequant.zig:430-437 */
 static void deq_iq4_nl(const uint8_t *b, float *out) {
     float d = h16(b);
@@ -235,6 +277,8 @@ int hko_dequantize_row(int t, const uint8_t *src, size_t src_len, float *dst, si
         case HKO_Q4_K: deq_q4_k(b, o); break;
         case HKO_Q6_K: deq_q6_k(b, o); break;
         case HKO_IQ4_NL: deq_iq4_nl(b, o); break;
+        case HKO_Q5_K: deq_q5_k(b, o); break;
+        case HKO_IQ4_XS: deq_iq4_xs(b, o); break;
         case HKO_Q4_0: case HKO_Q4_1: case HKO_Q5_0: case HKO_Q5_1: deq_low_bit(t, b, o); break;
         }
     }
@@ -360,19 +404,24 @@ static float dot_low_bit(int t, const uint8_t *row, size_t nb, const hko_block_a
 }
 
 /* vecdot.zig:482-522 k4Block / dotQ4K */
-static float dot_q4_k(const uint8_t *row, size_t nsb, const hko_block_q8k *a) {
+static float dot_q4_k(int t, const uint8_t *row, size_t nsb, const hko_block_q8k *a) {
     float accf[8] = {0}, corr[8] = {0};
     int32_t lo[32], hi[32], t0[8], t1[8];
+    const int five = t == HKO_Q5_K, qoff = five ? 48 : 16;
     for (size_t i = 0; i < nsb; i++) {
-        const uint8_t *b = row + i * 144;
+        const uint8_t *b = row + i * (size_t)hko_block_bytes(t);
         uint8_t sc[8], mn[8];
         hko_scales_mins_k4_words(b + 4, sc, mn);
         int32_t acci[8] = {0};
         for (int p = 0; p < 4; p++) {
-            const uint8_t *q = b + 16 + 32 * p;
+            const uint8_t *q = b + qoff + 32 * p;
             for (int j = 0; j < 32; j++) {
                 lo[j] = q[j] & 0x0F;
                 hi[j] = q[j] >> 4;
+                if (five) { /* k4Block has_high (vecdot.zig:492-495) */
+                    lo[j] |= ((b[16 + j] >> (2 * p)) & 1) << 4;
+                    hi[j] |= ((b[16 + j] >> (2 * p + 1)) & 1) << 4;
+                }
             }
             dp32(t0, lo, a[i].qs + p * 64);
             dp32(t1, hi, a[i].qs + p * 64 + 32);
@@ -387,6 +436,30 @@ static float dot_q4_k(const uint8_t *row, size_t nsb, const hko_block_q8k *a) {
         }
     }
     return reduce8(accf) - reduce8(corr);
+}
+
+/* vecdot.zig:572-597 dotIQ4XS: per 32-weight sub-block the signed codebook dot (dps lanes) times
+ * its scale, then one fma per super-block. */
+static float dot_iq4_xs(const uint8_t *row, size_t nsb, const hko_block_q8k *a) {
+    float accf[8] = {0};
+    int32_t w[32], t0[8];
+    for (size_t i = 0; i < nsb; i++) {
+        const uint8_t *b = row + i * 136;
+        int32_t acci[8] = {0};
+        for (int ib = 0; ib < 8; ib++) {
+            const uint8_t *qs = b + 8 + 16 * ib;
+            for (int j = 0; j < 16; j++) {
+                w[j] = kvalues_iq4nl[qs[j] & 0x0F];
+                w[j + 16] = kvalues_iq4nl[qs[j] >> 4];
+            }
+            dp32(t0, w, a[i].qs + 32 * ib);
+            int32_t ls = iq4xs_ls(b, ib);
+            for (int L = 0; L < 8; L++) acci[L] += t0[L] * ls;
+        }
+        float s = h16(b) * a[i].d;
+        for (int L = 0; L < 8; L++) accf[L] = fmaf((float)acci[L], s, accf[L]);
+    }
+    return reduce8(accf);
 }
 
 /* vecdot.zig:533-570 dotQ6K */
@@ -424,7 +497,8 @@ float hko_dot_row(int t, const uint8_t *row, size_t k, const hko_block_a8 *a8, c
     switch (t) {
     case HKO_Q8_0: case HKO_IQ4_NL: return dot_legacy(t, row, k / 32, a8);
     case HKO_Q4_0: case HKO_Q4_1: case HKO_Q5_0: case HKO_Q5_1: return dot_low_bit(t, row, k / 32, a8);
-    case HKO_Q4_K: return dot_q4_k(row, k / QK_K, q8k);
+    case HKO_Q4_K: case HKO_Q5_K: return dot_q4_k(t, row, k / QK_K, q8k);
+    case HKO_IQ4_XS: return dot_iq4_xs(row, k / QK_K, q8k);
     case HKO_Q6_K: return dot_q6_k(row, k / QK_K, q8k);
     default: return NAN;
     }
@@ -438,13 +512,24 @@ float hko_dot_row(int t, const uint8_t *row, size_t k, const hko_block_a8 *a8, c
 
 /* unpack.zig:81-160 for Q4_K and Q6_K: vals unsigned, sc and mn per 16 weights. */
 typedef struct {
-    uint8_t vals[256];
+    int16_t vals[256]; /* unsigned quants, or IQ4_XS's signed codebook values */
     int32_t sc[16], mn[16];
     float d, e;
 } kblock;
 
 static void unpack_k(int t, const uint8_t *b, kblock *o) {
-    if (t == HKO_Q4_K) {
+    if (t == HKO_IQ4_XS) { /* unpack.zig:160-179: signed codebook values, no mins */
+        o->d = o->e = h16(b);
+        for (int ib = 0; ib < 8; ib++) {
+            o->sc[2 * ib] = o->sc[2 * ib + 1] = iq4xs_ls(b, ib);
+            o->mn[2 * ib] = o->mn[2 * ib + 1] = 0;
+            for (int j = 0; j < 16; j++) {
+                o->vals[32 * ib + j] = kvalues_iq4nl[b[8 + 16 * ib + j] & 0x0F];
+                o->vals[32 * ib + j + 16] = kvalues_iq4nl[b[8 + 16 * ib + j] >> 4];
+            }
+        }
+    } else if (t == HKO_Q4_K || t == HKO_Q5_K) { /* unpack.zig:118-139 */
+        const int five = t == HKO_Q5_K, qoff = five ? 48 : 16;
         o->d = h16(b);
         o->e = h16(b + 2);
         for (int j = 0; j < 8; j++) {
@@ -455,8 +540,8 @@ static void unpack_k(int t, const uint8_t *b, kblock *o) {
         }
         for (int c = 0; c < 4; c++)
             for (int l = 0; l < 32; l++) {
-                o->vals[64 * c + l] = b[16 + 32 * c + l] & 0x0F;
-                o->vals[64 * c + 32 + l] = b[16 + 32 * c + l] >> 4;
+                o->vals[64 * c + l] = (b[qoff + 32 * c + l] & 0x0F) + (five && ((b[16 + l] >> (2 * c)) & 1) ? 16 : 0);
+                o->vals[64 * c + 32 + l] = (b[qoff + 32 * c + l] >> 4) + (five && ((b[16 + l] >> (2 * c + 1)) & 1) ? 16 : 0);
             }
     } else {
         const uint8_t *ql = b, *qh = b + 128;

@@ -26,8 +26,10 @@ extern "C" {
 #define HKO_Q5_0 0x18
 #define HKO_Q5_1 0x19
 #define HKO_Q4_K 0x42
+#define HKO_Q5_K 0x43
 #define HKO_Q6_K 0x44
 #define HKO_IQ4_NL 0x55
+#define HKO_IQ4_XS 0x56
 
 /* Activation blocks, byte-identical to the reference structs. */
 typedef struct {

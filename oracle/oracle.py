@@ -17,6 +17,7 @@ LIB_PATH = os.path.join(HERE, "libhk_oracle.so")
 
 Q8_0, Q4_K, Q6_K, IQ4_NL = 0x16, 0x42, 0x44, 0x55
 Q4_0, Q4_1, Q5_0, Q5_1 = 0x15, 0x17, 0x18, 0x19
+Q5_K, IQ4_XS = 0x43, 0x56
 _A8 = (Q8_0, IQ4_NL, Q4_0, Q4_1, Q5_0, Q5_1)
 
 A8_DTYPE = np.dtype([("d", "<f4"), ("s", "<i4"), ("qs", "i1", (32,))])  # vecdot.zig:22-26
@@ -59,11 +60,11 @@ def _p(a: np.ndarray | None):
 
 
 def block_elems(t: int) -> int:
-    return {Q4_K: 256, Q6_K: 256, **{f: 32 for f in _A8}}[t]
+    return {Q4_K: 256, Q6_K: 256, Q5_K: 256, IQ4_XS: 256, **{f: 32 for f in _A8}}[t]
 
 
 def block_bytes(t: int) -> int:
-    return {Q8_0: 34, IQ4_NL: 18, Q4_K: 144, Q6_K: 210, Q4_0: 18, Q4_1: 20, Q5_0: 22, Q5_1: 24}[t]
+    return {Q8_0: 34, IQ4_NL: 18, Q4_K: 144, Q6_K: 210, Q4_0: 18, Q4_1: 20, Q5_0: 22, Q5_1: 24, Q5_K: 176, IQ4_XS: 136}[t]
 
 
 def act_kind(t: int) -> int:

@@ -23,9 +23,10 @@ from hk_amd import synth
 from oracle import oracle as O
 from tests.helpers import load_fixture
 
-FMTS = [F.Q8_0, F.Q4_K, F.Q6_K, F.IQ4_NL, F.Q4_0, F.Q4_1, F.Q5_0, F.Q5_1]
+FMTS = [F.Q8_0, F.Q4_K, F.Q6_K, F.IQ4_NL, F.Q4_0, F.Q4_1, F.Q5_0, F.Q5_1, F.Q5_K, F.IQ4_XS]
 FIXTURES = F.NAMES
-GGML_TYPE = {F.Q8_0: 8, F.Q4_K: 12, F.Q6_K: 14, F.IQ4_NL: 20, F.Q4_0: 2, F.Q4_1: 3, F.Q5_0: 6, F.Q5_1: 7}
+GGML_TYPE = {F.Q8_0: 8, F.Q4_K: 12, F.Q6_K: 14, F.IQ4_NL: 20, F.Q4_0: 2, F.Q4_1: 3, F.Q5_0: 6, F.Q5_1: 7,
+             F.Q5_K: 13, F.IQ4_XS: 23}
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -123,6 +124,44 @@ def test_decode_closed_forms_on_constructed_blocks(t):
         want = [np.float32(uj) * np.float32(0.5) + np.float32(-1.25) if has_m else np.float32(uj - zp) * np.float32(0.5)
                 for uj in u]
         assert np.array_equal(O.dequantize(t, b, 32), np.array(want, np.float32))
+    elif t == F.Q5_K:
+        # Q4_K's block with qh[32] before qs: weight l of chunk c's low (high) half takes bit 2c
+        # (2c + 1) of qh[l] as its fifth bit.
+        b = np.zeros(176, np.uint8)
+        b[0:2] = np.array([1.0], np.float16).view(np.uint8)
+        b[2:4] = np.array([0.25], np.float16).view(np.uint8)
+        for j in range(8):
+            sc, mn = j + 1, 2 * j
+            if j < 4:
+                b[4 + j], b[8 + j] = sc, mn
+            else:
+                b[8 + j] = sc | (mn << 4)
+        b[16:48] = (np.arange(32) * 37 % 256).astype(np.uint8)
+        b[48:176] = 0x53
+        got = O.dequantize(t, b, 256)
+        for c in range(4):
+            for half in range(2):
+                j = 2 * c + half
+                for l in range(32):
+                    u = (3 if half == 0 else 5) + 16 * ((int(b[16 + l]) >> j) & 1)
+                    assert got[64 * c + 32 * half + l] == np.float32(np.float32(j + 1) * np.float32(u) - np.float32(0.25 * 2 * j))
+    elif t == F.IQ4_XS:
+        # d, scales_h (2 bits per sub-block), scales_l (4 bits per sub-block), 16 B of indices per
+        # sub-block; sub-block scale = 6-bit value - 32.
+        b = np.zeros(136, np.uint8)
+        b[0:2] = np.array([0.5], np.float16).view(np.uint8)
+        ls6 = [0, 63, 32, 31, 1, 40, 17, 50]
+        sh = sum((v >> 4) << (2 * ib) for ib, v in enumerate(ls6))
+        b[2:4] = np.array([sh], "<u2").view(np.uint8)
+        for ib, v in enumerate(ls6):
+            b[4 + ib // 2] |= (v & 15) << (4 * (ib % 2))
+        b[8:136] = np.tile((np.arange(16) | ((15 - np.arange(16)) << 4)).astype(np.uint8), 8)
+        got = O.dequantize(t, b, 256)
+        kv = F.KVALUES_IQ4NL
+        for ib, v in enumerate(ls6):
+            dl = np.float32(0.5) * np.float32(v - 32)
+            want = [dl * np.float32(kv[j]) for j in range(16)] + [dl * np.float32(kv[15 - j]) for j in range(16)]
+            assert np.array_equal(got[32 * ib:32 * ib + 32], np.array(want, np.float32))
     else:  # Q6_K
         b = np.zeros(210, np.uint8)
         b[208:210] = np.array([0.5], np.float16).view(np.uint8)
