@@ -197,7 +197,7 @@ def main():
                                   ("qwen3-0.6b-ffn-down", F.Q4_K, 1024, 3072),
                                   ("llama8b-ffn-down", F.Q4_K, H, FF),
                                   ("llama8b-ffn-up", F.IQ4_NL, FF, H), ("llama8b-ffn-down", F.Q6_K, H, FF)] + \
-                                 [("llama8b-ffn-up", t, FF, H) for t in (F.Q4_0, F.Q4_1, F.Q5_0, F.Q5_1)]:
+                                 [("llama8b-ffn-up", t, FF, H) for t in (F.Q4_0, F.Q4_1, F.Q5_0, F.Q5_1, F.Q5_K, F.IQ4_XS)]:
             n = 512
             reuse = layers[0]["gate"] if (t, m_, k_) == (F.Q4_K, FF, H) else None
             w = reuse or upload_synth(t, m_, k_, synth.seed_for(3, m_ + k_ + t))
@@ -259,7 +259,7 @@ def main():
                                       frac_hbm_peak=round(b8_bytes / (us8 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4))
         mv = []
         for (name, t, m_, k_) in [("llama8b-ffn-up", F.IQ4_NL, FF, H), ("llama8b-ffn-down", F.Q6_K, H, FF)] + \
-                                 [("llama8b-ffn-up", t, FF, H) for t in (F.Q4_0, F.Q4_1, F.Q5_0, F.Q5_1)]:
+                                 [("llama8b-ffn-up", t, FF, H) for t in (F.Q4_0, F.Q4_1, F.Q5_0, F.Q5_1, F.Q5_K, F.IQ4_XS)]:
             ws = [upload_synth(t, m_, k_, synth.seed_for(5, 100 * t + i)) for i in range(12)]
             xv = torch.randn(1, k_, device=dev)
             yv = torch.empty(1, m_, device=dev)

@@ -18,7 +18,7 @@ inline int block_elems(int t) {
     switch (t) {
     case HKHIP_Q8_0: case HKHIP_IQ4_NL: case HKHIP_Q4_0: case HKHIP_Q4_1: case HKHIP_Q5_0: case HKHIP_Q5_1:
         return 32;
-    case HKHIP_Q4_K: case HKHIP_Q6_K: return 256;
+    case HKHIP_Q4_K: case HKHIP_Q5_K: case HKHIP_Q6_K: case HKHIP_IQ4_XS: return 256;
     default: return 0;
     }
 }
@@ -31,6 +31,8 @@ inline int block_bytes(int t) {
     case HKHIP_IQ4_NL: return 18;
     case HKHIP_Q4_K: return 144;
     case HKHIP_Q6_K: return 210;
+    case HKHIP_Q5_K: return 176;
+    case HKHIP_IQ4_XS: return 136;
     case HKHIP_Q4_0: return 18;
     case HKHIP_Q4_1: return 20;
     case HKHIP_Q5_0: return 22;
@@ -59,12 +61,14 @@ __host__ __device__ constexpr SideGeom side_geom(int t, uint32_t nbr) {
                     has_qh(t) ? (((has_m(t) ? 4 : 2) * nbr + 3) & ~3u) + 4 * nbr : (has_m(t) ? 4 : 2) * nbr};
 }
 
-// Device layout of a weight matrix. Q4_K keeps the 144-byte file blocks (already 16-byte
-// aligned). The 2-byte-aligned formats are split at upload into a quant plane whose blocks
+// Device layout of a weight matrix. Q4_K and Q5_K keep the 144- / 176-byte file blocks (already
+// 16-byte aligned). The 2-byte-aligned formats are split at upload into a quant plane whose blocks
 // are 16-byte aligned and a plane of f16 scales, one per block, in block order:
 //   Q8_0   quant plane: 32 B per block (qs)        scale plane: d
 //   IQ4_NL quant plane: 16 B per block (qs)        scale plane: d
 //   Q6_K   quant plane: 208 B per block (ql qh sc) scale plane: d
+//   IQ4_XS quant plane: 128 B per block (qs)       side plane: the 8-B header (d, scales_h,
+//                                                   scales_l), block order
 //   Q4_0 / Q4_1 / Q5_0 / Q5_1  quant plane: 16 B per block (qs, file nibble order)
 //          side plane, one record per row of nbr = cols/32 blocks: d[nbr] f16, then m[nbr] f16
 //          (Q4_1, Q5_1), then, from the next 4-byte boundary, qh[nbr] u32 (Q5_0, Q5_1; bit j =
@@ -85,14 +89,17 @@ inline WLayout weight_layout(int t, uint32_t rows, uint32_t cols) {
     case HKHIP_Q8_0: L.qblock = 32; break;
     case HKHIP_IQ4_NL: case HKHIP_Q4_0: case HKHIP_Q4_1: case HKHIP_Q5_0: case HKHIP_Q5_1: L.qblock = 16; break;
     case HKHIP_Q6_K: L.qblock = 208; break;
+    case HKHIP_Q5_K: L.qblock = 176; break;
+    case HKHIP_IQ4_XS: L.qblock = 128; break;
     }
     L.quant_bytes = nb * L.qblock;
-    if (t == HKHIP_Q4_K) {
+    if (t == HKHIP_Q4_K || t == HKHIP_Q5_K) {
         L.scale_off = L.quant_bytes;
         L.total = L.quant_bytes;
     } else {
         L.scale_off = align256(L.quant_bytes);
-        const uint64_t side = block_elems(t) == 32 ? uint64_t(rows) * side_geom(t, cols / 32).stride : nb * 2;
+        const uint64_t side = block_elems(t) == 32 ? uint64_t(rows) * side_geom(t, cols / 32).stride
+                            : nb * (t == HKHIP_IQ4_XS ? 8 : 2);
         L.total = align256(L.scale_off + side); // the kernels read the scales as aligned words
     }
     return L;

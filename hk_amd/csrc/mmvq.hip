@@ -91,13 +91,16 @@ struct RowRef {
 
 template <int T> struct MvFmt;
 
-template <> struct MvFmt<HKHIP_Q4_K> {
+// Q4_K and Q5_K (hk's file blocks, 144 / 176 B; Q5_K adds qh[32] before qs).
+template <int T> struct MvK4 {
     static constexpr bool kq = true;
+    static constexpr bool five = (T == HKHIP_Q5_K);
+    static constexpr uint32_t BB = five ? 176 : 144, QO = five ? 48 : 16; // block bytes, qs offset
     __device__ static uint32_t units(uint32_t K) { return K / 64; }
     __device__ static uint32_t lds_chunk(uint32_t c) { return swz<3>(c); }
     __device__ static uint32_t bs_index(uint32_t g) { return g; }
     struct W {
-        uint4 h, q0, q1;
+        uint4 h, q0, q1, x0, x1; // x: Q5_K's qh[32]
     };
     struct AU {
         uint32_t q[16];
@@ -105,7 +108,7 @@ template <> struct MvFmt<HKHIP_Q4_K> {
         float d;
     };
     __device__ static RowRef row(const uint8_t *w, const uint16_t *, uint32_t r, uint32_t K) {
-        return RowRef{w + uint64_t(r) * (K / 256) * 144, nullptr};
+        return RowRef{w + uint64_t(r) * (K / 256) * BB, nullptr};
     }
     // Offset in the token of the j-th 16-value chunk of unit u (natural order; chunks ascend in j).
     __device__ static uint32_t chunk_off(uint32_t u, uint32_t j) { return 64 * u + 16 * j; }
@@ -119,8 +122,16 @@ template <> struct MvFmt<HKHIP_Q4_K> {
         return a;
     }
     __device__ static W load(const RowRef &R, uint32_t u) {
-        const uint8_t *blk = R.w + (u >> 2) * 144;
-        return W{ldw(blk), ldw(blk + 16 + 32 * (u & 3)), ldw(blk + 32 + 32 * (u & 3))};
+        const uint8_t *blk = R.w + (u >> 2) * BB;
+        W w;
+        w.h = ldw(blk);
+        w.q0 = ldw(blk + QO + 32 * (u & 3));
+        w.q1 = ldw(blk + QO + 16 + 32 * (u & 3));
+        if constexpr (five) {
+            w.x0 = ldw(blk + 16);
+            w.x1 = ldw(blk + 32);
+        }
+        return w;
     }
     // Unit u = quarter q of super-block sb: activation bytes 64q..64q+63, bsums 4q..4q+3.
     __device__ static AU act(const ActL &A, uint32_t t, uint32_t u) {
@@ -160,10 +171,15 @@ template <> struct MvFmt<HKHIP_Q4_K> {
         P p;
         p.sc0 = scw & 0xFF; p.sc1 = (scw >> 8) & 0xFF; p.mn0 = mnw & 0xFF; p.mn1 = (mnw >> 8) & 0xFF;
         const uint32_t qw[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
+        const uint32_t xw[8] = {w.x0.x, w.x0.y, w.x0.z, w.x0.w, w.x1.x, w.x1.y, w.x1.z, w.x1.w};
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             p.lo[i] = qw[i] & 0x0F0F0F0Fu;
             p.hi[i] = (qw[i] >> 4) & 0x0F0F0F0Fu;
+            if constexpr (five) { // k4Block has_high: bits 2q / 2q+1 of qh[l] (vecdot.zig:492-495)
+                p.lo[i] |= ((xw[i] >> (2 * q)) & 0x01010101u) << 4;
+                p.hi[i] |= ((xw[i] >> (2 * q + 1)) & 0x01010101u) << 4;
+            }
         }
         p.d = f16_bits_to_f32(h.x & 0xFFFF);
         p.dmin = f16_bits_to_f32(h.x >> 16);
@@ -179,6 +195,65 @@ template <> struct MvFmt<HKHIP_Q4_K> {
         }
         acc = fmaf((float)(slo * p.sc0 + shi * p.sc1), p.d * a.d, acc);
         corr = fmaf((float)(p.mn0 * a.b01 + p.mn1 * a.b23), p.dmin * a.d, corr);
+    }
+    __device__ static void dot(const W &w, uint32_t u, const AU &a, float &acc, float &corr) {
+        dotp(prep(w, u), a, acc, corr);
+    }
+};
+template <> struct MvFmt<HKHIP_Q4_K> : MvK4<HKHIP_Q4_K> {};
+template <> struct MvFmt<HKHIP_Q5_K> : MvK4<HKHIP_Q5_K> {};
+
+// IQ4_XS (dotIQ4XS, vecdot.zig:572-597): a unit is sub-blocks 2q, 2q+1 of a super-block: 32 B of
+// codebook indices (quant plane, 128 B per block) and the block's 8-B header (side plane: d,
+// scales_h, scales_l); against Q8K, so the activation side is Q4_K's.
+template <> struct MvFmt<HKHIP_IQ4_XS> : MvK4<HKHIP_Q4_K> {
+    struct W {
+        uint4 q0, q1;
+        uint2 h;
+    };
+    __device__ static RowRef row(const uint8_t *w, const uint16_t *ws, uint32_t r, uint32_t K) {
+        return RowRef{w + uint64_t(r) * (K / 256) * 128, ws + uint64_t(r) * (K / 256) * 4};
+    }
+    __device__ static W load(const RowRef &R, uint32_t u) {
+        const uint8_t *q = R.w + (u >> 2) * 128 + 32 * (u & 3);
+        W w;
+        w.q0 = ldw(q);
+        w.q1 = ldw(q + 16);
+        w.h = *reinterpret_cast<const uint2 *>(R.ws + (u >> 2) * 4);
+        return w;
+    }
+    struct P {
+        uint32_t q[16];
+        int ls0, ls1;
+        float d;
+    };
+    __device__ static P prep(const W &w, uint32_t u) {
+        const uint32_t q = u & 3;
+        P p;
+        const uint32_t qw[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
+#pragma unroll
+        for (int s = 0; s < 2; s++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                p.q[8 * s + i] = iq4nl_lookup4(qw[4 * s + i] & 0x0F0F0F0Fu);
+                p.q[8 * s + 4 + i] = iq4nl_lookup4((qw[4 * s + i] >> 4) & 0x0F0F0F0Fu);
+            }
+        // Sub-block scale: low 4 bits from scales_l (byte q: sub-block 2q low nibble, 2q+1 high),
+        // high 2 bits from scales_h, minus 32.
+        const uint32_t sl = (w.h.y >> (8 * q)) & 0xFF, shb = (w.h.x >> (16 + 4 * q)) & 0xF;
+        p.ls0 = int((sl & 0xF) | ((shb & 3) << 4)) - 32;
+        p.ls1 = int((sl >> 4) | ((shb >> 2) << 4)) - 32;
+        p.d = f16_bits_to_f32(w.h.x & 0xFFFF);
+        return p;
+    }
+    __device__ static void dotp(const P &p, const AU &a, float &acc, float &) {
+        int s0 = 0, s1 = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            s0 = sdot4(p.q[i], a.q[i], s0);
+            s1 = sdot4(p.q[8 + i], a.q[8 + i], s1);
+        }
+        acc = fmaf((float)(s0 * p.ls0 + s1 * p.ls1), p.d * a.d, acc);
     }
     __device__ static void dot(const W &w, uint32_t u, const AU &a, float &acc, float &corr) {
         dotp(prep(w, u), a, acc, corr);
@@ -1004,6 +1079,8 @@ static mv_kernel_t kernel_for(int t, int nt) {
     switch (t) {
     case HKHIP_Q4_K: return pick<HKHIP_Q4_K>(nt);
     case HKHIP_Q6_K: return pick<HKHIP_Q6_K>(nt);
+    case HKHIP_Q5_K: return pick<HKHIP_Q5_K>(nt);
+    case HKHIP_IQ4_XS: return pick<HKHIP_IQ4_XS>(nt);
     case HKHIP_Q8_0: return pick<HKHIP_Q8_0>(nt);
     case HKHIP_IQ4_NL: return pick<HKHIP_IQ4_NL>(nt);
     case HKHIP_Q4_0: return pick<HKHIP_Q4_0>(nt);
@@ -1025,14 +1102,16 @@ __host__ __device__ constexpr int mvr_rows(int nt, int c) { return nt == 1 ? (c 
 // Largest C per (format, NT): the activations of NT*C units must fit the register file next to
 // two steps of weights.
 __host__ __device__ constexpr int mvr_cmax(int t, int nt) {
-    return t == HKHIP_Q4_K ? (nt == 1 ? 4 : nt == 8 ? 1 : 2)
+    return t == HKHIP_Q4_K || t == HKHIP_IQ4_XS ? (nt == 1 ? 4 : nt == 8 ? 1 : 2)
+         : t == HKHIP_Q5_K ? (nt == 1 ? 2 : 1)
          : t == HKHIP_Q6_K ? (nt == 1 ? 4 : nt == 2 ? 2 : 1)
                            : (nt == 1 ? 8 : nt == 8 ? 2 : 4);
 }
 // Waves per workgroup: MVR_NWAVES (a budget of 256 registers per lane), or 4 (512) for the
 // variants that need more.
 __host__ __device__ constexpr int mvr_nw(int t, int nt, int c) {
-    return (t == HKHIP_Q6_K && nt * c >= 4) || (t == HKHIP_Q4_K && nt * c >= 8 && nt < 8) ||
+    return ((t == HKHIP_Q6_K || t == HKHIP_Q5_K) && nt * c >= 4) ||
+                   ((t == HKHIP_Q4_K || t == HKHIP_IQ4_XS) && nt * c >= 8 && nt < 8) ||
                    (legacy32(t) && c >= 4 && nt * c >= 8)
                ? 4
                : MVR_NWAVES;
@@ -1084,6 +1163,8 @@ static mv_kernel_t kernelr_for(int t, int nt, int c, int ks) {
     switch (t) {
     case HKHIP_Q4_K: return mvr_pick<HKHIP_Q4_K>(nt, c, ks);
     case HKHIP_Q6_K: return mvr_pick<HKHIP_Q6_K>(nt, c, ks);
+    case HKHIP_Q5_K: return mvr_pick<HKHIP_Q5_K>(nt, c, ks);
+    case HKHIP_IQ4_XS: return mvr_pick<HKHIP_IQ4_XS>(nt, c, ks);
     case HKHIP_Q8_0: return mvr_pick<HKHIP_Q8_0>(nt, c, ks);
     case HKHIP_IQ4_NL: return mvr_pick<HKHIP_IQ4_NL>(nt, c, ks);
     case HKHIP_Q4_0: return mvr_pick<HKHIP_Q4_0>(nt, c, ks);
@@ -1148,7 +1229,7 @@ static hipError_t launch_mv_chunk(int t, const MvPartDesc *parts, int nparts, ui
                                   uint32_t n, int mode, hipStream_t s) {
     const float *x = act.x;
     if (n < 1 || n > 8 || nparts < 1 || nparts > MV_PARTS) return hipErrorInvalidValue;
-    const bool kq = (t == HKHIP_Q4_K || t == HKHIP_Q6_K);
+    const bool kq = act_kind(t) == HKHIP_ACT_Q8K;
     {
         // Register kernel when the shape fits it.
         const uint32_t units = kq ? K / 64 : K / 32;
@@ -1272,7 +1353,7 @@ static hipError_t launch_mv_chunk(int t, const MvPartDesc *parts, int nparts, ui
 hipError_t launch_mmvq_parts(int t, const MvPartDesc *parts, int nparts, uint32_t K, const float *x,
                              const uint8_t *xq, uint32_t n, int mode, hipStream_t s) {
     if (n < 1 || nparts < 1 || nparts > MV_PARTS) return hipErrorInvalidValue;
-    const bool kq = (t == HKHIP_Q4_K || t == HKHIP_Q6_K);
+    const bool kq = act_kind(t) == HKHIP_ACT_Q8K;
     // Q4_K and Q6_K from 4 tokens with a prepared input: the small-batch MFMA kernel (it needs the
     // quantizer's token-interleaved planes, so not for an f32 input).
     if (!x && n >= SK_MIN_TOKENS) {

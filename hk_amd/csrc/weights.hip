@@ -1,7 +1,8 @@
 // Weight upload repack (file layout -> device layout) and the bit-exact dequantizer.
 //
 // The decoders restate src/quant/dequant.zig (q4_0 24-31, q4_1 33-41, q5_0 43-56, q5_1 58-72,
-// q8_0 74-78, scaleMinK4 166-175, q4_k 177-202, q6_k 237-267, iq4_nl 430-437). The library is
+// q8_0 74-78, scaleMinK4 166-175, q4_k 177-202, q5_k 204-235, q6_k 237-267, iq4_nl 430-437,
+// iq4_xs 439-455). The library is
 // built with -ffp-contract=off, so every multiply and add below rounds separately, as in the Zig
 // source, and the f32 results are bit-identical to hk's CPU decoders.
 #include "common.hpp"
@@ -44,6 +45,12 @@ __global__ void repack_kernel(int t, const uint8_t *__restrict__ src, uint8_t *_
         }
         uint8_t *q = dst + b * 16;
         for (int j = 0; j < 16; j++) q[j] = s[o + j];
+    } else if (t == HKHIP_IQ4_XS) { // blocks.zig:35: d, scales_h, scales_l[4] | qs[128]
+        const uint8_t *s = src + b * 136;
+        uint8_t *hdr = dst + scale_off + b * 8;
+        for (int j = 0; j < 8; j++) hdr[j] = s[j];
+        uint8_t *q = dst + b * 128;
+        for (int j = 0; j < 128; j++) q[j] = s[8 + j];
     } else if (t == HKHIP_Q8_0) {
         const uint8_t *s = src + b * 34;
         scales[b] = uint16_t(s[0] | (s[1] << 8));
@@ -65,7 +72,7 @@ __global__ void repack_kernel(int t, const uint8_t *__restrict__ src, uint8_t *_
 hipError_t launch_repack(int t, const uint8_t *src, uint8_t *dst, uint32_t rows, uint32_t cols, hipStream_t s) {
     WLayout L = weight_layout(t, rows, cols);
     uint64_t nb = uint64_t(rows) * (cols / block_elems(t));
-    if (t == HKHIP_Q4_K) return hipMemcpyAsync(dst, src, L.total, hipMemcpyDeviceToDevice, s);
+    if (t == HKHIP_Q4_K || t == HKHIP_Q5_K) return hipMemcpyAsync(dst, src, L.total, hipMemcpyDeviceToDevice, s);
     if (nb == 0) return hipSuccess;
     uint32_t grid = uint32_t((nb + 255) / 256);
     repack_kernel<<<grid, 256, 0, s>>>(t, src, dst, nb, L.scale_off, cols / 32);
@@ -120,9 +127,20 @@ __global__ void dequant_kernel(int t, const uint8_t *__restrict__ w, uint32_t co
         uint32_t idx = j < 16 ? (byte & 0x0F) : (byte >> 4);
         int8_t q = (int8_t)(iq4nl_lookup4(idx) & 0xFF);
         v = d * (float)q;
-    } else if (t == HKHIP_Q4_K) {
+    } else if (t == HKHIP_IQ4_XS) { // dequant.zig:439-455
+        const uint64_t b = r * (cols / 256) + c / 256;
+        const uint8_t *hdr = w + scale_off + b * 8;
+        const uint32_t j = c % 256, ib = j / 32, l = j % 32;
+        const uint32_t scales_h = hdr[2] | (hdr[3] << 8);
+        const uint32_t lo = (hdr[4 + ib / 2] >> (4 * (ib % 2))) & 0x0F, hi = (scales_h >> (2 * ib)) & 3;
+        const float dl = f16_bits_to_f32(hdr[0] | (hdr[1] << 8)) * (float)(int(lo | (hi << 4)) - 32);
+        const uint8_t byte = w[b * 128 + 16 * ib + (l & 15)];
+        const int8_t q = (int8_t)(iq4nl_lookup4(l < 16 ? (byte & 0x0F) : (byte >> 4)) & 0xFF);
+        v = dl * (float)q;
+    } else if (t == HKHIP_Q4_K || t == HKHIP_Q5_K) { // Q5_K: dequant.zig:204-235
+        const bool five = t == HKHIP_Q5_K;
         uint64_t b = r * (cols / 256) + c / 256;
-        const uint8_t *blk = w + b * 144;
+        const uint8_t *blk = w + b * (five ? 176 : 144);
         float d = f16_bits_to_f32(blk[0] | (blk[1] << 8));
         float dmin = f16_bits_to_f32(blk[2] | (blk[3] << 8));
         uint32_t j = c % 256;
@@ -131,8 +149,9 @@ __global__ void dequant_kernel(int t, const uint8_t *__restrict__ w, uint32_t co
         scale_min_k4(int(2 * chunk + hi), blk + 4, sc, mn);
         float d1 = d * (float)sc;
         float m1 = dmin * (float)mn;
-        uint8_t q = blk[16 + 32 * chunk + l];
+        uint8_t q = blk[(five ? 48 : 16) + 32 * chunk + l];
         uint32_t nib = hi ? (q >> 4) : (q & 0x0F);
+        if (five) nib += ((blk[16 + l] >> (2 * chunk + hi)) & 1) * 16;
         v = d1 * (float)nib - m1;
     } else { // Q6_K
         uint64_t b = r * (cols / 256) + c / 256;

@@ -29,15 +29,17 @@
 extern "C" {
 #endif
 
-/* hk StorageType codes handled by the HIP kernels (src/format.zig:49-53,75,77,84). */
+/* hk StorageType codes handled by the HIP kernels (src/format.zig:49-53,75-77,84-85). */
 #define HKHIP_Q4_0 0x15
 #define HKHIP_Q8_0 0x16
 #define HKHIP_Q4_1 0x17
 #define HKHIP_Q5_0 0x18
 #define HKHIP_Q5_1 0x19
 #define HKHIP_Q4_K 0x42
+#define HKHIP_Q5_K 0x43
 #define HKHIP_Q6_K 0x44
 #define HKHIP_IQ4_NL 0x55
+#define HKHIP_IQ4_XS 0x56
 
 /* Activation kinds (src/quant/vecdot.zig:183-191 ActKind). */
 #define HKHIP_ACT_A8 0  /* per 32: d = amax/127, round half away, s = sum q */

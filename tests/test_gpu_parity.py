@@ -19,7 +19,7 @@ from tests.helpers import PARITY_TOL, load_fixture, parity_err
 
 pytestmark = pytest.mark.gpu
 
-FMTS = [F.Q8_0, F.Q4_K, F.Q6_K, F.IQ4_NL, F.Q4_0, F.Q4_1, F.Q5_0, F.Q5_1]
+FMTS = [F.Q8_0, F.Q4_K, F.Q6_K, F.IQ4_NL, F.Q4_0, F.Q4_1, F.Q5_0, F.Q5_1, F.Q5_K, F.IQ4_XS]
 FIXTURES = F.NAMES
 LOW4 = [F.Q4_0, F.Q4_1, F.Q5_0, F.Q5_1]
 
@@ -243,7 +243,7 @@ def test_errors(eng, torch_cuda):
         eng.upload(np.zeros(100 * 34 // 32, np.uint8), F.Q8_0, 1, 100)
     assert e.value.code == -2  # UNSUPPORTED_SHAPE: cols not a multiple of 32
     with pytest.raises(HipError) as e:
-        eng.upload(np.zeros(176, np.uint8), 0x43, 1, 256)  # Q5_K: not on this path
+        eng.upload(np.zeros(84, np.uint8), 0x40, 1, 256)  # Q2_K: not on this path
     assert e.value.code == -1
     raw = synth.weights_np(F.Q4_K, 4, 256, seed=1)
     w = eng.upload(raw, F.Q4_K, 4, 256)
@@ -385,6 +385,9 @@ def test_matvec_parts_large_k(eng, torch_cuda, t, k, n):
     # the 4/5-bit formats: register kernel C = 8, LDS kernel, K slices
     (F.Q4_0, 16384, 1), (F.Q4_1, 16416, 1), (F.Q5_0, 8192, 2), (F.Q5_1, 4096, 8),
     (F.Q4_0, 14336, 4), (F.Q4_1, 14336, 8), (F.Q5_0, 20480, 1), (F.Q5_1, 16384, 2),
+    # Q5_K and IQ4_XS: register kernel, LDS kernel (including the NT = 6-8 variants), K slices
+    (F.Q5_K, 8192, 1), (F.Q5_K, 16384, 1), (F.Q5_K, 4096, 2), (F.Q5_K, 4096, 7), (F.Q5_K, 14336, 8),
+    (F.IQ4_XS, 16384, 1), (F.IQ4_XS, 8192, 2), (F.IQ4_XS, 4096, 5), (F.IQ4_XS, 14336, 8), (F.IQ4_XS, 16640, 1),
 ])
 @pytest.mark.parametrize("prepared", [False, True])
 def test_matvec_kernel_variants(eng, torch_cuda, t, k, n, prepared):
