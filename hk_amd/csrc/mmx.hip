@@ -54,6 +54,11 @@ template <> struct Fmt<HKHIP_IQ4_NL> {
 template <int T> struct Fmt4 {
     static constexpr uint32_t RB = 128, W16 = 4, W4 = 0, WSB = has_qh(T) ? 2048 : 1024, DAB = 32;
 };
+// IQ4_XS: IQ4_NL's 16 B per 32 weights; the 8-B block header (d, scales_h, scales_l) per row and
+// step as one 4-B load per lane (lane L: row L/2's word L%2).
+template <> struct Fmt<HKHIP_IQ4_XS> {
+    static constexpr uint32_t RB = 128, W16 = 4, W4 = 0, WSB = 256, DAB = 4;
+};
 template <> struct Fmt<HKHIP_Q4_0> : Fmt4<HKHIP_Q4_0> {};
 template <> struct Fmt<HKHIP_Q4_1> : Fmt4<HKHIP_Q4_1> {};
 template <> struct Fmt<HKHIP_Q5_0> : Fmt4<HKHIP_Q5_0> {};
@@ -65,7 +70,7 @@ template <int T, int TOK, int NW> struct MxSlot {
     uint8_t ws[NW][Fmt<T>::WSB];             // per wave, the rows' f16 scales of the step
     // Activation scales: Q6_K per token (wave m fills tokens 64m..64m+63); A8 per block and token,
     // block-major ([8][TOK]), so that four consecutive tokens' scales are one 16-byte read.
-    float da[T == HKHIP_Q6_K ? 64 * NW : 8 * TOK];
+    float da[T == HKHIP_Q6_K || T == HKHIP_IQ4_XS ? 64 * NW : 8 * TOK];
     int sa[has_m(T) ? 8 * TOK : 1]; // Q4_1 / Q5_1: the blocks' activation sums s, as da
 };
 
@@ -110,8 +115,10 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
     using F = Fmt<T>;
     using Slot = MxSlot<T, TOK, NW>;
     constexpr bool q6 = (T == HKHIP_Q6_K);
+    constexpr bool xs = (T == HKHIP_IQ4_XS);
+    constexpr bool kqa = q6 || xs; // Q8K activations: one scale per token and super-block
     static_assert(NB == 2 || NB == 3, "ring depth");
-    static_assert(q6 ? TOK <= 64 * NW : (8 * TOK) % (64 * NW) == 0, "token scales per wave");
+    static_assert(kqa ? TOK <= 64 * NW : (8 * TOK) % (64 * NW) == 0, "token scales per wave");
     __shared__ __attribute__((aligned(16))) Slot ring0[KS];
     __shared__ __attribute__((aligned(16))) Slot ring1[KS];
     __shared__ __attribute__((aligned(16))) Slot ring2[KS];
@@ -152,7 +159,7 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
     // ---- per-lane 32-bit offsets of the direct loads (mmx_supports checks that they fit) ----
     constexpr uint32_t TPW = TOK / NW; // token rows per wave
     static_assert(TPW % 4 == 0, "token rows per wave");
-    constexpr uint32_t DAL = q6 ? 1 : 8 * TOK / (64 * NW);         // token-scale loads per wave
+    constexpr uint32_t DAL = kqa ? 1 : 8 * TOK / (64 * NW);        // token-scale loads per wave
     constexpr uint32_t CPW = TPW / 4 + F::W16 + F::W4 + 1 + DAL + (has_qh(T) ? 1 : 0) + (has_m(T) ? DAL : 0);
     // Weights: 16-byte piece P = 64*i + lane of the wave's area is row P/(RB/16), piece P%(RB/16);
     // rows of 256 or 128 bytes are swizzled (piece c of row r at c ^ (r & 15), resp. r & 7) so
@@ -185,6 +192,7 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
     const uint32_t sidebase = srow * G.stride;
     const uint32_t sbase = q6 ? srow * nsb : !low4 ? srow * G.stride : sidebase + (h && has_m(T) ? G.m_off : 0);
     const uint32_t qhbase = sidebase + G.qh_off + 16 * h;
+    const uint32_t xsoff = clamp_row(r0 + 32 * wave + lane / 2) * nsb * 8 + 4 * (lane % 2);
     // Token data: activation int8 rows, swizzled like the weights; token scales.
     uint32_t aoff[TPW / 4];
 #pragma unroll
@@ -198,7 +206,7 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
     uint32_t doff[DAL];
 #pragma unroll
     for (uint32_t i = 0; i < DAL; i++) {
-        if constexpr (q6) {
+        if constexpr (kqa) {
             const uint32_t tl = 64 * wave + lane;
             doff[i] = clamp_tok(t0 + (tl < TOK ? tl : 0)) * nsb * 4;
         } else {
@@ -219,6 +227,9 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
         const uint8_t *gd = reinterpret_cast<const uint8_t *>(a.ad);
         if constexpr (q6) {
             load_lds4(a.ws + (((sbase + sb) >> 1) << 2), &S.ws[wave][0]);
+            load_lds4(gd + doff[0] + 4 * sb, &S.da[64 * wave]);
+        } else if constexpr (xs) {
+            load_lds4(a.ws + xsoff + 8 * sb, &S.ws[wave][0]);
             load_lds4(gd + doff[0] + 4 * sb, &S.da[64 * wave]);
         } else {
             load_lds16(a.ws + sbase + 16 * sb, &S.ws[wave][0]);
@@ -338,12 +349,13 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
                     wv[c] = *reinterpret_cast<const v4i *>(blk + 16 * ((2 * c + h) ^ sw));
                 } else {
                     const uint4 x = *reinterpret_cast<const uint4 *>(blk + 16 * (c ^ (j & 7)));
-                    const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
+                    const uint32_t xw[4] = {x.x, x.y, x.z, x.w};
                     uint32_t qh = 0;
+                    constexpr int TL = xs ? HKHIP_IQ4_NL : T; // IQ4_XS: IQ4_NL's codebook
                     if constexpr (has_qh(T))
                         qh = *reinterpret_cast<const uint32_t *>(&S.ws[wave][1024 + 16 * (32 * (c / 4) + j) + 4 * (c % 4)]);
 #pragma unroll
-                    for (int i = 0; i < 4; i++) wv[c][i] = int(low_bit_word<T>(xs[i], qh, h, i));
+                    for (int i = 0; i < 4; i++) wv[c][i] = int(low_bit_word<TL>(xw[i], qh, h, i));
                 }
             }
             float mw[8];
@@ -353,11 +365,23 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
 #pragma unroll
                 for (int c = 0; c < 8; c++) mw[c] = f16_bits_to_f32((mw4[c / 2] >> (16 * (c & 1))) & 0xFFFF);
             }
-            const uint4 s16 = *reinterpret_cast<const uint4 *>(&S.ws[wave][16 * j]);
-            const uint32_t sw4[4] = {s16.x, s16.y, s16.z, s16.w};
             float dw[8];
+            if constexpr (xs) {
+                // d * ls_c (exact in f32): ls_c = scales_l nibble | scales_h bits << 4, minus 32
+                // (dequant.zig:443-447).
+                const uint2 hd = *reinterpret_cast<const uint2 *>(&S.ws[wave][8 * j]);
+                const float d = f16_bits_to_f32(hd.x & 0xFFFF);
 #pragma unroll
-            for (int c = 0; c < 8; c++) dw[c] = f16_bits_to_f32((sw4[c / 2] >> (16 * (c & 1))) & 0xFFFF);
+                for (int c = 0; c < 8; c++) {
+                    const uint32_t lo = (hd.y >> (4 * c)) & 0xF, hi = (hd.x >> (16 + 2 * c)) & 3;
+                    dw[c] = d * (float)(int(lo | (hi << 4)) - 32);
+                }
+            } else {
+                const uint4 s16 = *reinterpret_cast<const uint4 *>(&S.ws[wave][16 * j]);
+                const uint32_t sw4[4] = {s16.x, s16.y, s16.z, s16.w};
+#pragma unroll
+                for (int c = 0; c < 8; c++) dw[c] = f16_bits_to_f32((sw4[c / 2] >> (16 * (c & 1))) & 0xFFFF);
+            }
             load_a(0);
 #pragma unroll
             for (int t = 0; t < TT; t++) {
@@ -365,7 +389,7 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
                 for (int c = 0; c < 8; c++) {
                     const v16i p = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[c], wv[c], v16i{}, 0, 0, 0);
                     // Scales of this lane's 16 outputs: tokens 32t + 8g + 4h + (0..3).
-                    const float4 *dap = reinterpret_cast<const float4 *>(&S.da[c * TOK + 32 * t + 4 * h]);
+                    const float4 *dap = reinterpret_cast<const float4 *>(&S.da[(xs ? 0 : c * TOK) + 32 * t + 4 * h]);
 #pragma unroll
                     for (int g = 0; g < 4; g++) {
                         const float4 dv = dap[2 * g];
@@ -463,7 +487,7 @@ template <int T> hipError_t launch_low4(const MxArgs &a, hipStream_t s, uint32_t
 } // namespace mx
 
 bool mmx_supports(int t, uint32_t rows, uint32_t cols, uint32_t n) {
-    if (t != HKHIP_Q6_K && !legacy32(t)) return false;
+    if (t != HKHIP_Q6_K && t != HKHIP_IQ4_XS && !legacy32(t)) return false;
     if (cols % 256 != 0 || rows == 0 || n == 0) return false;
     // 32-bit per-lane byte offsets: quant plane, scale plane and activations.
     const WLayout W = weight_layout(t, rows, cols);
@@ -475,7 +499,7 @@ hipError_t launch_mmx(int t, const uint8_t *w, uint32_t rows, uint32_t cols, con
     if (!mmx_supports(t, rows, cols, n)) return hipErrorInvalidValue;
     const WLayout W = weight_layout(t, rows, cols);
     const ActLayout A = act_layout(n, cols);
-    const bool q6 = t == HKHIP_Q6_K;
+    const bool q6 = act_kind(t) == HKHIP_ACT_Q8K; // Q6_K, IQ4_XS
     mx::MxArgs a{};
     a.w = w;
     a.ws = w + W.scale_off;
@@ -509,6 +533,10 @@ hipError_t launch_mmx(int t, const uint8_t *w, uint32_t rows, uint32_t cols, con
     case HKHIP_Q4_1: return mx::launch_low4<HKHIP_Q4_1>(a, s, blocks(8, 2), blocks(4, 2));
     case HKHIP_Q5_0: return mx::launch_low4<HKHIP_Q5_0>(a, s, blocks(8, 2), blocks(4, 2));
     case HKHIP_Q5_1: return mx::launch_low4<HKHIP_Q5_1>(a, s, blocks(8, 2), blocks(4, 2));
+    case HKHIP_IQ4_XS:
+        if (blocks(8, 2) >= 224) return mx::launch_cfg<HKHIP_IQ4_XS, 8, 2, 2>(a, s);
+        if (blocks(4, 2) >= 128 && cols >= 1024) return mx::launch_cfg<HKHIP_IQ4_XS, 4, 2, 2, 2>(a, s);
+        return mx::launch_cfg<HKHIP_IQ4_XS, 4, 1, 2>(a, s);
     default: return hipErrorInvalidValue;
     }
 }
