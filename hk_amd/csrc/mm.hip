@@ -289,9 +289,8 @@ hipError_t launch_mm(int t, const uint8_t *w, uint32_t rows, uint32_t cols, cons
     if (n >= SK_MIN_TOKENS && mmsk_supports(t, rows, cols, n)) return launch_mmsk(t, w, rows, cols, xq, n, y, bias, mode, s);
     if (mm2_supports(t, rows, cols, n)) return launch_mm2(t, w, rows, cols, xq, n, y, bias, mode, s);
     if (mmx_supports(t, rows, cols, n)) return launch_mmx(t, w, rows, cols, xq, n, y, bias, mode, s);
-    // Q4_0..Q5_1 rows that are not whole super-blocks, and Q5_K (no GEMM kernel of its own yet):
-    // decode passes of 8 tokens.
-    if ((legacy32(t) && t != HKHIP_Q8_0 && t != HKHIP_IQ4_NL) || t == HKHIP_Q5_K)
+    // Q4_0..Q5_1 rows that are not whole super-blocks: decode passes of 8 tokens.
+    if (legacy32(t) && t != HKHIP_Q8_0 && t != HKHIP_IQ4_NL)
         return launch_mmvq(t, w, rows, cols, xq, n, y, bias, mode, s);
     WLayout W = weight_layout(t, rows, cols);
     ActLayout A = act_layout(n, cols);

@@ -59,6 +59,10 @@ template <int T> struct Fmt4 {
 template <> struct Fmt<HKHIP_IQ4_XS> {
     static constexpr uint32_t RB = 128, W16 = 4, W4 = 0, WSB = 256, DAB = 4;
 };
+// Q5_K: hk's 176-B blocks as they are (header, qh[32], qs[128]); rows unswizzled like Q6_K's.
+template <> struct Fmt<HKHIP_Q5_K> {
+    static constexpr uint32_t RB = 176, W16 = 5, W4 = 2, WSB = 16, DAB = 4;
+};
 template <> struct Fmt<HKHIP_Q4_0> : Fmt4<HKHIP_Q4_0> {};
 template <> struct Fmt<HKHIP_Q4_1> : Fmt4<HKHIP_Q4_1> {};
 template <> struct Fmt<HKHIP_Q5_0> : Fmt4<HKHIP_Q5_0> {};
@@ -70,8 +74,10 @@ template <int T, int TOK, int NW> struct MxSlot {
     uint8_t ws[NW][Fmt<T>::WSB];             // per wave, the rows' f16 scales of the step
     // Activation scales: Q6_K per token (wave m fills tokens 64m..64m+63); A8 per block and token,
     // block-major ([8][TOK]), so that four consecutive tokens' scales are one 16-byte read.
-    float da[T == HKHIP_Q6_K || T == HKHIP_IQ4_XS ? 64 * NW : 8 * TOK];
-    int sa[has_m(T) ? 8 * TOK : 1]; // Q4_1 / Q5_1: the blocks' activation sums s, as da
+    float da[T == HKHIP_Q6_K || T == HKHIP_IQ4_XS || T == HKHIP_Q5_K ? 64 * NW : 8 * TOK];
+    // Q4_1 / Q5_1: the blocks' activation sums s, as da; Q5_K: each sub-block's two bsums
+    // (int16 pair), [8][TOK].
+    int sa[has_m(T) || T == HKHIP_Q5_K ? 8 * TOK : 1];
 };
 
 struct MxArgs {
@@ -80,7 +86,8 @@ struct MxArgs {
     uint32_t rows, cols, n;
     const int8_t *aqs;
     const float *ad;
-    const int32_t *as; // A8 block sums (Q4_1, Q5_1)
+    const int32_t *as;  // A8 block sums (Q4_1, Q5_1)
+    const int16_t *abs; // Q8K bsums (Q5_K)
     float *y;
     const float *bias;
     int mode;
@@ -116,7 +123,10 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
     using Slot = MxSlot<T, TOK, NW>;
     constexpr bool q6 = (T == HKHIP_Q6_K);
     constexpr bool xs = (T == HKHIP_IQ4_XS);
-    constexpr bool kqa = q6 || xs; // Q8K activations: one scale per token and super-block
+    constexpr bool k5 = (T == HKHIP_Q5_K);
+    constexpr bool kqa = q6 || xs || k5; // Q8K activations: one scale per token and super-block
+    constexpr bool unswz = q6 || k5;     // rows not a power of two of pieces: no swizzle, word tail
+    constexpr uint32_t DBS = 8 * TOK / (64 * NW); // Q5_K: bsum-pair loads per wave
     static_assert(NB == 2 || NB == 3, "ring depth");
     static_assert(kqa ? TOK <= 64 * NW : (8 * TOK) % (64 * NW) == 0, "token scales per wave");
     __shared__ __attribute__((aligned(16))) Slot ring0[KS];
@@ -160,7 +170,8 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
     constexpr uint32_t TPW = TOK / NW; // token rows per wave
     static_assert(TPW % 4 == 0, "token rows per wave");
     constexpr uint32_t DAL = kqa ? 1 : 8 * TOK / (64 * NW);        // token-scale loads per wave
-    constexpr uint32_t CPW = TPW / 4 + F::W16 + F::W4 + 1 + DAL + (has_qh(T) ? 1 : 0) + (has_m(T) ? DAL : 0);
+    constexpr uint32_t CPW = TPW / 4 + F::W16 + F::W4 + (k5 ? 0 : 1) + DAL + (has_qh(T) ? 1 : 0) + (has_m(T) ? DAL : 0) +
+                             (k5 ? DBS : 0);
     // Weights: 16-byte piece P = 64*i + lane of the wave's area is row P/(RB/16), piece P%(RB/16);
     // rows of 256 or 128 bytes are swizzled (piece c of row r at c ^ (r & 15), resp. r & 7) so
     // the 32 rows one operand read covers hit distinct banks. Q6_K's 208-byte rows need no
@@ -171,10 +182,10 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
     for (uint32_t i = 0; i < F::W16; i++) {
         const uint32_t P = 64 * i + lane, lr = P / PPR, pc = P % PPR;
         const uint32_t rr = clamp_row(r0 + 32 * wave + lr);
-        const uint32_t c = q6 ? pc : (pc ^ (lr & (PPR - 1)));
+        const uint32_t c = unswz ? pc : (pc ^ (lr & (PPR - 1)));
         woff[i] = rr * nsb * F::RB + 16 * c;
     }
-    if constexpr (q6) {
+    if constexpr (unswz) {
 #pragma unroll
         for (uint32_t i = 0; i < F::W4; i++) {
             const uint32_t Wd = 64 * 4 * F::W16 + 64 * i + lane; // 4-byte word of the wave's area
@@ -193,6 +204,16 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
     const uint32_t sbase = q6 ? srow * nsb : !low4 ? srow * G.stride : sidebase + (h && has_m(T) ? G.m_off : 0);
     const uint32_t qhbase = sidebase + G.qh_off + 16 * h;
     const uint32_t xsoff = clamp_row(r0 + 32 * wave + lane / 2) * nsb * 8 + 4 * (lane % 2);
+    // Q5_K bsum pairs: load i of wave m covers entries 64*(DBS*m + i) .. of [8][TOK]: sub-block
+    // e / TOK (bsums 2c, 2c + 1: bytes 4c of the super-block's 32), token e % TOK.
+    uint32_t boff[k5 ? DBS : 1];
+    if constexpr (k5) {
+#pragma unroll
+        for (uint32_t i = 0; i < DBS; i++) {
+            const uint32_t e = 64 * (DBS * wave + i) + lane;
+            boff[i] = clamp_tok(t0 + e % TOK) * (K / 16) * 2 + 4 * (e / TOK);
+        }
+    }
     // Token data: activation int8 rows, swizzled like the weights; token scales.
     uint32_t aoff[TPW / 4];
 #pragma unroll
@@ -231,6 +252,11 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
         } else if constexpr (xs) {
             load_lds4(a.ws + xsoff + 8 * sb, &S.ws[wave][0]);
             load_lds4(gd + doff[0] + 4 * sb, &S.da[64 * wave]);
+        } else if constexpr (k5) {
+            load_lds4(gd + doff[0] + 4 * sb, &S.da[64 * wave]);
+            const uint8_t *gb = reinterpret_cast<const uint8_t *>(a.abs);
+#pragma unroll
+            for (uint32_t i = 0; i < DBS; i++) load_lds4(gb + boff[i] + 32 * sb, &S.sa[64 * (DBS * wave + i)]);
         } else {
             load_lds16(a.ws + sbase + 16 * sb, &S.ws[wave][0]);
             if constexpr (has_qh(T)) load_lds16(a.ws + qhbase + 32 * sb, &S.ws[wave][1024]);
@@ -343,9 +369,33 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
             // IQ4_NL: the block's 16 bytes, low nibbles for h = 0, high for h = 1).
             const uint8_t *blk = &S.w[wave][F::RB * j];
             v4i wv[8];
+            float dw[8], mw[8];
+            if constexpr (k5) {
+                // Sub-block c of this lane's row half: nibble c%2 of qs bytes 32(c/2) + 16h.., fifth
+                // bit c of qh bytes 16h.. (k4Block has_high); scales and mins by the word unpack
+                // (vecdot.zig:461-474).
+                const uint4 hd = *reinterpret_cast<const uint4 *>(blk);
+                const uint4 qh4 = *reinterpret_cast<const uint4 *>(blk + 16 + 16 * h);
+                const uint32_t qhw[4] = {qh4.x, qh4.y, qh4.z, qh4.w};
+                const uint32_t k1 = 0x3f3f3f3fu, k2 = 0x0f0f0f0fu, k3 = 0x03030303u;
+                const uint32_t scw[2] = {hd.y & k1, (hd.w & k2) | (((hd.y >> 6) & k3) << 4)};
+                const uint32_t mnw[2] = {hd.z & k1, ((hd.w >> 4) & k2) | (((hd.z >> 6) & k3) << 4)};
+                const float d = f16_bits_to_f32(hd.x & 0xFFFF), dmin = f16_bits_to_f32(hd.x >> 16);
+#pragma unroll
+                for (int c = 0; c < 8; c++) {
+                    const uint4 x = *reinterpret_cast<const uint4 *>(blk + 48 + 32 * (c / 2) + 16 * h);
+                    const uint32_t xw[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        wv[c][i] = int(((xw[i] >> (4 * (c & 1))) & 0x0F0F0F0Fu) | (((qhw[i] >> c) & 0x01010101u) << 4));
+                    dw[c] = d * (float)((scw[c / 4] >> (8 * (c % 4))) & 0xFF);
+                    mw[c] = dmin * (float)((mnw[c / 4] >> (8 * (c % 4))) & 0xFF);
+                }
+            }
 #pragma unroll
             for (int c = 0; c < 8; c++) {
-                if constexpr (T == HKHIP_Q8_0) {
+                if constexpr (k5) {
+                } else if constexpr (T == HKHIP_Q8_0) {
                     wv[c] = *reinterpret_cast<const v4i *>(blk + 16 * ((2 * c + h) ^ sw));
                 } else {
                     const uint4 x = *reinterpret_cast<const uint4 *>(blk + 16 * (c ^ (j & 7)));
@@ -358,15 +408,14 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
                     for (int i = 0; i < 4; i++) wv[c][i] = int(low_bit_word<TL>(xw[i], qh, h, i));
                 }
             }
-            float mw[8];
             if constexpr (has_m(T)) {
                 const uint4 m16 = *reinterpret_cast<const uint4 *>(&S.ws[wave][16 * (32 + j)]);
                 const uint32_t mw4[4] = {m16.x, m16.y, m16.z, m16.w};
 #pragma unroll
                 for (int c = 0; c < 8; c++) mw[c] = f16_bits_to_f32((mw4[c / 2] >> (16 * (c & 1))) & 0xFFFF);
             }
-            float dw[8];
-            if constexpr (xs) {
+            if constexpr (k5) {
+            } else if constexpr (xs) {
                 // d * ls_c (exact in f32): ls_c = scales_l nibble | scales_h bits << 4, minus 32
                 // (dequant.zig:443-447).
                 const uint2 hd = *reinterpret_cast<const uint2 *>(&S.ws[wave][8 * j]);
@@ -389,7 +438,7 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
                 for (int c = 0; c < 8; c++) {
                     const v16i p = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[c], wv[c], v16i{}, 0, 0, 0);
                     // Scales of this lane's 16 outputs: tokens 32t + 8g + 4h + (0..3).
-                    const float4 *dap = reinterpret_cast<const float4 *>(&S.da[(xs ? 0 : c * TOK) + 32 * t + 4 * h]);
+                    const float4 *dap = reinterpret_cast<const float4 *>(&S.da[(xs || k5 ? 0 : c * TOK) + 32 * t + 4 * h]);
 #pragma unroll
                     for (int g = 0; g < 4; g++) {
                         const float4 dv = dap[2 * g];
@@ -403,6 +452,15 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
 #pragma unroll
                             for (int e = 0; e < 4; e++)
                                 acc[t][4 * g + e] = fmaf(mw[c], ds[e] * (float)ss[e], acc[t][4 * g + e]);
+                        }
+                        if constexpr (k5) { // - dmin * mn_c * da * (bsum 2c + bsum 2c+1)
+                            const int4 bv = *reinterpret_cast<const int4 *>(&S.sa[c * TOK + 32 * t + 4 * h + 8 * g]);
+                            const int bb[4] = {bv.x, bv.y, bv.z, bv.w};
+#pragma unroll
+                            for (int e = 0; e < 4; e++) {
+                                const int b32 = int(int16_t(bb[e] & 0xFFFF)) + int(int16_t(uint32_t(bb[e]) >> 16));
+                                acc[t][4 * g + e] = fmaf(-mw[c], ds[e] * (float)b32, acc[t][4 * g + e]);
+                            }
                         }
                     }
                 }
@@ -487,7 +545,7 @@ template <int T> hipError_t launch_low4(const MxArgs &a, hipStream_t s, uint32_t
 } // namespace mx
 
 bool mmx_supports(int t, uint32_t rows, uint32_t cols, uint32_t n) {
-    if (t != HKHIP_Q6_K && t != HKHIP_IQ4_XS && !legacy32(t)) return false;
+    if (t != HKHIP_Q6_K && t != HKHIP_IQ4_XS && t != HKHIP_Q5_K && !legacy32(t)) return false;
     if (cols % 256 != 0 || rows == 0 || n == 0) return false;
     // 32-bit per-lane byte offsets: quant plane, scale plane and activations.
     const WLayout W = weight_layout(t, rows, cols);
@@ -509,6 +567,7 @@ hipError_t launch_mmx(int t, const uint8_t *w, uint32_t rows, uint32_t cols, con
     a.aqs = reinterpret_cast<const int8_t *>(xq + (q6 ? A.k_qs : A.a8_qs));
     a.ad = reinterpret_cast<const float *>(xq + (q6 ? A.k_d : A.a8_d));
     a.as = reinterpret_cast<const int32_t *>(xq + A.a8_s);
+    a.abs = reinterpret_cast<const int16_t *>(xq + A.k_bs);
     a.y = y;
     a.bias = bias;
     a.mode = mode;
@@ -533,6 +592,9 @@ hipError_t launch_mmx(int t, const uint8_t *w, uint32_t rows, uint32_t cols, con
     case HKHIP_Q4_1: return mx::launch_low4<HKHIP_Q4_1>(a, s, blocks(8, 2), blocks(4, 2));
     case HKHIP_Q5_0: return mx::launch_low4<HKHIP_Q5_0>(a, s, blocks(8, 2), blocks(4, 2));
     case HKHIP_Q5_1: return mx::launch_low4<HKHIP_Q5_1>(a, s, blocks(8, 2), blocks(4, 2));
+    case HKHIP_Q5_K: // the offset term makes it Q4_1-like; two K slices do not fit with 176-B rows
+        if (blocks(4, 2) >= 160) return mx::launch_cfg<HKHIP_Q5_K, 4, 2, 2>(a, s);
+        return mx::launch_cfg<HKHIP_Q5_K, 4, 1, 2>(a, s);
     case HKHIP_IQ4_XS:
         if (blocks(8, 2) >= 224) return mx::launch_cfg<HKHIP_IQ4_XS, 8, 2, 2>(a, s);
         if (blocks(4, 2) >= 128 && cols >= 1024) return mx::launch_cfg<HKHIP_IQ4_XS, 4, 2, 2, 2>(a, s);
