@@ -328,9 +328,11 @@ int hkhip_gemm(hkhip_engine *eng, const hkhip_mat *m, const void *xq_dev, float 
 static uint32_t gemm_min_tokens(int t) {
     switch (t) {
     case HKHIP_Q6_K:
+    case HKHIP_Q5_K: // Q6_K's (its GEMM is VALU-bound too; not measured separately)
     case HKHIP_Q8_0: return 33;
     case HKHIP_IQ4_NL:
-    case HKHIP_Q4_0: case HKHIP_Q4_1: case HKHIP_Q5_0: case HKHIP_Q5_1: return 25; // IQ4_NL's (same quant bytes)
+    case HKHIP_Q4_0: case HKHIP_Q4_1: case HKHIP_Q5_0: case HKHIP_Q5_1: case HKHIP_IQ4_XS:
+        return 25; // IQ4_NL's (same quant bytes per 32 weights)
     default: return 9;
     }
 }
