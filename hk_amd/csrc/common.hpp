@@ -107,7 +107,8 @@ inline WLayout weight_layout(int t, uint32_t rows, uint32_t cols) {
 
 // Activation-quant buffer for n tokens of k values. Both kinds live side by side so one
 // input serves Q8_0 / IQ4_NL (A8) and Q4_K / Q6_K (Q8K) products alike:
-//   a8_qs [n][k] i8, a8_d [n][k/32] f32, a8_s [n][k/32] i32,
+//   a8_qs [n][k] i8, a8_d [n][k/32] f32, a8_s [n][k/32] i32, a8_ds [n][k/32] f32 = d * (f32)s
+//         (the offset operand of Q4_1 / Q5_1, as kernelLegacy forms it, gemm.zig:165),
 //   k_qs  [n][k] i8, k_d  [n][k/256] f32, k_bs [n][k/16] i16,
 //   k_mb  [n][k/256][16] bf16: per super-block, its 8 sub-blocks' 32-value sums as exact bf16
 //         integers, bsum32 = 64*u + v with v in [0, 63]: 64*u for the 8 sub-blocks, then v --
@@ -123,7 +124,7 @@ inline WLayout weight_layout(int t, uint32_t rows, uint32_t cols) {
 constexpr uint32_t SK_MAX_TOKENS = 32;
 constexpr uint32_t SK_MIN_TOKENS = 4; // below, the decode kernels are faster
 struct ActLayout {
-    uint64_t a8_qs, a8_d, a8_s, k_qs, k_d, k_bs, k_mb, k_il, k_ilmb, k_ild, total;
+    uint64_t a8_qs, a8_d, a8_s, a8_ds, k_qs, k_d, k_bs, k_mb, k_il, k_ilmb, k_ild, total;
     uint32_t tiles; // 16-token tiles of the interleaved planes (0: none)
 };
 
@@ -134,6 +135,7 @@ inline ActLayout act_layout(uint32_t n, uint32_t k) {
     L.a8_qs = o; o = align256(o + nk);
     L.a8_d = o;  o = align256(o + nk / 32 * 4);
     L.a8_s = o;  o = align256(o + nk / 32 * 4);
+    L.a8_ds = o; o = align256(o + nk / 32 * 4);
     L.k_qs = o;  o = align256(o + (k % QK_K == 0 ? nk : 0));
     L.k_d = o;   o = align256(o + (k % QK_K == 0 ? nk / QK_K * 4 : 0));
     L.k_bs = o;  o = align256(o + (k % QK_K == 0 ? nk / 16 * 2 : 0));

@@ -12,7 +12,8 @@
 //  * 32-weight formats: y += (dw[r,c]*da[t,c]) * I_c per block c (I_c exact). One 32x32x32
 //    int8 MFMA yields the tile's I_c; then per output one multiply (dw*da), one convert and one
 //    fma. Q4_0 / Q5_0 weights enter as u - zp (kernelLegacy's acci - zp*s); Q4_1 / Q5_1 as u,
-//    plus m[r,c] * (da[t,c] * s[t,c]) per output (kernelLegacy's has_m term).
+//    plus m[r,c] * (da[t,c] * s[t,c]) per output (kernelLegacy's has_m term; the product comes
+//    precomputed from qact).
 // Only the f32 summation order differs from the reference.
 //
 // Structure (as the Q4_K ring kernel): a workgroup of NW waves owns 32*NW rows x 32*TT tokens;
@@ -75,9 +76,9 @@ template <int T, int TOK, int NW> struct MxSlot {
     // Activation scales: Q6_K per token (wave m fills tokens 64m..64m+63); A8 per block and token,
     // block-major ([8][TOK]), so that four consecutive tokens' scales are one 16-byte read.
     float da[T == HKHIP_Q6_K || T == HKHIP_IQ4_XS || T == HKHIP_Q5_K ? 64 * NW : 8 * TOK];
-    // Q4_1 / Q5_1: the blocks' activation sums s, as da; Q5_K: each sub-block's two bsums
+    // Q4_1 / Q5_1: the blocks' d_a * s (f32 bits), as da; Q5_K: each sub-block's two bsums
     // (int16 pair), [8][TOK].
-    int sa[has_m(T) || T == HKHIP_Q5_K ? 8 * TOK : 1];
+    uint32_t sa[has_m(T) || T == HKHIP_Q5_K ? 8 * TOK : 1];
 };
 
 struct MxArgs {
@@ -86,7 +87,7 @@ struct MxArgs {
     uint32_t rows, cols, n;
     const int8_t *aqs;
     const float *ad;
-    const int32_t *as;  // A8 block sums (Q4_1, Q5_1)
+    const float *ads;   // A8 d * s per block (Q4_1, Q5_1)
     const int16_t *abs; // Q8K bsums (Q5_K)
     float *y;
     const float *bias;
@@ -263,7 +264,7 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
 #pragma unroll
             for (uint32_t i = 0; i < DAL; i++) load_lds4(gd + doff[i] + 32 * sb, &S.da[64 * (DAL * wave + i)]);
             if constexpr (has_m(T)) {
-                const uint8_t *gs = reinterpret_cast<const uint8_t *>(a.as);
+                const uint8_t *gs = reinterpret_cast<const uint8_t *>(a.ads);
 #pragma unroll
                 for (uint32_t i = 0; i < DAL; i++) load_lds4(gs + doff[i] + 32 * sb, &S.sa[64 * (DAL * wave + i)]);
             }
@@ -447,11 +448,10 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
                         for (int e = 0; e < 4; e++)
                             acc[t][4 * g + e] = fmaf((float)p[4 * g + e], dw[c] * ds[e], acc[t][4 * g + e]);
                         if constexpr (has_m(T)) {
-                            const int4 sv = *reinterpret_cast<const int4 *>(&S.sa[c * TOK + 32 * t + 4 * h + 8 * g]);
-                            const int ss[4] = {sv.x, sv.y, sv.z, sv.w};
+                            const float4 sv = *reinterpret_cast<const float4 *>(&S.sa[c * TOK + 32 * t + 4 * h + 8 * g]);
+                            const float dss[4] = {sv.x, sv.y, sv.z, sv.w};
 #pragma unroll
-                            for (int e = 0; e < 4; e++)
-                                acc[t][4 * g + e] = fmaf(mw[c], ds[e] * (float)ss[e], acc[t][4 * g + e]);
+                            for (int e = 0; e < 4; e++) acc[t][4 * g + e] = fmaf(mw[c], dss[e], acc[t][4 * g + e]);
                         }
                         if constexpr (k5) { // - dmin * mn_c * da * (bsum 2c + bsum 2c+1)
                             const int4 bv = *reinterpret_cast<const int4 *>(&S.sa[c * TOK + 32 * t + 4 * h + 8 * g]);
@@ -566,7 +566,7 @@ hipError_t launch_mmx(int t, const uint8_t *w, uint32_t rows, uint32_t cols, con
     a.n = n;
     a.aqs = reinterpret_cast<const int8_t *>(xq + (q6 ? A.k_qs : A.a8_qs));
     a.ad = reinterpret_cast<const float *>(xq + (q6 ? A.k_d : A.a8_d));
-    a.as = reinterpret_cast<const int32_t *>(xq + A.a8_s);
+    a.ads = reinterpret_cast<const float *>(xq + A.a8_ds);
     a.abs = reinterpret_cast<const int16_t *>(xq + A.k_bs);
     a.y = y;
     a.bias = bias;

@@ -6,7 +6,7 @@ namespace hkhip {
 
 // A8: one thread per value; a 32-lane half-wave owns one block.
 __global__ void qact_a8_kernel(const float *__restrict__ x, uint64_t total, int8_t *__restrict__ qs,
-                               float *__restrict__ dout, int32_t *__restrict__ sout) {
+                               float *__restrict__ dout, int32_t *__restrict__ sout, float *__restrict__ dsout) {
     const uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     const A8Q r = quant_a8_halfwave(i < total ? x[i] : 0.0f);
     if (i < total) {
@@ -14,6 +14,7 @@ __global__ void qact_a8_kernel(const float *__restrict__ x, uint64_t total, int8
         if ((i & 31) == 0) {
             dout[i / 32] = r.d;
             sout[i / 32] = r.s;
+            dsout[i / 32] = r.d * (float)r.s;
         }
     }
 }
@@ -79,7 +80,8 @@ hipError_t launch_qact(const float *x, uint32_t n, uint32_t k, int kind, uint8_t
         uint64_t grid = (total + 255) / 256;
         qact_a8_kernel<<<uint32_t(grid), 256, 0, s>>>(x, total, reinterpret_cast<int8_t *>(xq + L.a8_qs),
                                                       reinterpret_cast<float *>(xq + L.a8_d),
-                                                      reinterpret_cast<int32_t *>(xq + L.a8_s));
+                                                      reinterpret_cast<int32_t *>(xq + L.a8_s),
+                                                      reinterpret_cast<float *>(xq + L.a8_ds));
     } else {
         uint64_t nb = total / QK_K;
         uint64_t grid = (nb + 3) / 4; // 4 waves per workgroup
