@@ -110,6 +110,8 @@ inline WLayout weight_layout(int t, uint32_t rows, uint32_t cols) {
 //   a8_qs [n][k] i8, a8_d [n][k/32] f32, a8_s [n][k/32] i32, a8_ds [n][k/32] f32 = d * (f32)s
 //         (the offset operand of Q4_1 / Q5_1, as kernelLegacy forms it, gemm.zig:165),
 //   k_qs  [n][k] i8, k_d  [n][k/256] f32, k_bs [n][k/16] i16,
+//   k_db  [n][k/32] f32: d * (f32)(bsum of the 32 values of each sub-block), the Q5_K GEMM's
+//         min-term operand,
 //   k_mb  [n][k/256][16] bf16: per super-block, its 8 sub-blocks' 32-value sums as exact bf16
 //         integers, bsum32 = 64*u + v with v in [0, 63]: 64*u for the 8 sub-blocks, then v --
 //         the token-side operand of the GEMM's integer min term, precomputed once
@@ -124,7 +126,7 @@ inline WLayout weight_layout(int t, uint32_t rows, uint32_t cols) {
 constexpr uint32_t SK_MAX_TOKENS = 32;
 constexpr uint32_t SK_MIN_TOKENS = 4; // below, the decode kernels are faster
 struct ActLayout {
-    uint64_t a8_qs, a8_d, a8_s, a8_ds, k_qs, k_d, k_bs, k_mb, k_il, k_ilmb, k_ild, total;
+    uint64_t a8_qs, a8_d, a8_s, a8_ds, k_qs, k_d, k_bs, k_db, k_mb, k_il, k_ilmb, k_ild, total;
     uint32_t tiles; // 16-token tiles of the interleaved planes (0: none)
 };
 
@@ -139,6 +141,7 @@ inline ActLayout act_layout(uint32_t n, uint32_t k) {
     L.k_qs = o;  o = align256(o + (k % QK_K == 0 ? nk : 0));
     L.k_d = o;   o = align256(o + (k % QK_K == 0 ? nk / QK_K * 4 : 0));
     L.k_bs = o;  o = align256(o + (k % QK_K == 0 ? nk / 16 * 2 : 0));
+    L.k_db = o;  o = align256(o + (k % QK_K == 0 ? nk / 32 * 4 : 0));
     L.k_mb = o;  o = align256(o + (k % QK_K == 0 ? nk / QK_K * 32 : 0));
     L.tiles = (k % QK_K == 0 && n >= 1 && n <= SK_MAX_TOKENS) ? (n + 15) / 16 : 0;
     const uint64_t tk = uint64_t(L.tiles) * 16 * k; // interleaved entries (padded tokens)

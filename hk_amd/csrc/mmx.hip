@@ -76,8 +76,8 @@ template <int T, int TOK, int NW> struct MxSlot {
     // Activation scales: Q6_K per token (wave m fills tokens 64m..64m+63); A8 per block and token,
     // block-major ([8][TOK]), so that four consecutive tokens' scales are one 16-byte read.
     float da[T == HKHIP_Q6_K || T == HKHIP_IQ4_XS || T == HKHIP_Q5_K ? 64 * NW : 8 * TOK];
-    // Q4_1 / Q5_1: the blocks' d_a * s (f32 bits), as da; Q5_K: each sub-block's two bsums
-    // (int16 pair), [8][TOK].
+    // Q4_1 / Q5_1: the blocks' d_a * s; Q5_K: each sub-block's d_a * bsum32 (f32 bits, [8][TOK]
+    // as da).
     uint32_t sa[has_m(T) || T == HKHIP_Q5_K ? 8 * TOK : 1];
 };
 
@@ -88,7 +88,7 @@ struct MxArgs {
     const int8_t *aqs;
     const float *ad;
     const float *ads;   // A8 d * s per block (Q4_1, Q5_1)
-    const int16_t *abs; // Q8K bsums (Q5_K)
+    const float *adb;   // Q8K d * bsum32 per sub-block (Q5_K)
     float *y;
     const float *bias;
     int mode;
@@ -205,14 +205,14 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
     const uint32_t sbase = q6 ? srow * nsb : !low4 ? srow * G.stride : sidebase + (h && has_m(T) ? G.m_off : 0);
     const uint32_t qhbase = sidebase + G.qh_off + 16 * h;
     const uint32_t xsoff = clamp_row(r0 + 32 * wave + lane / 2) * nsb * 8 + 4 * (lane % 2);
-    // Q5_K bsum pairs: load i of wave m covers entries 64*(DBS*m + i) .. of [8][TOK]: sub-block
-    // e / TOK (bsums 2c, 2c + 1: bytes 4c of the super-block's 32), token e % TOK.
+    // Q5_K d_a * bsum32: load i of wave m covers entries 64*(DBS*m + i) .. of [8][TOK]: sub-block
+    // e / TOK, token e % TOK.
     uint32_t boff[k5 ? DBS : 1];
     if constexpr (k5) {
 #pragma unroll
         for (uint32_t i = 0; i < DBS; i++) {
             const uint32_t e = 64 * (DBS * wave + i) + lane;
-            boff[i] = clamp_tok(t0 + e % TOK) * (K / 16) * 2 + 4 * (e / TOK);
+            boff[i] = clamp_tok(t0 + e % TOK) * (K / 32) * 4 + 4 * (e / TOK);
         }
     }
     // Token data: activation int8 rows, swizzled like the weights; token scales.
@@ -255,7 +255,7 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
             load_lds4(gd + doff[0] + 4 * sb, &S.da[64 * wave]);
         } else if constexpr (k5) {
             load_lds4(gd + doff[0] + 4 * sb, &S.da[64 * wave]);
-            const uint8_t *gb = reinterpret_cast<const uint8_t *>(a.abs);
+            const uint8_t *gb = reinterpret_cast<const uint8_t *>(a.adb);
 #pragma unroll
             for (uint32_t i = 0; i < DBS; i++) load_lds4(gb + boff[i] + 32 * sb, &S.sa[64 * (DBS * wave + i)]);
         } else {
@@ -453,14 +453,11 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
 #pragma unroll
                             for (int e = 0; e < 4; e++) acc[t][4 * g + e] = fmaf(mw[c], dss[e], acc[t][4 * g + e]);
                         }
-                        if constexpr (k5) { // - dmin * mn_c * da * (bsum 2c + bsum 2c+1)
-                            const int4 bv = *reinterpret_cast<const int4 *>(&S.sa[c * TOK + 32 * t + 4 * h + 8 * g]);
-                            const int bb[4] = {bv.x, bv.y, bv.z, bv.w};
+                        if constexpr (k5) { // - dmin * mn_c * (da * bsum32_c)
+                            const float4 bv = *reinterpret_cast<const float4 *>(&S.sa[c * TOK + 32 * t + 4 * h + 8 * g]);
+                            const float db[4] = {bv.x, bv.y, bv.z, bv.w};
 #pragma unroll
-                            for (int e = 0; e < 4; e++) {
-                                const int b32 = int(int16_t(bb[e] & 0xFFFF)) + int(int16_t(uint32_t(bb[e]) >> 16));
-                                acc[t][4 * g + e] = fmaf(-mw[c], ds[e] * (float)b32, acc[t][4 * g + e]);
-                            }
+                            for (int e = 0; e < 4; e++) acc[t][4 * g + e] = fmaf(-mw[c], db[e], acc[t][4 * g + e]);
                         }
                     }
                 }
@@ -567,7 +564,7 @@ hipError_t launch_mmx(int t, const uint8_t *w, uint32_t rows, uint32_t cols, con
     a.aqs = reinterpret_cast<const int8_t *>(xq + (q6 ? A.k_qs : A.a8_qs));
     a.ad = reinterpret_cast<const float *>(xq + (q6 ? A.k_d : A.a8_d));
     a.ads = reinterpret_cast<const float *>(xq + A.a8_ds);
-    a.abs = reinterpret_cast<const int16_t *>(xq + A.k_bs);
+    a.adb = reinterpret_cast<const float *>(xq + A.k_db);
     a.y = y;
     a.bias = bias;
     a.mode = mode;

@@ -38,7 +38,7 @@ struct QactIl {
 
 __global__ void qact_q8k_kernel(const float *__restrict__ x, uint64_t nblocks, int8_t *__restrict__ qs,
                                 float *__restrict__ dout, int16_t *__restrict__ bsout, uint16_t *__restrict__ mbout,
-                                QactIl il) {
+                                float *__restrict__ dbout, QactIl il) {
     const uint32_t lane = threadIdx.x & 63;
     const uint64_t b = (uint64_t(blockIdx.x) * blockDim.x + threadIdx.x) / 64;
     if (b >= nblocks) return; // whole waves exit together
@@ -55,6 +55,7 @@ __global__ void qact_q8k_kernel(const float *__restrict__ x, uint64_t nblocks, i
     if ((lane & 7) == 0) {
         mbout[b * 16 + lane / 8] = mu;
         mbout[b * 16 + 8 + lane / 8] = mv;
+        dbout[b * 8 + lane / 8] = r.d * (float)b32;
     }
     if (il.tiles) {
         const uint32_t b32i = uint32_t(b); // tokens <= SK_MAX_TOKENS: a small index
@@ -89,6 +90,7 @@ hipError_t launch_qact(const float *x, uint32_t n, uint32_t k, int kind, uint8_t
                                                        reinterpret_cast<float *>(xq + L.k_d),
                                                        reinterpret_cast<int16_t *>(xq + L.k_bs),
                                                        reinterpret_cast<uint16_t *>(xq + L.k_mb),
+                                                       reinterpret_cast<float *>(xq + L.k_db),
                                                        QactIl{xq + L.k_il, reinterpret_cast<uint16_t *>(xq + L.k_ilmb),
                                                               reinterpret_cast<float *>(xq + L.k_ild), L.tiles, n,
                                                               k / QK_K});
