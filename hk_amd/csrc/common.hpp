@@ -106,7 +106,7 @@ inline WLayout weight_layout(int t, uint32_t rows, uint32_t cols) {
 }
 
 // Activation-quant buffer for n tokens of k values. Both kinds live side by side so one
-// input serves Q8_0 / IQ4_NL (A8) and Q4_K / Q6_K (Q8K) products alike:
+// input serves the 32-weight formats (A8) and the super-block formats (Q8K) alike:
 //   a8_qs [n][k] i8, a8_d [n][k/32] f32, a8_s [n][k/32] i32, a8_ds [n][k/32] f32 = d * (f32)s
 //         (the offset operand of Q4_1 / Q5_1, as kernelLegacy forms it, gemm.zig:165),
 //   k_qs  [n][k] i8, k_d  [n][k/256] f32, k_bs [n][k/16] i16,
