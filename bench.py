@@ -293,6 +293,29 @@ def main():
         for w_ in ws:
             eng.free(w_)
 
+        # Upload from host memory: the file bytes of a 14336x4096 matrix from an mmap'd file view
+        # (hk loads tensors as views of the mmap'd container), through hkhip_upload (H2D copy, then
+        # the on-device repack for the formats whose blocks are not 16-byte aligned).
+        import tempfile
+
+        import numpy as np
+        up = []
+        for t in (F.Q4_K, F.IQ4_NL, F.Q6_K):
+            raw = synth.weights_np(t, FF, H, seed=synth.seed_for(6, t))
+            with tempfile.NamedTemporaryFile(dir="/tmp", suffix=".bin") as fh:
+                raw.tofile(fh.name)
+                view = np.memmap(fh.name, dtype=np.uint8, mode="r").reshape(raw.shape)
+                eng.free(eng.upload(view, t, FF, H))  # warm-up
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                for _ in range(3):
+                    eng.free(eng.upload(view, t, FF, H))
+                torch.cuda.synchronize()
+                dt = (time.perf_counter() - t0) / 3
+                del view
+            up.append(dict(fmt=FMT_NAME[t], shape=f"{FF}x{H}", ms=round(dt * 1e3, 2), gbs=round(raw.nbytes / dt / 1e9, 2)))
+        extra["upload_from_mmap"] = up
+
         # Config 2: a batch-1 decode step through every linear layer of a Qwen3-0.6B-shaped decoder
         # (28 x {q 2048x1024, k/v 1024x1024, o 1024x2048, gate/up 3072x1024, down 1024x3072} Q4_K +
         # the 151936x1024 Q6_K lm_head), four fused launches per layer as in the 8B step.

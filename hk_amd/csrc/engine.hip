@@ -183,7 +183,7 @@ int hkhip_upload(hkhip_engine *eng, const void *src, uint64_t bytes, uint8_t t, 
     void *mem = nullptr;
     HIP_TRY(hipMalloc(&mem, L.total ? L.total : 1), "hipMalloc weights");
     hipError_t e = hipSuccess;
-    if (t == HKHIP_Q4_K) {
+    if (t == HKHIP_Q4_K || t == HKHIP_Q5_K) { // device layout = file layout
         e = hipMemcpyAsync(mem, src, need, src_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, eng->cur);
     } else {
         const uint8_t *staged = reinterpret_cast<const uint8_t *>(src);
