@@ -157,6 +157,45 @@ __device__ __forceinline__ v16f min_j(const uint32_t *tm, v8bf mn, uint32_t h, f
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, w), mn, v16f{}, 0, 0, 0);
 }
 
+// Q5_K: four 5-bit quants u (bytes; even bytes ev, odd od, as 16-bit lanes) times a factor e
+// in [0, 7], minus 16e: per byte (u - 16)*e in [-112, 105] as a two's-complement byte (packed
+// 16-bit multiply-adds keep the bytes apart; the low byte of each lane is the wanted one).
+// -16e in both 16-bit lanes, for a factor e held as e * 0x00010001.
+__device__ __forceinline__ uint32_t neg16(uint32_t m) { return ((0u - 16u * (m & 0xFFFFu)) & 0xFFFFu) * 0x00010001u; }
+__device__ __forceinline__ uint32_t plane_c16(uint32_t ev, uint32_t od, uint32_t m, uint32_t c) {
+    const us2 pe = __builtin_bit_cast(us2, ev) * __builtin_bit_cast(us2, m) + __builtin_bit_cast(us2, c);
+    const us2 po = __builtin_bit_cast(us2, od) * __builtin_bit_cast(us2, m) + __builtin_bit_cast(us2, c);
+    return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, po), __builtin_bit_cast(uint32_t, pe), 0x06020400u);
+}
+
+// Q5_K's row-side min-term operand: per sub-block s, 16*d*sc_s - dmin*mn_s (the weights enter
+// the planes as u - 16, and 16*sum(sc*a) = 16*sc*bsum32 returns through the min term), split as
+// min_operands does.
+__device__ __forceinline__ MinB min_operands_k5(uint32_t scl, uint32_t sch, float d, uint32_t mnl, uint32_t mnh,
+                                                float dmin, uint32_t h) {
+    uint32_t w[3][4];
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+        uint32_t p[3];
+        const float sc = (float)(((s < 4 ? scl : sch) >> (8 * (s & 3))) & 0xFF);
+        const float mn = (float)(((s < 4 ? mnl : mnh) >> (8 * (s & 3))) & 0xFF);
+        bf16_split3(16.0f * d * sc - dmin * mn, p);
+#pragma unroll
+        for (int q = 0; q < 3; q++) {
+            if (s & 1)
+                w[q][s / 2] |= p[q] << 16;
+            else
+                w[q][s / 2] = p[q];
+        }
+    }
+    MinB m;
+    m.b1 = __builtin_bit_cast(v8bf, make_uint4(w[0][0], w[0][1], w[0][2], w[0][3]));
+    m.b2 = __builtin_bit_cast(v8bf, make_uint4(w[1][0], w[1][1], w[1][2], w[1][3]));
+    const uint32_t q = h ? 0 : 2;
+    m.b3 = __builtin_bit_cast(v8bf, make_uint4(w[q][0], w[q][1], w[q][2], w[q][3]));
+    return m;
+}
+
 // Four nibble bytes (values 0..15) times a 3-bit scale factor: each byte product is at most
 // 105, so a packed 16-bit multiply of the word keeps every byte separate.
 __device__ __forceinline__ uint32_t mul_bytes(uint32_t nib, uint32_t f2) {
@@ -172,9 +211,13 @@ template <int TOK> struct Q2Smem {
 // Large-tile variant: weights go global -> registers (each lane its own row half), loaded
 // while the previous super-block computes; activations and token data through LDS, double
 // buffered. Measured faster than staging the weights in LDS for this tile.
-template <int Q2_NW, int Q2_TT>
+// Q5_K (T = HKHIP_Q5_K) runs the same tile: the fifth bits come from the lane's half of qh, the
+// planes hold (u - 16)*sh and (u - 16)*sl, and the min term carries 16*d*sc - dmin*mn.
+template <int T, int Q2_NW, int Q2_TT>
 __global__ __launch_bounds__(Q2_NW * 64, 2) void mm2_q4k_reg_kernel(Mm2Args a) {
     constexpr int Q2_ROWS = 32 * Q2_NW, Q2_TOK = 32 * Q2_TT;
+    constexpr bool k5 = (T == HKHIP_Q5_K);
+    constexpr uint32_t BB = k5 ? 176 : 144, QO = k5 ? 48 : 16; // block bytes, qs offset
     extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
     Q2Smem<Q2_TOK> &S = *reinterpret_cast<Q2Smem<Q2_TOK> *>(smem_raw);
     const uint32_t tid = threadIdx.x, lane = tid & 63;
@@ -200,7 +243,7 @@ __global__ __launch_bounds__(Q2_NW * 64, 2) void mm2_q4k_reg_kernel(Mm2Args a) {
     const uint32_t r0 = rb * Q2_ROWS, t0 = tb * Q2_TOK;
     const uint32_t myrow = r0 + 32 * wave + j;
     const uint32_t wrow = myrow < a.rows ? myrow : a.rows - 1;
-    const uint8_t *wbase = a.w + uint64_t(wrow) * nsb * 144;
+    const uint8_t *wbase = a.w + uint64_t(wrow) * nsb * BB;
 
     // ---- staging of one super-block of activations ----
     // The int8 values go global -> LDS directly (global_load_lds_dwordx4: lane L of a wave writes
@@ -255,12 +298,13 @@ __global__ __launch_bounds__(Q2_NW * 64, 2) void mm2_q4k_reg_kernel(Mm2Args a) {
     };
 
     // ---- this lane's weights: its row's half (h) of a super-block ----
-    uint4 wh, wq[4];
+    uint4 wh, wq[4], wx;
     auto wload = [&](uint32_t sb) {
-        const uint8_t *blk = wbase + uint64_t(sb) * 144;
+        const uint8_t *blk = wbase + uint64_t(sb) * BB;
         wh = ldg16(blk);
 #pragma unroll
-        for (int p = 0; p < 4; p++) wq[p] = ldg16(blk + 16 + 32 * p + 16 * h);
+        for (int p = 0; p < 4; p++) wq[p] = ldg16(blk + QO + 32 * p + 16 * h);
+        if constexpr (k5) wx = ldg16(blk + 16 + 16 * h); // qh bytes 16h.. (this lane's weights)
     };
 
     v16f acc[Q2_TT];
@@ -277,7 +321,7 @@ __global__ __launch_bounds__(Q2_NW * 64, 2) void mm2_q4k_reg_kernel(Mm2Args a) {
 
     for (uint32_t sb = 0; sb < nsb; sb++) {
         const uint32_t buf = sb & 1;
-        const uint4 ch = wh, c0 = wq[0], c1 = wq[1], c2 = wq[2], c3 = wq[3];
+        const uint4 ch = wh, c0 = wq[0], c1 = wq[1], c2 = wq[2], c3 = wq[3], cx = wx;
         const uint32_t nx = sb + 1 < nsb ? sb + 1 : sb;
         stage_load(nx, buf ^ 1);
 
@@ -296,17 +340,34 @@ __global__ __launch_bounds__(Q2_NW * 64, 2) void mm2_q4k_reg_kernel(Mm2Args a) {
             const uint32_t she = (se >> 3) * 0x00010001u, sle = (se & 7) * 0x00010001u;
             const uint32_t sho = (so >> 3) * 0x00010001u, slo = (so & 7) * 0x00010001u;
             const uint32_t qw[4] = {cq[p].x, cq[p].y, cq[p].z, cq[p].w};
+            const uint32_t xw[4] = {cx.x, cx.y, cx.z, cx.w};
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const uint32_t ne = qw[i] & 0x0F0F0F0Fu, no = (qw[i] >> 4) & 0x0F0F0F0Fu;
-                bhi[2 * p][i] = int(mul_bytes(ne, she));
-                blo[2 * p][i] = int(mul_bytes(ne, sle));
-                bhi[2 * p + 1][i] = int(mul_bytes(no, sho));
-                blo[2 * p + 1][i] = int(mul_bytes(no, slo));
+                if constexpr (k5) {
+                    // Fifth bits: bit 2p (low nibbles) / 2p + 1 (high) of qh (k4Block has_high).
+                    const uint32_t ue = ne | (((xw[i] >> (2 * p)) & 0x01010101u) << 4);
+                    const uint32_t uo = no | (((xw[i] >> (2 * p + 1)) & 0x01010101u) << 4);
+                    const uint32_t ee = ue & 0x00FF00FFu, eo = (ue >> 8) & 0x00FF00FFu;
+                    const uint32_t oe = uo & 0x00FF00FFu, oo = (uo >> 8) & 0x00FF00FFu;
+                    bhi[2 * p][i] = int(plane_c16(ee, eo, she, neg16(she)));
+                    blo[2 * p][i] = int(plane_c16(ee, eo, sle, neg16(sle)));
+                    bhi[2 * p + 1][i] = int(plane_c16(oe, oo, sho, neg16(sho)));
+                    blo[2 * p + 1][i] = int(plane_c16(oe, oo, slo, neg16(slo)));
+                } else {
+                    bhi[2 * p][i] = int(mul_bytes(ne, she));
+                    blo[2 * p][i] = int(mul_bytes(ne, sle));
+                    bhi[2 * p + 1][i] = int(mul_bytes(no, sho));
+                    blo[2 * p + 1][i] = int(mul_bytes(no, slo));
+                }
             }
         }
         // Min-term operands of this lane's row.
-        const MinB mB = min_operands(mnl, mnh, dmin, h);
+        MinB mB;
+        if constexpr (k5)
+            mB = min_operands_k5(scl, sch, d, mnl, mnh, dmin, h);
+        else
+            mB = min_operands(mnl, mnh, dmin, h);
 
         // A operand of tile t, sub-block s: token 32t + j, chunk 2s + h (swizzled).
         const int8_t *abase = &S.a[buf][j * 256];
@@ -614,15 +675,18 @@ __global__ __launch_bounds__(NW * KS * 64, 2) void mm2_q4k_kernel(Mm2Args a) {
 bool mm2_supports(int t, uint32_t rows, uint32_t cols, uint32_t n) {
     // The kernels' per-lane byte offsets are 32-bit: weights rows*cols*9/16 bytes, activations
     // n*cols bytes.
+    if (t == HKHIP_Q5_K) // the register tile only, where it fills the GPU (mmx takes the rest)
+        return cols % 256 == 0 && ((rows + 255) / 256) * ((n + 127) / 128) >= 192 &&
+               uint64_t(rows) * (cols / 256) * 176 < (1ull << 32) && uint64_t(n) * cols < (1ull << 32);
     return t == HKHIP_Q4_K && cols % 256 == 0 && rows > 0 && n > 0 &&
            uint64_t(rows) * (cols / 256) * 144 < (1ull << 32) && uint64_t(n) * cols < (1ull << 32);
 }
 
 typedef void (*mm2_kernel_t)(Mm2Args);
 
-template <int NW, int TT>
+template <int NW, int TT, int T = HKHIP_Q4_K>
 static hipError_t launch_mm2_reg(const Mm2Args &a0, hipStream_t s) {
-    const mm2_kernel_t k = mm2_q4k_reg_kernel<NW, TT>;
+    const mm2_kernel_t k = mm2_q4k_reg_kernel<T, NW, TT>;
     constexpr size_t lds = sizeof(Q2Smem<32 * TT>);
     static bool attr = false;
     if (!attr) {
@@ -672,6 +736,7 @@ hipError_t launch_mm2(int t, const uint8_t *w, uint32_t rows, uint32_t cols, con
     // Below that, K slices give the SIMDs a second wave (measured at 512 tokens: 4096x14336
     // 104 -> 87 us with two slices, 1024x3072 16.8 -> 10.7 us with four).
     const uint32_t nsb = cols / 256;
+    if (t == HKHIP_Q5_K) return launch_mm2_reg<8, 4, HKHIP_Q5_K>(a, s); // mm2_supports: large shapes only
     if (blocks(8, 4) >= 192) return launch_mm2_reg<8, 4>(a, s);
     if (blocks(4, 2) >= 160) return nsb >= 4 ? launch_mm2_cfg<4, 2, 2, 2>(a, s) : launch_mm2_cfg<4, 2, 2>(a, s);
     if (blocks(2, 1) >= 128) {
