@@ -197,7 +197,8 @@ def main():
                                   ("qwen3-0.6b-ffn-down", F.Q4_K, 1024, 3072),
                                   ("llama8b-ffn-down", F.Q4_K, H, FF),
                                   ("llama8b-ffn-up", F.IQ4_NL, FF, H), ("llama8b-ffn-down", F.Q6_K, H, FF)] + \
-                                 [("llama8b-ffn-up", t, FF, H) for t in (F.Q4_0, F.Q4_1, F.Q5_0, F.Q5_1, F.Q5_K, F.IQ4_XS)]:
+                                 [("llama8b-ffn-up", t, FF, H) for t in (F.Q4_0, F.Q4_1, F.Q5_0, F.Q5_1, F.Q5_K, F.IQ4_XS)] + \
+                                 [("llama8b-ffn-down", F.Q5_K, H, FF)]:
             n = 512
             reuse = layers[0]["gate"] if (t, m_, k_) == (F.Q4_K, FF, H) else None
             w = reuse or upload_synth(t, m_, k_, synth.seed_for(3, m_ + k_ + t))

@@ -59,9 +59,9 @@ typedef unsigned short us2 __attribute__((ext_vector_type(2)));
 //   da  per token, the Q8K scale
 // Every wave issues the same loads (waves past the tokens load duplicates into their own spare
 // entries), so the in-order memory counter can be waited on with a constant.
-template <int TOK, int NW> struct Q2Slot {
+template <int TOK, int NW, int WB = 4608> struct Q2Slot {
     int8_t a[TOK * 256];
-    uint8_t w[NW][4608];
+    uint8_t w[NW][WB]; // 32 rows x 144 (Q4_K) or 176 (Q5_K) bytes
     uint32_t mb[NW * 32][8]; // token t at mb[t]; wave m's load fills tokens 32m..32m+31
     float da[NW * 64];       // token t at da[t]; wave m's load fills tokens 64m..64m+63
 };
@@ -433,10 +433,14 @@ __global__ __launch_bounds__(Q2_NW * 64, 2) void mm2_q4k_reg_kernel(Mm2Args a) {
 // KS > 1 splits K: the workgroup's waves form KS slices of NW waves; slice k takes super-blocks
 // k, k + KS, ... through a ring of its own, and the slices' partial tiles are added in LDS (in
 // slice order) at the end. For matrices too small to give every SIMD two waves otherwise.
-template <int NW, int TT, int NB, int KS = 1>
+template <int NW, int TT, int NB, int KS = 1, int T = HKHIP_Q4_K>
 __global__ __launch_bounds__(NW * KS * 64, 2) void mm2_q4k_kernel(Mm2Args a) {
     constexpr int ROWS = 32 * NW, TOK = 32 * TT;
-    using Slot = Q2Slot<TOK, NW>;
+    // Q5_K: 176-byte rows (5 x 1 KB + 512 B per wave and step), the register tile's planes and
+    // a second exact integer, Jsc = sum sc*bsum32, for the 16*sum(sc*a) the planes' u - 16 removes.
+    constexpr bool k5 = (T == HKHIP_Q5_K);
+    constexpr uint32_t BB = k5 ? 176 : 144, PR = BB / 16, WR = BB / 4, W16 = k5 ? 5 : 4, QO = k5 ? 48 : 16;
+    using Slot = Q2Slot<TOK, NW, 32 * BB>;
     static_assert(NB == 2 || NB == 3, "ring depth");
     // The ring's slots are LDS objects of their own, and the loop below is unrolled over them.
     __shared__ __attribute__((aligned(16))) Slot ring0[KS];
@@ -478,22 +482,22 @@ __global__ __launch_bounds__(NW * KS * 64, 2) void mm2_q4k_kernel(Mm2Args a) {
     // ---- the direct loads of one super-block into a slot (CPW per wave) ----
     constexpr uint32_t TPW = TOK / NW; // token rows per wave
     static_assert(TPW % 4 == 0, "token rows per wave");
-    constexpr uint32_t CPW = TPW / 4 + 6 + 1 + 1; // a + w + mb + da
+    constexpr uint32_t CPW = TPW / 4 + W16 + 2 + 1 + 1; // a + w + mb + da
     // Weight bytes of this wave: 16-byte piece P (64*i + lane, i < 4) is byte 16*(P%9) of row
     // P/9's block; the last 512 bytes (pieces 256..287) go as 4-byte words 1024 + 64*i + lane.
     // Per-lane 32-bit byte offsets from uniform bases (mm2_supports checks that they fit).
-    uint32_t woff[6];
+    uint32_t woff[W16 + 2];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (uint32_t i = 0; i < W16; i++) {
         const uint32_t P = 64 * i + lane;
-        const uint32_t row = r0 + 32 * wave + P / 9, rr = row < a.rows ? row : a.rows - 1;
-        woff[i] = rr * nsb * 144 + 16 * (P % 9);
+        const uint32_t row = r0 + 32 * wave + P / PR, rr = row < a.rows ? row : a.rows - 1;
+        woff[i] = rr * nsb * BB + 16 * (P % PR);
     }
 #pragma unroll
     for (int i = 0; i < 2; i++) {
-        const uint32_t Wd = 1024 + 64 * i + lane; // 4-byte word index in the wave's area
-        const uint32_t row = r0 + 32 * wave + Wd / 36, rr = row < a.rows ? row : a.rows - 1;
-        woff[4 + i] = rr * nsb * 144 + 4 * (Wd % 36);
+        const uint32_t Wd = 256 * W16 + 64 * i + lane; // 4-byte word index in the wave's area
+        const uint32_t row = r0 + 32 * wave + Wd / WR, rr = row < a.rows ? row : a.rows - 1;
+        woff[W16 + i] = rr * nsb * BB + 4 * (Wd % WR);
     }
     uint32_t aoff[TPW / 4];
 #pragma unroll
@@ -507,11 +511,11 @@ __global__ __launch_bounds__(NW * KS * 64, 2) void mm2_q4k_kernel(Mm2Args a) {
         const int8_t *ga = a.aqs + 256 * sb;
 #pragma unroll
         for (uint32_t i = 0; i < TPW / 4; i++) load_lds16(ga + aoff[i], &S.a[(TPW * wave + 4 * i) * 256]);
-        const uint8_t *gw = a.w + uint64_t(sb) * 144;
+        const uint8_t *gw = a.w + uint64_t(sb) * BB;
 #pragma unroll
-        for (int i = 0; i < 4; i++) load_lds16(gw + woff[i], &S.w[wave][1024 * i]);
+        for (uint32_t i = 0; i < W16; i++) load_lds16(gw + woff[i], &S.w[wave][1024 * i]);
 #pragma unroll
-        for (int i = 0; i < 2; i++) load_lds4(gw + woff[4 + i], &S.w[wave][4096 + 256 * i]);
+        for (int i = 0; i < 2; i++) load_lds4(gw + woff[W16 + i], &S.w[wave][1024 * W16 + 256 * i]);
         {
             const uint32_t tl = 32 * wave + lane / 2, tok = t0 + (tl < TOK ? tl : 0);
             const uint32_t tk = tok < a.n ? tok : a.n - 1;
@@ -551,11 +555,12 @@ __global__ __launch_bounds__(NW * KS * 64, 2) void mm2_q4k_kernel(Mm2Args a) {
         Slot &S = slot_at(ic);
         if (KS == 1 || ks + KS * st < nsb) {
             // Unpack this lane's row half (h) from LDS: header, then both planes of 8 sub-blocks.
-            const uint8_t *blk = &S.w[wave][144 * j];
+            const uint8_t *blk = &S.w[wave][BB * j];
             const uint4 ch = *reinterpret_cast<const uint4 *>(blk);
-            uint4 cq[4];
+            uint4 cq[4], cx{};
 #pragma unroll
-            for (int p = 0; p < 4; p++) cq[p] = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * p + 16 * h);
+            for (int p = 0; p < 4; p++) cq[p] = *reinterpret_cast<const uint4 *>(blk + QO + 32 * p + 16 * h);
+            if constexpr (k5) cx = *reinterpret_cast<const uint4 *>(blk + 16 + 16 * h);
             // Scales: vecdot.zig:461-474 word form.
             const uint32_t k1 = 0x3f3f3f3fu, k2 = 0x0f0f0f0fu, k3 = 0x03030303u;
             const uint32_t scl = ch.y & k1, mnl = ch.z & k1;
@@ -570,17 +575,30 @@ __global__ __launch_bounds__(NW * KS * 64, 2) void mm2_q4k_kernel(Mm2Args a) {
                 const uint32_t she = (se >> 3) * 0x00010001u, sle = (se & 7) * 0x00010001u;
                 const uint32_t sho = (so >> 3) * 0x00010001u, slo = (so & 7) * 0x00010001u;
                 const uint32_t qw[4] = {cq[p].x, cq[p].y, cq[p].z, cq[p].w};
+                const uint32_t xw[4] = {cx.x, cx.y, cx.z, cx.w};
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const uint32_t ne = qw[i] & 0x0F0F0F0Fu, no = (qw[i] >> 4) & 0x0F0F0F0Fu;
-                    bhi[2 * p][i] = int(mul_bytes(ne, she));
-                    blo[2 * p][i] = int(mul_bytes(ne, sle));
-                    bhi[2 * p + 1][i] = int(mul_bytes(no, sho));
-                    blo[2 * p + 1][i] = int(mul_bytes(no, slo));
+                    if constexpr (k5) {
+                        const uint32_t ue = ne | (((xw[i] >> (2 * p)) & 0x01010101u) << 4);
+                        const uint32_t uo = no | (((xw[i] >> (2 * p + 1)) & 0x01010101u) << 4);
+                        const uint32_t ee = ue & 0x00FF00FFu, eo = (ue >> 8) & 0x00FF00FFu;
+                        const uint32_t oe = uo & 0x00FF00FFu, oo = (uo >> 8) & 0x00FF00FFu;
+                        bhi[2 * p][i] = int(plane_c16(ee, eo, she, neg16(she)));
+                        blo[2 * p][i] = int(plane_c16(ee, eo, sle, neg16(sle)));
+                        bhi[2 * p + 1][i] = int(plane_c16(oe, oo, sho, neg16(sho)));
+                        blo[2 * p + 1][i] = int(plane_c16(oe, oo, slo, neg16(slo)));
+                    } else {
+                        bhi[2 * p][i] = int(mul_bytes(ne, she));
+                        blo[2 * p][i] = int(mul_bytes(ne, sle));
+                        bhi[2 * p + 1][i] = int(mul_bytes(no, sho));
+                        blo[2 * p + 1][i] = int(mul_bytes(no, slo));
+                    }
                 }
             }
             // Min-term operand of this lane's row.
             const v8bf mB = min_b(mnl, mnh);
+            const v8bf sB = k5 ? min_b(scl, sch) : mB; // Q5_K: the scales as exact bf16 integers
             const float ndmin = -dmin;
 
             // A operand of tile t, sub-block s: token 32t + j, chunk 2s + h (swizzled).
@@ -596,6 +614,8 @@ __global__ __launch_bounds__(NW * KS * 64, 2) void mm2_q4k_kernel(Mm2Args a) {
 #pragma unroll
             for (int t = 0; t < TT; t++) {
                 const v16f jt = min_j(S.mb[32 * t + j], mB, h, acc[t][15]);
+                v16f js = {};
+                if constexpr (k5) js = min_j(S.mb[32 * t + j], sB, h, jt[15]);
                 // One accumulator: the sh-plane chain, times 8, then the sl-plane chain on top.
                 v16i sacc = {};
 #pragma unroll
@@ -614,7 +634,8 @@ __global__ __launch_bounds__(NW * KS * 64, 2) void mm2_q4k_kernel(Mm2Args a) {
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
                         const int v = 4 * g + e;
-                        acc[t][v] = fmaf(fmaf((float)sacc[v], d, ndmin * jt[v]), ds[e], acc[t][v]);
+                        const float iv = k5 ? fmaf(16.0f, js[v], (float)sacc[v]) : (float)sacc[v];
+                        acc[t][v] = fmaf(fmaf(iv, d, ndmin * jt[v]), ds[e], acc[t][v]);
                     }
                 }
             }
@@ -675,8 +696,9 @@ __global__ __launch_bounds__(NW * KS * 64, 2) void mm2_q4k_kernel(Mm2Args a) {
 bool mm2_supports(int t, uint32_t rows, uint32_t cols, uint32_t n) {
     // The kernels' per-lane byte offsets are 32-bit: weights rows*cols*9/16 bytes, activations
     // n*cols bytes.
-    if (t == HKHIP_Q5_K) // the register tile only, where it fills the GPU (mmx takes the rest)
-        return cols % 256 == 0 && ((rows + 255) / 256) * ((n + 127) / 128) >= 192 &&
+    if (t == HKHIP_Q5_K) // the register tile and the 128-row ring tile, where they fill the GPU
+        return cols % 256 == 0 &&
+               (((rows + 255) / 256) * ((n + 127) / 128) >= 192 || ((rows + 127) / 128) * ((n + 63) / 64) >= 160) &&
                uint64_t(rows) * (cols / 256) * 176 < (1ull << 32) && uint64_t(n) * cols < (1ull << 32);
     return t == HKHIP_Q4_K && cols % 256 == 0 && rows > 0 && n > 0 &&
            uint64_t(rows) * (cols / 256) * 144 < (1ull << 32) && uint64_t(n) * cols < (1ull << 32);
@@ -700,10 +722,10 @@ static hipError_t launch_mm2_reg(const Mm2Args &a0, hipStream_t s) {
     return hipGetLastError();
 }
 
-template <int NW, int TT, int NB, int KS = 1>
+template <int NW, int TT, int NB, int KS = 1, int T = HKHIP_Q4_K>
 static hipError_t launch_mm2_cfg(const Mm2Args &a0, hipStream_t s) {
-    const mm2_kernel_t k = mm2_q4k_kernel<NW, TT, NB, KS>;
-    static_assert(NB * KS * sizeof(Q2Slot<32 * TT, NW>) <= 160 * 1024, "LDS");
+    const mm2_kernel_t k = mm2_q4k_kernel<NW, TT, NB, KS, T>;
+    static_assert(NB * KS * sizeof(Q2Slot<32 * TT, NW, T == HKHIP_Q5_K ? 5632 : 4608>) <= 160 * 1024, "LDS");
     constexpr size_t lds = 0; // the ring is static
     Mm2Args a = a0;
     a.rblocks = (a.rows + 32 * NW - 1) / (32 * NW);
@@ -736,7 +758,8 @@ hipError_t launch_mm2(int t, const uint8_t *w, uint32_t rows, uint32_t cols, con
     // Below that, K slices give the SIMDs a second wave (measured at 512 tokens: 4096x14336
     // 104 -> 87 us with two slices, 1024x3072 16.8 -> 10.7 us with four).
     const uint32_t nsb = cols / 256;
-    if (t == HKHIP_Q5_K) return launch_mm2_reg<8, 4, HKHIP_Q5_K>(a, s); // mm2_supports: large shapes only
+    if (t == HKHIP_Q5_K) // mm2_supports: these two tiles only (two K slices would not fit the LDS)
+        return blocks(8, 4) >= 192 ? launch_mm2_reg<8, 4, HKHIP_Q5_K>(a, s) : launch_mm2_cfg<4, 2, 2, 1, HKHIP_Q5_K>(a, s);
     if (blocks(8, 4) >= 192) return launch_mm2_reg<8, 4>(a, s);
     if (blocks(4, 2) >= 160) return nsb >= 4 ? launch_mm2_cfg<4, 2, 2, 2>(a, s) : launch_mm2_cfg<4, 2, 2>(a, s);
     if (blocks(2, 1) >= 128) {

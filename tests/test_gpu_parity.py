@@ -293,7 +293,8 @@ def test_baseline_prefill_shapes(eng, torch_cuda, t, m, k):
                          [(t, 9000, 512, 260, 0) for t in LOW4 + [F.IQ4_XS]] + [(F.IQ4_XS, 1000, 768, 50, 0),
                                                                         (F.Q5_K, 4000, 1280, 300, 1), (F.Q5_K, 9000, 512, 260, 0),
                                                                         (F.Q5_K, 1000, 768, 50, 1),
-                                                                        (F.Q5_K, 12288, 512, 520, 1), (F.Q5_K, 12300, 768, 512, 0)])
+                                                                        (F.Q5_K, 12288, 512, 520, 1), (F.Q5_K, 12300, 768, 512, 0),
+                                                                        (F.Q5_K, 4096, 1024, 512, 1), (F.Q5_K, 4100, 768, 330, 0)])
 def test_gemm_configs_other_formats(eng, torch_cuda, t, m, k, n, mode):
     """The Q6_K / Q8_0 / IQ4_NL GEMM's configurations: IQ4_NL split over two K slices (5
     super-blocks) and its 256-row tile; ragged rows and tokens, bias, accumulate."""
