@@ -325,14 +325,16 @@ int hkhip_gemm(hkhip_engine *eng, const hkhip_mat *m, const void *xq_dev, float 
 // Fewest tokens for which the GEMM beats 8-token matvec passes (measured on MI355X at the
 // Llama-3-8B FFN shapes: a GEMM pass costs about as much at 16 tokens as at 64, while each
 // matvec pass of 8 tokens streams the weights once more).
-static uint32_t gemm_min_tokens(int t) {
+static uint32_t gemm_min_tokens(int t, uint32_t rows) {
     switch (t) {
     case HKHIP_Q6_K:
-    case HKHIP_Q5_K: // Q6_K's (its GEMM is VALU-bound too; not measured separately)
     case HKHIP_Q8_0: return 33;
-    case HKHIP_IQ4_NL:
-    case HKHIP_Q4_0: case HKHIP_Q4_1: case HKHIP_Q5_0: case HKHIP_Q5_1: case HKHIP_IQ4_XS:
-        return 25; // IQ4_NL's (same quant bytes per 32 weights)
+    case HKHIP_IQ4_NL: return 25;
+    case HKHIP_Q5_K: case HKHIP_Q4_0: case HKHIP_Q4_1: case HKHIP_Q5_0: case HKHIP_Q5_1: case HKHIP_IQ4_XS:
+        // Measured at 9-64 tokens: with 14336 rows the GEMM is as fast as two decode passes from
+        // 9 tokens (34-44 us either way); with 4096 rows (K 14336) it costs 105-140 us at any
+        // count, which the passes (20-24 us per 8 tokens) reach at 40-48 tokens.
+        return rows >= 8192 ? 9 : 41;
     default: return 9;
     }
 }
@@ -342,7 +344,7 @@ int hkhip_mm(hkhip_engine *eng, const hkhip_mat *m, const void *xq_dev, float *y
     // The CPU engine tiles from min_tiled_tokens = 8 (matmul.zig:18); here the register matvec
     // covers up to 8 tokens and, below the GEMM's break-even, runs in passes of 8.
     if (n <= 8) return hkhip_matvec(eng, m, xq_dev, y_dev, n, bias_dev, mode);
-    if (n >= gemm_min_tokens(m->t)) return hkhip_gemm(eng, m, xq_dev, y_dev, n, bias_dev, mode);
+    if (n >= gemm_min_tokens(m->t, m->rows)) return hkhip_gemm(eng, m, xq_dev, y_dev, n, bias_dev, mode);
     int rc = enter(eng);
     if (rc || (rc = check_product(m, xq_dev, y_dev, n, mode))) return rc;
     HIP_TRY(launch_mmvq(m->t, reinterpret_cast<const uint8_t *>(m->mem), m->rows, m->cols,
