@@ -331,10 +331,12 @@ static uint32_t gemm_min_tokens(int t, uint32_t rows) {
     case HKHIP_Q8_0: return 33;
     case HKHIP_IQ4_NL: return 25;
     case HKHIP_Q5_K: case HKHIP_Q4_0: case HKHIP_Q4_1: case HKHIP_Q5_0: case HKHIP_Q5_1: case HKHIP_IQ4_XS:
-        // Measured at 9-64 tokens: with 14336 rows the GEMM is as fast as two decode passes from
-        // 9 tokens (34-44 us either way); with 4096 rows (K 14336) it costs 105-140 us at any
-        // count, which the passes (20-24 us per 8 tokens) reach at 40-48 tokens.
-        return rows >= 8192 ? 9 : 41;
+        // Measured at 9-64 tokens: with 14336 rows the GEMM beats two decode passes from 9
+        // tokens; with 4096 rows (K 14336) it costs 50-120 us at any count (Q4_1 50, IQ4_XS 66,
+        // Q5_1 82, Q5_0 98, Q4_0 104, Q5_K 118), which the passes (20-25 us per 8 tokens) reach at
+        // the counts below.
+        if (rows >= 8192) return 9;
+        return t == HKHIP_Q4_1 ? 17 : (t == HKHIP_IQ4_XS || t == HKHIP_Q5_1) ? 25 : t == HKHIP_Q5_0 ? 33 : 41;
     default: return 9;
     }
 }

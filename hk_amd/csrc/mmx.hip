@@ -536,6 +536,16 @@ template <int T> hipError_t launch_low4(const MxArgs &a, hipStream_t s, uint32_t
     } else {
         if (b42 >= 128 && a.cols >= 1024) return launch_cfg<T, 4, 2, 2, 2>(a, s);
     }
+    // Long rows and few row blocks or tokens (measured at the 8B FFN shapes, 9-64 tokens): 64-row
+    // tiles split over K slices (Q4_1 4096 x 14336: 127 -> 50 us, 14336 x 4096 at <= 32 tokens:
+    // 40 -> 19 us). Not for Q4_0, which measured slower so (104 -> 120 us), nor for 14336 rows
+    // past one token tile (the grid doubles: 34 -> 74 us).
+    if (T != HKHIP_Q4_0 && a.cols >= 4096 && (a.rows < 8192 || a.n <= 32)) {
+        if constexpr (has_qh(T))
+            return launch_cfg<T, 2, 1, 2, 2>(a, s);
+        else
+            return launch_cfg<T, 2, 1, 2, 4>(a, s);
+    }
     return launch_cfg<T, 4, 1, 2>(a, s);
 }
 
@@ -595,6 +605,7 @@ hipError_t launch_mmx(int t, const uint8_t *w, uint32_t rows, uint32_t cols, con
     case HKHIP_IQ4_XS:
         if (blocks(8, 2) >= 224) return mx::launch_cfg<HKHIP_IQ4_XS, 8, 2, 2>(a, s);
         if (blocks(4, 2) >= 128 && cols >= 1024) return mx::launch_cfg<HKHIP_IQ4_XS, 4, 2, 2, 2>(a, s);
+        if (cols >= 4096 && (rows < 8192 || n <= 32)) return mx::launch_cfg<HKHIP_IQ4_XS, 2, 1, 2, 4>(a, s);
         return mx::launch_cfg<HKHIP_IQ4_XS, 4, 1, 2>(a, s);
     default: return hipErrorInvalidValue;
     }
