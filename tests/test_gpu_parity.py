@@ -294,7 +294,10 @@ def test_baseline_prefill_shapes(eng, torch_cuda, t, m, k):
                                                                         (F.Q5_K, 4000, 1280, 300, 1), (F.Q5_K, 9000, 512, 260, 0),
                                                                         (F.Q5_K, 1000, 768, 50, 1),
                                                                         (F.Q5_K, 12288, 512, 520, 1), (F.Q5_K, 12300, 768, 512, 0),
-                                                                        (F.Q5_K, 4096, 1024, 512, 1), (F.Q5_K, 4100, 768, 330, 0)])
+                                                                        (F.Q5_K, 4096, 1024, 512, 1), (F.Q5_K, 4100, 768, 330, 0)] +
+                         # 64-row tiles over K slices: few row blocks (K 4096), or few tokens
+                         [(t, 1000, 4096, 40, 1) for t in (F.Q4_1, F.Q5_0, F.Q5_1, F.IQ4_XS)] +
+                         [(t, 9000, 4352, 20, 0) for t in (F.Q4_1, F.Q5_0, F.Q5_1, F.IQ4_XS)])
 def test_gemm_configs_other_formats(eng, torch_cuda, t, m, k, n, mode):
     """The Q6_K / Q8_0 / IQ4_NL GEMM's configurations: IQ4_NL split over two K slices (5
     super-blocks) and its 256-row tile; ragged rows and tokens, bias, accumulate."""
