@@ -31,3 +31,19 @@ def parity_err(got: np.ndarray, want: np.ndarray) -> float:
 
 
 PARITY_TOL = 1e-3  # max relative error 1e-3 against hk's CPU kernels
+
+
+def tie_rows(k: int) -> np.ndarray:
+    """Activations on which round-half-away and round-half-even disagree, with hand-checkable
+    quantized values (reference vecdot.zig:134-148, 150-180: Zig's @round rounds half away).
+
+    Every 32-value block starts with -127, so amax = 127: the A8 scale is d = 127/127 = 1 and
+    1/d = 1 exactly, and for Q8K the signed max of every 256-block is -127, so iscale =
+    -127/-127 = 1. Then q = round(x) exactly, and the other values k + 0.5 (k = -15..14) are ties:
+    round-half-away gives k + 1 for k >= 0 and k for k < 0; rint would give the even neighbour.
+    Returns x [1][k] and the expected q [1][k] (int64)."""
+    blk = np.concatenate([[-127.0], np.arange(-15, 16) + 0.5]).astype(np.float32)  # 32 values
+    x = np.tile(blk, k // 32)[None, :]
+    q = np.where(x >= 0, np.floor(x) + 1, np.ceil(x) - 1).astype(np.int64)  # away from zero
+    q[:, ::32] = -127
+    return x, q

@@ -15,7 +15,7 @@ from hk_amd import formats as F
 from hk_amd import synth
 from hk_amd.engine import ACCUMULATE, SILU_MUL
 from oracle import oracle as O
-from tests.helpers import PARITY_TOL, load_fixture, parity_err
+from tests.helpers import PARITY_TOL, load_fixture, parity_err, tie_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -96,7 +96,7 @@ def _act_cases():
     x[2, 200] = -7.5                      # tie on |x|: the first one sets the sign of d
     x[3] *= 1e-30                         # tiny (denormal-range) values
     x[4] = synth.activations_np(1, 1024, 3, outliers=0.01)[0]
-    return x
+    return np.concatenate([x, tie_rows(1024)[0]])  # ties k + 0.5 at scale 1: round half away
 
 
 @pytest.mark.parametrize("kind", [F.ACT_A8, F.ACT_Q8K])
@@ -109,6 +109,24 @@ def test_qact_bit_exact(eng, torch_cuda, kind):
     got = eng.act_export(xq, n, k, kind)
     want = np.concatenate([(O.quantize_a8 if kind == F.ACT_A8 else O.quantize_q8k)(x[i]) for i in range(n)])
     assert np.array_equal(got, want.view(np.uint8))
+    tie = want[-(k // (32 if kind == F.ACT_A8 else 256)):]
+    assert np.array_equal(tie["qs"].astype(np.int64).ravel(), tie_rows(k)[1][0])  # the closed form
+
+
+@pytest.mark.parametrize("t", FMTS)
+def test_in_kernel_qact_rounds_ties_away(eng, torch_cuda, t):
+    """The decode kernels' own quantization of an f32 input, on tie values (tests.helpers.tie_rows):
+    rounding them to even instead of away from zero moves the outputs by several percent."""
+    torch = torch_cuda
+    m, k = 200, 1024
+    raw = synth.weights_np(t, m, k, seed=2100 + t)
+    x = tie_rows(k)[0]
+    w = eng.upload(raw, t, m, k)
+    y = torch.full((1, m), float("nan"), device="cuda")
+    eng.matvec_parts([w], [y], 1, x=torch.from_numpy(x).cuda())
+    torch.cuda.synchronize()
+    assert parity_err(y.cpu().numpy(), O.matmul(t, raw, m, k, x, 1, tiled=False)) <= PARITY_TOL
+    eng.free(w)
 
 
 # ---------------------------------------------------------------------------------------- products
@@ -636,3 +654,123 @@ def test_gemm_unaligned_output(eng, torch_cuda, t):
         assert parity_err(y.view(n, m).cpu().numpy(), want) <= PARITY_TOL
         assert torch.isnan(buf[:off]).all() and torch.isnan(buf[off + n * m:]).all()
     eng.free(w)
+
+
+# ---------------------------------------------------------------------------------------- the timed paths
+
+TIMED = {
+    # bench.py's batch-1 decode step (config 4): fused launches on an f32 input, quantized in-kernel
+    "llama8b-qkv": (F.Q4_K, [4096, 1024, 1024], 4096),
+    "llama8b-o": (F.Q4_K, [4096], 4096),
+    "llama8b-gate-up": (F.Q4_K, [14336, 14336], 4096),
+    "llama8b-down": (F.Q4_K, [4096], 14336),
+    "llama8b-lm-head": (F.Q6_K, [128256], 4096),
+    # config 2 (Qwen3-0.6B decode step)
+    "qwen-qkv": (F.Q4_K, [2048, 1024, 1024], 1024),
+    "qwen-o": (F.Q4_K, [1024], 2048),
+    "qwen-gate-up": (F.Q4_K, [3072, 3072], 1024),
+    "qwen-down": (F.Q4_K, [1024], 3072),
+    "qwen-lm-head": (F.Q6_K, [151936], 1024),
+    # config 1 and config 5's batch-1 products
+    "config1-q8_0": (F.Q8_0, [3072], 1024),
+    "config5-iq4_nl-up": (F.IQ4_NL, [14336], 4096),
+    "config5-q6_k-down": (F.Q6_K, [4096], 14336),
+}
+
+
+@pytest.mark.parametrize("n,prepared", [(1, False), (8, True)])
+@pytest.mark.parametrize("workload", list(TIMED))
+def test_timed_decode_paths(eng, torch_cuda, workload, n, prepared):
+    """Every product the bench times, at its full shape and through the same entry point and
+    kernel choice: hkhip_matvec_parts on the f32 input (batch 1; the kernel quantizes it) or on an
+    input prepared by hkhip_qact (batch 8, as the batch-8 step runs it), with the bench's fusion
+    of parts. Tall matrices are checked on a sample of rows (each output row depends only on its
+    weight row): the first and last, rows around 16/64-row edges and random ones."""
+    torch = torch_cuda
+    t, heights, k = TIMED[workload]
+    outl = 0.01 if workload.startswith("config5") else 0.0
+    x = synth.activations_np(n, k, seed=2200 + n, outliers=outl)
+    raws = [synth.weights_np(t, m, k, seed=2300 + i + m) for i, m in enumerate(heights)]
+    mats = [eng.upload(r, t, m, k) for r, m in zip(raws, heights)]
+    ys = [torch.full((n, m), float("nan"), device="cuda") for m in heights]
+    xd = torch.from_numpy(x).cuda()
+    if prepared:
+        xq = torch.empty(eng.act_bytes(n, k), dtype=torch.uint8, device="cuda")
+        eng.qact(xd, n, k, F.ACT_KIND[t], xq)
+        eng.matvec_parts(mats, ys, n, xq=xq)
+    else:
+        eng.matvec_parts(mats, ys, n, x=xd)
+    torch.cuda.synchronize()
+    for w in mats:
+        eng.free(w)
+    rng = np.random.default_rng(2400)
+    for r, m, y in zip(raws, heights, ys):
+        got = y.cpu().numpy()
+        assert np.isfinite(got).all()
+        if m > 4096:
+            rows = np.unique(np.concatenate([np.array([0, 1, 15, 16, 63, 64, 65, m // 2, m - 65, m - 64, m - 17,
+                                                       m - 16, m - 2, m - 1]), rng.integers(0, m, 64)]))
+        else:
+            rows = np.arange(m)
+        want = O.matmul(t, r[rows], len(rows), k, x, n, tiled=False, threads=16)
+        assert parity_err(got[:, rows], want) <= PARITY_TOL, workload
+
+
+def test_engine_from_another_thread(torch_cuda):
+    """An engine created and loaded on one thread, then driven from a worker thread, as hk's
+    server does (tests/test_gpu.zig:446-478 checkOtherThread): every entry point makes the
+    engine's device current, so upload, qact, the products and sync work there."""
+    import threading
+
+    from hk_amd import Engine
+
+    torch = torch_cuda
+    t, m, k = F.Q4_K, 300, 1024
+    raw = synth.weights_np(t, m, k, seed=2500)
+    raw2 = synth.weights_np(F.Q8_0, 64, k, seed=2501)
+    x = synth.activations_np(12, k, seed=2502)
+    e = Engine(0)  # its own stream: nothing here depends on torch's stream
+    w = e.upload(raw, t, m, k)
+    xd = torch.from_numpy(x).cuda()
+    ys = {n: torch.full((n, m), float("nan"), device="cuda") for n in (1, 12)}
+    y2 = torch.full((1, 64), float("nan"), device="cuda")
+    torch.cuda.synchronize()
+    out = {}
+
+    def job():
+        try:
+            w2 = e.upload(raw2, F.Q8_0, 64, k)
+            xq = torch.empty(e.act_bytes(12, k), dtype=torch.uint8, device="cuda")
+            e.qact(xd, 12, k, F.ACT_Q8K, xq)
+            e.mm(w, xq, ys[12], 12)
+            e.matvec_parts([w], [ys[1]], 1, x=xd[:1])
+            e.matvec_parts([w2], [y2], 1, x=xd[:1])
+            e.sync()
+            e.free(w2)
+            out["ok"] = True
+        except Exception as exc:  # reported by the main thread
+            out["err"] = exc
+
+    th = threading.Thread(target=job)
+    th.start()
+    th.join()
+    assert out.get("ok"), out.get("err")
+    for n, y in ys.items():
+        assert parity_err(y.cpu().numpy(), O.matmul(t, raw, m, k, x[:n], n)) <= PARITY_TOL
+    assert parity_err(y2.cpu().numpy(), O.matmul(F.Q8_0, raw2, 64, k, x[:1], 1)) <= PARITY_TOL
+    e.close()
+
+
+@pytest.mark.parametrize("t", [F.Q5_K, F.Q4_0, F.Q4_1, F.IQ4_XS])
+@pytest.mark.parametrize("n", [9, 12, 16])
+def test_mm_tall_break_even(eng, torch_cuda, t, n):
+    """hkhip_mm on matrices of at least 8192 rows switches these formats to the GEMM from 9 tokens:
+    the ragged 32-token tile at 9-16 tokens, with bias and accumulate."""
+    m, k = 9000, 4096
+    raw = synth.weights_np(t, m, k, seed=2600 + t)
+    x = synth.activations_np(n, k, seed=2601 + n)
+    bias = np.linspace(-1, 1, m).astype(np.float32)
+    y0 = synth.activations_np(n, m, seed=2602)
+    got = run(eng, torch_cuda, t, raw, m, k, x, path="mm", bias=bias, mode=1, y0=y0)
+    want = O.matmul(t, raw, m, k, x, n, bias=bias, threads=16) + y0
+    assert parity_err(got, want) <= PARITY_TOL

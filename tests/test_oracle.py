@@ -21,7 +21,7 @@ import pytest
 from hk_amd import formats as F
 from hk_amd import synth
 from oracle import oracle as O
-from tests.helpers import load_fixture
+from tests.helpers import load_fixture, tie_rows
 
 FMTS = [F.Q8_0, F.Q4_K, F.Q6_K, F.IQ4_NL, F.Q4_0, F.Q4_1, F.Q5_0, F.Q5_1, F.Q5_K, F.IQ4_XS]
 FIXTURES = F.NAMES
@@ -246,6 +246,20 @@ def test_quantize_q8k_invariants():
         clamped = q == 127
         assert np.all(err[~clamped] <= abs(blk["d"]) * 0.5 * (1 + 1e-5) + 1e-37)
     assert blocks[2]["d"] > 0 and blocks[3]["d"] < 0  # the tie rule: first index sets the sign
+
+
+def test_quantizers_round_ties_half_away():
+    """Tie values k + 0.5 at scale exactly 1 (tests.helpers.tie_rows): both quantizers must round
+    them away from zero, as Zig's @round does (vecdot.zig:141, 172); rint would fail here."""
+    x, q = tie_rows(512)
+    a8 = O.quantize_a8(x[0])
+    assert np.all(a8["d"] == 1.0)
+    assert np.array_equal(a8["qs"].astype(np.int64).ravel(), q[0])
+    assert np.array_equal(a8["s"], q[0].reshape(-1, 32).sum(axis=1))
+    qk = O.quantize_q8k(x[0])
+    assert np.all(qk["d"] == 1.0)
+    assert np.array_equal(qk["qs"].astype(np.int64).ravel(), q[0])
+    assert np.array_equal(qk["bsums"].astype(np.int64).ravel(), q[0].reshape(-1, 16).sum(axis=1))
 
 
 # ------------------------------------------------------------------------------------ dots
