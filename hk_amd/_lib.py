@@ -66,6 +66,7 @@ SIGNATURES = {
     "hkhip_matvec_parts": (_I, [_P, _MP, _U32, _P, _P, _U32, _P, _P, _I]),
     "hkhip_gemm": (_I, [_P, _MP, _P, _P, _U32, _P, _I]),
     "hkhip_mm": (_I, [_P, _MP, _P, _P, _U32, _P, _I]),
+    "hkhip_mm_noalloc": (_I, [_P, _MP, _P, _P, _U32, _P, _I]),
     "hkhip_gemm_host": (_I, [_U8, _P, _P, _P, _P, _U64, _U64, _U64]),
     "hkhip_gemv_q8_0": (_I, [_P, _P, _P, _P, _U64, _U64]),
     "hkhip_gemv_q4_0": (_I, [_P, _P, _P, _P, _U64, _U64]),

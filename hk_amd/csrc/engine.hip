@@ -25,6 +25,16 @@ struct hkhip_engine {
 
 static thread_local char g_err[512] = "";
 
+// Activation buffer of hkhip_mm_noalloc: a file-scope device array, so that entry point needs no
+// allocation. Every device holds its own copy until the process ends. Host code never passes the
+// array's name to a kernel or a copy (on the host it is only a stand-in for the symbol): it uses
+// the per-device address that hkhip_init looks up with hipGetSymbolAddress.
+static __device__ __align__(256) uint8_t scratch[HKHIP_NOALLOC_SCRATCH_BYTES];
+
+static constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void *g_scratch_ptr[kMaxDevices] = {};
+
 static int fail(int code, const char *fmt, ...) {
     va_list ap;
     va_start(ap, fmt);
@@ -71,6 +81,17 @@ int hkhip_init(int device, hkhip_engine **out) {
     HIP_TRY(hipGetDeviceProperties(&p, device), "hipGetDeviceProperties");
     if (strncmp(p.gcnArchName, "gfx950", 6) != 0)
         return fail(HKHIP_E_NO_DEVICE, "device %d is %s; the kernels are built for gfx950", device, p.gcnArchName);
+    if (device >= kMaxDevices) return fail(HKHIP_E_NO_DEVICE, "device %d: at most %d devices", device, kMaxDevices);
+    {
+        // Once per device, with that device current: the address of this device's copy of the
+        // no-allocation entry point's activation buffer.
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        if (!g_scratch_ptr[device]) {
+            void *ptr = nullptr;
+            HIP_TRY(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+            g_scratch_ptr[device] = ptr;
+        }
+    }
     hkhip_engine *e = new hkhip_engine();
     e->device = device;
     hipError_t err = hipStreamCreateWithFlags(&e->own, hipStreamNonBlocking);
@@ -352,6 +373,22 @@ int hkhip_mm(hkhip_engine *eng, const hkhip_mat *m, const void *xq_dev, float *y
     HIP_TRY(launch_mmvq(m->t, reinterpret_cast<const uint8_t *>(m->mem), m->rows, m->cols,
                         reinterpret_cast<const uint8_t *>(xq_dev), n, y_dev, bias_dev, mode, eng->cur), "mmvq launch");
     return HKHIP_OK;
+}
+
+int hkhip_mm_noalloc(hkhip_engine *eng, const hkhip_mat *m, const float *x_dev, float *y_dev, uint32_t n,
+                     const float *bias_dev, int mode) {
+    int rc = enter(eng);
+    if (rc || (rc = check_product(m, x_dev, y_dev, n, mode))) return rc;
+    if (n == 0) return HKHIP_OK;
+    const uint64_t need = act_layout(n, m->cols).total;
+    if (need > HKHIP_NOALLOC_SCRATCH_BYTES)
+        return fail(HKHIP_E_UNSUPPORTED_SHAPE,
+                    "hkhip_mm_noalloc: %u tokens x %u cols need %llu bytes of activation buffer, over its %llu",
+                    n, m->cols, (unsigned long long)need, (unsigned long long)HKHIP_NOALLOC_SCRATCH_BYTES);
+    void *xq = g_scratch_ptr[eng->device]; // set by hkhip_init for this engine's device
+    if (!xq) return fail(HKHIP_E_DEVICE_FAILED, "no activation buffer for device %d", eng->device);
+    if ((rc = hkhip_qact(eng, x_dev, n, m->cols, act_kind(m->t), xq))) return rc;
+    return hkhip_mm(eng, m, xq, y_dev, n, bias_dev, mode);
 }
 
 // ---- host-pointer products on a process-wide default engine ----

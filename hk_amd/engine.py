@@ -170,6 +170,11 @@ class Engine:
         (mm: cuda/engine.zig:581-611; matmul.zig:18,107)."""
         check(lib().hkhip_mm(self._h, ctypes.byref(m.raw), _ptr(xq), _ptr(y), n, _ptr(bias), mode))
 
+    def mm_noalloc(self, m: DevMat, x, y, n: int, bias=None, mode: int = STORE) -> None:
+        """mm on an f32 input x [n][cols], quantized into the library's fixed activation buffer:
+        allocates nothing (for callers that cannot). Calls on one device share that buffer."""
+        check(lib().hkhip_mm_noalloc(self._h, ctypes.byref(m.raw), _ptr(x), _ptr(y), n, _ptr(bias), mode))
+
 
 # -- host-pointer products (abi_ops.gemm / gemv, c_api hk_gemv_*) ---------------------------
 

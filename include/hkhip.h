@@ -152,6 +152,19 @@ int hkhip_mm(hkhip_engine *eng, const hkhip_mat *m, const void *xq_dev, float *y
 int hkhip_matvec_parts(hkhip_engine *eng, const hkhip_mat *mats, uint32_t nparts, const float *x_dev,
                        const void *xq_dev, uint32_t n, float *const *ys, const float *const *biases, int mode);
 
+/* ---- product without allocation (no counterpart in the reference) ----
+ * For callers that cannot allocate device memory: code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc. Same result as hkhip_qact(x_dev -> xq) followed by
+ * hkhip_mm(m, xq, ...), bit for bit, but the activation buffer is a fixed device array inside the
+ * library (HKHIP_NOALLOC_SCRATCH_BYTES per device, held until the process ends), so the call
+ * allocates nothing. Refuses (UNSUPPORTED_SHAPE) inputs whose buffer, hkhip_act_bytes(n, cols),
+ * exceeds that size: e.g. 512 tokens at cols 14336 (19.4 MiB) fit, 1024 tokens there do not.
+ * All calls on one device share the buffer: calls that overlap in time on one device (two
+ * streams, two threads) race, so serialise them. */
+#define HKHIP_NOALLOC_SCRATCH_BYTES (24ull << 20)
+int hkhip_mm_noalloc(hkhip_engine *eng, const hkhip_mat *m, const float *x_dev, float *y_dev, uint32_t n,
+                     const float *bias_dev, int mode);
+
 /* ---- host-pointer products (secondary boundary: src/c_api.zig:1380-1400, hk.h:451-453,
  * src/engine/abi_ops.zig:65-107) ----
  * y[t*m + r] = dot(W[r], x[t]) + bias[r] with W, x, bias, y in host memory, on the process's
