@@ -20,7 +20,11 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libhkhip.so")
 BUILD_DIR = os.path.join(HERE, "_build")
-SOURCES = ["engine.hip", "weights.hip", "qact.hip", "mmvq.hip", "mm.hip", "mm2.hip", "mmsk.hip", "mmx.hip"]
+# mmvq_<format>.hip instantiate the decode kernels per format (the largest part of the build), so
+# they compile in parallel; build() always recompiles everything.
+MMVQ_FORMATS = ["q4_k", "q6_k", "q5_k", "iq4_xs", "q8_0", "iq4_nl", "q4_0", "q4_1", "q5_0", "q5_1"]
+SOURCES = ["engine.hip", "weights.hip", "qact.hip", "mmvq.hip", "mm.hip", "mm2.hip", "mmsk.hip", "mmx.hip"] + \
+    [f"mmvq_{f}.hip" for f in MMVQ_FORMATS]
 ARCH = "gfx950"
 
 
@@ -55,7 +59,7 @@ def _compile(src: str) -> str:
 def build(jobs: int | None = None) -> str:
     """Compile every source and link libhkhip.so. Always rebuilds."""
     os.makedirs(BUILD_DIR, exist_ok=True)
-    jobs = jobs or min(len(SOURCES), os.cpu_count() or 4)
+    jobs = jobs or min(len(SOURCES), os.cpu_count() or 4, 16)
     with cf.ThreadPoolExecutor(jobs) as ex:
         objs = list(ex.map(_compile, SOURCES))
     tmp = OUT + ".tmp"
