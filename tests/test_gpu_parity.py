@@ -317,8 +317,13 @@ def test_baseline_prefill_shapes(eng, torch_cuda, t, m, k):
                          [(t, 1000, 4096, 40, 1) for t in (F.Q4_1, F.Q5_0, F.Q5_1, F.IQ4_XS)] +
                          [(t, 9000, 4352, 20, 0) for t in (F.Q4_1, F.Q5_0, F.Q5_1, F.IQ4_XS)])
 def test_gemm_configs_other_formats(eng, torch_cuda, t, m, k, n, mode):
-    """The Q6_K / Q8_0 / IQ4_NL GEMM's configurations: IQ4_NL split over two K slices (5
-    super-blocks) and its 256-row tile; ragged rows and tokens, bias, accumulate."""
+    """The configurations of the mmx / mm2 GEMM tiles for the formats other than Q4_K: IQ4_NL over
+    two K slices (5 super-blocks) and its 256-row tile; Q6_K and Q8_0 tiles; Q4_0..Q5_1 and IQ4_XS
+    on the 256-row tile (9000 rows) and the 128-row two-slice tile (4000 rows, with an uneven
+    17-block split at K 1280); the 64-row tiles over K slices (two for Q5_0 / Q5_1, four for Q4_1 /
+    IQ4_XS) at cols >= 4096 with few row blocks or few tokens; Q5_K on the Q4_K register tile
+    (12288 / 12300 rows) and on mmx / the 128-row ring tile otherwise; ragged rows and tokens,
+    bias, accumulate."""
     raw = synth.weights_np(t, m, k, seed=1400 + m)
     x = synth.activations_np(n, k, seed=1401, outliers=0.01)
     bias = np.linspace(-1, 1, m).astype(np.float32) if mode else None
