@@ -25,8 +25,10 @@ Also reported:
                 Qwen3-0.6B-shaped decoder, tokens/s)
   measured_peaks  this GPU's dense int8 MFMA rate and HBM read rate from probe kernels
                 (hk_amd/csrc/peak.hip), quoted beside the published peaks the fractions use
-  cpu_baseline  the oracle's restatement of hk's CPU kernels on the host cores, on a bounded
-                sample (the 14336x4096 Q4_K matvec, repeated for ~10 s)
+  cpu_baseline  hk's CPU decode kernel restated with its SIMD paths (oracle/hk_cpu_simd.c, best
+                instruction set of the host chosen at run time) on the host's physical cores, on a
+                bounded sample (the 14336x4096 Q4_K matvec, repeated for ~10 s), plus one thread
+  wall_s        wall-clock seconds of each phase of this run
 """
 from __future__ import annotations
 
@@ -62,6 +64,15 @@ def main():
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for {args.gpus}).",
               file=sys.stderr)
         sys.exit(2)
+
+    T0 = time.perf_counter()
+    phases = {}
+    mark = [T0]
+
+    def phase(name):
+        now = time.perf_counter()
+        phases[name] = round(now - mark[0], 2)
+        mark[0] = now
 
     import torch
 
@@ -99,6 +110,7 @@ def main():
                        for i, (name, r, c) in enumerate(shapes)})
     lm_head = upload_synth(F.Q6_K, V, H, synth.seed_for(4, 999))
     torch.cuda.synchronize()
+    phase("import_and_weights")
 
     # ---- activations (resident): one input per distinct product input ----
     x_h = torch.randn(1, H, device=dev)
@@ -148,6 +160,7 @@ def main():
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
         ms = e0.elapsed_time(e1) / args.steps
+        phase("decode_step")
         result["decode"] = dict(ms_per_step=ms, wall_ms_per_step=1e3 * wall / args.steps,
                                 gbs=step_bytes / (ms * 1e-3) / 1e9, tokens_per_s=1e3 / ms,
                                 weight_bytes=weight_bytes, step_bytes=step_bytes)
@@ -183,6 +196,7 @@ def main():
         torch.cuda.synchronize()
         us = 1e3 * e0.elapsed_time(e1) / (reps * len(pairs))
         kbytes = 2 * pairs[0][0].file_bytes + 4 * H + 2 * 4 * FF
+        phase("roofline_kernel")
         result["kernel"] = dict(name="mmvr_kernel<Q4_K, NT=1, C=1> (gate+up fused, f32 input quantized in-kernel)",
                                 shape="2x14336x4096",
                                 launches=reps * len(pairs), avg_us=us, bytes_per_launch=kbytes,
@@ -210,9 +224,18 @@ def main():
             tops = 2.0 * m_ * n * k_ / (us * 1e-6) / 1e12
             pre.append(dict(shape=f"{m_}x{k_}x{n}", fmt=FMT_NAME[t], workload=name, avg_us=round(us, 2),
                             tops=round(tops, 2), frac_int8_peak=round(tops / INT8_PEAK_TOPS, 4)))
+            if (t, m_, k_) == (F.Q4_K, FF, H):
+                # The same GEMM with its activation quantization (qact of the f32 input) in the
+                # timed region: prefill of one layer input as the engine runs it.
+                us_q = time_graph(torch, eng, stream,
+                                  lambda: (eng.qact(x, n, k_, F.ACT_Q8K, xq), eng.gemm(w, xq, yy, n)), 5)
+                tq = 2.0 * m_ * n * k_ / (us_q * 1e-6) / 1e12
+                pre.append(dict(shape=f"{m_}x{k_}x{n}", fmt=FMT_NAME[t], workload=name + " (qact + gemm)",
+                                avg_us=round(us_q, 2), tops=round(tq, 2), frac_int8_peak=round(tq / INT8_PEAK_TOPS, 4)))
             if reuse is None:
                 eng.free(w)
         result["prefill"] = pre
+        phase("prefill")
 
     # ---- BASELINE config 4 at batch 8 (the decode step for 8 tokens) and config 5's batch-1
     # matvecs (IQ4_NL gate/up, Q6_K down), each rotating over 12 distinct matrices so that the
@@ -349,16 +372,19 @@ def main():
                 eng.free(m)
         eng.free(qhead)
         result["extra"] = extra
+        phase("extra")
 
     # ---- this GPU's measured peaks, quoted beside the published ones (the fractions use those) ----
     peaks = None
     if args.only == "all":
         peaks = measured_peaks()
+        phase("measured_peaks")
 
     # ---- CPU baseline: the oracle on the host cores, bounded sample ----
     cpu = None
     if not args.no_cpu and args.only == "all":
         cpu = cpu_baseline(args.cpu_seconds)
+        phase("cpu_baseline")
 
     dec = result.get("decode", {})
     ker = result.get("kernel", {})
@@ -390,6 +416,7 @@ def main():
         "extra": result.get("extra"),
         "measured_peaks": peaks,
         "cpu_baseline": cpu,
+        "wall_s": dict(phases, total=round(time.perf_counter() - T0, 2)),
     }
     print(json.dumps(line), flush=True)
     eng.close()
@@ -455,43 +482,70 @@ def time_graph(torch, eng, stream, fn, reps: int, per_graph: int = 10) -> float:
     return 1e3 * e0.elapsed_time(e1) / (reps * per_graph)
 
 
+def physical_cores() -> int:
+    """Physical cores among the CPUs this process may run on (hyperthread siblings count once)."""
+    cpus = sorted(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else list(range(os.cpu_count() or 1))
+    seen = set()
+    for c in cpus:
+        base = f"/sys/devices/system/cpu/cpu{c}/topology/"
+        try:
+            with open(base + "physical_package_id") as f1, open(base + "core_id") as f2:
+                seen.add((f1.read().strip(), f2.read().strip()))
+        except OSError:
+            seen.add(("cpu", str(c)))
+    return max(1, len(seen))
+
+
+def cpu_model() -> str:
+    fields = {}
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if ":" in line:
+                    key, val = (p.strip() for p in line.split(":", 1))
+                    fields.setdefault(key, val)
+                if not line.strip() and fields:
+                    break
+    except OSError:
+        return "unknown"
+    name = fields.get("model name", "unknown")
+    return f"{name} (vendor {fields.get('vendor_id', '?')}, family {fields.get('cpu family', '?')}, " \
+           f"model {fields.get('model', '?')}, stepping {fields.get('stepping', '?')})"
+
+
 def cpu_baseline(seconds: float):
-    """hk's CPU kernel arithmetic (the oracle's C restatement) on the host cores: the Q4_K
-    14336x4096 batch-1 matvec, repeated for about `seconds`. Reported in GB/s of weights."""
+    """hk's CPU decode kernel (its SIMD restatement, oracle/hk_cpu_simd.c: the dpu primitive of
+    isa.zig on the best instruction set this host has, 16 KiB row chunks as matmul.zig hands them
+    out) on the host's physical cores: the Q4_K 14336x4096 batch-1 matvec, repeated for about
+    `seconds`, plus a single-thread figure. Reported in GB/s of weights + activations."""
     import numpy as np
 
     from hk_amd import formats as F, synth
     from oracle import oracle as O
 
-    cores = min(os.cpu_count() or 1, 16)
+    cores = physical_cores()
+    level = O.simd_level()
     m, k = LLAMA8B["ffn"], LLAMA8B["hidden"]
     raw = synth.weights_np(F.Q4_K, m, k, synth.seed_for(4, 0))
-    x = synth.activations_np(1, k, 1)
-    O.matmul(F.Q4_K, raw, m, k, x, 1, threads=cores)
+    x = synth.activations_np(1, k, 1)[0]
+    O.matvec_q4k_simd(raw, m, k, x, threads=cores, level=level)
     reps, t0 = 0, time.perf_counter()
     while time.perf_counter() - t0 < seconds:
-        O.matmul(F.Q4_K, raw, m, k, x, 1, threads=cores)
+        O.matvec_q4k_simd(raw, m, k, x, threads=cores, level=level)
         reps += 1
     dt = (time.perf_counter() - t0) / reps
     nbytes = raw.nbytes + 4 * k + 4 * m
     # The same product on one thread, for a figure comparable to hk-kernels' single-thread runs.
     reps1, t1 = 0, time.perf_counter()
     while time.perf_counter() - t1 < max(1.0, seconds / 4):
-        O.matmul(F.Q4_K, raw, m, k, x, 1, threads=1)
+        O.matvec_q4k_simd(raw, m, k, x, threads=1, level=level)
         reps1 += 1
     dt1 = (time.perf_counter() - t1) / reps1
-    model = "unknown"
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
     return {"value": round(nbytes / dt / 1e9, 2), "unit": "GB/s", "cores": cores, "kind": "port",
-            "sample": f"Q4_K 14336x4096 matvec, batch 1, {reps} reps in {seconds:.0f} s (OpenMP, scalar C)",
-            "single_thread_value": round(nbytes / dt1 / 1e9, 2), "cpu_model": model}
+            "sample": f"Q4_K 14336x4096 matvec, batch 1, {reps} reps in {seconds:.0f} s; hk's decode kernel "
+                      f"({O.simd_level_name(level)} dot primitive, 16 KiB row chunks, OpenMP over {cores} physical cores)",
+            "isa": O.simd_level_name(level),
+            "single_thread_value": round(nbytes / dt1 / 1e9, 2), "cpu_model": cpu_model()}
 
 
 if __name__ == "__main__":

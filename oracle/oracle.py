@@ -51,6 +51,11 @@ def lib() -> ctypes.CDLL:
         L.hko_matmul_path.argtypes = [I, P, S, S, P, S, P, P, I, I]
         L.hko_f16_to_f32.argtypes = [ctypes.c_uint16]
         L.hko_f16_to_f32.restype = F
+        L.hkc_pick_level.argtypes = [ctypes.c_char_p]
+        L.hkc_pick_level.restype = I
+        L.hkc_level_name.argtypes = [I]
+        L.hkc_level_name.restype = ctypes.c_char_p
+        L.hkc_matvec_q4k.argtypes = [I, P, S, S, P, P, I]
         _lib = L
     return _lib
 
@@ -133,3 +138,30 @@ def scale_min_k4(j: int, packed: np.ndarray):
     mn = ctypes.c_uint8()
     lib().hko_scale_min_k4(j, _p(p), ctypes.byref(sc), ctypes.byref(mn))
     return sc.value, mn.value
+
+
+# -- hk's SIMD decode kernel (hk_cpu_simd.c): the benchmark's CPU baseline --------------------
+
+SIMD_LEVELS = ("avx512-vnni", "avx2-vnni", "avx2", "generic")
+
+
+def simd_level(name: str | None = None) -> int:
+    """The instruction-set level hk would run here (kernels.zig:55-85), or the named one; -1 if
+    the processor lacks it."""
+    return lib().hkc_pick_level(None if name is None else name.encode())
+
+
+def simd_level_name(level: int) -> str:
+    return lib().hkc_level_name(level).decode()
+
+
+def matvec_q4k_simd(w: np.ndarray, m: int, k: int, x: np.ndarray, threads: int = 1,
+                    level: int | None = None) -> np.ndarray:
+    """y = W x for a Q4_K matrix and one token through hk's SIMD kernel at `level`."""
+    lv = simd_level() if level is None else level
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    y = np.empty(m, np.float32)
+    if lib().hkc_matvec_q4k(lv, _p(w), m, k, _p(x), _p(y), threads) != 0:
+        raise ValueError(f"hkc_matvec_q4k failed (level {lv})")
+    return y

@@ -333,3 +333,24 @@ def test_matmul_dispatch_and_threads():
         y4 = O.matmul(t, raw, m, k, x, n, threads=4)
         assert np.array_equal(y1, y4)
         assert np.array_equal(y1, O.matmul(t, raw, m, k, x, n, tiled=(n >= 8)))
+
+
+# ------------------------------------------------------------------------------------ CPU baseline
+
+def test_simd_baseline_levels_match_oracle():
+    """hk's SIMD decode kernel (the bench's CPU baseline) at every instruction-set level this
+    processor runs gives the oracle's Q4_K matvec bit for bit: the integer dot primitive has one
+    exact definition (isa.zig:57-88) and the lanes are summed in the same order."""
+    m, k = 77, 2048
+    raw = synth.weights_np(F.Q4_K, m, k, seed=41)
+    x = synth.activations_np(1, k, seed=42, outliers=0.01)
+    want = O.matmul(F.Q4_K, raw, m, k, x, 1, tiled=False)[0]
+    ran = []
+    for name in O.SIMD_LEVELS:
+        lv = O.simd_level(name)
+        if lv < 0:
+            continue
+        got = O.matvec_q4k_simd(raw, m, k, x, threads=3, level=lv)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), name
+        ran.append(name)
+    assert "generic" in ran and O.simd_level_name(O.simd_level()) == ran[0]
