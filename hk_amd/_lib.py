@@ -35,6 +35,27 @@ class HkhipMat(ctypes.Structure):
     ]
 
 
+class NetConfig(ctypes.Structure):
+    """hkhip_net_config."""
+    _fields_ = [(n, ctypes.c_uint32) for n in ("dim", "n_layers", "n_heads", "n_kv_heads", "head_dim", "ffn_dim",
+                                                  "vocab", "rope_dim", "rope_neox", "max_ctx")] + \
+               [("rms_eps", ctypes.c_float), ("rope_base", ctypes.c_float)]
+
+
+class NetTensor(ctypes.Structure):
+    """hkhip_net_tensor: hk file-layout bytes in host memory (data NULL: absent)."""
+    _fields_ = [("data", ctypes.c_void_p), ("bytes", ctypes.c_uint64), ("t", ctypes.c_uint8)]
+
+
+NET_LAYER_FIELDS = ("attn_norm", "wq", "wk", "wv", "bq", "bk", "bv", "q_norm", "k_norm", "wo", "ffn_norm",
+                    "w_gate", "w_up", "w_down")
+
+
+class NetLayer(ctypes.Structure):
+    """hkhip_net_layer."""
+    _fields_ = [(n, NetTensor) for n in NET_LAYER_FIELDS]
+
+
 _P, _U8, _U32, _U64, _I = ctypes.c_void_p, ctypes.c_uint8, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int
 _FP = ctypes.POINTER(ctypes.c_float)
 _MP = ctypes.POINTER(HkhipMat)
@@ -64,10 +85,18 @@ SIGNATURES = {
     "hkhip_act_export": (_I, [_P, _P, _U32, _U32, _I, _P]),
     "hkhip_matvec": (_I, [_P, _MP, _P, _P, _U32, _P, _I]),
     "hkhip_matvec_parts": (_I, [_P, _MP, _U32, _P, _P, _U32, _P, _P, _I]),
+    "hkhip_matvec_parts_rmsnorm": (_I, [_P, _MP, _U32, _P, _P, ctypes.c_float, _U32, _P, _P, _I]),
     "hkhip_gemm": (_I, [_P, _MP, _P, _P, _U32, _P, _I]),
     "hkhip_mm": (_I, [_P, _MP, _P, _P, _U32, _P, _I]),
     "hkhip_mm_noalloc": (_I, [_P, _MP, _P, _P, _U32, _P, _I]),
     "hkhip_gemm_host": (_I, [_U8, _P, _P, _P, _P, _U64, _U64, _U64]),
+    "hkhip_net_create": (_I, [_P, ctypes.POINTER(NetConfig), ctypes.POINTER(_P)]),
+    "hkhip_net_destroy": (None, [_P]),
+    "hkhip_net_load_layer": (_I, [_P, _U32, ctypes.POINTER(NetLayer)]),
+    "hkhip_net_load_io": (_I, [_P, NetTensor, NetTensor, NetTensor]),
+    "hkhip_net_forward": (_I, [_P, _P, _U32, _U32]),
+    "hkhip_net_logits": (_I, [_P, _P]),
+    "hkhip_net_logits_dev": (_P, [_P]),
     "hkhip_gemv_q8_0": (_I, [_P, _P, _P, _P, _U64, _U64]),
     "hkhip_gemv_q4_0": (_I, [_P, _P, _P, _P, _U64, _U64]),
     "hkhip_gemv_q4_k": (_I, [_P, _P, _P, _P, _U64, _U64]),

@@ -23,7 +23,7 @@ BUILD_DIR = os.path.join(HERE, "_build")
 # mmvq_<format>.hip instantiate the decode kernels per format (the largest part of the build), so
 # they compile in parallel; build() always recompiles everything.
 MMVQ_FORMATS = ["q4_k", "q6_k", "q5_k", "iq4_xs", "q8_0", "iq4_nl", "q4_0", "q4_1", "q5_0", "q5_1"]
-SOURCES = ["engine.hip", "weights.hip", "qact.hip", "mmvq.hip", "mm.hip", "mm2.hip", "mmsk.hip", "mmx.hip"] + \
+SOURCES = ["engine.hip", "weights.hip", "qact.hip", "mmvq.hip", "mm.hip", "mm2.hip", "mmsk.hip", "mmx.hip", "net.hip"] + \
     [f"mmvq_{f}.hip" for f in MMVQ_FORMATS]
 ARCH = "gfx950"
 

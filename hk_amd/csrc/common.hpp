@@ -7,7 +7,18 @@
 
 #include "../../include/hkhip.h"
 
+// One engine: a device and the stream its work goes to (own: created at init; cur: the one in use).
+struct hkhip_engine {
+    int device;
+    hipStream_t own;
+    hipStream_t cur;
+    char name[128];
+};
+
 namespace hkhip {
+
+// Sets the thread's hkhip_last_error() message and returns code.
+int set_error(int code, const char *fmt, ...);
 
 constexpr uint32_t QK_K = 256;
 
@@ -233,6 +244,9 @@ __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
 hipError_t launch_repack(int t, const uint8_t *src, uint8_t *dst, uint32_t rows, uint32_t cols, hipStream_t s);
 hipError_t launch_dequant(int t, const uint8_t *w, uint32_t rows, uint32_t cols, uint32_t row0, uint32_t nrows,
                           float *out, hipStream_t s);
+// Rows ids[0..n) (device array; each below rows) decoded to out [n][cols] (embedding lookup).
+hipError_t launch_dequant_gather(int t, const uint8_t *w, uint32_t rows, uint32_t cols, const uint32_t *ids, uint32_t n,
+                                 float *out, hipStream_t s);
 hipError_t launch_qact(const float *x, uint32_t n, uint32_t k, int kind, uint8_t *xq, hipStream_t s);
 hipError_t launch_act_pack(const uint8_t *xq, uint32_t n, uint32_t k, int kind, uint8_t *out, hipStream_t s);
 // One matrix of a fused decode launch (all parts share cols and the input).
@@ -244,6 +258,12 @@ struct MvPartDesc {
 };
 hipError_t launch_mmvq_parts(int t, const MvPartDesc *parts, int nparts, uint32_t K, const float *x,
                              const uint8_t *xq, uint32_t n, int mode, hipStream_t s);
+// The same with the f32 input RMS-normalized per token first (norm weights [cols], eps), fused into
+// the kernel's staging; hipErrorNotSupported when the chosen kernel cannot fuse it (the caller then
+// normalizes separately).
+hipError_t launch_mmvq_parts_norm(int t, const MvPartDesc *parts, int nparts, uint32_t K, const float *x,
+                                  const uint8_t *xq, uint32_t n, int mode, const float *norm, float eps,
+                                  hipStream_t s);
 hipError_t launch_mmvq(int t, const uint8_t *w, uint32_t rows, uint32_t cols, const uint8_t *xq, uint32_t n,
                        float *y, const float *bias, int mode, hipStream_t s);
 bool mm2_supports(int t, uint32_t rows, uint32_t cols, uint32_t n);

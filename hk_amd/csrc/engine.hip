@@ -16,13 +16,6 @@
 
 using namespace hkhip;
 
-struct hkhip_engine {
-    int device;
-    hipStream_t own;
-    hipStream_t cur;
-    char name[128];
-};
-
 static thread_local char g_err[512] = "";
 
 // Activation buffer of hkhip_mm_noalloc: a file-scope device array, so that entry point needs no
@@ -36,6 +29,14 @@ static std::mutex g_scratch_mu;
 static void *g_scratch_ptr[kMaxDevices] = {};
 
 static int fail(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hkhip::set_error(int code, const char *fmt, ...) {
     va_list ap;
     va_start(ap, fmt);
     vsnprintf(g_err, sizeof g_err, fmt, ap);
@@ -328,6 +329,33 @@ int hkhip_matvec_parts(hkhip_engine *eng, const hkhip_mat *mats, uint32_t nparts
     if (n == 0) return HKHIP_OK;
     HIP_TRY(launch_mmvq_parts(mats[0].t, parts, int(nparts), mats[0].cols, x_dev,
                               reinterpret_cast<const uint8_t *>(xq_dev), n, mode, eng->cur), "mmvq launch");
+    return HKHIP_OK;
+}
+
+int hkhip_matvec_parts_rmsnorm(hkhip_engine *eng, const hkhip_mat *mats, uint32_t nparts, const float *x_dev,
+                               const float *norm_dev, float eps, uint32_t n, float *const *ys,
+                               const float *const *biases, int mode) {
+    int rc = enter(eng);
+    if (rc) return rc;
+    if (!mats || !ys || nparts < 1 || nparts > 4) return fail(HKHIP_E_BAD_ARGUMENT, "need 1..4 parts, got %u", nparts);
+    if (!x_dev || !norm_dev) return fail(HKHIP_E_BAD_ARGUMENT, "null input or norm weights");
+    MvPartDesc parts[4];
+    for (uint32_t i = 0; i < nparts; i++) {
+        if ((rc = check_product(&mats[i], x_dev, ys[i], n, mode))) return rc;
+        if (mode == HKHIP_SILU_MUL && biases && biases[i])
+            return fail(HKHIP_E_BAD_ARGUMENT, "silu(gate)*up takes no bias");
+        if (mats[i].t != mats[0].t || mats[i].cols != mats[0].cols)
+            return fail(HKHIP_E_BAD_ARGUMENT, "fused parts must share type and cols");
+        parts[i] = MvPartDesc{reinterpret_cast<const uint8_t *>(mats[i].mem), ys[i], biases ? biases[i] : nullptr,
+                              mats[i].rows};
+    }
+    if (n > 8) return fail(HKHIP_E_UNSUPPORTED_SHAPE, "the fused norm takes at most 8 tokens, got %u", n);
+    if (n == 0) return HKHIP_OK;
+    const hipError_t e = launch_mmvq_parts_norm(mats[0].t, parts, int(nparts), mats[0].cols, x_dev, nullptr, n, mode,
+                                                norm_dev, eps, eng->cur);
+    if (e == hipErrorNotSupported)
+        return fail(HKHIP_E_UNSUPPORTED_SHAPE, "no fused-norm kernel for %u tokens of %u cols", n, mats[0].cols);
+    HIP_TRY(e, "mmvq launch");
     return HKHIP_OK;
 }
 

@@ -126,7 +126,7 @@ static MvAct mv_act_at(const MvAct &a, bool kq, uint32_t K, uint32_t t0) {
 
 // One launch (register kernel) or a few (LDS kernel) for at most 8 tokens.
 static hipError_t launch_mv_chunk(int t, const MvPartDesc *parts, int nparts, uint32_t K, const MvAct &act,
-                                  uint32_t n, int mode, hipStream_t s) {
+                                  uint32_t n, int mode, const float *norm, float eps, hipStream_t s) {
     const float *x = act.x;
     if (n < 1 || n > 8 || nparts < 1 || nparts > MV_PARTS) return hipErrorInvalidValue;
     const bool kq = act_kind(t) == HKHIP_ACT_Q8K;
@@ -163,13 +163,19 @@ static hipError_t launch_mv_chunk(int t, const MvPartDesc *parts, int nparts, ui
                 k = kernels_for(t, lg, 8);
             }
         }
+        // A fused RMS norm needs LDS for one partial sum per 16 inputs after the staging area.
+        const uint32_t nflat = (nt == 1 ? 1u : n) * K;
+        const uint32_t norm_bytes = norm ? nflat / 4 : 0;
+        if (norm && !x) return hipErrorNotSupported;
         if (k && x) {
             // An f32 input is staged whole in LDS; when it does not fit, the LDS kernel splits the
             // tokens over launches.
             uint32_t need = mvr_lds_bytes(int(n), K, kq);
             if (ks > 1) need = ((need + 15) & ~15u) + uint32_t(mvr_nw(t, nt, c)) * 64 * nt * 4;
+            if (norm) need = ((need + 15) & ~15u) + norm_bytes;
             if (need > MV_LDS_MAX) k = nullptr;
         }
+        if (!k && norm) return hipErrorNotSupported;
         if (k) {
             MvArgs a{};
             uint32_t rows = 0;
@@ -193,9 +199,12 @@ static hipError_t launch_mv_chunk(int t, const MvPartDesc *parts, int nparts, ui
             a.gqs = act.qs;
             a.gd = act.d;
             a.gbs = act.bs;
+            a.norm = norm;
+            a.eps = eps;
             if (rows == 0) return hipSuccess;
             if (spw) {
-                const uint32_t rs = 64u >> lg, lds = x ? mvr_lds_bytes(1, K, kq) : 0;
+                const uint32_t rs = 64u >> lg;
+                const uint32_t lds = x ? (norm ? mvr_norm_offset(1, K, kq, 0) + norm_bytes : mvr_lds_bytes(1, K, kq)) : 0;
                 if (lds > MV_LDS_MAX) return hipErrorInvalidValue;
                 const uint32_t waves = (rows + rs * spw - 1) / (rs * spw);
                 hipLaunchKernelGGL(k, dim3((waves + snw - 1) / snw), dim3(snw * 64), lds, s, a);
@@ -205,6 +214,7 @@ static hipError_t launch_mv_chunk(int t, const MvPartDesc *parts, int nparts, ui
             const int nw = mvr_nw(t, nt, c), nrg = nw / ks;
             uint32_t lds = x ? mvr_lds_bytes(int(n), K, kq) : 0;
             if (ks > 1) lds = ((lds + 15) & ~15u) + uint32_t(nw) * 64 * nt * 4; // partials
+            if (norm) lds = mvr_norm_offset(nt == 1 ? 1u : n, K, kq, ks > 1 ? uint32_t(nw) * 64 * nt * 4 : 0) + norm_bytes;
             if (lds > MV_LDS_MAX) return hipErrorInvalidValue;
             const uint32_t cap = uint32_t(cu_count() * resident_per_cu(k, nw * 64, lds));
             const uint32_t want = (rows + nrg * R - 1) / (nrg * R);
@@ -222,6 +232,7 @@ static hipError_t launch_mv_chunk(int t, const MvPartDesc *parts, int nparts, ui
             return hipGetLastError();
         }
     }
+    if (norm) return hipErrorNotSupported;
     // Tokens per launch: as many as the LDS holds (all 8 at every BASELINE shape).
     int per = int(n);
     while (per > 1 && mv_lds_bytes(per, K, kq) > MV_LDS_MAX) per--;
@@ -280,7 +291,14 @@ static hipError_t launch_mv_chunk(int t, const MvPartDesc *parts, int nparts, ui
 
 hipError_t launch_mmvq_parts(int t, const MvPartDesc *parts, int nparts, uint32_t K, const float *x,
                              const uint8_t *xq, uint32_t n, int mode, hipStream_t s) {
+    return launch_mmvq_parts_norm(t, parts, nparts, K, x, xq, n, mode, nullptr, 0.0f, s);
+}
+
+hipError_t launch_mmvq_parts_norm(int t, const MvPartDesc *parts, int nparts, uint32_t K, const float *x,
+                                  const uint8_t *xq, uint32_t n, int mode, const float *norm, float eps,
+                                  hipStream_t s) {
     if (n < 1 || nparts < 1 || nparts > MV_PARTS) return hipErrorInvalidValue;
+    if (norm && !x) return hipErrorNotSupported;
     const bool kq = act_kind(t) == HKHIP_ACT_Q8K;
     // Q4_K and Q6_K from 4 tokens with a prepared input: the small-batch MFMA kernel (it needs the
     // quantizer's token-interleaved planes, so not for an f32 input).
@@ -306,7 +324,7 @@ hipError_t launch_mmvq_parts(int t, const MvPartDesc *parts, int nparts, uint32_
             pc[i] = parts[i];
             pc[i].y = parts[i].y + uint64_t(t0) * (mode == HKHIP_SILU_MUL ? parts[i].rows / 2 : parts[i].rows);
         }
-        const hipError_t e = launch_mv_chunk(t, pc, nparts, K, t0 ? mv_act_at(act, kq, K, t0) : act, nc, mode, s);
+        const hipError_t e = launch_mv_chunk(t, pc, nparts, K, t0 ? mv_act_at(act, kq, K, t0) : act, nc, mode, norm, eps, s);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;

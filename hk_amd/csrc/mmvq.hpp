@@ -50,7 +50,16 @@ struct MvArgs {
     int mode;
     int lpr_log2;
     uint32_t ntok; // tokens actually present (register kernel; at most its NT)
+    // Register kernel on an f32 input: when set, the input is first RMS-normalized per token,
+    // x * (1 / sqrt(mean(x^2) + eps)) * norm (ops.zig:10-29 rmsNorm), then quantized.
+    const float *norm;
+    float eps;
 };
+
+// Chunks of 1024 inputs a wave of the register kernel stages in one pass (its prefetch depth).
+__host__ __device__ constexpr int mvr_pb(bool kq, int nt, int c, int nw) {
+    return (kq ? 4 : 2) * nt * c / nw < 1 ? 1 : (kq ? 4 : 2) * nt * c / nw > 4 ? 4 : (kq ? 4 : 2) * nt * c / nw;
+}
 
 __device__ __forceinline__ uint4 ldw(const void *p) { return *reinterpret_cast<const uint4 *>(p); }
 
@@ -731,6 +740,10 @@ __device__ __forceinline__ typename F::AU load_unit(const int8_t *gqs, const int
 __host__ __device__ inline uint32_t mvr_lds_bytes(int nt, uint32_t K, bool kq) {
     return nt * K + (kq ? nt * K / 8 + nt * (K / 256) * 4 : nt * (K / 32) * 4);
 }
+// The fused norm's per-lane sums follow the staging area and the K-slice partials (`extra`).
+__host__ __device__ inline uint32_t mvr_norm_offset(uint32_t nt, uint32_t K, bool kq, uint32_t extra) {
+    return ((mvr_lds_bytes(int(nt), K, kq) + 15) & ~15u) + extra;
+}
 
 // Quantizes 1024 consecutive inputs per wave (lane l holds values 16l..16l+15 of the chunk) with
 // the qact arithmetic and writes them to the LDS staging area in the engine's activation layout.
@@ -878,8 +891,7 @@ __global__ __launch_bounds__(NW * 64) void mmvr_kernel(MvArgs a) {
     const uint32_t nflat = ntok * K;
     // Chunks of 1024 inputs per wave: at most NT*K/1024/NW = (4 or 2)*NT*C/NW. Up to 4 are
     // loaded up front (clamped, always issued).
-    constexpr int CPW = (F::kq ? 4 : 2) * NT * C / NW;
-    constexpr int PB = CPW < 1 ? 1 : CPW > 4 ? 4 : CPW;
+    constexpr int PB = mvr_pb(F::kq, NT, C, NW);
     const uint32_t nchunk = (nflat + 1023) / 1024;
     float4 xv[PB][4];
     AU au[NT][C];
@@ -909,6 +921,63 @@ __global__ __launch_bounds__(NW * 64) void mmvr_kernel(MvArgs a) {
         int8_t *sqs = reinterpret_cast<int8_t *>(smem);
         int16_t *sbs = reinterpret_cast<int16_t *>(smem + nflat);
         float *sd = reinterpret_cast<float *>(smem + nflat + (F::kq ? nflat / 8 : 0));
+        // Fused RMS norm: per-lane sums of squares of 16 inputs to LDS (the first chunks from the
+        // registers, any further ones loaded once more), then every wave adds a token's sums in
+        // one fixed order, so all workgroups get the same factor.
+        float invt[NT];
+        auto norm_chunk = [&](float4 *v, uint32_t e) {
+            float inv = invt[0];
+#pragma unroll
+            for (int t = 1; t < NT; t++)
+                if (e / K == uint32_t(t)) inv = invt[t];
+            const float4 *wv = reinterpret_cast<const float4 *>(a.norm + (e < nflat ? e % K : 0));
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 w4 = wv[i];
+                v[i].x = (v[i].x * inv) * w4.x;
+                v[i].y = (v[i].y * inv) * w4.y;
+                v[i].z = (v[i].z * inv) * w4.z;
+                v[i].w = (v[i].w * inv) * w4.w;
+            }
+        };
+        if (a.norm) {
+            float *parts = reinterpret_cast<float *>(smem + mvr_norm_offset(ntok, K, F::kq, KS > 1 ? NW * 64 * NT * 4 : 0));
+            auto sumsq = [&](const float4 *v, uint32_t e) {
+                float ss = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    ss = fmaf(v[i].x, v[i].x, ss);
+                    ss = fmaf(v[i].y, v[i].y, ss);
+                    ss = fmaf(v[i].z, v[i].z, ss);
+                    ss = fmaf(v[i].w, v[i].w, ss);
+                }
+                parts[e / 16] = ss;
+            };
+#pragma unroll
+            for (int j = 0; j < PB; j++) {
+                const uint32_t e = 1024 * (wave + NW * j) + 16 * lane;
+                if (wave + NW * j < nchunk && e < nflat) sumsq(xv[j], e);
+            }
+            for (uint32_t c0 = wave + NW * PB; c0 < nchunk; c0 += NW) {
+                float4 tmp[4];
+                xload(c0, tmp);
+                const uint32_t e = 1024 * c0 + 16 * lane;
+                if (e < nflat) sumsq(tmp, e);
+            }
+            __syncthreads();
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                invt[t] = 0.0f;
+                if (uint32_t(t) >= ntok) continue;
+                float ss = 0.0f;
+                for (uint32_t q = t * (K / 16) + lane; q < (t + 1) * (K / 16); q += 64) ss += parts[q];
+#pragma unroll
+                for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+                invt[t] = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, float(K)) + a.eps));
+            }
+#pragma unroll
+            for (int j = 0; j < PB; j++) norm_chunk(xv[j], 1024 * (wave + NW * j) + 16 * lane);
+        }
 #pragma unroll
         for (int j = 0; j < PB; j++) {
             const uint32_t cidx = wave + NW * j;
@@ -918,6 +987,10 @@ __global__ __launch_bounds__(NW * 64) void mmvr_kernel(MvArgs a) {
         for (uint32_t c0 = wave + NW * PB; c0 < nchunk; c0 += NW * PB) {
 #pragma unroll
             for (int j = 0; j < PB; j++) xload(c0 + NW * j, xv[j]);
+            if (a.norm) {
+#pragma unroll
+                for (int j = 0; j < PB; j++) norm_chunk(xv[j], 1024 * (c0 + NW * j) + 16 * lane);
+            }
 #pragma unroll
             for (int j = 0; j < PB; j++) {
                 const uint32_t cidx = c0 + NW * j;

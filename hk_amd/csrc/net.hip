@@ -1,0 +1,606 @@
+// The whole-network device pass: embedding lookup, the decoder layers and the logits, on the
+// quantized-linear kernels of this library plus the few kernels of this file (RMS norm, per-head
+// norm + RoPE + K/V cache write, split-context attention and its combine, silu(gate)*up over
+// interleaved rows).
+//
+// Reference behaviour mirrored (layer order and arithmetic of hk's engines):
+//   layer order, residual adds         src/engine/cpu_backend.zig:248-322 forwardFrom
+//   device pass and graph replay       src/cuda/engine.zig:646-797 runBatch / forwardImpl / runPass
+//   rmsNorm / headNorm / swiglu        src/engine/ops.zig:10-38, 70-80
+//   RoPE inverse frequencies, angles   src/engine/ops.zig:96-160 ropeInvFreq (no scaling) / ropeAngles
+//   RoPE styles norm / neox            src/engine/ops.zig:164-185 ropeApply
+//   attention (causal, GQA, 1/sqrt(hd), split slices merged by max/sum)
+//                                      src/engine/attention.zig:44-133 run / merge
+//   K/V cache in f16                   src/engine/kv.zig:1-11
+//
+// MI355X-specific choices: decode passes (1-8 tokens) fuse the RMS norm into the input staging of
+// the q/k/v, gate/up and output products, make the residual adds accumulate-mode products, and
+// use one silu(gate)*up launch over gate/up rows interleaved at load; the pass reads the tokens and
+// positions from device memory, so one captured HIP graph per token count serves every position.
+// Attention splits the context into fixed slices of ATT_SLICE positions (slices past a token's
+// position only record an empty partial), so the launch shape never depends on the position.
+#include <hip/hip_fp16.h>
+
+#include <algorithm>
+#include <map>
+#include <math.h>
+#include <string.h>
+#include <vector>
+
+#include "common.hpp"
+
+using namespace hkhip;
+
+namespace {
+
+constexpr uint32_t ATT_SLICE = 256; // positions per attention slice
+constexpr uint32_t MAX_DECODE = 8;  // tokens of a pass that runs the decode kernels (and a graph)
+
+// ---------------------------------------------------------------------------------------------
+// Kernels
+// ---------------------------------------------------------------------------------------------
+
+__device__ __forceinline__ float block_sum(float v, float *red) {
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    const uint32_t w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    float s = 0.0f;
+    for (uint32_t i = 0; i < nw; i++) s += red[i];
+    return s;
+}
+
+// out[t] = x[t] * (1 / sqrt(mean(x[t]^2) + eps)) * w, one workgroup per row (ops.zig:10-29).
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                      float *__restrict__ out, uint32_t dim, float eps) {
+    __shared__ float red[4];
+    const float *xr = x + uint64_t(blockIdx.x) * dim;
+    float ss = 0.0f;
+    for (uint32_t i = threadIdx.x; i < dim; i += blockDim.x) ss = fmaf(xr[i], xr[i], ss);
+    ss = block_sum(ss, red);
+    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, float(dim)) + eps));
+    float *o = out + uint64_t(blockIdx.x) * dim;
+    for (uint32_t i = threadIdx.x; i < dim; i += blockDim.x) o[i] = (xr[i] * inv) * w[i];
+}
+
+// One wave per (token, head): heads 0..nh-1 are query heads (normalized, rotated, written back),
+// nh..nh+nkv-1 key heads (normalized, rotated, written to the f16 key cache), then nkv value heads
+// (to the f16 value cache). Position of token t: pos0[0] + t. Cache layout [kv head][max_ctx][hd].
+struct RopeArgs {
+    float *q;
+    const float *k, *v;
+    const float *q_norm, *k_norm; // [hd] or null
+    const float *inv_freq;        // [rope_dim / 2]
+    __half *kc, *vc;              // this layer's caches
+    const uint32_t *pos0;
+    uint32_t nh, nkv, hd, rope_half, neox, max_ctx;
+    float eps;
+};
+
+__global__ __launch_bounds__(64) void rope_kv_kernel(RopeArgs a) {
+    const uint32_t t = blockIdx.y, hh = blockIdx.x, lane = threadIdx.x;
+    const uint32_t pos = a.pos0[0] + t;
+    const uint32_t hd = a.hd, qd = a.nh * hd, kvd = a.nkv * hd;
+    const bool isq = hh < a.nh, isk = !isq && hh < a.nh + a.nkv;
+    if (!isq && !isk) { // value head: straight to the cache
+        const uint32_t g = hh - a.nh - a.nkv;
+        const float *src = a.v + uint64_t(t) * kvd + g * hd;
+        __half *dst = a.vc + (uint64_t(g) * a.max_ctx + pos) * hd;
+        for (uint32_t d = lane; d < hd; d += 64) dst[d] = __float2half(src[d]);
+        return;
+    }
+    const uint32_t g = isq ? hh : hh - a.nh;
+    const float *src = isq ? a.q + uint64_t(t) * qd + g * hd : a.k + uint64_t(t) * kvd + g * hd;
+    const float *nw = isq ? a.q_norm : a.k_norm;
+    __shared__ float h[512];
+    for (uint32_t d = lane; d < hd; d += 64) h[d] = src[d];
+    __syncthreads();
+    if (nw) { // headNorm: rmsNorm over the head (ops.zig:31-38)
+        float ss = 0.0f;
+        for (uint32_t d = lane; d < hd; d += 64) ss = fmaf(h[d], h[d], ss);
+        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, float(hd)) + a.eps));
+        __syncthreads();
+        for (uint32_t d = lane; d < hd; d += 64) h[d] = (h[d] * inv) * nw[d];
+        __syncthreads();
+    }
+    // ropeAngles (ops.zig:154-160): angle = f32(pos) * inv_freq[i]; ropeApply (164-185).
+    const float p = float(pos);
+    for (uint32_t i = lane; i < a.rope_half; i += 64) {
+        const float ang = p * a.inv_freq[i];
+        const float c = cosf(ang), s = sinf(ang);
+        const uint32_t i0 = a.neox ? i : 2 * i, i1 = a.neox ? i + a.rope_half : 2 * i + 1;
+        const float x0 = h[i0], x1 = h[i1];
+        h[i0] = x0 * c - x1 * s;
+        h[i1] = x0 * s + x1 * c;
+    }
+    __syncthreads();
+    if (isq) {
+        float *dst = a.q + uint64_t(t) * qd + g * hd;
+        for (uint32_t d = lane; d < hd; d += 64) dst[d] = h[d];
+    } else {
+        __half *dst = a.kc + (uint64_t(g) * a.max_ctx + pos) * hd;
+        for (uint32_t d = lane; d < hd; d += 64) dst[d] = __float2half(h[d]);
+    }
+}
+
+// Attention over one slice of the context for the `group` query heads of one key/value head and
+// one token: one wave per query head, 64 positions per step (lane = position for the scores,
+// lane = dimensions for the value sums), online softmax. Writes {max, sum, acc[hd]} per (token,
+// head, slice); a slice past the token's position writes {-inf, 0, 0...}.
+struct AttnArgs {
+    const float *q;
+    const __half *kc, *vc;
+    float *part;
+    const uint32_t *pos0;
+    uint32_t nh, nkv, hd, max_ctx, nslice;
+    float scale;
+};
+
+template <int HD>
+__global__ __launch_bounds__(1024) void attn_slice_kernel(AttnArgs a) {
+    constexpr int DL = HD / 64; // dimensions per lane
+    const uint32_t t = blockIdx.y, kvh = blockIdx.x / a.nslice, sl = blockIdx.x % a.nslice;
+    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const uint32_t group = a.nh / a.nkv, h = kvh * group + w;
+    const uint32_t pos = a.pos0[0] + t;
+    const uint32_t p_begin = sl * ATT_SLICE;
+    const uint32_t p_end = min(p_begin + ATT_SLICE, pos + 1); // exclusive
+    float *out = a.part + ((uint64_t(t) * a.nh + h) * a.nslice + sl) * (HD + 2);
+    extern __shared__ float qs[]; // [group][HD]
+    float *qw = qs + w * HD;
+    const float *qsrc = a.q + (uint64_t(t) * a.nh + h) * HD;
+#pragma unroll
+    for (int j = 0; j < DL; j++) qw[lane + 64 * j] = qsrc[lane + 64 * j];
+    __syncthreads();
+    float m = -INFINITY, l = 0.0f, acc[DL];
+#pragma unroll
+    for (int j = 0; j < DL; j++) acc[j] = 0.0f;
+    const __half *kb = a.kc + uint64_t(kvh) * a.max_ctx * HD;
+    const __half *vb = a.vc + uint64_t(kvh) * a.max_ctx * HD;
+    for (uint32_t p0 = p_begin; p0 < p_end; p0 += 64) {
+        const uint32_t pp = p0 + lane;
+        float s = -INFINITY;
+        if (pp < p_end) {
+            const uint4 *kr = reinterpret_cast<const uint4 *>(kb + uint64_t(pp) * HD);
+            float dot = 0.0f;
+#pragma unroll
+            for (int c = 0; c < HD / 8; c++) {
+                const uint4 u = kr[c];
+                const __half2 *hp = reinterpret_cast<const __half2 *>(&u);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float2 f = __half22float2(hp[e]);
+                    dot = fmaf(qw[8 * c + 2 * e], f.x, dot);
+                    dot = fmaf(qw[8 * c + 2 * e + 1], f.y, dot);
+                }
+            }
+            s = dot * a.scale;
+        }
+        float mx = s;
+        for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        const float mn = fmaxf(m, mx);
+        const float pr = pp < p_end ? expf(s - mn) : 0.0f;
+        float ps = pr;
+        for (int o = 32; o >= 1; o >>= 1) ps += __shfl_xor(ps, o);
+        const float corr = m == -INFINITY ? 0.0f : expf(m - mn);
+        l = l * corr + ps;
+#pragma unroll
+        for (int j = 0; j < DL; j++) acc[j] *= corr;
+        const uint32_t cnt = p_end - p0 < 64 ? p_end - p0 : 64;
+        for (uint32_t i = 0; i < cnt; i++) {
+            const float pi = __shfl(pr, int(i));
+            const __half *vr = vb + uint64_t(p0 + i) * HD;
+#pragma unroll
+            for (int j = 0; j < DL; j++) acc[j] = fmaf(pi, __half2float(vr[lane + 64 * j]), acc[j]);
+        }
+        m = mn;
+    }
+    if (lane == 0) {
+        out[0] = m;
+        out[1] = l;
+    }
+#pragma unroll
+    for (int j = 0; j < DL; j++) out[2 + lane + 64 * j] = acc[j];
+}
+
+// att[t][h*hd..] = merge of the slices' partials (attention.zig:113-133 merge).
+__global__ __launch_bounds__(256) void attn_combine_kernel(const float *__restrict__ part, float *__restrict__ att,
+                                                           uint32_t nh, uint32_t hd, uint32_t nslice) {
+    const uint32_t t = blockIdx.y, h = blockIdx.x;
+    const float *p = part + (uint64_t(t) * nh + h) * nslice * (hd + 2);
+    float big = -INFINITY;
+    for (uint32_t s = 0; s < nslice; s++)
+        if (p[s * (hd + 2) + 1] != 0.0f) big = fmaxf(big, p[s * (hd + 2)]);
+    float total = 0.0f;
+    for (uint32_t s = 0; s < nslice; s++)
+        if (p[s * (hd + 2) + 1] != 0.0f) total += expf(p[s * (hd + 2)] - big) * p[s * (hd + 2) + 1];
+    const float inv = 1.0f / total;
+    float *o = att + (uint64_t(t) * nh + h) * hd;
+    for (uint32_t d = threadIdx.x; d < hd; d += blockDim.x) {
+        float v = 0.0f;
+        for (uint32_t s = 0; s < nslice; s++)
+            if (p[s * (hd + 2) + 1] != 0.0f) v += expf(p[s * (hd + 2)] - big) * p[s * (hd + 2) + 2 + d];
+        o[d] = v * inv;
+    }
+}
+
+// h[t][i] = silu(gu[t][2i]) * gu[t][2i+1] (gate/up rows interleaved; ops.zig:70-80 swiglu).
+__global__ __launch_bounds__(256) void swiglu_pairs_kernel(const float *__restrict__ gu, float *__restrict__ h,
+                                                           uint64_t total) {
+    const uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < total) h[i] = silu_mul(gu[2 * i], gu[2 * i + 1]);
+}
+
+} // namespace
+
+// ---------------------------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------------------------
+
+struct hkhip_net {
+    hkhip_engine *eng;
+    hkhip_net_config cfg;
+    struct Layer {
+        hkhip_mat wq{}, wk{}, wv{}, wo{}, wgu{}, wd{};
+        float *attn_norm = nullptr, *ffn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
+        float *bq = nullptr, *bk = nullptr, *bv = nullptr;
+        bool loaded = false;
+    };
+    std::vector<Layer> layers;
+    hkhip_mat embd{}, output{};
+    float *out_norm = nullptr;
+    // Device buffers ([MAX tokens][...] sized for the largest pass seen).
+    std::vector<void *> owned;
+    uint32_t cap = 0; // tokens the pass buffers hold
+    float *x = nullptr, *xb = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *gu = nullptr,
+          *h = nullptr, *part = nullptr, *logits = nullptr, *inv_freq = nullptr;
+    uint8_t *xq = nullptr;
+    __half *kc = nullptr, *vc = nullptr;
+    uint32_t *tok = nullptr, *pos = nullptr;
+    std::map<uint32_t, hipGraphExec_t> graphs;
+    std::map<uint32_t, int> runs; // eager runs per decode token count (a graph is captured after one)
+    uint32_t last_n = 0;
+};
+
+namespace {
+
+int hfail(hipError_t e, const char *what) {
+    return set_error(e == hipErrorOutOfMemory ? HKHIP_E_OUT_OF_DEVICE_MEMORY : HKHIP_E_DEVICE_FAILED, "%s: %s", what,
+                     hipGetErrorString(e));
+}
+#define NET_TRY(expr, what)                           \
+    do {                                              \
+        hipError_t e_ = (expr);                       \
+        if (e_ != hipSuccess) return hfail(e_, what); \
+    } while (0)
+
+uint32_t qdim(const hkhip_net_config &c) { return c.n_heads * c.head_dim; }
+uint32_t kvdim(const hkhip_net_config &c) { return c.n_kv_heads * c.head_dim; }
+uint32_t nslices(const hkhip_net_config &c) { return (c.max_ctx + ATT_SLICE - 1) / ATT_SLICE; }
+
+int dev_alloc(hkhip_net *n, uint64_t bytes, void **p) {
+    NET_TRY(hipMalloc(p, bytes ? bytes : 1), "hipMalloc");
+    n->owned.push_back(*p);
+    return HKHIP_OK;
+}
+
+// An f32 vector of `len` floats to the device (null for an absent optional tensor).
+int load_vec(hkhip_net *n, const hkhip_net_tensor &t, uint32_t len, bool optional, float **out, const char *name) {
+    *out = nullptr;
+    if (!t.data) {
+        if (optional) return HKHIP_OK;
+        return set_error(HKHIP_E_BAD_ARGUMENT, "%s is required", name);
+    }
+    if (t.t != HKHIP_F32 || t.bytes != uint64_t(len) * 4)
+        return set_error(HKHIP_E_BAD_ARGUMENT, "%s: expected %u f32 values (type 0x00), got type 0x%02x, %llu bytes", name,
+                         len, t.t, (unsigned long long)t.bytes);
+    int rc = dev_alloc(n, t.bytes, reinterpret_cast<void **>(out));
+    if (rc) return rc;
+    return hkhip_copy_h2d(n->eng, *out, t.data, t.bytes);
+}
+
+int load_mat(hkhip_net *n, const hkhip_net_tensor &t, uint32_t rows, uint32_t cols, hkhip_mat *out, const char *name) {
+    if (!t.data) return set_error(HKHIP_E_BAD_ARGUMENT, "%s is required", name);
+    const int rc = hkhip_upload(n->eng, t.data, t.bytes, t.t, rows, cols, 0, out);
+    if (rc) return set_error(rc, "%s (%ux%u): %s", name, rows, cols, hkhip_last_error());
+    return HKHIP_OK;
+}
+
+// Pass buffers for up to `want` tokens.
+int ensure_cap(hkhip_net *n, uint32_t want) {
+    if (want <= n->cap) return HKHIP_OK;
+    const hkhip_net_config &c = n->cfg;
+    // Freed buffers belong to captured graphs too: drop them.
+    for (auto &g : n->graphs) (void)hipGraphExecDestroy(g.second);
+    n->graphs.clear();
+    n->runs.clear();
+    float **bufs[] = {&n->x, &n->xb, &n->q, &n->k, &n->v, &n->att, &n->gu, &n->h, &n->part,
+                      reinterpret_cast<float **>(&n->tok)};
+    for (float **b : bufs) {
+        if (*b) {
+            (void)hipFree(*b);
+            for (auto &o : n->owned)
+                if (o == *b) o = nullptr;
+            *b = nullptr;
+        }
+    }
+    if (n->xq) {
+        (void)hipFree(n->xq);
+        for (auto &o : n->owned)
+            if (o == n->xq) o = nullptr;
+        n->xq = nullptr;
+    }
+    const uint64_t T = want;
+    const uint32_t maxk = std::max(std::max(c.dim, qdim(c)), c.ffn_dim);
+    int rc;
+    if ((rc = dev_alloc(n, T * c.dim * 4, (void **)&n->x)) || (rc = dev_alloc(n, T * std::max(c.dim, qdim(c)) * 4, (void **)&n->xb)) ||
+        (rc = dev_alloc(n, T * qdim(c) * 4, (void **)&n->q)) || (rc = dev_alloc(n, T * kvdim(c) * 4, (void **)&n->k)) ||
+        (rc = dev_alloc(n, T * kvdim(c) * 4, (void **)&n->v)) || (rc = dev_alloc(n, T * qdim(c) * 4, (void **)&n->att)) ||
+        (rc = dev_alloc(n, T * 2 * c.ffn_dim * 4, (void **)&n->gu)) || (rc = dev_alloc(n, T * c.ffn_dim * 4, (void **)&n->h)) ||
+        (rc = dev_alloc(n, T * c.n_heads * nslices(c) * (c.head_dim + 2) * 4, (void **)&n->part)) ||
+        (rc = dev_alloc(n, hkhip_act_bytes(want, maxk), (void **)&n->xq)) ||
+        (rc = dev_alloc(n, T * 4, (void **)&n->tok)))
+        return rc;
+    n->cap = want;
+    return HKHIP_OK;
+}
+
+// The products of one pass. xin: f32 input [n][cols]; norm: fused RMS norm weights or null.
+int product(hkhip_net *net, uint32_t n, const hkhip_mat *mats, uint32_t nparts, const float *xin, const float *norm,
+            float *const *ys, const float *const *biases, int mode) {
+    hkhip_engine *eng = net->eng;
+    const uint32_t cols = mats[0].cols;
+    if (n <= MAX_DECODE) {
+        if (norm) {
+            const int rc = hkhip_matvec_parts_rmsnorm(eng, mats, nparts, xin, norm, net->cfg.rms_eps, n, ys, biases, mode);
+            if (rc != HKHIP_E_UNSUPPORTED_SHAPE) return rc;
+            hipLaunchKernelGGL(rmsnorm_kernel, dim3(n), dim3(256), 0, eng->cur, xin, norm, net->xb, cols, net->cfg.rms_eps);
+            NET_TRY(hipGetLastError(), "rmsnorm");
+            xin = net->xb;
+        }
+        return hkhip_matvec_parts(eng, mats, nparts, xin, nullptr, n, ys, biases, mode);
+    }
+    if (norm) {
+        hipLaunchKernelGGL(rmsnorm_kernel, dim3(n), dim3(256), 0, eng->cur, xin, norm, net->xb, cols, net->cfg.rms_eps);
+        NET_TRY(hipGetLastError(), "rmsnorm");
+        xin = net->xb;
+    }
+    int rc = hkhip_qact(eng, xin, n, cols, act_kind(mats[0].t), net->xq);
+    for (uint32_t i = 0; !rc && i < nparts; i++)
+        rc = hkhip_mm(eng, &mats[i], net->xq, ys[i], n, biases ? biases[i] : nullptr, mode);
+    return rc;
+}
+
+int run_pass(hkhip_net *net, uint32_t n) {
+    const hkhip_net_config &c = net->cfg;
+    hkhip_engine *eng = net->eng;
+    hipStream_t s = eng->cur;
+    const uint32_t ns = nslices(c);
+    int rc;
+    NET_TRY(launch_dequant_gather(net->embd.t, reinterpret_cast<const uint8_t *>(net->embd.mem), net->embd.rows, c.dim,
+                                  net->tok, n, net->x, s), "embedding");
+    for (uint32_t li = 0; li < c.n_layers; li++) {
+        const hkhip_net::Layer &L = net->layers[li];
+        {
+            const hkhip_mat mats[3] = {L.wq, L.wk, L.wv};
+            float *const ys[3] = {net->q, net->k, net->v};
+            const float *const bs[3] = {L.bq, L.bk, L.bv};
+            if ((rc = product(net, n, mats, 3, net->x, L.attn_norm, ys, bs, HKHIP_STORE))) return rc;
+        }
+        const uint64_t cache_layer = uint64_t(c.n_kv_heads) * c.max_ctx * c.head_dim;
+        RopeArgs ra{net->q, net->k, net->v, L.q_norm, L.k_norm, net->inv_freq, net->kc + li * cache_layer,
+                    net->vc + li * cache_layer, net->pos, c.n_heads, c.n_kv_heads, c.head_dim, c.rope_dim / 2,
+                    c.rope_neox, c.max_ctx, c.rms_eps};
+        hipLaunchKernelGGL(rope_kv_kernel, dim3(c.n_heads + 2 * c.n_kv_heads, n), dim3(64), 0, s, ra);
+        NET_TRY(hipGetLastError(), "rope / kv write");
+        AttnArgs aa{net->q, net->kc + li * cache_layer, net->vc + li * cache_layer, net->part, net->pos, c.n_heads,
+                    c.n_kv_heads, c.head_dim, c.max_ctx, ns, 1.0f / sqrtf(float(c.head_dim))};
+        const dim3 ag(c.n_kv_heads * ns, n), ab(64 * (c.n_heads / c.n_kv_heads));
+        const uint32_t alds = (c.n_heads / c.n_kv_heads) * c.head_dim * 4;
+        switch (c.head_dim) {
+        case 64: hipLaunchKernelGGL(attn_slice_kernel<64>, ag, ab, alds, s, aa); break;
+        case 128: hipLaunchKernelGGL(attn_slice_kernel<128>, ag, ab, alds, s, aa); break;
+        case 256: hipLaunchKernelGGL(attn_slice_kernel<256>, ag, ab, alds, s, aa); break;
+        default: return set_error(HKHIP_E_UNSUPPORTED_SHAPE, "head_dim %u", c.head_dim);
+        }
+        NET_TRY(hipGetLastError(), "attention");
+        hipLaunchKernelGGL(attn_combine_kernel, dim3(c.n_heads, n), dim3(128), 0, s, net->part, net->att, c.n_heads,
+                           c.head_dim, ns);
+        NET_TRY(hipGetLastError(), "attention combine");
+        {
+            float *const ys[1] = {net->x};
+            if ((rc = product(net, n, &L.wo, 1, net->att, nullptr, ys, nullptr, HKHIP_ACCUMULATE))) return rc;
+        }
+        if (n <= MAX_DECODE) {
+            float *const ys[1] = {net->h};
+            if ((rc = product(net, n, &L.wgu, 1, net->x, L.ffn_norm, ys, nullptr, HKHIP_SILU_MUL))) return rc;
+        } else {
+            float *const ys[1] = {net->gu};
+            if ((rc = product(net, n, &L.wgu, 1, net->x, L.ffn_norm, ys, nullptr, HKHIP_STORE))) return rc;
+            const uint64_t total = uint64_t(n) * c.ffn_dim;
+            hipLaunchKernelGGL(swiglu_pairs_kernel, dim3(uint32_t((total + 255) / 256)), dim3(256), 0, s, net->gu, net->h,
+                               total);
+            NET_TRY(hipGetLastError(), "swiglu");
+        }
+        {
+            float *const ys[1] = {net->x};
+            if ((rc = product(net, n, &L.wd, 1, net->h, nullptr, ys, nullptr, HKHIP_ACCUMULATE))) return rc;
+        }
+    }
+    // Logits of the last token (cpu_backend.zig:324-331 logitsFor).
+    float *const ys[1] = {net->logits};
+    return product(net, 1, &net->output, 1, net->x + uint64_t(n - 1) * c.dim, net->out_norm, ys, nullptr, HKHIP_STORE);
+}
+
+} // namespace
+
+extern "C" {
+
+int hkhip_net_create(hkhip_engine *eng, const hkhip_net_config *cfg, hkhip_net **out) {
+    if (!eng || !cfg || !out) return set_error(HKHIP_E_BAD_ARGUMENT, "null argument");
+    *out = nullptr;
+    const hkhip_net_config &c = *cfg;
+    if (!c.dim || !c.n_layers || !c.n_heads || !c.n_kv_heads || c.n_heads % c.n_kv_heads || !c.ffn_dim || !c.vocab ||
+        !c.max_ctx)
+        return set_error(HKHIP_E_BAD_ARGUMENT, "bad network shape");
+    if (c.head_dim != 64 && c.head_dim != 128 && c.head_dim != 256)
+        return set_error(HKHIP_E_UNSUPPORTED_SHAPE, "head_dim %u: 64, 128 or 256", c.head_dim);
+    if (c.n_heads / c.n_kv_heads > 16) return set_error(HKHIP_E_UNSUPPORTED_SHAPE, "at most 16 query heads per kv head");
+    if (c.rope_dim % 2 || c.rope_dim > c.head_dim) return set_error(HKHIP_E_BAD_ARGUMENT, "rope_dim %u", c.rope_dim);
+    if (hipSetDevice(eng->device) != hipSuccess) return set_error(HKHIP_E_DEVICE_FAILED, "hipSetDevice");
+    hkhip_net *n = new hkhip_net();
+    n->eng = eng;
+    n->cfg = c;
+    n->layers.resize(c.n_layers);
+    int rc = HKHIP_OK;
+    const uint64_t cache = uint64_t(c.n_layers) * c.n_kv_heads * c.max_ctx * c.head_dim * 2;
+    if ((rc = dev_alloc(n, cache, (void **)&n->kc)) || (rc = dev_alloc(n, cache, (void **)&n->vc)) ||
+        (rc = dev_alloc(n, uint64_t(c.vocab) * 4, (void **)&n->logits)) ||
+        (rc = dev_alloc(n, 4, (void **)&n->pos)) ||
+        (rc = dev_alloc(n, c.rope_dim / 2 * 4 + 4, (void **)&n->inv_freq)) || (rc = ensure_cap(n, MAX_DECODE))) {
+        hkhip_net_destroy(n);
+        return rc;
+    }
+    // ropeInvFreq without scaling (ops.zig:96-146): base^(-2i/n_rot) in f64, then f32.
+    std::vector<float> f(c.rope_dim / 2 + 1, 0.0f);
+    for (uint32_t i = 0; i < c.rope_dim / 2; i++)
+        f[i] = float(pow(double(c.rope_base), -double(2 * i) / double(c.rope_dim)));
+    if ((rc = hkhip_copy_h2d(eng, n->inv_freq, f.data(), f.size() * 4))) {
+        hkhip_net_destroy(n);
+        return rc;
+    }
+    *out = n;
+    return HKHIP_OK;
+}
+
+void hkhip_net_destroy(hkhip_net *net) {
+    if (!net) return;
+    (void)hipSetDevice(net->eng->device);
+    (void)hipStreamSynchronize(net->eng->cur);
+    for (auto &g : net->graphs) (void)hipGraphExecDestroy(g.second);
+    for (auto &L : net->layers) {
+        hkhip_mat *ms[] = {&L.wq, &L.wk, &L.wv, &L.wo, &L.wgu, &L.wd};
+        for (hkhip_mat *m : ms) hkhip_free(net->eng, m);
+    }
+    hkhip_free(net->eng, &net->embd);
+    hkhip_free(net->eng, &net->output);
+    for (void *p : net->owned)
+        if (p) (void)hipFree(p);
+    delete net;
+}
+
+int hkhip_net_load_layer(hkhip_net *net, uint32_t li, const hkhip_net_layer *l) {
+    if (!net || !l) return set_error(HKHIP_E_BAD_ARGUMENT, "null argument");
+    const hkhip_net_config &c = net->cfg;
+    if (li >= c.n_layers) return set_error(HKHIP_E_BAD_ARGUMENT, "layer %u of %u", li, c.n_layers);
+    hkhip_net::Layer &L = net->layers[li];
+    if (L.loaded) return set_error(HKHIP_E_BAD_ARGUMENT, "layer %u is already loaded", li);
+    const uint32_t qd = qdim(c), kvd = kvdim(c);
+    int rc;
+    if ((rc = load_vec(net, l->attn_norm, c.dim, false, &L.attn_norm, "attn_norm")) ||
+        (rc = load_vec(net, l->ffn_norm, c.dim, false, &L.ffn_norm, "ffn_norm")) ||
+        (rc = load_vec(net, l->q_norm, c.head_dim, true, &L.q_norm, "q_norm")) ||
+        (rc = load_vec(net, l->k_norm, c.head_dim, true, &L.k_norm, "k_norm")) ||
+        (rc = load_vec(net, l->bq, qd, true, &L.bq, "bq")) || (rc = load_vec(net, l->bk, kvd, true, &L.bk, "bk")) ||
+        (rc = load_vec(net, l->bv, kvd, true, &L.bv, "bv")))
+        return rc;
+    if (l->wq.t != l->wk.t || l->wq.t != l->wv.t)
+        return set_error(HKHIP_E_BAD_ARGUMENT, "wq, wk and wv must share their type (one fused launch)");
+    if (l->w_gate.t != l->w_up.t) return set_error(HKHIP_E_BAD_ARGUMENT, "w_gate and w_up must share their type");
+    if ((rc = load_mat(net, l->wq, qd, c.dim, &L.wq, "wq")) || (rc = load_mat(net, l->wk, kvd, c.dim, &L.wk, "wk")) ||
+        (rc = load_mat(net, l->wv, kvd, c.dim, &L.wv, "wv")) || (rc = load_mat(net, l->wo, c.dim, qd, &L.wo, "wo")) ||
+        (rc = load_mat(net, l->w_down, c.dim, c.ffn_dim, &L.wd, "w_down")))
+        return rc;
+    // Gate and up rows interleaved (row 2i = gate i, 2i + 1 = up i) for the fused silu(gate)*up.
+    const int64_t rb = hkhip_matrix_bytes(l->w_gate.t, 1, c.dim);
+    if (rb < 0) return int(rb);
+    if (!l->w_gate.data || !l->w_up.data || l->w_gate.bytes != uint64_t(rb) * c.ffn_dim || l->w_up.bytes != l->w_gate.bytes)
+        return set_error(HKHIP_E_BAD_ARGUMENT, "w_gate / w_up: expected %llu bytes each",
+                         (unsigned long long)(uint64_t(rb) * c.ffn_dim));
+    std::vector<uint8_t> inter(uint64_t(rb) * 2 * c.ffn_dim);
+    const uint8_t *g = static_cast<const uint8_t *>(l->w_gate.data), *u = static_cast<const uint8_t *>(l->w_up.data);
+    for (uint32_t i = 0; i < c.ffn_dim; i++) {
+        memcpy(&inter[(2 * uint64_t(i)) * rb], g + uint64_t(i) * rb, size_t(rb));
+        memcpy(&inter[(2 * uint64_t(i) + 1) * rb], u + uint64_t(i) * rb, size_t(rb));
+    }
+    const hkhip_net_tensor gu{inter.data(), inter.size(), l->w_gate.t};
+    if ((rc = load_mat(net, gu, 2 * c.ffn_dim, c.dim, &L.wgu, "w_gate/w_up"))) return rc;
+    L.loaded = true;
+    return HKHIP_OK;
+}
+
+int hkhip_net_load_io(hkhip_net *net, hkhip_net_tensor tok_embd, hkhip_net_tensor out_norm, hkhip_net_tensor output) {
+    if (!net) return set_error(HKHIP_E_BAD_ARGUMENT, "null network");
+    const hkhip_net_config &c = net->cfg;
+    int rc;
+    if ((rc = load_mat(net, tok_embd, c.vocab, c.dim, &net->embd, "tok_embd")) ||
+        (rc = load_vec(net, out_norm, c.dim, false, &net->out_norm, "out_norm")) ||
+        (rc = load_mat(net, output, c.vocab, c.dim, &net->output, "output")))
+        return rc;
+    return HKHIP_OK;
+}
+
+int hkhip_net_forward(hkhip_net *net, const uint32_t *tokens, uint32_t n, uint32_t pos0) {
+    if (!net || (n && !tokens)) return set_error(HKHIP_E_BAD_ARGUMENT, "null argument");
+    const hkhip_net_config &c = net->cfg;
+    if (n == 0) return HKHIP_OK;
+    if (!net->embd.mem || !net->output.mem) return set_error(HKHIP_E_BAD_ARGUMENT, "tok_embd / output not loaded");
+    for (const auto &L : net->layers)
+        if (!L.loaded) return set_error(HKHIP_E_BAD_ARGUMENT, "a layer is not loaded");
+    if (uint64_t(pos0) + n > c.max_ctx) return set_error(HKHIP_E_UNSUPPORTED_SHAPE, "context full: %u + %u > %u", pos0, n, c.max_ctx);
+    for (uint32_t i = 0; i < n; i++)
+        if (tokens[i] >= c.vocab) return set_error(HKHIP_E_BAD_ARGUMENT, "token %u >= vocab %u", tokens[i], c.vocab);
+    if (hipSetDevice(net->eng->device) != hipSuccess) return set_error(HKHIP_E_DEVICE_FAILED, "hipSetDevice");
+    int rc;
+    if ((rc = ensure_cap(net, n))) return rc;
+    if (n > MAX_DECODE) { // prefill: run directly
+        hipStream_t s = net->eng->cur;
+        NET_TRY(hipMemcpyAsync(net->tok, tokens, n * 4, hipMemcpyHostToDevice, s), "tokens");
+        NET_TRY(hipMemcpyAsync(net->pos, &pos0, 4, hipMemcpyHostToDevice, s), "position");
+        if ((rc = run_pass(net, n))) return rc;
+        NET_TRY(hipStreamSynchronize(s), "prefill pass");
+        net->last_n = n;
+        return HKHIP_OK;
+    }
+    hipStream_t s = net->eng->cur;
+    NET_TRY(hipMemcpyAsync(net->tok, tokens, n * 4, hipMemcpyHostToDevice, s), "tokens");
+    NET_TRY(hipMemcpyAsync(net->pos, &pos0, 4, hipMemcpyHostToDevice, s), "position");
+    auto it = net->graphs.find(n);
+    if (it != net->graphs.end()) {
+        NET_TRY(hipGraphLaunch(it->second, s), "graph launch");
+    } else if (net->runs[n]++ == 0) {
+        if ((rc = run_pass(net, n))) return rc; // first pass of this size: eager (fills the launch caches)
+    } else {
+        hipGraph_t g = nullptr;
+        NET_TRY(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "begin capture");
+        rc = run_pass(net, n);
+        const hipError_t e = hipStreamEndCapture(s, &g);
+        if (rc) {
+            if (g) (void)hipGraphDestroy(g);
+            return rc;
+        }
+        NET_TRY(e, "end capture");
+        hipGraphExec_t ex = nullptr;
+        const hipError_t ei = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        NET_TRY(ei, "graph instantiate");
+        net->graphs[n] = ex;
+        NET_TRY(hipGraphLaunch(ex, s), "graph launch");
+    }
+    // The host arrays the copies read are the caller's: wait for them before returning.
+    NET_TRY(hipStreamSynchronize(s), "pass");
+    net->last_n = n;
+    return HKHIP_OK;
+}
+
+int hkhip_net_logits(hkhip_net *net, float *host_out) {
+    if (!net || !host_out) return set_error(HKHIP_E_BAD_ARGUMENT, "null argument");
+    if (!net->last_n) return set_error(HKHIP_E_BAD_ARGUMENT, "no forward pass yet");
+    return hkhip_copy_d2h(net->eng, host_out, net->logits, uint64_t(net->cfg.vocab) * 4);
+}
+
+const float *hkhip_net_logits_dev(hkhip_net *net) { return net ? net->logits : nullptr; }
+
+} // extern "C"

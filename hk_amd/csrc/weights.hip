@@ -92,10 +92,10 @@ __device__ __forceinline__ void scale_min_k4(int j, const uint8_t *q, uint32_t &
 
 // One thread per output weight of rows [row0, row0 + nrows). Out is [nrows][cols].
 __global__ void dequant_kernel(int t, const uint8_t *__restrict__ w, uint32_t cols, uint32_t row0, uint64_t total,
-                               uint64_t scale_off, float *__restrict__ out) {
+                               uint64_t scale_off, float *__restrict__ out, const uint32_t *__restrict__ ids) {
     uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i >= total) return;
-    uint64_t r = row0 + i / cols;
+    uint64_t r = ids ? uint64_t(ids[i / cols]) : row0 + i / cols; // gather: output row j is row ids[j]
     uint32_t c = uint32_t(i % cols);
     const uint16_t *scales = reinterpret_cast<const uint16_t *>(w + scale_off);
     float v;
@@ -177,7 +177,18 @@ hipError_t launch_dequant(int t, const uint8_t *w, uint32_t rows, uint32_t cols,
     if (total == 0) return hipSuccess;
     uint64_t grid = (total + 255) / 256;
     if (grid > 0x7fffffffu) return hipErrorInvalidValue;
-    dequant_kernel<<<uint32_t(grid), 256, 0, s>>>(t, w, cols, row0, total, L.scale_off, out);
+    dequant_kernel<<<uint32_t(grid), 256, 0, s>>>(t, w, cols, row0, total, L.scale_off, out, nullptr);
+    return hipGetLastError();
+}
+
+hipError_t launch_dequant_gather(int t, const uint8_t *w, uint32_t rows, uint32_t cols, const uint32_t *ids, uint32_t n,
+                                 float *out, hipStream_t s) {
+    WLayout L = weight_layout(t, rows, cols);
+    uint64_t total = uint64_t(n) * cols;
+    if (total == 0) return hipSuccess;
+    uint64_t grid = (total + 255) / 256;
+    if (grid > 0x7fffffffu) return hipErrorInvalidValue;
+    dequant_kernel<<<uint32_t(grid), 256, 0, s>>>(t, w, cols, 0, total, L.scale_off, out, ids);
     return hipGetLastError();
 }
 

@@ -161,6 +161,14 @@ class Engine:
         bp = None if biases is None else (ctypes.c_void_p * k)(*[_ptr(b) for b in biases])
         check(lib().hkhip_matvec_parts(self._h, arr, k, _ptr(x), _ptr(xq), n, yp, bp, mode))
 
+    def matvec_parts_rmsnorm(self, mats, ys, n: int, x, norm, eps: float, biases=None, mode: int = STORE) -> None:
+        """matvec_parts on rmsnorm(x) * norm, the norm fused into the products' input staging."""
+        k = len(mats)
+        arr = (HkhipMat * k)(*[m.raw for m in mats])
+        yp = (ctypes.c_void_p * k)(*[_ptr(y) for y in ys])
+        bp = None if biases is None else (ctypes.c_void_p * k)(*[_ptr(b) for b in biases])
+        check(lib().hkhip_matvec_parts_rmsnorm(self._h, arr, k, _ptr(x), _ptr(norm), eps, n, yp, bp, mode))
+
     def gemm(self, m: DevMat, xq, y, n: int, bias=None, mode: int = STORE) -> None:
         check(lib().hkhip_gemm(self._h, ctypes.byref(m.raw), _ptr(xq), _ptr(y), n, _ptr(bias), mode))
 

@@ -105,3 +105,32 @@ def weights_torch(t: int, rows: int, cols: int, seed: int, device="cuda"):
         if has_m:
             raw[:, 2:4] = (-(torch.randn(nb, device=device, generator=g) * 0.02).abs()).half().view(torch.uint8).view(nb, 2)
     return raw.view(rows, -1)
+
+
+def model_np(cfg, fmt: int, seed: int, out_fmt: int | None = None, embd_fmt: int | None = None,
+             qk_norm: bool = True, bias: bool = False) -> dict:
+    """A random decoder of `cfg`'s shape (hk_amd.net.Config): matrices in `fmt` (output in out_fmt,
+    embedding in embd_fmt) as (raw blocks, type); norms 1 + N(0, 0.1); optional q/k norms and
+    q/k/v biases. Same dict layout as hk_amd.net.Net.load takes."""
+    rng = np.random.default_rng(seed)
+    qd, kvd = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
+
+    def vec(n, base=1.0, sd=0.1):
+        return (base + sd * rng.standard_normal(n)).astype(np.float32)
+
+    def mat(t, rows, cols):
+        return weights_np(t, rows, cols, int(rng.integers(1 << 30))), t
+
+    layers = []
+    for _ in range(cfg.n_layers):
+        layers.append({
+            "attn_norm": vec(cfg.dim), "ffn_norm": vec(cfg.dim),
+            "wq": mat(fmt, qd, cfg.dim), "wk": mat(fmt, kvd, cfg.dim), "wv": mat(fmt, kvd, cfg.dim),
+            "wo": mat(fmt, cfg.dim, qd), "w_gate": mat(fmt, cfg.ffn_dim, cfg.dim), "w_up": mat(fmt, cfg.ffn_dim, cfg.dim),
+            "w_down": mat(fmt, cfg.dim, cfg.ffn_dim),
+            "q_norm": vec(cfg.head_dim) if qk_norm else None, "k_norm": vec(cfg.head_dim) if qk_norm else None,
+            "bq": vec(qd, 0.0, 0.5) if bias else None, "bk": vec(kvd, 0.0, 0.5) if bias else None,
+            "bv": vec(kvd, 0.0, 0.5) if bias else None,
+        })
+    return {"layers": layers, "tok_embd": mat(embd_fmt or fmt, cfg.vocab, cfg.dim), "out_norm": vec(cfg.dim),
+            "output": mat(out_fmt or fmt, cfg.vocab, cfg.dim)}

@@ -151,6 +151,14 @@ int hkhip_mm(hkhip_engine *eng, const hkhip_mat *m, const void *xq_dev, float *y
  * NULLs. 1 <= n <= 8. */
 int hkhip_matvec_parts(hkhip_engine *eng, const hkhip_mat *mats, uint32_t nparts, const float *x_dev,
                        const void *xq_dev, uint32_t n, float *const *ys, const float *const *biases, int mode);
+/* The same on rmsnorm(x): each token's input is first scaled by 1 / sqrt(mean(x^2) + eps) and
+ * multiplied by norm_dev [cols] (src/engine/ops.zig:10-29 rmsNorm), inside the products' own input
+ * quantization -- the norm, prepare and runParts of cpu_backend.zig:264-271 in one launch. The
+ * input must be f32; returns UNSUPPORTED_SHAPE for more than 8 tokens or rows too long for the
+ * register decode kernel (the caller then normalizes separately). */
+int hkhip_matvec_parts_rmsnorm(hkhip_engine *eng, const hkhip_mat *mats, uint32_t nparts, const float *x_dev,
+                               const float *norm_dev, float eps, uint32_t n, float *const *ys,
+                               const float *const *biases, int mode);
 
 /* ---- product without allocation (no counterpart in the reference) ----
  * For callers that cannot allocate device memory: code under HIP graph capture, tight serving
@@ -164,6 +172,49 @@ int hkhip_matvec_parts(hkhip_engine *eng, const hkhip_mat *mats, uint32_t nparts
 #define HKHIP_NOALLOC_SCRATCH_BYTES (24ull << 20)
 int hkhip_mm_noalloc(hkhip_engine *eng, const hkhip_mat *m, const float *x_dev, float *y_dev, uint32_t n,
                      const float *bias_dev, int mode);
+
+/* ---- whole network (the device engine's pass: src/cuda/engine.zig:646-797 runBatch / runPass,
+ * with the CPU engine's layer order src/engine/cpu_backend.zig:248-322 forwardFrom) ----
+ * A decoder of n_layers blocks, each
+ *   xb = rmsnorm(x) * attn_norm; q, k, v = Wq xb + bq, Wk xb + bk, Wv xb + bv;
+ *   q, k = rope(headnorm(q, q_norm), headnorm(k, k_norm)); K/V cache (f16) += k, v at the position;
+ *   att = causal GQA attention softmax(q K^T / sqrt(head_dim)) V; x += Wo att;
+ *   xb = rmsnorm(x) * ffn_norm; x += Wdown (silu(Wgate xb) * (Wup xb)),
+ * between an embedding lookup (a row of tok_embd, decoded) and logits = Woutput (rmsnorm(x) *
+ * out_norm) of the last token. One sequence per network (a K/V cache of max_ctx positions).
+ * Passes of up to 8 tokens run the decode kernels (RMS norm fused into the products' input
+ * quantization, residual adds as accumulate-mode products, gate/up as one silu(gate)*up launch)
+ * and are captured in a HIP graph per token count after their first run; longer passes (prompt
+ * prefill) run the MFMA GEMMs. Matrices are hk file-layout bytes in host memory, copied at load;
+ * Wgate and Wup must share their type. Vectors (norms, biases) are f32 (HKHIP_F32). */
+#define HKHIP_F32 0x00 /* hk StorageType f32 (src/format.zig:28) */
+typedef struct hkhip_net hkhip_net;
+typedef struct hkhip_net_config {
+    uint32_t dim, n_layers, n_heads, n_kv_heads, head_dim, ffn_dim, vocab;
+    uint32_t rope_dim;  /* rotated dimensions of a head (head_dim for full rotary) */
+    uint32_t rope_neox; /* 0: pairs (2i, 2i+1) ("norm" style); 1: pairs (i, i + rope_dim/2) */
+    uint32_t max_ctx;   /* K/V cache positions */
+    float rms_eps, rope_base;
+} hkhip_net_config;
+/* A tensor in hk's file layout in host memory; data NULL for an absent optional tensor. */
+typedef struct hkhip_net_tensor {
+    const void *data;
+    uint64_t bytes;
+    uint8_t t;
+} hkhip_net_tensor;
+typedef struct hkhip_net_layer {
+    hkhip_net_tensor attn_norm, wq, wk, wv, bq, bk, bv, q_norm, k_norm, wo, ffn_norm, w_gate, w_up, w_down;
+} hkhip_net_layer;
+int hkhip_net_create(hkhip_engine *eng, const hkhip_net_config *cfg, hkhip_net **out);
+void hkhip_net_destroy(hkhip_net *net);
+int hkhip_net_load_layer(hkhip_net *net, uint32_t layer, const hkhip_net_layer *l);
+int hkhip_net_load_io(hkhip_net *net, hkhip_net_tensor tok_embd, hkhip_net_tensor out_norm, hkhip_net_tensor output);
+/* Runs tokens[0..n) at positions pos0.. of the sequence (the cache keeps positions < pos0). */
+int hkhip_net_forward(hkhip_net *net, const uint32_t *tokens, uint32_t n, uint32_t pos0);
+/* Logits of the last token of the last forward: vocab floats, to host memory. */
+int hkhip_net_logits(hkhip_net *net, float *host_out);
+/* The same logits in device memory (valid until the next forward). */
+const float *hkhip_net_logits_dev(hkhip_net *net);
 
 /* ---- host-pointer products (secondary boundary: src/c_api.zig:1380-1400, hk.h:451-453,
  * src/engine/abi_ops.zig:65-107) ----

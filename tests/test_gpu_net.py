@@ -1,0 +1,97 @@
+"""The whole-network HIP pass (hkhip_net_*) against the CPU restatement of hk's forward pass
+(oracle/net_oracle.py) on tiny random models, in the manner of the reference's device tests
+(tests/test_gpu.zig:12, 49-123: a model run on the device and on the CPU, logits compared by
+cosine >= 0.9999). Every pass is checked: a prefill (GEMM path, more than 8 tokens), then decode
+passes of 1-8 tokens (decode kernels with the fused RMS norm; the first of each size eager, later
+ones replayed from a captured HIP graph), across attention slices of 256 positions."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from hk_amd import formats as F
+from hk_amd import synth
+from hk_amd.net import Config
+from oracle.net_oracle import Oracle
+
+pytestmark = pytest.mark.gpu
+
+COS_MIN = 0.9999      # tests/test_gpu.zig:49-123
+ABS_FRAC = 2e-2       # and no logit further than 2% of the largest from the CPU's
+
+
+@pytest.fixture(scope="module")
+def eng():
+    import torch
+
+    from hk_amd import Engine
+
+    assert torch.cuda.is_available(), "GPU tests need a visible MI355X"
+    e = Engine(0)
+    yield e
+    e.close()
+
+
+def check(got: np.ndarray, want: np.ndarray, what: str):
+    got, want = got.astype(np.float64), want.astype(np.float64)
+    cos = float(got @ want / (np.linalg.norm(got) * np.linalg.norm(want)))
+    err = float(np.max(np.abs(got - want)) / np.max(np.abs(want)))
+    assert np.isfinite(got).all(), what
+    assert cos >= COS_MIN and err <= ABS_FRAC, f"{what}: cos {cos:.6f}, max err {err:.2e}"
+
+
+CASES = {
+    # Qwen3-like: q/k norms, neox RoPE, GQA 2:1, head_dim 64; Q4_K body, Q6_K output, Q8_0 embedding
+    "qwen-q4k": (Config(dim=256, n_layers=2, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=512, vocab=512,
+                        max_ctx=600, rope_neox=True, rope_base=1e6), F.Q4_K, F.Q6_K, F.Q8_0, True, False),
+    # Llama-like: no q/k norms, pairwise RoPE, q/k/v biases, GQA 4:1, head_dim 128; Q8_0 body
+    "llama-q8_0": (Config(dim=512, n_layers=2, n_heads=8, n_kv_heads=2, head_dim=128, ffn_dim=768, vocab=400,
+                          max_ctx=300, rope_neox=False, rope_base=5e5, rms_eps=1e-5), F.Q8_0, F.Q8_0, F.Q4_K, False, True),
+    # IQ4_NL body with Q4_K output; partial rotary (half the head), no GQA
+    "iq4nl-partial-rope": (Config(dim=256, n_layers=1, n_heads=4, n_kv_heads=4, head_dim=64, ffn_dim=256, vocab=300,
+                                  max_ctx=300, rope_dim=32), F.IQ4_NL, F.Q4_K, F.Q6_K, True, False),
+}
+
+
+@pytest.mark.parametrize("case", list(CASES))
+def test_net_passes_match_cpu(eng, case):
+    from hk_amd.net import Net
+
+    cfg, fmt, out_fmt, embd_fmt, qk_norm, bias = CASES[case]
+    model = synth.model_np(cfg, fmt, seed=4000 + len(case), out_fmt=out_fmt, embd_fmt=embd_fmt, qk_norm=qk_norm,
+                           bias=bias)
+    rng = np.random.default_rng(4100)
+    cpu = Oracle(cfg, model)
+    with Net(eng, cfg) as net:
+        net.load(model)
+        pos = 0
+        # prefill past the first attention slice, then decode passes; repeated sizes replay graphs
+        for n in [260, 1, 1, 1, 3, 3, 8, 8, 1, 17, 1]:
+            if pos + n > cfg.max_ctx:
+                break
+            toks = rng.integers(0, cfg.vocab, n)
+            net.forward(toks, pos)
+            want = cpu.forward(toks, pos)
+            check(net.logits(), want, f"{case} pass of {n} at {pos}")
+            print(case, n, pos, "ok", flush=True)
+            pos += n
+
+
+def test_net_rejects(eng):
+    from hk_amd import HipError
+    from hk_amd.net import Net
+
+    cfg = Config(dim=256, n_layers=1, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=256, vocab=64, max_ctx=16)
+    with pytest.raises(HipError):
+        Net(eng, Config(dim=256, n_layers=1, n_heads=4, n_kv_heads=2, head_dim=96, ffn_dim=256, vocab=64, max_ctx=16))
+    model = synth.model_np(cfg, F.Q4_K, seed=4200)
+    with Net(eng, cfg) as net:
+        with pytest.raises(HipError):
+            net.forward([1, 2], 0)  # nothing loaded yet
+        net.load(model)
+        with pytest.raises(HipError):
+            net.forward([1] * 10, 10)  # past max_ctx
+        with pytest.raises(HipError):
+            net.forward([64], 0)  # token outside the vocabulary
+        net.forward([1, 2, 3], 0)
+        assert np.isfinite(net.logits()).all()

@@ -779,3 +779,55 @@ def test_mm_tall_break_even(eng, torch_cuda, t, n):
     got = run(eng, torch_cuda, t, raw, m, k, x, path="mm", bias=bias, mode=1, y0=y0)
     want = O.matmul(t, raw, m, k, x, n, bias=bias, threads=16) + y0
     assert parity_err(got, want) <= PARITY_TOL
+
+
+# ---------------------------------------------------------------------------------------- fused RMS norm
+
+@pytest.mark.parametrize("t", FMTS)
+@pytest.mark.parametrize("n,k", [(1, 1024), (1, 4096), (3, 2048), (8, 4096), (1, 14336), (2, 3072)])
+def test_matvec_parts_rmsnorm(eng, torch_cuda, t, n, k):
+    """hkhip_matvec_parts_rmsnorm: rmsnorm(x) * w (ops.zig:10-29) fused into the products' input
+    quantization, q/k/v-style parts with biases, against the oracle's products of the CPU norm."""
+    from oracle.net_oracle import rms_norm
+
+    torch = torch_cuda
+    heights = [96, 40]
+    raws = [synth.weights_np(t, m, k, seed=2700 + i + t) for i, m in enumerate(heights)]
+    x = synth.activations_np(n, k, seed=2701 + n, outliers=0.01) * 3.0
+    w = (1.0 + 0.1 * np.random.default_rng(2702).standard_normal(k)).astype(np.float32)
+    eps = 1e-6
+    mats = [eng.upload(r, t, m, k) for r, m in zip(raws, heights)]
+    ys = [torch.full((n, m), float("nan"), device="cuda") for m in heights]
+    biases = [torch.from_numpy(np.linspace(-1, 1, m).astype(np.float32)).cuda() for m in heights]
+    eng.matvec_parts_rmsnorm(mats, ys, n, torch.from_numpy(x).cuda(), torch.from_numpy(w).cuda(), eps, biases=biases)
+    torch.cuda.synchronize()
+    xb = np.stack([rms_norm(x[i], w, eps) for i in range(n)])
+    for r, m, y, b in zip(raws, heights, ys, biases):
+        want = O.matmul(t, r, m, k, xb, n, bias=b.cpu().numpy(), tiled=False)
+        assert parity_err(y.cpu().numpy(), want) <= PARITY_TOL
+    for mm in mats:
+        eng.free(mm)
+
+
+def test_matvec_parts_rmsnorm_silu_and_limits(eng, torch_cuda):
+    from hk_amd import HipError
+    from oracle.net_oracle import rms_norm
+
+    torch = torch_cuda
+    t, m, k, n = F.Q4_K, 2 * 200, 4096, 2
+    raw = synth.weights_np(t, m, k, seed=2710)
+    x = synth.activations_np(n, k, seed=2711)
+    w = (1.0 + 0.1 * np.random.default_rng(2712).standard_normal(k)).astype(np.float32)
+    mat = eng.upload(raw, t, m, k)
+    y = torch.full((n, m // 2), float("nan"), device="cuda")
+    xd, wd = torch.from_numpy(x).cuda(), torch.from_numpy(w).cuda()
+    eng.matvec_parts_rmsnorm([mat], [y], n, xd, wd, 1e-5, mode=SILU_MUL)
+    torch.cuda.synchronize()
+    xb = np.stack([rms_norm(x[i], w, 1e-5) for i in range(n)])
+    want = silu_mul_ref(O.matmul(t, raw, m, k, xb, n, tiled=False))
+    assert parity_err(y.cpu().numpy(), want) <= PARITY_TOL
+    x9 = torch.zeros(9, k, device="cuda")
+    with pytest.raises(HipError) as e:
+        eng.matvec_parts_rmsnorm([mat], [torch.zeros(9, m, device="cuda")], 9, x9, wd, 1e-5)
+    assert e.value.code == -2
+    eng.free(mat)

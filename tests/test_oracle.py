@@ -354,3 +354,23 @@ def test_simd_baseline_levels_match_oracle():
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), name
         ran.append(name)
     assert "generic" in ran and O.simd_level_name(O.simd_level()) == ran[0]
+
+
+def test_net_oracle_cache_consistency():
+    """The CPU network restatement gives the same last-token logits whether a sequence runs as one
+    prefill or token by token (its K/V cache carries the earlier positions), and the causal mask
+    makes a prefix's logits independent of what follows."""
+    from hk_amd.net import Config
+    from oracle.net_oracle import Oracle
+
+    cfg = Config(dim=256, n_layers=2, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=256, vocab=128, max_ctx=32)
+    model = synth.model_np(cfg, F.Q4_K, seed=77, out_fmt=F.Q6_K, embd_fmt=F.Q8_0)
+    toks = np.random.default_rng(78).integers(0, cfg.vocab, 9)
+    whole = Oracle(cfg, model).forward(toks, 0)
+    step = Oracle(cfg, model)
+    for i, tk in enumerate(toks):
+        last = step.forward([tk], i)
+    assert np.allclose(whole, last, rtol=0, atol=1e-4 * np.abs(whole).max())
+    part = Oracle(cfg, model)
+    part.forward(toks[:5], 0)
+    assert np.allclose(part.forward(toks[5:], 5), whole, rtol=0, atol=1e-4 * np.abs(whole).max())
