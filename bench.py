@@ -371,6 +371,7 @@ def main():
             for m in lw.values():
                 eng.free(m)
         eng.free(qhead)
+        extra["network_qwen3_0_6b"] = network_bench(torch, eng, F, synth)
         result["extra"] = extra
         phase("extra")
 
@@ -420,6 +421,43 @@ def main():
     }
     print(json.dumps(line), flush=True)
     eng.close()
+
+
+def network_bench(torch, eng, F, synth):
+    """The whole-network device pass (hk_amd.net) on a random Qwen3-0.6B-shaped model (config 2's
+    shapes: 28 layers, dim 1024, 16 query / 8 key-value heads of 128, q/k norms, FFN 3072, vocabulary
+    151936; Q4_K layers, Q6_K output and embedding): a 512-token prompt prefill, then 64 decode
+    passes of one token (one HIP graph replay each, positions 512..575), timed on the host clock
+    around each call (the call returns when its pass is done)."""
+    import numpy as np
+
+    from hk_amd.net import Config, Net
+
+    cfg = Config(dim=1024, n_layers=28, n_heads=16, n_kv_heads=8, head_dim=128, ffn_dim=3072, vocab=151936,
+                 max_ctx=2048, rope_neox=True, rope_base=1e6)
+    model = synth.model_np(cfg, F.Q4_K, seed=synth.seed_for(2, 500), out_fmt=F.Q6_K, embd_fmt=F.Q6_K)
+    rng = np.random.default_rng(7)
+    with Net(eng, cfg) as net:
+        net.load(model)
+        del model
+        prompt = rng.integers(0, cfg.vocab, 512)
+        net.forward(prompt, 0)  # warm-up (first GEMM launches)
+        t0 = time.perf_counter()
+        net.forward(prompt, 0)
+        pre_s = time.perf_counter() - t0
+        toks = rng.integers(0, cfg.vocab, 64)
+        for i in range(4):  # eager run, capture, replays
+            net.forward(toks[i:i + 1], 512 + i)
+        t0 = time.perf_counter()
+        for i in range(64):
+            net.forward(toks[i:i + 1], 512 + i)
+        dec_s = (time.perf_counter() - t0) / 64
+        ok = bool(np.isfinite(net.logits()).all())
+    return {"prefill_512_ms": round(pre_s * 1e3, 2), "prefill_tokens_per_s": round(512 / pre_s, 1),
+            "decode_ms_per_token": round(dec_s * 1e3, 3), "decode_tokens_per_s": round(1 / dec_s, 1),
+            "context": "positions 512-575", "finite_logits": ok,
+            "what": "whole network on the device: embedding, 28 layers (fused rmsnorm+qact products, rope, f16 KV "
+                    "cache, split-context attention), logits; host wall clock per forward call"}
 
 
 def measured_peaks():

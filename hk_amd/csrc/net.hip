@@ -33,7 +33,7 @@ using namespace hkhip;
 
 namespace {
 
-constexpr uint32_t ATT_SLICE = 256; // positions per attention slice
+constexpr uint32_t ATT_SLICE = 64; // positions per attention slice (one step of the kernel)
 constexpr uint32_t MAX_DECODE = 8;  // tokens of a pass that runs the decode kernels (and a graph)
 
 // ---------------------------------------------------------------------------------------------
@@ -125,59 +125,101 @@ __global__ __launch_bounds__(64) void rope_kv_kernel(RopeArgs a) {
     }
 }
 
-// Attention over one slice of the context for the `group` query heads of one key/value head and
-// one token: one wave per query head, 64 positions per step (lane = position for the scores,
-// lane = dimensions for the value sums), online softmax. Writes {max, sum, acc[hd]} per (token,
-// head, slice); a slice past the token's position writes {-inf, 0, 0...}.
+// Attention over one slice of the context for one (token, query head): one wave each, four per
+// workgroup. Per step of 64 positions every lane issues its position's key row (lane = position)
+// and its dimensions of all 64 value rows (lane = dimensions [DL*lane, DL*lane + DL)) before any
+// use, so a step costs one memory round trip; then the scores, the online softmax update and the
+// value sums from registers. Writes {max, sum, acc[hd]} per (token, head, slice); a slice past the
+// token's position writes {-inf, 0, 0...}.
 struct AttnArgs {
     const float *q;
     const __half *kc, *vc;
     float *part;
     const uint32_t *pos0;
-    uint32_t nh, nkv, hd, max_ctx, nslice;
+    uint32_t n, nh, nkv, hd, max_ctx, nslice;
     float scale;
 };
 
+// A lane's DL dimensions of one value row: DL halves in one (DL = 1: the low half) or two words.
+template <int DL> struct VRow {
+    uint32_t w[DL > 2 ? 2 : 1];
+    __device__ float get(int j) const {
+        const uint32_t b = DL == 1 ? w[0] : w[j >> 1] >> (16 * (j & 1));
+        return __half2float(__ushort_as_half(uint16_t(b & 0xFFFFu)));
+    }
+    __device__ void load(const __half *p) {
+        if constexpr (DL == 1)
+            w[0] = *reinterpret_cast<const uint16_t *>(p);
+        else if constexpr (DL == 2)
+            w[0] = *reinterpret_cast<const uint32_t *>(p);
+        else {
+            const uint2 u = *reinterpret_cast<const uint2 *>(p);
+            w[0] = u.x;
+            w[1] = u.y;
+        }
+    }
+    // Ties the loaded words to this point, so the compiler keeps the loads where they are issued
+    // (ahead of every use) instead of sinking each next to its use.
+    __device__ void pin() {
+#pragma unroll
+        for (int i = 0; i < (DL > 2 ? 2 : 1); i++) asm volatile("" : "+v"(w[i]));
+    }
+};
+
 template <int HD>
-__global__ __launch_bounds__(1024) void attn_slice_kernel(AttnArgs a) {
-    constexpr int DL = HD / 64; // dimensions per lane
-    const uint32_t t = blockIdx.y, kvh = blockIdx.x / a.nslice, sl = blockIdx.x % a.nslice;
+__global__ __launch_bounds__(256) void attn_slice_kernel(AttnArgs a) {
+    constexpr int DL = HD / 64;
     const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const uint32_t group = a.nh / a.nkv, h = kvh * group + w;
+    const uint32_t item = blockIdx.x * 4 + w; // (token, head, slice), slice fastest
+    __shared__ float qs[4][HD];
+    const bool live = item < a.n * a.nh * a.nslice;
+    const uint32_t sl = item % a.nslice, h = (item / a.nslice) % a.nh, t = item / (a.nslice * a.nh);
+    if (live) {
+        const float *qsrc = a.q + (uint64_t(t) * a.nh + h) * HD;
+#pragma unroll
+        for (int j = 0; j < DL; j++) qs[w][lane + 64 * j] = qsrc[lane + 64 * j];
+    }
+    __syncthreads();
+    if (!live) return;
+    const uint32_t kvh = h / (a.nh / a.nkv);
     const uint32_t pos = a.pos0[0] + t;
     const uint32_t p_begin = sl * ATT_SLICE;
     const uint32_t p_end = min(p_begin + ATT_SLICE, pos + 1); // exclusive
-    float *out = a.part + ((uint64_t(t) * a.nh + h) * a.nslice + sl) * (HD + 2);
-    extern __shared__ float qs[]; // [group][HD]
-    float *qw = qs + w * HD;
-    const float *qsrc = a.q + (uint64_t(t) * a.nh + h) * HD;
-#pragma unroll
-    for (int j = 0; j < DL; j++) qw[lane + 64 * j] = qsrc[lane + 64 * j];
-    __syncthreads();
+    float *out = a.part + (uint64_t(item)) * (HD + 2);
+    const float *qw = qs[w];
     float m = -INFINITY, l = 0.0f, acc[DL];
 #pragma unroll
     for (int j = 0; j < DL; j++) acc[j] = 0.0f;
     const __half *kb = a.kc + uint64_t(kvh) * a.max_ctx * HD;
-    const __half *vb = a.vc + uint64_t(kvh) * a.max_ctx * HD;
+    const __half *vb = a.vc + uint64_t(kvh) * a.max_ctx * HD + DL * lane;
     for (uint32_t p0 = p_begin; p0 < p_end; p0 += 64) {
-        const uint32_t pp = p0 + lane;
-        float s = -INFINITY;
-        if (pp < p_end) {
-            const uint4 *kr = reinterpret_cast<const uint4 *>(kb + uint64_t(pp) * HD);
-            float dot = 0.0f;
+        const uint32_t pp = p0 + lane, last = p_end - 1;
+        uint4 kr[HD / 8];
+        const uint4 *krow = reinterpret_cast<const uint4 *>(kb + uint64_t(pp < p_end ? pp : last) * HD);
 #pragma unroll
-            for (int c = 0; c < HD / 8; c++) {
-                const uint4 u = kr[c];
-                const __half2 *hp = reinterpret_cast<const __half2 *>(&u);
+        for (int c = 0; c < HD / 8; c++) kr[c] = krow[c];
+        VRow<DL> vr[64];
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const float2 f = __half22float2(hp[e]);
-                    dot = fmaf(qw[8 * c + 2 * e], f.x, dot);
-                    dot = fmaf(qw[8 * c + 2 * e + 1], f.y, dot);
-                }
-            }
-            s = dot * a.scale;
+        for (int i = 0; i < 64; i++) {
+            const uint32_t pv = p0 + i < p_end ? p0 + i : last;
+            vr[i].load(vb + uint64_t(pv) * HD);
         }
+#pragma unroll
+        for (int c = 0; c < HD / 8; c++) asm volatile("" : "+v"(kr[c].x), "+v"(kr[c].y), "+v"(kr[c].z), "+v"(kr[c].w));
+#pragma unroll
+        for (int i = 0; i < 64; i++) vr[i].pin();
+        float dot = 0.0f;
+#pragma unroll
+        for (int c = 0; c < HD / 8; c++) {
+            const __half2 *hp = reinterpret_cast<const __half2 *>(&kr[c]);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float2 f = __half22float2(hp[e]);
+                dot = fmaf(qw[8 * c + 2 * e], f.x, dot);
+                dot = fmaf(qw[8 * c + 2 * e + 1], f.y, dot);
+            }
+        }
+        const float s = pp < p_end ? dot * a.scale : -INFINITY;
         float mx = s;
         for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
         const float mn = fmaxf(m, mx);
@@ -188,12 +230,11 @@ __global__ __launch_bounds__(1024) void attn_slice_kernel(AttnArgs a) {
         l = l * corr + ps;
 #pragma unroll
         for (int j = 0; j < DL; j++) acc[j] *= corr;
-        const uint32_t cnt = p_end - p0 < 64 ? p_end - p0 : 64;
-        for (uint32_t i = 0; i < cnt; i++) {
-            const float pi = __shfl(pr, int(i));
-            const __half *vr = vb + uint64_t(p0 + i) * HD;
 #pragma unroll
-            for (int j = 0; j < DL; j++) acc[j] = fmaf(pi, __half2float(vr[lane + 64 * j]), acc[j]);
+        for (int i = 0; i < 64; i++) {
+            const float pi = __shfl(pr, i); // 0 for positions past the slice
+#pragma unroll
+            for (int j = 0; j < DL; j++) acc[j] = fmaf(pi, vr[i].get(j), acc[j]);
         }
         m = mn;
     }
@@ -202,26 +243,48 @@ __global__ __launch_bounds__(1024) void attn_slice_kernel(AttnArgs a) {
         out[1] = l;
     }
 #pragma unroll
-    for (int j = 0; j < DL; j++) out[2 + lane + 64 * j] = acc[j];
+    for (int j = 0; j < DL; j++) out[2 + DL * lane + j] = acc[j];
 }
 
-// att[t][h*hd..] = merge of the slices' partials (attention.zig:113-133 merge).
+// att[t][h*hd..] = merge of the slices' partials (attention.zig:113-133 merge): every thread
+// reads one slice's {max, sum} (all loads in flight at once), the block reduces them, the weights
+// exp(m_s - max m) of the non-empty slices go to LDS, then thread d sums its dimension over the
+// slices with the loads of eight slices issued together.
 __global__ __launch_bounds__(256) void attn_combine_kernel(const float *__restrict__ part, float *__restrict__ att,
                                                            uint32_t nh, uint32_t hd, uint32_t nslice) {
+    extern __shared__ float wts[]; // [nslice]
+    __shared__ float red[4];
     const uint32_t t = blockIdx.y, h = blockIdx.x;
     const float *p = part + (uint64_t(t) * nh + h) * nslice * (hd + 2);
     float big = -INFINITY;
-    for (uint32_t s = 0; s < nslice; s++)
+    for (uint32_t s = threadIdx.x; s < nslice; s += blockDim.x)
         if (p[s * (hd + 2) + 1] != 0.0f) big = fmaxf(big, p[s * (hd + 2)]);
-    float total = 0.0f;
-    for (uint32_t s = 0; s < nslice; s++)
-        if (p[s * (hd + 2) + 1] != 0.0f) total += expf(p[s * (hd + 2)] - big) * p[s * (hd + 2) + 1];
-    const float inv = 1.0f / total;
+    for (int o = 32; o >= 1; o >>= 1) big = fmaxf(big, __shfl_xor(big, o));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = big;
+    __syncthreads();
+    big = red[0];
+    for (uint32_t i = 1; i < (blockDim.x >> 6); i++) big = fmaxf(big, red[i]);
+    float tot = 0.0f;
+    for (uint32_t s = threadIdx.x; s < nslice; s += blockDim.x) {
+        const float l = p[s * (hd + 2) + 1];
+        const float wgt = l != 0.0f ? expf(p[s * (hd + 2)] - big) : 0.0f;
+        wts[s] = wgt;
+        tot = fmaf(wgt, l, tot);
+    }
+    tot = block_sum(tot, red);
+    const float inv = 1.0f / tot;
     float *o = att + (uint64_t(t) * nh + h) * hd;
     for (uint32_t d = threadIdx.x; d < hd; d += blockDim.x) {
         float v = 0.0f;
-        for (uint32_t s = 0; s < nslice; s++)
-            if (p[s * (hd + 2) + 1] != 0.0f) v += expf(p[s * (hd + 2)] - big) * p[s * (hd + 2) + 2 + d];
+        uint32_t s = 0;
+        for (; s + 8 <= nslice; s += 8) {
+            float pv[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) pv[i] = p[(s + i) * (hd + 2) + 2 + d];
+#pragma unroll
+            for (int i = 0; i < 8; i++) v = fmaf(wts[s + i], pv[i], v);
+        }
+        for (; s < nslice; s++) v = fmaf(wts[s], p[s * (hd + 2) + 2 + d], v);
         o[d] = v * inv;
     }
 }
@@ -258,7 +321,8 @@ struct hkhip_net {
           *h = nullptr, *part = nullptr, *logits = nullptr, *inv_freq = nullptr;
     uint8_t *xq = nullptr;
     __half *kc = nullptr, *vc = nullptr;
-    uint32_t *tok = nullptr, *pos = nullptr;
+    uint32_t *io = nullptr, *tok = nullptr, *pos = nullptr; // device {pos, tokens[cap]}
+    uint32_t *stage = nullptr;                               // pinned host copy of io
     std::map<uint32_t, hipGraphExec_t> graphs;
     std::map<uint32_t, int> runs; // eager runs per decode token count (a graph is captured after one)
     uint32_t last_n = 0;
@@ -317,7 +381,11 @@ int ensure_cap(hkhip_net *n, uint32_t want) {
     n->graphs.clear();
     n->runs.clear();
     float **bufs[] = {&n->x, &n->xb, &n->q, &n->k, &n->v, &n->att, &n->gu, &n->h, &n->part,
-                      reinterpret_cast<float **>(&n->tok)};
+                      reinterpret_cast<float **>(&n->io)};
+    if (n->stage) {
+        (void)hipHostFree(n->stage);
+        n->stage = nullptr;
+    }
     for (float **b : bufs) {
         if (*b) {
             (void)hipFree(*b);
@@ -341,8 +409,11 @@ int ensure_cap(hkhip_net *n, uint32_t want) {
         (rc = dev_alloc(n, T * 2 * c.ffn_dim * 4, (void **)&n->gu)) || (rc = dev_alloc(n, T * c.ffn_dim * 4, (void **)&n->h)) ||
         (rc = dev_alloc(n, T * c.n_heads * nslices(c) * (c.head_dim + 2) * 4, (void **)&n->part)) ||
         (rc = dev_alloc(n, hkhip_act_bytes(want, maxk), (void **)&n->xq)) ||
-        (rc = dev_alloc(n, T * 4, (void **)&n->tok)))
+        (rc = dev_alloc(n, (T + 1) * 4, (void **)&n->io)))
         return rc;
+    n->pos = n->io;
+    n->tok = n->io + 1;
+    NET_TRY(hipHostMalloc(reinterpret_cast<void **>(&n->stage), (T + 1) * 4, hipHostMallocDefault), "hipHostMalloc");
     n->cap = want;
     return HKHIP_OK;
 }
@@ -395,18 +466,17 @@ int run_pass(hkhip_net *net, uint32_t n) {
                     c.rope_neox, c.max_ctx, c.rms_eps};
         hipLaunchKernelGGL(rope_kv_kernel, dim3(c.n_heads + 2 * c.n_kv_heads, n), dim3(64), 0, s, ra);
         NET_TRY(hipGetLastError(), "rope / kv write");
-        AttnArgs aa{net->q, net->kc + li * cache_layer, net->vc + li * cache_layer, net->part, net->pos, c.n_heads,
+        AttnArgs aa{net->q, net->kc + li * cache_layer, net->vc + li * cache_layer, net->part, net->pos, n, c.n_heads,
                     c.n_kv_heads, c.head_dim, c.max_ctx, ns, 1.0f / sqrtf(float(c.head_dim))};
-        const dim3 ag(c.n_kv_heads * ns, n), ab(64 * (c.n_heads / c.n_kv_heads));
-        const uint32_t alds = (c.n_heads / c.n_kv_heads) * c.head_dim * 4;
+        const dim3 ag((n * c.n_heads * ns + 3) / 4), ab(256);
         switch (c.head_dim) {
-        case 64: hipLaunchKernelGGL(attn_slice_kernel<64>, ag, ab, alds, s, aa); break;
-        case 128: hipLaunchKernelGGL(attn_slice_kernel<128>, ag, ab, alds, s, aa); break;
-        case 256: hipLaunchKernelGGL(attn_slice_kernel<256>, ag, ab, alds, s, aa); break;
+        case 64: hipLaunchKernelGGL(attn_slice_kernel<64>, ag, ab, 0, s, aa); break;
+        case 128: hipLaunchKernelGGL(attn_slice_kernel<128>, ag, ab, 0, s, aa); break;
+        case 256: hipLaunchKernelGGL(attn_slice_kernel<256>, ag, ab, 0, s, aa); break;
         default: return set_error(HKHIP_E_UNSUPPORTED_SHAPE, "head_dim %u", c.head_dim);
         }
         NET_TRY(hipGetLastError(), "attention");
-        hipLaunchKernelGGL(attn_combine_kernel, dim3(c.n_heads, n), dim3(128), 0, s, net->part, net->att, c.n_heads,
+        hipLaunchKernelGGL(attn_combine_kernel, dim3(c.n_heads, n), dim3(std::min(256u, std::max(64u, (c.head_dim + 63) / 64 * 64))), ns * 4, s, net->part, net->att, c.n_heads,
                            c.head_dim, ns);
         NET_TRY(hipGetLastError(), "attention combine");
         {
@@ -447,7 +517,6 @@ int hkhip_net_create(hkhip_engine *eng, const hkhip_net_config *cfg, hkhip_net *
         return set_error(HKHIP_E_BAD_ARGUMENT, "bad network shape");
     if (c.head_dim != 64 && c.head_dim != 128 && c.head_dim != 256)
         return set_error(HKHIP_E_UNSUPPORTED_SHAPE, "head_dim %u: 64, 128 or 256", c.head_dim);
-    if (c.n_heads / c.n_kv_heads > 16) return set_error(HKHIP_E_UNSUPPORTED_SHAPE, "at most 16 query heads per kv head");
     if (c.rope_dim % 2 || c.rope_dim > c.head_dim) return set_error(HKHIP_E_BAD_ARGUMENT, "rope_dim %u", c.rope_dim);
     if (hipSetDevice(eng->device) != hipSuccess) return set_error(HKHIP_E_DEVICE_FAILED, "hipSetDevice");
     hkhip_net *n = new hkhip_net();
@@ -458,7 +527,6 @@ int hkhip_net_create(hkhip_engine *eng, const hkhip_net_config *cfg, hkhip_net *
     const uint64_t cache = uint64_t(c.n_layers) * c.n_kv_heads * c.max_ctx * c.head_dim * 2;
     if ((rc = dev_alloc(n, cache, (void **)&n->kc)) || (rc = dev_alloc(n, cache, (void **)&n->vc)) ||
         (rc = dev_alloc(n, uint64_t(c.vocab) * 4, (void **)&n->logits)) ||
-        (rc = dev_alloc(n, 4, (void **)&n->pos)) ||
         (rc = dev_alloc(n, c.rope_dim / 2 * 4 + 4, (void **)&n->inv_freq)) || (rc = ensure_cap(n, MAX_DECODE))) {
         hkhip_net_destroy(n);
         return rc;
@@ -488,6 +556,7 @@ void hkhip_net_destroy(hkhip_net *net) {
     hkhip_free(net->eng, &net->output);
     for (void *p : net->owned)
         if (p) (void)hipFree(p);
+    if (net->stage) (void)hipHostFree(net->stage);
     delete net;
 }
 
@@ -557,16 +626,19 @@ int hkhip_net_forward(hkhip_net *net, const uint32_t *tokens, uint32_t n, uint32
     if ((rc = ensure_cap(net, n))) return rc;
     if (n > MAX_DECODE) { // prefill: run directly
         hipStream_t s = net->eng->cur;
-        NET_TRY(hipMemcpyAsync(net->tok, tokens, n * 4, hipMemcpyHostToDevice, s), "tokens");
-        NET_TRY(hipMemcpyAsync(net->pos, &pos0, 4, hipMemcpyHostToDevice, s), "position");
+        net->stage[0] = pos0;
+        memcpy(net->stage + 1, tokens, n * 4);
+        NET_TRY(hipMemcpyAsync(net->io, net->stage, (n + 1) * 4, hipMemcpyHostToDevice, s), "tokens");
         if ((rc = run_pass(net, n))) return rc;
         NET_TRY(hipStreamSynchronize(s), "prefill pass");
         net->last_n = n;
         return HKHIP_OK;
     }
     hipStream_t s = net->eng->cur;
-    NET_TRY(hipMemcpyAsync(net->tok, tokens, n * 4, hipMemcpyHostToDevice, s), "tokens");
-    NET_TRY(hipMemcpyAsync(net->pos, &pos0, 4, hipMemcpyHostToDevice, s), "position");
+    // One copy of {position, tokens} from pinned memory; the pass reads both from the device.
+    net->stage[0] = pos0;
+    memcpy(net->stage + 1, tokens, n * 4);
+    NET_TRY(hipMemcpyAsync(net->io, net->stage, (n + 1) * 4, hipMemcpyHostToDevice, s), "tokens");
     auto it = net->graphs.find(n);
     if (it != net->graphs.end()) {
         NET_TRY(hipGraphLaunch(it->second, s), "graph launch");
@@ -589,7 +661,7 @@ int hkhip_net_forward(hkhip_net *net, const uint32_t *tokens, uint32_t n, uint32
         net->graphs[n] = ex;
         NET_TRY(hipGraphLaunch(ex, s), "graph launch");
     }
-    // The host arrays the copies read are the caller's: wait for them before returning.
+    // The pass is done when forward returns (the next call reuses the pinned staging buffer).
     NET_TRY(hipStreamSynchronize(s), "pass");
     net->last_n = n;
     return HKHIP_OK;
