@@ -24,20 +24,42 @@ constexpr uint32_t QK_K = 256;
 
 inline uint64_t align256(uint64_t x) { return (x + 255) & ~uint64_t(255); }
 
-// Block geometry in hk's file layout (src/quant/blocks.zig:17-34).
-inline int block_elems(int t) {
+// The formats whose products decode the weights to floats (fallback.hip).
+__host__ __device__ constexpr bool fallback_type(int t) {
+    return t == HKHIP_Q2_K || t == HKHIP_Q3_K || t == HKHIP_IQ2_XXS || t == HKHIP_IQ2_XS || t == HKHIP_IQ2_S ||
+           t == HKHIP_IQ3_XXS || t == HKHIP_IQ3_S || t == HKHIP_IQ1_S || t == HKHIP_IQ1_M || t == HKHIP_TQ1_0 ||
+           t == HKHIP_TQ2_0 || t == HKHIP_MXFP4 || t == HKHIP_NVFP4;
+}
+
+// Block geometry in hk's file layout (src/quant/blocks.zig:13-40).
+__host__ __device__ inline int block_elems(int t) {
     switch (t) {
     case HKHIP_Q8_0: case HKHIP_IQ4_NL: case HKHIP_Q4_0: case HKHIP_Q4_1: case HKHIP_Q5_0: case HKHIP_Q5_1:
+    case HKHIP_MXFP4:
         return 32;
+    case HKHIP_NVFP4: return 64;
     case HKHIP_Q4_K: case HKHIP_Q5_K: case HKHIP_Q6_K: case HKHIP_IQ4_XS: return 256;
-    default: return 0;
+    default: return fallback_type(t) ? 256 : 0;
     }
 }
 __host__ __device__ inline int block_bytes_dev(int t) {
     return t == HKHIP_Q4_0 ? 18 : t == HKHIP_Q4_1 ? 20 : t == HKHIP_Q5_0 ? 22 : t == HKHIP_Q5_1 ? 24 : 0;
 }
-inline int block_bytes(int t) {
+__host__ __device__ inline int block_bytes(int t) {
     switch (t) {
+    case HKHIP_Q2_K: return 84;
+    case HKHIP_Q3_K: return 110;
+    case HKHIP_IQ2_XXS: return 66;
+    case HKHIP_IQ2_XS: return 74;
+    case HKHIP_IQ2_S: return 82;
+    case HKHIP_IQ3_XXS: return 98;
+    case HKHIP_IQ3_S: return 110;
+    case HKHIP_IQ1_S: return 50;
+    case HKHIP_IQ1_M: return 56;
+    case HKHIP_TQ1_0: return 54;
+    case HKHIP_TQ2_0: return 66;
+    case HKHIP_MXFP4: return 17;
+    case HKHIP_NVFP4: return 36;
     case HKHIP_Q8_0: return 34;
     case HKHIP_IQ4_NL: return 18;
     case HKHIP_Q4_K: return 144;
@@ -52,7 +74,10 @@ inline int block_bytes(int t) {
     }
 }
 // vecdot.zig:185-191
-inline int act_kind(int t) { return block_elems(t) == 32 ? HKHIP_ACT_A8 : HKHIP_ACT_Q8K; }
+inline int act_kind(int t) {
+    if (t == HKHIP_NVFP4) return HKHIP_ACT_F32;
+    return block_elems(t) == 32 ? HKHIP_ACT_A8 : HKHIP_ACT_Q8K;
+}
 // The 32-weight formats (A8 activations).
 __host__ __device__ constexpr bool legacy32(int t) {
     return t == HKHIP_Q8_0 || t == HKHIP_IQ4_NL || t == HKHIP_Q4_0 || t == HKHIP_Q4_1 || t == HKHIP_Q5_0 ||
@@ -103,8 +128,9 @@ inline WLayout weight_layout(int t, uint32_t rows, uint32_t cols) {
     case HKHIP_Q5_K: L.qblock = 176; break;
     case HKHIP_IQ4_XS: L.qblock = 128; break;
     }
+    if (fallback_type(t)) L.qblock = uint32_t(block_bytes(t)); // file layout, no planes
     L.quant_bytes = nb * L.qblock;
-    if (t == HKHIP_Q4_K || t == HKHIP_Q5_K) {
+    if (t == HKHIP_Q4_K || t == HKHIP_Q5_K || fallback_type(t)) {
         L.scale_off = L.quant_bytes;
         L.total = L.quant_bytes;
     } else {
@@ -247,6 +273,15 @@ hipError_t launch_dequant(int t, const uint8_t *w, uint32_t rows, uint32_t cols,
 // Rows ids[0..n) (device array; each below rows) decoded to out [n][cols] (embedding lookup).
 hipError_t launch_dequant_gather(int t, const uint8_t *w, uint32_t rows, uint32_t cols, const uint32_t *ids, uint32_t n,
                                  float *out, hipStream_t s);
+
+// fallback.hip: the float-decode formats (fallback_type): bit-exact decode of rows (or of rows
+// ids[] when ids is not null) and the decode-based products for 1..8 tokens of an f32 input (x)
+// or of a prepared activation buffer (xq; not NVFP4, whose products take f32 inputs).
+hipError_t launch_fb_dequant(int t, const uint8_t *w, uint32_t cols, uint32_t row0, const uint32_t *ids, uint32_t nrows,
+                             float *out, hipStream_t s);
+struct MvPartDesc;
+hipError_t launch_fb_mv(int t, const MvPartDesc *parts, int nparts, uint32_t K, const float *x, const uint8_t *xq,
+                        uint32_t n, int mode, hipStream_t s);
 hipError_t launch_qact(const float *x, uint32_t n, uint32_t k, int kind, uint8_t *xq, hipStream_t s);
 hipError_t launch_act_pack(const uint8_t *xq, uint32_t n, uint32_t k, int kind, uint8_t *out, hipStream_t s);
 // One matrix of a fused decode launch (all parts share cols and the input).

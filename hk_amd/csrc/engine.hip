@@ -205,7 +205,7 @@ int hkhip_upload(hkhip_engine *eng, const void *src, uint64_t bytes, uint8_t t, 
     void *mem = nullptr;
     HIP_TRY(hipMalloc(&mem, L.total ? L.total : 1), "hipMalloc weights");
     hipError_t e = hipSuccess;
-    if (t == HKHIP_Q4_K || t == HKHIP_Q5_K) { // device layout = file layout
+    if (t == HKHIP_Q4_K || t == HKHIP_Q5_K || fallback_type(t)) { // device layout = file layout
         e = hipMemcpyAsync(mem, src, need, src_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, eng->cur);
     } else {
         const uint8_t *staged = reinterpret_cast<const uint8_t *>(src);
@@ -292,15 +292,24 @@ static int check_product(const hkhip_mat *m, const void *xq, float *y, uint32_t 
         return fail(HKHIP_E_BAD_ARGUMENT, "unknown mode %d", mode);
     if (mode == HKHIP_SILU_MUL && (m->rows % 2 || n > 8))
         return fail(HKHIP_E_BAD_ARGUMENT, "silu(gate)*up needs interleaved gate/up rows (even count) and n <= 8");
-    if (act_kind(m->t) == HKHIP_ACT_Q8K && m->cols % QK_K) return fail(HKHIP_E_UNSUPPORTED_SHAPE, "bad cols");
+    if ((act_kind(m->t) == HKHIP_ACT_Q8K || fallback_type(m->t)) && m->cols % QK_K)
+        return fail(HKHIP_E_UNSUPPORTED_SHAPE, "cols %u: the products of this type take whole 256-value groups", m->cols);
     if (n && (!xq || !y)) return fail(HKHIP_E_BAD_ARGUMENT, "null buffer");
+    return HKHIP_OK;
+}
+
+// NVFP4 is dotted against the f32 input itself (vecdot.zig:189): no prepared buffer holds it.
+static int check_prepared(const hkhip_mat *m) {
+    if (act_kind(m->t) == HKHIP_ACT_F32)
+        return fail(HKHIP_E_UNSUPPORTED_TYPE, "type 0x%02x takes an f32 input: use hkhip_matvec_parts with x, "
+                                              "hkhip_mm_noalloc or hkhip_gemm_host", m->t);
     return HKHIP_OK;
 }
 
 int hkhip_matvec(hkhip_engine *eng, const hkhip_mat *m, const void *xq_dev, float *y_dev, uint32_t n,
                  const float *bias_dev, int mode) {
     int rc = enter(eng);
-    if (rc || (rc = check_product(m, xq_dev, y_dev, n, mode))) return rc;
+    if (rc || (rc = check_product(m, xq_dev, y_dev, n, mode)) || (rc = check_prepared(m))) return rc;
     if (n > 8) return fail(HKHIP_E_UNSUPPORTED_SHAPE, "matvec takes at most 8 tokens, got %u", n);
     if (mode == HKHIP_SILU_MUL && bias_dev) return fail(HKHIP_E_BAD_ARGUMENT, "silu(gate)*up takes no bias");
     if (n == 0) return HKHIP_OK;
@@ -362,7 +371,7 @@ int hkhip_matvec_parts_rmsnorm(hkhip_engine *eng, const hkhip_mat *mats, uint32_
 int hkhip_gemm(hkhip_engine *eng, const hkhip_mat *m, const void *xq_dev, float *y_dev, uint32_t n,
                const float *bias_dev, int mode) {
     int rc = enter(eng);
-    if (rc || (rc = check_product(m, xq_dev, y_dev, n, mode))) return rc;
+    if (rc || (rc = check_product(m, xq_dev, y_dev, n, mode)) || (rc = check_prepared(m))) return rc;
     if (mode == HKHIP_SILU_MUL) return fail(HKHIP_E_BAD_ARGUMENT, "silu(gate)*up is a decode mode (hkhip_matvec)");
     if (n == 0) return HKHIP_OK;
     if ((n + 63) / 64 > 65535u) return fail(HKHIP_E_UNSUPPORTED_SHAPE, "too many tokens: %u", n);
@@ -397,7 +406,7 @@ int hkhip_mm(hkhip_engine *eng, const hkhip_mat *m, const void *xq_dev, float *y
     if (n <= 8) return hkhip_matvec(eng, m, xq_dev, y_dev, n, bias_dev, mode);
     if (n >= gemm_min_tokens(m->t, m->rows)) return hkhip_gemm(eng, m, xq_dev, y_dev, n, bias_dev, mode);
     int rc = enter(eng);
-    if (rc || (rc = check_product(m, xq_dev, y_dev, n, mode))) return rc;
+    if (rc || (rc = check_product(m, xq_dev, y_dev, n, mode)) || (rc = check_prepared(m))) return rc;
     HIP_TRY(launch_mmvq(m->t, reinterpret_cast<const uint8_t *>(m->mem), m->rows, m->cols,
                         reinterpret_cast<const uint8_t *>(xq_dev), n, y_dev, bias_dev, mode, eng->cur), "mmvq launch");
     return HKHIP_OK;
@@ -413,6 +422,11 @@ int hkhip_mm_noalloc(hkhip_engine *eng, const hkhip_mat *m, const float *x_dev, 
         return fail(HKHIP_E_UNSUPPORTED_SHAPE,
                     "hkhip_mm_noalloc: %u tokens x %u cols need %llu bytes of activation buffer, over its %llu",
                     n, m->cols, (unsigned long long)need, (unsigned long long)HKHIP_NOALLOC_SCRATCH_BYTES);
+    if (act_kind(m->t) == HKHIP_ACT_F32) { // dotted against the f32 input: no buffer needed
+        MvPartDesc p{reinterpret_cast<const uint8_t *>(m->mem), y_dev, bias_dev, m->rows};
+        HIP_TRY(launch_fb_mv(m->t, &p, 1, m->cols, x_dev, nullptr, n, mode, eng->cur), "mmvq launch");
+        return HKHIP_OK;
+    }
     void *xq = g_scratch_ptr[eng->device]; // set by hkhip_init for this engine's device
     if (!xq) return fail(HKHIP_E_DEVICE_FAILED, "no activation buffer for device %d", eng->device);
     if ((rc = hkhip_qact(eng, x_dev, n, m->cols, act_kind(m->t), xq))) return rc;
@@ -459,9 +473,19 @@ int hkhip_gemm_host(uint8_t t, const void *w, const float *x, const float *bias,
     if (!rc && bias) rc = hkhip_alloc(eng, m * 4, &db);
     if (!rc) rc = hkhip_copy_h2d(eng, dx, x, xbytes);
     if (!rc && bias) rc = hkhip_copy_h2d(eng, db, bias, m * 4);
-    if (!rc) rc = hkhip_qact(eng, reinterpret_cast<float *>(dx), uint32_t(n), uint32_t(k), act_kind(t), dq);
-    if (!rc) rc = hkhip_mm(eng, &mat, dq, reinterpret_cast<float *>(dy), uint32_t(n), reinterpret_cast<float *>(db),
-                           HKHIP_STORE);
+    if (act_kind(t) == HKHIP_ACT_F32) { // products on the f32 input itself, 8 tokens per pass
+        for (uint64_t t0 = 0; !rc && t0 < n; t0 += 8) {
+            const uint32_t nc = uint32_t(n - t0 < 8 ? n - t0 : 8);
+            float *yc = reinterpret_cast<float *>(dy) + t0 * m;
+            const float *bc = reinterpret_cast<float *>(db);
+            rc = hkhip_matvec_parts(eng, &mat, 1, reinterpret_cast<float *>(dx) + t0 * k, nullptr, nc, &yc, &bc,
+                                    HKHIP_STORE);
+        }
+    } else {
+        if (!rc) rc = hkhip_qact(eng, reinterpret_cast<float *>(dx), uint32_t(n), uint32_t(k), act_kind(t), dq);
+        if (!rc) rc = hkhip_mm(eng, &mat, dq, reinterpret_cast<float *>(dy), uint32_t(n), reinterpret_cast<float *>(db),
+                               HKHIP_STORE);
+    }
     if (!rc) rc = hkhip_copy_d2h(eng, y, dy, ybytes);
     hkhip_free(eng, &mat);
     hkhip_dev_free(eng, dx);

@@ -284,6 +284,7 @@ __global__ __launch_bounds__(256) void mm_kernel(MmArgs a) {
 hipError_t launch_mm(int t, const uint8_t *w, uint32_t rows, uint32_t cols, const uint8_t *xq, uint32_t n,
                      float *y, const float *bias, int mode, hipStream_t s) {
     if (rows == 0 || n == 0) return hipSuccess;
+    if (fallback_type(t)) return launch_mmvq(t, w, rows, cols, xq, n, y, bias, mode, s); // decode passes of 8
     // Few tokens: the weights dominate, so the kernel that streams them (small-batch MFMA); many:
     // the tiled GEMM.
     if (n >= SK_MIN_TOKENS && mmsk_supports(t, rows, cols, n)) return launch_mmsk(t, w, rows, cols, xq, n, y, bias, mode, s);

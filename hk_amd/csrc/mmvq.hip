@@ -299,6 +299,7 @@ hipError_t launch_mmvq_parts_norm(int t, const MvPartDesc *parts, int nparts, ui
                                   hipStream_t s) {
     if (n < 1 || nparts < 1 || nparts > MV_PARTS) return hipErrorInvalidValue;
     if (norm && !x) return hipErrorNotSupported;
+    if (fallback_type(t)) return norm ? hipErrorNotSupported : launch_fb_mv(t, parts, nparts, K, x, xq, n, mode, s);
     const bool kq = act_kind(t) == HKHIP_ACT_Q8K;
     // Q4_K and Q6_K from 4 tokens with a prepared input: the small-batch MFMA kernel (it needs the
     // quantizer's token-interleaved planes, so not for an f32 input).

@@ -438,6 +438,17 @@ int product(hkhip_net *net, uint32_t n, const hkhip_mat *mats, uint32_t nparts, 
         NET_TRY(hipGetLastError(), "rmsnorm");
         xin = net->xb;
     }
+    if (act_kind(mats[0].t) == HKHIP_ACT_F32) { // dotted against the f32 input: passes of 8 tokens
+        int rc = HKHIP_OK;
+        for (uint32_t t0 = 0; !rc && t0 < n; t0 += MAX_DECODE) {
+            const uint32_t nc = n - t0 < MAX_DECODE ? n - t0 : MAX_DECODE;
+            float *yc[4];
+            for (uint32_t i = 0; i < nparts; i++)
+                yc[i] = ys[i] + uint64_t(t0) * (mode == HKHIP_SILU_MUL ? mats[i].rows / 2 : mats[i].rows);
+            rc = hkhip_matvec_parts(eng, mats, nparts, xin + uint64_t(t0) * cols, nullptr, nc, yc, biases, mode);
+        }
+        return rc;
+    }
     int rc = hkhip_qact(eng, xin, n, cols, act_kind(mats[0].t), net->xq);
     for (uint32_t i = 0; !rc && i < nparts; i++)
         rc = hkhip_mm(eng, &mats[i], net->xq, ys[i], n, biases ? biases[i] : nullptr, mode);

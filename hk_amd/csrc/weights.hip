@@ -172,6 +172,7 @@ __global__ void dequant_kernel(int t, const uint8_t *__restrict__ w, uint32_t co
 
 hipError_t launch_dequant(int t, const uint8_t *w, uint32_t rows, uint32_t cols, uint32_t row0, uint32_t nrows,
                           float *out, hipStream_t s) {
+    if (fallback_type(t)) return launch_fb_dequant(t, w, cols, row0, nullptr, nrows, out, s);
     WLayout L = weight_layout(t, rows, cols);
     uint64_t total = uint64_t(nrows) * cols;
     if (total == 0) return hipSuccess;
@@ -183,6 +184,7 @@ hipError_t launch_dequant(int t, const uint8_t *w, uint32_t rows, uint32_t cols,
 
 hipError_t launch_dequant_gather(int t, const uint8_t *w, uint32_t rows, uint32_t cols, const uint32_t *ids, uint32_t n,
                                  float *out, hipStream_t s) {
+    if (fallback_type(t)) return launch_fb_dequant(t, w, cols, 0, ids, n, out, s);
     WLayout L = weight_layout(t, rows, cols);
     uint64_t total = uint64_t(n) * cols;
     if (total == 0) return hipSuccess;

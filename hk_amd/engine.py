@@ -138,7 +138,7 @@ class Engine:
     def prepare(self, x, n: int, k: int, mats, xq) -> None:
         """Quantizes x [n][k] once for every kind the products in `mats` read
         (prepare: cuda/engine.zig:614-630; Cpu.prepare: cpu_backend.zig:214-225)."""
-        for kind in sorted({formats.ACT_KIND[m.t] for m in mats}):
+        for kind in sorted({formats.ACT_KIND[m.t] for m in mats} - {formats.ACT_F32}):
             self.qact(x, n, k, kind, xq)
 
     def act_export(self, xq, n: int, k: int, kind: int) -> np.ndarray:

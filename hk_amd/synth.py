@@ -51,6 +51,17 @@ def weights_np(t: int, rows: int, cols: int, seed: int) -> np.ndarray:
         raw[:, 208:210] = _f16_scales_np(rng, nb, 127.0).view(np.uint8).reshape(nb, 2)
     elif t == formats.IQ4_NL:
         raw[:, 0:2] = _f16_scales_np(rng, nb, 1.0).view(np.uint8).reshape(nb, 2)
+    elif t in _FB_D:
+        for off, div in _FB_D[t]:
+            raw[:, off:off + 2] = _f16_scales_np(rng, nb, div).view(np.uint8).reshape(nb, 2)
+    elif t == formats.IQ1_M:
+        # the f16 scale is the top nibbles of the four 16-bit scale words (bytes 48..55)
+        bits = _f16_scales_np(rng, nb, 1.0).view(np.uint16).astype(np.uint32)
+        for i in range(4):
+            hi = (bits >> (4 * i)) & 0xF
+            raw[:, 49 + 2 * i] = (raw[:, 49 + 2 * i] & 0x0F) | (hi << 4).astype(np.uint8)
+    elif t == formats.MXFP4:
+        raw[:, 0] = rng.integers(118, 126, size=nb)  # E8M0 exponents around 2^-4 .. 2^-9
     elif t in _LOW_BIT:
         div, has_m = _LOW_BIT[t]
         raw[:, 0:2] = _f16_scales_np(rng, nb, div).view(np.uint8).reshape(nb, 2)
@@ -58,6 +69,12 @@ def weights_np(t: int, rows: int, cols: int, seed: int) -> np.ndarray:
             raw[:, 2:4] = (-_f16_scales_np(rng, nb, 1.0)).view(np.uint8).reshape(nb, 2)
     return raw.reshape(rows, -1)
 
+
+# The float-decode formats' f16 scale fields: (byte offset, divisor of |N(0, 0.02)|).
+_FB_D = {formats.Q2_K: ((80, 1.0), (82, 1.0)), formats.Q3_K: ((108, 1.0),), formats.IQ2_XXS: ((0, 1.0),),
+         formats.IQ2_XS: ((0, 1.0),), formats.IQ2_S: ((0, 1.0),), formats.IQ3_XXS: ((0, 1.0),),
+         formats.IQ3_S: ((0, 1.0),), formats.IQ1_S: ((0, 1.0),), formats.TQ1_0: ((52, 1.0),),
+         formats.TQ2_0: ((64, 1.0),)}
 
 # Q4_0 / Q4_1 / Q5_0 / Q5_1: scale divisor, has an offset m (f16 at bytes 2..3).
 _LOW_BIT = {formats.Q4_0: (8.0, False), formats.Q4_1: (16.0, True), formats.Q5_0: (16.0, False),

@@ -40,10 +40,27 @@ extern "C" {
 #define HKHIP_Q6_K 0x44
 #define HKHIP_IQ4_NL 0x55
 #define HKHIP_IQ4_XS 0x56
+/* Formats whose products decode the weights to floats first, hk's "exact fallback" (vecdot.zig
+ * dotCanonK / dotCanonLegacy / dotGeneric): upload, bit-exact decode and products (1..8 tokens per
+ * decode pass; longer inputs in passes), no MFMA GEMM (src/format.zig:71-93). */
+#define HKHIP_Q2_K 0x40
+#define HKHIP_Q3_K 0x41
+#define HKHIP_IQ1_S 0x50
+#define HKHIP_IQ1_M 0x51
+#define HKHIP_IQ2_XXS 0x52
+#define HKHIP_IQ2_XS 0x53
+#define HKHIP_IQ3_XXS 0x54
+#define HKHIP_IQ2_S 0x57
+#define HKHIP_IQ3_S 0x58
+#define HKHIP_TQ1_0 0x60
+#define HKHIP_TQ2_0 0x61
+#define HKHIP_MXFP4 0x62
+#define HKHIP_NVFP4 0x63 /* dotted against the f32 input (vecdot.zig:189): products need x, not xq */
 
 /* Activation kinds (src/quant/vecdot.zig:183-191 ActKind). */
 #define HKHIP_ACT_A8 0  /* per 32: d = amax/127, round half away, s = sum q */
 #define HKHIP_ACT_Q8K 1 /* per 256: signed-max scale, clamp 127, 16 bsums   */
+#define HKHIP_ACT_F32 2 /* no quantization (NVFP4): products read the f32 input itself */
 
 /* Output modes of the products. */
 #define HKHIP_STORE 0      /* y  = W x + bias */

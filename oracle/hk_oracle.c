@@ -57,7 +57,7 @@ int hko_block_elems(int t) {
     switch (t) {
     case HKO_Q8_0: case HKO_IQ4_NL: case HKO_Q4_0: case HKO_Q4_1: case HKO_Q5_0: case HKO_Q5_1: return 32;
     case HKO_Q4_K: case HKO_Q5_K: case HKO_Q6_K: case HKO_IQ4_XS: return QK_K;
-    default: return 0;
+    default: return hko_fb_block_elems(t);
     }
 }
 
@@ -73,7 +73,7 @@ int hko_block_bytes(int t) {
     case HKO_Q4_1: return 20;   /* blocks.zig:14 */
     case HKO_Q5_0: return 22;   /* blocks.zig:15 */
     case HKO_Q5_1: return 24;   /* blocks.zig:16 */
-    default: return 0;
+    default: return hko_fb_block_bytes(t);
     }
 }
 
@@ -82,7 +82,7 @@ int hko_act_kind(int t) {
     case HKO_Q8_0: case HKO_IQ4_NL: case HKO_Q4_0: case HKO_Q4_1: case HKO_Q5_0: case HKO_Q5_1:
         return 0; /* vecdot.zig:187 */
     case HKO_Q4_K: case HKO_Q5_K: case HKO_Q6_K: case HKO_IQ4_XS: return 1; /* vecdot.zig:188 */
-    default: return -1;
+    default: return hko_fb_act_kind(t);
     }
 }
 
@@ -280,6 +280,7 @@ int hko_dequantize_row(int t, const uint8_t *src, size_t src_len, float *dst, si
         case HKO_Q5_K: deq_q5_k(b, o); break;
         case HKO_IQ4_XS: deq_iq4_xs(b, o); break;
         case HKO_Q4_0: case HKO_Q4_1: case HKO_Q5_0: case HKO_Q5_1: deq_low_bit(t, b, o); break;
+        default: hko_fb_decode_block(t, b, o); break;
         }
     }
     return 0;
@@ -625,6 +626,7 @@ static float tile_legacy(int t, const uint8_t *row, size_t nb, const hko_block_a
 
 int hko_matmul_path(int t, const uint8_t *w, size_t m, size_t k, const float *x, size_t n,
                     const float *bias, float *y, int threads, int tiled) {
+    if (hko_fb_block_elems(t)) return hko_fb_matmul(t, w, m, k, x, n, bias, y, threads);
     int elems = hko_block_elems(t), kind = hko_act_kind(t);
     if (!elems || kind < 0) return -1;
     if (k % (size_t)elems || k % 32) return -2;

@@ -30,6 +30,20 @@ extern "C" {
 #define HKO_Q6_K 0x44
 #define HKO_IQ4_NL 0x55
 #define HKO_IQ4_XS 0x56
+/* Formats hk decodes to floats before its dots (src/format.zig:71-93). */
+#define HKO_Q2_K 0x40
+#define HKO_Q3_K 0x41
+#define HKO_IQ1_S 0x50
+#define HKO_IQ1_M 0x51
+#define HKO_IQ2_XXS 0x52
+#define HKO_IQ2_XS 0x53
+#define HKO_IQ3_XXS 0x54
+#define HKO_IQ2_S 0x57
+#define HKO_IQ3_S 0x58
+#define HKO_TQ1_0 0x60
+#define HKO_TQ2_0 0x61
+#define HKO_MXFP4 0x62
+#define HKO_NVFP4 0x63
 
 /* Activation blocks, byte-identical to the reference structs. */
 typedef struct {
@@ -80,6 +94,15 @@ int hko_matmul(int t, const uint8_t *w, size_t m, size_t k, const float *x, size
 /* Force one of the two CPU paths regardless of n: 0 = rows (vecdot), 1 = tiles (gemm). */
 int hko_matmul_path(int t, const uint8_t *w, size_t m, size_t k, const float *x, size_t n,
                     const float *bias, float *y, int threads, int tiled);
+
+/* hk_oracle_fallback.c: geometry, activation kind (0 A8, 1 Q8K, 2 f32), one block decoded to
+ * floats (bit-exact), and the products (float64 restatement of hk's dots). */
+int hko_fb_block_elems(int t);
+int hko_fb_block_bytes(int t);
+int hko_fb_act_kind(int t);
+int hko_fb_decode_block(int t, const uint8_t *b, float *out);
+int hko_fb_matmul(int t, const uint8_t *w, size_t m, size_t k, const float *x, size_t n, const float *bias, float *y,
+                  int threads);
 
 #ifdef __cplusplus
 }

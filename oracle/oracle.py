@@ -51,6 +51,9 @@ def lib() -> ctypes.CDLL:
         L.hko_matmul_path.argtypes = [I, P, S, S, P, S, P, P, I, I]
         L.hko_f16_to_f32.argtypes = [ctypes.c_uint16]
         L.hko_f16_to_f32.restype = F
+        L.hko_block_elems.argtypes = [I]
+        L.hko_block_bytes.argtypes = [I]
+        L.hko_act_kind.argtypes = [I]
         L.hkc_pick_level.argtypes = [ctypes.c_char_p]
         L.hkc_pick_level.restype = I
         L.hkc_level_name.argtypes = [I]
@@ -65,16 +68,22 @@ def _p(a: np.ndarray | None):
 
 
 def block_elems(t: int) -> int:
-    return {Q4_K: 256, Q6_K: 256, Q5_K: 256, IQ4_XS: 256, **{f: 32 for f in _A8}}[t]
+    e = lib().hko_block_elems(t)
+    if not e:
+        raise KeyError(t)
+    return e
 
 
 def block_bytes(t: int) -> int:
-    return {Q8_0: 34, IQ4_NL: 18, Q4_K: 144, Q6_K: 210, Q4_0: 18, Q4_1: 20, Q5_0: 22, Q5_1: 24, Q5_K: 176, IQ4_XS: 136}[t]
+    b = lib().hko_block_bytes(t)
+    if not b:
+        raise KeyError(t)
+    return b
 
 
 def act_kind(t: int) -> int:
-    """0 = A8 (per 32), 1 = Q8K (per 256); vecdot.zig:185-191."""
-    return 0 if t in _A8 else 1
+    """0 = A8 (per 32), 1 = Q8K (per 256), 2 = f32; vecdot.zig:185-191."""
+    return lib().hko_act_kind(t)
 
 
 def dequantize(t: int, raw: np.ndarray, n: int) -> np.ndarray:

@@ -50,8 +50,8 @@ def test_sizes_match_the_block_table():
         assert F.matrix_bytes(t, 7, elems * 3) == 7 * 3 * nbytes
     assert L.hkhip_matrix_bytes(F.Q4_K, 14336, 4096) == 33030144
     assert L.hkhip_matrix_bytes(F.Q6_K, 128256, 4096) == 430940160
-    assert L.hkhip_supports(0x40) == 0  # Q2_K is not on this path
-    assert L.hkhip_matrix_bytes(0x40, 1, 256) == -1  # UNSUPPORTED_TYPE
+    assert L.hkhip_supports(0x01) == 0  # f16 is not on this path
+    assert L.hkhip_matrix_bytes(0x01, 1, 256) == -1  # UNSUPPORTED_TYPE
     assert L.hkhip_matrix_bytes(F.Q4_K, 1, 100) == -2  # UNSUPPORTED_SHAPE
     assert b"whole number" in L.hkhip_last_error()
 

@@ -261,7 +261,7 @@ def test_errors(eng, torch_cuda):
         eng.upload(np.zeros(100 * 34 // 32, np.uint8), F.Q8_0, 1, 100)
     assert e.value.code == -2  # UNSUPPORTED_SHAPE: cols not a multiple of 32
     with pytest.raises(HipError) as e:
-        eng.upload(np.zeros(84, np.uint8), 0x40, 1, 256)  # Q2_K: not on this path
+        eng.upload(np.zeros(512, np.uint8), 0x01, 1, 256)  # f16: not on this path
     assert e.value.code == -1
     raw = synth.weights_np(F.Q4_K, 4, 256, seed=1)
     w = eng.upload(raw, F.Q4_K, 4, 256)

@@ -26,7 +26,8 @@ from tests.helpers import load_fixture, tie_rows
 FMTS = [F.Q8_0, F.Q4_K, F.Q6_K, F.IQ4_NL, F.Q4_0, F.Q4_1, F.Q5_0, F.Q5_1, F.Q5_K, F.IQ4_XS]
 FIXTURES = F.NAMES
 GGML_TYPE = {F.Q8_0: 8, F.Q4_K: 12, F.Q6_K: 14, F.IQ4_NL: 20, F.Q4_0: 2, F.Q4_1: 3, F.Q5_0: 6, F.Q5_1: 7,
-             F.Q5_K: 13, F.IQ4_XS: 23}
+             F.Q5_K: 13, F.IQ4_XS: 23, F.Q2_K: 10, F.Q3_K: 11, F.IQ2_XXS: 16, F.IQ2_XS: 17, F.IQ3_XXS: 18,
+             F.IQ1_S: 19, F.IQ3_S: 21, F.IQ2_S: 22, F.IQ1_M: 29, F.TQ1_0: 34, F.TQ2_0: 35, F.MXFP4: 39, F.NVFP4: 40}
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -36,7 +37,7 @@ def built():
 
 # ------------------------------------------------------------------------------------ decoders
 
-@pytest.mark.parametrize("t", FMTS)
+@pytest.mark.parametrize("t", FMTS + list(F.FALLBACK))
 def test_fixture_geometry(t):
     fx = load_fixture(FIXTURES[t])
     assert fx["ggml_type"] == GGML_TYPE[t]
@@ -44,7 +45,7 @@ def test_fixture_geometry(t):
     assert (O.block_elems(t), O.block_bytes(t)) == F.INFO[t]
 
 
-@pytest.mark.parametrize("t", FMTS)
+@pytest.mark.parametrize("t", FMTS + list(F.FALLBACK))
 def test_decoders_match_reference_fixtures(t):
     fx = load_fixture(FIXTURES[t])
     k = fx["blocks_per_row"] * fx["block_elems"]
@@ -374,3 +375,61 @@ def test_net_oracle_cache_consistency():
     part = Oracle(cfg, model)
     part.forward(toks[:5], 0)
     assert np.allclose(part.forward(toks[5:], 5), whole, rtol=0, atol=1e-4 * np.abs(whole).max())
+
+
+# ------------------------------------------------------------------------------------ float-decode formats
+
+def test_fallback_decoder_closed_forms():
+    """Hand-built blocks whose values follow from the format definitions alone."""
+    # TQ2_0: 2-bit codes 0..3 mean -1, 0, 1, 2 (hk: q - 1) times d = 1.0 (f16 0x3C00).
+    b = np.zeros(66, np.uint8)
+    b[0:64] = 0b11100100  # codes 0, 1, 2, 3 in the four 2-bit fields of every byte
+    b[64:66] = [0x00, 0x3C]
+    got = O.dequantize(F.TQ2_0, b, 256)
+    want = np.concatenate([np.full(32, c - 1.0) for _ in range(2) for c in range(4)])
+    assert np.array_equal(got, want)
+    # MXFP4: E8M0 exponent 128 halves to 2^0 = 1; nibbles index the doubled E2M1 table.
+    b = np.zeros(17, np.uint8)
+    b[0] = 128
+    b[1:17] = np.arange(16, dtype=np.uint8) | (np.arange(16, dtype=np.uint8)[::-1] << 4)
+    fp4 = np.array([0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12], np.float32)
+    assert np.array_equal(O.dequantize(F.MXFP4, b, 32), np.concatenate([fp4, fp4[::-1]]))
+    # NVFP4: E4M3 scale 0x38 (exponent 7, mantissa 0) is 1.0, halved to 0.5.
+    b = np.zeros(36, np.uint8)
+    b[0:4] = 0x38
+    b[4:36] = 0x71  # low nibble 1 (value 1), high nibble 7 (value 12)
+    got = O.dequantize(F.NVFP4, b, 64).reshape(4, 2, 8)
+    assert np.all(got[:, 0] == 0.5) and np.all(got[:, 1] == 6.0)
+    # TQ1_0: every base-3 digit 0 decodes to -1, so an all-zero block with d = 1 is all -1.
+    b = np.zeros(54, np.uint8)
+    b[52:54] = [0x00, 0x3C]
+    assert np.array_equal(O.dequantize(F.TQ1_0, b, 256), np.full(256, -1.0, np.float32))
+
+
+@pytest.mark.parametrize("t", list(F.FALLBACK))
+def test_fallback_products_use_hks_activation_kind(t):
+    """The float-decode formats' products take the activation form vecdot.zig:185-191 assigns
+    (Q8K for the K and IQ/TQ families, A8 for MXFP4, f32 for NVFP4): the oracle's product equals
+    the decoded weights times the activations quantized that way, and differs from the other ways."""
+    m, k, n = 9, 512, 3
+    raw = synth.weights_np(t, m, k, seed=50 + t)
+    x = synth.activations_np(n, k, seed=51)
+    w = np.stack([O.dequantize(t, raw[r], k) for r in range(m)]).astype(np.float64)
+
+    def acts(kind):
+        if kind == F.ACT_F32:
+            return x.astype(np.float64)
+        out = []
+        for i in range(n):
+            a = O.quantize_q8k(x[i]) if kind == F.ACT_Q8K else O.quantize_a8(x[i])
+            out.append((a["d"][:, None].astype(np.float64) * a["qs"]).ravel())
+        return np.stack(out)
+
+    got = O.matmul(t, raw, m, k, x, n)
+    for kind in (F.ACT_A8, F.ACT_Q8K, F.ACT_F32):
+        want = acts(kind) @ w.T
+        err = np.max(np.abs(got - want)) / np.max(np.abs(want))
+        if kind == F.ACT_KIND[t]:
+            assert err <= 1e-6
+        else:
+            assert err > 1e-4
