@@ -95,3 +95,34 @@ def test_net_rejects(eng):
             net.forward([64], 0)  # token outside the vocabulary
         net.forward([1, 2, 3], 0)
         assert np.isfinite(net.logits()).all()
+
+
+@pytest.mark.parametrize("arch,fmt,tie,vec_type", [("qwen3", F.Q4_K, False, 1), ("qwen2", F.Q8_0, True, 0),
+                                                   ("llama", F.Q5_K, False, 2)])
+def test_net_from_hk_file(eng, tmp_path, arch, fmt, tie, vec_type):
+    """A decoder stored in an .hk container (tensors written to the reference's layout), read with
+    hk_amd.hkfile (memory-mapped, tensors uploaded from views of the mapping) into the HIP pass,
+    against the CPU forward of the same tensors; qwen2 carries q/k/v biases and a tied output."""
+    from hk_amd.hkfile import HkFile
+    from tests.hkwriter import write_model
+
+    cfg = Config(dim=256, n_layers=2, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=512, vocab=300, max_ctx=200,
+                 rope_neox=arch != "llama", rope_base=1e6 if arch != "llama" else 5e5)
+    model = synth.model_np(cfg, fmt, seed=4600, out_fmt=F.Q6_K, embd_fmt=F.Q8_0, qk_norm=arch == "qwen3",
+                           bias=arch == "qwen2")
+    path = str(tmp_path / f"{arch}.hk")
+    write_model(path, arch, cfg, model, tie_output=tie, vec_type=vec_type)
+    rng = np.random.default_rng(4601)
+    with HkFile(path) as f:
+        fcfg = f.config(max_ctx=cfg.max_ctx)
+        cpu = Oracle(fcfg, f.model(fcfg))
+        net = f.load_net(eng, max_ctx=cfg.max_ctx)
+        try:
+            pos = 0
+            for n in (20, 1, 1, 2):
+                toks = rng.integers(0, cfg.vocab, n)
+                net.forward(toks, pos)
+                check(net.logits(), cpu.forward(toks, pos), f"{arch} from .hk, pass of {n} at {pos}")
+                pos += n
+        finally:
+            net.close()
