@@ -433,3 +433,37 @@ def test_fallback_products_use_hks_activation_kind(t):
             assert err <= 1e-6
         else:
             assert err > 1e-4
+
+
+def test_net_oracle_pieces_closed_forms():
+    """Closed forms of the CPU network restatement's pieces: RMS norm of a constant vector is
+    the weights times sign(c) / sqrt(1 + eps / c^2); RoPE at position 0 is the identity and at any
+    position rotates each (i, i + half) or (2i, 2i + 1) pair by pos * base^(-2i/d), keeping its
+    length; attention over a single position returns that position's value row."""
+    from hk_amd.net import Config
+    from oracle.net_oracle import Oracle, rms_norm
+
+    w = np.linspace(0.5, 1.5, 64).astype(np.float32)
+    for c in (3.0, -0.25):
+        got = rms_norm(np.full(64, c, np.float32), w, 1e-6)
+        assert np.allclose(got, w * np.sign(c) / np.sqrt(1 + 1e-6 / c ** 2), rtol=1e-6)
+    for neox in (True, False):
+        cfg = Config(dim=64, n_layers=1, n_heads=1, n_kv_heads=1, head_dim=64, ffn_dim=256, vocab=16, max_ctx=8,
+                     rope_neox=neox, rope_base=10000.0)
+        model = synth.model_np(cfg, F.Q8_0, seed=5)
+        o = Oracle(cfg, model)
+        v = np.random.default_rng(6).standard_normal(64).astype(np.float32)
+        assert np.array_equal(o._rope(v, 0), v)
+        r = o._rope(v, 5)
+        i0, i1 = (np.arange(32), np.arange(32) + 32) if neox else (np.arange(0, 64, 2), np.arange(1, 64, 2))
+        ang = 5 * 10000.0 ** (-2 * np.arange(32) / 64)
+        want0 = v[i0] * np.cos(ang) - v[i1] * np.sin(ang)
+        assert np.allclose(r[i0], want0, atol=1e-5)
+        assert np.allclose(np.hypot(r[i0], r[i1]), np.hypot(v[i0], v[i1]), rtol=1e-5)
+        # one token: its attention output is its own value row (f16 cache)
+        o.forward([3], 0)
+        raw, t = model["layers"][0]["wv"]
+        x = O.dequantize(model["tok_embd"][1], model["tok_embd"][0][3], 64)
+        xb = rms_norm(x, model["layers"][0]["attn_norm"], cfg.rms_eps)
+        vrow = O.matmul(t, raw, 64, 64, xb[None], 1)[0]
+        assert np.array_equal(o.vc[0, 0, 0], vrow.astype(np.float16))
