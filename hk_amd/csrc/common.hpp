@@ -146,6 +146,10 @@ inline WLayout weight_layout(int t, uint32_t rows, uint32_t cols) {
 // input serves the 32-weight formats (A8) and the super-block formats (Q8K) alike:
 //   a8_qs [n][k] i8, a8_d [n][k/32] f32, a8_s [n][k/32] i32, a8_ds [n][k/32] f32 = d * (f32)s
 //         (the offset operand of Q4_1 / Q5_1, as kernelLegacy forms it, gemm.zig:165),
+//   a8_dsb [k/256][n][3][8] bf16: a8_ds of the 8 blocks of each super-block as three bf16
+//         parts (hi + mid + lo = the f32 value exactly), super-block major so that a token
+//         range of one super-block is contiguous -- the token-side operand of the Q4_1 / Q5_1
+//         GEMM's offset term, which runs on bf16 MFMAs,
 //   k_qs  [n][k] i8, k_d  [n][k/256] f32, k_bs [n][k/16] i16,
 //   k_db  [n][k/32] f32: d * (f32)(bsum of the 32 values of each sub-block), the Q5_K GEMM's
 //         min-term operand,
@@ -163,7 +167,7 @@ inline WLayout weight_layout(int t, uint32_t rows, uint32_t cols) {
 constexpr uint32_t SK_MAX_TOKENS = 32;
 constexpr uint32_t SK_MIN_TOKENS = 4; // below, the decode kernels are faster
 struct ActLayout {
-    uint64_t a8_qs, a8_d, a8_s, a8_ds, k_qs, k_d, k_bs, k_db, k_mb, k_il, k_ilmb, k_ild, total;
+    uint64_t a8_qs, a8_d, a8_s, a8_ds, a8_dsb, k_qs, k_d, k_bs, k_db, k_mb, k_il, k_ilmb, k_ild, total;
     uint32_t tiles; // 16-token tiles of the interleaved planes (0: none)
 };
 
@@ -175,6 +179,7 @@ inline ActLayout act_layout(uint32_t n, uint32_t k) {
     L.a8_d = o;  o = align256(o + nk / 32 * 4);
     L.a8_s = o;  o = align256(o + nk / 32 * 4);
     L.a8_ds = o; o = align256(o + nk / 32 * 4);
+    L.a8_dsb = o; o = align256(o + (k % QK_K == 0 ? nk / QK_K * 48 : 0));
     L.k_qs = o;  o = align256(o + (k % QK_K == 0 ? nk : 0));
     L.k_d = o;   o = align256(o + (k % QK_K == 0 ? nk / QK_K * 4 : 0));
     L.k_bs = o;  o = align256(o + (k % QK_K == 0 ? nk / 16 * 2 : 0));

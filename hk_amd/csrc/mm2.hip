@@ -47,6 +47,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+typedef short s2v __attribute__((ext_vector_type(2)));
 
 // Shapes: NW waves per workgroup (32 rows each), TT token tiles of 32 per wave, NB super-blocks
 // in flight; the workgroup covers 32*NW rows x 32*TT tokens. The large configuration amortizes
@@ -82,19 +83,17 @@ struct Mm2Args {
 
 __device__ __forceinline__ uint4 ldg16(const void *p) { return *reinterpret_cast<const uint4 *>(p); }
 
-// fp32 -> bf16 bits, round to nearest even (finite inputs).
-__device__ __forceinline__ uint32_t bf16_rne(float x) {
-    const uint32_t u = __builtin_bit_cast(uint32_t, x);
-    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
-}
-// x as three bf16 parts p[0] + p[1] + p[2] (each the rounding of what the previous ones leave;
-// their sum is x to within 2^-24 relative).
+// x as three bf16 parts hi + mid + lo, each the top 16 bits of an f32 (the low 16 bits of the
+// returned words are left as they fall): hi keeps x's leading 8 significant bits, mid the next 8
+// of the remainder, lo the rest, which then has at most 8 -- so the sum is x exactly.
 __device__ __forceinline__ void bf16_split3(float x, uint32_t p[3]) {
-    p[0] = bf16_rne(x);
-    const float r1 = x - __builtin_bit_cast(float, p[0] << 16);
-    p[1] = bf16_rne(r1);
-    p[2] = bf16_rne(r1 - __builtin_bit_cast(float, p[1] << 16));
+    p[0] = __builtin_bit_cast(uint32_t, x) & 0xFFFF0000u;
+    const float r1 = x - __builtin_bit_cast(float, p[0]);
+    p[1] = __builtin_bit_cast(uint32_t, r1) & 0xFFFF0000u;
+    p[2] = __builtin_bit_cast(uint32_t, r1 - __builtin_bit_cast(float, p[1]));
 }
+// Two split values as bf16 pairs, x0 in the low half: the top halves of a and b.
+__device__ __forceinline__ uint32_t bf16_pair(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
 
 // Row-side min-term operands of one super-block: -dmin*mn of the 8 sub-blocks (6-bit mins in
 // the bytes of mnl, mnh) in three bf16 parts, as the B operands of the three 32x32x16 MFMAs:
@@ -111,7 +110,7 @@ __device__ __forceinline__ MinB min_operands(uint32_t mnl, uint32_t mnh, float d
 #pragma unroll
         for (int q = 0; q < 3; q++) {
             if (s & 1)
-                w[q][s / 2] |= p[q] << 16;
+                w[q][s / 2] = bf16_pair(w[q][s / 2], p[q]);
             else
                 w[q][s / 2] = p[q];
         }
@@ -183,7 +182,7 @@ __device__ __forceinline__ MinB min_operands_k5(uint32_t scl, uint32_t sch, floa
 #pragma unroll
         for (int q = 0; q < 3; q++) {
             if (s & 1)
-                w[q][s / 2] |= p[q] << 16;
+                w[q][s / 2] = bf16_pair(w[q][s / 2], p[q]);
             else
                 w[q][s / 2] = p[q];
         }
@@ -279,13 +278,13 @@ __global__ __launch_bounds__(Q2_NW * 64, 2) void mm2_q4k_reg_kernel(Mm2Args a) {
             uint32_t w[3][4];
 #pragma unroll
             for (int s = 0; s < 8; s++) {
-                const int b32 = int(int16_t(bw[s] & 0xFFFF)) + int(int16_t(bw[s] >> 16));
+                const int b32 = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2v, bw[s]), s2v{1, 1}, 0, false);
                 uint32_t p[3];
                 bf16_split3(ok ? sda * (float)b32 : 0.0f, p);
 #pragma unroll
                 for (int q = 0; q < 3; q++) {
                     if (s & 1)
-                        w[q][s / 2] |= p[q] << 16;
+                        w[q][s / 2] = bf16_pair(w[q][s / 2], p[q]);
                     else
                         w[q][s / 2] = p[q];
                 }

@@ -34,6 +34,7 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
 // Per-format geometry of one super-block step (256 weights of 32 rows = one wave's share).
 template <int T> struct Fmt;
@@ -69,16 +70,21 @@ template <> struct Fmt<HKHIP_Q4_1> : Fmt4<HKHIP_Q4_1> {};
 template <> struct Fmt<HKHIP_Q5_0> : Fmt4<HKHIP_Q5_0> {};
 template <> struct Fmt<HKHIP_Q5_1> : Fmt4<HKHIP_Q5_1> {};
 
-template <int T, int TOK, int NW> struct MxSlot {
+// MF: the Q4_1 / Q5_1 offset term on MFMAs (the single-slice tiles); with K slices the ring has
+// no room for its operand and the term is one fma per output and block.
+template <int T, int TOK, int NW, bool MF = true> struct MxSlot {
     int8_t a[TOK * 256];                     // chunk c of token t at c ^ (t & 15)
     uint8_t w[NW][32 * Fmt<T>::RB];          // per wave, its 32 rows' bytes of the step
     uint8_t ws[NW][Fmt<T>::WSB];             // per wave, the rows' f16 scales of the step
     // Activation scales: Q6_K per token (wave m fills tokens 64m..64m+63); A8 per block and token,
     // block-major ([8][TOK]), so that four consecutive tokens' scales are one 16-byte read.
     float da[T == HKHIP_Q6_K || T == HKHIP_IQ4_XS || T == HKHIP_Q5_K ? 64 * NW : 8 * TOK];
-    // Q4_1 / Q5_1: the blocks' d_a * s; Q5_K: each sub-block's d_a * bsum32 (f32 bits, [8][TOK]
-    // as da).
-    uint32_t sa[has_m(T) || T == HKHIP_Q5_K ? 8 * TOK : 1];
+    // Q5_K: each sub-block's d_a * bsum32; Q4_1 / Q5_1 without MF: the blocks' d_a * s (f32
+    // bits, [8][TOK] as da).
+    uint32_t sa[T == HKHIP_Q5_K || (has_m(T) && !MF) ? 8 * TOK : 1];
+    // Q4_1 / Q5_1: the blocks' d_a * s as three bf16 parts, [token][part][8] (a8_dsb), in 1-KB
+    // chunks, one load per wave (waves past the last chunk load it again).
+    uint32_t dsb[has_m(T) && MF ? 256 * ((TOK * 48 + 1023) / 1024) : 0];
 };
 
 struct MxArgs {
@@ -87,7 +93,8 @@ struct MxArgs {
     uint32_t rows, cols, n;
     const int8_t *aqs;
     const float *ad;
-    const float *ads;   // A8 d * s per block (Q4_1, Q5_1)
+    const float *ads;    // A8 d * s per block (Q4_1, Q5_1)
+    const uint8_t *adsb; // the same in bf16 parts, [k/256][n][48 B]
     const float *adb;   // Q8K d * bsum32 per sub-block (Q5_K)
     float *y;
     const float *bias;
@@ -121,7 +128,8 @@ template <int T, int NW, int TT, int NB, int KS = 1>
 __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
     constexpr int TOK = 32 * TT;
     using F = Fmt<T>;
-    using Slot = MxSlot<T, TOK, NW>;
+    constexpr bool mf = has_m(T) && KS == 1; // offset term on MFMAs
+    using Slot = MxSlot<T, TOK, NW, KS == 1>;
     constexpr bool q6 = (T == HKHIP_Q6_K);
     constexpr bool xs = (T == HKHIP_IQ4_XS);
     constexpr bool k5 = (T == HKHIP_Q5_K);
@@ -171,7 +179,7 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
     constexpr uint32_t TPW = TOK / NW; // token rows per wave
     static_assert(TPW % 4 == 0, "token rows per wave");
     constexpr uint32_t DAL = kqa ? 1 : 8 * TOK / (64 * NW);        // token-scale loads per wave
-    constexpr uint32_t CPW = TPW / 4 + F::W16 + F::W4 + (k5 ? 0 : 1) + DAL + (has_qh(T) ? 1 : 0) + (has_m(T) ? DAL : 0) +
+    constexpr uint32_t CPW = TPW / 4 + F::W16 + F::W4 + (k5 ? 0 : 1) + DAL + (has_qh(T) ? 1 : 0) + (mf ? 1 : has_m(T) ? DAL : 0) +
                              (k5 ? DBS : 0);
     // Weights: 16-byte piece P = 64*i + lane of the wave's area is row P/(RB/16), piece P%(RB/16);
     // rows of 256 or 128 bytes are swizzled (piece c of row r at c ^ (r & 15), resp. r & 7) so
@@ -237,6 +245,15 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
         }
     }
 
+    // Q4_1 / Q5_1 offset operand: byte e = 1024*wave + 16*lane of the token range's 48-byte rows.
+    constexpr uint32_t DSC = (TOK * 48 + 1023) / 1024; // 1-KB chunks of the offset operand
+    static_assert(!mf || DSC <= NW, "one offset-operand load per wave");
+    const uint32_t dsc = wave < DSC ? wave : DSC - 1;
+    uint32_t dsboff = 0;
+    if constexpr (mf) {
+        const uint32_t e = 1024 * dsc + 16 * lane;
+        dsboff = clamp_tok(t0 + e / 48) * 48 + e % 48;
+    }
     auto issue = [&](uint32_t sb, Slot &S) {
         const int8_t *ga = a.aqs + 256 * sb;
 #pragma unroll
@@ -263,7 +280,9 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
             if constexpr (has_qh(T)) load_lds16(a.ws + qhbase + 32 * sb, &S.ws[wave][1024]);
 #pragma unroll
             for (uint32_t i = 0; i < DAL; i++) load_lds4(gd + doff[i] + 32 * sb, &S.da[64 * (DAL * wave + i)]);
-            if constexpr (has_m(T)) {
+            if constexpr (mf) {
+                load_lds16(a.adsb + uint64_t(sb) * a.n * 48 + dsboff, &S.dsb[256 * dsc]);
+            } else if constexpr (has_m(T)) {
                 const uint8_t *gs = reinterpret_cast<const uint8_t *>(a.ads);
 #pragma unroll
                 for (uint32_t i = 0; i < DAL; i++) load_lds4(gs + doff[i] + 32 * sb, &S.sa[64 * (DAL * wave + i)]);
@@ -409,11 +428,35 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
                     for (int i = 0; i < 4; i++) wv[c][i] = int(low_bit_word<TL>(xw[i], qh, h, i));
                 }
             }
-            if constexpr (has_m(T)) {
+            // Q4_1 / Q5_1 offset term, sum_c m[r,c] * (d_a * s)[t,c] over the super-block's 8 blocks,
+            // on bf16 MFMAs: m (an f16) is hi + lo exactly (8 + at most 3 significant bits), the
+            // token side hi + mid + lo (a8_dsb); three 32x32x16 MFMAs pair (hi|mid) with m's hi and
+            // lo and the token lo with m's hi -- every partial product down to 2^-24 relative.
+            v8bf mB1, mB2, mB3;
+            if constexpr (has_m(T) && !mf) {
                 const uint4 m16 = *reinterpret_cast<const uint4 *>(&S.ws[wave][16 * (32 + j)]);
                 const uint32_t mw4[4] = {m16.x, m16.y, m16.z, m16.w};
 #pragma unroll
                 for (int c = 0; c < 8; c++) mw[c] = f16_bits_to_f32((mw4[c / 2] >> (16 * (c & 1))) & 0xFFFF);
+            } else if constexpr (mf) {
+                const uint4 m16 = *reinterpret_cast<const uint4 *>(&S.ws[wave][16 * (32 + j)]);
+                const uint32_t mw4[4] = {m16.x, m16.y, m16.z, m16.w};
+                uint32_t mh[4], ml[4];
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    uint32_t hi2[2], lo2[2];
+#pragma unroll
+                    for (int e = 0; e < 2; e++) {
+                        const float m = f16_bits_to_f32((mw4[q] >> (16 * e)) & 0xFFFF);
+                        hi2[e] = __builtin_bit_cast(uint32_t, m) & 0xFFFF0000u;
+                        lo2[e] = __builtin_bit_cast(uint32_t, m - __builtin_bit_cast(float, hi2[e]));
+                    }
+                    mh[q] = __builtin_amdgcn_perm(hi2[1], hi2[0], 0x07060302u);
+                    ml[q] = __builtin_amdgcn_perm(lo2[1], lo2[0], 0x07060302u);
+                }
+                mB1 = __builtin_bit_cast(v8bf, make_uint4(mh[0], mh[1], mh[2], mh[3]));
+                mB2 = __builtin_bit_cast(v8bf, make_uint4(ml[0], ml[1], ml[2], ml[3]));
+                mB3 = h ? v8bf{} : mB1;
             }
             if constexpr (k5) {
             } else if constexpr (xs) {
@@ -447,7 +490,7 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
 #pragma unroll
                         for (int e = 0; e < 4; e++)
                             acc[t][4 * g + e] = fmaf((float)p[4 * g + e], dw[c] * ds[e], acc[t][4 * g + e]);
-                        if constexpr (has_m(T)) {
+                        if constexpr (has_m(T) && !mf) {
                             const float4 sv = *reinterpret_cast<const float4 *>(&S.sa[c * TOK + 32 * t + 4 * h + 8 * g]);
                             const float dss[4] = {sv.x, sv.y, sv.z, sv.w};
 #pragma unroll
@@ -460,6 +503,14 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
                             for (int e = 0; e < 4; e++) acc[t][4 * g + e] = fmaf(-mw[c], db[e], acc[t][4 * g + e]);
                         }
                     }
+                }
+                if constexpr (mf) {
+                    const uint32_t *tm = &S.dsb[12 * (32 * t + j)];
+                    const v8bf a12 = __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4 *>(tm + 4 * h));
+                    const v8bf a3 = __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4 *>(tm + 8));
+                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a12, mB1, acc[t], 0, 0, 0);
+                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a12, mB2, acc[t], 0, 0, 0);
+                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a3, mB3, acc[t], 0, 0, 0);
                 }
                 if (t + 1 < TT) load_a(t + 1);
             }
@@ -520,7 +571,7 @@ typedef void (*mx_kernel_t)(MxArgs);
 
 template <int T, int NW, int TT, int NB, int KS = 1>
 hipError_t launch_cfg(const MxArgs &a0, hipStream_t s) {
-    static_assert(NB * KS * sizeof(MxSlot<T, 32 * TT, NW>) <= 160 * 1024, "LDS");
+    static_assert(NB * KS * sizeof(MxSlot<T, 32 * TT, NW, KS == 1>) <= 160 * 1024, "LDS");
     MxArgs a = a0;
     a.rblocks = (a.rows + 32 * NW - 1) / (32 * NW);
     a.tblocks = (a.n + 32 * TT - 1) / (32 * TT);
@@ -574,6 +625,7 @@ hipError_t launch_mmx(int t, const uint8_t *w, uint32_t rows, uint32_t cols, con
     a.aqs = reinterpret_cast<const int8_t *>(xq + (q6 ? A.k_qs : A.a8_qs));
     a.ad = reinterpret_cast<const float *>(xq + (q6 ? A.k_d : A.a8_d));
     a.ads = reinterpret_cast<const float *>(xq + A.a8_ds);
+    a.adsb = xq + A.a8_dsb;
     a.adb = reinterpret_cast<const float *>(xq + A.k_db);
     a.y = y;
     a.bias = bias;

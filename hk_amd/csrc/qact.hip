@@ -4,17 +4,33 @@
 
 namespace hkhip {
 
-// A8: one thread per value; a 32-lane half-wave owns one block.
+// A8: one thread per value; a 32-lane half-wave owns one block. dsb (a8_dsb; null when k is
+// not a multiple of 256): d * s in three bf16 parts, [k/256][n][3][8].
 __global__ void qact_a8_kernel(const float *__restrict__ x, uint64_t total, int8_t *__restrict__ qs,
-                               float *__restrict__ dout, int32_t *__restrict__ sout, float *__restrict__ dsout) {
+                               float *__restrict__ dout, int32_t *__restrict__ sout, float *__restrict__ dsout,
+                               uint16_t *__restrict__ dsb, uint32_t n, uint32_t kb) {
     const uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     const A8Q r = quant_a8_halfwave(i < total ? x[i] : 0.0f);
     if (i < total) {
         qs[i] = (int8_t)r.q;
         if ((i & 31) == 0) {
-            dout[i / 32] = r.d;
-            sout[i / 32] = r.s;
-            dsout[i / 32] = r.d * (float)r.s;
+            const uint64_t b = i / 32;
+            const float ds = r.d * (float)r.s;
+            dout[b] = r.d;
+            sout[b] = r.s;
+            dsout[b] = ds;
+            if (dsb) {
+                // hi keeps the leading 8 significant bits, mid the next 8, lo the rest (<= 8).
+                const uint32_t t = uint32_t(b / kb), c = uint32_t(b % kb);
+                const uint32_t p0 = __builtin_bit_cast(uint32_t, ds) & 0xFFFF0000u;
+                const float r1 = ds - __builtin_bit_cast(float, p0);
+                const uint32_t p1 = __builtin_bit_cast(uint32_t, r1) & 0xFFFF0000u;
+                const uint32_t p2 = __builtin_bit_cast(uint32_t, r1 - __builtin_bit_cast(float, p1));
+                uint16_t *o = dsb + ((uint64_t(c / 8) * n + t) * 3) * 8 + c % 8;
+                o[0] = uint16_t(p0 >> 16);
+                o[8] = uint16_t(p1 >> 16);
+                o[16] = uint16_t(p2 >> 16);
+            }
         }
     }
 }
@@ -82,7 +98,9 @@ hipError_t launch_qact(const float *x, uint32_t n, uint32_t k, int kind, uint8_t
         qact_a8_kernel<<<uint32_t(grid), 256, 0, s>>>(x, total, reinterpret_cast<int8_t *>(xq + L.a8_qs),
                                                       reinterpret_cast<float *>(xq + L.a8_d),
                                                       reinterpret_cast<int32_t *>(xq + L.a8_s),
-                                                      reinterpret_cast<float *>(xq + L.a8_ds));
+                                                      reinterpret_cast<float *>(xq + L.a8_ds),
+                                                      k % QK_K == 0 ? reinterpret_cast<uint16_t *>(xq + L.a8_dsb) : nullptr,
+                                                      n, k / 32);
     } else {
         uint64_t nb = total / QK_K;
         uint64_t grid = (nb + 3) / 4; // 4 waves per workgroup
