@@ -66,15 +66,17 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ 
 
 // One wave per (token, head): heads 0..nh-1 are query heads (normalized, rotated, written back),
 // nh..nh+nkv-1 key heads (normalized, rotated, written to the f16 key cache), then nkv value heads
-// (to the f16 value cache). Position of token t: pos0[0] + t. Cache layout [kv head][max_ctx][hd].
+// (to the f16 value cache, and transposed to [kv head][hd][vt_stride] for the prefill attention).
+// Position of token t: pos0[0] + t. Cache layout [kv head][max_ctx][hd].
 struct RopeArgs {
     float *q;
     const float *k, *v;
     const float *q_norm, *k_norm; // [hd] or null
     const float *inv_freq;        // [rope_dim / 2]
     __half *kc, *vc;              // this layer's caches
+    __half *vt;                   // this layer's transposed value cache [nkv][hd][vt_stride]
     const uint32_t *pos0;
-    uint32_t nh, nkv, hd, rope_half, neox, max_ctx;
+    uint32_t nh, nkv, hd, rope_half, neox, max_ctx, vt_stride;
     float eps;
 };
 
@@ -87,7 +89,12 @@ __global__ __launch_bounds__(64) void rope_kv_kernel(RopeArgs a) {
         const uint32_t g = hh - a.nh - a.nkv;
         const float *src = a.v + uint64_t(t) * kvd + g * hd;
         __half *dst = a.vc + (uint64_t(g) * a.max_ctx + pos) * hd;
-        for (uint32_t d = lane; d < hd; d += 64) dst[d] = __float2half(src[d]);
+        __half *dt = a.vt + uint64_t(g) * hd * a.vt_stride + pos;
+        for (uint32_t d = lane; d < hd; d += 64) {
+            const __half v = __float2half(src[d]);
+            dst[d] = v;
+            dt[uint64_t(d) * a.vt_stride] = v;
+        }
         return;
     }
     const uint32_t g = isq ? hh : hh - a.nh;
@@ -246,6 +253,139 @@ __global__ __launch_bounds__(256) void attn_slice_kernel(AttnArgs a) {
     for (int j = 0; j < DL; j++) out[2 + DL * lane + j] = acc[j];
 }
 
+// Prefill attention (passes of more than MAX_DECODE tokens) on the f16 MFMA units, one wave per
+// (32-token tile, query head), four per workgroup; no LDS, no barriers. Per tile of 32 positions:
+//   S^T[pos][tok] = K[pos] . q[tok]: A = key rows (f16, exact), B = q split as f16 hi + lo (q - hi
+//       rounded again; together q to ~2^-22), two MFMA chains over head_dim in steps of 16;
+//   online softmax per token (a lane holds one token's 16 scores; the two lane halves meet by one
+//       exchange), the scores scaled and masked as attn_slice_kernel does;
+//   O^T[dim][tok] += V^T[dim][pos] . P^T[pos][tok]: A = the transposed value cache (positions
+//       contiguous per dimension), B = the probabilities split as f16 hi + lo.
+// The key rows are loaded in the order rho (bits 2 and 3 of the row swapped), which puts each
+// lane half's 16 scores exactly on the 8 + 8 positions the second product's B operand needs, so
+// the probabilities go from the first product's output to the second's input without moving.
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+struct AttnPArgs {
+    const float *q;
+    const __half *kc, *vt; // this layer's key cache [nkv][max_ctx][hd], value cache transposed [nkv][hd][vt_stride]
+    float *att;
+    const uint32_t *pos0;
+    uint32_t n, nh, nkv, max_ctx, vt_stride;
+    float scale;
+};
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_prefill_kernel(AttnPArgs a) {
+    constexpr int NCH = HD / 16, NDT = HD / 32;
+    const uint32_t lane = threadIdx.x & 63, h = lane >> 5, j = lane & 31;
+    const uint32_t item = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const uint32_t ntile = (a.n + 31) / 32;
+    if (item >= ntile * a.nh) return; // whole waves; the kernel has no barrier
+    const uint32_t head = item % a.nh, tile = item / a.nh;
+    const uint32_t kvh = head / (a.nh / a.nkv);
+    const uint32_t pos0 = a.pos0[0];
+    const uint32_t t = tile * 32 + j, tc = t < a.n ? t : a.n - 1; // this lane's token (clamped)
+    const uint32_t tpos = pos0 + tc;
+    const uint32_t pend = pos0 + min(tile * 32 + 32, a.n); // positions [0, pend) are needed
+
+    v8h qh[NCH], ql[NCH];
+    {
+        const float *qrow = a.q + (uint64_t(tc) * a.nh + head) * HD;
+#pragma unroll
+        for (int c = 0; c < NCH; c++) {
+            const float4 x0 = *reinterpret_cast<const float4 *>(qrow + 16 * c + 8 * h);
+            const float4 x1 = *reinterpret_cast<const float4 *>(qrow + 16 * c + 8 * h + 4);
+            const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const _Float16 hi = (_Float16)xs[e];
+                qh[c][e] = hi;
+                ql[c][e] = (_Float16)(xs[e] - (float)hi);
+            }
+        }
+    }
+    v16f acc[NDT];
+#pragma unroll
+    for (int d = 0; d < NDT; d++) acc[d] = v16f{};
+    float m = -INFINITY, l = 0.0f;
+    const __half *kb = a.kc + uint64_t(kvh) * a.max_ctx * HD;
+    const __half *vb = a.vt + uint64_t(kvh) * HD * a.vt_stride;
+    const uint32_t rj = (j & ~12u) | ((j & 4u) << 1) | ((j & 8u) >> 1); // rho(j)
+    for (uint32_t p0 = 0; p0 < pend; p0 += 32) {
+        v8h ka[NCH], va[NDT][2];
+        {
+            const uint32_t kp = p0 + rj < a.max_ctx ? p0 + rj : a.max_ctx - 1;
+            const v8h *krow = reinterpret_cast<const v8h *>(kb + uint64_t(kp) * HD);
+#pragma unroll
+            for (int c = 0; c < NCH; c++) ka[c] = krow[2 * c + h];
+#pragma unroll
+            for (int d = 0; d < NDT; d++)
+#pragma unroll
+                for (int cc = 0; cc < 2; cc++)
+                    va[d][cc] = *reinterpret_cast<const v8h *>(vb + uint64_t(32 * d + j) * a.vt_stride + p0 + 16 * cc + 8 * h);
+        }
+        v16f s = v16f{};
+#pragma unroll
+        for (int c = 0; c < NCH; c++) {
+            s = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[c], qh[c], s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[c], ql[c], s, 0, 0, 0);
+        }
+        // Score v of this lane: position p0 + 16(g >> 1) + 8h + 4(g & 1) + e, g = v / 4, e = v % 4.
+        float sv[16], mx = -INFINITY;
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int g = v / 4, e = v % 4;
+            const uint32_t pp = p0 + 16 * (g >> 1) + 8 * h + 4 * (g & 1) + e;
+            sv[v] = pp <= tpos ? s[v] * a.scale : -INFINITY;
+            mx = fmaxf(mx, sv[v]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float mn = fmaxf(m, mx);
+        const float corr = m == -INFINITY ? 0.0f : expf(m - mn);
+        float pv[16], ps = 0.0f;
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            pv[v] = sv[v] == -INFINITY ? 0.0f : expf(sv[v] - mn);
+            ps += pv[v];
+        }
+        ps += __shfl_xor(ps, 32);
+        l = l * corr + ps;
+        m = mn;
+#pragma unroll
+        for (int d = 0; d < NDT; d++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[d][v] *= corr;
+#pragma unroll
+        for (int cc = 0; cc < 2; cc++) {
+            v8h ph, pl;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const _Float16 hi = (_Float16)pv[8 * cc + e];
+                ph[e] = hi;
+                pl[e] = (_Float16)(pv[8 * cc + e] - (float)hi);
+            }
+#pragma unroll
+            for (int d = 0; d < NDT; d++) {
+                acc[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[d][cc], ph, acc[d], 0, 0, 0);
+                acc[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[d][cc], pl, acc[d], 0, 0, 0);
+            }
+        }
+    }
+    if (t < a.n) {
+        // acc[d][v]: dimension 32d + 8g + 4h + e of this lane's token.
+        const float inv = 1.0f / l;
+        float *o = a.att + (uint64_t(t) * a.nh + head) * HD;
+#pragma unroll
+        for (int d = 0; d < NDT; d++)
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+                *reinterpret_cast<float4 *>(o + 32 * d + 8 * g + 4 * h) =
+                    make_float4(acc[d][4 * g] * inv, acc[d][4 * g + 1] * inv, acc[d][4 * g + 2] * inv, acc[d][4 * g + 3] * inv);
+    }
+}
+
 // att[t][h*hd..] = merge of the slices' partials (attention.zig:113-133 merge): every thread
 // reads one slice's {max, sum} (all loads in flight at once), the block reduces them, the weights
 // exp(m_s - max m) of the non-empty slices go to LDS, then thread d sums its dimension over the
@@ -320,7 +460,7 @@ struct hkhip_net {
     float *x = nullptr, *xb = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *gu = nullptr,
           *h = nullptr, *part = nullptr, *logits = nullptr, *inv_freq = nullptr;
     uint8_t *xq = nullptr;
-    __half *kc = nullptr, *vc = nullptr;
+    __half *kc = nullptr, *vc = nullptr, *vt = nullptr;
     uint32_t *io = nullptr, *tok = nullptr, *pos = nullptr; // device {pos, tokens[cap]}
     uint32_t *stage = nullptr;                               // pinned host copy of io
     std::map<uint32_t, hipGraphExec_t> graphs;
@@ -343,6 +483,8 @@ int hfail(hipError_t e, const char *what) {
 uint32_t qdim(const hkhip_net_config &c) { return c.n_heads * c.head_dim; }
 uint32_t kvdim(const hkhip_net_config &c) { return c.n_kv_heads * c.head_dim; }
 uint32_t nslices(const hkhip_net_config &c) { return (c.max_ctx + ATT_SLICE - 1) / ATT_SLICE; }
+uint32_t vt_stride(const hkhip_net_config &c) { return (c.max_ctx + 31) / 32 * 32; }
+bool prefill_mfma(const hkhip_net_config &c) { return c.head_dim == 64 || c.head_dim == 128; }
 
 int dev_alloc(hkhip_net *n, uint64_t bytes, void **p) {
     NET_TRY(hipMalloc(p, bytes ? bytes : 1), "hipMalloc");
@@ -407,7 +549,8 @@ int ensure_cap(hkhip_net *n, uint32_t want) {
         (rc = dev_alloc(n, T * qdim(c) * 4, (void **)&n->q)) || (rc = dev_alloc(n, T * kvdim(c) * 4, (void **)&n->k)) ||
         (rc = dev_alloc(n, T * kvdim(c) * 4, (void **)&n->v)) || (rc = dev_alloc(n, T * qdim(c) * 4, (void **)&n->att)) ||
         (rc = dev_alloc(n, T * 2 * c.ffn_dim * 4, (void **)&n->gu)) || (rc = dev_alloc(n, T * c.ffn_dim * 4, (void **)&n->h)) ||
-        (rc = dev_alloc(n, T * c.n_heads * nslices(c) * (c.head_dim + 2) * 4, (void **)&n->part)) ||
+        (rc = dev_alloc(n, (prefill_mfma(c) ? std::min<uint64_t>(T, MAX_DECODE) : T) * c.n_heads * nslices(c) * (c.head_dim + 2) * 4,
+                        (void **)&n->part)) ||
         (rc = dev_alloc(n, hkhip_act_bytes(want, maxk), (void **)&n->xq)) ||
         (rc = dev_alloc(n, (T + 1) * 4, (void **)&n->io)))
         return rc;
@@ -472,24 +615,36 @@ int run_pass(hkhip_net *net, uint32_t n) {
             if ((rc = product(net, n, mats, 3, net->x, L.attn_norm, ys, bs, HKHIP_STORE))) return rc;
         }
         const uint64_t cache_layer = uint64_t(c.n_kv_heads) * c.max_ctx * c.head_dim;
+        const uint64_t vt_layer = uint64_t(c.n_kv_heads) * c.head_dim * vt_stride(c);
         RopeArgs ra{net->q, net->k, net->v, L.q_norm, L.k_norm, net->inv_freq, net->kc + li * cache_layer,
-                    net->vc + li * cache_layer, net->pos, c.n_heads, c.n_kv_heads, c.head_dim, c.rope_dim / 2,
-                    c.rope_neox, c.max_ctx, c.rms_eps};
+                    net->vc + li * cache_layer, net->vt + li * vt_layer, net->pos, c.n_heads, c.n_kv_heads, c.head_dim,
+                    c.rope_dim / 2, c.rope_neox, c.max_ctx, vt_stride(c), c.rms_eps};
         hipLaunchKernelGGL(rope_kv_kernel, dim3(c.n_heads + 2 * c.n_kv_heads, n), dim3(64), 0, s, ra);
         NET_TRY(hipGetLastError(), "rope / kv write");
-        AttnArgs aa{net->q, net->kc + li * cache_layer, net->vc + li * cache_layer, net->part, net->pos, n, c.n_heads,
-                    c.n_kv_heads, c.head_dim, c.max_ctx, ns, 1.0f / sqrtf(float(c.head_dim))};
-        const dim3 ag((n * c.n_heads * ns + 3) / 4), ab(256);
-        switch (c.head_dim) {
-        case 64: hipLaunchKernelGGL(attn_slice_kernel<64>, ag, ab, 0, s, aa); break;
-        case 128: hipLaunchKernelGGL(attn_slice_kernel<128>, ag, ab, 0, s, aa); break;
-        case 256: hipLaunchKernelGGL(attn_slice_kernel<256>, ag, ab, 0, s, aa); break;
-        default: return set_error(HKHIP_E_UNSUPPORTED_SHAPE, "head_dim %u", c.head_dim);
+        if (n > MAX_DECODE && prefill_mfma(c)) {
+            AttnPArgs pa{net->q, net->kc + li * cache_layer, net->vt + li * vt_layer, net->att, net->pos, n, c.n_heads,
+                         c.n_kv_heads, c.max_ctx, vt_stride(c), 1.0f / sqrtf(float(c.head_dim))};
+            const dim3 pg(((n + 31) / 32 * c.n_heads + 3) / 4), pb(256);
+            if (c.head_dim == 64)
+                hipLaunchKernelGGL(attn_prefill_kernel<64>, pg, pb, 0, s, pa);
+            else
+                hipLaunchKernelGGL(attn_prefill_kernel<128>, pg, pb, 0, s, pa);
+            NET_TRY(hipGetLastError(), "prefill attention");
+        } else {
+            AttnArgs aa{net->q, net->kc + li * cache_layer, net->vc + li * cache_layer, net->part, net->pos, n, c.n_heads,
+                        c.n_kv_heads, c.head_dim, c.max_ctx, ns, 1.0f / sqrtf(float(c.head_dim))};
+            const dim3 ag((n * c.n_heads * ns + 3) / 4), ab(256);
+            switch (c.head_dim) {
+            case 64: hipLaunchKernelGGL(attn_slice_kernel<64>, ag, ab, 0, s, aa); break;
+            case 128: hipLaunchKernelGGL(attn_slice_kernel<128>, ag, ab, 0, s, aa); break;
+            case 256: hipLaunchKernelGGL(attn_slice_kernel<256>, ag, ab, 0, s, aa); break;
+            default: return set_error(HKHIP_E_UNSUPPORTED_SHAPE, "head_dim %u", c.head_dim);
+            }
+            NET_TRY(hipGetLastError(), "attention");
+            hipLaunchKernelGGL(attn_combine_kernel, dim3(c.n_heads, n), dim3(std::min(256u, std::max(64u, (c.head_dim + 63) / 64 * 64))), ns * 4, s, net->part, net->att, c.n_heads,
+                               c.head_dim, ns);
+            NET_TRY(hipGetLastError(), "attention combine");
         }
-        NET_TRY(hipGetLastError(), "attention");
-        hipLaunchKernelGGL(attn_combine_kernel, dim3(c.n_heads, n), dim3(std::min(256u, std::max(64u, (c.head_dim + 63) / 64 * 64))), ns * 4, s, net->part, net->att, c.n_heads,
-                           c.head_dim, ns);
-        NET_TRY(hipGetLastError(), "attention combine");
         {
             float *const ys[1] = {net->x};
             if ((rc = product(net, n, &L.wo, 1, net->att, nullptr, ys, nullptr, HKHIP_ACCUMULATE))) return rc;
@@ -536,11 +691,20 @@ int hkhip_net_create(hkhip_engine *eng, const hkhip_net_config *cfg, hkhip_net *
     n->layers.resize(c.n_layers);
     int rc = HKHIP_OK;
     const uint64_t cache = uint64_t(c.n_layers) * c.n_kv_heads * c.max_ctx * c.head_dim * 2;
+    const uint64_t vtc = uint64_t(c.n_layers) * c.n_kv_heads * c.head_dim * vt_stride(c) * 2;
     if ((rc = dev_alloc(n, cache, (void **)&n->kc)) || (rc = dev_alloc(n, cache, (void **)&n->vc)) ||
+        (rc = dev_alloc(n, vtc, (void **)&n->vt)) ||
         (rc = dev_alloc(n, uint64_t(c.vocab) * 4, (void **)&n->logits)) ||
         (rc = dev_alloc(n, c.rope_dim / 2 * 4 + 4, (void **)&n->inv_freq)) || (rc = ensure_cap(n, MAX_DECODE))) {
         hkhip_net_destroy(n);
         return rc;
+    }
+    // Positions a pass has not written yet are read (and weighted by 0) by the prefill attention:
+    // they must hold finite values.
+    if (hipMemset(n->kc, 0, cache) != hipSuccess || hipMemset(n->vc, 0, cache) != hipSuccess ||
+        hipMemset(n->vt, 0, vtc) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+        hkhip_net_destroy(n);
+        return set_error(HKHIP_E_DEVICE_FAILED, "clearing the caches");
     }
     // ropeInvFreq without scaling (ops.zig:96-146): base^(-2i/n_rot) in f64, then f32.
     std::vector<float> f(c.rope_dim / 2 + 1, 0.0f);
