@@ -132,6 +132,34 @@ __global__ __launch_bounds__(64) void rope_kv_kernel(RopeArgs a) {
     }
 }
 
+// Value rows of a prefill pass to the f16 caches, 16 tokens of one key/value head per workgroup:
+// the rows go to the value cache as they are and, through an LDS tile, to the transposed cache
+// with consecutive lanes on consecutive positions (decode passes write both in rope_kv_kernel).
+__global__ __launch_bounds__(256) void v_cache_kernel(const float *__restrict__ v, __half *__restrict__ vc,
+                                                      __half *__restrict__ vt, const uint32_t *__restrict__ pos0,
+                                                      uint32_t n, uint32_t nkv, uint32_t hd, uint32_t max_ctx,
+                                                      uint32_t vt_stride) {
+    __shared__ __half tile[16][258];
+    const uint32_t g = blockIdx.x, t0 = blockIdx.y * 16, tid = threadIdx.x;
+    const uint32_t nt = n - t0 < 16 ? n - t0 : 16, pos = pos0[0] + t0, kvd = nkv * hd;
+    for (uint32_t i = 4 * tid; i < nt * hd; i += 1024) { // hd is a multiple of 64: four values of one row
+        const uint32_t tt = i / hd, d = i % hd;
+        const float4 x = *reinterpret_cast<const float4 *>(v + uint64_t(t0 + tt) * kvd + g * hd + d);
+        const __half h4[4] = {__float2half(x.x), __float2half(x.y), __float2half(x.z), __float2half(x.w)};
+        __half *dst = vc + (uint64_t(g) * max_ctx + pos + tt) * hd + d;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            dst[k] = h4[k];
+            tile[tt][d + k] = h4[k];
+        }
+    }
+    __syncthreads();
+    for (uint32_t i = tid; i < hd * 16; i += 256) {
+        const uint32_t d = i / 16, tt = i % 16;
+        if (tt < nt) vt[(uint64_t(g) * hd + d) * vt_stride + pos + tt] = tile[tt][d];
+    }
+}
+
 // Attention over one slice of the context for one (token, query head): one wave each, four per
 // workgroup. Per step of 64 positions every lane issues its position's key row (lane = position)
 // and its dimensions of all 64 value rows (lane = dimensions [DL*lane, DL*lane + DL)) before any
@@ -253,8 +281,10 @@ __global__ __launch_bounds__(256) void attn_slice_kernel(AttnArgs a) {
     for (int j = 0; j < DL; j++) out[2 + DL * lane + j] = acc[j];
 }
 
-// Prefill attention (passes of more than MAX_DECODE tokens) on the f16 MFMA units, one wave per
-// (32-token tile, query head), four per workgroup; no LDS, no barriers. Per tile of 32 positions:
+// Prefill attention (passes of more than MAX_DECODE tokens) on the f16 MFMA units, one workgroup
+// per (32-token tile, query head); its four waves take every fourth tile of 32 positions and merge
+// their partial results through LDS at the end (max / sum rescaling, as the slice merge does).
+// Per tile of 32 positions:
 //   S^T[pos][tok] = K[pos] . q[tok]: A = key rows (f16, exact), B = q split as f16 hi + lo (q - hi
 //       rounded again; together q to ~2^-22), two MFMA chains over head_dim in steps of 16;
 //   online softmax per token (a lane holds one token's 16 scores; the two lane halves meet by one
@@ -280,9 +310,8 @@ template <int HD>
 __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnPArgs a) {
     constexpr int NCH = HD / 16, NDT = HD / 32;
     const uint32_t lane = threadIdx.x & 63, h = lane >> 5, j = lane & 31;
-    const uint32_t item = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const uint32_t ntile = (a.n + 31) / 32;
-    if (item >= ntile * a.nh) return; // whole waves; the kernel has no barrier
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t item = blockIdx.x; // < ntile * nh (the grid)
     const uint32_t head = item % a.nh, tile = item / a.nh;
     const uint32_t kvh = head / (a.nh / a.nkv);
     const uint32_t pos0 = a.pos0[0];
@@ -313,7 +342,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnPArgs a) {
     const __half *kb = a.kc + uint64_t(kvh) * a.max_ctx * HD;
     const __half *vb = a.vt + uint64_t(kvh) * HD * a.vt_stride;
     const uint32_t rj = (j & ~12u) | ((j & 4u) << 1) | ((j & 8u) >> 1); // rho(j)
-    for (uint32_t p0 = 0; p0 < pend; p0 += 32) {
+    for (uint32_t p0 = 32 * wave; p0 < pend; p0 += 128) {
         v8h ka[NCH], va[NDT][2];
         {
             const uint32_t kp = p0 + rj < a.max_ctx ? p0 + rj : a.max_ctx - 1;
@@ -373,16 +402,51 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnPArgs a) {
             }
         }
     }
-    if (t < a.n) {
-        // acc[d][v]: dimension 32d + 8g + 4h + e of this lane's token.
-        const float inv = 1.0f / l;
-        float *o = a.att + (uint64_t(t) * a.nh + head) * HD;
+    // Merge: waves 1-3 leave {m, l, acc} in LDS (a wave without tiles: m = -inf, l = 0), wave 0
+    // rescales all four to the common maximum, sums and writes.
+    __shared__ float red_m[3][64], red_l[3][64];
+    __shared__ float4 red_acc[3][NDT * 4][64];
+    if (wave > 0) {
+        red_m[wave - 1][lane] = m;
+        red_l[wave - 1][lane] = l;
 #pragma unroll
         for (int d = 0; d < NDT; d++)
 #pragma unroll
             for (int g = 0; g < 4; g++)
-                *reinterpret_cast<float4 *>(o + 32 * d + 8 * g + 4 * h) =
-                    make_float4(acc[d][4 * g] * inv, acc[d][4 * g + 1] * inv, acc[d][4 * g + 2] * inv, acc[d][4 * g + 3] * inv);
+                red_acc[wave - 1][4 * d + g][lane] = make_float4(acc[d][4 * g], acc[d][4 * g + 1], acc[d][4 * g + 2], acc[d][4 * g + 3]);
+    }
+    __syncthreads();
+    if (wave > 0) return;
+    float big = m;
+#pragma unroll
+    for (int w = 0; w < 3; w++) big = fmaxf(big, red_m[w][lane]);
+    const float c0 = m == -INFINITY ? 0.0f : expf(m - big);
+    float lt = l * c0, cw[3];
+#pragma unroll
+    for (int w = 0; w < 3; w++) {
+        const float mw = red_m[w][lane];
+        cw[w] = mw == -INFINITY ? 0.0f : expf(mw - big);
+        lt = fmaf(red_l[w][lane], cw[w], lt);
+    }
+    if (t < a.n) {
+        // acc[d][v]: dimension 32d + 8g + 4h + e of this lane's token.
+        const float inv = 1.0f / lt;
+        float *o = a.att + (uint64_t(t) * a.nh + head) * HD;
+#pragma unroll
+        for (int d = 0; d < NDT; d++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                float4 r = make_float4(acc[d][4 * g] * c0, acc[d][4 * g + 1] * c0, acc[d][4 * g + 2] * c0, acc[d][4 * g + 3] * c0);
+#pragma unroll
+                for (int w = 0; w < 3; w++) {
+                    const float4 x = red_acc[w][4 * d + g][lane];
+                    r.x = fmaf(x.x, cw[w], r.x);
+                    r.y = fmaf(x.y, cw[w], r.y);
+                    r.z = fmaf(x.z, cw[w], r.z);
+                    r.w = fmaf(x.w, cw[w], r.w);
+                }
+                *reinterpret_cast<float4 *>(o + 32 * d + 8 * g + 4 * h) = make_float4(r.x * inv, r.y * inv, r.z * inv, r.w * inv);
+            }
     }
 }
 
@@ -619,12 +683,20 @@ int run_pass(hkhip_net *net, uint32_t n) {
         RopeArgs ra{net->q, net->k, net->v, L.q_norm, L.k_norm, net->inv_freq, net->kc + li * cache_layer,
                     net->vc + li * cache_layer, net->vt + li * vt_layer, net->pos, c.n_heads, c.n_kv_heads, c.head_dim,
                     c.rope_dim / 2, c.rope_neox, c.max_ctx, vt_stride(c), c.rms_eps};
-        hipLaunchKernelGGL(rope_kv_kernel, dim3(c.n_heads + 2 * c.n_kv_heads, n), dim3(64), 0, s, ra);
+        // Prefill passes write the value heads with v_cache_kernel (coalesced transposed writes).
+        const bool vsep = n > MAX_DECODE;
+        hipLaunchKernelGGL(rope_kv_kernel, dim3(c.n_heads + (vsep ? 1 : 2) * c.n_kv_heads, n), dim3(64), 0, s, ra);
         NET_TRY(hipGetLastError(), "rope / kv write");
+        if (vsep) {
+            hipLaunchKernelGGL(v_cache_kernel, dim3(c.n_kv_heads, (n + 15) / 16), dim3(256), 0, s, net->v,
+                               net->vc + li * cache_layer, net->vt + li * vt_layer, net->pos, n, c.n_kv_heads, c.head_dim,
+                               c.max_ctx, vt_stride(c));
+            NET_TRY(hipGetLastError(), "value cache");
+        }
         if (n > MAX_DECODE && prefill_mfma(c)) {
             AttnPArgs pa{net->q, net->kc + li * cache_layer, net->vt + li * vt_layer, net->att, net->pos, n, c.n_heads,
                          c.n_kv_heads, c.max_ctx, vt_stride(c), 1.0f / sqrtf(float(c.head_dim))};
-            const dim3 pg(((n + 31) / 32 * c.n_heads + 3) / 4), pb(256);
+            const dim3 pg((n + 31) / 32 * c.n_heads), pb(256);
             if (c.head_dim == 64)
                 hipLaunchKernelGGL(attn_prefill_kernel<64>, pg, pb, 0, s, pa);
             else
