@@ -267,7 +267,7 @@ __global__ __launch_bounds__(256) void attn_slice_kernel(AttnArgs a) {
         for (int j = 0; j < DL; j++) acc[j] *= corr;
 #pragma unroll
         for (int i = 0; i < 64; i++) {
-            const float pi = __shfl(pr, i); // 0 for positions past the slice
+            const float pi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pr), i)); // 0 past the slice
 #pragma unroll
             for (int j = 0; j < DL; j++) acc[j] = fmaf(pi, vr[i].get(j), acc[j]);
         }
@@ -279,6 +279,126 @@ __global__ __launch_bounds__(256) void attn_slice_kernel(AttnArgs a) {
     }
 #pragma unroll
     for (int j = 0; j < DL; j++) out[2 + DL * lane + j] = acc[j];
+}
+
+// Decode attention (passes of up to MAX_DECODE tokens): one workgroup of NWV waves per (query
+// head, token); wave w takes the 64-position steps w, w + NWV, ... of the context up to the
+// token's position, and the waves' {max, sum, acc} are merged in LDS at the end, as the slice
+// merge does (attention.zig:113-133) -- no partials in memory, no second launch. In a step a lane
+// loads its position's key row (scores: lane = position), then the value rows go 16 bytes per
+// lane: lane = (row r of the RPI rows one load covers, 8 dimensions), so a step is HD/8 + 64/RPI
+// loads per lane; the RPI partial sums of a dimension are added across lanes once, at the end.
+template <int HD, int NWV>
+__global__ __launch_bounds__(NWV * 64) void attn_decode_kernel(AttnArgs a, float *__restrict__ att) {
+    constexpr int LPR = HD / 8, RPI = 64 / LPR, NI = 64 / RPI; // lanes per value row, rows per load, loads
+    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const uint32_t vr_ = lane / LPR, vc = lane % LPR; // value row within a load, dimension chunk
+    const uint32_t h = blockIdx.x, t = blockIdx.y;
+    __shared__ float qs[NWV][HD];
+    __shared__ float red_m[NWV], red_l[NWV];
+    __shared__ float red_acc[NWV][HD];
+    const uint32_t kvh = h / (a.nh / a.nkv);
+    const uint32_t pos = a.pos0[0] + t;
+    const uint32_t nstep = pos / 64 + 1;
+    const float *qsrc = a.q + (uint64_t(t) * a.nh + h) * HD;
+    float qv[HD / 64];
+#pragma unroll
+    for (int j = 0; j < HD / 64; j++) qv[j] = qsrc[lane + 64 * j];
+    float m = -INFINITY, l = 0.0f, acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) acc[j] = 0.0f;
+    const __half *kb = a.kc + uint64_t(kvh) * a.max_ctx * HD;
+    const __half *vb = a.vc + uint64_t(kvh) * a.max_ctx * HD + 8 * vc;
+    const float *qw = qs[w];
+    bool first = true;
+    for (uint32_t st = w; st < nstep; st += NWV) {
+        const uint32_t p0 = 64 * st, p_end = min(p0 + 64, pos + 1);
+        const uint32_t pp = p0 + lane, last = p_end - 1;
+        uint4 kr[HD / 8], vv[NI];
+        const uint4 *krow = reinterpret_cast<const uint4 *>(kb + uint64_t(pp < p_end ? pp : last) * HD);
+#pragma unroll
+        for (int c = 0; c < HD / 8; c++) kr[c] = krow[c];
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const uint32_t pv = p0 + RPI * i + vr_;
+            vv[i] = *reinterpret_cast<const uint4 *>(vb + uint64_t(pv < p_end ? pv : last) * HD);
+        }
+        if (first) { // q (loaded before the keys) to this wave's LDS row
+#pragma unroll
+            for (int j = 0; j < HD / 64; j++) qs[w][lane + 64 * j] = qv[j];
+            first = false;
+        }
+#pragma unroll
+        for (int c = 0; c < HD / 8; c++) asm volatile("" : "+v"(kr[c].x), "+v"(kr[c].y), "+v"(kr[c].z), "+v"(kr[c].w));
+#pragma unroll
+        for (int i = 0; i < NI; i++) asm volatile("" : "+v"(vv[i].x), "+v"(vv[i].y), "+v"(vv[i].z), "+v"(vv[i].w));
+        float dot = 0.0f;
+#pragma unroll
+        for (int c = 0; c < HD / 8; c++) {
+            const __half2 *hp = reinterpret_cast<const __half2 *>(&kr[c]);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float2 f = __half22float2(hp[e]);
+                dot = fmaf(qw[8 * c + 2 * e], f.x, dot);
+                dot = fmaf(qw[8 * c + 2 * e + 1], f.y, dot);
+            }
+        }
+        const float s = pp < p_end ? dot * a.scale : -INFINITY;
+        float mx = s;
+        for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        const float mn = fmaxf(m, mx);
+        const float pr = pp < p_end ? expf(s - mn) : 0.0f;
+        float ps = pr;
+        for (int o = 32; o >= 1; o >>= 1) ps += __shfl_xor(ps, o);
+        const float corr = m == -INFINITY ? 0.0f : expf(m - mn);
+        l = l * corr + ps;
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc[j] *= corr;
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const float pi = __shfl(pr, RPI * i + vr_); // 0 for positions past the step
+            const __half2 *hp = reinterpret_cast<const __half2 *>(&vv[i]);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float2 f = __half22float2(hp[e]);
+                acc[2 * e] = fmaf(pi, f.x, acc[2 * e]);
+                acc[2 * e + 1] = fmaf(pi, f.y, acc[2 * e + 1]);
+            }
+        }
+        m = mn;
+    }
+    // The RPI row groups' sums of each dimension chunk (lanes vc, vc + LPR, ...).
+#pragma unroll
+    for (int o = LPR; o < 64; o <<= 1)
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc[j] += __shfl_xor(acc[j], o);
+    if (lane == 0) {
+        red_m[w] = m;
+        red_l[w] = l;
+    }
+    if (lane < LPR) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) red_acc[w][8 * lane + j] = acc[j];
+    }
+    __syncthreads();
+    float big = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NWV; i++)
+        if (red_l[i] != 0.0f) big = fmaxf(big, red_m[i]);
+    float tot = 0.0f, wt[NWV];
+#pragma unroll
+    for (int i = 0; i < NWV; i++) {
+        wt[i] = red_l[i] != 0.0f ? expf(red_m[i] - big) : 0.0f;
+        tot = fmaf(wt[i], red_l[i], tot);
+    }
+    const float inv = 1.0f / tot;
+    float *o = att + (uint64_t(t) * a.nh + h) * HD;
+    for (uint32_t d = threadIdx.x; d < HD; d += NWV * 64) {
+        float v = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NWV; i++) v = fmaf(wt[i], red_acc[i][d], v);
+        o[d] = v * inv;
+    }
 }
 
 // Prefill attention (passes of more than MAX_DECODE tokens) on the f16 MFMA units, one workgroup
@@ -613,8 +733,7 @@ int ensure_cap(hkhip_net *n, uint32_t want) {
         (rc = dev_alloc(n, T * qdim(c) * 4, (void **)&n->q)) || (rc = dev_alloc(n, T * kvdim(c) * 4, (void **)&n->k)) ||
         (rc = dev_alloc(n, T * kvdim(c) * 4, (void **)&n->v)) || (rc = dev_alloc(n, T * qdim(c) * 4, (void **)&n->att)) ||
         (rc = dev_alloc(n, T * 2 * c.ffn_dim * 4, (void **)&n->gu)) || (rc = dev_alloc(n, T * c.ffn_dim * 4, (void **)&n->h)) ||
-        (rc = dev_alloc(n, (prefill_mfma(c) ? std::min<uint64_t>(T, MAX_DECODE) : T) * c.n_heads * nslices(c) * (c.head_dim + 2) * 4,
-                        (void **)&n->part)) ||
+        (rc = dev_alloc(n, (prefill_mfma(c) ? 1 : T) * c.n_heads * nslices(c) * (c.head_dim + 2) * 4, (void **)&n->part)) ||
         (rc = dev_alloc(n, hkhip_act_bytes(want, maxk), (void **)&n->xq)) ||
         (rc = dev_alloc(n, (T + 1) * 4, (void **)&n->io)))
         return rc;
@@ -702,6 +821,17 @@ int run_pass(hkhip_net *net, uint32_t n) {
             else
                 hipLaunchKernelGGL(attn_prefill_kernel<128>, pg, pb, 0, s, pa);
             NET_TRY(hipGetLastError(), "prefill attention");
+        } else if (n <= MAX_DECODE) {
+            AttnArgs aa{net->q, net->kc + li * cache_layer, net->vc + li * cache_layer, nullptr, net->pos, n, c.n_heads,
+                        c.n_kv_heads, c.head_dim, c.max_ctx, 0, 1.0f / sqrtf(float(c.head_dim))};
+            const dim3 dg(c.n_heads, n);
+            if (c.head_dim == 64)
+                hipLaunchKernelGGL((attn_decode_kernel<64, 8>), dg, dim3(512), 0, s, aa, net->att);
+            else if (c.head_dim == 128)
+                hipLaunchKernelGGL((attn_decode_kernel<128, 8>), dg, dim3(512), 0, s, aa, net->att);
+            else
+                hipLaunchKernelGGL((attn_decode_kernel<256, 4>), dg, dim3(256), 0, s, aa, net->att);
+            NET_TRY(hipGetLastError(), "decode attention");
         } else {
             AttnArgs aa{net->q, net->kc + li * cache_layer, net->vc + li * cache_layer, net->part, net->pos, n, c.n_heads,
                         c.n_kv_heads, c.head_dim, c.max_ctx, ns, 1.0f / sqrtf(float(c.head_dim))};
