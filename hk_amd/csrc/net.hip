@@ -281,19 +281,21 @@ __global__ __launch_bounds__(256) void attn_slice_kernel(AttnArgs a) {
     for (int j = 0; j < DL; j++) out[2 + DL * lane + j] = acc[j];
 }
 
-// Decode attention (passes of up to MAX_DECODE tokens): one workgroup of NWV waves per (query
-// head, token); wave w takes the 64-position steps w, w + NWV, ... of the context up to the
-// token's position, and the waves' {max, sum, acc} are merged in LDS at the end, as the slice
-// merge does (attention.zig:113-133) -- no partials in memory, no second launch. In a step a lane
+// Decode attention (passes of up to MAX_DECODE tokens): G workgroups of NWV waves per (query head,
+// token), G fixed by the context length so that every 64-position step of a full context has a
+// wave of its own (the context's loads spread over G times more CUs than one workgroup would
+// use); wave w of chunk g takes step g*NWV + w. A workgroup merges its waves' {max, sum, acc} in
+// LDS (as the slice merge does, attention.zig:113-133) and writes the chunk's partial ({-inf, 0,
+// 0...} past the token's position); attn_combine_kernel merges the G partials. In a step a lane
 // loads its position's key row (scores: lane = position), then the value rows go 16 bytes per
 // lane: lane = (row r of the RPI rows one load covers, 8 dimensions), so a step is HD/8 + 64/RPI
 // loads per lane; the RPI partial sums of a dimension are added across lanes once, at the end.
 template <int HD, int NWV>
-__global__ __launch_bounds__(NWV * 64) void attn_decode_kernel(AttnArgs a, float *__restrict__ att) {
+__global__ __launch_bounds__(NWV * 64) void attn_decode_kernel(AttnArgs a) {
     constexpr int LPR = HD / 8, RPI = 64 / LPR, NI = 64 / RPI; // lanes per value row, rows per load, loads
     const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const uint32_t vr_ = lane / LPR, vc = lane % LPR; // value row within a load, dimension chunk
-    const uint32_t h = blockIdx.x, t = blockIdx.y;
+    const uint32_t g = blockIdx.x, h = blockIdx.y, t = blockIdx.z;
     __shared__ float qs[NWV][HD];
     __shared__ float red_m[NWV], red_l[NWV];
     __shared__ float red_acc[NWV][HD];
@@ -311,7 +313,7 @@ __global__ __launch_bounds__(NWV * 64) void attn_decode_kernel(AttnArgs a, float
     const __half *vb = a.vc + uint64_t(kvh) * a.max_ctx * HD + 8 * vc;
     const float *qw = qs[w];
     bool first = true;
-    for (uint32_t st = w; st < nstep; st += NWV) {
+    for (uint32_t st = g * NWV + w; st < nstep; st += gridDim.x * NWV) {
         const uint32_t p0 = 64 * st, p_end = min(p0 + 64, pos + 1);
         const uint32_t pp = p0 + lane, last = p_end - 1;
         uint4 kr[HD / 8], vv[NI];
@@ -391,13 +393,17 @@ __global__ __launch_bounds__(NWV * 64) void attn_decode_kernel(AttnArgs a, float
         wt[i] = red_l[i] != 0.0f ? expf(red_m[i] - big) : 0.0f;
         tot = fmaf(wt[i], red_l[i], tot);
     }
-    const float inv = 1.0f / tot;
-    float *o = att + (uint64_t(t) * a.nh + h) * HD;
+    // The chunk's partial: {max, sum, acc} (unnormalized), as attn_combine_kernel reads them.
+    float *out = a.part + ((uint64_t(t) * a.nh + h) * gridDim.x + g) * (HD + 2);
     for (uint32_t d = threadIdx.x; d < HD; d += NWV * 64) {
         float v = 0.0f;
 #pragma unroll
         for (int i = 0; i < NWV; i++) v = fmaf(wt[i], red_acc[i][d], v);
-        o[d] = v * inv;
+        out[2 + d] = v;
+    }
+    if (threadIdx.x == 0) {
+        out[0] = big;
+        out[1] = tot;
     }
 }
 
@@ -733,7 +739,8 @@ int ensure_cap(hkhip_net *n, uint32_t want) {
         (rc = dev_alloc(n, T * qdim(c) * 4, (void **)&n->q)) || (rc = dev_alloc(n, T * kvdim(c) * 4, (void **)&n->k)) ||
         (rc = dev_alloc(n, T * kvdim(c) * 4, (void **)&n->v)) || (rc = dev_alloc(n, T * qdim(c) * 4, (void **)&n->att)) ||
         (rc = dev_alloc(n, T * 2 * c.ffn_dim * 4, (void **)&n->gu)) || (rc = dev_alloc(n, T * c.ffn_dim * 4, (void **)&n->h)) ||
-        (rc = dev_alloc(n, (prefill_mfma(c) ? 1 : T) * c.n_heads * nslices(c) * (c.head_dim + 2) * 4, (void **)&n->part)) ||
+        (rc = dev_alloc(n, (prefill_mfma(c) ? MAX_DECODE : std::max<uint64_t>(T, MAX_DECODE)) * c.n_heads * nslices(c) * (c.head_dim + 2) * 4,
+                        (void **)&n->part)) ||
         (rc = dev_alloc(n, hkhip_act_bytes(want, maxk), (void **)&n->xq)) ||
         (rc = dev_alloc(n, (T + 1) * 4, (void **)&n->io)))
         return rc;
@@ -824,14 +831,19 @@ int run_pass(hkhip_net *net, uint32_t n) {
         } else if (n <= MAX_DECODE) {
             AttnArgs aa{net->q, net->kc + li * cache_layer, net->vc + li * cache_layer, nullptr, net->pos, n, c.n_heads,
                         c.n_kv_heads, c.head_dim, c.max_ctx, 0, 1.0f / sqrtf(float(c.head_dim))};
-            const dim3 dg(c.n_heads, n);
+            aa.part = net->part;
+            const uint32_t G = (ns + 3) / 4;
+            const dim3 dg(G, c.n_heads, n);
             if (c.head_dim == 64)
-                hipLaunchKernelGGL((attn_decode_kernel<64, 8>), dg, dim3(512), 0, s, aa, net->att);
+                hipLaunchKernelGGL((attn_decode_kernel<64, 4>), dg, dim3(256), 0, s, aa);
             else if (c.head_dim == 128)
-                hipLaunchKernelGGL((attn_decode_kernel<128, 8>), dg, dim3(512), 0, s, aa, net->att);
+                hipLaunchKernelGGL((attn_decode_kernel<128, 4>), dg, dim3(256), 0, s, aa);
             else
-                hipLaunchKernelGGL((attn_decode_kernel<256, 4>), dg, dim3(256), 0, s, aa, net->att);
+                hipLaunchKernelGGL((attn_decode_kernel<256, 4>), dg, dim3(256), 0, s, aa);
             NET_TRY(hipGetLastError(), "decode attention");
+            hipLaunchKernelGGL(attn_combine_kernel, dim3(c.n_heads, n), dim3(std::min(256u, std::max(64u, (c.head_dim + 63) / 64 * 64))),
+                               G * 4, s, net->part, net->att, c.n_heads, c.head_dim, G);
+            NET_TRY(hipGetLastError(), "decode attention combine");
         } else {
             AttnArgs aa{net->q, net->kc + li * cache_layer, net->vc + li * cache_layer, net->part, net->pos, n, c.n_heads,
                         c.n_kv_heads, c.head_dim, c.max_ctx, ns, 1.0f / sqrtf(float(c.head_dim))};

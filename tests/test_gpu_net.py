@@ -126,3 +126,30 @@ def test_net_from_hk_file(eng, tmp_path, arch, fmt, tie, vec_type):
                 pos += n
         finally:
             net.close()
+
+
+def test_net_long_context(eng):
+    """Decode passes past 512 positions, where a decode attention wave takes more than one
+    64-position step (eight waves per (head, token)); a prefill of 1030 tokens (four-wave MFMA
+    tiles over 33 position tiles) before them."""
+    from hk_amd.net import Net
+
+    cfg = Config(dim=128, n_layers=1, n_heads=2, n_kv_heads=1, head_dim=64, ffn_dim=256, vocab=256, max_ctx=1100,
+                 rope_neox=True, rope_base=1e4)
+    model = synth.model_np(cfg, F.Q8_0, seed=4500, out_fmt=F.Q8_0, embd_fmt=F.Q8_0, qk_norm=False, bias=False)
+    rng = np.random.default_rng(4501)
+    cpu = Oracle(cfg, model)
+    worst = 0.0
+    with Net(eng, cfg) as net:
+        net.load(model)
+        pos = 0
+        for n in [1030, 1, 1, 3, 8, 8, 1]:
+            toks = rng.integers(0, cfg.vocab, n)
+            net.forward(toks, pos)
+            got, want = net.logits().astype(np.float64), cpu.forward(toks, pos).astype(np.float64)
+            err = float(np.max(np.abs(got - want)) / np.max(np.abs(want)))
+            worst = max(worst, err)
+            check(got, want, f"long context: pass of {n} at {pos}")
+            pos += n
+    print("long context: worst relative logit error", worst)
+    assert worst <= 1e-3
