@@ -300,8 +300,6 @@ __global__ __launch_bounds__(NWV * 64) void attn_decode_kernel(AttnArgs a) {
     __shared__ float red_m[NWV], red_l[NWV];
     __shared__ float red_acc[NWV][HD];
     const uint32_t kvh = h / (a.nh / a.nkv);
-    const uint32_t pos = a.pos0[0] + t;
-    const uint32_t nstep = pos / 64 + 1;
     const float *qsrc = a.q + (uint64_t(t) * a.nh + h) * HD;
     float qv[HD / 64];
 #pragma unroll
@@ -312,24 +310,27 @@ __global__ __launch_bounds__(NWV * 64) void attn_decode_kernel(AttnArgs a) {
     const __half *kb = a.kc + uint64_t(kvh) * a.max_ctx * HD;
     const __half *vb = a.vc + uint64_t(kvh) * a.max_ctx * HD + 8 * vc;
     const float *qw = qs[w];
-    bool first = true;
-    for (uint32_t st = g * NWV + w; st < nstep; st += gridDim.x * NWV) {
-        const uint32_t p0 = 64 * st, p_end = min(p0 + 64, pos + 1);
-        const uint32_t pp = p0 + lane, last = p_end - 1;
-        uint4 kr[HD / 8], vv[NI];
-        const uint4 *krow = reinterpret_cast<const uint4 *>(kb + uint64_t(pp < p_end ? pp : last) * HD);
+    // The launch gives every 64-position step of the context a wave of its own (G * NWV steps), so
+    // a wave has one step, and its loads need not wait for the position: rows are clamped to the
+    // cache only, and rows past the token's position (finite: the caches start zeroed) are masked.
+    const uint32_t p0 = 64 * (g * NWV + w);
+    const uint32_t pp = p0 + lane, lastc = a.max_ctx - 1;
+    uint4 kr[HD / 8], vv[NI];
+    {
+        const uint4 *krow = reinterpret_cast<const uint4 *>(kb + uint64_t(pp < lastc ? pp : lastc) * HD);
 #pragma unroll
         for (int c = 0; c < HD / 8; c++) kr[c] = krow[c];
 #pragma unroll
         for (int i = 0; i < NI; i++) {
             const uint32_t pv = p0 + RPI * i + vr_;
-            vv[i] = *reinterpret_cast<const uint4 *>(vb + uint64_t(pv < p_end ? pv : last) * HD);
+            vv[i] = *reinterpret_cast<const uint4 *>(vb + uint64_t(pv < lastc ? pv : lastc) * HD);
         }
-        if (first) { // q (loaded before the keys) to this wave's LDS row
+    }
+    const uint32_t pos = a.pos0[0] + t;
+    if (p0 <= pos) {
+        const uint32_t p_end = min(p0 + 64, pos + 1);
 #pragma unroll
-            for (int j = 0; j < HD / 64; j++) qs[w][lane + 64 * j] = qv[j];
-            first = false;
-        }
+        for (int j = 0; j < HD / 64; j++) qs[w][lane + 64 * j] = qv[j];
 #pragma unroll
         for (int c = 0; c < HD / 8; c++) asm volatile("" : "+v"(kr[c].x), "+v"(kr[c].y), "+v"(kr[c].z), "+v"(kr[c].w));
 #pragma unroll
