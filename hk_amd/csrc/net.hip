@@ -752,6 +752,15 @@ int ensure_cap(hkhip_net *n, uint32_t want) {
     return HKHIP_OK;
 }
 
+// The prefill products on the quantized input already in net->xq.
+int gemms(hkhip_net *net, uint32_t n, const hkhip_mat *mats, uint32_t nparts, float *const *ys, const float *const *biases,
+          int mode) {
+    int rc = HKHIP_OK;
+    for (uint32_t i = 0; !rc && i < nparts; i++)
+        rc = hkhip_mm(net->eng, &mats[i], net->xq, ys[i], n, biases ? biases[i] : nullptr, mode);
+    return rc;
+}
+
 // The products of one pass. xin: f32 input [n][cols]; norm: fused RMS norm weights or null.
 int product(hkhip_net *net, uint32_t n, const hkhip_mat *mats, uint32_t nparts, const float *xin, const float *norm,
             float *const *ys, const float *const *biases, int mode) {
@@ -766,6 +775,11 @@ int product(hkhip_net *net, uint32_t n, const hkhip_mat *mats, uint32_t nparts, 
             xin = net->xb;
         }
         return hkhip_matvec_parts(eng, mats, nparts, xin, nullptr, n, ys, biases, mode);
+    }
+    if (norm && act_kind(mats[0].t) != HKHIP_ACT_F32) { // the norm folded into the quantizer
+        NET_TRY(launch_qact_row(xin, n, cols, act_kind(mats[0].t), net->xq, norm, net->cfg.rms_eps, false, eng->cur),
+                "rmsnorm + qact");
+        return gemms(net, n, mats, nparts, ys, biases, mode);
     }
     if (norm) {
         hipLaunchKernelGGL(rmsnorm_kernel, dim3(n), dim3(256), 0, eng->cur, xin, norm, net->xb, cols, net->cfg.rms_eps);
@@ -783,10 +797,8 @@ int product(hkhip_net *net, uint32_t n, const hkhip_mat *mats, uint32_t nparts, 
         }
         return rc;
     }
-    int rc = hkhip_qact(eng, xin, n, cols, act_kind(mats[0].t), net->xq);
-    for (uint32_t i = 0; !rc && i < nparts; i++)
-        rc = hkhip_mm(eng, &mats[i], net->xq, ys[i], n, biases ? biases[i] : nullptr, mode);
-    return rc;
+    const int rc = hkhip_qact(eng, xin, n, cols, act_kind(mats[0].t), net->xq);
+    return rc ? rc : gemms(net, n, mats, nparts, ys, biases, mode);
 }
 
 int run_pass(hkhip_net *net, uint32_t n) {
@@ -870,6 +882,13 @@ int run_pass(hkhip_net *net, uint32_t n) {
         } else {
             float *const ys[1] = {net->gu};
             if ((rc = product(net, n, &L.wgu, 1, net->x, L.ffn_norm, ys, nullptr, HKHIP_STORE))) return rc;
+            if (act_kind(L.wd.t) != HKHIP_ACT_F32) { // silu(gate) * up folded into the down input's quantizer
+                NET_TRY(launch_qact_row(net->gu, n, c.ffn_dim, act_kind(L.wd.t), net->xq, nullptr, 0.0f, true, s),
+                        "swiglu + qact");
+                float *const yd[1] = {net->x};
+                if ((rc = gemms(net, n, &L.wd, 1, yd, nullptr, HKHIP_ACCUMULATE))) return rc;
+                continue;
+            }
             const uint64_t total = uint64_t(n) * c.ffn_dim;
             hipLaunchKernelGGL(swiglu_pairs_kernel, dim3(uint32_t((total + 255) / 256)), dim3(256), 0, s, net->gu, net->h,
                                total);

@@ -4,35 +4,45 @@
 
 namespace hkhip {
 
-// A8: one thread per value; a 32-lane half-wave owns one block. dsb (a8_dsb; null when k is
-// not a multiple of 256): d * s in three bf16 parts, [k/256][n][3][8].
-__global__ void qact_a8_kernel(const float *__restrict__ x, uint64_t total, int8_t *__restrict__ qs,
-                               float *__restrict__ dout, int32_t *__restrict__ sout, float *__restrict__ dsout,
-                               uint16_t *__restrict__ dsb, uint32_t n, uint32_t kb) {
-    const uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    const A8Q r = quant_a8_halfwave(i < total ? x[i] : 0.0f);
-    if (i < total) {
-        qs[i] = (int8_t)r.q;
-        if ((i & 31) == 0) {
-            const uint64_t b = i / 32;
-            const float ds = r.d * (float)r.s;
-            dout[b] = r.d;
-            sout[b] = r.s;
-            dsout[b] = ds;
-            if (dsb) {
-                // hi keeps the leading 8 significant bits, mid the next 8, lo the rest (<= 8).
-                const uint32_t t = uint32_t(b / kb), c = uint32_t(b % kb);
-                const uint32_t p0 = __builtin_bit_cast(uint32_t, ds) & 0xFFFF0000u;
-                const float r1 = ds - __builtin_bit_cast(float, p0);
-                const uint32_t p1 = __builtin_bit_cast(uint32_t, r1) & 0xFFFF0000u;
-                const uint32_t p2 = __builtin_bit_cast(uint32_t, r1 - __builtin_bit_cast(float, p1));
-                uint16_t *o = dsb + ((uint64_t(c / 8) * n + t) * 3) * 8 + c % 8;
-                o[0] = uint16_t(p0 >> 16);
-                o[8] = uint16_t(p1 >> 16);
-                o[16] = uint16_t(p2 >> 16);
-            }
+// The A8 planes (dsb, a8_dsb: null when k is not a multiple of 256: d * s in three bf16 parts,
+// [k/256][n][3][8]).
+struct A8Out {
+    int8_t *qs;
+    float *d;
+    int32_t *s;
+    float *ds;
+    uint16_t *dsb;
+    uint32_t n, kb; // tokens, blocks per row
+};
+// Value i of the input (block i / 32); the lane of each block's first value writes the block's data.
+__device__ __forceinline__ void a8_out(const A8Out &o, uint64_t i, const A8Q &r) {
+    o.qs[i] = (int8_t)r.q;
+    if ((i & 31) == 0) {
+        const uint64_t b = i / 32;
+        const float ds = r.d * (float)r.s;
+        o.d[b] = r.d;
+        o.s[b] = r.s;
+        o.ds[b] = ds;
+        if (o.dsb) {
+            // hi keeps the leading 8 significant bits, mid the next 8, lo the rest (<= 8).
+            const uint32_t t = uint32_t(b / o.kb), c = uint32_t(b % o.kb);
+            const uint32_t p0 = __builtin_bit_cast(uint32_t, ds) & 0xFFFF0000u;
+            const float r1 = ds - __builtin_bit_cast(float, p0);
+            const uint32_t p1 = __builtin_bit_cast(uint32_t, r1) & 0xFFFF0000u;
+            const uint32_t p2 = __builtin_bit_cast(uint32_t, r1 - __builtin_bit_cast(float, p1));
+            uint16_t *q = o.dsb + ((uint64_t(c / 8) * o.n + t) * 3) * 8 + c % 8;
+            q[0] = uint16_t(p0 >> 16);
+            q[8] = uint16_t(p1 >> 16);
+            q[16] = uint16_t(p2 >> 16);
         }
     }
+}
+
+// A8: one thread per value; a 32-lane half-wave owns one block.
+__global__ void qact_a8_kernel(const float *__restrict__ x, uint64_t total, A8Out o) {
+    const uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const A8Q r = quant_a8_halfwave(i < total ? x[i] : 0.0f);
+    if (i < total) a8_out(o, i, r);
 }
 
 // Q8K: one wave per 256-value block, four consecutive values per lane.
@@ -52,13 +62,21 @@ struct QactIl {
     uint32_t tiles, n, nsb;
 };
 
-__global__ void qact_q8k_kernel(const float *__restrict__ x, uint64_t nblocks, int8_t *__restrict__ qs,
-                                float *__restrict__ dout, int16_t *__restrict__ bsout, uint16_t *__restrict__ mbout,
-                                float *__restrict__ dbout, QactIl il) {
-    const uint32_t lane = threadIdx.x & 63;
-    const uint64_t b = (uint64_t(blockIdx.x) * blockDim.x + threadIdx.x) / 64;
-    if (b >= nblocks) return; // whole waves exit together
-    const Q8KQ r = quant_q8k_wave(reinterpret_cast<const float4 *>(x + b * QK_K)[lane], lane);
+struct Q8KOut {
+    int8_t *qs;
+    float *d;
+    int16_t *bs;
+    uint16_t *mb;
+    float *db;
+    QactIl il;
+};
+// Block b of the input, quantized by one wave (r: this lane's part).
+__device__ __forceinline__ void q8k_out(const Q8KOut &o, uint64_t b, uint32_t lane, const Q8KQ &r) {
+    int8_t *qs = o.qs;
+    float *dout = o.d, *dbout = o.db;
+    int16_t *bsout = o.bs;
+    uint16_t *mbout = o.mb;
+    const QactIl &il = o.il;
     reinterpret_cast<uint32_t *>(qs + b * QK_K)[lane] = r.packed;
     if ((lane & 3) == 0) bsout[b * 16 + lane / 4] = (int16_t)r.bsum;
     if (lane == 0) dout[b] = r.d;
@@ -89,30 +107,108 @@ __global__ void qact_q8k_kernel(const float *__restrict__ x, uint64_t nblocks, i
     }
 }
 
+__global__ void qact_q8k_kernel(const float *__restrict__ x, uint64_t nblocks, Q8KOut o) {
+    const uint32_t lane = threadIdx.x & 63;
+    const uint64_t b = (uint64_t(blockIdx.x) * blockDim.x + threadIdx.x) / 64;
+    if (b >= nblocks) return; // whole waves exit together
+    q8k_out(o, b, lane, quant_q8k_wave(reinterpret_cast<const float4 *>(x + b * QK_K)[lane], lane));
+}
+
+// The quantizers with the producer's last step folded in, one workgroup of 256 threads per token
+// row (k values):
+//   norm:  value i = (x[i] * inv) * norm[i], inv = 1 / sqrt(mean(x^2) + eps) (ops.zig:10-29; the
+//          sum of squares in the order of the standalone RMS norm kernel: 256 strided partial
+//          sums, then the workgroup reduction);
+//   pairs: value i = silu(x[2i]) * x[2i + 1] (x holds 2k values per row: gate/up interleaved,
+//          ops.zig:70-80 swiglu).
+// Then each block is quantized as qact_a8_kernel / qact_q8k_kernel quantize it.
+struct RowIn {
+    const float *x;
+    const float *norm; // or null
+    float eps;
+    int pairs;
+    uint32_t k;
+};
+__device__ __forceinline__ float row_value(const RowIn &in, const float *xr, float inv, uint32_t i) {
+    if (in.pairs) return silu_mul(xr[2 * i], xr[2 * i + 1]);
+    if (in.norm) return (xr[i] * inv) * in.norm[i];
+    return xr[i];
+}
+__device__ __forceinline__ float row_inv(const RowIn &in, const float *xr) {
+    __shared__ float red[4];
+    if (!in.norm) return 1.0f;
+    float ss = 0.0f;
+    for (uint32_t i = threadIdx.x; i < in.k; i += 256) ss = fmaf(xr[i], xr[i], ss);
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    ss = red[0] + red[1] + red[2] + red[3];
+    return __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, float(in.k)) + in.eps));
+}
+
+__global__ __launch_bounds__(256) void qact_a8_row_kernel(RowIn in, A8Out o) {
+    const uint32_t t = blockIdx.x;
+    const float *xr = in.x + uint64_t(t) * in.k * (in.pairs ? 2 : 1);
+    const float inv = row_inv(in, xr);
+    for (uint32_t i0 = 0; i0 < in.k; i0 += 256) { // k is a multiple of 32: whole half-waves
+        const uint32_t i = i0 + threadIdx.x;
+        const bool live = i < in.k;
+        const A8Q r = quant_a8_halfwave(live ? row_value(in, xr, inv, i) : 0.0f);
+        if (live) a8_out(o, uint64_t(t) * in.k + i, r);
+    }
+}
+
+__global__ __launch_bounds__(256) void qact_q8k_row_kernel(RowIn in, Q8KOut o) {
+    const uint32_t t = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const float *xr = in.x + uint64_t(t) * in.k * (in.pairs ? 2 : 1);
+    const float inv = row_inv(in, xr);
+    const uint32_t nsb = in.k / QK_K;
+    for (uint32_t sb = w; sb < nsb; sb += 4) {
+        const uint32_t i = sb * QK_K + 4 * lane;
+        const float4 v = make_float4(row_value(in, xr, inv, i), row_value(in, xr, inv, i + 1),
+                                     row_value(in, xr, inv, i + 2), row_value(in, xr, inv, i + 3));
+        q8k_out(o, uint64_t(t) * nsb + sb, lane, quant_q8k_wave(v, lane));
+    }
+}
+
+static A8Out a8_planes(uint8_t *xq, const ActLayout &L, uint32_t n, uint32_t k) {
+    return A8Out{reinterpret_cast<int8_t *>(xq + L.a8_qs), reinterpret_cast<float *>(xq + L.a8_d),
+                 reinterpret_cast<int32_t *>(xq + L.a8_s), reinterpret_cast<float *>(xq + L.a8_ds),
+                 k % QK_K == 0 ? reinterpret_cast<uint16_t *>(xq + L.a8_dsb) : nullptr, n, k / 32};
+}
+static Q8KOut q8k_planes(uint8_t *xq, const ActLayout &L, uint32_t n, uint32_t k) {
+    return Q8KOut{reinterpret_cast<int8_t *>(xq + L.k_qs), reinterpret_cast<float *>(xq + L.k_d),
+                  reinterpret_cast<int16_t *>(xq + L.k_bs), reinterpret_cast<uint16_t *>(xq + L.k_mb),
+                  reinterpret_cast<float *>(xq + L.k_db),
+                  QactIl{xq + L.k_il, reinterpret_cast<uint16_t *>(xq + L.k_ilmb), reinterpret_cast<float *>(xq + L.k_ild),
+                         L.tiles, n, k / QK_K}};
+}
+
 hipError_t launch_qact(const float *x, uint32_t n, uint32_t k, int kind, uint8_t *xq, hipStream_t s) {
     ActLayout L = act_layout(n, k);
     uint64_t total = uint64_t(n) * k;
     if (total == 0) return hipSuccess;
     if (kind == HKHIP_ACT_A8) {
         uint64_t grid = (total + 255) / 256;
-        qact_a8_kernel<<<uint32_t(grid), 256, 0, s>>>(x, total, reinterpret_cast<int8_t *>(xq + L.a8_qs),
-                                                      reinterpret_cast<float *>(xq + L.a8_d),
-                                                      reinterpret_cast<int32_t *>(xq + L.a8_s),
-                                                      reinterpret_cast<float *>(xq + L.a8_ds),
-                                                      k % QK_K == 0 ? reinterpret_cast<uint16_t *>(xq + L.a8_dsb) : nullptr,
-                                                      n, k / 32);
+        qact_a8_kernel<<<uint32_t(grid), 256, 0, s>>>(x, total, a8_planes(xq, L, n, k));
     } else {
         uint64_t nb = total / QK_K;
         uint64_t grid = (nb + 3) / 4; // 4 waves per workgroup
-        qact_q8k_kernel<<<uint32_t(grid), 256, 0, s>>>(x, nb, reinterpret_cast<int8_t *>(xq + L.k_qs),
-                                                       reinterpret_cast<float *>(xq + L.k_d),
-                                                       reinterpret_cast<int16_t *>(xq + L.k_bs),
-                                                       reinterpret_cast<uint16_t *>(xq + L.k_mb),
-                                                       reinterpret_cast<float *>(xq + L.k_db),
-                                                       QactIl{xq + L.k_il, reinterpret_cast<uint16_t *>(xq + L.k_ilmb),
-                                                              reinterpret_cast<float *>(xq + L.k_ild), L.tiles, n,
-                                                              k / QK_K});
+        qact_q8k_kernel<<<uint32_t(grid), 256, 0, s>>>(x, nb, q8k_planes(xq, L, n, k));
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_qact_row(const float *x, uint32_t n, uint32_t k, int kind, uint8_t *xq, const float *norm, float eps,
+                           bool pairs, hipStream_t s) {
+    if (n == 0 || k == 0) return hipSuccess;
+    if (k % 32 || (kind != HKHIP_ACT_A8 && k % QK_K)) return hipErrorInvalidValue;
+    const ActLayout L = act_layout(n, k);
+    const RowIn in{x, norm, eps, pairs ? 1 : 0, k};
+    if (kind == HKHIP_ACT_A8)
+        qact_a8_row_kernel<<<n, 256, 0, s>>>(in, a8_planes(xq, L, n, k));
+    else
+        qact_q8k_row_kernel<<<n, 256, 0, s>>>(in, q8k_planes(xq, L, n, k));
     return hipGetLastError();
 }
 
