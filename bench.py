@@ -456,8 +456,9 @@ def network_bench(torch, eng, F, synth):
     return {"prefill_512_ms": round(pre_s * 1e3, 2), "prefill_tokens_per_s": round(512 / pre_s, 1),
             "decode_ms_per_token": round(dec_s * 1e3, 3), "decode_tokens_per_s": round(1 / dec_s, 1),
             "context": "positions 512-575", "finite_logits": ok,
-            "what": "whole network on the device: embedding, 28 layers (fused rmsnorm+qact products, rope, f16 KV "
-                    "cache, split-context attention), logits; host wall clock per forward call"}
+            "what": "whole network on the device: embedding, 28 layers (RMS norm fused into the products' input "
+                    "quantization, rope, f16 KV cache; prefill attention on f16 MFMAs, decode attention over "
+                    "context chunks), logits; host wall clock per forward call"}
 
 
 def measured_peaks():
