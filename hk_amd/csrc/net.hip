@@ -70,24 +70,24 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ 
 // Position of token t: pos0[0] + t. Cache layout [kv head][max_ctx][hd].
 struct RopeArgs {
     float *q;
-    const float *k, *v;
+    const float *k, *v; // rows of the fused q/k/v output: stride sq (q) and skv (k, v) floats per token
     const float *q_norm, *k_norm; // [hd] or null
     const float *inv_freq;        // [rope_dim / 2]
     __half *kc, *vc;              // this layer's caches
     __half *vt;                   // this layer's transposed value cache [nkv][hd][vt_stride]
     const uint32_t *pos0;
-    uint32_t nh, nkv, hd, rope_half, neox, max_ctx, vt_stride;
+    uint32_t nh, nkv, hd, rope_half, neox, max_ctx, vt_stride, sq, skv;
     float eps;
 };
 
 __global__ __launch_bounds__(64) void rope_kv_kernel(RopeArgs a) {
     const uint32_t t = blockIdx.y, hh = blockIdx.x, lane = threadIdx.x;
     const uint32_t pos = a.pos0[0] + t;
-    const uint32_t hd = a.hd, qd = a.nh * hd, kvd = a.nkv * hd;
+    const uint32_t hd = a.hd;
     const bool isq = hh < a.nh, isk = !isq && hh < a.nh + a.nkv;
     if (!isq && !isk) { // value head: straight to the cache
         const uint32_t g = hh - a.nh - a.nkv;
-        const float *src = a.v + uint64_t(t) * kvd + g * hd;
+        const float *src = a.v + uint64_t(t) * a.skv + g * hd;
         __half *dst = a.vc + (uint64_t(g) * a.max_ctx + pos) * hd;
         __half *dt = a.vt + uint64_t(g) * hd * a.vt_stride + pos;
         for (uint32_t d = lane; d < hd; d += 64) {
@@ -98,7 +98,7 @@ __global__ __launch_bounds__(64) void rope_kv_kernel(RopeArgs a) {
         return;
     }
     const uint32_t g = isq ? hh : hh - a.nh;
-    const float *src = isq ? a.q + uint64_t(t) * qd + g * hd : a.k + uint64_t(t) * kvd + g * hd;
+    const float *src = isq ? a.q + uint64_t(t) * a.sq + g * hd : a.k + uint64_t(t) * a.skv + g * hd;
     const float *nw = isq ? a.q_norm : a.k_norm;
     __shared__ float h[512];
     for (uint32_t d = lane; d < hd; d += 64) h[d] = src[d];
@@ -124,7 +124,7 @@ __global__ __launch_bounds__(64) void rope_kv_kernel(RopeArgs a) {
     }
     __syncthreads();
     if (isq) {
-        float *dst = a.q + uint64_t(t) * qd + g * hd;
+        float *dst = a.q + uint64_t(t) * a.sq + g * hd;
         for (uint32_t d = lane; d < hd; d += 64) dst[d] = h[d];
     } else {
         __half *dst = a.kc + (uint64_t(g) * a.max_ctx + pos) * hd;
@@ -137,11 +137,11 @@ __global__ __launch_bounds__(64) void rope_kv_kernel(RopeArgs a) {
 // with consecutive lanes on consecutive positions (decode passes write both in rope_kv_kernel).
 __global__ __launch_bounds__(256) void v_cache_kernel(const float *__restrict__ v, __half *__restrict__ vc,
                                                       __half *__restrict__ vt, const uint32_t *__restrict__ pos0,
-                                                      uint32_t n, uint32_t nkv, uint32_t hd, uint32_t max_ctx,
+                                                      uint32_t n, uint32_t skv, uint32_t hd, uint32_t max_ctx,
                                                       uint32_t vt_stride) {
     __shared__ __half tile[16][258];
     const uint32_t g = blockIdx.x, t0 = blockIdx.y * 16, tid = threadIdx.x;
-    const uint32_t nt = n - t0 < 16 ? n - t0 : 16, pos = pos0[0] + t0, kvd = nkv * hd;
+    const uint32_t nt = n - t0 < 16 ? n - t0 : 16, pos = pos0[0] + t0, kvd = skv; // row stride of v
     for (uint32_t i = 4 * tid; i < nt * hd; i += 1024) { // hd is a multiple of 64: four values of one row
         const uint32_t tt = i / hd, d = i % hd;
         const float4 x = *reinterpret_cast<const float4 *>(v + uint64_t(t0 + tt) * kvd + g * hd + d);
@@ -167,12 +167,13 @@ __global__ __launch_bounds__(256) void v_cache_kernel(const float *__restrict__ 
 // value sums from registers. Writes {max, sum, acc[hd]} per (token, head, slice); a slice past the
 // token's position writes {-inf, 0, 0...}.
 struct AttnArgs {
-    const float *q;
+    const float *q; // stride sq floats per token
     const __half *kc, *vc;
     float *part;
     const uint32_t *pos0;
     uint32_t n, nh, nkv, hd, max_ctx, nslice;
     float scale;
+    uint32_t sq;
 };
 
 // A lane's DL dimensions of one value row: DL halves in one (DL = 1: the low half) or two words.
@@ -210,7 +211,7 @@ __global__ __launch_bounds__(256) void attn_slice_kernel(AttnArgs a) {
     const bool live = item < a.n * a.nh * a.nslice;
     const uint32_t sl = item % a.nslice, h = (item / a.nslice) % a.nh, t = item / (a.nslice * a.nh);
     if (live) {
-        const float *qsrc = a.q + (uint64_t(t) * a.nh + h) * HD;
+        const float *qsrc = a.q + uint64_t(t) * a.sq + h * HD;
 #pragma unroll
         for (int j = 0; j < DL; j++) qs[w][lane + 64 * j] = qsrc[lane + 64 * j];
     }
@@ -300,7 +301,7 @@ __global__ __launch_bounds__(NWV * 64) void attn_decode_kernel(AttnArgs a) {
     __shared__ float red_m[NWV], red_l[NWV];
     __shared__ float red_acc[NWV][HD];
     const uint32_t kvh = h / (a.nh / a.nkv);
-    const float *qsrc = a.q + (uint64_t(t) * a.nh + h) * HD;
+    const float *qsrc = a.q + uint64_t(t) * a.sq + h * HD;
     float qv[HD / 64];
 #pragma unroll
     for (int j = 0; j < HD / 64; j++) qv[j] = qsrc[lane + 64 * j];
@@ -431,6 +432,7 @@ struct AttnPArgs {
     const uint32_t *pos0;
     uint32_t n, nh, nkv, max_ctx, vt_stride;
     float scale;
+    uint32_t sq; // q row stride (floats per token)
 };
 
 template <int HD>
@@ -448,7 +450,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnPArgs a) {
 
     v8h qh[NCH], ql[NCH];
     {
-        const float *qrow = a.q + (uint64_t(tc) * a.nh + head) * HD;
+        const float *qrow = a.q + uint64_t(tc) * a.sq + head * HD;
 #pragma unroll
         for (int c = 0; c < NCH; c++) {
             const float4 x0 = *reinterpret_cast<const float4 *>(qrow + 16 * c + 8 * h);
@@ -637,9 +639,9 @@ struct hkhip_net {
     hkhip_engine *eng;
     hkhip_net_config cfg;
     struct Layer {
-        hkhip_mat wq{}, wk{}, wv{}, wo{}, wgu{}, wd{};
+        hkhip_mat wqkv{}, wo{}, wgu{}, wd{}; // q, k and v rows stacked: one product, one output row per token
         float *attn_norm = nullptr, *ffn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
-        float *bq = nullptr, *bk = nullptr, *bv = nullptr;
+        float *bqkv = nullptr;
         bool loaded = false;
     };
     std::vector<Layer> layers;
@@ -648,7 +650,7 @@ struct hkhip_net {
     // Device buffers ([MAX tokens][...] sized for the largest pass seen).
     std::vector<void *> owned;
     uint32_t cap = 0; // tokens the pass buffers hold
-    float *x = nullptr, *xb = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *gu = nullptr,
+    float *x = nullptr, *xb = nullptr, *qkv = nullptr, *att = nullptr, *gu = nullptr,
           *h = nullptr, *part = nullptr, *logits = nullptr, *inv_freq = nullptr;
     uint8_t *xq = nullptr;
     __half *kc = nullptr, *vc = nullptr, *vt = nullptr;
@@ -673,6 +675,7 @@ int hfail(hipError_t e, const char *what) {
 
 uint32_t qdim(const hkhip_net_config &c) { return c.n_heads * c.head_dim; }
 uint32_t kvdim(const hkhip_net_config &c) { return c.n_kv_heads * c.head_dim; }
+uint32_t qkvdim(const hkhip_net_config &c) { return qdim(c) + 2 * kvdim(c); }
 uint32_t nslices(const hkhip_net_config &c) { return (c.max_ctx + ATT_SLICE - 1) / ATT_SLICE; }
 uint32_t vt_stride(const hkhip_net_config &c) { return (c.max_ctx + 31) / 32 * 32; }
 bool prefill_mfma(const hkhip_net_config &c) { return c.head_dim == 64 || c.head_dim == 128; }
@@ -705,6 +708,29 @@ int load_mat(hkhip_net *n, const hkhip_net_tensor &t, uint32_t rows, uint32_t co
     return HKHIP_OK;
 }
 
+// The q, k, v biases as one vector (zeros for an absent one); null when none is given.
+int load_qkv_bias(hkhip_net *n, const hkhip_net_layer *l, uint32_t qd, uint32_t kvd, float **out) {
+    *out = nullptr;
+    const hkhip_net_tensor *b[3] = {&l->bq, &l->bk, &l->bv};
+    const uint32_t len[3] = {qd, kvd, kvd};
+    const char *name[3] = {"bq", "bk", "bv"};
+    if (!b[0]->data && !b[1]->data && !b[2]->data) return HKHIP_OK;
+    std::vector<float> all(qd + 2 * kvd, 0.0f);
+    uint32_t off = 0;
+    for (int i = 0; i < 3; i++) {
+        if (b[i]->data) {
+            if (b[i]->t != HKHIP_F32 || b[i]->bytes != uint64_t(len[i]) * 4)
+                return set_error(HKHIP_E_BAD_ARGUMENT, "%s: expected %u f32 values (type 0x00), got type 0x%02x, %llu bytes",
+                                 name[i], len[i], b[i]->t, (unsigned long long)b[i]->bytes);
+            memcpy(all.data() + off, b[i]->data, b[i]->bytes);
+        }
+        off += len[i];
+    }
+    int rc = dev_alloc(n, all.size() * 4, reinterpret_cast<void **>(out));
+    if (rc) return rc;
+    return hkhip_copy_h2d(n->eng, *out, all.data(), all.size() * 4);
+}
+
 // Pass buffers for up to `want` tokens.
 int ensure_cap(hkhip_net *n, uint32_t want) {
     if (want <= n->cap) return HKHIP_OK;
@@ -713,7 +739,7 @@ int ensure_cap(hkhip_net *n, uint32_t want) {
     for (auto &g : n->graphs) (void)hipGraphExecDestroy(g.second);
     n->graphs.clear();
     n->runs.clear();
-    float **bufs[] = {&n->x, &n->xb, &n->q, &n->k, &n->v, &n->att, &n->gu, &n->h, &n->part,
+    float **bufs[] = {&n->x, &n->xb, &n->qkv, &n->att, &n->gu, &n->h, &n->part,
                       reinterpret_cast<float **>(&n->io)};
     if (n->stage) {
         (void)hipHostFree(n->stage);
@@ -737,8 +763,7 @@ int ensure_cap(hkhip_net *n, uint32_t want) {
     const uint32_t maxk = std::max(std::max(c.dim, qdim(c)), c.ffn_dim);
     int rc;
     if ((rc = dev_alloc(n, T * c.dim * 4, (void **)&n->x)) || (rc = dev_alloc(n, T * std::max(c.dim, qdim(c)) * 4, (void **)&n->xb)) ||
-        (rc = dev_alloc(n, T * qdim(c) * 4, (void **)&n->q)) || (rc = dev_alloc(n, T * kvdim(c) * 4, (void **)&n->k)) ||
-        (rc = dev_alloc(n, T * kvdim(c) * 4, (void **)&n->v)) || (rc = dev_alloc(n, T * qdim(c) * 4, (void **)&n->att)) ||
+        (rc = dev_alloc(n, T * qkvdim(c) * 4, (void **)&n->qkv)) || (rc = dev_alloc(n, T * qdim(c) * 4, (void **)&n->att)) ||
         (rc = dev_alloc(n, T * 2 * c.ffn_dim * 4, (void **)&n->gu)) || (rc = dev_alloc(n, T * c.ffn_dim * 4, (void **)&n->h)) ||
         (rc = dev_alloc(n, (prefill_mfma(c) ? MAX_DECODE : std::max<uint64_t>(T, MAX_DECODE)) * c.n_heads * nslices(c) * (c.head_dim + 2) * 4,
                         (void **)&n->part)) ||
@@ -812,29 +837,30 @@ int run_pass(hkhip_net *net, uint32_t n) {
     for (uint32_t li = 0; li < c.n_layers; li++) {
         const hkhip_net::Layer &L = net->layers[li];
         {
-            const hkhip_mat mats[3] = {L.wq, L.wk, L.wv};
-            float *const ys[3] = {net->q, net->k, net->v};
-            const float *const bs[3] = {L.bq, L.bk, L.bv};
-            if ((rc = product(net, n, mats, 3, net->x, L.attn_norm, ys, bs, HKHIP_STORE))) return rc;
+            float *const ys[1] = {net->qkv};
+            const float *const bs[1] = {L.bqkv};
+            if ((rc = product(net, n, &L.wqkv, 1, net->x, L.attn_norm, ys, bs, HKHIP_STORE))) return rc;
         }
         const uint64_t cache_layer = uint64_t(c.n_kv_heads) * c.max_ctx * c.head_dim;
         const uint64_t vt_layer = uint64_t(c.n_kv_heads) * c.head_dim * vt_stride(c);
-        RopeArgs ra{net->q, net->k, net->v, L.q_norm, L.k_norm, net->inv_freq, net->kc + li * cache_layer,
+        float *const q = net->qkv, *const k = q + qdim(c), *const v = k + kvdim(c);
+        const uint32_t S = qkvdim(c);
+        RopeArgs ra{q, k, v, L.q_norm, L.k_norm, net->inv_freq, net->kc + li * cache_layer,
                     net->vc + li * cache_layer, net->vt + li * vt_layer, net->pos, c.n_heads, c.n_kv_heads, c.head_dim,
-                    c.rope_dim / 2, c.rope_neox, c.max_ctx, vt_stride(c), c.rms_eps};
+                    c.rope_dim / 2, c.rope_neox, c.max_ctx, vt_stride(c), S, S, c.rms_eps};
         // Prefill passes write the value heads with v_cache_kernel (coalesced transposed writes).
         const bool vsep = n > MAX_DECODE;
         hipLaunchKernelGGL(rope_kv_kernel, dim3(c.n_heads + (vsep ? 1 : 2) * c.n_kv_heads, n), dim3(64), 0, s, ra);
         NET_TRY(hipGetLastError(), "rope / kv write");
         if (vsep) {
-            hipLaunchKernelGGL(v_cache_kernel, dim3(c.n_kv_heads, (n + 15) / 16), dim3(256), 0, s, net->v,
-                               net->vc + li * cache_layer, net->vt + li * vt_layer, net->pos, n, c.n_kv_heads, c.head_dim,
+            hipLaunchKernelGGL(v_cache_kernel, dim3(c.n_kv_heads, (n + 15) / 16), dim3(256), 0, s, v,
+                               net->vc + li * cache_layer, net->vt + li * vt_layer, net->pos, n, S, c.head_dim,
                                c.max_ctx, vt_stride(c));
             NET_TRY(hipGetLastError(), "value cache");
         }
         if (n > MAX_DECODE && prefill_mfma(c)) {
-            AttnPArgs pa{net->q, net->kc + li * cache_layer, net->vt + li * vt_layer, net->att, net->pos, n, c.n_heads,
-                         c.n_kv_heads, c.max_ctx, vt_stride(c), 1.0f / sqrtf(float(c.head_dim))};
+            AttnPArgs pa{q, net->kc + li * cache_layer, net->vt + li * vt_layer, net->att, net->pos, n, c.n_heads,
+                         c.n_kv_heads, c.max_ctx, vt_stride(c), 1.0f / sqrtf(float(c.head_dim)), S};
             const dim3 pg((n + 31) / 32 * c.n_heads), pb(256);
             if (c.head_dim == 64)
                 hipLaunchKernelGGL(attn_prefill_kernel<64>, pg, pb, 0, s, pa);
@@ -842,8 +868,8 @@ int run_pass(hkhip_net *net, uint32_t n) {
                 hipLaunchKernelGGL(attn_prefill_kernel<128>, pg, pb, 0, s, pa);
             NET_TRY(hipGetLastError(), "prefill attention");
         } else if (n <= MAX_DECODE) {
-            AttnArgs aa{net->q, net->kc + li * cache_layer, net->vc + li * cache_layer, nullptr, net->pos, n, c.n_heads,
-                        c.n_kv_heads, c.head_dim, c.max_ctx, 0, 1.0f / sqrtf(float(c.head_dim))};
+            AttnArgs aa{q, net->kc + li * cache_layer, net->vc + li * cache_layer, nullptr, net->pos, n, c.n_heads,
+                        c.n_kv_heads, c.head_dim, c.max_ctx, 0, 1.0f / sqrtf(float(c.head_dim)), S};
             aa.part = net->part;
             const uint32_t G = (ns + 3) / 4;
             const dim3 dg(G, c.n_heads, n);
@@ -858,8 +884,8 @@ int run_pass(hkhip_net *net, uint32_t n) {
                                G * 4, s, net->part, net->att, c.n_heads, c.head_dim, G);
             NET_TRY(hipGetLastError(), "decode attention combine");
         } else {
-            AttnArgs aa{net->q, net->kc + li * cache_layer, net->vc + li * cache_layer, net->part, net->pos, n, c.n_heads,
-                        c.n_kv_heads, c.head_dim, c.max_ctx, ns, 1.0f / sqrtf(float(c.head_dim))};
+            AttnArgs aa{q, net->kc + li * cache_layer, net->vc + li * cache_layer, net->part, net->pos, n, c.n_heads,
+                        c.n_kv_heads, c.head_dim, c.max_ctx, ns, 1.0f / sqrtf(float(c.head_dim)), S};
             const dim3 ag((n * c.n_heads * ns + 3) / 4), ab(256);
             switch (c.head_dim) {
             case 64: hipLaunchKernelGGL(attn_slice_kernel<64>, ag, ab, 0, s, aa); break;
@@ -958,7 +984,7 @@ void hkhip_net_destroy(hkhip_net *net) {
     (void)hipStreamSynchronize(net->eng->cur);
     for (auto &g : net->graphs) (void)hipGraphExecDestroy(g.second);
     for (auto &L : net->layers) {
-        hkhip_mat *ms[] = {&L.wq, &L.wk, &L.wv, &L.wo, &L.wgu, &L.wd};
+        hkhip_mat *ms[] = {&L.wqkv, &L.wo, &L.wgu, &L.wd};
         for (hkhip_mat *m : ms) hkhip_free(net->eng, m);
     }
     hkhip_free(net->eng, &net->embd);
@@ -981,16 +1007,32 @@ int hkhip_net_load_layer(hkhip_net *net, uint32_t li, const hkhip_net_layer *l) 
         (rc = load_vec(net, l->ffn_norm, c.dim, false, &L.ffn_norm, "ffn_norm")) ||
         (rc = load_vec(net, l->q_norm, c.head_dim, true, &L.q_norm, "q_norm")) ||
         (rc = load_vec(net, l->k_norm, c.head_dim, true, &L.k_norm, "k_norm")) ||
-        (rc = load_vec(net, l->bq, qd, true, &L.bq, "bq")) || (rc = load_vec(net, l->bk, kvd, true, &L.bk, "bk")) ||
-        (rc = load_vec(net, l->bv, kvd, true, &L.bv, "bv")))
+        (rc = load_qkv_bias(net, l, qd, kvd, &L.bqkv)))
         return rc;
     if (l->wq.t != l->wk.t || l->wq.t != l->wv.t)
         return set_error(HKHIP_E_BAD_ARGUMENT, "wq, wk and wv must share their type (one fused launch)");
     if (l->w_gate.t != l->w_up.t) return set_error(HKHIP_E_BAD_ARGUMENT, "w_gate and w_up must share their type");
-    if ((rc = load_mat(net, l->wq, qd, c.dim, &L.wq, "wq")) || (rc = load_mat(net, l->wk, kvd, c.dim, &L.wk, "wk")) ||
-        (rc = load_mat(net, l->wv, kvd, c.dim, &L.wv, "wv")) || (rc = load_mat(net, l->wo, c.dim, qd, &L.wo, "wo")) ||
-        (rc = load_mat(net, l->w_down, c.dim, c.ffn_dim, &L.wd, "w_down")))
+    if ((rc = load_mat(net, l->wo, c.dim, qd, &L.wo, "wo")) || (rc = load_mat(net, l->w_down, c.dim, c.ffn_dim, &L.wd, "w_down")))
         return rc;
+    {
+        // q, k and v rows stacked into one matrix (one product launch, one output row per token).
+        const int64_t qb = hkhip_matrix_bytes(l->wq.t, 1, c.dim);
+        if (qb < 0) return int(qb);
+        const hkhip_net_tensor *parts[3] = {&l->wq, &l->wk, &l->wv};
+        const uint32_t prow[3] = {qd, kvd, kvd};
+        const char *pname[3] = {"wq", "wk", "wv"};
+        std::vector<uint8_t> qkv(uint64_t(qb) * (qd + 2 * kvd));
+        uint64_t off = 0;
+        for (int i = 0; i < 3; i++) {
+            const uint64_t want = uint64_t(qb) * prow[i];
+            if (!parts[i]->data || parts[i]->bytes != want)
+                return set_error(HKHIP_E_BAD_ARGUMENT, "%s: expected %llu bytes", pname[i], (unsigned long long)want);
+            memcpy(qkv.data() + off, parts[i]->data, want);
+            off += want;
+        }
+        const hkhip_net_tensor t{qkv.data(), qkv.size(), l->wq.t};
+        if ((rc = load_mat(net, t, qd + 2 * kvd, c.dim, &L.wqkv, "wq/wk/wv"))) return rc;
+    }
     // Gate and up rows interleaved (row 2i = gate i, 2i + 1 = up i) for the fused silu(gate)*up.
     const int64_t rb = hkhip_matrix_bytes(l->w_gate.t, 1, c.dim);
     if (rb < 0) return int(rb);
