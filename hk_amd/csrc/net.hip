@@ -77,15 +77,25 @@ struct RopeArgs {
     __half *vt;                   // this layer's transposed value cache [nkv][hd][vt_stride]
     const uint32_t *pos0;
     uint32_t nh, nkv, hd, rope_half, neox, max_ctx, vt_stride, sq, skv;
+    uint32_t nheads; // heads this launch covers: nh + nkv (keys), + nkv (values)
     float eps;
 };
 
-__global__ __launch_bounds__(64) void rope_kv_kernel(RopeArgs a) {
-    const uint32_t t = blockIdx.y, hh = blockIdx.x, lane = threadIdx.x;
+// Four heads per workgroup, one per wave; each wave works on its own LDS row, so the waves never
+// wait for each other (a wave's LDS accesses complete in order: only the compiler must keep them
+// in order, which the wave barriers do).
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+}
+__global__ __launch_bounds__(256) void rope_kv_kernel(RopeArgs a) {
+    const uint32_t t = blockIdx.y, w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint32_t hh = 4 * blockIdx.x + w;
     const uint32_t pos = a.pos0[0] + t;
     const uint32_t hd = a.hd;
+    if (hh >= a.nheads) return; // past the last head launched (whole wave; no workgroup barriers below)
     const bool isq = hh < a.nh, isk = !isq && hh < a.nh + a.nkv;
-    if (!isq && !isk) { // value head: straight to the cache
+    if (!isq && !isk) { // value head: straight to the caches
         const uint32_t g = hh - a.nh - a.nkv;
         const float *src = a.v + uint64_t(t) * a.skv + g * hd;
         __half *dst = a.vc + (uint64_t(g) * a.max_ctx + pos) * hd;
@@ -100,17 +110,18 @@ __global__ __launch_bounds__(64) void rope_kv_kernel(RopeArgs a) {
     const uint32_t g = isq ? hh : hh - a.nh;
     const float *src = isq ? a.q + uint64_t(t) * a.sq + g * hd : a.k + uint64_t(t) * a.skv + g * hd;
     const float *nw = isq ? a.q_norm : a.k_norm;
-    __shared__ float h[512];
+    __shared__ float hs[4][256];
+    float *h = hs[w];
     for (uint32_t d = lane; d < hd; d += 64) h[d] = src[d];
-    __syncthreads();
+    wave_sync();
     if (nw) { // headNorm: rmsNorm over the head (ops.zig:31-38)
         float ss = 0.0f;
         for (uint32_t d = lane; d < hd; d += 64) ss = fmaf(h[d], h[d], ss);
         for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
         const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, float(hd)) + a.eps));
-        __syncthreads();
+        wave_sync();
         for (uint32_t d = lane; d < hd; d += 64) h[d] = (h[d] * inv) * nw[d];
-        __syncthreads();
+        wave_sync();
     }
     // ropeAngles (ops.zig:154-160): angle = f32(pos) * inv_freq[i]; ropeApply (164-185).
     const float p = float(pos);
@@ -122,7 +133,7 @@ __global__ __launch_bounds__(64) void rope_kv_kernel(RopeArgs a) {
         h[i0] = x0 * c - x1 * s;
         h[i1] = x0 * s + x1 * c;
     }
-    __syncthreads();
+    wave_sync();
     if (isq) {
         float *dst = a.q + uint64_t(t) * a.sq + g * hd;
         for (uint32_t d = lane; d < hd; d += 64) dst[d] = h[d];
@@ -847,10 +858,11 @@ int run_pass(hkhip_net *net, uint32_t n) {
         const uint32_t S = qkvdim(c);
         RopeArgs ra{q, k, v, L.q_norm, L.k_norm, net->inv_freq, net->kc + li * cache_layer,
                     net->vc + li * cache_layer, net->vt + li * vt_layer, net->pos, c.n_heads, c.n_kv_heads, c.head_dim,
-                    c.rope_dim / 2, c.rope_neox, c.max_ctx, vt_stride(c), S, S, c.rms_eps};
+                    c.rope_dim / 2, c.rope_neox, c.max_ctx, vt_stride(c), S, S, 0, c.rms_eps};
         // Prefill passes write the value heads with v_cache_kernel (coalesced transposed writes).
         const bool vsep = n > MAX_DECODE;
-        hipLaunchKernelGGL(rope_kv_kernel, dim3(c.n_heads + (vsep ? 1 : 2) * c.n_kv_heads, n), dim3(64), 0, s, ra);
+        ra.nheads = c.n_heads + (vsep ? 1 : 2) * c.n_kv_heads;
+        hipLaunchKernelGGL(rope_kv_kernel, dim3((ra.nheads + 3) / 4, n), dim3(256), 0, s, ra);
         NET_TRY(hipGetLastError(), "rope / kv write");
         if (vsep) {
             hipLaunchKernelGGL(v_cache_kernel, dim3(c.n_kv_heads, (n + 15) / 16), dim3(256), 0, s, v,
