@@ -650,7 +650,10 @@ struct hkhip_net {
     hkhip_engine *eng;
     hkhip_net_config cfg;
     struct Layer {
-        hkhip_mat wqkv{}, wo{}, wgu{}, wd{}; // q, k and v rows stacked: one product, one output row per token
+        // q, k and v rows stacked (one product, one output row per token) when the three share their
+        // type; else three products into three regions of the q/k/v buffer.
+        hkhip_mat wqkv{}, wq{}, wk{}, wv{}, wo{}, wgu{}, wd{};
+        bool stacked = true;
         float *attn_norm = nullptr, *ffn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
         float *bqkv = nullptr;
         bool loaded = false;
@@ -848,17 +851,32 @@ int run_pass(hkhip_net *net, uint32_t n) {
     for (uint32_t li = 0; li < c.n_layers; li++) {
         const hkhip_net::Layer &L = net->layers[li];
         {
-            float *const ys[1] = {net->qkv};
-            const float *const bs[1] = {L.bqkv};
-            if ((rc = product(net, n, &L.wqkv, 1, net->x, L.attn_norm, ys, bs, HKHIP_STORE))) return rc;
+            if (L.stacked) {
+                float *const ys[1] = {net->qkv};
+                const float *const bs[1] = {L.bqkv};
+                if ((rc = product(net, n, &L.wqkv, 1, net->x, L.attn_norm, ys, bs, HKHIP_STORE))) return rc;
+            } else {
+                const hkhip_mat *ms[3] = {&L.wq, &L.wk, &L.wv};
+                float *const out[3] = {net->qkv, net->qkv + uint64_t(net->cap) * qdim(c),
+                                       net->qkv + uint64_t(net->cap) * (qdim(c) + kvdim(c))};
+                const uint32_t boff[3] = {0, qdim(c), qdim(c) + kvdim(c)};
+                for (int i = 0; i < 3; i++) {
+                    float *const ys[1] = {out[i]};
+                    const float *const bs[1] = {L.bqkv ? L.bqkv + boff[i] : nullptr};
+                    if ((rc = product(net, n, ms[i], 1, net->x, L.attn_norm, ys, bs, HKHIP_STORE))) return rc;
+                }
+            }
         }
         const uint64_t cache_layer = uint64_t(c.n_kv_heads) * c.max_ctx * c.head_dim;
         const uint64_t vt_layer = uint64_t(c.n_kv_heads) * c.head_dim * vt_stride(c);
-        float *const q = net->qkv, *const k = q + qdim(c), *const v = k + kvdim(c);
-        const uint32_t S = qkvdim(c);
+        // Rows of q, k, v: stride S (stacked) or their own regions of the buffer (qd, kvd).
+        float *const q = net->qkv;
+        float *const k = L.stacked ? q + qdim(c) : q + uint64_t(net->cap) * qdim(c);
+        float *const v = L.stacked ? k + kvdim(c) : k + uint64_t(net->cap) * kvdim(c);
+        const uint32_t S = L.stacked ? qkvdim(c) : qdim(c), SKV = L.stacked ? qkvdim(c) : kvdim(c);
         RopeArgs ra{q, k, v, L.q_norm, L.k_norm, net->inv_freq, net->kc + li * cache_layer,
                     net->vc + li * cache_layer, net->vt + li * vt_layer, net->pos, c.n_heads, c.n_kv_heads, c.head_dim,
-                    c.rope_dim / 2, c.rope_neox, c.max_ctx, vt_stride(c), S, S, 0, c.rms_eps};
+                    c.rope_dim / 2, c.rope_neox, c.max_ctx, vt_stride(c), S, SKV, 0, c.rms_eps};
         // Prefill passes write the value heads with v_cache_kernel (coalesced transposed writes).
         const bool vsep = n > MAX_DECODE;
         ra.nheads = c.n_heads + (vsep ? 1 : 2) * c.n_kv_heads;
@@ -866,7 +884,7 @@ int run_pass(hkhip_net *net, uint32_t n) {
         NET_TRY(hipGetLastError(), "rope / kv write");
         if (vsep) {
             hipLaunchKernelGGL(v_cache_kernel, dim3(c.n_kv_heads, (n + 15) / 16), dim3(256), 0, s, v,
-                               net->vc + li * cache_layer, net->vt + li * vt_layer, net->pos, n, S, c.head_dim,
+                               net->vc + li * cache_layer, net->vt + li * vt_layer, net->pos, n, SKV, c.head_dim,
                                c.max_ctx, vt_stride(c));
             NET_TRY(hipGetLastError(), "value cache");
         }
@@ -996,7 +1014,7 @@ void hkhip_net_destroy(hkhip_net *net) {
     (void)hipStreamSynchronize(net->eng->cur);
     for (auto &g : net->graphs) (void)hipGraphExecDestroy(g.second);
     for (auto &L : net->layers) {
-        hkhip_mat *ms[] = {&L.wqkv, &L.wo, &L.wgu, &L.wd};
+        hkhip_mat *ms[] = {&L.wqkv, &L.wq, &L.wk, &L.wv, &L.wo, &L.wgu, &L.wd};
         for (hkhip_mat *m : ms) hkhip_free(net->eng, m);
     }
     hkhip_free(net->eng, &net->embd);
@@ -1021,12 +1039,15 @@ int hkhip_net_load_layer(hkhip_net *net, uint32_t li, const hkhip_net_layer *l) 
         (rc = load_vec(net, l->k_norm, c.head_dim, true, &L.k_norm, "k_norm")) ||
         (rc = load_qkv_bias(net, l, qd, kvd, &L.bqkv)))
         return rc;
-    if (l->wq.t != l->wk.t || l->wq.t != l->wv.t)
-        return set_error(HKHIP_E_BAD_ARGUMENT, "wq, wk and wv must share their type (one fused launch)");
     if (l->w_gate.t != l->w_up.t) return set_error(HKHIP_E_BAD_ARGUMENT, "w_gate and w_up must share their type");
     if ((rc = load_mat(net, l->wo, c.dim, qd, &L.wo, "wo")) || (rc = load_mat(net, l->w_down, c.dim, c.ffn_dim, &L.wd, "w_down")))
         return rc;
-    {
+    L.stacked = l->wq.t == l->wk.t && l->wq.t == l->wv.t;
+    if (!L.stacked) {
+        if ((rc = load_mat(net, l->wq, qd, c.dim, &L.wq, "wq")) || (rc = load_mat(net, l->wk, kvd, c.dim, &L.wk, "wk")) ||
+            (rc = load_mat(net, l->wv, kvd, c.dim, &L.wv, "wv")))
+            return rc;
+    } else {
         // q, k and v rows stacked into one matrix (one product launch, one output row per token).
         const int64_t qb = hkhip_matrix_bytes(l->wq.t, 1, c.dim);
         if (qb < 0) return int(qb);

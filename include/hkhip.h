@@ -203,7 +203,9 @@ int hkhip_mm_noalloc(hkhip_engine *eng, const hkhip_mat *m, const float *x_dev, 
  * quantization, residual adds as accumulate-mode products, gate/up as one silu(gate)*up launch)
  * and are captured in a HIP graph per token count after their first run; longer passes (prompt
  * prefill) run the MFMA GEMMs. Matrices are hk file-layout bytes in host memory, copied at load;
- * Wgate and Wup must share their type. Vectors (norms, biases) are f32 (HKHIP_F32). */
+ * Wgate and Wup must share their type; Wq, Wk and Wv that share theirs run as one product over
+ * their stacked rows (else as three, e.g. a Q6_K Wv beside Q4_K Wq / Wk as in Q4_K_M files).
+ * Vectors (norms, biases) are f32 (HKHIP_F32). */
 #define HKHIP_F32 0x00 /* hk StorageType f32 (src/format.zig:28) */
 typedef struct hkhip_net hkhip_net;
 typedef struct hkhip_net_config {

@@ -153,3 +153,28 @@ def test_net_long_context(eng):
             pos += n
     print("long context: worst relative logit error", worst)
     assert worst <= 1e-3
+
+
+def test_net_mixed_types(eng):
+    """Layers whose q, k and v matrices differ in type (a Q6_K Wv and Wdown beside Q4_K, as Q4_K_M
+    files have them in some layers) run as three q/k/v products into separate regions; with
+    q/k/v biases (their offsets into the stacked bias vector), prefill and decode passes."""
+    from hk_amd.net import Net
+
+    cfg = Config(dim=256, n_layers=2, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=512, vocab=300, max_ctx=300,
+                 rope_neox=True, rope_base=1e6)
+    model = synth.model_np(cfg, F.Q4_K, seed=4600, out_fmt=F.Q6_K, embd_fmt=F.Q8_0, qk_norm=True, bias=True)
+    kvd = cfg.n_kv_heads * cfg.head_dim
+    rng = np.random.default_rng(4601)
+    model["layers"][0]["wv"] = (synth.weights_np(F.Q6_K, kvd, cfg.dim, 4602), F.Q6_K)
+    model["layers"][1]["wq"] = (synth.weights_np(F.Q8_0, cfg.n_heads * cfg.head_dim, cfg.dim, 4603), F.Q8_0)
+    model["layers"][0]["w_down"] = (synth.weights_np(F.Q6_K, cfg.dim, cfg.ffn_dim, 4604), F.Q6_K)
+    cpu = Oracle(cfg, model)
+    with Net(eng, cfg) as net:
+        net.load(model)
+        pos = 0
+        for n in [40, 1, 3, 8, 1]:
+            toks = rng.integers(0, cfg.vocab, n)
+            net.forward(toks, pos)
+            check(net.logits(), cpu.forward(toks, pos), f"mixed types: pass of {n} at {pos}")
+            pos += n
