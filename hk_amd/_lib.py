@@ -39,7 +39,8 @@ class NetConfig(ctypes.Structure):
     """hkhip_net_config."""
     _fields_ = [(n, ctypes.c_uint32) for n in ("dim", "n_layers", "n_heads", "n_kv_heads", "head_dim", "ffn_dim",
                                                   "vocab", "rope_dim", "rope_neox", "max_ctx")] + \
-               [("rms_eps", ctypes.c_float), ("rope_base", ctypes.c_float)]
+               [("rms_eps", ctypes.c_float), ("rope_base", ctypes.c_float), ("inv_freq", ctypes.c_void_p),
+                ("rope_mscale", ctypes.c_float)]
 
 
 class NetTensor(ctypes.Structure):

@@ -78,6 +78,7 @@ struct RopeArgs {
     const uint32_t *pos0;
     uint32_t nh, nkv, hd, rope_half, neox, max_ctx, vt_stride, sq, skv;
     uint32_t nheads; // heads this launch covers: nh + nkv (keys), + nkv (values)
+    float mscale;    // multiplier of every cos and sin (ops.zig ropeMscale)
     float eps;
 };
 
@@ -127,7 +128,7 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(RopeArgs a) {
     const float p = float(pos);
     for (uint32_t i = lane; i < a.rope_half; i += 64) {
         const float ang = p * a.inv_freq[i];
-        const float c = cosf(ang), s = sinf(ang);
+        const float c = cosf(ang) * a.mscale, s = sinf(ang) * a.mscale;
         const uint32_t i0 = a.neox ? i : 2 * i, i1 = a.neox ? i + a.rope_half : 2 * i + 1;
         const float x0 = h[i0], x1 = h[i1];
         h[i0] = x0 * c - x1 * s;
@@ -876,7 +877,7 @@ int run_pass(hkhip_net *net, uint32_t n) {
         const uint32_t S = L.stacked ? qkvdim(c) : qdim(c), SKV = L.stacked ? qkvdim(c) : kvdim(c);
         RopeArgs ra{q, k, v, L.q_norm, L.k_norm, net->inv_freq, net->kc + li * cache_layer,
                     net->vc + li * cache_layer, net->vt + li * vt_layer, net->pos, c.n_heads, c.n_kv_heads, c.head_dim,
-                    c.rope_dim / 2, c.rope_neox, c.max_ctx, vt_stride(c), S, SKV, 0, c.rms_eps};
+                    c.rope_dim / 2, c.rope_neox, c.max_ctx, vt_stride(c), S, SKV, 0, c.rope_mscale, c.rms_eps};
         // Prefill passes write the value heads with v_cache_kernel (coalesced transposed writes).
         const bool vsep = n > MAX_DECODE;
         ra.nheads = c.n_heads + (vsep ? 1 : 2) * c.n_kv_heads;
@@ -996,10 +997,18 @@ int hkhip_net_create(hkhip_engine *eng, const hkhip_net_config *cfg, hkhip_net *
         hkhip_net_destroy(n);
         return set_error(HKHIP_E_DEVICE_FAILED, "clearing the caches");
     }
+    // The caller's inverse frequencies (hk computes them with any scaling on the host), or
     // ropeInvFreq without scaling (ops.zig:96-146): base^(-2i/n_rot) in f64, then f32.
     std::vector<float> f(c.rope_dim / 2 + 1, 0.0f);
     for (uint32_t i = 0; i < c.rope_dim / 2; i++)
-        f[i] = float(pow(double(c.rope_base), -double(2 * i) / double(c.rope_dim)));
+        f[i] = c.inv_freq ? c.inv_freq[i] : float(pow(double(c.rope_base), -double(2 * i) / double(c.rope_dim)));
+    n->cfg.inv_freq = nullptr; // the caller's array is not kept
+    for (uint32_t i = 0; i < c.rope_dim / 2; i++)
+        if (!(f[i] > 0.0f) || !std::isfinite(f[i])) {
+            hkhip_net_destroy(n);
+            return set_error(HKHIP_E_BAD_ARGUMENT, "inv_freq[%u] = %g: expected a positive number", i, double(f[i]));
+        }
+    if (!(n->cfg.rope_mscale > 0.0f)) n->cfg.rope_mscale = 1.0f;
     if ((rc = hkhip_copy_h2d(eng, n->inv_freq, f.data(), f.size() * 4))) {
         hkhip_net_destroy(n);
         return rc;

@@ -9,7 +9,8 @@ Layouts followed (reference files):
     data / residual / scale offset + size u64 x 6, block_size u16, sparsity_ratio f32
                                                 src/tensor_toc.zig:39-101
   header / range validation                     src/reader.zig:20-60
-  configuration from metadata                   src/engine/config.zig:225-320 fromMetadata
+  configuration from metadata                   src/engine/config.zig:225-320 fromMetadata,
+                                                163-223 parseRopeScaling
   tensor names, shapes, tied output              src/engine/weights.zig:96-240
 """
 from __future__ import annotations
@@ -202,17 +203,56 @@ class HkFile:
             raise HkFormatError(f"head_count {n_heads} is not a multiple of head_count_kv {n_kv}")
         head_dim = int(opt("attention.key_length", 0)) or dim // n_heads
         rope_dim = int(opt("rope.dimension_count", head_dim))
-        scaling = m.get(f"{arch}.rope.scaling.type", "none")
-        if scaling != "none" or float(opt("rope.scaling.factor", 1.0)) != 1.0:
-            raise HkFormatError(f"rope scaling '{scaling}' is not supported by the HIP network pass")
+        scaling = self._rope_scaling(arch, int(opt("context_length", 2048)), rope_dim)
+        factors = None
+        if "rope_freqs.weight" in self.by_name:  # llama3 scaling as llama.cpp files carry it
+            factors = self.vec("rope_freqs.weight", rope_dim // 2)
+            if not (np.isfinite(factors).all() and (factors > 0).all()):
+                raise HkFormatError("'rope_freqs.weight' holds a value that is not a positive number")
         style = m.get("hk.rope_style", "norm" if fam == "llama" else "neox")
         vocab = self.entry("token_embd.weight").shape[0]
         cfg = Config(dim=dim, n_layers=need("block_count"), n_heads=n_heads, n_kv_heads=n_kv, head_dim=head_dim,
                      ffn_dim=need("feed_forward_length"), vocab=vocab, max_ctx=max_ctx, rope_dim=rope_dim,
                      rope_neox=style == "neox", rms_eps=float(opt("attention.layer_norm_rms_epsilon", 1e-5)),
-                     rope_base=float(opt("rope.freq_base", 10000.0)))
+                     rope_base=float(opt("rope.freq_base", 10000.0)), rope_scaling=scaling, rope_freq_factors=factors)
         cfg.qk_norm, cfg.qkv_bias = fam == "qwen3", fam == "qwen2"
         return cfg
+
+    def _rope_scaling(self, arch: str, ctx_train: int, rope_dim: int):
+        """RopeScaling from the metadata (config.zig:163-223 parseRopeScaling): the type, or a bare
+        factor meaning linear; factor >= 1; the original context (default the training context);
+        llama3's band (hk.rope.low/high_freq_factor), yarn's (hk.rope.beta_fast/slow) and magnitude."""
+        from .rope import KINDS, RopeScaling
+
+        m = self.metadata
+        kind = m.get(f"{arch}.rope.scaling.type")
+        factor = m.get(f"{arch}.rope.scaling.factor")
+        if kind is None:
+            kind = "linear" if factor is not None else "none"
+        if kind not in KINDS:
+            raise HkFormatError(f"rope scaling type '{kind}' is not supported (supported: {', '.join(KINDS)})")
+        if kind == "none":
+            return None
+        if factor is None:
+            raise HkFormatError(f"rope scaling '{kind}' needs '{arch}.rope.scaling.factor'")
+        factor = float(factor)
+        if not (np.isfinite(factor) and factor >= 1.0):
+            raise HkFormatError(f"rope scaling factor {factor} must be at least 1")
+        r = RopeScaling(kind, factor, int(m.get(f"{arch}.rope.scaling.original_context_length", ctx_train)))
+        if kind == "llama3":
+            r.low_freq_factor = float(m.get("hk.rope.low_freq_factor", r.low_freq_factor))
+            r.high_freq_factor = float(m.get("hk.rope.high_freq_factor", r.high_freq_factor))
+            if not (0 < r.low_freq_factor < r.high_freq_factor):
+                raise HkFormatError("llama3 rope scaling needs 0 < low_freq_factor < high_freq_factor")
+        elif kind == "yarn":
+            r.beta_fast = float(m.get("hk.rope.beta_fast", r.beta_fast))
+            r.beta_slow = float(m.get("hk.rope.beta_slow", r.beta_slow))
+            r.attn_factor = float(m.get(f"{arch}.rope.scaling.attn_factor", r.attn_factor))
+            if not (r.beta_fast > 0 and r.beta_slow > 0 and r.attn_factor > 0):
+                raise HkFormatError("yarn rope scaling needs positive beta_fast, beta_slow and attn_factor")
+        if kind != "linear" and (r.orig_ctx == 0 or rope_dim == 0):
+            raise HkFormatError("rope scaling needs the original context length")
+        return r
 
     def model(self, cfg) -> dict:
         """The decoder's tensors (weights.zig:96-176): matrices as views of the mapping, vectors f32;

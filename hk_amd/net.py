@@ -9,6 +9,7 @@ from dataclasses import dataclass
 
 import numpy as np
 
+from . import rope
 from ._lib import NET_LAYER_FIELDS, NetConfig, NetLayer, NetTensor, check, lib
 
 F32 = 0x00  # hk StorageType f32
@@ -28,11 +29,17 @@ class Config:
     rope_neox: bool = True     # pairs (i, i + half); False: (2i, 2i + 1)
     rms_eps: float = 1e-6
     rope_base: float = 1e6
+    rope_scaling: rope.RopeScaling | None = None  # none / linear / llama3 / yarn
+    rope_freq_factors: np.ndarray | None = None   # per-frequency divisors (a file's rope_freqs.weight)
+
+    def inv_freq(self) -> np.ndarray:
+        return rope.inv_freq(self.rope_base, self.rope_dim or self.head_dim, self.rope_scaling, self.rope_freq_factors)
 
     def c(self) -> NetConfig:
+        self._inv = np.ascontiguousarray(self.inv_freq(), np.float32)  # read by hkhip_net_create
         return NetConfig(self.dim, self.n_layers, self.n_heads, self.n_kv_heads, self.head_dim, self.ffn_dim,
                          self.vocab, self.rope_dim or self.head_dim, int(self.rope_neox), self.max_ctx,
-                         self.rms_eps, self.rope_base)
+                         self.rms_eps, self.rope_base, self._inv.ctypes.data, rope.mscale(self.rope_scaling))
 
 
 def _tensor(v, keep: list) -> NetTensor:

@@ -214,6 +214,12 @@ typedef struct hkhip_net_config {
     uint32_t rope_neox; /* 0: pairs (2i, 2i+1) ("norm" style); 1: pairs (i, i + rope_dim/2) */
     uint32_t max_ctx;   /* K/V cache positions */
     float rms_eps, rope_base;
+    /* RoPE as hk's model setup computes it for its device engines (src/engine/model.zig:123-124,
+     * ops.zig ropeInvFreq / ropeMscale; src/cuda/engine.zig takes both at init): rope_dim / 2
+     * inverse frequencies in host memory, read at create (NULL: rope_base^(-2i/rope_dim), no
+     * scaling), and the multiplier of every cos and sin (0: 1; yarn scaling sets it). */
+    const float *inv_freq;
+    float rope_mscale;
 } hkhip_net_config;
 /* A tensor in hk's file layout in host memory; data NULL for an absent optional tensor. */
 typedef struct hkhip_net_tensor {

@@ -3,8 +3,9 @@ checker of the HIP network pass; the product never calls it).
 
 Follows src/engine/cpu_backend.zig:237-331 (embed, forwardFrom, logitsFor) with the oracle's
 restatement of the quantized products (oracle.matmul: quantizeA8 / quantizeQ8K of the input, then
-hk's integer dots), src/engine/ops.zig rmsNorm (10-29), headNorm (31-38), ropeInvFreq without
-scaling (96-146), ropeAngles (154-160), ropeApply (164-185), swiglu (70-80), and causal GQA
+hk's integer dots), src/engine/ops.zig rmsNorm (10-29), headNorm (31-38), ropeInvFreq with the
+none / linear / llama3 / yarn scalings and frequency factors (93-146), ropeMscale (148-152),
+ropeAngles (154-160), ropeApply (164-185), swiglu (70-80), and causal GQA
 attention softmax(q k^T / sqrt(head_dim)) v over an f16 key/value cache (src/engine/kv.zig:1-11,
 attention.zig:44-110), evaluated in float64 from the f16-rounded cache.
 """
@@ -22,6 +23,46 @@ def rms_norm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
     return (x * inv) * w
 
 
+def rope_inv_freq(base, n_rot: int, sc=None, factors=None) -> np.ndarray:
+    """src/engine/ops.zig:96-146 ropeInvFreq: base^(-2i/n_rot) in float64, stretched by the scaling
+    `sc` (fields of src/engine/config.zig:48-62; None: no scaling), divided by the optional
+    per-frequency factors, rounded to float32."""
+    i = np.arange(n_rot // 2, dtype=np.float64)
+    nr, b = np.float64(n_rot), np.float64(np.float32(base))
+    inv = b ** (-(2.0 * i) / nr)
+    kind = getattr(sc, "kind", "none")
+    if kind != "none":
+        f = np.float64(np.float32(sc.factor))
+    if kind == "linear":
+        inv = inv / f
+    elif kind == "llama3":
+        old = np.float64(sc.orig_ctx)
+        lf, hf = np.float64(np.float32(sc.low_freq_factor)), np.float64(np.float32(sc.high_freq_factor))
+        wl = 2.0 * np.pi / inv
+        smooth = (old / wl - lf) / (hf - lf)
+        mid = (1.0 - smooth) * inv / f + smooth * inv
+        inv = np.where(wl < old / hf, inv, np.where(wl > old / lf, inv / f, mid))
+    elif kind == "yarn":
+        ctx = np.float64(sc.orig_ctx)
+        dim = lambda rot: nr * np.log(ctx / (rot * 2.0 * np.pi)) / (2.0 * np.log(b))
+        lo = max(0.0, np.floor(dim(np.float64(np.float32(sc.beta_fast)))))
+        hi = min(nr - 1.0, np.ceil(dim(np.float64(np.float32(sc.beta_slow)))))
+        if lo == hi:
+            hi += 0.001
+        ramp = np.clip((i - lo) / (hi - lo), 0.0, 1.0)
+        inv = (inv / f) * ramp + inv * (1.0 - ramp)
+    if factors is not None:
+        inv = inv / np.asarray(factors, np.float32).astype(np.float64)
+    return inv.astype(np.float32)
+
+
+def rope_mscale(sc=None) -> float:
+    """src/engine/ops.zig:148-152 ropeMscale: attn_factor * (0.1 ln(factor) + 1) for yarn, else 1."""
+    if getattr(sc, "kind", "none") != "yarn":
+        return 1.0
+    return float(np.float32(sc.attn_factor) * np.float32(1.0 + 0.1 * np.log(np.float64(np.float32(sc.factor)))))
+
+
 class Oracle:
     def __init__(self, cfg, model: dict):
         self.cfg, self.m = cfg, model
@@ -29,7 +70,9 @@ class Oracle:
         self.kc = np.zeros((L, cfg.n_kv_heads, cfg.max_ctx, hd), np.float16)
         self.vc = np.zeros_like(self.kc)
         rd = cfg.rope_dim or hd
-        self.inv_freq = np.array([np.float64(cfg.rope_base) ** (-2.0 * i / rd) for i in range(rd // 2)], np.float32)
+        sc = getattr(cfg, "rope_scaling", None)
+        self.inv_freq = rope_inv_freq(cfg.rope_base, rd, sc, getattr(cfg, "rope_freq_factors", None))
+        self.mscale = rope_mscale(sc)
 
     def _mm(self, mat, x, bias=None):
         raw, t = mat
@@ -40,7 +83,8 @@ class Oracle:
         c = self.cfg
         half = (c.rope_dim or c.head_dim) // 2
         ang = np.float32(pos) * self.inv_freq
-        cs, sn = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+        cs = (np.cos(ang).astype(np.float32) * np.float32(self.mscale)).astype(np.float32)
+        sn = (np.sin(ang).astype(np.float32) * np.float32(self.mscale)).astype(np.float32)
         v = v.copy()
         if c.rope_neox:
             a, b = v[:half].copy(), v[half:2 * half].copy()

@@ -60,10 +60,11 @@ def write_hk(path: str, metadata: dict, tensors: list) -> None:
 
 
 def write_model(path: str, arch: str, cfg, model: dict, tie_output: bool = False, vec_type: int = 0,
-                style_key: bool = True) -> None:
+                style_key: bool = True, extra_meta: dict | None = None, rope_freqs=None) -> None:
     """A decoder in hk's tensor naming (weights.zig:96-176) and metadata keys (config.zig:225-320).
     vec_type: 0 f32, 1 f16 or 2 bf16 for the norm and bias vectors; style_key: write hk.rope_style
-    (else the architecture's default applies)."""
+    (else the architecture's default applies); extra_meta: more keys (rope scaling); rope_freqs:
+    the rope_freqs.weight tensor (f32)."""
     md = {"general.architecture": arch, f"{arch}.embedding_length": cfg.dim, f"{arch}.block_count": cfg.n_layers,
           f"{arch}.feed_forward_length": cfg.ffn_dim, f"{arch}.attention.head_count": cfg.n_heads,
           f"{arch}.attention.head_count_kv": cfg.n_kv_heads, f"{arch}.attention.key_length": cfg.head_dim,
@@ -72,6 +73,7 @@ def write_model(path: str, arch: str, cfg, model: dict, tie_output: bool = False
           }
     if style_key:
         md["hk.rope_style"] = "neox" if cfg.rope_neox else "norm"
+    md.update(extra_meta or {})
 
     def vec(v):
         v = np.asarray(v, np.float32)
@@ -94,6 +96,9 @@ def write_model(path: str, arch: str, cfg, model: dict, tie_output: bool = False
     qd, kvd = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
     add_mat("token_embd.weight", model["tok_embd"], cfg.vocab, cfg.dim)
     add_vec("output_norm.weight", model["out_norm"])
+    if rope_freqs is not None:
+        f = np.asarray(rope_freqs, np.float32)
+        ts.append(("rope_freqs.weight", 0, (len(f),), f.tobytes()))
     if not tie_output:
         add_mat("output.weight", model["output"], cfg.vocab, cfg.dim)
     for i, L in enumerate(model["layers"]):

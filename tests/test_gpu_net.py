@@ -178,3 +178,29 @@ def test_net_mixed_types(eng):
             net.forward(toks, pos)
             check(net.logits(), cpu.forward(toks, pos), f"mixed types: pass of {n} at {pos}")
             pos += n
+
+
+@pytest.mark.parametrize("kind", ["llama3", "yarn", "linear"])
+def test_net_rope_scaling(eng, kind):
+    """Scaled RoPE: the host computes the inverse frequencies (and yarn's cos/sin magnitude) as hk's
+    model setup does and hands them to the pass (hkhip_net_config.inv_freq / rope_mscale); llama3
+    with per-frequency factors (a file's rope_freqs.weight)."""
+    from hk_amd.net import Net
+    from hk_amd.rope import RopeScaling
+
+    sc = {"llama3": RopeScaling("llama3", 8.0, 64), "yarn": RopeScaling("yarn", 4.0, 64, attn_factor=0.9),
+          "linear": RopeScaling("linear", 4.0)}[kind]
+    cfg = Config(dim=256, n_layers=1, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=256, vocab=200, max_ctx=200,
+                 rope_neox=kind != "llama3", rope_base=5e5, rope_scaling=sc,
+                 rope_freq_factors=(1.0 + np.arange(32, dtype=np.float32) / 16) if kind == "llama3" else None)
+    model = synth.model_np(cfg, F.Q8_0, seed=4700, qk_norm=kind == "yarn")
+    rng = np.random.default_rng(4701)
+    cpu = Oracle(cfg, model)
+    with Net(eng, cfg) as net:
+        net.load(model)
+        pos = 0
+        for n in [30, 1, 4, 1]:
+            toks = rng.integers(0, cfg.vocab, n)
+            net.forward(toks, pos)
+            check(net.logits(), cpu.forward(toks, pos), f"{kind} rope: pass of {n} at {pos}")
+            pos += n

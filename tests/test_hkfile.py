@@ -76,3 +76,43 @@ def test_refuses_corrupt_files(tmp_path):
             f.mat("w", 2, 512)
         assert f.mat("w", 2, 256)[1] == F.Q4_K
     os.remove(p)
+
+
+def test_rope_scaling_from_metadata(tmp_path):
+    """parseRopeScaling (config.zig:163-223): the type or a bare factor (linear), the original
+    context defaulting to the training one, llama3's band and yarn's keys, the rope_freqs.weight
+    factors; bad values refused."""
+    cfg = Config(dim=256, n_layers=1, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=256, vocab=64, max_ctx=64)
+    model = synth.model_np(cfg, F.Q8_0, seed=5, qk_norm=False)
+    p = str(tmp_path / "r.hk")
+    factors = 1.0 + np.arange(32, dtype=np.float32) / 8
+    write_model(p, "llama", cfg, model, rope_freqs=factors,
+                extra_meta={"llama.rope.scaling.type": "llama3", "llama.rope.scaling.factor": 8.0,
+                            "llama.rope.scaling.original_context_length": 8192, "hk.rope.high_freq_factor": 5.0})
+    with HkFile(p) as f:
+        c = f.config(max_ctx=64)
+        r = c.rope_scaling
+        assert (r.kind, r.factor, r.orig_ctx, r.low_freq_factor, r.high_freq_factor) == ("llama3", 8.0, 8192, 1.0, 5.0)
+        assert np.array_equal(c.rope_freq_factors, factors)
+    write_model(p, "llama", cfg, model, extra_meta={"llama.rope.scaling.factor": 2.0})
+    with HkFile(p) as f:
+        r = f.config(max_ctx=64).rope_scaling
+        assert (r.kind, r.factor, r.orig_ctx) == ("linear", 2.0, 4096)  # bare factor; training context
+    write_model(p, "qwen2", cfg, model, extra_meta={"qwen2.rope.scaling.type": "yarn", "qwen2.rope.scaling.factor": 4.0,
+                                                     "qwen2.rope.scaling.attn_factor": 0.5, "hk.rope.beta_fast": 16.0})
+    with HkFile(p) as f:
+        r = f.config(max_ctx=64).rope_scaling
+        assert (r.kind, r.factor, r.beta_fast, r.beta_slow, r.attn_factor) == ("yarn", 4.0, 16.0, 1.0, 0.5)
+    for bad, msg in (({"llama.rope.scaling.type": "dynamic", "llama.rope.scaling.factor": 2.0}, "not supported"),
+                     ({"llama.rope.scaling.type": "linear"}, "needs"),
+                     ({"llama.rope.scaling.factor": 0.5}, "at least 1"),
+                     ({"llama.rope.scaling.type": "llama3", "llama.rope.scaling.factor": 8.0,
+                       "hk.rope.low_freq_factor": 4.0}, "low_freq_factor")):
+        write_model(p, "llama", cfg, model, extra_meta=bad)
+        with HkFile(p) as f:
+            with pytest.raises(HkFormatError, match=msg):
+                f.config(max_ctx=64)
+    write_model(p, "llama", cfg, model, rope_freqs=-factors)
+    with HkFile(p) as f:
+        with pytest.raises(HkFormatError, match="positive"):
+            f.config(max_ctx=64)

@@ -467,3 +467,42 @@ def test_net_oracle_pieces_closed_forms():
         xb = rms_norm(x, model["layers"][0]["attn_norm"], cfg.rms_eps)
         vrow = O.matmul(t, raw, 64, 64, xb[None], 1)[0]
         assert np.array_equal(o.vc[0, 0, 0], vrow.astype(np.float16))
+
+
+# Inverse frequencies for head width 64 that the reference's own tests hold (values from Hugging
+# Face Transformers' rope initializers; src/engine/ops.zig:292-343, compared there within 2e-6).
+ROPE_PROBES = {
+    "llama3": (dict(kind="llama3", factor=8.0, orig_ctx=8192, low_freq_factor=1.0, high_freq_factor=4.0), 500000.0,
+               [(0, 1.0), (1, 6.636012793e-01), (7, 5.666961893e-02), (8, 3.760603070e-02), (12, 7.292665076e-03),
+                (16, 5.248460220e-04), (20, 3.428102355e-05), (24, 6.647869668e-06), (31, 3.767322596e-07)]),
+    "yarn": (dict(kind="yarn", factor=4.0, orig_ctx=4096), 10000.0,
+             [(0, 1.0), (1, 7.498942018e-01), (7, 1.333521456e-01), (8, 1.000000015e-01), (12, 2.797399648e-02),
+              (16, 6.538461894e-03), (20, 1.337886788e-03), (24, 2.500000119e-04), (31, 3.333803761e-05)]),
+    "linear": (dict(kind="linear", factor=4.0), 10000.0,
+               [(0, 0.25), (1, 1.874735504e-01), (16, 2.499999944e-03), (31, 3.333803761e-05)]),
+}
+
+
+@pytest.mark.parametrize("which", ["oracle", "host"])
+@pytest.mark.parametrize("case", list(ROPE_PROBES))
+def test_rope_inv_freq_reference_probes(which, case):
+    """Both restatements of ropeInvFreq -- the oracle's and the host code that feeds the device pass
+    (hk_amd/rope.py) -- against the reference's golden probes; plus the yarn magnitude
+    (1.138629436 for factor 4), 1 for the others, and plain RoPE (no scaling: 1 and 4x the linear
+    probe at 31), and frequency factors dividing the result."""
+    from hk_amd.rope import RopeScaling, inv_freq, mscale
+    from oracle.net_oracle import rope_inv_freq, rope_mscale
+
+    kw, base, probes = ROPE_PROBES[case]
+    sc = RopeScaling(**kw)
+    f = rope_inv_freq if which == "oracle" else inv_freq
+    ms = rope_mscale if which == "oracle" else mscale
+    out = f(base, 64, sc)
+    for i, want in probes:
+        assert abs(float(out[i]) - want) <= 2e-6 * want, (case, i, float(out[i]), want)
+    assert abs(ms(sc) - (1.138629436 if case == "yarn" else 1.0)) <= 1e-6
+    plain = f(10000.0, 64, None)
+    assert plain[0] == 1.0 and abs(float(plain[31]) - 4 * 3.333803761e-05) <= 1e-5 * 4 * 3.333803761e-05
+    factors = 1.0 + np.arange(32, dtype=np.float32)
+    with_f = f(10000.0, 64, None, factors)
+    assert np.allclose(with_f, plain / factors, rtol=1e-6)
