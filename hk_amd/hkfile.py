@@ -202,6 +202,9 @@ class HkFile:
         if n_heads % n_kv:
             raise HkFormatError(f"head_count {n_heads} is not a multiple of head_count_kv {n_kv}")
         head_dim = int(opt("attention.key_length", 0)) or dim // n_heads
+        # A sliding window changes which positions are visible: refused, as config.zig:271-279 does.
+        if int(opt("attention.sliding_window", 0) or 0) > 0:
+            raise HkFormatError(f"sliding window attention ({int(opt('attention.sliding_window', 0))}) is not supported")
         rope_dim = int(opt("rope.dimension_count", head_dim))
         scaling = self._rope_scaling(arch, int(opt("context_length", 2048)), rope_dim)
         factors = None

@@ -112,6 +112,10 @@ def test_rope_scaling_from_metadata(tmp_path):
         with HkFile(p) as f:
             with pytest.raises(HkFormatError, match=msg):
                 f.config(max_ctx=64)
+    write_model(p, "llama", cfg, model, extra_meta={"llama.attention.sliding_window": 4096})
+    with HkFile(p) as f:
+        with pytest.raises(HkFormatError, match="sliding window"):
+            f.config(max_ctx=64)
     write_model(p, "llama", cfg, model, rope_freqs=-factors)
     with HkFile(p) as f:
         with pytest.raises(HkFormatError, match="positive"):
