@@ -372,6 +372,7 @@ def main():
                 eng.free(m)
         eng.free(qhead)
         extra["network_qwen3_0_6b"] = network_bench(torch, eng, F, synth)
+        extra["network_llama3_8b"] = network_bench(torch, eng, F, synth, "llama3_8b")
         result["extra"] = extra
         phase("extra")
 
@@ -423,19 +424,37 @@ def main():
     eng.close()
 
 
-def network_bench(torch, eng, F, synth):
-    """The whole-network device pass (hk_amd.net) on a random Qwen3-0.6B-shaped model (config 2's
-    shapes: 28 layers, dim 1024, 16 query / 8 key-value heads of 128, q/k norms, FFN 3072, vocabulary
-    151936; Q4_K layers, Q6_K output and embedding): a 512-token prompt prefill, then 64 decode
-    passes of one token (one HIP graph replay each, positions 512..575), timed on the host clock
-    around each call (the call returns when its pass is done)."""
+def network_bench(torch, eng, F, synth, which: str = "qwen3_0_6b"):
+    """The whole-network device pass (hk_amd.net) on a random model of a real shape: a 512-token
+    prompt prefill, then 64 decode passes of one token (one HIP graph replay each, positions
+    512..575), timed on the host clock around each call (the call returns when its pass is done).
+      qwen3_0_6b: config 2's shapes (28 layers, dim 1024, 16 query / 8 key-value heads of 128, q/k
+        norms, FFN 3072, vocabulary 151936); Q4_K layers, Q6_K output and embedding.
+      llama3_8b:  config 4's shapes (32 layers, dim 4096, 32 / 8 heads of 128, FFN 14336,
+        vocabulary 128256, llama3 RoPE scaling: factor 8 over 8192 positions, base 500000);
+        Q4_K layers and embedding, Q6_K output. Every layer gets the same random matrices (their
+        own device copies: no layer reads another's), which keeps the host synthesis short."""
     import numpy as np
 
     from hk_amd.net import Config, Net
+    from hk_amd.rope import RopeScaling
 
-    cfg = Config(dim=1024, n_layers=28, n_heads=16, n_kv_heads=8, head_dim=128, ffn_dim=3072, vocab=151936,
-                 max_ctx=2048, rope_neox=True, rope_base=1e6)
-    model = synth.model_np(cfg, F.Q4_K, seed=synth.seed_for(2, 500), out_fmt=F.Q6_K, embd_fmt=F.Q6_K)
+    if which == "llama3_8b":
+        cfg = Config(dim=4096, n_layers=32, n_heads=32, n_kv_heads=8, head_dim=128, ffn_dim=14336, vocab=128256,
+                     max_ctx=2048, rope_neox=False, rope_base=500000.0, rms_eps=1e-5,
+                     rope_scaling=RopeScaling("llama3", 8.0, 8192, 1.0, 4.0))
+        one = synth.model_np(Config(dim=4096, n_layers=1, n_heads=32, n_kv_heads=8, head_dim=128, ffn_dim=14336,
+                                    vocab=8, max_ctx=16), F.Q4_K, seed=synth.seed_for(4, 500), qk_norm=False)
+        rng_w = np.random.default_rng(synth.seed_for(4, 501))
+        model = {"layers": one["layers"] * cfg.n_layers, "out_norm": (1.0 + 0.1 * rng_w.standard_normal(4096)).astype(np.float32),
+                 "tok_embd": (synth.weights_np(F.Q4_K, cfg.vocab, cfg.dim, synth.seed_for(4, 502)), F.Q4_K),
+                 "output": (synth.weights_np(F.Q6_K, cfg.vocab, cfg.dim, synth.seed_for(4, 503)), F.Q6_K)}
+        n_layers_desc = "32 layers (dim 4096, GQA 32/8, FFN 14336, llama3-scaled RoPE)"
+    else:
+        cfg = Config(dim=1024, n_layers=28, n_heads=16, n_kv_heads=8, head_dim=128, ffn_dim=3072, vocab=151936,
+                     max_ctx=2048, rope_neox=True, rope_base=1e6)
+        model = synth.model_np(cfg, F.Q4_K, seed=synth.seed_for(2, 500), out_fmt=F.Q6_K, embd_fmt=F.Q6_K)
+        n_layers_desc = "28 layers (dim 1024, GQA 16/8 with q/k norms, FFN 3072)"
     rng = np.random.default_rng(7)
     with Net(eng, cfg) as net:
         net.load(model)
@@ -456,9 +475,9 @@ def network_bench(torch, eng, F, synth):
     return {"prefill_512_ms": round(pre_s * 1e3, 2), "prefill_tokens_per_s": round(512 / pre_s, 1),
             "decode_ms_per_token": round(dec_s * 1e3, 3), "decode_tokens_per_s": round(1 / dec_s, 1),
             "context": "positions 512-575", "finite_logits": ok,
-            "what": "whole network on the device: embedding, 28 layers (RMS norm fused into the products' input "
-                    "quantization, rope, f16 KV cache; prefill attention on f16 MFMAs, decode attention over "
-                    "context chunks), logits; host wall clock per forward call"}
+            "what": f"whole network on the device: embedding, {n_layers_desc}: RMS norm fused into the products' "
+                    "input quantization, rope, f16 KV cache, prefill attention on f16 MFMAs, decode attention over "
+                    "context chunks; logits; host wall clock per forward call"}
 
 
 def measured_peaks():
