@@ -802,11 +802,22 @@ int gemms(hkhip_net *net, uint32_t n, const hkhip_mat *mats, uint32_t nparts, fl
 }
 
 // The products of one pass. xin: f32 input [n][cols]; norm: fused RMS norm weights or null.
+// Whether a product of n tokens runs quantizer + hkhip_mm (GEMM, or the small-batch MFMA kernel
+// for the formats that have it) rather than the decode kernels on the f32 input: the decode
+// kernels' per-token dot work grows with the token count, the small-batch kernel's does not, but
+// the quantizer launches cost a few microseconds each. Measured on whole Llama-3-8B-shaped passes:
+// 4 tokens 3.3 ms on the decode kernels (their 4-token form) against 4.0 on the small-batch path;
+// 5, 6 and 8 tokens (the decode kernels' 8-token form) 4.9, 5.2 and 5.9 ms against 4.0-4.3.
+constexpr uint32_t NET_SK_MIN = 5;
+bool gemm_path(uint32_t n, int t) {
+    return n > MAX_DECODE || (n >= NET_SK_MIN && (t == HKHIP_Q4_K || t == HKHIP_Q6_K));
+}
+
 int product(hkhip_net *net, uint32_t n, const hkhip_mat *mats, uint32_t nparts, const float *xin, const float *norm,
             float *const *ys, const float *const *biases, int mode) {
     hkhip_engine *eng = net->eng;
     const uint32_t cols = mats[0].cols;
-    if (n <= MAX_DECODE) {
+    if (!gemm_path(n, mats[0].t)) {
         if (norm) {
             const int rc = hkhip_matvec_parts_rmsnorm(eng, mats, nparts, xin, norm, net->cfg.rms_eps, n, ys, biases, mode);
             if (rc != HKHIP_E_UNSUPPORTED_SHAPE) return rc;
@@ -933,13 +944,13 @@ int run_pass(hkhip_net *net, uint32_t n) {
             float *const ys[1] = {net->x};
             if ((rc = product(net, n, &L.wo, 1, net->att, nullptr, ys, nullptr, HKHIP_ACCUMULATE))) return rc;
         }
-        if (n <= MAX_DECODE) {
+        if (!gemm_path(n, L.wgu.t)) {
             float *const ys[1] = {net->h};
             if ((rc = product(net, n, &L.wgu, 1, net->x, L.ffn_norm, ys, nullptr, HKHIP_SILU_MUL))) return rc;
         } else {
             float *const ys[1] = {net->gu};
             if ((rc = product(net, n, &L.wgu, 1, net->x, L.ffn_norm, ys, nullptr, HKHIP_STORE))) return rc;
-            if (act_kind(L.wd.t) != HKHIP_ACT_F32) { // silu(gate) * up folded into the down input's quantizer
+            if (gemm_path(n, L.wd.t) && act_kind(L.wd.t) != HKHIP_ACT_F32) { // silu(gate) * up folded into the down input's quantizer
                 NET_TRY(launch_qact_row(net->gu, n, c.ffn_dim, act_kind(L.wd.t), net->xq, nullptr, 0.0f, true, s),
                         "swiglu + qact");
                 float *const yd[1] = {net->x};
