@@ -28,6 +28,7 @@
 #include <vector>
 
 #include "common.hpp"
+#include "quant.hpp"
 
 using namespace hkhip;
 
@@ -89,6 +90,36 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0)
     __builtin_amdgcn_wave_barrier();
 }
+// One head row in a wave's LDS row h (hd values, lanes strided by 64): headNorm when nw is given
+// (rmsNorm over the head, ops.zig:31-38), then ropeAngles / ropeApply at position pos (ops.zig:
+// 154-185). The decode attention kernel runs the same steps on the rows it needs, so both give the
+// same values.
+__device__ __forceinline__ void head_norm_rope(float *h, const float *src, const float *nw, uint32_t pos,
+                                               const RopeArgs &a, uint32_t lane) {
+    const uint32_t hd = a.hd;
+    for (uint32_t d = lane; d < hd; d += 64) h[d] = src[d];
+    wave_sync();
+    if (nw) {
+        float ss = 0.0f;
+        for (uint32_t d = lane; d < hd; d += 64) ss = fmaf(h[d], h[d], ss);
+        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, float(hd)) + a.eps));
+        wave_sync();
+        for (uint32_t d = lane; d < hd; d += 64) h[d] = (h[d] * inv) * nw[d];
+        wave_sync();
+    }
+    const float p = float(pos);
+    for (uint32_t i = lane; i < a.rope_half; i += 64) {
+        const float ang = p * a.inv_freq[i];
+        const float c = cosf(ang) * a.mscale, s = sinf(ang) * a.mscale;
+        const uint32_t i0 = a.neox ? i : 2 * i, i1 = a.neox ? i + a.rope_half : 2 * i + 1;
+        const float x0 = h[i0], x1 = h[i1];
+        h[i0] = x0 * c - x1 * s;
+        h[i1] = x0 * s + x1 * c;
+    }
+    wave_sync();
+}
+
 __global__ __launch_bounds__(256) void rope_kv_kernel(RopeArgs a) {
     const uint32_t t = blockIdx.y, w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const uint32_t hh = 4 * blockIdx.x + w;
@@ -110,31 +141,9 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(RopeArgs a) {
     }
     const uint32_t g = isq ? hh : hh - a.nh;
     const float *src = isq ? a.q + uint64_t(t) * a.sq + g * hd : a.k + uint64_t(t) * a.skv + g * hd;
-    const float *nw = isq ? a.q_norm : a.k_norm;
     __shared__ float hs[4][256];
     float *h = hs[w];
-    for (uint32_t d = lane; d < hd; d += 64) h[d] = src[d];
-    wave_sync();
-    if (nw) { // headNorm: rmsNorm over the head (ops.zig:31-38)
-        float ss = 0.0f;
-        for (uint32_t d = lane; d < hd; d += 64) ss = fmaf(h[d], h[d], ss);
-        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
-        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, float(hd)) + a.eps));
-        wave_sync();
-        for (uint32_t d = lane; d < hd; d += 64) h[d] = (h[d] * inv) * nw[d];
-        wave_sync();
-    }
-    // ropeAngles (ops.zig:154-160): angle = f32(pos) * inv_freq[i]; ropeApply (164-185).
-    const float p = float(pos);
-    for (uint32_t i = lane; i < a.rope_half; i += 64) {
-        const float ang = p * a.inv_freq[i];
-        const float c = cosf(ang) * a.mscale, s = sinf(ang) * a.mscale;
-        const uint32_t i0 = a.neox ? i : 2 * i, i1 = a.neox ? i + a.rope_half : 2 * i + 1;
-        const float x0 = h[i0], x1 = h[i1];
-        h[i0] = x0 * c - x1 * s;
-        h[i1] = x0 * s + x1 * c;
-    }
-    wave_sync();
+    head_norm_rope(h, src, isq ? a.q_norm : a.k_norm, pos, a, lane);
     if (isq) {
         float *dst = a.q + uint64_t(t) * a.sq + g * hd;
         for (uint32_t d = lane; d < hd; d += 64) dst[d] = h[d];
@@ -186,6 +195,13 @@ struct AttnArgs {
     uint32_t n, nh, nkv, hd, max_ctx, nslice;
     float scale;
     uint32_t sq;
+    // Decode only. att: with one chunk per (head, token) the normalized result goes straight here
+    // (part unused). fused (one-token passes): q is the projection's raw output, and the kernel
+    // does rope_kv_kernel's work itself (the q and new key head norms and rotations, the new key
+    // and value rows into the caches), with r's fields.
+    float *att;
+    int fused;
+    RopeArgs r;
 };
 
 // A lane's DL dimensions of one value row: DL halves in one (DL = 1: the low half) or two words.
@@ -295,14 +311,81 @@ __global__ __launch_bounds__(256) void attn_slice_kernel(AttnArgs a) {
 }
 
 // Decode attention (passes of up to MAX_DECODE tokens): G workgroups of NWV waves per (query head,
-// token), G fixed by the context length so that every 64-position step of a full context has a
-// wave of its own (the context's loads spread over G times more CUs than one workgroup would
-// use); wave w of chunk g takes step g*NWV + w. A workgroup merges its waves' {max, sum, acc} in
-// LDS (as the slice merge does, attention.zig:113-133) and writes the chunk's partial ({-inf, 0,
-// 0...} past the token's position); attn_combine_kernel merges the G partials. In a step a lane
-// loads its position's key row (scores: lane = position), then the value rows go 16 bytes per
-// lane: lane = (row r of the RPI rows one load covers, 8 dimensions), so a step is HD/8 + 64/RPI
-// loads per lane; the RPI partial sums of a dimension are added across lanes once, at the end.
+// token), G set by the context the pass reaches (host side: a power of two, so that every 64-position
+// step up to the last position has a wave of its own; the context's loads spread over G times more
+// CUs than one workgroup would use); wave w of chunk g takes step g*NWV + w. A workgroup merges its
+// waves' {max, sum, acc} in LDS (as the slice merge does, attention.zig:113-133) and writes the
+// chunk's partial ({-inf, 0, 0...} past the token's position), which attn_combine_kernel merges;
+// with G = 1 it writes the normalized result itself. In a step a lane loads its position's key row
+// (scores: lane = position), then the value rows go 16 bytes per lane: lane = (row r of the RPI rows
+// one load covers, 8 dimensions), so a step is HD/8 + 64/RPI loads per lane; the RPI partial sums of
+// a dimension are added across lanes once, at the end.
+//
+// One-token passes run fused: the raw q row is normalized and rotated by each wave (the same steps
+// as rope_kv_kernel), and the wave whose step holds the token's position builds the new key row
+// (norm, rotation, f16) and value row, uses them in place of the cache rows it loaded, and -- in the
+// first query head of each key/value group -- writes them to the caches.
+// Sum / max over a wave: DPP moves within each row of 16 lanes, then the four rows' results.
+__device__ __forceinline__ float wave_sum_f(float v) {
+    v += dpp_f<DPP_XOR1>(v);
+    v += dpp_f<DPP_XOR2>(v);
+    v += dpp_f<DPP_HALF_MIRROR>(v);
+    v += dpp_f<DPP_MIRROR>(v);
+    return (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
+}
+__device__ __forceinline__ float wave_max_f(float v) {
+    const float r = row_max(v);
+    return fmaxf(fmaxf(readlane_f(r, 0), readlane_f(r, 16)), fmaxf(readlane_f(r, 32), readlane_f(r, 48)));
+}
+
+// The fused decode pass's q row (and, with kx, the new key row) of one head: headNorm (ops.zig:
+// 31-38) from registers, then the rotation of ropeAngles / ropeApply (ops.zig:154-185) in the rows'
+// LDS copies hq / hk, one sin/cos per angle for both rows. nw*, fr: norm weights and inv_freq
+// entries lane + 64 j / lane + 64 f, loaded by the caller.
+template <int HD> constexpr int rope_regs() { return (HD / 2 + 63) / 64; }
+template <int HD, bool KEY>
+__device__ __forceinline__ void qk_norm_rope(float *hq, float *hk, const float (&qx)[HD / 64], const float (&kx)[HD / 64],
+                                             const float (&qnw)[HD / 64], const float (&knw)[HD / 64],
+                                             const float (&fr)[rope_regs<HD>()], uint32_t pos, const RopeArgs &a,
+                                             uint32_t lane) {
+    float ssq = 0.0f, ssk = 0.0f;
+#pragma unroll
+    for (int j = 0; j < HD / 64; j++) {
+        ssq = fmaf(qx[j], qx[j], ssq);
+        if (KEY) ssk = fmaf(kx[j], kx[j], ssk);
+    }
+    ssq = wave_sum_f(ssq);
+    if (KEY) ssk = wave_sum_f(ssk);
+    const float iq = a.q_norm ? __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ssq, float(HD)) + a.eps)) : 1.0f;
+    const float ik = KEY && a.k_norm ? __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ssk, float(HD)) + a.eps)) : 1.0f;
+#pragma unroll
+    for (int j = 0; j < HD / 64; j++) {
+        hq[lane + 64 * j] = a.q_norm ? (qx[j] * iq) * qnw[j] : qx[j];
+        if (KEY) hk[lane + 64 * j] = a.k_norm ? (kx[j] * ik) * knw[j] : kx[j];
+    }
+    wave_sync();
+    const float p = float(pos);
+#pragma unroll
+    for (int f = 0; f < rope_regs<HD>(); f++) {
+        const uint32_t i = lane + 64 * f;
+        if (i < a.rope_half) {
+            float sn, cs;
+            sincosf(p * fr[f], &sn, &cs);
+            const float c = cs * a.mscale, s = sn * a.mscale;
+            const uint32_t i0 = a.neox ? i : 2 * i, i1 = a.neox ? i + a.rope_half : 2 * i + 1;
+            const float x0 = hq[i0], x1 = hq[i1];
+            hq[i0] = x0 * c - x1 * s;
+            hq[i1] = x0 * s + x1 * c;
+            if (KEY) {
+                const float y0 = hk[i0], y1 = hk[i1];
+                hk[i0] = y0 * c - y1 * s;
+                hk[i1] = y0 * s + y1 * c;
+            }
+        }
+    }
+    wave_sync();
+}
+
 template <int HD, int NWV>
 __global__ __launch_bounds__(NWV * 64) void attn_decode_kernel(AttnArgs a) {
     constexpr int LPR = HD / 8, RPI = 64 / LPR, NI = 64 / RPI; // lanes per value row, rows per load, loads
@@ -311,12 +394,29 @@ __global__ __launch_bounds__(NWV * 64) void attn_decode_kernel(AttnArgs a) {
     const uint32_t g = blockIdx.x, h = blockIdx.y, t = blockIdx.z;
     __shared__ float qs[NWV][HD];
     __shared__ float red_m[NWV], red_l[NWV];
+    __shared__ float prs[NWV][64]; // a step's probabilities, for the value rows' lanes
     __shared__ float red_acc[NWV][HD];
-    const uint32_t kvh = h / (a.nh / a.nkv);
+    __shared__ float kn[NWV][HD];                                     // fused: the new key row, f32
+    __shared__ __attribute__((aligned(16))) __half kvh16[NWV][2][HD]; // fused: new key / value rows, f16
+    const uint32_t grp = a.nh / a.nkv, kvh = h / grp;
     const float *qsrc = a.q + uint64_t(t) * a.sq + h * HD;
-    float qv[HD / 64];
+    float qv[HD / 64], kx[HD / 64], vx[HD / 64];
 #pragma unroll
     for (int j = 0; j < HD / 64; j++) qv[j] = qsrc[lane + 64 * j];
+    // Fused: raw rows of the new key and value (one-token passes: token 0), the norm weights and the
+    // rotation frequencies, all loaded before the cache rows so that none waits behind them.
+    float qnw[HD / 64], knw[HD / 64], fr[rope_regs<HD>()];
+    if (a.fused) {
+#pragma unroll
+        for (int j = 0; j < HD / 64; j++) {
+            kx[j] = a.r.k[kvh * HD + lane + 64 * j];
+            vx[j] = a.r.v[kvh * HD + lane + 64 * j];
+            qnw[j] = a.r.q_norm ? a.r.q_norm[lane + 64 * j] : 1.0f;
+            knw[j] = a.r.k_norm ? a.r.k_norm[lane + 64 * j] : 1.0f;
+        }
+#pragma unroll
+        for (int f = 0; f < rope_regs<HD>(); f++) fr[f] = lane + 64 * f < a.r.rope_half ? a.r.inv_freq[lane + 64 * f] : 0.0f;
+    }
     float m = -INFINITY, l = 0.0f, acc[8];
 #pragma unroll
     for (int j = 0; j < 8; j++) acc[j] = 0.0f;
@@ -342,8 +442,50 @@ __global__ __launch_bounds__(NWV * 64) void attn_decode_kernel(AttnArgs a) {
     const uint32_t pos = a.pos0[0] + t;
     if (p0 <= pos) {
         const uint32_t p_end = min(p0 + 64, pos + 1);
+        // Fused pass, wave holding the new position: its score (dot_new, in the order of the cache
+        // rows' dot below) and value row (vnew) replace what the loads brought for that position.
+        const bool has_new = a.fused && pos < p0 + 64;
+        float dot_new = 0.0f;
+        uint4 vnew = make_uint4(0, 0, 0, 0);
+        if (a.fused) {
+            if (has_new) {
+                qk_norm_rope<HD, true>(qs[w], kn[w], qv, kx, qnw, knw, fr, pos, a.r, lane);
 #pragma unroll
-        for (int j = 0; j < HD / 64; j++) qs[w][lane + 64 * j] = qv[j];
+                for (int j = 0; j < HD / 64; j++) {
+                    kvh16[w][0][lane + 64 * j] = __float2half(kn[w][lane + 64 * j]);
+                    kvh16[w][1][lane + 64 * j] = __float2half(vx[j]);
+                }
+                wave_sync();
+                for (int c = 0; c < HD / 8; c++) {
+                    const uint4 kw = reinterpret_cast<const uint4 *>(kvh16[w][0])[c];
+                    const __half2 *hp = reinterpret_cast<const __half2 *>(&kw);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const float2 f = __half22float2(hp[e]);
+                        dot_new = fmaf(qs[w][8 * c + 2 * e], f.x, dot_new);
+                        dot_new = fmaf(qs[w][8 * c + 2 * e + 1], f.y, dot_new);
+                    }
+                }
+                vnew = *reinterpret_cast<const uint4 *>(&kvh16[w][1][8 * vc]);
+                if (h % grp == 0) { // one writer per key/value head
+                    __half *kd = a.r.kc + (uint64_t(kvh) * a.max_ctx + pos) * HD;
+                    __half *vd = a.r.vc + (uint64_t(kvh) * a.max_ctx + pos) * HD;
+                    __half *vtd = a.r.vt + uint64_t(kvh) * HD * a.r.vt_stride + pos;
+#pragma unroll
+                    for (int j = 0; j < HD / 64; j++) {
+                        const uint32_t d = lane + 64 * j;
+                        kd[d] = kvh16[w][0][d];
+                        vd[d] = kvh16[w][1][d];
+                        vtd[uint64_t(d) * a.r.vt_stride] = kvh16[w][1][d];
+                    }
+                }
+            } else {
+                qk_norm_rope<HD, false>(qs[w], kn[w], qv, kx, qnw, knw, fr, pos, a.r, lane);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < HD / 64; j++) qs[w][lane + 64 * j] = qv[j];
+        }
 #pragma unroll
         for (int c = 0; c < HD / 8; c++) asm volatile("" : "+v"(kr[c].x), "+v"(kr[c].y), "+v"(kr[c].z), "+v"(kr[c].w));
 #pragma unroll
@@ -359,21 +501,22 @@ __global__ __launch_bounds__(NWV * 64) void attn_decode_kernel(AttnArgs a) {
                 dot = fmaf(qw[8 * c + 2 * e + 1], f.y, dot);
             }
         }
+        if (has_new && pp == pos) dot = dot_new;
         const float s = pp < p_end ? dot * a.scale : -INFINITY;
-        float mx = s;
-        for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-        const float mn = fmaxf(m, mx);
+        const float mn = fmaxf(m, wave_max_f(s));
         const float pr = pp < p_end ? expf(s - mn) : 0.0f;
-        float ps = pr;
-        for (int o = 32; o >= 1; o >>= 1) ps += __shfl_xor(ps, o);
+        const float ps = wave_sum_f(pr);
+        prs[w][lane] = pr;
+        wave_sync();
         const float corr = m == -INFINITY ? 0.0f : expf(m - mn);
         l = l * corr + ps;
 #pragma unroll
         for (int j = 0; j < 8; j++) acc[j] *= corr;
 #pragma unroll
         for (int i = 0; i < NI; i++) {
-            const float pi = __shfl(pr, RPI * i + vr_); // 0 for positions past the step
-            const __half2 *hp = reinterpret_cast<const __half2 *>(&vv[i]);
+            const float pi = prs[w][RPI * i + vr_]; // 0 for positions past the step
+            const uint4 vw = has_new && p0 + RPI * i + vr_ == pos ? vnew : vv[i];
+            const __half2 *hp = reinterpret_cast<const __half2 *>(&vw);
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const float2 f = __half22float2(hp[e]);
@@ -406,6 +549,17 @@ __global__ __launch_bounds__(NWV * 64) void attn_decode_kernel(AttnArgs a) {
     for (int i = 0; i < NWV; i++) {
         wt[i] = red_l[i] != 0.0f ? expf(red_m[i] - big) : 0.0f;
         tot = fmaf(wt[i], red_l[i], tot);
+    }
+    if (a.att) { // one chunk: the normalized result (as attn_combine_kernel writes it)
+        const float inv = 1.0f / tot;
+        float *o = a.att + (uint64_t(t) * a.nh + h) * HD;
+        for (uint32_t d = threadIdx.x; d < HD; d += NWV * 64) {
+            float v = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NWV; i++) v = fmaf(wt[i], red_acc[i][d], v);
+            o[d] = v * inv;
+        }
+        return;
     }
     // The chunk's partial: {max, sum, acc} (unnormalized), as attn_combine_kernel reads them.
     float *out = a.part + ((uint64_t(t) * a.nh + h) * gridDim.x + g) * (HD + 2);
@@ -672,7 +826,7 @@ struct hkhip_net {
     uint32_t *io = nullptr, *tok = nullptr, *pos = nullptr; // device {pos, tokens[cap]}
     uint32_t *stage = nullptr;                               // pinned host copy of io
     std::map<uint32_t, hipGraphExec_t> graphs;
-    std::map<uint32_t, int> runs; // eager runs per decode token count (a graph is captured after one)
+    std::map<uint32_t, int> runs; // eager runs per decode shape: token count | attention chunks << 8 (a graph is captured after one)
     uint32_t last_n = 0;
 };
 
@@ -691,6 +845,10 @@ int hfail(hipError_t e, const char *what) {
 uint32_t qdim(const hkhip_net_config &c) { return c.n_heads * c.head_dim; }
 uint32_t kvdim(const hkhip_net_config &c) { return c.n_kv_heads * c.head_dim; }
 uint32_t qkvdim(const hkhip_net_config &c) { return qdim(c) + 2 * kvdim(c); }
+// Waves per decode attention workgroup (64 positions each). Four: a workgroup of eight takes longer
+// for the same positions (one CU then pulls twice the key and value bytes: 15.4 against 11.2 us per
+// layer at 576 positions with the merge), and with four the context's loads spread over more CUs.
+constexpr uint32_t ATT_DWAVES = 4;
 uint32_t nslices(const hkhip_net_config &c) { return (c.max_ctx + ATT_SLICE - 1) / ATT_SLICE; }
 uint32_t vt_stride(const hkhip_net_config &c) { return (c.max_ctx + 31) / 32 * 32; }
 bool prefill_mfma(const hkhip_net_config &c) { return c.head_dim == 64 || c.head_dim == 128; }
@@ -852,7 +1010,8 @@ int product(hkhip_net *net, uint32_t n, const hkhip_mat *mats, uint32_t nparts, 
     return rc ? rc : gemms(net, n, mats, nparts, ys, biases, mode);
 }
 
-int run_pass(hkhip_net *net, uint32_t n) {
+// gb: decode attention chunks per (head, token) (passes of up to MAX_DECODE tokens).
+int run_pass(hkhip_net *net, uint32_t n, uint32_t gb) {
     const hkhip_net_config &c = net->cfg;
     hkhip_engine *eng = net->eng;
     hipStream_t s = eng->cur;
@@ -889,11 +1048,14 @@ int run_pass(hkhip_net *net, uint32_t n) {
         RopeArgs ra{q, k, v, L.q_norm, L.k_norm, net->inv_freq, net->kc + li * cache_layer,
                     net->vc + li * cache_layer, net->vt + li * vt_layer, net->pos, c.n_heads, c.n_kv_heads, c.head_dim,
                     c.rope_dim / 2, c.rope_neox, c.max_ctx, vt_stride(c), S, SKV, 0, c.rope_mscale, c.rms_eps};
-        // Prefill passes write the value heads with v_cache_kernel (coalesced transposed writes).
-        const bool vsep = n > MAX_DECODE;
+        // Prefill passes write the value heads with v_cache_kernel (coalesced transposed writes);
+        // one-token passes do all of it in the attention kernel.
+        const bool vsep = n > MAX_DECODE, fused = n == 1;
         ra.nheads = c.n_heads + (vsep ? 1 : 2) * c.n_kv_heads;
-        hipLaunchKernelGGL(rope_kv_kernel, dim3((ra.nheads + 3) / 4, n), dim3(256), 0, s, ra);
-        NET_TRY(hipGetLastError(), "rope / kv write");
+        if (!fused) {
+            hipLaunchKernelGGL(rope_kv_kernel, dim3((ra.nheads + 3) / 4, n), dim3(256), 0, s, ra);
+            NET_TRY(hipGetLastError(), "rope / kv write");
+        }
         if (vsep) {
             hipLaunchKernelGGL(v_cache_kernel, dim3(c.n_kv_heads, (n + 15) / 16), dim3(256), 0, s, v,
                                net->vc + li * cache_layer, net->vt + li * vt_layer, net->pos, n, SKV, c.head_dim,
@@ -913,18 +1075,22 @@ int run_pass(hkhip_net *net, uint32_t n) {
             AttnArgs aa{q, net->kc + li * cache_layer, net->vc + li * cache_layer, nullptr, net->pos, n, c.n_heads,
                         c.n_kv_heads, c.head_dim, c.max_ctx, 0, 1.0f / sqrtf(float(c.head_dim)), S};
             aa.part = net->part;
-            const uint32_t G = (ns + 3) / 4;
-            const dim3 dg(G, c.n_heads, n);
+            aa.att = gb == 1 ? net->att : nullptr;
+            aa.fused = fused ? 1 : 0;
+            aa.r = ra;
+            const dim3 dg(gb, c.n_heads, n);
             if (c.head_dim == 64)
-                hipLaunchKernelGGL((attn_decode_kernel<64, 4>), dg, dim3(256), 0, s, aa);
+                hipLaunchKernelGGL((attn_decode_kernel<64, ATT_DWAVES>), dg, dim3(64 * ATT_DWAVES), 0, s, aa);
             else if (c.head_dim == 128)
-                hipLaunchKernelGGL((attn_decode_kernel<128, 4>), dg, dim3(256), 0, s, aa);
+                hipLaunchKernelGGL((attn_decode_kernel<128, ATT_DWAVES>), dg, dim3(64 * ATT_DWAVES), 0, s, aa);
             else
-                hipLaunchKernelGGL((attn_decode_kernel<256, 4>), dg, dim3(256), 0, s, aa);
+                hipLaunchKernelGGL((attn_decode_kernel<256, ATT_DWAVES>), dg, dim3(64 * ATT_DWAVES), 0, s, aa);
             NET_TRY(hipGetLastError(), "decode attention");
-            hipLaunchKernelGGL(attn_combine_kernel, dim3(c.n_heads, n), dim3(std::min(256u, std::max(64u, (c.head_dim + 63) / 64 * 64))),
-                               G * 4, s, net->part, net->att, c.n_heads, c.head_dim, G);
-            NET_TRY(hipGetLastError(), "decode attention combine");
+            if (gb > 1) {
+                hipLaunchKernelGGL(attn_combine_kernel, dim3(c.n_heads, n), dim3(std::min(256u, std::max(64u, (c.head_dim + 63) / 64 * 64))),
+                                   gb * 4, s, net->part, net->att, c.n_heads, c.head_dim, gb);
+                NET_TRY(hipGetLastError(), "decode attention combine");
+            }
         } else {
             AttnArgs aa{q, net->kc + li * cache_layer, net->vc + li * cache_layer, net->part, net->pos, n, c.n_heads,
                         c.n_kv_heads, c.head_dim, c.max_ctx, ns, 1.0f / sqrtf(float(c.head_dim)), S};
@@ -1133,7 +1299,7 @@ int hkhip_net_forward(hkhip_net *net, const uint32_t *tokens, uint32_t n, uint32
         net->stage[0] = pos0;
         memcpy(net->stage + 1, tokens, n * 4);
         NET_TRY(hipMemcpyAsync(net->io, net->stage, (n + 1) * 4, hipMemcpyHostToDevice, s), "tokens");
-        if ((rc = run_pass(net, n))) return rc;
+        if ((rc = run_pass(net, n, 0))) return rc;
         NET_TRY(hipStreamSynchronize(s), "prefill pass");
         net->last_n = n;
         return HKHIP_OK;
@@ -1143,15 +1309,23 @@ int hkhip_net_forward(hkhip_net *net, const uint32_t *tokens, uint32_t n, uint32
     net->stage[0] = pos0;
     memcpy(net->stage + 1, tokens, n * 4);
     NET_TRY(hipMemcpyAsync(net->io, net->stage, (n + 1) * 4, hipMemcpyHostToDevice, s), "tokens");
-    auto it = net->graphs.find(n);
+    // Decode attention chunks: a power of two covering the positions the pass reaches (ATT_DWAVES
+    // waves of 64 positions each), so that short contexts skip the merge launch; one graph per (size,
+    // chunks).
+    const uint32_t dw = ATT_DWAVES, gmax = (nslices(c) + dw - 1) / dw, need = (pos0 + n + 64 * dw - 1) / (64 * dw);
+    uint32_t gb = 1;
+    while (gb < need) gb <<= 1;
+    gb = std::min(gb, gmax);
+    const uint32_t key = n | (gb << 8);
+    auto it = net->graphs.find(key);
     if (it != net->graphs.end()) {
         NET_TRY(hipGraphLaunch(it->second, s), "graph launch");
-    } else if (net->runs[n]++ == 0) {
-        if ((rc = run_pass(net, n))) return rc; // first pass of this size: eager (fills the launch caches)
+    } else if (net->runs[key]++ == 0) {
+        if ((rc = run_pass(net, n, gb))) return rc; // first pass of this shape: eager (fills the launch caches)
     } else {
         hipGraph_t g = nullptr;
         NET_TRY(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "begin capture");
-        rc = run_pass(net, n);
+        rc = run_pass(net, n, gb);
         const hipError_t e = hipStreamEndCapture(s, &g);
         if (rc) {
             if (g) (void)hipGraphDestroy(g);
@@ -1162,7 +1336,7 @@ int hkhip_net_forward(hkhip_net *net, const uint32_t *tokens, uint32_t n, uint32
         const hipError_t ei = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
         (void)hipGraphDestroy(g);
         NET_TRY(ei, "graph instantiate");
-        net->graphs[n] = ex;
+        net->graphs[key] = ex;
         NET_TRY(hipGraphLaunch(ex, s), "graph launch");
     }
     // The pass is done when forward returns (the next call reuses the pinned staging buffer).

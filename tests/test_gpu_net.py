@@ -50,6 +50,10 @@ CASES = {
     # IQ4_NL body with Q4_K output; partial rotary (half the head), no GQA
     "iq4nl-partial-rope": (Config(dim=256, n_layers=1, n_heads=4, n_kv_heads=4, head_dim=64, ffn_dim=256, vocab=300,
                                   max_ctx=300, rope_dim=32), F.IQ4_NL, F.Q4_K, F.Q6_K, True, False),
+    # head_dim 256 (four-wave decode attention chunks of 256 positions: the decode passes after the
+    # prefill span two chunks and the merge), q/k norms, GQA 2:1
+    "hd256-q4k": (Config(dim=256, n_layers=1, n_heads=2, n_kv_heads=1, head_dim=256, ffn_dim=256, vocab=300,
+                         max_ctx=700, rope_neox=True, rope_base=1e4), F.Q4_K, F.Q8_0, F.Q8_0, True, False),
 }
 
 
@@ -129,9 +133,10 @@ def test_net_from_hk_file(eng, tmp_path, arch, fmt, tie, vec_type):
 
 
 def test_net_long_context(eng):
-    """Decode passes past 512 positions, where a decode attention wave takes more than one
-    64-position step (eight waves per (head, token)); a prefill of 1030 tokens (four-wave MFMA
-    tiles over 33 position tiles) before them."""
+    """Decode passes past 1030 positions, where decode attention runs over five chunk workgroups
+    of 256 positions per (head, token) and their merge (one-token passes fused with the key/value
+    writes, passes of 3 and 8 tokens after the separate rope / cache kernel); a prefill of 1030
+    tokens (four-wave MFMA tiles over 33 position tiles) before them."""
     from hk_amd.net import Net
 
     cfg = Config(dim=128, n_layers=1, n_heads=2, n_kv_heads=1, head_dim=64, ffn_dim=256, vocab=256, max_ctx=1100,
