@@ -23,18 +23,18 @@ static mv_kernel_t kernel_for(int t, int nt) {
     }
 }
 
-static mv_kernel_t kernelr_for(int t, int nt, int c, int ks) {
+static mv_kernel_t kernelr_for(int t, int nt, int c, int ks, bool norm) {
     switch (t) {
-    case HKHIP_Q4_K: return mvr_pick<HKHIP_Q4_K>(nt, c, ks);
-    case HKHIP_Q6_K: return mvr_pick<HKHIP_Q6_K>(nt, c, ks);
-    case HKHIP_Q5_K: return mvr_pick<HKHIP_Q5_K>(nt, c, ks);
-    case HKHIP_IQ4_XS: return mvr_pick<HKHIP_IQ4_XS>(nt, c, ks);
-    case HKHIP_Q8_0: return mvr_pick<HKHIP_Q8_0>(nt, c, ks);
-    case HKHIP_IQ4_NL: return mvr_pick<HKHIP_IQ4_NL>(nt, c, ks);
-    case HKHIP_Q4_0: return mvr_pick<HKHIP_Q4_0>(nt, c, ks);
-    case HKHIP_Q4_1: return mvr_pick<HKHIP_Q4_1>(nt, c, ks);
-    case HKHIP_Q5_0: return mvr_pick<HKHIP_Q5_0>(nt, c, ks);
-    case HKHIP_Q5_1: return mvr_pick<HKHIP_Q5_1>(nt, c, ks);
+    case HKHIP_Q4_K: return mvr_pick<HKHIP_Q4_K>(nt, c, ks, norm);
+    case HKHIP_Q6_K: return mvr_pick<HKHIP_Q6_K>(nt, c, ks, norm);
+    case HKHIP_Q5_K: return mvr_pick<HKHIP_Q5_K>(nt, c, ks, norm);
+    case HKHIP_IQ4_XS: return mvr_pick<HKHIP_IQ4_XS>(nt, c, ks, norm);
+    case HKHIP_Q8_0: return mvr_pick<HKHIP_Q8_0>(nt, c, ks, norm);
+    case HKHIP_IQ4_NL: return mvr_pick<HKHIP_IQ4_NL>(nt, c, ks, norm);
+    case HKHIP_Q4_0: return mvr_pick<HKHIP_Q4_0>(nt, c, ks, norm);
+    case HKHIP_Q4_1: return mvr_pick<HKHIP_Q4_1>(nt, c, ks, norm);
+    case HKHIP_Q5_0: return mvr_pick<HKHIP_Q5_0>(nt, c, ks, norm);
+    case HKHIP_Q5_1: return mvr_pick<HKHIP_Q5_1>(nt, c, ks, norm);
     default: return nullptr;
     }
 }
@@ -141,7 +141,7 @@ static hipError_t launch_mv_chunk(int t, const MvPartDesc *parts, int nparts, ui
             c = mvr_cmax(t, nt);
             while (ks < 8 && 64u * c * ks < units) ks *= 2;
         }
-        mv_kernel_t k = 64u * c * ks >= units ? kernelr_for(t, nt, c, ks) : nullptr;
+        mv_kernel_t k = 64u * c * ks >= units ? kernelr_for(t, nt, c, ks, norm != nullptr) : nullptr;
         uint32_t total_rows = 0;
         for (int i = 0; i < nparts; i++) total_rows += parts[i].rows;
         // One token, rows of at most 64 units. Rows of up to 32 units are packed 2^lg lanes per
@@ -165,7 +165,7 @@ static hipError_t launch_mv_chunk(int t, const MvPartDesc *parts, int nparts, ui
         }
         // A fused RMS norm needs LDS for one partial sum per 16 inputs after the staging area.
         const uint32_t nflat = (nt == 1 ? 1u : n) * K;
-        const uint32_t norm_bytes = norm ? nflat / 4 : 0;
+        const uint32_t norm_bytes = norm ? nflat / 4 + 64 : 0; // partial sums, then the tokens' factors
         if (norm && !x) return hipErrorNotSupported;
         if (k && x) {
             // An f32 input is staged whole in LDS; when it does not fit, the LDS kernel splits the

@@ -822,7 +822,7 @@ __device__ __forceinline__ void mvr_stage_chunk(const float4 *xv, uint32_t c, bo
 // results meet in LDS at the end.
 // LG < 6 packs short rows: a row takes 2^LG lanes (one unit each, C = 1), so a wave covers
 // 64 >> LG rows per row slot and step and its row addresses are per lane.
-template <int T, int NT, int C, int R, int NW, int KS, int LG = 6>
+template <int T, int NT, int C, int R, int NW, int KS, int LG = 6, bool NORM = true>
 __global__ __launch_bounds__(NW * 64) void mmvr_kernel(MvArgs a) {
     using F = MvFmt<T>;
     using W = typename F::W;
@@ -924,12 +924,11 @@ __global__ __launch_bounds__(NW * 64) void mmvr_kernel(MvArgs a) {
         // Fused RMS norm: per-lane sums of squares of 16 inputs to LDS (the first chunks from the
         // registers, any further ones loaded once more), then every wave adds a token's sums in
         // one fixed order, so all workgroups get the same factor.
-        float invt[NT];
+        // The tokens' factors go to LDS (after the partial sums), not registers: NT of them live
+        // through the staging pushed the 8-token kernels into spills.
+        float *sinv = reinterpret_cast<float *>(smem + mvr_norm_offset(ntok, K, F::kq, KS > 1 ? NW * 64 * NT * 4 : 0)) + nflat / 16;
         auto norm_chunk = [&](float4 *v, uint32_t e) {
-            float inv = invt[0];
-#pragma unroll
-            for (int t = 1; t < NT; t++)
-                if (e / K == uint32_t(t)) inv = invt[t];
+            const float inv = sinv[e < nflat ? e / K : 0];
             const float4 *wv = reinterpret_cast<const float4 *>(a.norm + (e < nflat ? e % K : 0));
 #pragma unroll
             for (int i = 0; i < 4; i++) {
@@ -940,7 +939,7 @@ __global__ __launch_bounds__(NW * 64) void mmvr_kernel(MvArgs a) {
                 v[i].w = (v[i].w * inv) * w4.w;
             }
         };
-        if (a.norm) {
+        if (NORM && a.norm) {
             float *parts = reinterpret_cast<float *>(smem + mvr_norm_offset(ntok, K, F::kq, KS > 1 ? NW * 64 * NT * 4 : 0));
             auto sumsq = [&](const float4 *v, uint32_t e) {
                 float ss = 0.0f;
@@ -965,18 +964,20 @@ __global__ __launch_bounds__(NW * 64) void mmvr_kernel(MvArgs a) {
                 if (e < nflat) sumsq(tmp, e);
             }
             __syncthreads();
-#pragma unroll
-            for (int t = 0; t < NT; t++) {
-                invt[t] = 0.0f;
-                if (uint32_t(t) >= ntok) continue;
+            // Wave w adds token w's sums (and w + NW, ...), in the same order in every workgroup.
+            for (uint32_t t = wave; t < ntok; t += NW) {
                 float ss = 0.0f;
                 for (uint32_t q = t * (K / 16) + lane; q < (t + 1) * (K / 16); q += 64) ss += parts[q];
 #pragma unroll
                 for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
-                invt[t] = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, float(K)) + a.eps));
+                if (lane == 0) sinv[t] = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, float(K)) + a.eps));
             }
+            __syncthreads();
 #pragma unroll
-            for (int j = 0; j < PB; j++) norm_chunk(xv[j], 1024 * (wave + NW * j) + 16 * lane);
+            for (int j = 0; j < PB; j++) {
+                norm_chunk(xv[j], 1024 * (wave + NW * j) + 16 * lane);
+                asm volatile("" ::: "memory");
+            }
         }
 #pragma unroll
         for (int j = 0; j < PB; j++) {
@@ -987,7 +988,7 @@ __global__ __launch_bounds__(NW * 64) void mmvr_kernel(MvArgs a) {
         for (uint32_t c0 = wave + NW * PB; c0 < nchunk; c0 += NW * PB) {
 #pragma unroll
             for (int j = 0; j < PB; j++) xload(c0 + NW * j, xv[j]);
-            if (a.norm) {
+            if (NORM && a.norm) {
 #pragma unroll
                 for (int j = 0; j < PB; j++) norm_chunk(xv[j], 1024 * (c0 + NW * j) + 16 * lane);
             }
@@ -1185,33 +1186,35 @@ __host__ __device__ constexpr int mvr_nw(int t, int nt, int c) {
                : MVR_NWAVES;
 }
 
-template <int T, int NT, int C, int KS>
+// NORM: the variant with the fused RMS norm of the input (the 8-token kernels also come without
+// it: its staging code alone pushed them past the register file, 21 -> 28 us for the 8B gate/up).
+template <int T, int NT, int C, int KS, bool NORM>
 mv_kernel_t mvr_if_fits() {
     if constexpr (C <= mvr_cmax(T, NT) && KS <= mvr_nw(T, NT, C))
-        return mmvr_kernel<T, NT, C, mvr_rows(NT, C), mvr_nw(T, NT, C), KS>;
+        return mmvr_kernel<T, NT, C, mvr_rows(NT, C), mvr_nw(T, NT, C), KS, 6, NORM>;
     else
         return nullptr;
 }
 
 // Units per lane c and slices ks: one slice for c <= cmax; beyond that, the largest c (cmax) in
 // 2, 4 or 8 slices.
-template <int T, int NT>
+template <int T, int NT, bool NORM>
 mv_kernel_t mvr_pick_c(int c, int ks) {
     constexpr int CM = mvr_cmax(T, NT);
     if (ks == 1) {
         switch (c) {
-        case 1: return mvr_if_fits<T, NT, 1, 1>();
-        case 2: return mvr_if_fits<T, NT, 2, 1>();
-        case 4: return mvr_if_fits<T, NT, 4, 1>();
-        case 8: return mvr_if_fits<T, NT, 8, 1>();
+        case 1: return mvr_if_fits<T, NT, 1, 1, NORM>();
+        case 2: return mvr_if_fits<T, NT, 2, 1, NORM>();
+        case 4: return mvr_if_fits<T, NT, 4, 1, NORM>();
+        case 8: return mvr_if_fits<T, NT, 8, 1, NORM>();
         default: return nullptr;
         }
     }
     if (c != CM) return nullptr;
     switch (ks) {
-    case 2: return mvr_if_fits<T, NT, CM, 2>();
-    case 4: return mvr_if_fits<T, NT, CM, 4>();
-    case 8: return mvr_if_fits<T, NT, CM, 8>();
+    case 2: return mvr_if_fits<T, NT, CM, 2, NORM>();
+    case 4: return mvr_if_fits<T, NT, CM, 4, NORM>();
+    case 8: return mvr_if_fits<T, NT, CM, 8, NORM>();
     default: return nullptr;
     }
 }
@@ -1240,12 +1243,12 @@ mv_kernel_t mvs_pick(int lg, int nw) {
 }
 
 template <int T>
-mv_kernel_t mvr_pick(int nt, int c, int ks) {
+mv_kernel_t mvr_pick(int nt, int c, int ks, bool norm) {
     switch (nt) {
-    case 1: return mvr_pick_c<T, 1>(c, ks);
-    case 2: return mvr_pick_c<T, 2>(c, ks);
-    case 4: return mvr_pick_c<T, 4>(c, ks);
-    case 8: return mvr_pick_c<T, 8>(c, ks);
+    case 1: return mvr_pick_c<T, 1, true>(c, ks);
+    case 2: return mvr_pick_c<T, 2, true>(c, ks);
+    case 4: return mvr_pick_c<T, 4, true>(c, ks);
+    case 8: return norm ? mvr_pick_c<T, 8, true>(c, ks) : mvr_pick_c<T, 8, false>(c, ks);
     default: return nullptr;
     }
 }
@@ -1254,34 +1257,34 @@ mv_kernel_t mvr_pick(int nt, int c, int ks) {
 // so the library builds in parallel; everything else only refers to them.
 #ifndef MMVQ_INSTANTIATE
 extern template mv_kernel_t pick<HKHIP_Q4_K>(int);
-extern template mv_kernel_t mvr_pick<HKHIP_Q4_K>(int, int, int);
+extern template mv_kernel_t mvr_pick<HKHIP_Q4_K>(int, int, int, bool);
 extern template mv_kernel_t mvs_pick<HKHIP_Q4_K>(int, int);
 extern template mv_kernel_t pick<HKHIP_Q6_K>(int);
-extern template mv_kernel_t mvr_pick<HKHIP_Q6_K>(int, int, int);
+extern template mv_kernel_t mvr_pick<HKHIP_Q6_K>(int, int, int, bool);
 extern template mv_kernel_t mvs_pick<HKHIP_Q6_K>(int, int);
 extern template mv_kernel_t pick<HKHIP_Q5_K>(int);
-extern template mv_kernel_t mvr_pick<HKHIP_Q5_K>(int, int, int);
+extern template mv_kernel_t mvr_pick<HKHIP_Q5_K>(int, int, int, bool);
 extern template mv_kernel_t mvs_pick<HKHIP_Q5_K>(int, int);
 extern template mv_kernel_t pick<HKHIP_IQ4_XS>(int);
-extern template mv_kernel_t mvr_pick<HKHIP_IQ4_XS>(int, int, int);
+extern template mv_kernel_t mvr_pick<HKHIP_IQ4_XS>(int, int, int, bool);
 extern template mv_kernel_t mvs_pick<HKHIP_IQ4_XS>(int, int);
 extern template mv_kernel_t pick<HKHIP_Q8_0>(int);
-extern template mv_kernel_t mvr_pick<HKHIP_Q8_0>(int, int, int);
+extern template mv_kernel_t mvr_pick<HKHIP_Q8_0>(int, int, int, bool);
 extern template mv_kernel_t mvs_pick<HKHIP_Q8_0>(int, int);
 extern template mv_kernel_t pick<HKHIP_IQ4_NL>(int);
-extern template mv_kernel_t mvr_pick<HKHIP_IQ4_NL>(int, int, int);
+extern template mv_kernel_t mvr_pick<HKHIP_IQ4_NL>(int, int, int, bool);
 extern template mv_kernel_t mvs_pick<HKHIP_IQ4_NL>(int, int);
 extern template mv_kernel_t pick<HKHIP_Q4_0>(int);
-extern template mv_kernel_t mvr_pick<HKHIP_Q4_0>(int, int, int);
+extern template mv_kernel_t mvr_pick<HKHIP_Q4_0>(int, int, int, bool);
 extern template mv_kernel_t mvs_pick<HKHIP_Q4_0>(int, int);
 extern template mv_kernel_t pick<HKHIP_Q4_1>(int);
-extern template mv_kernel_t mvr_pick<HKHIP_Q4_1>(int, int, int);
+extern template mv_kernel_t mvr_pick<HKHIP_Q4_1>(int, int, int, bool);
 extern template mv_kernel_t mvs_pick<HKHIP_Q4_1>(int, int);
 extern template mv_kernel_t pick<HKHIP_Q5_0>(int);
-extern template mv_kernel_t mvr_pick<HKHIP_Q5_0>(int, int, int);
+extern template mv_kernel_t mvr_pick<HKHIP_Q5_0>(int, int, int, bool);
 extern template mv_kernel_t mvs_pick<HKHIP_Q5_0>(int, int);
 extern template mv_kernel_t pick<HKHIP_Q5_1>(int);
-extern template mv_kernel_t mvr_pick<HKHIP_Q5_1>(int, int, int);
+extern template mv_kernel_t mvr_pick<HKHIP_Q5_1>(int, int, int, bool);
 extern template mv_kernel_t mvs_pick<HKHIP_Q5_1>(int, int);
 #endif
 

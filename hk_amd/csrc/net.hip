@@ -976,6 +976,13 @@ int product(hkhip_net *net, uint32_t n, const hkhip_mat *mats, uint32_t nparts, 
     hkhip_engine *eng = net->eng;
     const uint32_t cols = mats[0].cols;
     if (!gemm_path(n, mats[0].t)) {
+        if (norm && n > 4 && act_kind(mats[0].t) != HKHIP_ACT_F32) {
+            // 5-8 tokens: the norm folded into the quantizer, then the decode kernels on the prepared
+            // input (their 8-token form with the norm in the staging does not fit the registers).
+            NET_TRY(launch_qact_row(xin, n, cols, act_kind(mats[0].t), net->xq, norm, net->cfg.rms_eps, false, eng->cur),
+                    "rmsnorm + qact");
+            return hkhip_matvec_parts(eng, mats, nparts, nullptr, net->xq, n, ys, biases, mode);
+        }
         if (norm) {
             const int rc = hkhip_matvec_parts_rmsnorm(eng, mats, nparts, xin, norm, net->cfg.rms_eps, n, ys, biases, mode);
             if (rc != HKHIP_E_UNSUPPORTED_SHAPE) return rc;

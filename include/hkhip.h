@@ -200,9 +200,11 @@ int hkhip_mm_noalloc(hkhip_engine *eng, const hkhip_mat *m, const float *x_dev, 
  * between an embedding lookup (a row of tok_embd, decoded) and logits = Woutput (rmsnorm(x) *
  * out_norm) of the last token. One sequence per network (a K/V cache of max_ctx positions).
  * Passes of up to 8 tokens run the decode kernels (RMS norm fused into the products' input
- * quantization, residual adds as accumulate-mode products, gate/up as one silu(gate)*up launch)
- * and are captured in a HIP graph per token count after their first run; longer passes (prompt
- * prefill) run the MFMA GEMMs. Matrices are hk file-layout bytes in host memory, copied at load;
+ * quantization, residual adds as accumulate-mode products, gate/up as one silu(gate)*up launch;
+ * from 5 tokens the Q4_K / Q6_K products go through the fused quantizer and the small-batch MFMA
+ * kernel; one-token passes do the q/k norms, RoPE and cache writes inside the attention kernel)
+ * and are captured in a HIP graph per (token count, attention chunk count) after their first run;
+ * longer passes (prompt prefill) run the MFMA GEMMs. Matrices are hk file-layout bytes in host memory, copied at load;
  * Wgate and Wup must share their type; Wq, Wk and Wv that share theirs run as one product over
  * their stacked rows (else as three, e.g. a Q6_K Wv beside Q4_K Wq / Wk as in Q4_K_M files).
  * Vectors (norms, biases) are f32 (HKHIP_F32). */
