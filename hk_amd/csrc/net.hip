@@ -92,8 +92,8 @@ __device__ __forceinline__ void wave_sync() {
 }
 // One head row in a wave's LDS row h (hd values, lanes strided by 64): headNorm when nw is given
 // (rmsNorm over the head, ops.zig:31-38), then ropeAngles / ropeApply at position pos (ops.zig:
-// 154-185). The decode attention kernel runs the same steps on the rows it needs, so both give the
-// same values.
+// 154-185). The fused decode attention kernel runs the same steps on the rows it needs (its sums
+// over the head in another order, sin and cos from one sincosf), so the two agree to rounding.
 __device__ __forceinline__ void head_norm_rope(float *h, const float *src, const float *nw, uint32_t pos,
                                                const RopeArgs &a, uint32_t lane) {
     const uint32_t hd = a.hd;
@@ -324,7 +324,9 @@ __global__ __launch_bounds__(256) void attn_slice_kernel(AttnArgs a) {
 // One-token passes run fused: the raw q row is normalized and rotated by each wave (the same steps
 // as rope_kv_kernel), and the wave whose step holds the token's position builds the new key row
 // (norm, rotation, f16) and value row, uses them in place of the cache rows it loaded, and -- in the
-// first query head of each key/value group -- writes them to the caches.
+// first query head of each key/value group -- writes them to the caches. The kernel follows the
+// declarations below.
+
 // Sum / max over a wave: DPP moves within each row of 16 lanes, then the four rows' results.
 __device__ __forceinline__ float wave_sum_f(float v) {
     v += dpp_f<DPP_XOR1>(v);
