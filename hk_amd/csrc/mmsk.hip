@@ -31,7 +31,8 @@
 // The direct loads are issued as inline assembly (the compiler would otherwise wait for all of
 // them before any LDS read it cannot prove independent) and waited for with an explicit count;
 // the activation loads are ordinary, and the compiler's waits for them, which do not count the
-// direct loads, keep about one super-block less in flight: PF = 4 leaves two ahead.
+// direct loads, keep about one super-block less in flight. The launches use PF = 2: fewer bytes
+// in flight per wave, but twice the waves per SIMD of a deeper ring (see launch_mmsk_parts).
 
 #include "common.hpp"
 
@@ -467,8 +468,14 @@ hipError_t launch_mmsk_parts(int t, const MvPartDesc *parts, int nparts, uint32_
     const uint32_t nsb = cols / 256;
     uint32_t ks = 1;
     while (ks < sk_max_ks<RT>() && tiles * ks * 2 <= 2048 && nsb / (2 * ks) >= 4) ks *= 2;
-    const sk_kernel_t k = t == HKHIP_Q6_K ? (A.tiles == 1 ? sk_pick<HKHIP_Q6_K, 1, 4, RT>(ks) : sk_pick<HKHIP_Q6_K, 2, 3, RT>(ks))
-                                          : (A.tiles == 1 ? sk_pick<HKHIP_Q4_K, 1, 4, RT>(ks) : sk_pick<HKHIP_Q4_K, 2, 3, RT>(ks));
+    // A ring of two slots: one super-block in flight while the other is computed. Deeper rings keep
+    // more bytes in flight per wave but need more registers for the activations, which halves
+    // the waves per SIMD (Q4_K, 16 tokens: 116 VGPRs and four waves at two slots, 192 and two at
+    // four); measured at 8 tokens on Llama-3-8B shapes, two slots against four: q/k/v 8.5 vs 10.2 us,
+    // o 6.6 vs 7.0, gate/up 22.8 vs 23.6, down 14.4 vs 16.0, the Q6_K lm_head 126 vs 145; at 32
+    // tokens gate/up 31.2 vs 36.6 (three slots), lm_head 158 vs 182.
+    const sk_kernel_t k = t == HKHIP_Q6_K ? (A.tiles == 1 ? sk_pick<HKHIP_Q6_K, 1, 2, RT>(ks) : sk_pick<HKHIP_Q6_K, 2, 2, RT>(ks))
+                                          : (A.tiles == 1 ? sk_pick<HKHIP_Q4_K, 1, 2, RT>(ks) : sk_pick<HKHIP_Q4_K, 2, 2, RT>(ks));
     hipLaunchKernelGGL(k, dim3(tiles), dim3(ks * 64), 0, s, a);
     return hipGetLastError();
 }
