@@ -209,3 +209,29 @@ def test_net_rope_scaling(eng, kind):
             net.forward(toks, pos)
             check(net.logits(), cpu.forward(toks, pos), f"{kind} rope: pass of {n} at {pos}")
             pos += n
+
+
+def test_net_attention_chunk_boundaries(eng):
+    """Decode passes stepping across the context sizes where the attention chunk count changes (one
+    chunk of 256 positions per (head, token) up to 256, then 2, 4 and the cap): each chunk count is
+    its own captured graph, the one-chunk passes write the attention output directly and the
+    one-token passes do the key/value writes inside the attention kernel. Every pass is checked
+    against the CPU forward, so each reads the cache rows all earlier passes wrote."""
+    from hk_amd.net import Net
+
+    cfg = Config(dim=256, n_layers=2, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=512, vocab=256, max_ctx=1100,
+                 rope_neox=True, rope_base=1e4)
+    model = synth.model_np(cfg, F.Q4_K, seed=4800, out_fmt=F.Q8_0, embd_fmt=F.Q8_0, qk_norm=True, bias=False)
+    rng = np.random.default_rng(4801)
+    cpu = Oracle(cfg, model)
+    with Net(eng, cfg) as net:
+        net.load(model)
+        pos = 0
+        # 252 by prefill, then passes of 1 and 3 tokens over 256 (chunk counts 1 -> 2), a prefill to
+        # 509, passes over 512 (2 -> 4), a prefill to 1020 and passes over 1024 (4 -> the cap of 5)
+        plan = [252, 1, 1, 1, 1, 1, 3, 1, 248, 1, 1, 1, 3, 1, 505, 1, 1, 1, 3, 1, 8]
+        for n in plan:
+            toks = rng.integers(0, cfg.vocab, n)
+            net.forward(toks, pos)
+            check(net.logits(), cpu.forward(toks, pos), f"chunk boundaries: pass of {n} at {pos}")
+            pos += n
