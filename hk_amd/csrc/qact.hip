@@ -114,8 +114,8 @@ __global__ void qact_q8k_kernel(const float *__restrict__ x, uint64_t nblocks, Q
     q8k_out(o, b, lane, quant_q8k_wave(reinterpret_cast<const float4 *>(x + b * QK_K)[lane], lane));
 }
 
-// The quantizers with the producer's last step folded in, one workgroup of 256 threads per token
-// row (k values):
+// The quantizers with the producer's last step folded in, workgroups of 256 threads over pieces of
+// the token rows (k values each):
 //   norm:  value i = (x[i] * inv) * norm[i], inv = 1 / sqrt(mean(x^2) + eps) (ops.zig:10-29; the
 //          sum of squares in the order of the standalone RMS norm kernel: 256 strided partial
 //          sums, then the workgroup reduction);
@@ -146,13 +146,19 @@ __device__ __forceinline__ float row_inv(const RowIn &in, const float *xr) {
     return __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, float(in.k)) + in.eps));
 }
 
+// Grid (token row, piece of the row): a workgroup quantizes QACT_ROW_PIECE values of its row (the
+// norm's factor from the whole row, summed the same way in every workgroup), so a long row spreads
+// over several CUs instead of one workgroup looping over it.
+constexpr uint32_t QACT_ROW_PIECE = 1024;
+
 __global__ __launch_bounds__(256) void qact_a8_row_kernel(RowIn in, A8Out o) {
     const uint32_t t = blockIdx.x;
     const float *xr = in.x + uint64_t(t) * in.k * (in.pairs ? 2 : 1);
     const float inv = row_inv(in, xr);
-    for (uint32_t i0 = 0; i0 < in.k; i0 += 256) { // k is a multiple of 32: whole half-waves
+    const uint32_t i1 = min(in.k, QACT_ROW_PIECE * (blockIdx.y + 1));
+    for (uint32_t i0 = QACT_ROW_PIECE * blockIdx.y; i0 < i1; i0 += 256) { // k is a multiple of 32: whole half-waves
         const uint32_t i = i0 + threadIdx.x;
-        const bool live = i < in.k;
+        const bool live = i < i1;
         const A8Q r = quant_a8_halfwave(live ? row_value(in, xr, inv, i) : 0.0f);
         if (live) a8_out(o, uint64_t(t) * in.k + i, r);
     }
@@ -162,8 +168,8 @@ __global__ __launch_bounds__(256) void qact_q8k_row_kernel(RowIn in, Q8KOut o) {
     const uint32_t t = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const float *xr = in.x + uint64_t(t) * in.k * (in.pairs ? 2 : 1);
     const float inv = row_inv(in, xr);
-    const uint32_t nsb = in.k / QK_K;
-    for (uint32_t sb = w; sb < nsb; sb += 4) {
+    const uint32_t nsb = in.k / QK_K, sb = blockIdx.y * (QACT_ROW_PIECE / QK_K) + w; // one block per wave
+    if (sb < nsb) {
         const uint32_t i = sb * QK_K + 4 * lane;
         const float4 v = make_float4(row_value(in, xr, inv, i), row_value(in, xr, inv, i + 1),
                                      row_value(in, xr, inv, i + 2), row_value(in, xr, inv, i + 3));
@@ -205,10 +211,11 @@ hipError_t launch_qact_row(const float *x, uint32_t n, uint32_t k, int kind, uin
     if (k % 32 || (kind != HKHIP_ACT_A8 && k % QK_K)) return hipErrorInvalidValue;
     const ActLayout L = act_layout(n, k);
     const RowIn in{x, norm, eps, pairs ? 1 : 0, k};
+    const dim3 grid(n, (k + QACT_ROW_PIECE - 1) / QACT_ROW_PIECE);
     if (kind == HKHIP_ACT_A8)
-        qact_a8_row_kernel<<<n, 256, 0, s>>>(in, a8_planes(xq, L, n, k));
+        qact_a8_row_kernel<<<grid, 256, 0, s>>>(in, a8_planes(xq, L, n, k));
     else
-        qact_q8k_row_kernel<<<n, 256, 0, s>>>(in, q8k_planes(xq, L, n, k));
+        qact_q8k_row_kernel<<<grid, 256, 0, s>>>(in, q8k_planes(xq, L, n, k));
     return hipGetLastError();
 }
 
