@@ -201,10 +201,11 @@ __device__ __forceinline__ uint32_t mul_bytes(uint32_t nib, uint32_t f2) {
     return __builtin_bit_cast(uint32_t, __builtin_bit_cast(us2, nib) * __builtin_bit_cast(us2, f2));
 }
 
-template <int TOK> struct Q2Smem {
+template <int TOK, int NW> struct Q2Smem {
     int8_t a[2][TOK * 256];
     uint32_t mb[2][TOK][12]; // per token: 8 bf16 hi (words 0-3), mid (4-7), lo (8-11)
     float da[2][TOK];
+    float st[NW][1024]; // per wave: a 32x32 output tile transposed for its stores
 };
 
 // Large-tile variant: weights go global -> registers (each lane its own row half), loaded
@@ -218,7 +219,7 @@ __global__ __launch_bounds__(Q2_NW * 64, 2) void mm2_q4k_reg_kernel(Mm2Args a) {
     constexpr bool k5 = (T == HKHIP_Q5_K);
     constexpr uint32_t BB = k5 ? 176 : 144, QO = k5 ? 48 : 16; // block bytes, qs offset
     extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
-    Q2Smem<Q2_TOK> &S = *reinterpret_cast<Q2Smem<Q2_TOK> *>(smem_raw);
+    Q2Smem<Q2_TOK, Q2_NW> &S = *reinterpret_cast<Q2Smem<Q2_TOK, Q2_NW> *>(smem_raw);
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t h = lane >> 5, j = lane & 31;
@@ -312,17 +313,31 @@ __global__ __launch_bounds__(Q2_NW * 64, 2) void mm2_q4k_reg_kernel(Mm2Args a) {
 #pragma unroll
         for (int v = 0; v < 16; v++) acc[t][v] = 0.0f;
 
+    // Output: y[token][row], bias, accumulate. Each token tile is stored as soon as the last
+    // super-block has finished it, so its stores overlap the next tiles' MFMAs.
+    const float bias_r = (a.bias && myrow < a.rows) ? a.bias[myrow] : 0.0f;
+    const uint32_t rw0 = r0 + 32 * wave;
+    auto store_tile = [&](int t) {
+        const uint32_t tk0 = t0 + 32 * t;
+        if (a.wide && rw0 + 32 <= a.rows && tk0 + 32 <= a.n)
+            gemm_store_tile_wide(S.st[wave], acc[t], bias_r, a.y, a.rows, rw0, tk0, a.mode);
+        else
+            gemm_store_tile(acc[t], bias_r, a.y, a.rows, a.n, myrow, tk0, a.mode);
+    };
+
     stage_load(0, 0);
     wload(0);
     stage_store(0);
     __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): the direct-to-LDS loads have landed
     __syncthreads();
 
-    for (uint32_t sb = 0; sb < nsb; sb++) {
+    // One super-block; the last one (LAST) loads nothing ahead and stores each finished tile.
+    auto step = [&](uint32_t sb, auto last_c) {
+        constexpr bool LAST = decltype(last_c)::value;
         const uint32_t buf = sb & 1;
         const uint4 ch = wh, c0 = wq[0], c1 = wq[1], c2 = wq[2], c3 = wq[3], cx = wx;
-        const uint32_t nx = sb + 1 < nsb ? sb + 1 : sb;
-        stage_load(nx, buf ^ 1);
+        const uint32_t nx = sb + 1;
+        if constexpr (!LAST) stage_load(nx, buf ^ 1);
 
         // Unpack: scales (vecdot.zig:461-474 word form), then both planes of the 8 sub-blocks.
         const uint32_t k1 = 0x3f3f3f3fu, k2 = 0x0f0f0f0fu, k3 = 0x03030303u;
@@ -389,7 +404,8 @@ __global__ __launch_bounds__(Q2_NW * 64, 2) void mm2_q4k_reg_kernel(Mm2Args a) {
 #pragma unroll
             for (int s = 0; s < 8; s++) sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[s], blo[s], sacc, 0, 0, 0);
             if (t + 1 < Q2_TT) load_a(t + 1);
-            if (t == (Q2_TT > 1 ? 1 : 0)) wload(nx); // next super-block's weights, once this one's raw words are dead
+            if constexpr (!LAST)
+                if (t == (Q2_TT > 1 ? 1 : 0)) wload(nx); // next super-block's weights, once this one's raw words are dead
             // Token scales of this lane's 16 outputs: tokens 32t + 8g + 4h + (0..3).
             const float4 *dap = reinterpret_cast<const float4 *>(&S.da[buf][32 * t + 4 * h]);
 #pragma unroll
@@ -404,27 +420,17 @@ __global__ __launch_bounds__(Q2_NW * 64, 2) void mm2_q4k_reg_kernel(Mm2Args a) {
             }
             // Min term: tokens' da*bsum32 (A) x rows' -dmin*mn (B), bf16 hi/lo split.
             min_term(acc[t], S.mb[buf][32 * t + j], mB, h);
+            if constexpr (LAST) store_tile(t);
         }
 
-        stage_store(buf ^ 1);
-        __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): next super-block's activations are in LDS
-        __syncthreads();
-    }
-
-    // ---- store: y[token][row], bias, accumulate (the last step's barrier freed the LDS) ----
-    {
-        float *st = reinterpret_cast<float *>(smem_raw) + 1024 * wave;
-        const float b = (a.bias && myrow < a.rows) ? a.bias[myrow] : 0.0f;
-        const uint32_t rw0 = r0 + 32 * wave;
-#pragma unroll
-        for (int t = 0; t < Q2_TT; t++) {
-            const uint32_t tk0 = t0 + 32 * t;
-            if (a.wide && rw0 + 32 <= a.rows && tk0 + 32 <= a.n)
-                gemm_store_tile_wide(st, acc[t], b, a.y, a.rows, rw0, tk0, a.mode);
-            else
-                gemm_store_tile(acc[t], b, a.y, a.rows, a.n, myrow, tk0, a.mode);
+        if constexpr (!LAST) {
+            stage_store(buf ^ 1);
+            __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): next super-block's activations are in LDS
+            __syncthreads();
         }
-    }
+    };
+    for (uint32_t sb = 0; sb + 1 < nsb; sb++) step(sb, std::false_type{});
+    step(nsb - 1, std::true_type{});
 }
 
 
@@ -708,7 +714,7 @@ typedef void (*mm2_kernel_t)(Mm2Args);
 template <int NW, int TT, int T = HKHIP_Q4_K>
 static hipError_t launch_mm2_reg(const Mm2Args &a0, hipStream_t s) {
     const mm2_kernel_t k = mm2_q4k_reg_kernel<T, NW, TT>;
-    constexpr size_t lds = sizeof(Q2Smem<32 * TT>);
+    constexpr size_t lds = sizeof(Q2Smem<32 * TT, NW>);
     static bool attr = false;
     if (!attr) {
         (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k), hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
