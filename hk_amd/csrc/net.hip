@@ -604,7 +604,7 @@ struct AttnPArgs {
 };
 
 template <int HD>
-__global__ __launch_bounds__(256) void attn_prefill_kernel(AttnPArgs a) {
+__global__ __launch_bounds__(256, 2) void attn_prefill_kernel(AttnPArgs a) {
     constexpr int NCH = HD / 16, NDT = HD / 32;
     const uint32_t lane = threadIdx.x & 63, h = lane >> 5, j = lane & 31;
     const uint32_t wave = threadIdx.x >> 6;
@@ -616,22 +616,28 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnPArgs a) {
     const uint32_t tpos = pos0 + tc;
     const uint32_t pend = pos0 + min(tile * 32 + 32, a.n); // positions [0, pend) are needed
 
-    v8h qh[NCH], ql[NCH];
+    // The tile's q operands (the same 32 tokens for the four waves) live in LDS, split over the
+    // waves' lanes to build, so that they take no registers: with them in registers the kernel
+    // held one workgroup per CU.
+    __shared__ v8h qsh[NCH][64], qsl[NCH][64];
     {
         const float *qrow = a.q + uint64_t(tc) * a.sq + head * HD;
-#pragma unroll
-        for (int c = 0; c < NCH; c++) {
+        for (int c = int(wave); c < NCH; c += 4) {
             const float4 x0 = *reinterpret_cast<const float4 *>(qrow + 16 * c + 8 * h);
             const float4 x1 = *reinterpret_cast<const float4 *>(qrow + 16 * c + 8 * h + 4);
             const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            v8h hv, lv;
 #pragma unroll
             for (int e = 0; e < 8; e++) {
                 const _Float16 hi = (_Float16)xs[e];
-                qh[c][e] = hi;
-                ql[c][e] = (_Float16)(xs[e] - (float)hi);
+                hv[e] = hi;
+                lv[e] = (_Float16)(xs[e] - (float)hi);
             }
+            qsh[c][lane] = hv;
+            qsl[c][lane] = lv;
         }
     }
+    __syncthreads();
     v16f acc[NDT];
 #pragma unroll
     for (int d = 0; d < NDT; d++) acc[d] = v16f{};
@@ -655,8 +661,8 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnPArgs a) {
         v16f s = v16f{};
 #pragma unroll
         for (int c = 0; c < NCH; c++) {
-            s = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[c], qh[c], s, 0, 0, 0);
-            s = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[c], ql[c], s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[c], qsh[c][lane], s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[c], qsl[c][lane], s, 0, 0, 0);
         }
         // Score v of this lane: position p0 + 16(g >> 1) + 8h + 4(g & 1) + e, g = v / 4, e = v % 4.
         float sv[16], mx = -INFINITY;
