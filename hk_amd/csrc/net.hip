@@ -93,7 +93,7 @@ __device__ __forceinline__ void wave_sync() {
 // One head row in a wave's LDS row h (hd values, lanes strided by 64): headNorm when nw is given
 // (rmsNorm over the head, ops.zig:31-38), then ropeAngles / ropeApply at position pos (ops.zig:
 // 154-185). The fused decode attention kernel runs the same steps on the rows it needs (its sums
-// over the head in another order, sin and cos from one sincosf), so the two agree to rounding.
+// over the head in another order), so the two agree to rounding.
 __device__ __forceinline__ void head_norm_rope(float *h, const float *src, const float *nw, uint32_t pos,
                                                const RopeArgs &a, uint32_t lane) {
     const uint32_t hd = a.hd;
@@ -110,8 +110,9 @@ __device__ __forceinline__ void head_norm_rope(float *h, const float *src, const
     }
     const float p = float(pos);
     for (uint32_t i = lane; i < a.rope_half; i += 64) {
-        const float ang = p * a.inv_freq[i];
-        const float c = cosf(ang) * a.mscale, s = sinf(ang) * a.mscale;
+        float sn, cs;
+        sincosf(p * a.inv_freq[i], &sn, &cs);
+        const float c = cs * a.mscale, s = sn * a.mscale;
         const uint32_t i0 = a.neox ? i : 2 * i, i1 = a.neox ? i + a.rope_half : 2 * i + 1;
         const float x0 = h[i0], x1 = h[i1];
         h[i0] = x0 * c - x1 * s;
