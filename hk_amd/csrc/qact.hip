@@ -164,15 +164,51 @@ __global__ __launch_bounds__(256) void qact_a8_row_kernel(RowIn in, A8Out o) {
     }
 }
 
+// Four consecutive values i..i+3 of a row (i a multiple of 4), with 16-byte loads.
+__device__ __forceinline__ float4 row_values4(const RowIn &in, const float *xr, float inv, uint32_t i) {
+    if (in.pairs) {
+        const float4 a = *reinterpret_cast<const float4 *>(xr + 2 * i), b = *reinterpret_cast<const float4 *>(xr + 2 * i + 4);
+        return make_float4(silu_mul(a.x, a.y), silu_mul(a.z, a.w), silu_mul(b.x, b.y), silu_mul(b.z, b.w));
+    }
+    const float4 x = *reinterpret_cast<const float4 *>(xr + i);
+    if (!in.norm) return x;
+    const float4 w = *reinterpret_cast<const float4 *>(in.norm + i);
+    return make_float4((x.x * inv) * w.x, (x.y * inv) * w.y, (x.z * inv) * w.z, (x.w * inv) * w.w);
+}
+
 __global__ __launch_bounds__(256) void qact_q8k_row_kernel(RowIn in, Q8KOut o) {
     const uint32_t t = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const float *xr = in.x + uint64_t(t) * in.k * (in.pairs ? 2 : 1);
     const float inv = row_inv(in, xr);
     const uint32_t nsb = in.k / QK_K, sb = blockIdx.y * (QACT_ROW_PIECE / QK_K) + w; // one block per wave
-    if (sb < nsb) {
+    if (sb < nsb)
+        q8k_out(o, uint64_t(t) * nsb + sb, lane, quant_q8k_wave(row_values4(in, xr, inv, sb * QK_K + 4 * lane), lane));
+}
+
+// The norm case for rows of up to QACT_NORM_LDS values: one workgroup per row reads the row once
+// into LDS (16-byte loads), sums the squares there in row_inv's order, and its four waves quantize
+// the row's blocks from LDS.
+constexpr uint32_t QACT_NORM_LDS = 8192;
+__global__ __launch_bounds__(256) void qact_q8k_norm_row_kernel(RowIn in, Q8KOut o) {
+    __shared__ float4 xs4[QACT_NORM_LDS / 4];
+    __shared__ float red[4];
+    const float *xs = reinterpret_cast<const float *>(xs4);
+    const uint32_t t = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const float4 *xr4 = reinterpret_cast<const float4 *>(in.x + uint64_t(t) * in.k);
+    for (uint32_t j = threadIdx.x; j < in.k / 4; j += 256) xs4[j] = xr4[j];
+    __syncthreads();
+    float ss = 0.0f;
+    for (uint32_t i = threadIdx.x; i < in.k; i += 256) ss = fmaf(xs[i], xs[i], ss);
+    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+    if (lane == 0) red[w] = ss;
+    __syncthreads();
+    ss = red[0] + red[1] + red[2] + red[3];
+    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, float(in.k)) + in.eps));
+    const uint32_t nsb = in.k / QK_K;
+    for (uint32_t sb = w; sb < nsb; sb += 4) {
         const uint32_t i = sb * QK_K + 4 * lane;
-        const float4 v = make_float4(row_value(in, xr, inv, i), row_value(in, xr, inv, i + 1),
-                                     row_value(in, xr, inv, i + 2), row_value(in, xr, inv, i + 3));
+        const float4 x = xs4[i / 4], g = *reinterpret_cast<const float4 *>(in.norm + i);
+        const float4 v = make_float4((x.x * inv) * g.x, (x.y * inv) * g.y, (x.z * inv) * g.z, (x.w * inv) * g.w);
         q8k_out(o, uint64_t(t) * nsb + sb, lane, quant_q8k_wave(v, lane));
     }
 }
@@ -214,6 +250,8 @@ hipError_t launch_qact_row(const float *x, uint32_t n, uint32_t k, int kind, uin
     const dim3 grid(n, (k + QACT_ROW_PIECE - 1) / QACT_ROW_PIECE);
     if (kind == HKHIP_ACT_A8)
         qact_a8_row_kernel<<<grid, 256, 0, s>>>(in, a8_planes(xq, L, n, k));
+    else if (norm && k <= QACT_NORM_LDS)
+        qact_q8k_norm_row_kernel<<<n, 256, 0, s>>>(in, q8k_planes(xq, L, n, k));
     else
         qact_q8k_row_kernel<<<grid, 256, 0, s>>>(in, q8k_planes(xq, L, n, k));
     return hipGetLastError();
