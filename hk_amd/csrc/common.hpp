@@ -288,10 +288,9 @@ struct MvPartDesc;
 hipError_t launch_fb_mv(int t, const MvPartDesc *parts, int nparts, uint32_t K, const float *x, const uint8_t *xq,
                         uint32_t n, int mode, hipStream_t s);
 hipError_t launch_qact(const float *x, uint32_t n, uint32_t k, int kind, uint8_t *xq, hipStream_t s);
-// qact with the producer's last step folded in (one workgroup per token row): the RMS norm with
-// weights `norm` (or null), or, with `pairs`, silu(gate) * up of rows of 2k interleaved values.
+// qact with the RMS norm (weights `norm`, or null for none) folded in, by token rows.
 hipError_t launch_qact_row(const float *x, uint32_t n, uint32_t k, int kind, uint8_t *xq, const float *norm, float eps,
-                           bool pairs, hipStream_t s);
+                           hipStream_t s);
 hipError_t launch_act_pack(const uint8_t *xq, uint32_t n, uint32_t k, int kind, uint8_t *out, hipStream_t s);
 // One matrix of a fused decode launch (all parts share cols and the input).
 struct MvPartDesc {

@@ -290,8 +290,8 @@ static int check_product(const hkhip_mat *m, const void *xq, float *y, uint32_t 
     if (rc) return rc;
     if (mode != HKHIP_STORE && mode != HKHIP_ACCUMULATE && mode != HKHIP_SILU_MUL)
         return fail(HKHIP_E_BAD_ARGUMENT, "unknown mode %d", mode);
-    if (mode == HKHIP_SILU_MUL && (m->rows % 2 || n > 8))
-        return fail(HKHIP_E_BAD_ARGUMENT, "silu(gate)*up needs interleaved gate/up rows (even count) and n <= 8");
+    if (mode == HKHIP_SILU_MUL && m->rows % 2)
+        return fail(HKHIP_E_BAD_ARGUMENT, "silu(gate)*up needs interleaved gate/up rows (an even count)");
     if ((act_kind(m->t) == HKHIP_ACT_Q8K || fallback_type(m->t)) && m->cols % QK_K)
         return fail(HKHIP_E_UNSUPPORTED_SHAPE, "cols %u: the products of this type take whole 256-value groups", m->cols);
     if (n && (!xq || !y)) return fail(HKHIP_E_BAD_ARGUMENT, "null buffer");
@@ -372,7 +372,7 @@ int hkhip_gemm(hkhip_engine *eng, const hkhip_mat *m, const void *xq_dev, float 
                const float *bias_dev, int mode) {
     int rc = enter(eng);
     if (rc || (rc = check_product(m, xq_dev, y_dev, n, mode)) || (rc = check_prepared(m))) return rc;
-    if (mode == HKHIP_SILU_MUL) return fail(HKHIP_E_BAD_ARGUMENT, "silu(gate)*up is a decode mode (hkhip_matvec)");
+    if (mode == HKHIP_SILU_MUL && bias_dev) return fail(HKHIP_E_BAD_ARGUMENT, "silu(gate)*up takes no bias");
     if (n == 0) return HKHIP_OK;
     if ((n + 63) / 64 > 65535u) return fail(HKHIP_E_UNSUPPORTED_SHAPE, "too many tokens: %u", n);
     HIP_TRY(launch_mm(m->t, reinterpret_cast<const uint8_t *>(m->mem), m->rows, m->cols,
@@ -407,6 +407,7 @@ int hkhip_mm(hkhip_engine *eng, const hkhip_mat *m, const void *xq_dev, float *y
     if (n >= gemm_min_tokens(m->t, m->rows)) return hkhip_gemm(eng, m, xq_dev, y_dev, n, bias_dev, mode);
     int rc = enter(eng);
     if (rc || (rc = check_product(m, xq_dev, y_dev, n, mode)) || (rc = check_prepared(m))) return rc;
+    if (mode == HKHIP_SILU_MUL && bias_dev) return fail(HKHIP_E_BAD_ARGUMENT, "silu(gate)*up takes no bias");
     HIP_TRY(launch_mmvq(m->t, reinterpret_cast<const uint8_t *>(m->mem), m->rows, m->cols,
                         reinterpret_cast<const uint8_t *>(xq_dev), n, y_dev, bias_dev, mode, eng->cur), "mmvq launch");
     return HKHIP_OK;

@@ -265,6 +265,16 @@ __global__ __launch_bounds__(256) void mm_kernel(MmArgs a) {
 
     // ---- store token-major, with bias ----
     const uint32_t grow = r0 + myrow;
+    if (a.mode == HKHIP_SILU_MUL) { // lanes j, j ^ 1 hold rows 2i (gate) and 2i + 1 (up)
+        const float b = (a.bias && grow < a.rows) ? a.bias[grow] : 0.0f;
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const float g = accf[v] + b, u = __shfl_xor(g, 1);
+            const uint32_t tok = t0 + 32 * wt + 8 * (v / 4) + 4 * khalf + (v % 4);
+            if (grow < a.rows && (grow & 1) == 0 && tok < a.n) a.y[uint64_t(tok) * (a.rows / 2) + grow / 2] = silu_mul(g, u);
+        }
+        return;
+    }
     if (grow < a.rows) {
         const float b = a.bias ? a.bias[grow] : 0.0f;
 #pragma unroll

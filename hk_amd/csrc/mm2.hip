@@ -755,7 +755,7 @@ hipError_t launch_mm2(int t, const uint8_t *w, uint32_t rows, uint32_t cols, con
     a.y = y;
     a.bias = bias;
     a.mode = mode;
-    a.wide = (reinterpret_cast<uintptr_t>(y) % 16 == 0 && rows % 4 == 0) ? 1 : 0;
+    a.wide = (reinterpret_cast<uintptr_t>(y) % 16 == 0 && rows % (mode == HKHIP_SILU_MUL ? 8 : 4) == 0) ? 1 : 0;
     // The largest tile that still gives most of the 256 CUs a workgroup.
     auto blocks = [&](uint32_t nw, uint32_t tt) {
         return ((rows + 32 * nw - 1) / (32 * nw)) * ((n + 32 * tt - 1) / (32 * tt));

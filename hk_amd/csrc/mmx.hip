@@ -630,7 +630,7 @@ hipError_t launch_mmx(int t, const uint8_t *w, uint32_t rows, uint32_t cols, con
     a.y = y;
     a.bias = bias;
     a.mode = mode;
-    a.wide = (reinterpret_cast<uintptr_t>(y) % 16 == 0 && rows % 4 == 0) ? 1 : 0;
+    a.wide = (reinterpret_cast<uintptr_t>(y) % 16 == 0 && rows % (mode == HKHIP_SILU_MUL ? 8 : 4) == 0) ? 1 : 0;
     // Tile choice (measured at the 8B FFN shapes, 512 tokens): the largest tile that still gives
     // most CUs a workgroup.
     auto blocks = [&](uint32_t nw, uint32_t tt) {

@@ -797,13 +797,6 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float *__restri
     }
 }
 
-// h[t][i] = silu(gu[t][2i]) * gu[t][2i+1] (gate/up rows interleaved; ops.zig:70-80 swiglu).
-__global__ __launch_bounds__(256) void swiglu_pairs_kernel(const float *__restrict__ gu, float *__restrict__ h,
-                                                           uint64_t total) {
-    const uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i < total) h[i] = silu_mul(gu[2 * i], gu[2 * i + 1]);
-}
-
 } // namespace
 
 // ---------------------------------------------------------------------------------------------
@@ -828,7 +821,7 @@ struct hkhip_net {
     // Device buffers ([MAX tokens][...] sized for the largest pass seen).
     std::vector<void *> owned;
     uint32_t cap = 0; // tokens the pass buffers hold
-    float *x = nullptr, *xb = nullptr, *qkv = nullptr, *att = nullptr, *gu = nullptr,
+    float *x = nullptr, *xb = nullptr, *qkv = nullptr, *att = nullptr,
           *h = nullptr, *part = nullptr, *logits = nullptr, *inv_freq = nullptr;
     uint8_t *xq = nullptr;
     __half *kc = nullptr, *vc = nullptr, *vt = nullptr;
@@ -921,7 +914,7 @@ int ensure_cap(hkhip_net *n, uint32_t want) {
     for (auto &g : n->graphs) (void)hipGraphExecDestroy(g.second);
     n->graphs.clear();
     n->runs.clear();
-    float **bufs[] = {&n->x, &n->xb, &n->qkv, &n->att, &n->gu, &n->h, &n->part,
+    float **bufs[] = {&n->x, &n->xb, &n->qkv, &n->att, &n->h, &n->part,
                       reinterpret_cast<float **>(&n->io)};
     if (n->stage) {
         (void)hipHostFree(n->stage);
@@ -946,7 +939,7 @@ int ensure_cap(hkhip_net *n, uint32_t want) {
     int rc;
     if ((rc = dev_alloc(n, T * c.dim * 4, (void **)&n->x)) || (rc = dev_alloc(n, T * std::max(c.dim, qdim(c)) * 4, (void **)&n->xb)) ||
         (rc = dev_alloc(n, T * qkvdim(c) * 4, (void **)&n->qkv)) || (rc = dev_alloc(n, T * qdim(c) * 4, (void **)&n->att)) ||
-        (rc = dev_alloc(n, T * 2 * c.ffn_dim * 4, (void **)&n->gu)) || (rc = dev_alloc(n, T * c.ffn_dim * 4, (void **)&n->h)) ||
+        (rc = dev_alloc(n, T * c.ffn_dim * 4, (void **)&n->h)) ||
         (rc = dev_alloc(n, (prefill_mfma(c) ? MAX_DECODE : std::max<uint64_t>(T, MAX_DECODE)) * c.n_heads * nslices(c) * (c.head_dim + 2) * 4,
                         (void **)&n->part)) ||
         (rc = dev_alloc(n, hkhip_act_bytes(want, maxk), (void **)&n->xq)) ||
@@ -988,7 +981,7 @@ int product(hkhip_net *net, uint32_t n, const hkhip_mat *mats, uint32_t nparts, 
         if (norm && n > 4 && act_kind(mats[0].t) != HKHIP_ACT_F32) {
             // 5-8 tokens: the norm folded into the quantizer, then the decode kernels on the prepared
             // input (their 8-token form with the norm in the staging does not fit the registers).
-            NET_TRY(launch_qact_row(xin, n, cols, act_kind(mats[0].t), net->xq, norm, net->cfg.rms_eps, false, eng->cur),
+            NET_TRY(launch_qact_row(xin, n, cols, act_kind(mats[0].t), net->xq, norm, net->cfg.rms_eps, eng->cur),
                     "rmsnorm + qact");
             return hkhip_matvec_parts(eng, mats, nparts, nullptr, net->xq, n, ys, biases, mode);
         }
@@ -1002,7 +995,7 @@ int product(hkhip_net *net, uint32_t n, const hkhip_mat *mats, uint32_t nparts, 
         return hkhip_matvec_parts(eng, mats, nparts, xin, nullptr, n, ys, biases, mode);
     }
     if (norm && act_kind(mats[0].t) != HKHIP_ACT_F32) { // the norm folded into the quantizer
-        NET_TRY(launch_qact_row(xin, n, cols, act_kind(mats[0].t), net->xq, norm, net->cfg.rms_eps, false, eng->cur),
+        NET_TRY(launch_qact_row(xin, n, cols, act_kind(mats[0].t), net->xq, norm, net->cfg.rms_eps, eng->cur),
                 "rmsnorm + qact");
         return gemms(net, n, mats, nparts, ys, biases, mode);
     }
@@ -1126,23 +1119,9 @@ int run_pass(hkhip_net *net, uint32_t n, uint32_t gb) {
             float *const ys[1] = {net->x};
             if ((rc = product(net, n, &L.wo, 1, net->att, nullptr, ys, nullptr, HKHIP_ACCUMULATE))) return rc;
         }
-        if (!gemm_path(n, L.wgu.t)) {
+        { // gate/up with silu(gate) * up in the products' epilogue (decode kernels and GEMMs alike)
             float *const ys[1] = {net->h};
             if ((rc = product(net, n, &L.wgu, 1, net->x, L.ffn_norm, ys, nullptr, HKHIP_SILU_MUL))) return rc;
-        } else {
-            float *const ys[1] = {net->gu};
-            if ((rc = product(net, n, &L.wgu, 1, net->x, L.ffn_norm, ys, nullptr, HKHIP_STORE))) return rc;
-            if (gemm_path(n, L.wd.t) && act_kind(L.wd.t) != HKHIP_ACT_F32) { // silu(gate) * up folded into the down input's quantizer
-                NET_TRY(launch_qact_row(net->gu, n, c.ffn_dim, act_kind(L.wd.t), net->xq, nullptr, 0.0f, true, s),
-                        "swiglu + qact");
-                float *const yd[1] = {net->x};
-                if ((rc = gemms(net, n, &L.wd, 1, yd, nullptr, HKHIP_ACCUMULATE))) return rc;
-                continue;
-            }
-            const uint64_t total = uint64_t(n) * c.ffn_dim;
-            hipLaunchKernelGGL(swiglu_pairs_kernel, dim3(uint32_t((total + 255) / 256)), dim3(256), 0, s, net->gu, net->h,
-                               total);
-            NET_TRY(hipGetLastError(), "swiglu");
         }
         {
             float *const ys[1] = {net->x};

@@ -114,23 +114,18 @@ __global__ void qact_q8k_kernel(const float *__restrict__ x, uint64_t nblocks, Q
     q8k_out(o, b, lane, quant_q8k_wave(reinterpret_cast<const float4 *>(x + b * QK_K)[lane], lane));
 }
 
-// The quantizers with the producer's last step folded in, workgroups of 256 threads over pieces of
-// the token rows (k values each):
-//   norm:  value i = (x[i] * inv) * norm[i], inv = 1 / sqrt(mean(x^2) + eps) (ops.zig:10-29; the
-//          sum of squares in the order of the standalone RMS norm kernel: 256 strided partial
-//          sums, then the workgroup reduction);
-//   pairs: value i = silu(x[2i]) * x[2i + 1] (x holds 2k values per row: gate/up interleaved,
-//          ops.zig:70-80 swiglu).
-// Then each block is quantized as qact_a8_kernel / qact_q8k_kernel quantize it.
+// The quantizers with the RMS norm folded in, workgroups of 256 threads over the token rows (k
+// values each): value i = (x[i] * inv) * norm[i], inv = 1 / sqrt(mean(x^2) + eps) (ops.zig:10-29;
+// the sum of squares in the order of the standalone RMS norm kernel: 256 strided partial sums,
+// then the workgroup reduction). Then each block is quantized as qact_a8_kernel / qact_q8k_kernel
+// quantize it.
 struct RowIn {
     const float *x;
     const float *norm; // or null
     float eps;
-    int pairs;
     uint32_t k;
 };
 __device__ __forceinline__ float row_value(const RowIn &in, const float *xr, float inv, uint32_t i) {
-    if (in.pairs) return silu_mul(xr[2 * i], xr[2 * i + 1]);
     if (in.norm) return (xr[i] * inv) * in.norm[i];
     return xr[i];
 }
@@ -153,7 +148,7 @@ constexpr uint32_t QACT_ROW_PIECE = 1024;
 
 __global__ __launch_bounds__(256) void qact_a8_row_kernel(RowIn in, A8Out o) {
     const uint32_t t = blockIdx.x;
-    const float *xr = in.x + uint64_t(t) * in.k * (in.pairs ? 2 : 1);
+    const float *xr = in.x + uint64_t(t) * in.k;
     const float inv = row_inv(in, xr);
     const uint32_t i1 = min(in.k, QACT_ROW_PIECE * (blockIdx.y + 1));
     for (uint32_t i0 = QACT_ROW_PIECE * blockIdx.y; i0 < i1; i0 += 256) { // k is a multiple of 32: whole half-waves
@@ -166,10 +161,6 @@ __global__ __launch_bounds__(256) void qact_a8_row_kernel(RowIn in, A8Out o) {
 
 // Four consecutive values i..i+3 of a row (i a multiple of 4), with 16-byte loads.
 __device__ __forceinline__ float4 row_values4(const RowIn &in, const float *xr, float inv, uint32_t i) {
-    if (in.pairs) {
-        const float4 a = *reinterpret_cast<const float4 *>(xr + 2 * i), b = *reinterpret_cast<const float4 *>(xr + 2 * i + 4);
-        return make_float4(silu_mul(a.x, a.y), silu_mul(a.z, a.w), silu_mul(b.x, b.y), silu_mul(b.z, b.w));
-    }
     const float4 x = *reinterpret_cast<const float4 *>(xr + i);
     if (!in.norm) return x;
     const float4 w = *reinterpret_cast<const float4 *>(in.norm + i);
@@ -178,7 +169,7 @@ __device__ __forceinline__ float4 row_values4(const RowIn &in, const float *xr, 
 
 __global__ __launch_bounds__(256) void qact_q8k_row_kernel(RowIn in, Q8KOut o) {
     const uint32_t t = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const float *xr = in.x + uint64_t(t) * in.k * (in.pairs ? 2 : 1);
+    const float *xr = in.x + uint64_t(t) * in.k;
     const float inv = row_inv(in, xr);
     const uint32_t nsb = in.k / QK_K, sb = blockIdx.y * (QACT_ROW_PIECE / QK_K) + w; // one block per wave
     if (sb < nsb)
@@ -242,11 +233,11 @@ hipError_t launch_qact(const float *x, uint32_t n, uint32_t k, int kind, uint8_t
 }
 
 hipError_t launch_qact_row(const float *x, uint32_t n, uint32_t k, int kind, uint8_t *xq, const float *norm, float eps,
-                           bool pairs, hipStream_t s) {
+                           hipStream_t s) {
     if (n == 0 || k == 0) return hipSuccess;
     if (k % 32 || (kind != HKHIP_ACT_A8 && k % QK_K)) return hipErrorInvalidValue;
     const ActLayout L = act_layout(n, k);
-    const RowIn in{x, norm, eps, pairs ? 1 : 0, k};
+    const RowIn in{x, norm, eps, k};
     const dim3 grid(n, (k + QACT_ROW_PIECE - 1) / QACT_ROW_PIECE);
     if (kind == HKHIP_ACT_A8)
         qact_a8_row_kernel<<<grid, 256, 0, s>>>(in, a8_planes(xq, L, n, k));

@@ -67,8 +67,9 @@ extern "C" {
 #define HKHIP_ACCUMULATE 1 /* y += W x + bias (residual add fused into the product) */
 /* Fused gate/up of a SwiGLU FFN, the Vulkan engine's mmvq mode 2 (shaders/mmvq.comp:24,162-186):
  * W holds the gate and up rows interleaved (row 2i = gate i, row 2i + 1 = up i), y is [n][rows/2]
- * and y[t][i] = silu(g) * u with g, u the two rows' products, silu(g) = g / (1 + exp(-g)). Decode
- * products only (n <= 8: hkhip_matvec, hkhip_matvec_parts, hkhip_mm); rows even, no bias. */
+ * and y[t][i] = silu(g) * u with g, u the two rows' products, silu(g) = g / (1 + exp(-g)). Rows
+ * even, no bias. Every product takes it; in the GEMMs (no counterpart in the reference, whose
+ * prefill writes both rows and applies swiglu separately) it halves the output written. */
 #define HKHIP_SILU_MUL 2
 
 /* Error codes (src/cuda/engine.zig:31-40). */
@@ -152,7 +153,7 @@ int hkhip_act_export(hkhip_engine *eng, const void *xq_dev, uint32_t n, uint32_t
  * hkhip_mm:     picks matvec for n <= 8, then 8-token matvec passes up to the GEMM's break-even
  *               (Q6_K / Q8_0: 32 tokens, IQ4_NL: 24; Q4_K has none), then gemm (the CPU engine's
  *               switch is matmul.zig:18 min_tiled_tokens = 8).
- * mode is HKHIP_STORE, HKHIP_ACCUMULATE or (n <= 8, not hkhip_gemm) HKHIP_SILU_MUL. */
+ * mode is HKHIP_STORE, HKHIP_ACCUMULATE or HKHIP_SILU_MUL. */
 int hkhip_matvec(hkhip_engine *eng, const hkhip_mat *m, const void *xq_dev, float *y_dev, uint32_t n,
                  const float *bias_dev, int mode);
 int hkhip_gemm(hkhip_engine *eng, const hkhip_mat *m, const void *xq_dev, float *y_dev, uint32_t n,

@@ -534,8 +534,55 @@ def test_silu_mul_kernel_variants(eng, torch_cuda, t, k, n):
     eng.free(w)
 
 
+@pytest.mark.parametrize("t", FMTS)
+@pytest.mark.parametrize("n,m", [(9, 2 * 150), (40, 2 * 256), (200, 2 * 150), (64, 2 * 1024)])
+def test_silu_mul_gemm(eng, torch_cuda, t, n, m):
+    """Mode 2 through hkhip_mm past 8 tokens: the small-batch kernel, the decode passes and the
+    GEMMs' epilogues (their LDS-transposed 16-byte stores where rows are a multiple of 8, lane
+    pairs otherwise), against the oracle's product of the interleaved rows."""
+    torch = torch_cuda
+    k = 1024
+    raw = synth.weights_np(t, m, k, seed=1250 + t + m)
+    x = synth.activations_np(n, k, seed=1251 + n, outliers=0.01)
+    w = eng.upload(raw, t, m, k)
+    xd = torch.from_numpy(x).cuda()
+    xq = torch.empty(eng.act_bytes(n, k), dtype=torch.uint8, device="cuda")
+    eng.qact(xd, n, k, F.ACT_KIND[t], xq)
+    y = torch.full((n, m // 2), float("nan"), device="cuda")
+    eng.mm(w, xq, y, n, mode=SILU_MUL)
+    torch.cuda.synchronize()
+    want = silu_mul_ref(O.matmul(t, raw, m, k, x, n, tiled=True))
+    assert parity_err(y.cpu().numpy(), want) <= PARITY_TOL
+    eng.free(w)
+
+
+def test_silu_mul_gemm_large_tile(eng, torch_cuda):
+    """Mode 2 in the Q4_K register-tile GEMM (14336 x 256 at 512 tokens, the prefill gate/up
+    shape's tile): the epilogue's output equals silu(gate) * up of the same GEMM's stored rows
+    (expf aside, to 1e-6), and sampled gate/up pairs match the oracle."""
+    torch = torch_cuda
+    t, m, k, n = F.Q4_K, 14336, 256, 512
+    raw = synth.weights_np(t, m, k, seed=1260)
+    x = synth.activations_np(n, k, seed=1261)
+    w = eng.upload(raw, t, m, k)
+    xq = torch.empty(eng.act_bytes(n, k), dtype=torch.uint8, device="cuda")
+    eng.qact(torch.from_numpy(x).cuda(), n, k, F.ACT_KIND[t], xq)
+    y2 = torch.full((n, m), float("nan"), device="cuda")
+    ys = torch.full((n, m // 2), float("nan"), device="cuda")
+    eng.gemm(w, xq, y2, n)
+    eng.gemm(w, xq, ys, n, mode=SILU_MUL)
+    torch.cuda.synchronize()
+    got = ys.cpu().numpy()
+    assert parity_err(got, silu_mul_ref(y2.cpu().numpy())) <= 1e-6
+    pairs = np.random.default_rng(1262).choice(m // 2, 24, replace=False)
+    rows = np.stack([2 * pairs, 2 * pairs + 1], 1).reshape(-1)
+    want = silu_mul_ref(O.matmul(t, raw[rows], len(rows), k, x, n, tiled=True))
+    assert parity_err(got[:, pairs], want) <= PARITY_TOL
+    eng.free(w)
+
+
 def test_silu_mul_rejects(eng, torch_cuda):
-    """Mode 2 takes an even row count, no bias, at most 8 tokens, and no GEMM."""
+    """Mode 2 takes an even row count and no bias."""
     from hk_amd import HipError
 
     torch = torch_cuda
@@ -550,10 +597,13 @@ def test_silu_mul_rejects(eng, torch_cuda):
     with pytest.raises(HipError):
         eng.matvec(even, xq, y, 1, bias=b, mode=SILU_MUL)
     with pytest.raises(HipError):
-        eng.gemm(even, xq, y, 1, mode=SILU_MUL)
+        eng.gemm(even, xq, y, 16, bias=b, mode=SILU_MUL)
     with pytest.raises(HipError):
-        eng.mm(even, xq, y, 16, mode=SILU_MUL)
+        eng.mm(even, xq, y, 16, bias=b, mode=SILU_MUL)
+    with pytest.raises(HipError):
+        eng.gemm(odd, xq, y, 16, mode=SILU_MUL)
     eng.matvec(even, xq, y, 1, mode=SILU_MUL)
+    eng.gemm(even, xq, y, 16, mode=SILU_MUL)
     torch.cuda.synchronize()
     eng.free(odd)
     eng.free(even)
