@@ -16,8 +16,9 @@
 //
 // Two kernels:
 //  * mmvr_kernel (the decode path): lane l of a wave owns units l, l+64, ... of every row and
-//    holds their activations in registers; a wave streams a contiguous range of whole rows, so
-//    each activation register serves every row. Used when the activations fit the registers
+//    holds their activations in registers; a wave streams whole rows (one-token launches deal
+//    them to the waves in turn, a step's rows at a time), so each activation register serves
+//    every row. Used when the activations fit the registers
 //    (rows of up to 256-512 units, depending on format and token count).
 //  * mmvq_kernel (everything else): a row is shared by 2^k lanes that step through it, and the
 //    activations stay in LDS.
@@ -54,6 +55,10 @@ struct MvArgs {
     // x * (1 / sqrt(mean(x^2) + eps)) * norm (ops.zig:10-29 rmsNorm), then quantized.
     const float *norm;
     float eps;
+    // Register kernel: rows dealt to the row groups in turn, one step's rows (R * (64 >> LG)) at a
+    // time, instead of a contiguous range per group (a step's loads then cover one contiguous
+    // span of the matrix across the whole grid).
+    int interleave;
 };
 
 // Chunks of 1024 inputs a wave of the register kernel stages in one pass (its prefetch depth).
@@ -701,8 +706,11 @@ __global__ __launch_bounds__(NW * 64) void mmvq_kernel(MvArgs a) {
 
 // ---------------------------------------------------------------------------------------------
 // Register kernel: lane l of every wave owns units l, l+64, ... (C of them) of every row, and
-// keeps their activations for all NT tokens in registers. A wave streams a contiguous range of
-// whole rows, R rows per step, so row addresses are wave-uniform (scalar) and each activation
+// keeps their activations for all NT tokens in registers. A wave streams whole rows, R rows per
+// step (one token: step s of wave group g takes the step-sized row chunk s * groups + g, so that
+// each step's loads across the grid cover one contiguous span of the matrix, which measured
+// faster than a contiguous row range per wave; several tokens: a contiguous range, as their
+// kernels have no registers to spare), so row addresses are wave-uniform (scalar) and each activation
 // register is reused for every row. There is no LDS and no barrier: the first step's weight
 // loads are issued before the activations are read, and an f32 input is quantized by the lanes
 // themselves (a Q8K super-block is four consecutive units, i.e. four neighbouring lanes).
@@ -842,10 +850,19 @@ __global__ __launch_bounds__(NW * 64) void mmvr_kernel(MvArgs a) {
     const uint32_t total = a.ngroups; // rows of all parts
     // Mode HKHIP_SILU_MUL splits the rows in gate/up pairs, so that a pair stays in one wave.
     const uint32_t pr = a.mode == HKHIP_SILU_MUL ? 2u : 1u;
-    const uint32_t r0 = pr * uint32_t(uint64_t(total / pr) * gid / ngroups);
-    const uint32_t r1 = pr * uint32_t(uint64_t(total / pr) * (gid + 1) / ngroups);
+    // Interleaved: step st of this group covers rows (st * ngroups + gid) * RS .. + RS - 1 (clamped
+    // to the last row); contiguous: rows r0 .. r1 - 1, RS per step.
+    // One token only (the multi-token kernels are at the register limit), and not where a step's
+    // rows would split a gate/up pair.
+    const bool il = NT == 1 && a.interleave != 0 && (a.mode != HKHIP_SILU_MUL || RS % 2 == 0);
+    const uint32_t nch = (total + RS - 1) / RS;
+    const uint32_t r0 = il ? 0u : pr * uint32_t(uint64_t(total / pr) * gid / ngroups);
+    const uint32_t r1 = il ? total : pr * uint32_t(uint64_t(total / pr) * (gid + 1) / ngroups);
     // A wave without rows still helps stage the input (and reaches the barrier).
     const uint32_t rlast = r0 < r1 ? r1 - 1 : 0;
+    auto base = [&](uint32_t st) -> uint32_t { return il ? (st * ngroups + gid) * RS : r0 + st * RS; };
+    // Row whose result lane j keeps (lane j = step j / RS, row j % RS of the step).
+    auto row_of = [&](uint32_t j) -> uint32_t { return il ? base(j / RS) + j % RS : r0 + j; };
 
     // Row r of the concatenated parts: its part. Fields are copied member by member so the
     // argument block is never indexed dynamically (which would move it to scratch).
@@ -915,8 +932,10 @@ __global__ __launch_bounds__(NW * 64) void mmvr_kernel(MvArgs a) {
             }
         }
     }
-    const uint32_t ns = (r1 - r0 + RS - 1) / RS; // steps of this wave
-    load(wa, r0);
+    const uint32_t ns = il ? (gid < nch ? (nch - gid + ngroups - 1) / ngroups : 0u)
+                           : (r1 - r0 + RS - 1) / RS; // steps of this wave
+    const uint32_t nres = il ? (ns * RS) : r1 - r0;  // lanes holding a result (rows past the end skipped)
+    load(wa, base(0));
     if (a.x) {
         int8_t *sqs = reinterpret_cast<int8_t *>(smem);
         int16_t *sbs = reinterpret_cast<int16_t *>(smem + nflat);
@@ -1011,21 +1030,21 @@ __global__ __launch_bounds__(NW * 64) void mmvr_kernel(MvArgs a) {
     }
     // The second step is issued only now, so that the barrier does not wait for every wave to get
     // two steps of loads past a busy memory pipeline.
-    if (ns > 1) load(wb, r0 + RS);
+    if (ns > 1) load(wb, base(1));
 
-    // Lane j keeps the result of row r0 + j; the launch gives no wave more than 64 rows, so the
+    // Lane j keeps the result of row row_of(j); the launch gives no wave more than 64 rows, so the
     // results are stored once, at the end, and the loop issues no load but weights.
     float res[NT];
-    const uint32_t fbase = r0;
     auto flush = [&](uint32_t n) {
         if (a.mode == HKHIP_SILU_MUL) {
-            // Lane 2i holds gate row r0 + 2i, lane 2i + 1 its up row (r0 is even).
+            // Lane 2i holds a gate row, lane 2i + 1 its up row (r0 and the interleaved steps' first
+            // rows are even).
             float up[NT];
 #pragma unroll
             for (int t = 0; t < NT; t++) up[t] = __shfl_down(res[t], 1);
-            if (lane < n && (lane & 1) == 0) {
-                const MvPart q = locate(fbase + lane);
-                const uint32_t o = (fbase + lane - q.gstart) / 2;
+            if (lane < n && (lane & 1) == 0 && row_of(lane) < total) {
+                const MvPart q = locate(row_of(lane));
+                const uint32_t o = (row_of(lane) - q.gstart) / 2;
 #pragma unroll
                 for (int t = 0; t < NT; t++) {
                     if (NT > 1 && uint32_t(t) >= a.ntok) break;
@@ -1034,8 +1053,8 @@ __global__ __launch_bounds__(NW * 64) void mmvr_kernel(MvArgs a) {
             }
             return;
         }
-        if (lane < n) {
-            const uint32_t r = fbase + lane;
+        if (lane < n && row_of(lane) < total) {
+            const uint32_t r = row_of(lane);
             MvPart q = a.p[0];
 #pragma unroll
             for (int i = 1; i < MV_PARTS; i++) {
@@ -1059,7 +1078,8 @@ __global__ __launch_bounds__(NW * 64) void mmvr_kernel(MvArgs a) {
             }
         }
     };
-    auto compute = [&](const W (*w)[C], uint32_t rb) {
+    auto compute = [&](const W (*w)[C], uint32_t st) {
+        const uint32_t rb = base(st);
 #pragma unroll
         for (int i = 0; i < R; i++) {
             if (rb + i * G >= r1) break;
@@ -1076,7 +1096,7 @@ __global__ __launch_bounds__(NW * 64) void mmvr_kernel(MvArgs a) {
                         if (NT == 1 || uint32_t(t) < a.ntok) F::dotp(pw, au[t][c], acc[t], corr[t]);
                 }
             }
-            const uint32_t slot = rb + i * G - fbase; // lane of the slot's first row
+            const uint32_t slot = st * RS + i * G; // lane of the slot's first row
 #pragma unroll
             for (int t = 0; t < NT; t++) {
                 const float v = group_sum(acc[t] - corr[t], LG);
@@ -1096,15 +1116,15 @@ __global__ __launch_bounds__(NW * 64) void mmvr_kernel(MvArgs a) {
     // peeled so that nothing is loaded past the range.
     uint32_t s = 0;
     for (; s + 3 < ns; s += 2) {
-        compute(wa, r0 + s * RS);
-        load(wa, r0 + (s + 2) * RS);
-        compute(wb, r0 + (s + 1) * RS);
-        load(wb, r0 + (s + 3) * RS);
+        compute(wa, s);
+        load(wa, base(s + 2));
+        compute(wb, s + 1);
+        load(wb, base(s + 3));
     }
-    auto step = [&](const W (*w)[C], uint32_t st) { compute(w, r0 + st * RS); };
+    auto step = [&](const W (*w)[C], uint32_t st) { compute(w, st); };
     if (s + 2 < ns) {
         step(wa, s);
-        load(wa, r0 + (s + 2) * RS);
+        load(wa, base(s + 2));
         step(wb, s + 1);
         step(wa, s + 2);
     } else if (s + 1 < ns) {
@@ -1127,10 +1147,10 @@ __global__ __launch_bounds__(NW * 64) void mmvr_kernel(MvArgs a) {
             for (int k = 1; k < KS; k++)
 #pragma unroll
                 for (int t = 0; t < NT; t++) res[t] += cb[(k * 64 + lane) * NT + t];
-            flush(r1 - r0);
+            flush(nres);
         }
     } else {
-        flush(r1 - r0);
+        flush(nres);
     }
 }
 

@@ -517,10 +517,12 @@ def test_silu_mul_parts(eng, torch_cuda, t, n, prepared):
 
 
 @pytest.mark.parametrize("t,k,n", [(F.Q4_K, 14336, 8), (F.Q4_K, 16640, 1), (F.Q8_0, 16416, 2),
-                                   (F.Q6_K, 20480, 1), (F.IQ4_NL, 4096, 8)])
+                                   (F.Q6_K, 20480, 1), (F.IQ4_NL, 4096, 8), (F.Q4_K, 4096, 1),
+                                   (F.Q8_0, 4096, 1), (F.Q4_K, 2048, 1)])
 def test_silu_mul_kernel_variants(eng, torch_cuda, t, k, n):
-    """Mode 2 where rows are split over K-slice waves and where the LDS kernel runs (rows longer
-    than the register kernel takes)."""
+    """Mode 2 where rows are split over K-slice waves, where the LDS kernel runs (rows longer
+    than the register kernel takes), and in the one-token register kernels whose steps hold one
+    row (rows then stay in contiguous ranges per wave, so a gate/up pair is never split)."""
     torch = torch_cuda
     m = 2 * 150
     raw = synth.weights_np(t, m, k, seed=1200 + t + k)
