@@ -579,8 +579,9 @@ __global__ __launch_bounds__(NWV * 64) void attn_decode_kernel(AttnArgs a) {
 }
 
 // Prefill attention (passes of more than MAX_DECODE tokens) on the f16 MFMA units, one workgroup
-// per (32-token tile, query head); its four waves take every fourth tile of 32 positions and merge
-// their partial results through LDS at the end (max / sum rescaling, as the slice merge does).
+// per (32-token tile, query head), the tiles with the most positions first; its NWV waves take
+// every NWV-th tile of 32 positions and merge their partial results through LDS at the end (max /
+// sum rescaling, as the slice merge does).
 // Per tile of 32 positions:
 //   S^T[pos][tok] = K[pos] . q[tok]: A = key rows (f16, exact), B = q split as f16 hi + lo (q - hi
 //       rounded again; together q to ~2^-22), two MFMA chains over head_dim in steps of 16;
@@ -604,13 +605,23 @@ struct AttnPArgs {
     uint32_t sq; // q row stride (floats per token)
 };
 
-template <int HD>
-__global__ __launch_bounds__(256, 2) void attn_prefill_kernel(AttnPArgs a) {
+// LDS of attn_prefill_kernel<HD, NWV>: the q operands, then the merge area of waves 1..NWV-1.
+template <int HD, int NWV> struct AttnPSmem {
+    v8h qsh[HD / 16][64], qsl[HD / 16][64];
+    float red_m[NWV - 1][64], red_l[NWV - 1][64];
+    float4 red_acc[NWV - 1][HD / 8][64];
+};
+
+template <int HD, int NWV>
+__global__ __launch_bounds__(NWV * 64, 2) void attn_prefill_kernel(AttnPArgs a) {
     constexpr int NCH = HD / 16, NDT = HD / 32;
+    extern __shared__ __attribute__((aligned(16))) uint8_t attn_smem[];
+    AttnPSmem<HD, NWV> &S = *reinterpret_cast<AttnPSmem<HD, NWV> *>(attn_smem);
     const uint32_t lane = threadIdx.x & 63, h = lane >> 5, j = lane & 31;
     const uint32_t wave = threadIdx.x >> 6;
     const uint32_t item = blockIdx.x; // < ntile * nh (the grid)
-    const uint32_t head = item % a.nh, tile = item / a.nh;
+    const uint32_t ntile = (a.n + 31) / 32;
+    const uint32_t head = item % a.nh, tile = ntile - 1 - item / a.nh; // longest prefixes first
     const uint32_t kvh = head / (a.nh / a.nkv);
     const uint32_t pos0 = a.pos0[0];
     const uint32_t t = tile * 32 + j, tc = t < a.n ? t : a.n - 1; // this lane's token (clamped)
@@ -620,10 +631,11 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(AttnPArgs a) {
     // The tile's q operands (the same 32 tokens for the four waves) live in LDS, split over the
     // waves' lanes to build, so that they take no registers: with them in registers the kernel
     // held one workgroup per CU.
-    __shared__ v8h qsh[NCH][64], qsl[NCH][64];
+    auto &qsh = S.qsh;
+    auto &qsl = S.qsl;
     {
         const float *qrow = a.q + uint64_t(tc) * a.sq + head * HD;
-        for (int c = int(wave); c < NCH; c += 4) {
+        for (int c = int(wave); c < NCH; c += NWV) {
             const float4 x0 = *reinterpret_cast<const float4 *>(qrow + 16 * c + 8 * h);
             const float4 x1 = *reinterpret_cast<const float4 *>(qrow + 16 * c + 8 * h + 4);
             const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
@@ -646,25 +658,36 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(AttnPArgs a) {
     const __half *kb = a.kc + uint64_t(kvh) * a.max_ctx * HD;
     const __half *vb = a.vt + uint64_t(kvh) * HD * a.vt_stride;
     const uint32_t rj = (j & ~12u) | ((j & 4u) << 1) | ((j & 8u) >> 1); // rho(j)
-    for (uint32_t p0 = 32 * wave; p0 < pend; p0 += 128) {
-        v8h ka[NCH], va[NDT][2];
-        {
-            const uint32_t kp = p0 + rj < a.max_ctx ? p0 + rj : a.max_ctx - 1;
-            const v8h *krow = reinterpret_cast<const v8h *>(kb + uint64_t(kp) * HD);
+    // The key rows of the next tile of positions are loaded once this tile's scores are issued,
+    // and its value rows once this tile's output products are: each lands while the other half
+    // of the step runs, with no second set of registers.
+    v8h ka[NCH], va[NDT][2];
+    auto load_k = [&](uint32_t p0) {
+        const uint32_t kp = p0 + rj < a.max_ctx ? p0 + rj : a.max_ctx - 1;
+        const v8h *krow = reinterpret_cast<const v8h *>(kb + uint64_t(kp) * HD);
 #pragma unroll
-            for (int c = 0; c < NCH; c++) ka[c] = krow[2 * c + h];
+        for (int c = 0; c < NCH; c++) ka[c] = krow[2 * c + h];
+    };
+    auto load_v = [&](uint32_t p0) {
 #pragma unroll
-            for (int d = 0; d < NDT; d++)
+        for (int d = 0; d < NDT; d++)
 #pragma unroll
-                for (int cc = 0; cc < 2; cc++)
-                    va[d][cc] = *reinterpret_cast<const v8h *>(vb + uint64_t(32 * d + j) * a.vt_stride + p0 + 16 * cc + 8 * h);
-        }
+            for (int cc = 0; cc < 2; cc++)
+                va[d][cc] = *reinterpret_cast<const v8h *>(vb + uint64_t(32 * d + j) * a.vt_stride + p0 + 16 * cc + 8 * h);
+    };
+    if (32 * wave < pend) {
+        load_k(32 * wave);
+        load_v(32 * wave);
+    }
+    for (uint32_t p0 = 32 * wave; p0 < pend; p0 += 32 * NWV) {
+        const uint32_t pn = p0 + 32 * NWV;
         v16f s = v16f{};
 #pragma unroll
         for (int c = 0; c < NCH; c++) {
             s = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[c], qsh[c][lane], s, 0, 0, 0);
             s = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[c], qsl[c][lane], s, 0, 0, 0);
         }
+        if (pn < pend) load_k(pn);
         // Score v of this lane: position p0 + 16(g >> 1) + 8h + 4(g & 1) + e, g = v / 4, e = v % 4.
         float sv[16], mx = -INFINITY;
 #pragma unroll
@@ -676,11 +699,13 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(AttnPArgs a) {
         }
         mx = fmaxf(mx, __shfl_xor(mx, 32));
         const float mn = fmaxf(m, mx);
-        const float corr = m == -INFINITY ? 0.0f : expf(m - mn);
+        // The hardware exponential (v_exp_f32 on x * log2 e: relative error ~1e-6 over the
+        // softmax's range x <= 0), measured 1 us of the 17 us of a 512-token Llama-3-8B layer.
+        const float corr = m == -INFINITY ? 0.0f : __expf(m - mn);
         float pv[16], ps = 0.0f;
 #pragma unroll
         for (int v = 0; v < 16; v++) {
-            pv[v] = sv[v] == -INFINITY ? 0.0f : expf(sv[v] - mn);
+            pv[v] = sv[v] == -INFINITY ? 0.0f : __expf(sv[v] - mn);
             ps += pv[v];
         }
         ps += __shfl_xor(ps, 32);
@@ -705,11 +730,13 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(AttnPArgs a) {
                 acc[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[d][cc], pl, acc[d], 0, 0, 0);
             }
         }
+        if (pn < pend) load_v(pn);
     }
-    // Merge: waves 1-3 leave {m, l, acc} in LDS (a wave without tiles: m = -inf, l = 0), wave 0
-    // rescales all four to the common maximum, sums and writes.
-    __shared__ float red_m[3][64], red_l[3][64];
-    __shared__ float4 red_acc[3][NDT * 4][64];
+    // Merge: waves 1.. leave {m, l, acc} in LDS (a wave without tiles: m = -inf, l = 0), wave 0
+    // rescales all of them to the common maximum, sums and writes.
+    auto &red_m = S.red_m;
+    auto &red_l = S.red_l;
+    auto &red_acc = S.red_acc;
     if (wave > 0) {
         red_m[wave - 1][lane] = m;
         red_l[wave - 1][lane] = l;
@@ -723,11 +750,11 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(AttnPArgs a) {
     if (wave > 0) return;
     float big = m;
 #pragma unroll
-    for (int w = 0; w < 3; w++) big = fmaxf(big, red_m[w][lane]);
+    for (int w = 0; w < NWV - 1; w++) big = fmaxf(big, red_m[w][lane]);
     const float c0 = m == -INFINITY ? 0.0f : expf(m - big);
-    float lt = l * c0, cw[3];
+    float lt = l * c0, cw[NWV - 1];
 #pragma unroll
-    for (int w = 0; w < 3; w++) {
+    for (int w = 0; w < NWV - 1; w++) {
         const float mw = red_m[w][lane];
         cw[w] = mw == -INFINITY ? 0.0f : expf(mw - big);
         lt = fmaf(red_l[w][lane], cw[w], lt);
@@ -742,7 +769,7 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(AttnPArgs a) {
             for (int g = 0; g < 4; g++) {
                 float4 r = make_float4(acc[d][4 * g] * c0, acc[d][4 * g + 1] * c0, acc[d][4 * g + 2] * c0, acc[d][4 * g + 3] * c0);
 #pragma unroll
-                for (int w = 0; w < 3; w++) {
+                for (int w = 0; w < NWV - 1; w++) {
                     const float4 x = red_acc[w][4 * d + g][lane];
                     r.x = fmaf(x.x, cw[w], r.x);
                     r.y = fmaf(x.y, cw[w], r.y);
@@ -752,6 +779,19 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(AttnPArgs a) {
                 *reinterpret_cast<float4 *>(o + 32 * d + 8 * g + 4 * h) = make_float4(r.x * inv, r.y * inv, r.z * inv, r.w * inv);
             }
     }
+}
+
+template <int HD, int NWV> hipError_t launch_attn_prefill(dim3 grid, const AttnPArgs &pa, hipStream_t s) {
+    constexpr size_t lds = sizeof(AttnPSmem<HD, NWV>);
+    static_assert(lds <= 160 * 1024, "LDS");
+    static bool attr = false;
+    if (!attr) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(attn_prefill_kernel<HD, NWV>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+        attr = true;
+    }
+    hipLaunchKernelGGL((attn_prefill_kernel<HD, NWV>), grid, dim3(NWV * 64), lds, s, pa);
+    return hipGetLastError();
 }
 
 // att[t][h*hd..] = merge of the slices' partials (attention.zig:113-133 merge): every thread
@@ -1074,12 +1114,11 @@ int run_pass(hkhip_net *net, uint32_t n, uint32_t gb) {
         if (n > MAX_DECODE && prefill_mfma(c)) {
             AttnPArgs pa{q, net->kc + li * cache_layer, net->vt + li * vt_layer, net->att, net->pos, n, c.n_heads,
                          c.n_kv_heads, c.max_ctx, vt_stride(c), 1.0f / sqrtf(float(c.head_dim)), S};
-            const dim3 pg((n + 31) / 32 * c.n_heads), pb(256);
-            if (c.head_dim == 64)
-                hipLaunchKernelGGL(attn_prefill_kernel<64>, pg, pb, 0, s, pa);
-            else
-                hipLaunchKernelGGL(attn_prefill_kernel<128>, pg, pb, 0, s, pa);
-            NET_TRY(hipGetLastError(), "prefill attention");
+            const dim3 pg((n + 31) / 32 * c.n_heads);
+            // Four waves: eight per workgroup (two per SIMD, the key tiles split eight ways) measured
+            // 21.3 vs 18.4 us per Llama-3-8B layer and 15.2 vs 16.4 us per Qwen3-0.6B layer.
+            const hipError_t ae = c.head_dim == 64 ? launch_attn_prefill<64, 4>(pg, pa, s) : launch_attn_prefill<128, 4>(pg, pa, s);
+            NET_TRY(ae, "prefill attention");
         } else if (n <= MAX_DECODE) {
             AttnArgs aa{q, net->kc + li * cache_layer, net->vc + li * cache_layer, nullptr, net->pos, n, c.n_heads,
                         c.n_kv_heads, c.head_dim, c.max_ctx, 0, 1.0f / sqrtf(float(c.head_dim)), S};
