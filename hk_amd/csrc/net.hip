@@ -81,6 +81,7 @@ struct RopeArgs {
     uint32_t nheads; // heads this launch covers: nh + nkv (keys), + nkv (values)
     float mscale;    // multiplier of every cos and sin (ops.zig ropeMscale)
     float eps;
+    uint32_t ntok;   // tokens of the pass (the prefill launch's value rows)
 };
 
 // Four heads per workgroup, one per wave; each wave works on its own LDS row, so the waves never
@@ -121,9 +122,9 @@ __device__ __forceinline__ void head_norm_rope(float *h, const float *src, const
     wave_sync();
 }
 
-__global__ __launch_bounds__(256) void rope_kv_kernel(RopeArgs a) {
-    const uint32_t t = blockIdx.y, w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const uint32_t hh = 4 * blockIdx.x + w;
+__device__ __forceinline__ void rope_kv_block(const RopeArgs &a, uint32_t bx, uint32_t t) {
+    const uint32_t w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint32_t hh = 4 * bx + w;
     const uint32_t pos = a.pos0[0] + t;
     const uint32_t hd = a.hd;
     if (hh >= a.nheads) return; // past the last head launched (whole wave; no workgroup barriers below)
@@ -154,15 +155,17 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(RopeArgs a) {
     }
 }
 
+__global__ __launch_bounds__(256) void rope_kv_kernel(RopeArgs a) { rope_kv_block(a, blockIdx.x, blockIdx.y); }
+
 // Value rows of a prefill pass to the f16 caches, 16 tokens of one key/value head per workgroup:
 // the rows go to the value cache as they are and, through an LDS tile, to the transposed cache
 // with consecutive lanes on consecutive positions (decode passes write both in rope_kv_kernel).
-__global__ __launch_bounds__(256) void v_cache_kernel(const float *__restrict__ v, __half *__restrict__ vc,
-                                                      __half *__restrict__ vt, const uint32_t *__restrict__ pos0,
-                                                      uint32_t n, uint32_t skv, uint32_t hd, uint32_t max_ctx,
-                                                      uint32_t vt_stride) {
+__device__ __forceinline__ void v_cache_block(const float *__restrict__ v, __half *__restrict__ vc,
+                                              __half *__restrict__ vt, const uint32_t *__restrict__ pos0, uint32_t n,
+                                              uint32_t skv, uint32_t hd, uint32_t max_ctx, uint32_t vt_stride,
+                                              uint32_t g, uint32_t ty) {
     __shared__ __half tile[16][258];
-    const uint32_t g = blockIdx.x, t0 = blockIdx.y * 16, tid = threadIdx.x;
+    const uint32_t t0 = ty * 16, tid = threadIdx.x;
     const uint32_t nt = n - t0 < 16 ? n - t0 : 16, pos = pos0[0] + t0, kvd = skv; // row stride of v
     for (uint32_t i = 4 * tid; i < nt * hd; i += 1024) { // hd is a multiple of 64: four values of one row
         const uint32_t tt = i / hd, d = i % hd;
@@ -180,6 +183,17 @@ __global__ __launch_bounds__(256) void v_cache_kernel(const float *__restrict__ 
         const uint32_t d = i / 16, tt = i % 16;
         if (tt < nt) vt[(uint64_t(g) * hd + d) * vt_stride + pos + tt] = tile[tt][d];
     }
+}
+
+// A prefill pass's rope / key writes (the first rx * n workgroups, as rope_kv_kernel's grid
+// (rx, n)) and value writes (the rest, nkv x ceil(n / 16) workgroups of 16 tokens of one head) in one launch.
+__global__ __launch_bounds__(256) void rope_kv_v_kernel(RopeArgs a, const float *__restrict__ v, uint32_t rx) {
+    const uint32_t b = blockIdx.x, nr = rx * a.ntok;
+    if (b < nr)
+        rope_kv_block(a, b % rx, b / rx);
+    else
+        v_cache_block(v, a.vc, a.vt, a.pos0, a.ntok, a.skv, a.hd, a.max_ctx, a.vt_stride, (b - nr) % a.nkv,
+                      (b - nr) / a.nkv);
 }
 
 // Attention over one slice of the context for one (token, query head): one wave each, four per
@@ -1097,19 +1111,18 @@ int run_pass(hkhip_net *net, uint32_t n, uint32_t gb) {
         RopeArgs ra{q, k, v, L.q_norm, L.k_norm, net->inv_freq, net->kc + li * cache_layer,
                     net->vc + li * cache_layer, net->vt + li * vt_layer, net->pos, c.n_heads, c.n_kv_heads, c.head_dim,
                     c.rope_dim / 2, c.rope_neox, c.max_ctx, vt_stride(c), S, SKV, 0, c.rope_mscale, c.rms_eps};
-        // Prefill passes write the value heads with v_cache_kernel (coalesced transposed writes);
+        // Prefill passes write the value heads with v_cache_block (coalesced transposed writes);
         // one-token passes do all of it in the attention kernel.
         const bool vsep = n > MAX_DECODE, fused = n == 1;
         ra.nheads = c.n_heads + (vsep ? 1 : 2) * c.n_kv_heads;
-        if (!fused) {
+        if (vsep) { // one launch: rope / key writes, then the value rows
+            ra.ntok = n;
+            const uint32_t rx = (ra.nheads + 3) / 4;
+            hipLaunchKernelGGL(rope_kv_v_kernel, dim3(rx * n + c.n_kv_heads * ((n + 15) / 16)), dim3(256), 0, s, ra, v, rx);
+            NET_TRY(hipGetLastError(), "rope / kv write");
+        } else if (!fused) {
             hipLaunchKernelGGL(rope_kv_kernel, dim3((ra.nheads + 3) / 4, n), dim3(256), 0, s, ra);
             NET_TRY(hipGetLastError(), "rope / kv write");
-        }
-        if (vsep) {
-            hipLaunchKernelGGL(v_cache_kernel, dim3(c.n_kv_heads, (n + 15) / 16), dim3(256), 0, s, v,
-                               net->vc + li * cache_layer, net->vt + li * vt_layer, net->pos, n, SKV, c.head_dim,
-                               c.max_ctx, vt_stride(c));
-            NET_TRY(hipGetLastError(), "value cache");
         }
         if (n > MAX_DECODE && prefill_mfma(c)) {
             AttnPArgs pa{q, net->kc + li * cache_layer, net->vt + li * vt_layer, net->att, net->pos, n, c.n_heads,
