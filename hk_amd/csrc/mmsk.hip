@@ -14,9 +14,9 @@
 //  * J: one v_mfma_f32_16x16x32_bf16 over exact bf16 integers: the mins against the tokens'
 //    bsum32 = 64*u + v (the activation buffer's k_ilmb plane), exact in f32 (|J| < 2^22).
 // Q6_K (kernelK with the 16-weight groups): y += da*d*I, I = sum_g sc_g * sum_{k in g} (q - 32)*a.
-// A lane's 16 weights of a chunk are one group, so the signed 8-bit scale folds into them as
-// three int8 digit planes, sc = 64*e2 + 8*e1 + e0 with digits in [-3, 4] (each (q - 32)*e in
-// [-128, 124]); one int32 chain ((P2 << 3) + P1 << 3) + P0 gives I exactly (as the prefill GEMM).
+// A lane's 16 weights of a chunk are one group, so the signed 8-bit scale folds into them,
+// w = sc*(q - 32), split into two int8 planes 4*w = 256*H + L (H in [-63, 64], L in [-128, 124]);
+// one int32 chain (H-sum << 8) + L-sum gives 4*I exactly (as the prefill GEMM).
 //
 // Layout. A workgroup owns 16 rows of one part (fused products: up to 4 matrices reading the
 // same input, their row tiles numbered in sequence); its KS waves split the super-blocks and add
@@ -76,21 +76,6 @@ __device__ __forceinline__ uint32_t mul_bytes(uint32_t nib, uint32_t f2) {
 
 __device__ __forceinline__ v4i ld16(const void *g) { return *reinterpret_cast<const v4i *>(g); }
 
-// Q6_K: bytes q (each in [0, 63]) times a digit e in [-3, 4], minus 32*e, per byte as a
-// two's-complement byte (even and odd bytes through packed 16-bit multiply-adds, interleaved back
-// by a byte permute); sc = 64*e2 + 8*e1 + e0 with digits in [-3, 4].
-__device__ __forceinline__ uint32_t plane4(uint32_t ev, uint32_t od, uint32_t m, uint32_t c) {
-    const us2 pe = __builtin_bit_cast(us2, ev) * __builtin_bit_cast(us2, m) + __builtin_bit_cast(us2, c);
-    const us2 po = __builtin_bit_cast(us2, od) * __builtin_bit_cast(us2, m) + __builtin_bit_cast(us2, c);
-    return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, po), __builtin_bit_cast(uint32_t, pe), 0x06020400u);
-}
-__device__ __forceinline__ void digits(int sc, int e[3]) {
-    e[0] = ((sc + 3) & 7) - 3;
-    const int r = (sc - e[0]) >> 3;
-    e[1] = ((r + 3) & 7) - 3;
-    e[2] = (r - e[1]) >> 3;
-}
-__device__ __forceinline__ uint32_t lo16x2(int v) { return (uint32_t(v) & 0xFFFFu) * 0x00010001u; }
 // s_waitcnt vmcnt(N), as assembly with a memory clobber so that no memory access (the LDS
 // reads of the slot just waited for, in particular) moves across it.
 template <int N> __device__ __forceinline__ void wait_vm() {
@@ -125,41 +110,39 @@ __device__ __forceinline__ void sk_step_q6k(const uint8_t *slot, const SkAct<NTT
     const uint32_t scs[4] = {scw.x, scw.y, scw.z, scw.w};
     const uint32_t dword = *reinterpret_cast<const uint32_t *>(slot + 16 * 208 + 4 * p);
     const float d = f16_bits_to_f32(dodd ? dword >> 16 : dword & 0xFFFF);
-    v4i P[3][4];
+    // Planes H, L of the group-scaled weights (4*w = 256*H + L); 4*I is scaled by d/4.
+    v4i P[2][4];
 #pragma unroll
     for (int c = 0; c < 4; c++) {
         const int n = c >> 1;
         const uint32_t sidx = 8 * n + 4 * (c & 1) + 2 * (g >> 1) + (g & 1);
         const int sc = int(int8_t((scs[sidx / 4] >> (8 * (sidx % 4))) & 0xFF));
-        int e[3];
-        digits(sc, e);
+        const uint32_t m = half2_of(sc), k = half2_of(32 - 32 * sc);
         const uint32_t qs = 2 * (2 * (c & 1) + (g >> 1));
         const uint32_t lw[4] = {ql[n].x, ql[n].y, ql[n].z, ql[n].w};
         const uint32_t hw[4] = {qh[n].x, qh[n].y, qh[n].z, qh[n].w};
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const uint32_t q = ((lw[i] >> (4 * (c & 1))) & 0x0F0F0F0Fu) | (((hw[i] >> qs) & 0x03030303u) << 4);
-            const uint32_t ev = q & 0x00FF00FFu, od = (q >> 8) & 0x00FF00FFu;
-#pragma unroll
-            for (int k = 0; k < 3; k++) P[k][c][i] = int(plane4(ev, od, lo16x2(e[k]), lo16x2(-32 * e[k])));
+            int hp, lp;
+            q6k_planes(q, m, k, hp, lp);
+            P[0][c][i] = hp;
+            P[1][c][i] = lp;
         }
     }
+    const float d4 = 0.25f * d;
     float dr[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) dr[i] = __shfl(d, int(4 * g + i));
+    for (int i = 0; i < 4; i++) dr[i] = __shfl(d4, int(4 * g + i));
 #pragma unroll
     for (int tt = 0; tt < NTT; tt++) {
         v4i s = {0, 0, 0, 0};
 #pragma unroll
-        for (int c = 0; c < 4; c++) s = __builtin_amdgcn_mfma_i32_16x16x64_i8(P[2][c], x.a[tt][c], s, 0, 0, 0);
+        for (int c = 0; c < 4; c++) s = __builtin_amdgcn_mfma_i32_16x16x64_i8(P[0][c], x.a[tt][c], s, 0, 0, 0);
 #pragma unroll
-        for (int i = 0; i < 4; i++) s[i] <<= 3;
+        for (int i = 0; i < 4; i++) s[i] <<= 8;
 #pragma unroll
         for (int c = 0; c < 4; c++) s = __builtin_amdgcn_mfma_i32_16x16x64_i8(P[1][c], x.a[tt][c], s, 0, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 4; i++) s[i] <<= 3;
-#pragma unroll
-        for (int c = 0; c < 4; c++) s = __builtin_amdgcn_mfma_i32_16x16x64_i8(P[0][c], x.a[tt][c], s, 0, 0, 0);
 #pragma unroll
         for (int i = 0; i < 4; i++) acc[0][tt][i] = fmaf((float)s[i], dr[i] * (x.da[tt] * keep), acc[0][tt][i]);
     }

@@ -5,10 +5,10 @@
 // kernelLegacy 131-176 for the 32-weight blocks):
 //  * Q6_K: per row r, token t and super-block b, y += d[r,b]*da[t,b] * I with the exact integer
 //    I = sum_g sc[r,b,g] * sum_{k in g} (q[r,k] - 32) * a[t,k] over the 16 groups of 16. The
-//    signed 8-bit group scale is folded into the weights as three int8 planes: sc = 64*e2 +
-//    8*e1 + e0 with digits in [-3, 4], so every plane value (q - 32)*e lies in [-128, 124].
-//    Each MFMA lane holds 16 weights of one group, so a lane's plane bytes share one digit. One
-//    int32 chain per tile gives ((P2 << 3) + P1 << 3) + P0 = I, the reference's integer.
+//    signed 8-bit group scale is folded into the weights, w = sc*(q - 32) in [-4096, 4096], and
+//    w is split into two int8 planes, 4*w = 256*H + L with H in [-63, 64] and L in [-128, 124].
+//    Each MFMA lane holds 16 weights of one group (one scale per lane and chunk). One int32
+//    chain per tile gives (H-sum << 8) + L-sum = 4*I, the reference's integer times four.
 //  * 32-weight formats: y += (dw[r,c]*da[t,c]) * I_c per block c (I_c exact). One 32x32x32
 //    int8 MFMA yields the tile's I_c; then per output one multiply (dw*da), one convert and one
 //    fma. Q4_0 / Q5_0 weights enter as u - zp (kernelLegacy's acci - zp*s); Q4_1 / Q5_1 as u,
@@ -103,24 +103,6 @@ struct MxArgs {
     uint32_t rblocks, tblocks;
 };
 
-// Bytes q (each in [0, 63]) times a digit e in [-3, 4], minus 32*e: per byte (q - 32)*e as a
-// two's-complement byte. Even and odd bytes go through packed 16-bit multiply-adds (the low
-// byte of each 16-bit product is the wanted byte) and are interleaved back by a byte permute.
-__device__ __forceinline__ uint32_t plane4(uint32_t ev, uint32_t od, uint32_t m, uint32_t c) {
-    const us2 pe = __builtin_bit_cast(us2, ev) * __builtin_bit_cast(us2, m) + __builtin_bit_cast(us2, c);
-    const us2 po = __builtin_bit_cast(us2, od) * __builtin_bit_cast(us2, m) + __builtin_bit_cast(us2, c);
-    return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, po), __builtin_bit_cast(uint32_t, pe), 0x06020400u);
-}
-
-// sc = 64*e2 + 8*e1 + e0, digits in [-3, 4] (e2 in [-2, 2] for sc in [-128, 127]).
-__device__ __forceinline__ void digits(int sc, int e[3]) {
-    e[0] = ((sc + 3) & 7) - 3;
-    const int r = (sc - e[0]) >> 3;
-    e[1] = ((r + 3) & 7) - 3;
-    e[2] = (r - e[1]) >> 3;
-}
-
-__device__ __forceinline__ uint32_t lo16x2(int v) { return (uint32_t(v) & 0xFFFFu) * 0x00010001u; }
 
 // KS > 1 splits K over KS slices of NW waves, each with its own ring; the partial tiles are
 // added in LDS in slice order at the end (as in the Q4_K ring kernel).
@@ -342,38 +324,36 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
             const uint32_t scs[4] = {scw.x, scw.y, scw.z, scw.w};
             const uint32_t dword = *reinterpret_cast<const uint32_t *>(&S.ws[wave][4 * j]);
             const float d = f16_bits_to_f32(((sbase + sb) & 1) ? dword >> 16 : dword & 0xFFFF);
-            v4i P[3][8];
+            // Planes H, L of the group-scaled weights (4*w = 256*H + L).
+            v4i P[2][8];
 #pragma unroll
             for (int c = 0; c < 8; c++) {
                 const int n = c / 4, p = c % 4;
                 const uint32_t sbyte = 8 * n + 2 * p + h;
                 const int sc = int(int8_t((scs[sbyte / 4] >> (8 * (sbyte % 4))) & 0xFF));
-                int e[3];
-                digits(sc, e);
+                const uint32_t m = half2_of(sc), k = half2_of(32 - 32 * sc);
                 const uint32_t qlw[4] = {ql[n][p & 1].x, ql[n][p & 1].y, ql[n][p & 1].z, ql[n][p & 1].w};
                 const uint32_t qhw[4] = {qh[n].x, qh[n].y, qh[n].z, qh[n].w};
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const uint32_t q = ((qlw[i] >> (4 * (p >> 1))) & 0x0F0F0F0Fu) | (((qhw[i] >> (2 * p)) & 0x03030303u) << 4);
-                    const uint32_t ev = q & 0x00FF00FFu, od = (q >> 8) & 0x00FF00FFu;
-#pragma unroll
-                    for (int k = 0; k < 3; k++) P[k][c][i] = int(plane4(ev, od, lo16x2(e[k]), lo16x2(-32 * e[k])));
+                    int hp, lp;
+                    q6k_planes(q, m, k, hp, lp);
+                    P[0][c][i] = hp;
+                    P[1][c][i] = lp;
                 }
             }
+            const float d4 = 0.25f * d;
             load_a(0);
 #pragma unroll
             for (int t = 0; t < TT; t++) {
                 v16i sacc = {};
 #pragma unroll
-                for (int c = 0; c < 8; c++) sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[c], P[2][c], sacc, 0, 0, 0);
+                for (int c = 0; c < 8; c++) sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[c], P[0][c], sacc, 0, 0, 0);
 #pragma unroll
-                for (int v = 0; v < 16; v++) sacc[v] <<= 3;
+                for (int v = 0; v < 16; v++) sacc[v] <<= 8;
 #pragma unroll
                 for (int c = 0; c < 8; c++) sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[c], P[1][c], sacc, 0, 0, 0);
-#pragma unroll
-                for (int v = 0; v < 16; v++) sacc[v] <<= 3;
-#pragma unroll
-                for (int c = 0; c < 8; c++) sacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[c], P[0][c], sacc, 0, 0, 0);
                 if (t + 1 < TT) load_a(t + 1);
                 const float4 *dap = reinterpret_cast<const float4 *>(&S.da[32 * t + 4 * h]);
 #pragma unroll
@@ -381,7 +361,7 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
                     const float4 dv = dap[2 * g];
                     const float ds[4] = {dv.x, dv.y, dv.z, dv.w};
 #pragma unroll
-                    for (int e = 0; e < 4; e++) acc[t][4 * g + e] = fmaf((float)sacc[4 * g + e], d * ds[e], acc[t][4 * g + e]);
+                    for (int e = 0; e < 4; e++) acc[t][4 * g + e] = fmaf((float)sacc[4 * g + e], d4 * ds[e], acc[t][4 * g + e]);
                 }
             }
         } else {
