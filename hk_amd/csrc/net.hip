@@ -35,7 +35,8 @@ using namespace hkhip;
 namespace {
 
 constexpr uint32_t ATT_SLICE = 64; // positions per attention slice (one step of the kernel)
-constexpr uint32_t MAX_DECODE = 8;  // tokens of a pass that runs the decode kernels (and a graph)
+constexpr uint32_t MAX_DECODE = 8;
+constexpr uint32_t ATT_MERGE_MAX = 256; // decode attention chunks the fused merge takes (more: attn_combine_kernel)  // tokens of a pass that runs the decode kernels (and a graph)
 
 // ---------------------------------------------------------------------------------------------
 // Kernels
@@ -217,6 +218,10 @@ struct AttnArgs {
     float *att;
     int fused;
     RopeArgs r;
+    // Several chunks: with cnt set, the last chunk workgroup of (head, token) to finish merges the
+    // partials into merge_out itself (cnt: one counter per (token, head), zero between launches).
+    uint32_t *cnt;
+    float *merge_out;
 };
 
 // A lane's DL dimensions of one value row: DL halves in one (DL = 1: the low half) or two words.
@@ -353,6 +358,52 @@ __device__ __forceinline__ float wave_sum_f(float v) {
 __device__ __forceinline__ float wave_max_f(float v) {
     const float r = row_max(v);
     return fmaxf(fmaxf(readlane_f(r, 0), readlane_f(r, 16)), fmaxf(readlane_f(r, 32), readlane_f(r, 48)));
+}
+
+// o[0..hd) = merge of nslice partials {max, sum, acc[hd]} at p (attention.zig:113-133 merge): every
+// thread reads one slice's {max, sum} (all loads in flight at once), the block reduces them, the
+// weights exp(m_s - max m) of the non-empty slices go to LDS (wts), then thread d sums its
+// dimension over the slices with the loads of eight slices issued together. red: one float per wave.
+// COH: the partials come from other workgroups of the same launch (agent-scope loads).
+template <bool COH = false>
+__device__ __forceinline__ void merge_partials(const float *p, float *o, uint32_t hd, uint32_t nslice, float *wts,
+                                               float *red) {
+    auto ld = [&](uint64_t i) -> float {
+        if constexpr (COH)
+            return __hip_atomic_load(const_cast<float *>(p) + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else
+            return p[i];
+    };
+    float big = -INFINITY;
+    for (uint32_t s = threadIdx.x; s < nslice; s += blockDim.x)
+        if (ld(s * (hd + 2) + 1) != 0.0f) big = fmaxf(big, ld(s * (hd + 2)));
+    for (int o = 32; o >= 1; o >>= 1) big = fmaxf(big, __shfl_xor(big, o));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = big;
+    __syncthreads();
+    big = red[0];
+    for (uint32_t i = 1; i < (blockDim.x >> 6); i++) big = fmaxf(big, red[i]);
+    float tot = 0.0f;
+    for (uint32_t s = threadIdx.x; s < nslice; s += blockDim.x) {
+        const float l = ld(s * (hd + 2) + 1);
+        const float wgt = l != 0.0f ? expf(ld(s * (hd + 2)) - big) : 0.0f;
+        wts[s] = wgt;
+        tot = fmaf(wgt, l, tot);
+    }
+    tot = block_sum(tot, red);
+    const float inv = 1.0f / tot;
+    for (uint32_t d = threadIdx.x; d < hd; d += blockDim.x) {
+        float v = 0.0f;
+        uint32_t s = 0;
+        for (; s + 8 <= nslice; s += 8) {
+            float pv[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) pv[i] = ld((s + i) * (hd + 2) + 2 + d);
+#pragma unroll
+            for (int i = 0; i < 8; i++) v = fmaf(wts[s + i], pv[i], v);
+        }
+        for (; s < nslice; s++) v = fmaf(wts[s], ld(s * (hd + 2) + 2 + d), v);
+        o[d] = v * inv;
+    }
 }
 
 // The fused decode pass's q row (and, with kx, the new key row) of one head: headNorm (ops.zig:
@@ -580,16 +631,72 @@ __global__ __launch_bounds__(NWV * 64) void attn_decode_kernel(AttnArgs a) {
     }
     // The chunk's partial: {max, sum, acc} (unnormalized), as attn_combine_kernel reads them.
     float *out = a.part + ((uint64_t(t) * a.nh + h) * gridDim.x + g) * (HD + 2);
+    // With the merge in this launch, the partial goes out by agent-scope stores (they complete at
+    // the device's coherent level, not in this XCD's L2), so no cache write-back is needed.
+    auto put = [&](uint32_t i, float v) {
+        if (a.cnt)
+            __hip_atomic_store(out + i, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else
+            out[i] = v;
+    };
     for (uint32_t d = threadIdx.x; d < HD; d += NWV * 64) {
         float v = 0.0f;
 #pragma unroll
         for (int i = 0; i < NWV; i++) v = fmaf(wt[i], red_acc[i][d], v);
-        out[2 + d] = v;
+        put(2 + d, v);
     }
     if (threadIdx.x == 0) {
-        out[0] = big;
-        out[1] = tot;
+        put(0, big);
+        put(1, tot);
     }
+    if (!a.cnt) return; // attn_combine_kernel merges
+    // Count the chunk in; the last of (head, token) to arrive merges every chunk's partial with
+    // agent-scope loads. Each wave waits for its stores to complete before the barrier, so the
+    // count follows the whole partial; no workgroup waits for another.
+    __shared__ uint32_t last;
+    __shared__ float mw[ATT_MERGE_MAX], mred[NWV];
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t *c = a.cnt + uint64_t(t) * a.nh + h;
+        last = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 == gridDim.x ? 1u : 0u;
+        if (last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!last) return;
+    if (gridDim.x <= 8) {
+        // One round of loads: thread d reads every chunk's {max, sum, acc[d]} at once.
+        const float *pp = a.part + (uint64_t(t) * a.nh + h) * gridDim.x * (HD + 2);
+        for (uint32_t d = threadIdx.x; d < HD; d += NWV * 64) {
+            float m[8], l[8], v[8];
+#pragma unroll
+            for (uint32_t i = 0; i < 8; i++) {
+                if (i < gridDim.x) {
+                    float *q = const_cast<float *>(pp) + i * (HD + 2);
+                    m[i] = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    l[i] = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    v[i] = __hip_atomic_load(q + 2 + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+            float mx = -INFINITY;
+#pragma unroll
+            for (uint32_t i = 0; i < 8; i++)
+                if (i < gridDim.x && l[i] != 0.0f) mx = fmaxf(mx, m[i]);
+            float sum = 0.0f, acc = 0.0f;
+#pragma unroll
+            for (uint32_t i = 0; i < 8; i++) {
+                if (i < gridDim.x) {
+                    const float wgt = l[i] != 0.0f ? expf(m[i] - mx) : 0.0f;
+                    sum = fmaf(wgt, l[i], sum);
+                    acc = fmaf(wgt, v[i], acc);
+                }
+            }
+            a.merge_out[(uint64_t(t) * a.nh + h) * HD + d] = acc * (1.0f / sum);
+        }
+        return;
+    }
+    merge_partials<true>(a.part + (uint64_t(t) * a.nh + h) * gridDim.x * (HD + 2), a.merge_out + (uint64_t(t) * a.nh + h) * HD,
+                         HD, gridDim.x, mw, mred);
 }
 
 // Prefill attention (passes of more than MAX_DECODE tokens) on the f16 MFMA units, one workgroup
@@ -808,47 +915,13 @@ template <int HD, int NWV> hipError_t launch_attn_prefill(dim3 grid, const AttnP
     return hipGetLastError();
 }
 
-// att[t][h*hd..] = merge of the slices' partials (attention.zig:113-133 merge): every thread
-// reads one slice's {max, sum} (all loads in flight at once), the block reduces them, the weights
-// exp(m_s - max m) of the non-empty slices go to LDS, then thread d sums its dimension over the
-// slices with the loads of eight slices issued together.
+// att[t][h*hd..] = merge of the slices' partials of (head h, token t).
 __global__ __launch_bounds__(256) void attn_combine_kernel(const float *__restrict__ part, float *__restrict__ att,
                                                            uint32_t nh, uint32_t hd, uint32_t nslice) {
     extern __shared__ float wts[]; // [nslice]
     __shared__ float red[4];
     const uint32_t t = blockIdx.y, h = blockIdx.x;
-    const float *p = part + (uint64_t(t) * nh + h) * nslice * (hd + 2);
-    float big = -INFINITY;
-    for (uint32_t s = threadIdx.x; s < nslice; s += blockDim.x)
-        if (p[s * (hd + 2) + 1] != 0.0f) big = fmaxf(big, p[s * (hd + 2)]);
-    for (int o = 32; o >= 1; o >>= 1) big = fmaxf(big, __shfl_xor(big, o));
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = big;
-    __syncthreads();
-    big = red[0];
-    for (uint32_t i = 1; i < (blockDim.x >> 6); i++) big = fmaxf(big, red[i]);
-    float tot = 0.0f;
-    for (uint32_t s = threadIdx.x; s < nslice; s += blockDim.x) {
-        const float l = p[s * (hd + 2) + 1];
-        const float wgt = l != 0.0f ? expf(p[s * (hd + 2)] - big) : 0.0f;
-        wts[s] = wgt;
-        tot = fmaf(wgt, l, tot);
-    }
-    tot = block_sum(tot, red);
-    const float inv = 1.0f / tot;
-    float *o = att + (uint64_t(t) * nh + h) * hd;
-    for (uint32_t d = threadIdx.x; d < hd; d += blockDim.x) {
-        float v = 0.0f;
-        uint32_t s = 0;
-        for (; s + 8 <= nslice; s += 8) {
-            float pv[8];
-#pragma unroll
-            for (int i = 0; i < 8; i++) pv[i] = p[(s + i) * (hd + 2) + 2 + d];
-#pragma unroll
-            for (int i = 0; i < 8; i++) v = fmaf(wts[s + i], pv[i], v);
-        }
-        for (; s < nslice; s++) v = fmaf(wts[s], p[s * (hd + 2) + 2 + d], v);
-        o[d] = v * inv;
-    }
+    merge_partials<false>(part + (uint64_t(t) * nh + h) * nslice * (hd + 2), att + (uint64_t(t) * nh + h) * hd, hd, nslice, wts, red);
 }
 
 } // namespace
@@ -880,6 +953,7 @@ struct hkhip_net {
     uint8_t *xq = nullptr;
     __half *kc = nullptr, *vc = nullptr, *vt = nullptr;
     uint32_t *io = nullptr, *tok = nullptr, *pos = nullptr; // device {pos, tokens[cap]}
+    uint32_t *att_cnt = nullptr; // [MAX_DECODE][n_heads] decode attention chunk counters (zero between launches)
     uint32_t *stage = nullptr;                               // pinned host copy of io
     std::map<uint32_t, hipGraphExec_t> graphs;
     std::map<uint32_t, int> runs; // eager runs per decode shape: token count | attention chunks << 8 (a graph is captured after one)
@@ -1001,6 +1075,12 @@ int ensure_cap(hkhip_net *n, uint32_t want) {
         return rc;
     n->pos = n->io;
     n->tok = n->io + 1;
+    if (!n->att_cnt) {
+        const uint64_t cb = uint64_t(MAX_DECODE) * c.n_heads * 4;
+        if ((rc = dev_alloc(n, cb, (void **)&n->att_cnt))) return rc;
+        NET_TRY(hipMemset(n->att_cnt, 0, cb), "attention counters");
+        NET_TRY(hipDeviceSynchronize(), "attention counters");
+    }
     NET_TRY(hipHostMalloc(reinterpret_cast<void **>(&n->stage), (T + 1) * 4, hipHostMallocDefault), "hipHostMalloc");
     n->cap = want;
     return HKHIP_OK;
@@ -1139,6 +1219,9 @@ int run_pass(hkhip_net *net, uint32_t n, uint32_t gb) {
             aa.att = gb == 1 ? net->att : nullptr;
             aa.fused = fused ? 1 : 0;
             aa.r = ra;
+            const bool merge_in = gb > 1 && gb <= ATT_MERGE_MAX;
+            aa.cnt = merge_in ? net->att_cnt : nullptr;
+            aa.merge_out = net->att;
             const dim3 dg(gb, c.n_heads, n);
             if (c.head_dim == 64)
                 hipLaunchKernelGGL((attn_decode_kernel<64, ATT_DWAVES>), dg, dim3(64 * ATT_DWAVES), 0, s, aa);
@@ -1147,7 +1230,7 @@ int run_pass(hkhip_net *net, uint32_t n, uint32_t gb) {
             else
                 hipLaunchKernelGGL((attn_decode_kernel<256, ATT_DWAVES>), dg, dim3(64 * ATT_DWAVES), 0, s, aa);
             NET_TRY(hipGetLastError(), "decode attention");
-            if (gb > 1) {
+            if (gb > 1 && !merge_in) {
                 hipLaunchKernelGGL(attn_combine_kernel, dim3(c.n_heads, n), dim3(std::min(256u, std::max(64u, (c.head_dim + 63) / 64 * 64))),
                                    gb * 4, s, net->part, net->att, c.n_heads, c.head_dim, gb);
                 NET_TRY(hipGetLastError(), "decode attention combine");

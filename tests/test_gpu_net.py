@@ -235,3 +235,25 @@ def test_net_attention_chunk_boundaries(eng):
             net.forward(toks, pos)
             check(net.logits(), cpu.forward(toks, pos), f"chunk boundaries: pass of {n} at {pos}")
             pos += n
+
+
+def test_net_many_attention_chunks(eng):
+    """Decode passes past 2048 positions, where decode attention runs over more than eight chunk
+    workgroups per (head, token): the last chunk to finish merges the others' partials with the
+    general merge (two rounds of loads); up to eight chunks it takes the one-round merge."""
+    from hk_amd.net import Net
+
+    cfg = Config(dim=128, n_layers=1, n_heads=2, n_kv_heads=1, head_dim=64, ffn_dim=256, vocab=256, max_ctx=2200,
+                 rope_neox=True, rope_base=1e4)
+    model = synth.model_np(cfg, F.Q8_0, seed=4900, out_fmt=F.Q8_0, embd_fmt=F.Q8_0, qk_norm=True, bias=False)
+    rng = np.random.default_rng(4901)
+    cpu = Oracle(cfg, model)
+    with Net(eng, cfg) as net:
+        net.load(model)
+        pos = 0
+        # 2040 by prefill (eight chunks for the passes up to 2048), then passes over 2048 (nine)
+        for n in [2040, 1, 3, 1, 1, 3, 1, 8, 1, 1]:
+            toks = rng.integers(0, cfg.vocab, n)
+            net.forward(toks, pos)
+            check(net.logits(), cpu.forward(toks, pos), f"many chunks: pass of {n} at {pos}")
+            pos += n
