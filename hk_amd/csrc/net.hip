@@ -975,10 +975,12 @@ int hfail(hipError_t e, const char *what) {
 uint32_t qdim(const hkhip_net_config &c) { return c.n_heads * c.head_dim; }
 uint32_t kvdim(const hkhip_net_config &c) { return c.n_kv_heads * c.head_dim; }
 uint32_t qkvdim(const hkhip_net_config &c) { return qdim(c) + 2 * kvdim(c); }
-// Waves per decode attention workgroup (64 positions each). Four: a workgroup of eight takes longer
-// for the same positions (one CU then pulls twice the key and value bytes: 15.4 against 11.2 us per
-// layer at 576 positions with the merge), and with four the context's loads spread over more CUs.
-constexpr uint32_t ATT_DWAVES = 4;
+// Waves per decode attention workgroup (64 positions each). Two: against four, the context's loads
+// spread over twice the CUs and each workgroup's dependent steps halve, while the chunks' merge
+// (in the same launch) stays one round of loads up to 1024 positions: 1.614 vs 1.645 ms per token
+// on Llama-3-8B shapes, 0.806 vs 0.854 on Qwen3-0.6B shapes at 512-575 positions. Eight took
+// longer still than four (one CU then pulls twice the key and value bytes).
+constexpr uint32_t ATT_DWAVES = 2;
 uint32_t nslices(const hkhip_net_config &c) { return (c.max_ctx + ATT_SLICE - 1) / ATT_SLICE; }
 uint32_t vt_stride(const hkhip_net_config &c) { return (c.max_ctx + 31) / 32 * 32; }
 bool prefill_mfma(const hkhip_net_config &c) { return c.head_dim == 64 || c.head_dim == 128; }

@@ -133,8 +133,8 @@ def test_net_from_hk_file(eng, tmp_path, arch, fmt, tie, vec_type):
 
 
 def test_net_long_context(eng):
-    """Decode passes past 1030 positions, where decode attention runs over five chunk workgroups
-    of 256 positions per (head, token) and their merge (one-token passes fused with the key/value
+    """Decode passes past 1030 positions, where decode attention runs over nine chunk workgroups
+    of 128 positions per (head, token) and their merge (one-token passes fused with the key/value
     writes, passes of 3 and 8 tokens after the separate rope / cache kernel); a prefill of 1030
     tokens (four-wave MFMA tiles over 33 position tiles) before them."""
     from hk_amd.net import Net
@@ -213,7 +213,7 @@ def test_net_rope_scaling(eng, kind):
 
 def test_net_attention_chunk_boundaries(eng):
     """Decode passes stepping across the context sizes where the attention chunk count changes (one
-    chunk of 256 positions per (head, token) up to 256, then 2, 4 and the cap): each chunk count is
+    chunk of 128 positions per (head, token) up to 128, then 2, 4 and 8 by 256, 512 and 1024): each chunk count is
     its own captured graph, the one-chunk passes write the attention output directly and the
     one-token passes do the key/value writes inside the attention kernel. Every pass is checked
     against the CPU forward, so each reads the cache rows all earlier passes wrote."""
@@ -227,8 +227,8 @@ def test_net_attention_chunk_boundaries(eng):
     with Net(eng, cfg) as net:
         net.load(model)
         pos = 0
-        # 252 by prefill, then passes of 1 and 3 tokens over 256 (chunk counts 1 -> 2), a prefill to
-        # 509, passes over 512 (2 -> 4), a prefill to 1020 and passes over 1024 (4 -> the cap of 5)
+        # 252 by prefill, then passes of 1 and 3 tokens over 256 (chunk counts 2 -> 4), a prefill to
+        # 509, passes over 512 (4 -> 8), a prefill to 1020 and passes over 1024 (8 -> the cap of 9)
         plan = [252, 1, 1, 1, 1, 1, 3, 1, 248, 1, 1, 1, 3, 1, 505, 1, 1, 1, 3, 1, 8]
         for n in plan:
             toks = rng.integers(0, cfg.vocab, n)
@@ -238,9 +238,10 @@ def test_net_attention_chunk_boundaries(eng):
 
 
 def test_net_many_attention_chunks(eng):
-    """Decode passes past 2048 positions, where decode attention runs over more than eight chunk
-    workgroups per (head, token): the last chunk to finish merges the others' partials with the
-    general merge (two rounds of loads); up to eight chunks it takes the one-round merge."""
+    """Decode passes past 1024 positions, where decode attention runs over more than eight chunk
+    workgroups of 128 positions per (head, token): the last chunk to finish merges the others'
+    partials with the general merge (two rounds of loads; up to eight chunks it takes the one-round
+    merge), past 2048 positions over the capped chunk count of 18."""
     from hk_amd.net import Net
 
     cfg = Config(dim=128, n_layers=1, n_heads=2, n_kv_heads=1, head_dim=64, ffn_dim=256, vocab=256, max_ctx=2200,
@@ -251,8 +252,9 @@ def test_net_many_attention_chunks(eng):
     with Net(eng, cfg) as net:
         net.load(model)
         pos = 0
-        # 2040 by prefill (eight chunks for the passes up to 2048), then passes over 2048 (nine)
-        for n in [2040, 1, 3, 1, 1, 3, 1, 8, 1, 1]:
+        # 1020 by prefill, passes over 1024 (8 -> 16 chunks), a prefill to 2035, passes over 2048
+        # (16 -> the cap of 18)
+        for n in [1020, 1, 3, 1, 1010, 1, 3, 8, 1, 1, 1]:
             toks = rng.integers(0, cfg.vocab, n)
             net.forward(toks, pos)
             check(net.logits(), cpu.forward(toks, pos), f"many chunks: pass of {n} at {pos}")
