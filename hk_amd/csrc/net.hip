@@ -979,7 +979,8 @@ uint32_t qkvdim(const hkhip_net_config &c) { return qdim(c) + 2 * kvdim(c); }
 // spread over twice the CUs and each workgroup's dependent steps halve, while the chunks' merge
 // (in the same launch) stays one round of loads up to 1024 positions: 1.614 vs 1.645 ms per token
 // on Llama-3-8B shapes, 0.806 vs 0.854 on Qwen3-0.6B shapes at 512-575 positions. Eight took
-// longer still than four (one CU then pulls twice the key and value bytes).
+// longer still than four (one CU then pulls twice the key and value bytes), and one (64 positions
+// per chunk, so past 512 positions the two-round merge) 1.691 / 0.844 ms.
 constexpr uint32_t ATT_DWAVES = 2;
 uint32_t nslices(const hkhip_net_config &c) { return (c.max_ctx + ATT_SLICE - 1) / ATT_SLICE; }
 uint32_t vt_stride(const hkhip_net_config &c) { return (c.max_ctx + 31) / 32 * 32; }
