@@ -48,6 +48,16 @@ class NetTensor(ctypes.Structure):
     _fields_ = [("data", ctypes.c_void_p), ("bytes", ctypes.c_uint64), ("t", ctypes.c_uint8)]
 
 
+class NetOptions(ctypes.Structure):
+    """hkhip_net_options (src/cuda/engine.zig:43-58 Options)."""
+    _fields_ = [(n, ctypes.c_uint32) for n in ("slots", "layers", "n_batch", "attn_merge_max")]
+
+
+class Item(ctypes.Structure):
+    """hkhip_item (src/engine/kv.zig:22-29 Item): {sequence, token, position}."""
+    _fields_ = [("seq", ctypes.c_uint64), ("token", ctypes.c_uint32), ("pos", ctypes.c_uint32)]
+
+
 NET_LAYER_FIELDS = ("attn_norm", "wq", "wk", "wv", "bq", "bk", "bv", "q_norm", "k_norm", "wo", "ffn_norm",
                     "w_gate", "w_up", "w_down")
 
@@ -92,6 +102,18 @@ SIGNATURES = {
     "hkhip_mm_noalloc": (_I, [_P, _MP, _P, _P, _U32, _P, _I]),
     "hkhip_gemm_host": (_I, [_U8, _P, _P, _P, _P, _U64, _U64, _U64]),
     "hkhip_net_create": (_I, [_P, ctypes.POINTER(NetConfig), ctypes.POINTER(_P)]),
+    "hkhip_net_create_opts": (_I, [_P, ctypes.POINTER(NetConfig), ctypes.POINTER(NetOptions), ctypes.POINTER(_P)]),
+    "hkhip_net_forward_items": (_I, [_P, ctypes.POINTER(Item), _U32]),
+    "hkhip_net_forward_partial": (_I, [_P, ctypes.POINTER(Item), _U32, _P]),
+    "hkhip_net_logits_rows": (_I, [_P, _P, _U32, _P]),
+    "hkhip_net_release": (None, [_P, _U64]),
+    "hkhip_net_max_rows": (_U32, [_P]),
+    "hkhip_net_layer_count": (_U32, [_P]),
+    "hkhip_net_is_partial": (_I, [_P]),
+    "hkhip_net_bytes_needed": (_U64, [ctypes.POINTER(NetConfig), ctypes.POINTER(NetOptions), ctypes.POINTER(NetLayer),
+                                      NetTensor, NetTensor, NetTensor]),
+    "hkhip_net_layer_bytes": (_U64, [ctypes.POINTER(NetConfig), ctypes.POINTER(NetLayer)]),
+    "hkhip_net_device_bytes": (_U64, [_P]),
     "hkhip_net_destroy": (None, [_P]),
     "hkhip_net_load_layer": (_I, [_P, _U32, ctypes.POINTER(NetLayer)]),
     "hkhip_net_load_io": (_I, [_P, NetTensor, NetTensor, NetTensor]),

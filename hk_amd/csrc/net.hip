@@ -34,9 +34,9 @@ using namespace hkhip;
 
 namespace {
 
-constexpr uint32_t ATT_SLICE = 64; // positions per attention slice (one step of the kernel)
-constexpr uint32_t MAX_DECODE = 8;
-constexpr uint32_t ATT_MERGE_MAX = 256; // decode attention chunks the fused merge takes (more: attn_combine_kernel)  // tokens of a pass that runs the decode kernels (and a graph)
+constexpr uint32_t ATT_SLICE = 64;      // positions per wave step of the decode attention
+constexpr uint32_t MAX_DECODE = 8;      // tokens of a pass that runs the decode kernels (and a graph)
+constexpr uint32_t ATT_MERGE_MAX = 256; // decode attention chunks the in-launch merge takes (more: attn_combine_kernel)
 
 // ---------------------------------------------------------------------------------------------
 // Kernels
@@ -69,15 +69,17 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ 
 // One wave per (token, head): heads 0..nh-1 are query heads (normalized, rotated, written back),
 // nh..nh+nkv-1 key heads (normalized, rotated, written to the f16 key cache), then nkv value heads
 // (to the f16 value cache, and transposed to [kv head][hd][vt_stride] for the prefill attention).
-// Position of token t: pos0[0] + t. Cache layout [kv head][max_ctx][hd].
+// Token t sits at position pos[t] of the sequence whose caches are slot slot[t]. Cache layout
+// [slot][layer][kv head][max_ctx][hd]; kc / vc / vt point at this layer of slot 0.
 struct RopeArgs {
     float *q;
     const float *k, *v; // rows of the fused q/k/v output: stride sq (q) and skv (k, v) floats per token
     const float *q_norm, *k_norm; // [hd] or null
     const float *inv_freq;        // [rope_dim / 2]
-    __half *kc, *vc;              // this layer's caches
-    __half *vt;                   // this layer's transposed value cache [nkv][hd][vt_stride]
-    const uint32_t *pos0;
+    __half *kc, *vc;              // this layer's caches (slot 0)
+    __half *vt;                   // this layer's transposed value cache [nkv][hd][vt_stride] (slot 0)
+    const uint32_t *pos, *slot;   // per token
+    uint64_t kv_slot, vt_slot;    // halves between slots of kc / vc and of vt
     uint32_t nh, nkv, hd, rope_half, neox, max_ctx, vt_stride, sq, skv;
     uint32_t nheads; // heads this launch covers: nh + nkv (keys), + nkv (values)
     float mscale;    // multiplier of every cos and sin (ops.zig ropeMscale)
@@ -126,15 +128,16 @@ __device__ __forceinline__ void head_norm_rope(float *h, const float *src, const
 __device__ __forceinline__ void rope_kv_block(const RopeArgs &a, uint32_t bx, uint32_t t) {
     const uint32_t w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const uint32_t hh = 4 * bx + w;
-    const uint32_t pos = a.pos0[0] + t;
+    const uint32_t pos = a.pos[t];
+    const uint64_t sl = a.slot[t];
     const uint32_t hd = a.hd;
     if (hh >= a.nheads) return; // past the last head launched (whole wave; no workgroup barriers below)
     const bool isq = hh < a.nh, isk = !isq && hh < a.nh + a.nkv;
     if (!isq && !isk) { // value head: straight to the caches
         const uint32_t g = hh - a.nh - a.nkv;
         const float *src = a.v + uint64_t(t) * a.skv + g * hd;
-        __half *dst = a.vc + (uint64_t(g) * a.max_ctx + pos) * hd;
-        __half *dt = a.vt + uint64_t(g) * hd * a.vt_stride + pos;
+        __half *dst = a.vc + sl * a.kv_slot + (uint64_t(g) * a.max_ctx + pos) * hd;
+        __half *dt = a.vt + sl * a.vt_slot + uint64_t(g) * hd * a.vt_stride + pos;
         for (uint32_t d = lane; d < hd; d += 64) {
             const __half v = __float2half(src[d]);
             dst[d] = v;
@@ -151,7 +154,7 @@ __device__ __forceinline__ void rope_kv_block(const RopeArgs &a, uint32_t bx, ui
         float *dst = a.q + uint64_t(t) * a.sq + g * hd;
         for (uint32_t d = lane; d < hd; d += 64) dst[d] = h[d];
     } else {
-        __half *dst = a.kc + (uint64_t(g) * a.max_ctx + pos) * hd;
+        __half *dst = a.kc + sl * a.kv_slot + (uint64_t(g) * a.max_ctx + pos) * hd;
         for (uint32_t d = lane; d < hd; d += 64) dst[d] = __float2half(h[d]);
     }
 }
@@ -160,19 +163,24 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(RopeArgs a) { rope_kv_bloc
 
 // Value rows of a prefill pass to the f16 caches, 16 tokens of one key/value head per workgroup:
 // the rows go to the value cache as they are and, through an LDS tile, to the transposed cache
-// with consecutive lanes on consecutive positions (decode passes write both in rope_kv_kernel).
-__device__ __forceinline__ void v_cache_block(const float *__restrict__ v, __half *__restrict__ vc,
-                                              __half *__restrict__ vt, const uint32_t *__restrict__ pos0, uint32_t n,
-                                              uint32_t skv, uint32_t hd, uint32_t max_ctx, uint32_t vt_stride,
-                                              uint32_t g, uint32_t ty) {
+// with consecutive lanes on consecutive tokens (consecutive positions within a sequence's run;
+// decode passes write both in rope_kv_kernel).
+__device__ __forceinline__ void v_cache_block(const RopeArgs &a, const float *__restrict__ v, uint32_t g, uint32_t ty) {
     __shared__ __half tile[16][258];
-    const uint32_t t0 = ty * 16, tid = threadIdx.x;
-    const uint32_t nt = n - t0 < 16 ? n - t0 : 16, pos = pos0[0] + t0, kvd = skv; // row stride of v
+    __shared__ uint32_t tpos[16];
+    __shared__ uint64_t tslot[16];
+    const uint32_t t0 = ty * 16, tid = threadIdx.x, hd = a.hd, n = a.ntok;
+    const uint32_t nt = n - t0 < 16 ? n - t0 : 16, kvd = a.skv; // row stride of v
+    if (tid < nt) {
+        tpos[tid] = a.pos[t0 + tid];
+        tslot[tid] = a.slot[t0 + tid];
+    }
+    __syncthreads();
     for (uint32_t i = 4 * tid; i < nt * hd; i += 1024) { // hd is a multiple of 64: four values of one row
         const uint32_t tt = i / hd, d = i % hd;
         const float4 x = *reinterpret_cast<const float4 *>(v + uint64_t(t0 + tt) * kvd + g * hd + d);
         const __half h4[4] = {__float2half(x.x), __float2half(x.y), __float2half(x.z), __float2half(x.w)};
-        __half *dst = vc + (uint64_t(g) * max_ctx + pos + tt) * hd + d;
+        __half *dst = a.vc + tslot[tt] * a.kv_slot + (uint64_t(g) * a.max_ctx + tpos[tt]) * hd + d;
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             dst[k] = h4[k];
@@ -182,7 +190,7 @@ __device__ __forceinline__ void v_cache_block(const float *__restrict__ v, __hal
     __syncthreads();
     for (uint32_t i = tid; i < hd * 16; i += 256) {
         const uint32_t d = i / 16, tt = i % 16;
-        if (tt < nt) vt[(uint64_t(g) * hd + d) * vt_stride + pos + tt] = tile[tt][d];
+        if (tt < nt) a.vt[tslot[tt] * a.vt_slot + (uint64_t(g) * hd + d) * a.vt_stride + tpos[tt]] = tile[tt][d];
     }
 }
 
@@ -193,22 +201,18 @@ __global__ __launch_bounds__(256) void rope_kv_v_kernel(RopeArgs a, const float 
     if (b < nr)
         rope_kv_block(a, b % rx, b / rx);
     else
-        v_cache_block(v, a.vc, a.vt, a.pos0, a.ntok, a.skv, a.hd, a.max_ctx, a.vt_stride, (b - nr) % a.nkv,
-                      (b - nr) / a.nkv);
+        v_cache_block(a, v, (b - nr) % a.nkv, (b - nr) / a.nkv);
 }
 
-// Attention over one slice of the context for one (token, query head): one wave each, four per
-// workgroup. Per step of 64 positions every lane issues its position's key row (lane = position)
-// and its dimensions of all 64 value rows (lane = dimensions [DL*lane, DL*lane + DL)) before any
-// use, so a step costs one memory round trip; then the scores, the online softmax update and the
-// value sums from registers. Writes {max, sum, acc[hd]} per (token, head, slice); a slice past the
-// token's position writes {-inf, 0, 0...}.
+// Decode attention arguments (the kernel below): per (token, query head) the context of the
+// token's own sequence, positions 0..pos[t] of slot slot[t].
 struct AttnArgs {
     const float *q; // stride sq floats per token
-    const __half *kc, *vc;
+    const __half *kc, *vc; // this layer of slot 0
     float *part;
-    const uint32_t *pos0;
-    uint32_t n, nh, nkv, hd, max_ctx, nslice;
+    const uint32_t *pos, *slot;
+    uint64_t kv_slot; // halves between slots
+    uint32_t n, nh, nkv, hd, max_ctx;
     float scale;
     uint32_t sq;
     // Decode only. att: with one chunk per (head, token) the normalized result goes straight here
@@ -249,86 +253,6 @@ template <int DL> struct VRow {
         for (int i = 0; i < (DL > 2 ? 2 : 1); i++) asm volatile("" : "+v"(w[i]));
     }
 };
-
-template <int HD>
-__global__ __launch_bounds__(256) void attn_slice_kernel(AttnArgs a) {
-    constexpr int DL = HD / 64;
-    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const uint32_t item = blockIdx.x * 4 + w; // (token, head, slice), slice fastest
-    __shared__ float qs[4][HD];
-    const bool live = item < a.n * a.nh * a.nslice;
-    const uint32_t sl = item % a.nslice, h = (item / a.nslice) % a.nh, t = item / (a.nslice * a.nh);
-    if (live) {
-        const float *qsrc = a.q + uint64_t(t) * a.sq + h * HD;
-#pragma unroll
-        for (int j = 0; j < DL; j++) qs[w][lane + 64 * j] = qsrc[lane + 64 * j];
-    }
-    __syncthreads();
-    if (!live) return;
-    const uint32_t kvh = h / (a.nh / a.nkv);
-    const uint32_t pos = a.pos0[0] + t;
-    const uint32_t p_begin = sl * ATT_SLICE;
-    const uint32_t p_end = min(p_begin + ATT_SLICE, pos + 1); // exclusive
-    float *out = a.part + (uint64_t(item)) * (HD + 2);
-    const float *qw = qs[w];
-    float m = -INFINITY, l = 0.0f, acc[DL];
-#pragma unroll
-    for (int j = 0; j < DL; j++) acc[j] = 0.0f;
-    const __half *kb = a.kc + uint64_t(kvh) * a.max_ctx * HD;
-    const __half *vb = a.vc + uint64_t(kvh) * a.max_ctx * HD + DL * lane;
-    for (uint32_t p0 = p_begin; p0 < p_end; p0 += 64) {
-        const uint32_t pp = p0 + lane, last = p_end - 1;
-        uint4 kr[HD / 8];
-        const uint4 *krow = reinterpret_cast<const uint4 *>(kb + uint64_t(pp < p_end ? pp : last) * HD);
-#pragma unroll
-        for (int c = 0; c < HD / 8; c++) kr[c] = krow[c];
-        VRow<DL> vr[64];
-#pragma unroll
-        for (int i = 0; i < 64; i++) {
-            const uint32_t pv = p0 + i < p_end ? p0 + i : last;
-            vr[i].load(vb + uint64_t(pv) * HD);
-        }
-#pragma unroll
-        for (int c = 0; c < HD / 8; c++) asm volatile("" : "+v"(kr[c].x), "+v"(kr[c].y), "+v"(kr[c].z), "+v"(kr[c].w));
-#pragma unroll
-        for (int i = 0; i < 64; i++) vr[i].pin();
-        float dot = 0.0f;
-#pragma unroll
-        for (int c = 0; c < HD / 8; c++) {
-            const __half2 *hp = reinterpret_cast<const __half2 *>(&kr[c]);
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const float2 f = __half22float2(hp[e]);
-                dot = fmaf(qw[8 * c + 2 * e], f.x, dot);
-                dot = fmaf(qw[8 * c + 2 * e + 1], f.y, dot);
-            }
-        }
-        const float s = pp < p_end ? dot * a.scale : -INFINITY;
-        float mx = s;
-        for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-        const float mn = fmaxf(m, mx);
-        const float pr = pp < p_end ? expf(s - mn) : 0.0f;
-        float ps = pr;
-        for (int o = 32; o >= 1; o >>= 1) ps += __shfl_xor(ps, o);
-        const float corr = m == -INFINITY ? 0.0f : expf(m - mn);
-        l = l * corr + ps;
-#pragma unroll
-        for (int j = 0; j < DL; j++) acc[j] *= corr;
-#pragma unroll
-        for (int i = 0; i < 64; i++) {
-            const float pi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pr), i)); // 0 past the slice
-#pragma unroll
-            for (int j = 0; j < DL; j++) acc[j] = fmaf(pi, vr[i].get(j), acc[j]);
-        }
-        m = mn;
-    }
-    if (lane == 0) {
-        out[0] = m;
-        out[1] = l;
-    }
-#pragma unroll
-    for (int j = 0; j < DL; j++) out[2 + DL * lane + j] = acc[j];
-}
 
 // Decode attention (passes of up to MAX_DECODE tokens): G workgroups of NWV waves per (query head,
 // token), G set by the context the pass reaches (host side: a power of two, so that every 64-position
@@ -488,8 +412,9 @@ __global__ __launch_bounds__(NWV * 64) void attn_decode_kernel(AttnArgs a) {
     float m = -INFINITY, l = 0.0f, acc[8];
 #pragma unroll
     for (int j = 0; j < 8; j++) acc[j] = 0.0f;
-    const __half *kb = a.kc + uint64_t(kvh) * a.max_ctx * HD;
-    const __half *vb = a.vc + uint64_t(kvh) * a.max_ctx * HD + 8 * vc;
+    const uint64_t sl = a.slot[t];
+    const __half *kb = a.kc + sl * a.kv_slot + uint64_t(kvh) * a.max_ctx * HD;
+    const __half *vb = a.vc + sl * a.kv_slot + uint64_t(kvh) * a.max_ctx * HD + 8 * vc;
     const float *qw = qs[w];
     // The launch gives every 64-position step of the context a wave of its own (G * NWV steps), so
     // a wave has one step, and its loads need not wait for the position: rows are clamped to the
@@ -507,7 +432,7 @@ __global__ __launch_bounds__(NWV * 64) void attn_decode_kernel(AttnArgs a) {
             vv[i] = *reinterpret_cast<const uint4 *>(vb + uint64_t(pv < lastc ? pv : lastc) * HD);
         }
     }
-    const uint32_t pos = a.pos0[0] + t;
+    const uint32_t pos = a.pos[t];
     if (p0 <= pos) {
         const uint32_t p_end = min(p0 + 64, pos + 1);
         // Fused pass, wave holding the new position: its score (dot_new, in the order of the cache
@@ -536,9 +461,9 @@ __global__ __launch_bounds__(NWV * 64) void attn_decode_kernel(AttnArgs a) {
                 }
                 vnew = *reinterpret_cast<const uint4 *>(&kvh16[w][1][8 * vc]);
                 if (h % grp == 0) { // one writer per key/value head
-                    __half *kd = a.r.kc + (uint64_t(kvh) * a.max_ctx + pos) * HD;
-                    __half *vd = a.r.vc + (uint64_t(kvh) * a.max_ctx + pos) * HD;
-                    __half *vtd = a.r.vt + uint64_t(kvh) * HD * a.r.vt_stride + pos;
+                    __half *kd = a.r.kc + sl * a.r.kv_slot + (uint64_t(kvh) * a.max_ctx + pos) * HD;
+                    __half *vd = a.r.vc + sl * a.r.kv_slot + (uint64_t(kvh) * a.max_ctx + pos) * HD;
+                    __half *vtd = a.r.vt + sl * a.r.vt_slot + uint64_t(kvh) * HD * a.r.vt_stride + pos;
 #pragma unroll
                     for (int j = 0; j < HD / 64; j++) {
                         const uint32_t d = lane + 64 * j;
@@ -651,19 +576,22 @@ __global__ __launch_bounds__(NWV * 64) void attn_decode_kernel(AttnArgs a) {
     }
     if (!a.cnt) return; // attn_combine_kernel merges
     // Count the chunk in; the last of (head, token) to arrive merges every chunk's partial with
-    // agent-scope loads. Each wave waits for its stores to complete before the barrier, so the
-    // count follows the whole partial; no workgroup waits for another.
+    // agent-scope loads. Every thread releases its partial stores (agent scope) before the barrier,
+    // the count is an acquire-release read-modify-write, and the merging workgroup acquires before
+    // its loads: the partials happen before the merge by the memory model, not by the hardware's
+    // store order. No workgroup waits for another.
     __shared__ uint32_t last;
     __shared__ float mw[ATT_MERGE_MAX], mred[NWV];
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     __syncthreads();
     if (threadIdx.x == 0) {
         uint32_t *c = a.cnt + uint64_t(t) * a.nh + h;
-        last = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 == gridDim.x ? 1u : 0u;
+        last = __hip_atomic_fetch_add(c, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) + 1 == gridDim.x ? 1u : 0u;
         if (last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     if (!last) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     if (gridDim.x <= 8) {
         // One round of loads: thread d reads every chunk's {max, sum, acc[d]} at once.
         const float *pp = a.part + (uint64_t(t) * a.nh + h) * gridDim.x * (HD + 2);
@@ -718,9 +646,10 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 
 struct AttnPArgs {
     const float *q;
-    const __half *kc, *vt; // this layer's key cache [nkv][max_ctx][hd], value cache transposed [nkv][hd][vt_stride]
+    const __half *kc, *vt; // this layer's key cache [nkv][max_ctx][hd], value cache transposed [nkv][hd][vt_stride], slot 0
     float *att;
-    const uint32_t *pos0;
+    const uint32_t *pos, *slot; // of the run's first token: the run is positions pos[0].. of slot slot[0]
+    uint64_t kv_slot, vt_slot;
     uint32_t n, nh, nkv, max_ctx, vt_stride;
     float scale;
     uint32_t sq; // q row stride (floats per token)
@@ -744,7 +673,8 @@ __global__ __launch_bounds__(NWV * 64, 2) void attn_prefill_kernel(AttnPArgs a) 
     const uint32_t ntile = (a.n + 31) / 32;
     const uint32_t head = item % a.nh, tile = ntile - 1 - item / a.nh; // longest prefixes first
     const uint32_t kvh = head / (a.nh / a.nkv);
-    const uint32_t pos0 = a.pos0[0];
+    const uint32_t pos0 = a.pos[0];
+    const uint64_t sl = a.slot[0];
     const uint32_t t = tile * 32 + j, tc = t < a.n ? t : a.n - 1; // this lane's token (clamped)
     const uint32_t tpos = pos0 + tc;
     const uint32_t pend = pos0 + min(tile * 32 + 32, a.n); // positions [0, pend) are needed
@@ -776,8 +706,8 @@ __global__ __launch_bounds__(NWV * 64, 2) void attn_prefill_kernel(AttnPArgs a) 
 #pragma unroll
     for (int d = 0; d < NDT; d++) acc[d] = v16f{};
     float m = -INFINITY, l = 0.0f;
-    const __half *kb = a.kc + uint64_t(kvh) * a.max_ctx * HD;
-    const __half *vb = a.vt + uint64_t(kvh) * HD * a.vt_stride;
+    const __half *kb = a.kc + sl * a.kv_slot + uint64_t(kvh) * a.max_ctx * HD;
+    const __half *vb = a.vt + sl * a.vt_slot + uint64_t(kvh) * HD * a.vt_stride;
     const uint32_t rj = (j & ~12u) | ((j & 4u) << 1) | ((j & 8u) >> 1); // rho(j)
     // The key rows of the next tile of positions are loaded once this tile's scores are issued,
     // and its value rows once this tile's output products are: each lands while the other half
@@ -933,6 +863,9 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float *__restri
 struct hkhip_net {
     hkhip_engine *eng;
     hkhip_net_config cfg;
+    uint32_t n_dev = 0;   // layers on the device
+    bool partial = false; // only the leading layers (no embedding, final norm or output)
+    uint32_t n_slots = 1, n_batch = 0, max_rows = 64, merge_max = ATT_MERGE_MAX;
     struct Layer {
         // q, k and v rows stacked (one product, one output row per token) when the three share their
         // type; else three products into three regions of the q/k/v buffer.
@@ -945,19 +878,24 @@ struct hkhip_net {
     std::vector<Layer> layers;
     hkhip_mat embd{}, output{};
     float *out_norm = nullptr;
-    // Device buffers ([MAX tokens][...] sized for the largest pass seen).
-    std::vector<void *> owned;
+    // Device buffers the network allocated, with their sizes (pass buffers: [cap tokens][...]).
+    std::vector<std::pair<void *, uint64_t>> owned;
     uint32_t cap = 0; // tokens the pass buffers hold
-    float *x = nullptr, *xb = nullptr, *qkv = nullptr, *att = nullptr,
-          *h = nullptr, *part = nullptr, *logits = nullptr, *inv_freq = nullptr;
+    float *x = nullptr, *xb = nullptr, *qkv = nullptr, *att = nullptr, *h = nullptr, *part = nullptr,
+          *logits = nullptr, *lx = nullptr, *inv_freq = nullptr;
     uint8_t *xq = nullptr;
-    __half *kc = nullptr, *vc = nullptr, *vt = nullptr;
-    uint32_t *io = nullptr, *tok = nullptr, *pos = nullptr; // device {pos, tokens[cap]}
+    __half *kc = nullptr, *vc = nullptr, *vt = nullptr; // [slot][layer][...]
+    uint32_t *io = nullptr, *tok = nullptr, *pos = nullptr, *slot = nullptr; // device [tok | pos | slot][cap]
     uint32_t *att_cnt = nullptr; // [MAX_DECODE][n_heads] decode attention chunk counters (zero between launches)
-    uint32_t *stage = nullptr;                               // pinned host copy of io
+    uint32_t *stage = nullptr;   // pinned host copy of io
+    // The current pass on the host: runs of consecutive positions of one sequence [begin, end).
+    std::vector<std::pair<uint32_t, uint32_t>> runs;
+    std::vector<uint64_t> owner; // sequence of each slot
+    std::vector<uint8_t> used;
     std::map<uint32_t, hipGraphExec_t> graphs;
-    std::map<uint32_t, int> runs; // eager runs per decode shape: token count | attention chunks << 8 (a graph is captured after one)
+    std::map<uint32_t, int> shape_runs; // eager runs per decode shape (a graph is captured after one)
     uint32_t last_n = 0;
+    bool last_hidden = false; // the last pass left full-network hidden states (logits rows can be read)
 };
 
 namespace {
@@ -985,11 +923,52 @@ constexpr uint32_t ATT_DWAVES = 2;
 uint32_t nslices(const hkhip_net_config &c) { return (c.max_ctx + ATT_SLICE - 1) / ATT_SLICE; }
 uint32_t vt_stride(const hkhip_net_config &c) { return (c.max_ctx + 31) / 32 * 32; }
 bool prefill_mfma(const hkhip_net_config &c) { return c.head_dim == 64 || c.head_dim == 128; }
+uint32_t layer_count(const hkhip_net_config &c, const hkhip_net_options &o) {
+    return o.layers == 0 || o.layers >= c.n_layers ? c.n_layers : o.layers;
+}
+uint32_t max_rows_of(const hkhip_net_options &o) { return o.n_batch ? std::min<uint32_t>(o.n_batch, 64) : 64; }
+uint32_t initial_cap(const hkhip_net_options &o) {
+    return std::max(std::max(o.n_batch, MAX_DECODE), max_rows_of(o));
+}
+
+// Device bytes of every buffer of a network (one function for the allocations and the estimate).
+struct NetSizes {
+    uint64_t cache, vtc, logits, inv_freq, part, att_cnt, lx;         // fixed
+    uint64_t x, xb, qkv, att, h, xq, io;                               // for cap tokens
+    uint64_t fixed() const { return 2 * cache + vtc + logits + inv_freq + part + att_cnt + lx; }
+    uint64_t per_cap() const { return x + xb + qkv + att + h + xq + io; }
+};
+NetSizes net_sizes(const hkhip_net_config &c, uint32_t slots, uint32_t n_dev, uint32_t max_rows, uint32_t cap) {
+    NetSizes z{};
+    const uint64_t sl = uint64_t(slots) * n_dev, T = cap;
+    z.cache = sl * c.n_kv_heads * c.max_ctx * c.head_dim * 2;
+    z.vtc = sl * c.n_kv_heads * c.head_dim * vt_stride(c) * 2;
+    z.logits = uint64_t(max_rows) * c.vocab * 4;
+    z.inv_freq = c.rope_dim / 2 * 4 + 4;
+    z.part = uint64_t(MAX_DECODE) * c.n_heads * nslices(c) * (c.head_dim + 2) * 4;
+    z.att_cnt = uint64_t(MAX_DECODE) * c.n_heads * 4;
+    z.lx = uint64_t(max_rows) * c.dim * 4;
+    const uint32_t maxk = std::max(std::max(c.dim, qdim(c)), c.ffn_dim);
+    z.x = T * c.dim * 4;
+    z.xb = T * std::max(c.dim, qdim(c)) * 4;
+    z.qkv = T * qkvdim(c) * 4;
+    z.att = T * qdim(c) * 4;
+    z.h = T * c.ffn_dim * 4;
+    z.xq = hkhip_act_bytes(cap, maxk);
+    z.io = 3 * T * 4;
+    return z;
+}
 
 int dev_alloc(hkhip_net *n, uint64_t bytes, void **p) {
     NET_TRY(hipMalloc(p, bytes ? bytes : 1), "hipMalloc");
-    n->owned.push_back(*p);
+    n->owned.push_back({*p, bytes});
     return HKHIP_OK;
+}
+void dev_free(hkhip_net *n, void *p) {
+    if (!p) return;
+    (void)hipFree(p);
+    for (auto &o : n->owned)
+        if (o.first == p) o = {nullptr, 0};
 }
 
 // An f32 vector of `len` floats to the device (null for an absent optional tensor).
@@ -1044,47 +1023,28 @@ int ensure_cap(hkhip_net *n, uint32_t want) {
     // Freed buffers belong to captured graphs too: drop them.
     for (auto &g : n->graphs) (void)hipGraphExecDestroy(g.second);
     n->graphs.clear();
-    n->runs.clear();
-    float **bufs[] = {&n->x, &n->xb, &n->qkv, &n->att, &n->h, &n->part,
-                      reinterpret_cast<float **>(&n->io)};
+    n->shape_runs.clear();
     if (n->stage) {
         (void)hipHostFree(n->stage);
         n->stage = nullptr;
     }
-    for (float **b : bufs) {
-        if (*b) {
-            (void)hipFree(*b);
-            for (auto &o : n->owned)
-                if (o == *b) o = nullptr;
-            *b = nullptr;
-        }
+    void **bufs[] = {(void **)&n->x, (void **)&n->xb, (void **)&n->qkv, (void **)&n->att, (void **)&n->h,
+                     (void **)&n->xq, (void **)&n->io};
+    for (void **b : bufs) {
+        dev_free(n, *b);
+        *b = nullptr;
     }
-    if (n->xq) {
-        (void)hipFree(n->xq);
-        for (auto &o : n->owned)
-            if (o == n->xq) o = nullptr;
-        n->xq = nullptr;
-    }
-    const uint64_t T = want;
-    const uint32_t maxk = std::max(std::max(c.dim, qdim(c)), c.ffn_dim);
+    const NetSizes z = net_sizes(c, n->n_slots, n->n_dev, n->max_rows, want);
     int rc;
-    if ((rc = dev_alloc(n, T * c.dim * 4, (void **)&n->x)) || (rc = dev_alloc(n, T * std::max(c.dim, qdim(c)) * 4, (void **)&n->xb)) ||
-        (rc = dev_alloc(n, T * qkvdim(c) * 4, (void **)&n->qkv)) || (rc = dev_alloc(n, T * qdim(c) * 4, (void **)&n->att)) ||
-        (rc = dev_alloc(n, T * c.ffn_dim * 4, (void **)&n->h)) ||
-        (rc = dev_alloc(n, (prefill_mfma(c) ? MAX_DECODE : std::max<uint64_t>(T, MAX_DECODE)) * c.n_heads * nslices(c) * (c.head_dim + 2) * 4,
-                        (void **)&n->part)) ||
-        (rc = dev_alloc(n, hkhip_act_bytes(want, maxk), (void **)&n->xq)) ||
-        (rc = dev_alloc(n, (T + 1) * 4, (void **)&n->io)))
+    if ((rc = dev_alloc(n, z.x, (void **)&n->x)) || (rc = dev_alloc(n, z.xb, (void **)&n->xb)) ||
+        (rc = dev_alloc(n, z.qkv, (void **)&n->qkv)) || (rc = dev_alloc(n, z.att, (void **)&n->att)) ||
+        (rc = dev_alloc(n, z.h, (void **)&n->h)) || (rc = dev_alloc(n, z.xq, (void **)&n->xq)) ||
+        (rc = dev_alloc(n, z.io, (void **)&n->io)))
         return rc;
-    n->pos = n->io;
-    n->tok = n->io + 1;
-    if (!n->att_cnt) {
-        const uint64_t cb = uint64_t(MAX_DECODE) * c.n_heads * 4;
-        if ((rc = dev_alloc(n, cb, (void **)&n->att_cnt))) return rc;
-        NET_TRY(hipMemset(n->att_cnt, 0, cb), "attention counters");
-        NET_TRY(hipDeviceSynchronize(), "attention counters");
-    }
-    NET_TRY(hipHostMalloc(reinterpret_cast<void **>(&n->stage), (T + 1) * 4, hipHostMallocDefault), "hipHostMalloc");
+    n->tok = n->io;
+    n->pos = n->io + want;
+    n->slot = n->io + 2 * uint64_t(want);
+    NET_TRY(hipHostMalloc(reinterpret_cast<void **>(&n->stage), z.io, hipHostMallocDefault), "hipHostMalloc");
     n->cap = want;
     return HKHIP_OK;
 }
@@ -1097,7 +1057,6 @@ int gemms(hkhip_net *net, uint32_t n, const hkhip_mat *mats, uint32_t nparts, fl
         rc = hkhip_mm(net->eng, &mats[i], net->xq, ys[i], n, biases ? biases[i] : nullptr, mode);
     return rc;
 }
-
 // The products of one pass. xin: f32 input [n][cols]; norm: fused RMS norm weights or null.
 // Whether a product of n tokens runs quantizer + hkhip_mm (GEMM, or the small-batch MFMA kernel
 // for the formats that have it) rather than the decode kernels on the f32 input: the decode
@@ -1156,16 +1115,52 @@ int product(hkhip_net *net, uint32_t n, const hkhip_mat *mats, uint32_t nparts, 
     return rc ? rc : gemms(net, n, mats, nparts, ys, biases, mode);
 }
 
-// gb: decode attention chunks per (head, token) (passes of up to MAX_DECODE tokens).
-int run_pass(hkhip_net *net, uint32_t n, uint32_t gb) {
+// Decode attention over tokens [t0, t0 + nt) of the pass (nt <= MAX_DECODE), gb chunks per
+// (head, token). fused: a one-token pass whose attention kernel also does the head norms, the
+// rotation and the cache writes (ra's fields).
+int decode_attention(hkhip_net *net, const RopeArgs &ra, const __half *kc, const __half *vc, uint32_t t0, uint32_t nt,
+                     uint32_t gb, bool fused) {
+    const hkhip_net_config &c = net->cfg;
+    hipStream_t s = net->eng->cur;
+    AttnArgs aa{ra.q + uint64_t(t0) * ra.sq, kc, vc, net->part, net->pos + t0, net->slot + t0, ra.kv_slot, nt,
+                c.n_heads, c.n_kv_heads, c.head_dim, c.max_ctx, 1.0f / sqrtf(float(c.head_dim)), ra.sq};
+    float *att = net->att + uint64_t(t0) * qdim(c);
+    aa.att = gb == 1 ? att : nullptr;
+    aa.fused = fused ? 1 : 0;
+    aa.r = ra;
+    const bool merge_in = gb > 1 && gb <= net->merge_max;
+    aa.cnt = merge_in ? net->att_cnt : nullptr;
+    aa.merge_out = att;
+    const dim3 dg(gb, c.n_heads, nt);
+    if (c.head_dim == 64)
+        hipLaunchKernelGGL((attn_decode_kernel<64, ATT_DWAVES>), dg, dim3(64 * ATT_DWAVES), 0, s, aa);
+    else if (c.head_dim == 128)
+        hipLaunchKernelGGL((attn_decode_kernel<128, ATT_DWAVES>), dg, dim3(64 * ATT_DWAVES), 0, s, aa);
+    else
+        hipLaunchKernelGGL((attn_decode_kernel<256, ATT_DWAVES>), dg, dim3(64 * ATT_DWAVES), 0, s, aa);
+    NET_TRY(hipGetLastError(), "decode attention");
+    if (gb > 1 && !merge_in) {
+        hipLaunchKernelGGL(attn_combine_kernel, dim3(c.n_heads, nt), dim3(std::min(256u, std::max(64u, (c.head_dim + 63) / 64 * 64))),
+                           gb * 4, s, net->part, att, c.n_heads, c.head_dim, gb);
+        NET_TRY(hipGetLastError(), "decode attention combine");
+    }
+    return HKHIP_OK;
+}
+
+// One pass over the device layers for the n tokens whose tokens / positions / slots are in net->io
+// (and, for a partial network, whose hidden states are in net->x). gb: decode attention chunks per
+// (head, token). lg: also the logits of the last token into net->logits.
+int run_pass(hkhip_net *net, uint32_t n, uint32_t gb, bool lg) {
     const hkhip_net_config &c = net->cfg;
     hkhip_engine *eng = net->eng;
     hipStream_t s = eng->cur;
-    const uint32_t ns = nslices(c);
     int rc;
-    NET_TRY(launch_dequant_gather(net->embd.t, reinterpret_cast<const uint8_t *>(net->embd.mem), net->embd.rows, c.dim,
-                                  net->tok, n, net->x, s), "embedding");
-    for (uint32_t li = 0; li < c.n_layers; li++) {
+    if (!net->partial)
+        NET_TRY(launch_dequant_gather(net->embd.t, reinterpret_cast<const uint8_t *>(net->embd.mem), net->embd.rows,
+                                      c.dim, net->tok, n, net->x, s), "embedding");
+    const uint64_t cache_layer = uint64_t(c.n_kv_heads) * c.max_ctx * c.head_dim;
+    const uint64_t vt_layer = uint64_t(c.n_kv_heads) * c.head_dim * vt_stride(c);
+    for (uint32_t li = 0; li < net->n_dev; li++) {
         const hkhip_net::Layer &L = net->layers[li];
         {
             if (L.stacked) {
@@ -1184,16 +1179,17 @@ int run_pass(hkhip_net *net, uint32_t n, uint32_t gb) {
                 }
             }
         }
-        const uint64_t cache_layer = uint64_t(c.n_kv_heads) * c.max_ctx * c.head_dim;
-        const uint64_t vt_layer = uint64_t(c.n_kv_heads) * c.head_dim * vt_stride(c);
         // Rows of q, k, v: stride S (stacked) or their own regions of the buffer (qd, kvd).
         float *const q = net->qkv;
         float *const k = L.stacked ? q + qdim(c) : q + uint64_t(net->cap) * qdim(c);
         float *const v = L.stacked ? k + kvdim(c) : k + uint64_t(net->cap) * kvdim(c);
         const uint32_t S = L.stacked ? qkvdim(c) : qdim(c), SKV = L.stacked ? qkvdim(c) : kvdim(c);
-        RopeArgs ra{q, k, v, L.q_norm, L.k_norm, net->inv_freq, net->kc + li * cache_layer,
-                    net->vc + li * cache_layer, net->vt + li * vt_layer, net->pos, c.n_heads, c.n_kv_heads, c.head_dim,
-                    c.rope_dim / 2, c.rope_neox, c.max_ctx, vt_stride(c), S, SKV, 0, c.rope_mscale, c.rms_eps};
+        __half *const kc = net->kc + li * cache_layer, *const vc = net->vc + li * cache_layer;
+        __half *const vtl = net->vt + li * vt_layer;
+        RopeArgs ra{q, k, v, L.q_norm, L.k_norm, net->inv_freq, kc, vc, vtl, net->pos, net->slot,
+                    uint64_t(net->n_dev) * cache_layer, uint64_t(net->n_dev) * vt_layer, c.n_heads, c.n_kv_heads,
+                    c.head_dim, c.rope_dim / 2, c.rope_neox, c.max_ctx, vt_stride(c), S, SKV, 0, c.rope_mscale,
+                    c.rms_eps};
         // Prefill passes write the value heads with v_cache_block (coalesced transposed writes);
         // one-token passes do all of it in the attention kernel.
         const bool vsep = n > MAX_DECODE, fused = n == 1;
@@ -1207,51 +1203,30 @@ int run_pass(hkhip_net *net, uint32_t n, uint32_t gb) {
             hipLaunchKernelGGL(rope_kv_kernel, dim3((ra.nheads + 3) / 4, n), dim3(256), 0, s, ra);
             NET_TRY(hipGetLastError(), "rope / kv write");
         }
-        if (n > MAX_DECODE && prefill_mfma(c)) {
-            AttnPArgs pa{q, net->kc + li * cache_layer, net->vt + li * vt_layer, net->att, net->pos, n, c.n_heads,
-                         c.n_kv_heads, c.max_ctx, vt_stride(c), 1.0f / sqrtf(float(c.head_dim)), S};
-            const dim3 pg((n + 31) / 32 * c.n_heads);
-            // Four waves: eight per workgroup (two per SIMD, the key tiles split eight ways) measured
-            // 21.3 vs 18.4 us per Llama-3-8B layer and 15.2 vs 16.4 us per Qwen3-0.6B layer.
-            const hipError_t ae = c.head_dim == 64 ? launch_attn_prefill<64, 4>(pg, pa, s) : launch_attn_prefill<128, 4>(pg, pa, s);
-            NET_TRY(ae, "prefill attention");
-        } else if (n <= MAX_DECODE) {
-            AttnArgs aa{q, net->kc + li * cache_layer, net->vc + li * cache_layer, nullptr, net->pos, n, c.n_heads,
-                        c.n_kv_heads, c.head_dim, c.max_ctx, 0, 1.0f / sqrtf(float(c.head_dim)), S};
-            aa.part = net->part;
-            aa.att = gb == 1 ? net->att : nullptr;
-            aa.fused = fused ? 1 : 0;
-            aa.r = ra;
-            const bool merge_in = gb > 1 && gb <= ATT_MERGE_MAX;
-            aa.cnt = merge_in ? net->att_cnt : nullptr;
-            aa.merge_out = net->att;
-            const dim3 dg(gb, c.n_heads, n);
-            if (c.head_dim == 64)
-                hipLaunchKernelGGL((attn_decode_kernel<64, ATT_DWAVES>), dg, dim3(64 * ATT_DWAVES), 0, s, aa);
-            else if (c.head_dim == 128)
-                hipLaunchKernelGGL((attn_decode_kernel<128, ATT_DWAVES>), dg, dim3(64 * ATT_DWAVES), 0, s, aa);
-            else
-                hipLaunchKernelGGL((attn_decode_kernel<256, ATT_DWAVES>), dg, dim3(64 * ATT_DWAVES), 0, s, aa);
-            NET_TRY(hipGetLastError(), "decode attention");
-            if (gb > 1 && !merge_in) {
-                hipLaunchKernelGGL(attn_combine_kernel, dim3(c.n_heads, n), dim3(std::min(256u, std::max(64u, (c.head_dim + 63) / 64 * 64))),
-                                   gb * 4, s, net->part, net->att, c.n_heads, c.head_dim, gb);
-                NET_TRY(hipGetLastError(), "decode attention combine");
-            }
+        if (n <= MAX_DECODE) {
+            if ((rc = decode_attention(net, ra, kc, vc, 0, n, gb, fused))) return rc;
         } else {
-            AttnArgs aa{q, net->kc + li * cache_layer, net->vc + li * cache_layer, net->part, net->pos, n, c.n_heads,
-                        c.n_kv_heads, c.head_dim, c.max_ctx, ns, 1.0f / sqrtf(float(c.head_dim)), S};
-            const dim3 ag((n * c.n_heads * ns + 3) / 4), ab(256);
-            switch (c.head_dim) {
-            case 64: hipLaunchKernelGGL(attn_slice_kernel<64>, ag, ab, 0, s, aa); break;
-            case 128: hipLaunchKernelGGL(attn_slice_kernel<128>, ag, ab, 0, s, aa); break;
-            case 256: hipLaunchKernelGGL(attn_slice_kernel<256>, ag, ab, 0, s, aa); break;
-            default: return set_error(HKHIP_E_UNSUPPORTED_SHAPE, "head_dim %u", c.head_dim);
+            // Each sequence's run of consecutive positions: longer than a decode pass on the MFMA
+            // prefill kernel, else (and for head dims it does not take) on the decode kernel, up to
+            // MAX_DECODE tokens per launch.
+            for (const auto &r : net->runs) {
+                const uint32_t len = r.second - r.first;
+                if (len > MAX_DECODE && prefill_mfma(c)) {
+                    AttnPArgs pa{q + uint64_t(r.first) * S, kc, vtl, net->att + uint64_t(r.first) * qdim(c),
+                                 net->pos + r.first, net->slot + r.first, ra.kv_slot, ra.vt_slot, len, c.n_heads,
+                                 c.n_kv_heads, c.max_ctx, vt_stride(c), 1.0f / sqrtf(float(c.head_dim)), S};
+                    const dim3 pg((len + 31) / 32 * c.n_heads);
+                    // Four waves: eight per workgroup (two per SIMD, the key tiles split eight ways)
+                    // measured 21.3 vs 18.4 us per Llama-3-8B layer and 15.2 vs 16.4 us per Qwen3-0.6B layer.
+                    const hipError_t ae = c.head_dim == 64 ? launch_attn_prefill<64, 4>(pg, pa, s)
+                                                           : launch_attn_prefill<128, 4>(pg, pa, s);
+                    NET_TRY(ae, "prefill attention");
+                } else {
+                    for (uint32_t t0 = r.first; t0 < r.second; t0 += MAX_DECODE)
+                        if ((rc = decode_attention(net, ra, kc, vc, t0, std::min(MAX_DECODE, r.second - t0), gb, false)))
+                            return rc;
+                }
             }
-            NET_TRY(hipGetLastError(), "attention");
-            hipLaunchKernelGGL(attn_combine_kernel, dim3(c.n_heads, n), dim3(std::min(256u, std::max(64u, (c.head_dim + 63) / 64 * 64))), ns * 4, s, net->part, net->att, c.n_heads,
-                               c.head_dim, ns);
-            NET_TRY(hipGetLastError(), "attention combine");
         }
         {
             float *const ys[1] = {net->x};
@@ -1266,19 +1241,182 @@ int run_pass(hkhip_net *net, uint32_t n, uint32_t gb) {
             if ((rc = product(net, n, &L.wd, 1, net->h, nullptr, ys, nullptr, HKHIP_ACCUMULATE))) return rc;
         }
     }
+    if (!lg) return HKHIP_OK;
     // Logits of the last token (cpu_backend.zig:324-331 logitsFor).
     float *const ys[1] = {net->logits};
     return product(net, 1, &net->output, 1, net->x + uint64_t(n - 1) * c.dim, net->out_norm, ys, nullptr, HKHIP_STORE);
+}
+
+// Checks a pass's items, assigns slots (engine.zig:556-568 slotFor) and stages tokens, positions
+// and slots in net->io; fills net->runs. Returns the largest position.
+int stage_items(hkhip_net *net, const hkhip_item *items, uint32_t n, uint32_t *max_pos) {
+    const hkhip_net_config &c = net->cfg;
+    if (net->n_batch && n > net->n_batch) return set_error(HKHIP_E_BAD_ARGUMENT, "%u items: n_batch is %u", n, net->n_batch);
+    for (uint32_t i = 0; i < n; i++) {
+        if (items[i].pos >= c.max_ctx)
+            return set_error(HKHIP_E_CONTEXT_FULL, "item %u: position %u, max_ctx %u", i, items[i].pos, c.max_ctx);
+        if (!net->partial && items[i].token >= c.vocab)
+            return set_error(HKHIP_E_BAD_ARGUMENT, "item %u: token %u >= vocab %u", i, items[i].token, c.vocab);
+    }
+    // Slots: the sequence's own, else a free one; positions of a sequence increase through the pass.
+    std::vector<uint32_t> sl(n);
+    std::vector<int64_t> last(net->n_slots, -1);
+    std::vector<uint8_t> used = net->used;
+    std::vector<uint64_t> owner = net->owner;
+    for (uint32_t i = 0; i < n; i++) {
+        uint32_t s = UINT32_MAX;
+        for (uint32_t j = 0; j < net->n_slots && s == UINT32_MAX; j++)
+            if (used[j] && owner[j] == items[i].seq) s = j;
+        for (uint32_t j = 0; j < net->n_slots && s == UINT32_MAX; j++)
+            if (!used[j]) {
+                used[j] = 1;
+                owner[j] = items[i].seq;
+                s = j;
+            }
+        if (s == UINT32_MAX)
+            return set_error(HKHIP_E_NO_SLOT, "item %u: all %u cache slots are held by other sequences", i, net->n_slots);
+        if (int64_t(items[i].pos) <= last[s])
+            return set_error(HKHIP_E_BAD_ARGUMENT, "item %u: position %u of sequence %llu after position %lld", i,
+                             items[i].pos, (unsigned long long)items[i].seq, (long long)last[s]);
+        last[s] = items[i].pos;
+        sl[i] = s;
+    }
+    int rc;
+    if ((rc = ensure_cap(net, n))) return rc;
+    net->used = used;
+    net->owner = owner;
+    uint32_t mp = 0;
+    net->runs.clear();
+    for (uint32_t i = 0; i < n; i++) {
+        net->stage[i] = items[i].token;
+        net->stage[net->cap + i] = items[i].pos;
+        net->stage[2 * net->cap + i] = sl[i];
+        mp = std::max(mp, items[i].pos);
+        if (i && sl[i] == sl[i - 1] && items[i].pos == items[i - 1].pos + 1)
+            net->runs.back().second = i + 1;
+        else
+            net->runs.push_back({i, i + 1});
+    }
+    *max_pos = mp;
+    NET_TRY(hipMemcpyAsync(net->io, net->stage, uint64_t(3) * net->cap * 4, hipMemcpyHostToDevice, net->eng->cur),
+            "items");
+    return HKHIP_OK;
+}
+
+int check_loaded(const hkhip_net *net) {
+    if (!net->partial && (!net->embd.mem || !net->output.mem))
+        return set_error(HKHIP_E_BAD_ARGUMENT, "tok_embd / output not loaded");
+    for (const auto &L : net->layers)
+        if (!L.loaded) return set_error(HKHIP_E_BAD_ARGUMENT, "a layer is not loaded");
+    return HKHIP_OK;
+}
+
+// A pass over n staged items (hidden states already in net->x for a partial network); the pass is
+// done when this returns (the next call reuses the pinned staging buffer).
+int forward_staged(hkhip_net *net, uint32_t n, uint32_t max_pos, bool lg) {
+    const hkhip_net_config &c = net->cfg;
+    hipStream_t s = net->eng->cur;
+    int rc;
+    // Decode attention chunks: a power of two covering positions 0..max_pos (ATT_DWAVES waves of 64
+    // positions each), so that short contexts skip the merge; one graph per (size, chunks).
+    const uint32_t dw = ATT_DWAVES, gmax = (nslices(c) + dw - 1) / dw, need = (max_pos + 64 * dw) / (64 * dw);
+    uint32_t gb = 1;
+    while (gb < need) gb <<= 1;
+    gb = std::min(gb, gmax);
+    if (n > MAX_DECODE) { // prefill: run directly
+        if ((rc = run_pass(net, n, gb, lg))) return rc;
+        NET_TRY(hipStreamSynchronize(s), "prefill pass");
+        return HKHIP_OK;
+    }
+    const uint32_t key = n | (gb << 8) | (lg ? 1u << 31 : 0u);
+    auto it = net->graphs.find(key);
+    if (it != net->graphs.end()) {
+        NET_TRY(hipGraphLaunch(it->second, s), "graph launch");
+    } else if (net->shape_runs[key]++ == 0) {
+        if ((rc = run_pass(net, n, gb, lg))) return rc; // first pass of this shape: eager (fills the launch caches)
+    } else {
+        hipGraph_t g = nullptr;
+        NET_TRY(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "begin capture");
+        rc = run_pass(net, n, gb, lg);
+        const hipError_t e = hipStreamEndCapture(s, &g);
+        if (rc) {
+            if (g) (void)hipGraphDestroy(g);
+            return rc;
+        }
+        NET_TRY(e, "end capture");
+        hipGraphExec_t ex = nullptr;
+        const hipError_t ei = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        NET_TRY(ei, "graph instantiate");
+        net->graphs[key] = ex;
+        NET_TRY(hipGraphLaunch(ex, s), "graph launch");
+    }
+    NET_TRY(hipStreamSynchronize(s), "pass");
+    return HKHIP_OK;
+}
+
+int forward_items(hkhip_net *net, const hkhip_item *items, uint32_t n, bool lg) {
+    if (!net || (n && !items)) return set_error(HKHIP_E_BAD_ARGUMENT, "null argument");
+    if (net->partial) return set_error(HKHIP_E_PARTIAL, "a partial network runs hkhip_net_forward_partial");
+    if (n == 0) return HKHIP_OK;
+    int rc;
+    if ((rc = check_loaded(net))) return rc;
+    if (hipSetDevice(net->eng->device) != hipSuccess) return set_error(HKHIP_E_DEVICE_FAILED, "hipSetDevice");
+    uint32_t max_pos = 0;
+    net->last_n = 0;
+    net->last_hidden = false;
+    if ((rc = stage_items(net, items, n, &max_pos)) || (rc = forward_staged(net, n, max_pos, lg))) return rc;
+    net->last_n = n;
+    net->last_hidden = true;
+    return HKHIP_OK;
+}
+
+// Device bytes of one layer's tensors as the network holds them (stacked q/k/v or three matrices,
+// interleaved gate/up, f32 vectors, the stacked bias); 0 when a matrix type has no kernel.
+uint64_t layer_dev_bytes(const hkhip_net_config &c, const hkhip_net_layer &l) {
+    const uint32_t qd = qdim(c), kvd = kvdim(c);
+    auto mat = [&](uint8_t t, uint32_t rows, uint32_t cols) -> uint64_t {
+        if (!block_elems(t) || cols % block_elems(t)) return 0;
+        return weight_layout(t, rows, cols).total;
+    };
+    uint64_t total = 2 * uint64_t(c.dim) * 4;
+    if (l.q_norm.data) total += uint64_t(c.head_dim) * 4;
+    if (l.k_norm.data) total += uint64_t(c.head_dim) * 4;
+    if (l.bq.data || l.bk.data || l.bv.data) total += uint64_t(qd + 2 * kvd) * 4;
+    uint64_t m[4];
+    if (l.wq.t == l.wk.t && l.wq.t == l.wv.t) {
+        m[0] = mat(l.wq.t, qd + 2 * kvd, c.dim);
+        if (!m[0]) return 0;
+        total += m[0];
+    } else {
+        m[0] = mat(l.wq.t, qd, c.dim);
+        m[1] = mat(l.wk.t, kvd, c.dim);
+        m[2] = mat(l.wv.t, kvd, c.dim);
+        if (!m[0] || !m[1] || !m[2]) return 0;
+        total += m[0] + m[1] + m[2];
+    }
+    m[0] = mat(l.wo.t, c.dim, qd);
+    m[1] = mat(l.w_gate.t, 2 * c.ffn_dim, c.dim);
+    m[2] = mat(l.w_down.t, c.dim, c.ffn_dim);
+    if (!m[0] || !m[1] || !m[2]) return 0;
+    return total + m[0] + m[1] + m[2];
+}
+
+bool config_ok(const hkhip_net_config &c) {
+    return c.dim && c.n_layers && c.n_heads && c.n_kv_heads && !(c.n_heads % c.n_kv_heads) && c.ffn_dim && c.vocab &&
+           c.max_ctx && (c.head_dim == 64 || c.head_dim == 128 || c.head_dim == 256) && !(c.rope_dim % 2) &&
+           c.rope_dim <= c.head_dim;
 }
 
 } // namespace
 
 extern "C" {
 
-int hkhip_net_create(hkhip_engine *eng, const hkhip_net_config *cfg, hkhip_net **out) {
+int hkhip_net_create_opts(hkhip_engine *eng, const hkhip_net_config *cfg, const hkhip_net_options *opts, hkhip_net **out) {
     if (!eng || !cfg || !out) return set_error(HKHIP_E_BAD_ARGUMENT, "null argument");
     *out = nullptr;
     const hkhip_net_config &c = *cfg;
+    const hkhip_net_options o = opts ? *opts : hkhip_net_options{};
     if (!c.dim || !c.n_layers || !c.n_heads || !c.n_kv_heads || c.n_heads % c.n_kv_heads || !c.ffn_dim || !c.vocab ||
         !c.max_ctx)
         return set_error(HKHIP_E_BAD_ARGUMENT, "bad network shape");
@@ -1289,21 +1427,30 @@ int hkhip_net_create(hkhip_engine *eng, const hkhip_net_config *cfg, hkhip_net *
     hkhip_net *n = new hkhip_net();
     n->eng = eng;
     n->cfg = c;
-    n->layers.resize(c.n_layers);
+    n->n_dev = layer_count(c, o);
+    n->partial = n->n_dev < c.n_layers;
+    n->n_slots = o.slots ? o.slots : 1;
+    n->n_batch = o.n_batch;
+    n->max_rows = max_rows_of(o);
+    n->merge_max = o.attn_merge_max ? std::min(o.attn_merge_max, ATT_MERGE_MAX) : ATT_MERGE_MAX;
+    n->layers.resize(n->n_dev);
+    n->owner.assign(n->n_slots, 0);
+    n->used.assign(n->n_slots, 0);
     int rc = HKHIP_OK;
-    const uint64_t cache = uint64_t(c.n_layers) * c.n_kv_heads * c.max_ctx * c.head_dim * 2;
-    const uint64_t vtc = uint64_t(c.n_layers) * c.n_kv_heads * c.head_dim * vt_stride(c) * 2;
-    if ((rc = dev_alloc(n, cache, (void **)&n->kc)) || (rc = dev_alloc(n, cache, (void **)&n->vc)) ||
-        (rc = dev_alloc(n, vtc, (void **)&n->vt)) ||
-        (rc = dev_alloc(n, uint64_t(c.vocab) * 4, (void **)&n->logits)) ||
-        (rc = dev_alloc(n, c.rope_dim / 2 * 4 + 4, (void **)&n->inv_freq)) || (rc = ensure_cap(n, MAX_DECODE))) {
+    const NetSizes z = net_sizes(c, n->n_slots, n->n_dev, n->max_rows, 0);
+    if ((rc = dev_alloc(n, z.cache, (void **)&n->kc)) || (rc = dev_alloc(n, z.cache, (void **)&n->vc)) ||
+        (rc = dev_alloc(n, z.vtc, (void **)&n->vt)) || (rc = dev_alloc(n, z.logits, (void **)&n->logits)) ||
+        (rc = dev_alloc(n, z.inv_freq, (void **)&n->inv_freq)) || (rc = dev_alloc(n, z.part, (void **)&n->part)) ||
+        (rc = dev_alloc(n, z.att_cnt, (void **)&n->att_cnt)) || (rc = dev_alloc(n, z.lx, (void **)&n->lx)) ||
+        (rc = ensure_cap(n, initial_cap(o)))) {
         hkhip_net_destroy(n);
         return rc;
     }
-    // Positions a pass has not written yet are read (and weighted by 0) by the prefill attention:
-    // they must hold finite values.
-    if (hipMemset(n->kc, 0, cache) != hipSuccess || hipMemset(n->vc, 0, cache) != hipSuccess ||
-        hipMemset(n->vt, 0, vtc) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+    // Positions a pass has not written yet are read (and weighted by 0) by the attention kernels:
+    // they must hold finite values. The chunk counters start at zero.
+    if (hipMemset(n->kc, 0, z.cache) != hipSuccess || hipMemset(n->vc, 0, z.cache) != hipSuccess ||
+        hipMemset(n->vt, 0, z.vtc) != hipSuccess || hipMemset(n->att_cnt, 0, z.att_cnt) != hipSuccess ||
+        hipDeviceSynchronize() != hipSuccess) {
         hkhip_net_destroy(n);
         return set_error(HKHIP_E_DEVICE_FAILED, "clearing the caches");
     }
@@ -1327,6 +1474,10 @@ int hkhip_net_create(hkhip_engine *eng, const hkhip_net_config *cfg, hkhip_net *
     return HKHIP_OK;
 }
 
+int hkhip_net_create(hkhip_engine *eng, const hkhip_net_config *cfg, hkhip_net **out) {
+    return hkhip_net_create_opts(eng, cfg, nullptr, out);
+}
+
 void hkhip_net_destroy(hkhip_net *net) {
     if (!net) return;
     (void)hipSetDevice(net->eng->device);
@@ -1338,8 +1489,8 @@ void hkhip_net_destroy(hkhip_net *net) {
     }
     hkhip_free(net->eng, &net->embd);
     hkhip_free(net->eng, &net->output);
-    for (void *p : net->owned)
-        if (p) (void)hipFree(p);
+    for (auto &p : net->owned)
+        if (p.first) (void)hipFree(p.first);
     if (net->stage) (void)hipHostFree(net->stage);
     delete net;
 }
@@ -1347,7 +1498,8 @@ void hkhip_net_destroy(hkhip_net *net) {
 int hkhip_net_load_layer(hkhip_net *net, uint32_t li, const hkhip_net_layer *l) {
     if (!net || !l) return set_error(HKHIP_E_BAD_ARGUMENT, "null argument");
     const hkhip_net_config &c = net->cfg;
-    if (li >= c.n_layers) return set_error(HKHIP_E_BAD_ARGUMENT, "layer %u of %u", li, c.n_layers);
+    if (li >= net->n_dev)
+        return set_error(HKHIP_E_BAD_ARGUMENT, "layer %u: the network holds layers 0..%u", li, net->n_dev - 1);
     hkhip_net::Layer &L = net->layers[li];
     if (L.loaded) return set_error(HKHIP_E_BAD_ARGUMENT, "layer %u is already loaded", li);
     const uint32_t qd = qdim(c), kvd = kvdim(c);
@@ -1405,7 +1557,9 @@ int hkhip_net_load_layer(hkhip_net *net, uint32_t li, const hkhip_net_layer *l) 
 
 int hkhip_net_load_io(hkhip_net *net, hkhip_net_tensor tok_embd, hkhip_net_tensor out_norm, hkhip_net_tensor output) {
     if (!net) return set_error(HKHIP_E_BAD_ARGUMENT, "null network");
+    if (net->partial) return set_error(HKHIP_E_PARTIAL, "a partial network has no embedding or output");
     const hkhip_net_config &c = net->cfg;
+    if (net->embd.mem || net->output.mem) return set_error(HKHIP_E_BAD_ARGUMENT, "tok_embd / output are already loaded");
     int rc;
     if ((rc = load_mat(net, tok_embd, c.vocab, c.dim, &net->embd, "tok_embd")) ||
         (rc = load_vec(net, out_norm, c.dim, false, &net->out_norm, "out_norm")) ||
@@ -1414,76 +1568,126 @@ int hkhip_net_load_io(hkhip_net *net, hkhip_net_tensor tok_embd, hkhip_net_tenso
     return HKHIP_OK;
 }
 
-int hkhip_net_forward(hkhip_net *net, const uint32_t *tokens, uint32_t n, uint32_t pos0) {
-    if (!net || (n && !tokens)) return set_error(HKHIP_E_BAD_ARGUMENT, "null argument");
-    const hkhip_net_config &c = net->cfg;
+int hkhip_net_forward_items(hkhip_net *net, const hkhip_item *items, uint32_t n) {
+    return forward_items(net, items, n, false);
+}
+
+int hkhip_net_forward_partial(hkhip_net *net, const hkhip_item *items, uint32_t n, float *hidden_host) {
+    if (!net || (n && (!items || !hidden_host))) return set_error(HKHIP_E_BAD_ARGUMENT, "null argument");
+    if (!net->partial) return set_error(HKHIP_E_PARTIAL, "hkhip_net_forward_partial needs a partial network");
     if (n == 0) return HKHIP_OK;
-    if (!net->embd.mem || !net->output.mem) return set_error(HKHIP_E_BAD_ARGUMENT, "tok_embd / output not loaded");
-    for (const auto &L : net->layers)
-        if (!L.loaded) return set_error(HKHIP_E_BAD_ARGUMENT, "a layer is not loaded");
-    if (uint64_t(pos0) + n > c.max_ctx) return set_error(HKHIP_E_UNSUPPORTED_SHAPE, "context full: %u + %u > %u", pos0, n, c.max_ctx);
-    for (uint32_t i = 0; i < n; i++)
-        if (tokens[i] >= c.vocab) return set_error(HKHIP_E_BAD_ARGUMENT, "token %u >= vocab %u", tokens[i], c.vocab);
-    if (hipSetDevice(net->eng->device) != hipSuccess) return set_error(HKHIP_E_DEVICE_FAILED, "hipSetDevice");
     int rc;
-    if ((rc = ensure_cap(net, n))) return rc;
-    if (n > MAX_DECODE) { // prefill: run directly
-        hipStream_t s = net->eng->cur;
-        net->stage[0] = pos0;
-        memcpy(net->stage + 1, tokens, n * 4);
-        NET_TRY(hipMemcpyAsync(net->io, net->stage, (n + 1) * 4, hipMemcpyHostToDevice, s), "tokens");
-        if ((rc = run_pass(net, n, 0))) return rc;
-        NET_TRY(hipStreamSynchronize(s), "prefill pass");
-        net->last_n = n;
-        return HKHIP_OK;
-    }
-    hipStream_t s = net->eng->cur;
-    // One copy of {position, tokens} from pinned memory; the pass reads both from the device.
-    net->stage[0] = pos0;
-    memcpy(net->stage + 1, tokens, n * 4);
-    NET_TRY(hipMemcpyAsync(net->io, net->stage, (n + 1) * 4, hipMemcpyHostToDevice, s), "tokens");
-    // Decode attention chunks: a power of two covering the positions the pass reaches (ATT_DWAVES
-    // waves of 64 positions each), so that short contexts skip the merge launch; one graph per (size,
-    // chunks).
-    const uint32_t dw = ATT_DWAVES, gmax = (nslices(c) + dw - 1) / dw, need = (pos0 + n + 64 * dw - 1) / (64 * dw);
-    uint32_t gb = 1;
-    while (gb < need) gb <<= 1;
-    gb = std::min(gb, gmax);
-    const uint32_t key = n | (gb << 8);
-    auto it = net->graphs.find(key);
-    if (it != net->graphs.end()) {
-        NET_TRY(hipGraphLaunch(it->second, s), "graph launch");
-    } else if (net->runs[key]++ == 0) {
-        if ((rc = run_pass(net, n, gb))) return rc; // first pass of this shape: eager (fills the launch caches)
-    } else {
-        hipGraph_t g = nullptr;
-        NET_TRY(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "begin capture");
-        rc = run_pass(net, n, gb);
-        const hipError_t e = hipStreamEndCapture(s, &g);
-        if (rc) {
-            if (g) (void)hipGraphDestroy(g);
-            return rc;
-        }
-        NET_TRY(e, "end capture");
-        hipGraphExec_t ex = nullptr;
-        const hipError_t ei = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
-        (void)hipGraphDestroy(g);
-        NET_TRY(ei, "graph instantiate");
-        net->graphs[key] = ex;
-        NET_TRY(hipGraphLaunch(ex, s), "graph launch");
-    }
-    // The pass is done when forward returns (the next call reuses the pinned staging buffer).
-    NET_TRY(hipStreamSynchronize(s), "pass");
+    if ((rc = check_loaded(net))) return rc;
+    if (hipSetDevice(net->eng->device) != hipSuccess) return set_error(HKHIP_E_DEVICE_FAILED, "hipSetDevice");
+    uint32_t max_pos = 0;
+    net->last_n = 0;
+    net->last_hidden = false;
+    if ((rc = stage_items(net, items, n, &max_pos))) return rc;
+    const uint64_t bytes = uint64_t(n) * net->cfg.dim * 4;
+    NET_TRY(hipMemcpyAsync(net->x, hidden_host, bytes, hipMemcpyHostToDevice, net->eng->cur), "hidden states in");
+    if ((rc = forward_staged(net, n, max_pos, false))) return rc;
+    NET_TRY(hipMemcpyAsync(hidden_host, net->x, bytes, hipMemcpyDeviceToHost, net->eng->cur), "hidden states out");
+    NET_TRY(hipStreamSynchronize(net->eng->cur), "hidden states out");
     net->last_n = n;
     return HKHIP_OK;
 }
 
+int hkhip_net_logits_rows(hkhip_net *net, const uint32_t *idx, uint32_t n, float *host_out) {
+    if (!net || !idx || !host_out) return set_error(HKHIP_E_BAD_ARGUMENT, "null argument");
+    if (!net->last_hidden) return set_error(HKHIP_E_BAD_ARGUMENT, "no full forward pass to read logits of");
+    if (n < 1 || n > net->max_rows) return set_error(HKHIP_E_BAD_ARGUMENT, "%u rows: 1..%u", n, net->max_rows);
+    const hkhip_net_config &c = net->cfg;
+    bool run = true;
+    for (uint32_t r = 0; r < n; r++) {
+        if (idx[r] >= net->last_n) return set_error(HKHIP_E_BAD_ARGUMENT, "row %u: item %u of %u", r, idx[r], net->last_n);
+        if (r && idx[r] != idx[r - 1] + 1) run = false;
+    }
+    if (hipSetDevice(net->eng->device) != hipSuccess) return set_error(HKHIP_E_DEVICE_FAILED, "hipSetDevice");
+    hipStream_t s = net->eng->cur;
+    const float *src = net->x + uint64_t(idx[0]) * c.dim;
+    if (!run) { // gather the rows
+        for (uint32_t r = 0; r < n; r++)
+            NET_TRY(hipMemcpyAsync(net->lx + uint64_t(r) * c.dim, net->x + uint64_t(idx[r]) * c.dim, uint64_t(c.dim) * 4,
+                                   hipMemcpyDeviceToDevice, s), "gather rows");
+        src = net->lx;
+    }
+    // One pass over the output matrix for every requested row (engine.zig:799-817).
+    float *const ys[1] = {net->logits};
+    int rc = product(net, n, &net->output, 1, src, net->out_norm, ys, nullptr, HKHIP_STORE);
+    if (rc) return rc;
+    NET_TRY(hipMemcpyAsync(host_out, net->logits, uint64_t(n) * c.vocab * 4, hipMemcpyDeviceToHost, s), "logits");
+    NET_TRY(hipStreamSynchronize(s), "logits");
+    return HKHIP_OK;
+}
+
+void hkhip_net_release(hkhip_net *net, uint64_t seq) {
+    if (!net) return;
+    for (uint32_t j = 0; j < net->n_slots; j++)
+        if (net->used[j] && net->owner[j] == seq) net->used[j] = 0;
+}
+
+uint32_t hkhip_net_max_rows(const hkhip_net *net) { return net ? net->max_rows : 0; }
+uint32_t hkhip_net_layer_count(const hkhip_net *net) { return net ? net->n_dev : 0; }
+int hkhip_net_is_partial(const hkhip_net *net) { return net && net->partial ? 1 : 0; }
+
+int hkhip_net_forward(hkhip_net *net, const uint32_t *tokens, uint32_t n, uint32_t pos0) {
+    if (!net || (n && !tokens)) return set_error(HKHIP_E_BAD_ARGUMENT, "null argument");
+    std::vector<hkhip_item> items(n);
+    for (uint32_t i = 0; i < n; i++) items[i] = hkhip_item{0, tokens[i], pos0 + i};
+    if (n && uint64_t(pos0) + n > net->cfg.max_ctx)
+        return set_error(HKHIP_E_CONTEXT_FULL, "context full: %u + %u > %u", pos0, n, net->cfg.max_ctx);
+    return forward_items(net, items.data(), n, true);
+}
+
 int hkhip_net_logits(hkhip_net *net, float *host_out) {
     if (!net || !host_out) return set_error(HKHIP_E_BAD_ARGUMENT, "null argument");
-    if (!net->last_n) return set_error(HKHIP_E_BAD_ARGUMENT, "no forward pass yet");
+    if (!net->last_hidden) return set_error(HKHIP_E_BAD_ARGUMENT, "no forward pass yet");
     return hkhip_copy_d2h(net->eng, host_out, net->logits, uint64_t(net->cfg.vocab) * 4);
 }
 
 const float *hkhip_net_logits_dev(hkhip_net *net) { return net ? net->logits : nullptr; }
+
+uint64_t hkhip_net_layer_bytes(const hkhip_net_config *cfg, const hkhip_net_layer *l) {
+    if (!cfg || !l || !config_ok(*cfg)) return 0;
+    return layer_dev_bytes(*cfg, *l);
+}
+
+uint64_t hkhip_net_bytes_needed(const hkhip_net_config *cfg, const hkhip_net_options *opts, const hkhip_net_layer *layers,
+                                hkhip_net_tensor tok_embd, hkhip_net_tensor out_norm, hkhip_net_tensor output) {
+    if (!cfg || !layers || !config_ok(*cfg)) return 0;
+    const hkhip_net_config &c = *cfg;
+    const hkhip_net_options o = opts ? *opts : hkhip_net_options{};
+    const uint32_t nl = layer_count(c, o);
+    const NetSizes z = net_sizes(c, o.slots ? o.slots : 1, nl, max_rows_of(o), initial_cap(o));
+    uint64_t total = z.fixed() + z.per_cap();
+    for (uint32_t i = 0; i < nl; i++) {
+        const uint64_t lb = layer_dev_bytes(c, layers[i]);
+        if (!lb) return 0;
+        total += lb;
+    }
+    if (nl == c.n_layers) {
+        if (!block_elems(tok_embd.t) || !block_elems(output.t) || c.dim % block_elems(tok_embd.t) ||
+            c.dim % block_elems(output.t))
+            return 0;
+        (void)out_norm;
+        total += weight_layout(tok_embd.t, c.vocab, c.dim).total + uint64_t(c.dim) * 4 +
+                 weight_layout(output.t, c.vocab, c.dim).total;
+    }
+    return total + HKHIP_NET_MARGIN_BYTES;
+}
+
+uint64_t hkhip_net_device_bytes(const hkhip_net *net) {
+    if (!net) return 0;
+    uint64_t total = 0;
+    for (const auto &p : net->owned) total += p.second;
+    for (const auto &L : net->layers) {
+        const hkhip_mat *ms[] = {&L.wqkv, &L.wq, &L.wk, &L.wv, &L.wo, &L.wgu, &L.wd};
+        for (const hkhip_mat *m : ms)
+            if (m->mem) total += m->dev_bytes;
+    }
+    if (net->embd.mem) total += net->embd.dev_bytes;
+    if (net->output.mem) total += net->output.dev_bytes;
+    return total;
+}
 
 } // extern "C"

@@ -1,7 +1,10 @@
-"""The whole-network device pass (hkhip_net_* in include/hkhip.h), as hk's engine interface sees it:
-load the layers' tensors (hk file-layout bytes, f32 vectors), run forward passes over one
-sequence, read the last token's logits (reference src/cuda/engine.zig:646-797, src/backend/backend.zig
-Device.forward / logits)."""
+"""The whole-network device pass (hkhip_net_* in include/hkhip.h), as hk's engine interface sees it
+(reference src/backend/backend.zig:128-209 Device, src/cuda/engine.zig Engine): load the layers'
+tensors (hk file-layout bytes, f32 vectors), run passes over the items of one or more sequences
+(`forward_items`, each sequence in its own cache slot), read the logits of chosen items
+(`logits_rows`), free a sequence's slot (`release`), run a partial network's leading layers on
+hidden states the caller embedded (`forward_partial`), and size a network before creating it
+(`bytes_needed`, `layer_bytes`: engine.zig:155-190)."""
 from __future__ import annotations
 
 import ctypes
@@ -10,7 +13,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from . import rope
-from ._lib import NET_LAYER_FIELDS, NetConfig, NetLayer, NetTensor, check, lib
+from ._lib import NET_LAYER_FIELDS, Item, NetConfig, NetLayer, NetOptions, NetTensor, check, lib
 
 F32 = 0x00  # hk StorageType f32
 
@@ -55,13 +58,53 @@ def _tensor(v, keep: list) -> NetTensor:
     return NetTensor(raw.ctypes.data, raw.nbytes, t)
 
 
+@dataclass
+class Options:
+    """src/cuda/engine.zig:43-58 Options."""
+    slots: int = 1
+    layers: int = 0          # leading layers on the device; 0: all (fewer: a partial network)
+    n_batch: int = 0         # most tokens per pass (0: buffers grown on demand)
+    attn_merge_max: int = 0  # test knob: decode attention chunks merged inside the launch (0: 256)
+
+    def c(self) -> NetOptions:
+        return NetOptions(self.slots, self.layers, self.n_batch, self.attn_merge_max)
+
+
+def _items(items) -> tuple:
+    """(ctypes array, count) of hkhip_item from (seq, token, pos) triples."""
+    arr = (Item * max(len(items), 1))(*[Item(int(s), int(t), int(p)) for s, t, p in items])
+    return arr, len(items)
+
+
+def _layer(tensors: dict, keep: list) -> NetLayer:
+    return NetLayer(*[_tensor(tensors.get(n), keep) for n in NET_LAYER_FIELDS])
+
+
+def bytes_needed(cfg: Config, model: dict, opts: Options | None = None) -> int:
+    """hkhip_net_bytes_needed: device bytes (with the 64 MiB margin) a network of cfg / opts holds for
+    the tensors of `model` (only their sizes and types are read)."""
+    keep: list = []
+    c, o = cfg.c(), (opts or Options()).c()
+    layers = (NetLayer * cfg.n_layers)(*[_layer(l, keep) for l in model["layers"]])
+    return int(lib().hkhip_net_bytes_needed(ctypes.byref(c), ctypes.byref(o), layers, _tensor(model["tok_embd"], keep),
+                                            _tensor(model["out_norm"], keep), _tensor(model["output"], keep)))
+
+
+def layer_bytes(cfg: Config, layer: dict) -> int:
+    """hkhip_net_layer_bytes: device bytes of one layer's tensors."""
+    keep: list = []
+    c = cfg.c()
+    return int(lib().hkhip_net_layer_bytes(ctypes.byref(c), ctypes.byref(_layer(layer, keep))))
+
+
 class Net:
-    def __init__(self, eng, cfg: Config):
+    def __init__(self, eng, cfg: Config, opts: Options | None = None):
         self.cfg = cfg
         self.eng = eng
+        self.opts = opts or Options()
         self._h = ctypes.c_void_p()
-        c = cfg.c()
-        check(lib().hkhip_net_create(eng._h, ctypes.byref(c), ctypes.byref(self._h)))
+        c, o = cfg.c(), self.opts.c()
+        check(lib().hkhip_net_create_opts(eng._h, ctypes.byref(c), ctypes.byref(o), ctypes.byref(self._h)))
 
     def close(self) -> None:
         if self._h:
@@ -76,18 +119,57 @@ class Net:
 
     def load_layer(self, i: int, tensors: dict) -> None:
         keep: list = []
-        layer = NetLayer(*[_tensor(tensors.get(n), keep) for n in NET_LAYER_FIELDS])
-        check(lib().hkhip_net_load_layer(self._h, i, ctypes.byref(layer)))
+        check(lib().hkhip_net_load_layer(self._h, i, ctypes.byref(_layer(tensors, keep))))
 
     def load_io(self, tok_embd, out_norm, output) -> None:
         keep: list = []
         check(lib().hkhip_net_load_io(self._h, _tensor(tok_embd, keep), _tensor(out_norm, keep), _tensor(output, keep)))
 
     def load(self, model: dict) -> None:
-        for i, layer in enumerate(model["layers"]):
+        for i, layer in enumerate(model["layers"][:self.layer_count]):
             self.load_layer(i, layer)
-        self.load_io(model["tok_embd"], model["out_norm"], model["output"])
+        if not self.is_partial:
+            self.load_io(model["tok_embd"], model["out_norm"], model["output"])
 
+    # Device.forward / forwardPartial / logits / release / maxRows / layerCount / isPartial
+    def forward_items(self, items) -> None:
+        """One pass over (seq, token, pos) items of one or more sequences."""
+        arr, n = _items(items)
+        check(lib().hkhip_net_forward_items(self._h, arr, n))
+
+    def forward_partial(self, items, hidden: np.ndarray) -> np.ndarray:
+        """A partial network's pass: hidden [n][dim] in, the state after its last layer out."""
+        arr, n = _items(items)
+        h = np.ascontiguousarray(hidden, dtype=np.float32).copy()
+        assert h.shape == (n, self.cfg.dim)
+        check(lib().hkhip_net_forward_partial(self._h, arr, n, h.ctypes.data))
+        return h
+
+    def logits_rows(self, indices) -> np.ndarray:
+        idx = np.ascontiguousarray(indices, dtype=np.uint32)
+        out = np.empty((idx.size, self.cfg.vocab), np.float32)
+        check(lib().hkhip_net_logits_rows(self._h, idx.ctypes.data, idx.size, out.ctypes.data))
+        return out
+
+    def release(self, seq: int) -> None:
+        lib().hkhip_net_release(self._h, seq)
+
+    @property
+    def max_rows(self) -> int:
+        return int(lib().hkhip_net_max_rows(self._h))
+
+    @property
+    def layer_count(self) -> int:
+        return int(lib().hkhip_net_layer_count(self._h))
+
+    @property
+    def is_partial(self) -> bool:
+        return bool(lib().hkhip_net_is_partial(self._h))
+
+    def device_bytes(self) -> int:
+        return int(lib().hkhip_net_device_bytes(self._h))
+
+    # one sequence (seq 0), the last token's logits computed inside the pass
     def forward(self, tokens, pos0: int) -> None:
         toks = np.ascontiguousarray(tokens, dtype=np.uint32)
         check(lib().hkhip_net_forward(self._h, toks.ctypes.data, toks.size, pos0))

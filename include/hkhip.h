@@ -191,31 +191,40 @@ int hkhip_matvec_parts_rmsnorm(hkhip_engine *eng, const hkhip_mat *mats, uint32_
 int hkhip_mm_noalloc(hkhip_engine *eng, const hkhip_mat *m, const float *x_dev, float *y_dev, uint32_t n,
                      const float *bias_dev, int mode);
 
-/* ---- whole network (the device engine's pass: src/cuda/engine.zig:646-797 runBatch / runPass,
- * with the CPU engine's layer order src/engine/cpu_backend.zig:248-322 forwardFrom) ----
+/* ---- whole network (the device engine: src/cuda/engine.zig Engine, driven through the seam
+ * src/backend/backend.zig:128-209 Device: forward(items), forwardPartial, logits(indices), release,
+ * maxRows, layerCount, isPartial; sized by bytesNeeded / layerBytes, engine.zig:155-190) ----
  * A decoder of n_layers blocks, each
  *   xb = rmsnorm(x) * attn_norm; q, k, v = Wq xb + bq, Wk xb + bk, Wv xb + bv;
  *   q, k = rope(headnorm(q, q_norm), headnorm(k, k_norm)); K/V cache (f16) += k, v at the position;
  *   att = causal GQA attention softmax(q K^T / sqrt(head_dim)) V; x += Wo att;
  *   xb = rmsnorm(x) * ffn_norm; x += Wdown (silu(Wgate xb) * (Wup xb)),
  * between an embedding lookup (a row of tok_embd, decoded) and logits = Woutput (rmsnorm(x) *
- * out_norm) of the last token. One sequence per network (a K/V cache of max_ctx positions).
- * Passes of up to 8 tokens run the decode kernels (RMS norm fused into the products' input
- * quantization, residual adds as accumulate-mode products, gate/up as one silu(gate)*up launch;
- * from 5 tokens the Q4_K / Q6_K products go through the fused quantizer and the small-batch MFMA
- * kernel; one-token passes do the q/k norms, RoPE and cache writes inside the attention kernel)
- * and are captured in a HIP graph per (token count, attention chunk count) after their first run;
- * longer passes (prompt prefill) run the MFMA GEMMs. Matrices are hk file-layout bytes in host memory, copied at load;
- * Wgate and Wup must share their type; Wq, Wk and Wv that share theirs run as one product over
- * their stacked rows (else as three, e.g. a Q6_K Wv beside Q4_K Wq / Wk as in Q4_K_M files).
- * Vectors (norms, biases) are f32 (HKHIP_F32). */
+ * out_norm) (the CPU engine's order, src/engine/cpu_backend.zig:248-331).
+ * A pass runs the tokens of one or more sequences (items); each sequence has its own K/V cache slot
+ * of max_ctx positions, assigned on the sequence's first item (engine.zig:556-568 slotFor) and freed
+ * by hkhip_net_release. Passes of up to 8 tokens run the decode kernels (RMS norm fused into the
+ * products' input quantization, residual adds as accumulate-mode products, gate/up as one
+ * silu(gate)*up launch; from 5 tokens the Q4_K / Q6_K products go through the fused quantizer and
+ * the small-batch MFMA kernel; one-token passes do the q/k norms, RoPE and cache writes inside the
+ * attention kernel) and are captured in a HIP graph per (token count, attention chunk count) after
+ * their first run: tokens, positions and slots are read from device memory. Longer passes run the
+ * MFMA GEMMs; their attention runs each sequence's consecutive run of positions longer than 8 on
+ * the f16 MFMA prefill kernel, the other items on the decode attention kernel.
+ * Matrices are hk file-layout bytes in host memory, copied at load; Wgate and Wup must share their
+ * type; Wq, Wk and Wv that share theirs run as one product over their stacked rows (else as three,
+ * e.g. a Q6_K Wv beside Q4_K Wq / Wk as in Q4_K_M files). Vectors (norms, biases) are f32 (HKHIP_F32). */
 #define HKHIP_F32 0x00 /* hk StorageType f32 (src/format.zig:28) */
+/* More error codes of the engine (src/cuda/engine.zig:31-40). */
+#define HKHIP_E_NO_SLOT -7       /* NoGpuSlot: every cache slot is held by another sequence */
+#define HKHIP_E_CONTEXT_FULL -8  /* ContextFull: an item's position is >= max_ctx */
+#define HKHIP_E_PARTIAL -9       /* PartialEngine: forward on a partial network (or forward_partial on a full one) */
 typedef struct hkhip_net hkhip_net;
 typedef struct hkhip_net_config {
     uint32_t dim, n_layers, n_heads, n_kv_heads, head_dim, ffn_dim, vocab;
     uint32_t rope_dim;  /* rotated dimensions of a head (head_dim for full rotary) */
     uint32_t rope_neox; /* 0: pairs (2i, 2i+1) ("norm" style); 1: pairs (i, i + rope_dim/2) */
-    uint32_t max_ctx;   /* K/V cache positions */
+    uint32_t max_ctx;   /* K/V cache positions per sequence (Options.n_ctx) */
     float rms_eps, rope_base;
     /* RoPE as hk's model setup computes it for its device engines (src/engine/model.zig:123-124,
      * ops.zig ropeInvFreq / ropeMscale; src/cuda/engine.zig takes both at init): rope_dim / 2
@@ -224,6 +233,16 @@ typedef struct hkhip_net_config {
     const float *inv_freq;
     float rope_mscale;
 } hkhip_net_config;
+/* src/cuda/engine.zig:43-58 Options. */
+typedef struct hkhip_net_options {
+    uint32_t slots;   /* sequences that can hold a cache at once (0: 1) */
+    uint32_t layers;  /* leading layers on the device; 0 or >= n_layers: all. Fewer: a partial network
+                       * (no embedding, final norm or output; hkhip_net_forward_partial only) */
+    uint32_t n_batch; /* most tokens in one pass; buffers are sized for it at create (0: grown on demand) */
+    /* Test knob (as the CUDA engine's slice_positions, engine.zig:268): most decode attention
+     * chunks merged inside the attention launch; more go through the separate merge kernel (0: 256). */
+    uint32_t attn_merge_max;
+} hkhip_net_options;
 /* A tensor in hk's file layout in host memory; data NULL for an absent optional tensor. */
 typedef struct hkhip_net_tensor {
     const void *data;
@@ -233,16 +252,66 @@ typedef struct hkhip_net_tensor {
 typedef struct hkhip_net_layer {
     hkhip_net_tensor attn_norm, wq, wk, wv, bq, bk, bv, q_norm, k_norm, wo, ffn_norm, w_gate, w_up, w_down;
 } hkhip_net_layer;
+/* One token of one sequence in a pass (src/engine/kv.zig:22-29 Item). seq identifies the sequence
+ * (hk passes its KvCache's address); items of one sequence appear in increasing position order. */
+typedef struct hkhip_item {
+    uint64_t seq;
+    uint32_t token;
+    uint32_t pos;
+} hkhip_item;
+/* Engine.init (engine.zig:276-...): caches for opts->slots sequences of cfg->max_ctx positions over
+ * the device layers. hkhip_net_create is the same with default options (one slot, every layer,
+ * buffers grown on demand). */
+int hkhip_net_create_opts(hkhip_engine *eng, const hkhip_net_config *cfg, const hkhip_net_options *opts,
+                          hkhip_net **out);
 int hkhip_net_create(hkhip_engine *eng, const hkhip_net_config *cfg, hkhip_net **out);
 void hkhip_net_destroy(hkhip_net *net);
+/* Layers at or past the device layer count are refused (a partial network holds only its own). */
 int hkhip_net_load_layer(hkhip_net *net, uint32_t layer, const hkhip_net_layer *l);
+/* Not for partial networks (they have no embedding or output). */
 int hkhip_net_load_io(hkhip_net *net, hkhip_net_tensor tok_embd, hkhip_net_tensor out_norm, hkhip_net_tensor output);
-/* Runs tokens[0..n) at positions pos0.. of the sequence (the cache keeps positions < pos0). */
+/* Device.forward (engine.zig:706-710): one pass over items[0..n) of one or more sequences; each
+ * item's key and value go to its sequence's slot, and every item attends to positions 0..pos of its
+ * own sequence (the items before it in the same pass included). Keeps every item's final hidden
+ * state for hkhip_net_logits_rows. Errors: NO_SLOT, CONTEXT_FULL, PARTIAL, BAD_ARGUMENT (token >=
+ * vocab, positions of a sequence not increasing, n > n_batch). Returns when the pass is done. */
+int hkhip_net_forward_items(hkhip_net *net, const hkhip_item *items, uint32_t n);
+/* Device.forwardPartial (engine.zig:716-721): a partial network's pass over items whose embedded
+ * hidden states hidden_host [n][dim] (host memory) the caller made; on return hidden_host holds the
+ * state after the last device layer. */
+int hkhip_net_forward_partial(hkhip_net *net, const hkhip_item *items, uint32_t n, float *hidden_host);
+/* Device.logits (engine.zig:799-817): logits of the given items of the last pass, one vocab row each
+ * in the order of idx, to host_out [n][vocab]; 1 <= n <= hkhip_net_max_rows. One pass over the
+ * output matrix for all rows. */
+int hkhip_net_logits_rows(hkhip_net *net, const uint32_t *idx, uint32_t n, float *host_out);
+/* Device.release (engine.zig:570-575): frees the slot of sequence seq (nothing if it holds none). */
+void hkhip_net_release(hkhip_net *net, uint64_t seq);
+/* Device.maxRows / layerCount / isPartial (backend.zig:147-185). */
+uint32_t hkhip_net_max_rows(const hkhip_net *net);
+uint32_t hkhip_net_layer_count(const hkhip_net *net);
+int hkhip_net_is_partial(const hkhip_net *net);
+/* Runs tokens[0..n) of slot 0's sequence (seq 0) at positions pos0.. and computes the last token's
+ * logits inside the pass (read with hkhip_net_logits / hkhip_net_logits_dev). */
 int hkhip_net_forward(hkhip_net *net, const uint32_t *tokens, uint32_t n, uint32_t pos0);
-/* Logits of the last token of the last forward: vocab floats, to host memory. */
+/* Logits of the last token of the last hkhip_net_forward: vocab floats, to host memory. */
 int hkhip_net_logits(hkhip_net *net, float *host_out);
-/* The same logits in device memory (valid until the next forward). */
+/* The logits buffer in device memory (the last forward's, or the last logits_rows' rows; valid
+ * until the next call). */
 const float *hkhip_net_logits_dev(hkhip_net *net);
+/* bytesNeeded / layerBytes (engine.zig:155-190), the planner's estimate (backend.zig:92-126
+ * probeCuda): device bytes a network of cfg / opts would allocate for these tensors (only their
+ * bytes and types are read; layers holds cfg->n_layers entries), plus a 64 MiB margin for the
+ * runtime, and the device bytes of one layer's tensors. Both count the device layouts (stacked
+ * q/k/v, interleaved gate/up, split planes), the caches (keys, values and the transposed values
+ * the prefill attention reads) and the pass buffers for max(n_batch, 8) tokens (64 when n_batch
+ * is 0). 0 on a bad argument. hkhip_net_device_bytes: what a network holds now (bytes_needed without the margin,
+ * once every tensor is loaded and with n_batch set). */
+#define HKHIP_NET_MARGIN_BYTES (64ull << 20)
+uint64_t hkhip_net_bytes_needed(const hkhip_net_config *cfg, const hkhip_net_options *opts,
+                                const hkhip_net_layer *layers, hkhip_net_tensor tok_embd, hkhip_net_tensor out_norm,
+                                hkhip_net_tensor output);
+uint64_t hkhip_net_layer_bytes(const hkhip_net_config *cfg, const hkhip_net_layer *l);
+uint64_t hkhip_net_device_bytes(const hkhip_net *net);
 
 /* ---- host-pointer products (secondary boundary: src/c_api.zig:1380-1400, hk.h:451-453,
  * src/engine/abi_ops.zig:65-107) ----

@@ -64,15 +64,31 @@ def rope_mscale(sc=None) -> float:
 
 
 class Oracle:
+    """hk's CPU forward over items of one or more sequences, each with its own f16 cache (a
+    KvCache per sequence, src/engine/kv.zig:22-29). `forward_items` mirrors Device.forward /
+    forwardPartial (src/backend/backend.zig:158-177): every layer writes the keys and values of all
+    items before any attends (src/cuda/engine.zig:674-675: "a token sees its predecessors in the
+    same pass"), an item attends to positions 0..pos of its own sequence; `logits_rows` mirrors
+    Device.logits (backend.zig:189-194) / logitsFor (cpu_backend.zig:324-331)."""
+
     def __init__(self, cfg, model: dict):
         self.cfg, self.m = cfg, model
-        hd, L = cfg.head_dim, cfg.n_layers
-        self.kc = np.zeros((L, cfg.n_kv_heads, cfg.max_ctx, hd), np.float16)
-        self.vc = np.zeros_like(self.kc)
-        rd = cfg.rope_dim or hd
+        self.caches: dict = {}  # seq -> (keys, values) [layer][kv head][max_ctx][hd] f16
+        rd = cfg.rope_dim or cfg.head_dim
         sc = getattr(cfg, "rope_scaling", None)
         self.inv_freq = rope_inv_freq(cfg.rope_base, rd, sc, getattr(cfg, "rope_freq_factors", None))
         self.mscale = rope_mscale(sc)
+        self.hidden = None
+
+    def _cache(self, seq):
+        if seq not in self.caches:
+            c = self.cfg
+            kc = np.zeros((c.n_layers, c.n_kv_heads, c.max_ctx, c.head_dim), np.float16)
+            self.caches[seq] = (kc, np.zeros_like(kc))
+        return self.caches[seq]
+
+    def release(self, seq) -> None:
+        self.caches.pop(seq, None)
 
     def _mm(self, mat, x, bias=None):
         raw, t = mat
@@ -94,20 +110,29 @@ class Oracle:
             v[0:2 * half:2], v[1:2 * half:2] = a * cs - b * sn, a * sn + b * cs
         return v
 
-    def forward(self, tokens, pos0: int) -> np.ndarray:
-        """Runs tokens at positions pos0..; returns the last token's logits."""
+    def embed(self, tokens) -> np.ndarray:
+        c = self.cfg
+        raw, t = self.m["tok_embd"]
+        return np.stack([O.dequantize(t, raw[tok], c.dim) for tok in tokens]).astype(np.float32)
+
+    def forward_items(self, items, hidden: np.ndarray | None = None, layers: int | None = None,
+                      first: int = 0) -> np.ndarray:
+        """Runs (seq, token, pos) items through layers [first, layers) (all by default), from their
+        embeddings or from `hidden` [n][dim]; returns the hidden states after the last layer run
+        (a partial device's leading layers, then the CPU's rest: cpu_backend.zig forwardFrom)."""
         c, m = self.cfg, self.m
-        n, hd = len(tokens), c.head_dim
-        raw, t = m["tok_embd"]
-        x = np.stack([O.dequantize(t, raw[tok], c.dim) for tok in tokens]).astype(np.float32)
+        n, hd = len(items), c.head_dim
+        x = self.embed([t for _, t, _ in items]) if hidden is None else np.array(hidden, np.float32)
         group = c.n_heads // c.n_kv_heads
-        for li, L in enumerate(m["layers"]):
+        nl = c.n_layers if layers is None else layers
+        for li in range(first, nl):
+            L = m["layers"][li]
             xb = np.stack([rms_norm(x[i], L["attn_norm"], c.rms_eps) for i in range(n)])
             q = self._mm(L["wq"], xb, L.get("bq"))
             k = self._mm(L["wk"], xb, L.get("bk"))
             v = self._mm(L["wv"], xb, L.get("bv"))
-            for i in range(n):
-                pos = pos0 + i
+            for i, (seq, _, pos) in enumerate(items):
+                kc, vc = self._cache(seq)
                 for h in range(c.n_heads):
                     s = q[i, h * hd:(h + 1) * hd]
                     if L.get("q_norm") is not None:
@@ -117,16 +142,16 @@ class Oracle:
                     s = k[i, g * hd:(g + 1) * hd]
                     if L.get("k_norm") is not None:
                         s = rms_norm(s, L["k_norm"], c.rms_eps)
-                    self.kc[li, g, pos] = self._rope(s, pos).astype(np.float16)
-                    self.vc[li, g, pos] = v[i, g * hd:(g + 1) * hd].astype(np.float16)
+                    kc[li, g, pos] = self._rope(s, pos).astype(np.float16)
+                    vc[li, g, pos] = v[i, g * hd:(g + 1) * hd].astype(np.float16)
             att = np.zeros((n, c.n_heads * hd), np.float32)
             scale = 1.0 / np.sqrt(np.float64(hd))
-            for i in range(n):
-                pos = pos0 + i
+            for i, (seq, _, pos) in enumerate(items):
+                kc, vc = self._cache(seq)
                 for h in range(c.n_heads):
                     g = h // group
-                    kk = self.kc[li, g, :pos + 1].astype(np.float64)
-                    vv = self.vc[li, g, :pos + 1].astype(np.float64)
+                    kk = kc[li, g, :pos + 1].astype(np.float64)
+                    vv = vc[li, g, :pos + 1].astype(np.float64)
                     sc = kk @ q[i, h * hd:(h + 1) * hd].astype(np.float64) * scale
                     p = np.exp(sc - sc.max())
                     att[i, h * hd:(h + 1) * hd] = (p @ vv) / p.sum()
@@ -137,5 +162,16 @@ class Oracle:
             with np.errstate(over="ignore"):
                 hmid = (gate / (np.float32(1) + np.exp(-gate)) * up).astype(np.float32)
             x = x + self._mm(L["w_down"], hmid)
-        xl = rms_norm(x[n - 1], m["out_norm"], c.rms_eps)
-        return self._mm(m["output"], xl[None])[0]
+        self.hidden = x
+        return x
+
+    def logits_rows(self, indices) -> np.ndarray:
+        """Logits of the given items of the last forward_items, one row each."""
+        m, c = self.m, self.cfg
+        xl = np.stack([rms_norm(self.hidden[i], m["out_norm"], c.rms_eps) for i in indices])
+        return self._mm(m["output"], xl)
+
+    def forward(self, tokens, pos0: int) -> np.ndarray:
+        """Runs tokens of sequence 0 at positions pos0..; returns the last token's logits."""
+        self.forward_items([(0, int(t), pos0 + i) for i, t in enumerate(tokens)])
+        return self.logits_rows([len(tokens) - 1])[0]

@@ -17,7 +17,12 @@ from oracle.net_oracle import Oracle
 pytestmark = pytest.mark.gpu
 
 COS_MIN = 0.9999      # tests/test_gpu.zig:49-123
-ABS_FRAC = 2e-2       # and no logit further than 2% of the largest from the CPU's
+# and no logit further than 2% of the largest from the CPU's: every product requantizes its input,
+# so a one-ulp change of the input moves the CPU restatement's own logits by up to ~1e-2 of the
+# largest on these models (tests/test_oracle.py::test_net_oracle_quantization_sensitivity); passes
+# that meet the products' 1e-3 are asserted to (test_net_long_context), and the hidden states after
+# a partial network's layers are (tests/test_gpu_net_items.py::test_partial_offload).
+ABS_FRAC = 2e-2
 
 
 @pytest.fixture(scope="module")
@@ -36,6 +41,7 @@ def check(got: np.ndarray, want: np.ndarray, what: str):
     got, want = got.astype(np.float64), want.astype(np.float64)
     cos = float(got @ want / (np.linalg.norm(got) * np.linalg.norm(want)))
     err = float(np.max(np.abs(got - want)) / np.max(np.abs(want)))
+    print(f"{what}: cos {cos:.7f} rel {err:.2e}", flush=True)
     assert np.isfinite(got).all(), what
     assert cos >= COS_MIN and err <= ABS_FRAC, f"{what}: cos {cos:.6f}, max err {err:.2e}"
 
