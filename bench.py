@@ -20,7 +20,7 @@ Also reported:
                 8B FFN shapes (14336x4096, 4096x14336) and the Qwen3-0.6B FFN shapes (3072x1024,
                 1024x3072), IQ4_NL 14336x4096 and Q6_K 4096x14336
   extra         the decode step at batch 8 (config 4); config 5's batch-1 matvecs (IQ4_NL
-                14336x4096, Q6_K 4096x14336) rotating over 12 matrices each; config 1 (the Q8_0
+                14336x4096, Q6_K 4096x14336) rotating over at least 512 MB of matrices each; config 1 (the Q8_0
                 3072x1024 matvec, rotating over 160 copies); config 2 (a batch-1 decode step of a
                 Qwen3-0.6B-shaped decoder, tokens/s)
   measured_peaks  this GPU's dense int8 MFMA rate and HBM read rate from probe kernels
@@ -238,8 +238,8 @@ def main():
         phase("prefill")
 
     # ---- BASELINE config 4 at batch 8 (the decode step for 8 tokens) and config 5's batch-1
-    # matvecs (IQ4_NL gate/up, Q6_K down), each rotating over 12 distinct matrices so that the
-    # 256 MB Infinity Cache cannot serve them.
+    # matvecs (IQ4_NL gate/up, Q6_K down, the other formats' gate/up), each rotating over at least
+    # 512 MB of distinct matrices so that the 256 MB Infinity Cache cannot serve them.
     if args.only in ("all", "extra"):
         extra = {}
         x_h8 = torch.randn(8, H, device=dev)
@@ -284,7 +284,9 @@ def main():
         mv = []
         for (name, t, m_, k_) in [("llama8b-ffn-up", F.IQ4_NL, FF, H), ("llama8b-ffn-down", F.Q6_K, H, FF)] + \
                                  [("llama8b-ffn-up", t, FF, H) for t in (F.Q4_0, F.Q4_1, F.Q5_0, F.Q5_1, F.Q5_K, F.IQ4_XS)]:
-            ws = [upload_synth(t, m_, k_, synth.seed_for(5, 100 * t + i)) for i in range(12)]
+            # at least 512 MB of distinct weights in the rotation (16+ copies at 4.5 bits per weight)
+            ncopy = max(12, -(-(512 << 20) // F.matrix_bytes(t, m_, k_)))
+            ws = [upload_synth(t, m_, k_, synth.seed_for(5, 100 * t + i)) for i in range(ncopy)]
             xv = torch.randn(1, k_, device=dev)
             yv = torch.empty(1, m_, device=dev)
 
@@ -585,22 +587,24 @@ def cpu_baseline(seconds: float):
     level = O.simd_level()
     m, k = LLAMA8B["ffn"], LLAMA8B["hidden"]
     raw = synth.weights_np(F.Q4_K, m, k, synth.seed_for(4, 0))
+    # 16 copies (528 MB) read in turn, so that the host's last-level cache cannot hold the weights
+    copies = [raw.copy() for _ in range(16)]
     x = synth.activations_np(1, k, 1)[0]
     O.matvec_q4k_simd(raw, m, k, x, threads=cores, level=level)
     reps, t0 = 0, time.perf_counter()
     while time.perf_counter() - t0 < seconds:
-        O.matvec_q4k_simd(raw, m, k, x, threads=cores, level=level)
+        O.matvec_q4k_simd(copies[reps % len(copies)], m, k, x, threads=cores, level=level)
         reps += 1
     dt = (time.perf_counter() - t0) / reps
     nbytes = raw.nbytes + 4 * k + 4 * m
     # The same product on one thread, for a figure comparable to hk-kernels' single-thread runs.
     reps1, t1 = 0, time.perf_counter()
     while time.perf_counter() - t1 < max(1.0, seconds / 4):
-        O.matvec_q4k_simd(raw, m, k, x, threads=1, level=level)
+        O.matvec_q4k_simd(copies[reps1 % len(copies)], m, k, x, threads=1, level=level)
         reps1 += 1
     dt1 = (time.perf_counter() - t1) / reps1
     return {"value": round(nbytes / dt / 1e9, 2), "unit": "GB/s", "cores": cores, "kind": "port",
-            "sample": f"Q4_K 14336x4096 matvec, batch 1, {reps} reps in {seconds:.0f} s; hk's decode kernel "
+            "sample": f"Q4_K 14336x4096 matvec, batch 1, {reps} reps in {seconds:.0f} s over 16 copies (528 MB); hk's decode kernel "
                       f"({O.simd_level_name(level)} dot primitive, 16 KiB row chunks, OpenMP over {cores} physical cores)",
             "isa": O.simd_level_name(level),
             "single_thread_value": round(nbytes / dt1 / 1e9, 2), "cpu_model": cpu_model()}

@@ -3,7 +3,7 @@ views of the mapping (hk's weights.Mat, reference src/engine/weights.zig:1-34), 
 tensors upload straight from those views into the HIP network pass (hk_amd.net).
 
 Layouts followed (reference files):
-  FileHeader, 128 bytes, little endian          src/format.zig:174-199
+  FileHeader, 128 bytes, little endian          src/format.zig:133-163
   metadata: key u16 + bytes, tag u8, len u32, value   src/metadata.zig:225-300
   tensor table: name u16 + bytes, type, tile layout, sparsity, ndim u8, shape u64 x ndim,
     data / residual / scale offset + size u64 x 6, block_size u16, sparsity_ratio f32
@@ -24,7 +24,7 @@ from . import formats
 
 MAGIC = b"HKNT"
 VERSION_MAJOR = 1
-HEADER = struct.Struct("<4sHHIHHQQQQQQQQQH38s")  # format.zig:174-195
+HEADER = struct.Struct("<4sHHIHHQQQQQQQQQH38s")  # format.zig:133-152 FileHeader
 assert HEADER.size == 128
 
 # metadata value tags (format.zig MetadataValueType)

@@ -120,3 +120,56 @@ def test_rope_scaling_from_metadata(tmp_path):
     with HkFile(p) as f:
         with pytest.raises(HkFormatError, match="positive"):
             f.config(max_ctx=64)
+
+
+def test_hand_built_container_bytes(tmp_path):
+    """A container written byte by byte from the reference's field order, not through
+    tests/hkwriter.py: FileHeader (src/format.zig:133-152: magic, versions, flags, alignment,
+    split index, counts, offsets and sizes, appendix, checksum, split count, 38 reserved bytes),
+    metadata (src/metadata.zig:225-264: key length u16, key, tag u8, value length u32, value) and one
+    tensor table entry (src/tensor_toc.zig:39-66: name length u16, name, storage type, tile layout,
+    sparsity, ndim, shape u64 x ndim, six u64 offsets / sizes, block size u16, sparsity ratio f32)."""
+    header = bytes.fromhex(
+        "484b4e54"          # magic "HKNT"
+        "0100" "0000"       # version 1.0
+        "03000000"          # flags
+        "8000" "0000"       # alignment 128, split index 0
+        "0100000000000000"  # tensor count 1
+        "0200000000000000"  # metadata kv count 2
+        "8000000000000000"  # metadata offset 128
+        "2000000000000000"  # metadata size 32
+        "a000000000000000"  # tensor table offset 160
+        "4d00000000000000"  # tensor table size 77
+        "0001000000000000"  # tensor data offset 256
+        "0000000000000000"  # appendix offset
+        "0000000000000000"  # checksum
+        "0100"              # split count 1
+        + "00" * 38)        # reserved
+    metadata = bytes.fromhex(
+        "0100" "6e" "02" "08000000" "0700000000000000"  # "n": int64 7
+        "0400" "61726368" "01" "05000000" "7177656e33")  # "arch": string "qwen3"
+    toc = bytes.fromhex(
+        "0100" "74"                                     # name "t"
+        "16" "00" "00" "02"                             # Q8_0, tile layout 0, no sparsity, 2 dims
+        "0100000000000000" "2000000000000000"           # shape (1, 32)
+        "0001000000000000" "2200000000000000"           # data at 256, 34 bytes
+        "0000000000000000" "0000000000000000"           # residual offset / size
+        "0000000000000000" "0000000000000000"           # scale offset / size
+        "2000" "0000c03e")                              # block size 32, sparsity ratio 0.375
+    block = bytes.fromhex("003c") + bytes(range(256 - 16, 256)) + bytes(range(16))  # d = 1.0, qs = -16..15
+    assert len(header) == 128 and len(metadata) == 32 and len(toc) == 77
+    raw = header + metadata + toc + bytes(256 - 237) + block
+    p = tmp_path / "hand.hk"
+    p.write_bytes(raw)
+    with HkFile(str(p)) as f:
+        assert f.version == (1, 0) and f.flags == 3 and f.alignment == 128 and f.split_count == 1
+        assert f.tensor_count == 1 and f.metadata == {"n": 7, "arch": "qwen3"}
+        e = f.entry("t")
+        assert (e.t, e.tile_layout, e.sparsity, e.shape) == (F.Q8_0, 0, 0, (1, 32))
+        assert (e.data_offset, e.data_size, e.block_size, e.sparsity_ratio) == (256, 34, 32, 0.375)
+        assert bytes(f.data("t")) == block
+        from oracle import oracle as O
+        assert np.array_equal(O.dequantize(F.Q8_0, np.frombuffer(block, np.uint8), 32), np.arange(-16, 16, dtype=np.float32))
+    p.write_bytes(raw[:200])  # the tensor table runs past the end
+    with pytest.raises(HkFormatError):
+        HkFile(str(p))
