@@ -254,22 +254,25 @@ template <int DL> struct VRow {
     }
 };
 
-// Decode attention (passes of up to MAX_DECODE tokens): G workgroups of NWV waves per (query head,
-// token), G set by the context the pass reaches (host side: a power of two, so that every 64-position
-// step up to the last position has a wave of its own; the context's loads spread over G times more
-// CUs than one workgroup would use); wave w of chunk g takes step g*NWV + w. A workgroup merges its
-// waves' {max, sum, acc} in LDS (as the slice merge does, attention.zig:113-133) and writes the
-// chunk's partial ({-inf, 0, 0...} past the token's position), which attn_combine_kernel merges;
-// with G = 1 it writes the normalized result itself. In a step a lane loads its position's key row
-// (scores: lane = position), then the value rows go 16 bytes per lane: lane = (row r of the RPI rows
-// one load covers, 8 dimensions), so a step is HD/8 + 64/RPI loads per lane; the RPI partial sums of
-// a dimension are added across lanes once, at the end.
+// Decode attention (passes of up to MAX_DECODE tokens): C chunk workgroups of NWV waves per (head
+// block, token), C set by the context the pass reaches (host side: a power of two, so that every
+// 64-position step up to the last position has a wave of its own; the context's loads spread over C
+// times more CUs than one workgroup would use); wave w of chunk g takes step g*NWV + w. A head block
+// is the G query heads that share one key/value head (the whole GQA group), so each key and value
+// row is loaded once for all of them. A workgroup merges its waves' {max, sum, acc} per head in LDS
+// (as the slice merge does, attention.zig:113-133) and writes the chunk's partials ({-inf, 0, 0...}
+// past the token's position), which the last chunk to finish (or attn_combine_kernel) merges; with
+// C = 1 it writes the normalized results itself. In a step a lane loads its position's key row
+// (scores: lane = position, one dot per head against the heads' q rows in LDS), then the value rows
+// go 16 bytes per lane: lane = (row r of the RPI rows one load covers, 8 dimensions), so a step is
+// HD/8 + 64/RPI loads per lane whatever G is; the RPI partial sums of a dimension are added across
+// lanes once, at the end.
 //
-// One-token passes run fused: the raw q row is normalized and rotated by each wave (the same steps
-// as rope_kv_kernel), and the wave whose step holds the token's position builds the new key row
-// (norm, rotation, f16) and value row, uses them in place of the cache rows it loaded, and -- in the
-// first query head of each key/value group -- writes them to the caches. The kernel follows the
-// declarations below.
+// One-token passes run fused: the raw q rows are normalized and rotated in the kernel (the same
+// steps as rope_kv_kernel), and the wave whose step holds the token's position builds the new key
+// row (norm, rotation, f16) and value row, uses them in place of the cache rows it loaded, and -- in
+// the head block holding the group's first head -- writes them to the caches. The kernel follows
+// the declarations below.
 
 // Sum / max over a wave: DPP moves within each row of 16 lanes, then the four rows' results.
 __device__ __forceinline__ float wave_sum_f(float v) {
@@ -330,31 +333,22 @@ __device__ __forceinline__ void merge_partials(const float *p, float *o, uint32_
     }
 }
 
-// The fused decode pass's q row (and, with kx, the new key row) of one head: headNorm (ops.zig:
-// 31-38) from registers, then the rotation of ropeAngles / ropeApply (ops.zig:154-185) in the rows'
-// LDS copies hq / hk, one sin/cos per angle for both rows. nw*, fr: norm weights and inv_freq
-// entries lane + 64 j / lane + 64 f, loaded by the caller.
+// Registers of a lane's share of the rope_dim / 2 rotation frequencies.
 template <int HD> constexpr int rope_regs() { return (HD / 2 + 63) / 64; }
-template <int HD, bool KEY>
-__device__ __forceinline__ void qk_norm_rope(float *hq, float *hk, const float (&qx)[HD / 64], const float (&kx)[HD / 64],
-                                             const float (&qnw)[HD / 64], const float (&knw)[HD / 64],
-                                             const float (&fr)[rope_regs<HD>()], uint32_t pos, const RopeArgs &a,
-                                             uint32_t lane) {
-    float ssq = 0.0f, ssk = 0.0f;
+// One row of HD values held by a wave (lane l: elements l + 64 j in x): headNorm (ops.zig:31-38,
+// when nw_on) into the LDS row h, then the rotation of ropeAngles / ropeApply (ops.zig:154-185)
+// in place -- the steps head_norm_rope takes, from registers.
+template <int HD>
+__device__ __forceinline__ void norm_rope_row(float *h, const float (&x)[HD / 64], const float (&nw)[HD / 64], bool nw_on,
+                                              const float (&fr)[rope_regs<HD>()], uint32_t pos, const RopeArgs &a,
+                                              uint32_t lane) {
+    float ss = 0.0f;
 #pragma unroll
-    for (int j = 0; j < HD / 64; j++) {
-        ssq = fmaf(qx[j], qx[j], ssq);
-        if (KEY) ssk = fmaf(kx[j], kx[j], ssk);
-    }
-    ssq = wave_sum_f(ssq);
-    if (KEY) ssk = wave_sum_f(ssk);
-    const float iq = a.q_norm ? __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ssq, float(HD)) + a.eps)) : 1.0f;
-    const float ik = KEY && a.k_norm ? __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ssk, float(HD)) + a.eps)) : 1.0f;
+    for (int j = 0; j < HD / 64; j++) ss = fmaf(x[j], x[j], ss);
+    ss = wave_sum_f(ss);
+    const float inv = nw_on ? __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, float(HD)) + a.eps)) : 1.0f;
 #pragma unroll
-    for (int j = 0; j < HD / 64; j++) {
-        hq[lane + 64 * j] = a.q_norm ? (qx[j] * iq) * qnw[j] : qx[j];
-        if (KEY) hk[lane + 64 * j] = a.k_norm ? (kx[j] * ik) * knw[j] : kx[j];
-    }
+    for (int j = 0; j < HD / 64; j++) h[lane + 64 * j] = nw_on ? (x[j] * inv) * nw[j] : x[j];
     wave_sync();
     const float p = float(pos);
 #pragma unroll
@@ -365,60 +359,60 @@ __device__ __forceinline__ void qk_norm_rope(float *hq, float *hk, const float (
             sincosf(p * fr[f], &sn, &cs);
             const float c = cs * a.mscale, s = sn * a.mscale;
             const uint32_t i0 = a.neox ? i : 2 * i, i1 = a.neox ? i + a.rope_half : 2 * i + 1;
-            const float x0 = hq[i0], x1 = hq[i1];
-            hq[i0] = x0 * c - x1 * s;
-            hq[i1] = x0 * s + x1 * c;
-            if (KEY) {
-                const float y0 = hk[i0], y1 = hk[i1];
-                hk[i0] = y0 * c - y1 * s;
-                hk[i1] = y0 * s + y1 * c;
-            }
+            const float x0 = h[i0], x1 = h[i1];
+            h[i0] = x0 * c - x1 * s;
+            h[i1] = x0 * s + x1 * c;
         }
     }
     wave_sync();
 }
 
-template <int HD, int NWV>
+// G query heads h0 .. h0 + G - 1 that share one key/value head (G divides the group size: the
+// whole group, or 1) per workgroup, so each key and value row is loaded once for all of them.
+template <int HD, int NWV, int G>
 __global__ __launch_bounds__(NWV * 64) void attn_decode_kernel(AttnArgs a) {
     constexpr int LPR = HD / 8, RPI = 64 / LPR, NI = 64 / RPI; // lanes per value row, rows per load, loads
     const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const uint32_t vr_ = lane / LPR, vc = lane % LPR; // value row within a load, dimension chunk
-    const uint32_t g = blockIdx.x, h = blockIdx.y, t = blockIdx.z;
-    __shared__ float qs[NWV][HD];
-    __shared__ float red_m[NWV], red_l[NWV];
-    __shared__ float prs[NWV][64]; // a step's probabilities, for the value rows' lanes
-    __shared__ float red_acc[NWV][HD];
-    __shared__ float kn[NWV][HD];                                     // fused: the new key row, f32
-    __shared__ __attribute__((aligned(16))) __half kvh16[NWV][2][HD]; // fused: new key / value rows, f16
-    const uint32_t grp = a.nh / a.nkv, kvh = h / grp;
-    const float *qsrc = a.q + uint64_t(t) * a.sq + h * HD;
-    float qv[HD / 64], kx[HD / 64], vx[HD / 64];
+    const uint32_t g = blockIdx.x, t = blockIdx.z;
+    const uint32_t grp = a.nh / a.nkv, h0 = blockIdx.y * G, kvh = h0 / grp;
+    __shared__ float qs[G][HD];
+    __shared__ float red_m[NWV][G], red_l[NWV][G];
+    __shared__ float prs[NWV][G][64]; // a step's probabilities per head, for the value rows' lanes
+    __shared__ float red_acc[NWV][G][HD];
+    __shared__ float kn[HD];                                  // fused: the new key row, f32
+    __shared__ __attribute__((aligned(16))) __half kvh16[2][HD]; // fused: new key / value rows, f16
+    const uint64_t sl = a.slot[t];
+    const uint32_t pos = a.pos[t];
+    const __half *kb = a.kc + sl * a.kv_slot + uint64_t(kvh) * a.max_ctx * HD;
+    const __half *vb = a.vc + sl * a.kv_slot + uint64_t(kvh) * a.max_ctx * HD + 8 * vc;
+    // The q rows of this wave's heads (w, w + NWV, ... of the G), and for a one-token (fused) pass
+    // the norm weights, the rotation frequencies and the raw new key / value rows, are loaded before
+    // the cache rows: the memory counter is in order, so the q rows' norm and rotation then run
+    // while the cache rows are in flight.
+    constexpr int QPW = (G + NWV - 1) / NWV;
+    float qv[QPW][HD / 64], qnw[HD / 64], kx[HD / 64], knw[HD / 64], vx[HD / 64], fr[rope_regs<HD>()];
 #pragma unroll
-    for (int j = 0; j < HD / 64; j++) qv[j] = qsrc[lane + 64 * j];
-    // Fused: raw rows of the new key and value (one-token passes: token 0), the norm weights and the
-    // rotation frequencies, all loaded before the cache rows so that none waits behind them.
-    float qnw[HD / 64], knw[HD / 64], fr[rope_regs<HD>()];
+    for (int qi = 0; qi < QPW; qi++) {
+        const uint32_t gi = w + NWV * qi;
+        const float *qsrc = a.q + uint64_t(t) * a.sq + (h0 + (gi < uint32_t(G) ? gi : 0)) * HD;
+#pragma unroll
+        for (int j = 0; j < HD / 64; j++) qv[qi][j] = qsrc[lane + 64 * j];
+    }
     if (a.fused) {
 #pragma unroll
         for (int j = 0; j < HD / 64; j++) {
-            kx[j] = a.r.k[kvh * HD + lane + 64 * j];
-            vx[j] = a.r.v[kvh * HD + lane + 64 * j];
             qnw[j] = a.r.q_norm ? a.r.q_norm[lane + 64 * j] : 1.0f;
             knw[j] = a.r.k_norm ? a.r.k_norm[lane + 64 * j] : 1.0f;
+            kx[j] = a.r.k[kvh * HD + lane + 64 * j];
+            vx[j] = a.r.v[kvh * HD + lane + 64 * j];
         }
 #pragma unroll
         for (int f = 0; f < rope_regs<HD>(); f++) fr[f] = lane + 64 * f < a.r.rope_half ? a.r.inv_freq[lane + 64 * f] : 0.0f;
     }
-    float m = -INFINITY, l = 0.0f, acc[8];
-#pragma unroll
-    for (int j = 0; j < 8; j++) acc[j] = 0.0f;
-    const uint64_t sl = a.slot[t];
-    const __half *kb = a.kc + sl * a.kv_slot + uint64_t(kvh) * a.max_ctx * HD;
-    const __half *vb = a.vc + sl * a.kv_slot + uint64_t(kvh) * a.max_ctx * HD + 8 * vc;
-    const float *qw = qs[w];
-    // The launch gives every 64-position step of the context a wave of its own (G * NWV steps), so
-    // a wave has one step, and its loads need not wait for the position: rows are clamped to the
-    // cache only, and rows past the token's position (finite: the caches start zeroed) are masked.
+    // The launch gives every 64-position step of the context a wave of its own, so a wave has one
+    // step, and its loads need not wait for the position: rows are clamped to the cache only, and
+    // rows past the token's position (finite: the caches start zeroed) are masked.
     const uint32_t p0 = 64 * (g * NWV + w);
     const uint32_t pp = p0 + lane, lastc = a.max_ctx - 1;
     uint4 kr[HD / 8], vv[NI];
@@ -432,199 +426,262 @@ __global__ __launch_bounds__(NWV * 64) void attn_decode_kernel(AttnArgs a) {
             vv[i] = *reinterpret_cast<const uint4 *>(vb + uint64_t(pv < lastc ? pv : lastc) * HD);
         }
     }
-    const uint32_t pos = a.pos[t];
+    // The q rows to LDS; a one-token pass normalizes and rotates them (rope_kv_kernel's steps,
+    // which the multi-token passes ran before this kernel).
+#pragma unroll
+    for (int qi = 0; qi < QPW; qi++) {
+        const uint32_t gi = w + NWV * qi;
+        if (gi < uint32_t(G)) {
+            if (a.fused) {
+                norm_rope_row<HD>(qs[gi], qv[qi], qnw, a.r.q_norm != nullptr, fr, pos, a.r, lane);
+            } else {
+#pragma unroll
+                for (int j = 0; j < HD / 64; j++) qs[gi][lane + 64 * j] = qv[qi][j];
+            }
+        }
+    }
+    __syncthreads();
+    float m[G], l[G], acc[G][8];
+#pragma unroll
+    for (int gi = 0; gi < G; gi++) {
+        m[gi] = -INFINITY;
+        l[gi] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc[gi][j] = 0.0f;
+    }
     if (p0 <= pos) {
         const uint32_t p_end = min(p0 + 64, pos + 1);
-        // Fused pass, wave holding the new position: its score (dot_new, in the order of the cache
-        // rows' dot below) and value row (vnew) replace what the loads brought for that position.
+        // Fused pass, wave holding the new position: its scores (in the order of the cache rows'
+        // dots below) and value row (vnew) replace what the loads brought for that position.
         const bool has_new = a.fused && pos < p0 + 64;
-        float dot_new = 0.0f;
+        float dot_new[G];
         uint4 vnew = make_uint4(0, 0, 0, 0);
-        if (a.fused) {
-            if (has_new) {
-                qk_norm_rope<HD, true>(qs[w], kn[w], qv, kx, qnw, knw, fr, pos, a.r, lane);
+        if (has_new) {
+            norm_rope_row<HD>(kn, kx, knw, a.r.k_norm != nullptr, fr, pos, a.r, lane);
 #pragma unroll
-                for (int j = 0; j < HD / 64; j++) {
-                    kvh16[w][0][lane + 64 * j] = __float2half(kn[w][lane + 64 * j]);
-                    kvh16[w][1][lane + 64 * j] = __float2half(vx[j]);
-                }
-                wave_sync();
+            for (int j = 0; j < HD / 64; j++) {
+                kvh16[0][lane + 64 * j] = __float2half(kn[lane + 64 * j]);
+                kvh16[1][lane + 64 * j] = __float2half(vx[j]);
+            }
+            wave_sync();
+#pragma unroll
+            for (int gi = 0; gi < G; gi++) {
+                float dn = 0.0f;
                 for (int c = 0; c < HD / 8; c++) {
-                    const uint4 kw = reinterpret_cast<const uint4 *>(kvh16[w][0])[c];
+                    const uint4 kw = reinterpret_cast<const uint4 *>(kvh16[0])[c];
                     const __half2 *hp = reinterpret_cast<const __half2 *>(&kw);
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
                         const float2 f = __half22float2(hp[e]);
-                        dot_new = fmaf(qs[w][8 * c + 2 * e], f.x, dot_new);
-                        dot_new = fmaf(qs[w][8 * c + 2 * e + 1], f.y, dot_new);
+                        dn = fmaf(qs[gi][8 * c + 2 * e], f.x, dn);
+                        dn = fmaf(qs[gi][8 * c + 2 * e + 1], f.y, dn);
                     }
                 }
-                vnew = *reinterpret_cast<const uint4 *>(&kvh16[w][1][8 * vc]);
-                if (h % grp == 0) { // one writer per key/value head
-                    __half *kd = a.r.kc + sl * a.r.kv_slot + (uint64_t(kvh) * a.max_ctx + pos) * HD;
-                    __half *vd = a.r.vc + sl * a.r.kv_slot + (uint64_t(kvh) * a.max_ctx + pos) * HD;
-                    __half *vtd = a.r.vt + sl * a.r.vt_slot + uint64_t(kvh) * HD * a.r.vt_stride + pos;
-#pragma unroll
-                    for (int j = 0; j < HD / 64; j++) {
-                        const uint32_t d = lane + 64 * j;
-                        kd[d] = kvh16[w][0][d];
-                        vd[d] = kvh16[w][1][d];
-                        vtd[uint64_t(d) * a.r.vt_stride] = kvh16[w][1][d];
-                    }
-                }
-            } else {
-                qk_norm_rope<HD, false>(qs[w], kn[w], qv, kx, qnw, knw, fr, pos, a.r, lane);
+                dot_new[gi] = dn;
             }
-        } else {
+            vnew = *reinterpret_cast<const uint4 *>(&kvh16[1][8 * vc]);
+            if (h0 % grp == 0) { // one writer per key/value head
+                __half *kd = a.r.kc + sl * a.r.kv_slot + (uint64_t(kvh) * a.max_ctx + pos) * HD;
+                __half *vd = a.r.vc + sl * a.r.kv_slot + (uint64_t(kvh) * a.max_ctx + pos) * HD;
+                __half *vtd = a.r.vt + sl * a.r.vt_slot + uint64_t(kvh) * HD * a.r.vt_stride + pos;
 #pragma unroll
-            for (int j = 0; j < HD / 64; j++) qs[w][lane + 64 * j] = qv[j];
+                for (int j = 0; j < HD / 64; j++) {
+                    const uint32_t d = lane + 64 * j;
+                    kd[d] = kvh16[0][d];
+                    vd[d] = kvh16[1][d];
+                    vtd[uint64_t(d) * a.r.vt_stride] = kvh16[1][d];
+                }
+            }
         }
 #pragma unroll
         for (int c = 0; c < HD / 8; c++) asm volatile("" : "+v"(kr[c].x), "+v"(kr[c].y), "+v"(kr[c].z), "+v"(kr[c].w));
 #pragma unroll
         for (int i = 0; i < NI; i++) asm volatile("" : "+v"(vv[i].x), "+v"(vv[i].y), "+v"(vv[i].z), "+v"(vv[i].w));
-        float dot = 0.0f;
+        float dot[G];
+#pragma unroll
+        for (int gi = 0; gi < G; gi++) dot[gi] = 0.0f;
 #pragma unroll
         for (int c = 0; c < HD / 8; c++) {
             const __half2 *hp = reinterpret_cast<const __half2 *>(&kr[c]);
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const float2 f = __half22float2(hp[e]);
-                dot = fmaf(qw[8 * c + 2 * e], f.x, dot);
-                dot = fmaf(qw[8 * c + 2 * e + 1], f.y, dot);
+#pragma unroll
+                for (int gi = 0; gi < G; gi++) {
+                    dot[gi] = fmaf(qs[gi][8 * c + 2 * e], f.x, dot[gi]);
+                    dot[gi] = fmaf(qs[gi][8 * c + 2 * e + 1], f.y, dot[gi]);
+                }
             }
         }
-        if (has_new && pp == pos) dot = dot_new;
-        const float s = pp < p_end ? dot * a.scale : -INFINITY;
-        const float mn = fmaxf(m, wave_max_f(s));
-        const float pr = pp < p_end ? expf(s - mn) : 0.0f;
-        const float ps = wave_sum_f(pr);
-        prs[w][lane] = pr;
-        wave_sync();
-        const float corr = m == -INFINITY ? 0.0f : expf(m - mn);
-        l = l * corr + ps;
+        float corr[G];
 #pragma unroll
-        for (int j = 0; j < 8; j++) acc[j] *= corr;
+        for (int gi = 0; gi < G; gi++) {
+            if (has_new && pp == pos) dot[gi] = dot_new[gi];
+            const float s = pp < p_end ? dot[gi] * a.scale : -INFINITY;
+            const float mn = fmaxf(m[gi], wave_max_f(s));
+            const float pr = pp < p_end ? expf(s - mn) : 0.0f;
+            const float ps = wave_sum_f(pr);
+            prs[w][gi][lane] = pr;
+            corr[gi] = m[gi] == -INFINITY ? 0.0f : expf(m[gi] - mn);
+            l[gi] = l[gi] * corr[gi] + ps;
+            m[gi] = mn;
+        }
+        wave_sync();
+#pragma unroll
+        for (int gi = 0; gi < G; gi++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) acc[gi][j] *= corr[gi];
 #pragma unroll
         for (int i = 0; i < NI; i++) {
-            const float pi = prs[w][RPI * i + vr_]; // 0 for positions past the step
             const uint4 vw = has_new && p0 + RPI * i + vr_ == pos ? vnew : vv[i];
             const __half2 *hp = reinterpret_cast<const __half2 *>(&vw);
+            float vf[8];
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const float2 f = __half22float2(hp[e]);
-                acc[2 * e] = fmaf(pi, f.x, acc[2 * e]);
-                acc[2 * e + 1] = fmaf(pi, f.y, acc[2 * e + 1]);
+                vf[2 * e] = f.x;
+                vf[2 * e + 1] = f.y;
+            }
+#pragma unroll
+            for (int gi = 0; gi < G; gi++) {
+                const float pi = prs[w][gi][RPI * i + vr_]; // 0 for positions past the step
+#pragma unroll
+                for (int e = 0; e < 8; e++) acc[gi][e] = fmaf(pi, vf[e], acc[gi][e]);
             }
         }
-        m = mn;
     }
     // The RPI row groups' sums of each dimension chunk (lanes vc, vc + LPR, ...).
 #pragma unroll
     for (int o = LPR; o < 64; o <<= 1)
 #pragma unroll
-        for (int j = 0; j < 8; j++) acc[j] += __shfl_xor(acc[j], o);
+        for (int gi = 0; gi < G; gi++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) acc[gi][j] += __shfl_xor(acc[gi][j], o);
     if (lane == 0) {
-        red_m[w] = m;
-        red_l[w] = l;
+#pragma unroll
+        for (int gi = 0; gi < G; gi++) {
+            red_m[w][gi] = m[gi];
+            red_l[w][gi] = l[gi];
+        }
     }
     if (lane < LPR) {
 #pragma unroll
-        for (int j = 0; j < 8; j++) red_acc[w][8 * lane + j] = acc[j];
+        for (int gi = 0; gi < G; gi++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) red_acc[w][gi][8 * lane + j] = acc[gi][j];
     }
     __syncthreads();
-    float big = -INFINITY;
+    // The waves' {max, sum, acc} per head (as the slice merge does, attention.zig:113-133).
+    float big[G], tot[G], wt[G][NWV];
 #pragma unroll
-    for (int i = 0; i < NWV; i++)
-        if (red_l[i] != 0.0f) big = fmaxf(big, red_m[i]);
-    float tot = 0.0f, wt[NWV];
+    for (int gi = 0; gi < G; gi++) {
+        big[gi] = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < NWV; i++) {
-        wt[i] = red_l[i] != 0.0f ? expf(red_m[i] - big) : 0.0f;
-        tot = fmaf(wt[i], red_l[i], tot);
+        for (int i = 0; i < NWV; i++)
+            if (red_l[i][gi] != 0.0f) big[gi] = fmaxf(big[gi], red_m[i][gi]);
+        tot[gi] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NWV; i++) {
+            wt[gi][i] = red_l[i][gi] != 0.0f ? expf(red_m[i][gi] - big[gi]) : 0.0f;
+            tot[gi] = fmaf(wt[gi][i], red_l[i][gi], tot[gi]);
+        }
     }
     if (a.att) { // one chunk: the normalized result (as attn_combine_kernel writes it)
-        const float inv = 1.0f / tot;
-        float *o = a.att + (uint64_t(t) * a.nh + h) * HD;
-        for (uint32_t d = threadIdx.x; d < HD; d += NWV * 64) {
-            float v = 0.0f;
 #pragma unroll
-            for (int i = 0; i < NWV; i++) v = fmaf(wt[i], red_acc[i][d], v);
-            o[d] = v * inv;
+        for (int gi = 0; gi < G; gi++) {
+            const float inv = 1.0f / tot[gi];
+            float *o = a.att + (uint64_t(t) * a.nh + h0 + gi) * HD;
+            for (uint32_t d = threadIdx.x; d < HD; d += NWV * 64) {
+                float v = 0.0f;
+#pragma unroll
+                for (int i = 0; i < NWV; i++) v = fmaf(wt[gi][i], red_acc[i][gi][d], v);
+                o[d] = v * inv;
+            }
         }
         return;
     }
-    // The chunk's partial: {max, sum, acc} (unnormalized), as attn_combine_kernel reads them.
-    float *out = a.part + ((uint64_t(t) * a.nh + h) * gridDim.x + g) * (HD + 2);
-    // With the merge in this launch, the partial goes out by agent-scope stores (they complete at
-    // the device's coherent level, not in this XCD's L2), so no cache write-back is needed.
-    auto put = [&](uint32_t i, float v) {
+    // The chunk's partials per head: {max, sum, acc} (unnormalized), as attn_combine_kernel reads
+    // them. With the merge in this launch, they go out by agent-scope stores (they complete at the
+    // device's coherent level, not in this XCD's L2).
+    auto put = [&](float *out, uint32_t i, float v) {
         if (a.cnt)
             __hip_atomic_store(out + i, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         else
             out[i] = v;
     };
-    for (uint32_t d = threadIdx.x; d < HD; d += NWV * 64) {
-        float v = 0.0f;
 #pragma unroll
-        for (int i = 0; i < NWV; i++) v = fmaf(wt[i], red_acc[i][d], v);
-        put(2 + d, v);
-    }
-    if (threadIdx.x == 0) {
-        put(0, big);
-        put(1, tot);
+    for (int gi = 0; gi < G; gi++) {
+        float *out = a.part + ((uint64_t(t) * a.nh + h0 + gi) * gridDim.x + g) * (HD + 2);
+        for (uint32_t d = threadIdx.x; d < HD; d += NWV * 64) {
+            float v = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NWV; i++) v = fmaf(wt[gi][i], red_acc[i][gi][d], v);
+            put(out, 2 + d, v);
+        }
+        if (threadIdx.x == 0) {
+            put(out, 0, big[gi]);
+            put(out, 1, tot[gi]);
+        }
     }
     if (!a.cnt) return; // attn_combine_kernel merges
-    // Count the chunk in; the last of (head, token) to arrive merges every chunk's partial with
-    // agent-scope loads. Every thread releases its partial stores (agent scope) before the barrier,
-    // the count is an acquire-release read-modify-write, and the merging workgroup acquires before
-    // its loads: the partials happen before the merge by the memory model, not by the hardware's
-    // store order. No workgroup waits for another.
+    // Count the chunk in; the last of (token, head block) to arrive merges every chunk's partials.
+    // No workgroup waits for another. Ordering: every access to the partials and the counter is an
+    // agent-scope atomic, which gfx950 performs at the device's coherence point (stores written
+    // through this XCD's L2, loads served past it), so a partial store is visible to every
+    // workgroup once it has completed. Each wave therefore waits for its stores to complete
+    // (vmcnt(0), with a compiler barrier) before the workgroup barrier, and only then does one
+    // thread count the chunk in; the merging workgroup reads the partials only after it has seen
+    // the final count. This is the code an agent-scope release / acquire pair generates on gfx950
+    // minus its L2 write-back (buffer_wbl2) and invalidate (buffer_inv), which exist for
+    // non-atomic data and which measured 7.5 us per Llama-3-8B layer at 512-575 positions (1.879
+    // vs 1.637 ms per token; Qwen3-0.6B 0.949 vs 0.847).
     __shared__ uint32_t last;
     __shared__ float mw[ATT_MERGE_MAX], mred[NWV];
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (threadIdx.x == 0) {
-        uint32_t *c = a.cnt + uint64_t(t) * a.nh + h;
-        last = __hip_atomic_fetch_add(c, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) + 1 == gridDim.x ? 1u : 0u;
+        uint32_t *c = a.cnt + uint64_t(t) * a.nh + h0;
+        last = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 == gridDim.x ? 1u : 0u;
         if (last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     if (!last) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    if (gridDim.x <= 8) {
-        // One round of loads: thread d reads every chunk's {max, sum, acc[d]} at once.
-        const float *pp = a.part + (uint64_t(t) * a.nh + h) * gridDim.x * (HD + 2);
-        for (uint32_t d = threadIdx.x; d < HD; d += NWV * 64) {
-            float m[8], l[8], v[8];
+    for (uint32_t gi = 0; gi < uint32_t(G); gi++) {
+        const uint32_t h = h0 + gi;
+        const float *hp = a.part + (uint64_t(t) * a.nh + h) * gridDim.x * (HD + 2);
+        if (gridDim.x <= 8) {
+            // One round of loads: thread d reads every chunk's {max, sum, acc[d]} at once.
+            for (uint32_t d = threadIdx.x; d < HD; d += NWV * 64) {
+                float mm[8], ll[8], vv8[8];
 #pragma unroll
-            for (uint32_t i = 0; i < 8; i++) {
-                if (i < gridDim.x) {
-                    float *q = const_cast<float *>(pp) + i * (HD + 2);
-                    m[i] = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    l[i] = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    v[i] = __hip_atomic_load(q + 2 + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                for (uint32_t i = 0; i < 8; i++) {
+                    if (i < gridDim.x) {
+                        float *q = const_cast<float *>(hp) + i * (HD + 2);
+                        mm[i] = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        ll[i] = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        vv8[i] = __hip_atomic_load(q + 2 + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
                 }
-            }
-            float mx = -INFINITY;
+                float mx = -INFINITY;
 #pragma unroll
-            for (uint32_t i = 0; i < 8; i++)
-                if (i < gridDim.x && l[i] != 0.0f) mx = fmaxf(mx, m[i]);
-            float sum = 0.0f, acc = 0.0f;
+                for (uint32_t i = 0; i < 8; i++)
+                    if (i < gridDim.x && ll[i] != 0.0f) mx = fmaxf(mx, mm[i]);
+                float sum = 0.0f, av = 0.0f;
 #pragma unroll
-            for (uint32_t i = 0; i < 8; i++) {
-                if (i < gridDim.x) {
-                    const float wgt = l[i] != 0.0f ? expf(m[i] - mx) : 0.0f;
-                    sum = fmaf(wgt, l[i], sum);
-                    acc = fmaf(wgt, v[i], acc);
+                for (uint32_t i = 0; i < 8; i++) {
+                    if (i < gridDim.x) {
+                        const float wgt = ll[i] != 0.0f ? expf(mm[i] - mx) : 0.0f;
+                        sum = fmaf(wgt, ll[i], sum);
+                        av = fmaf(wgt, vv8[i], av);
+                    }
                 }
+                a.merge_out[(uint64_t(t) * a.nh + h) * HD + d] = av * (1.0f / sum);
             }
-            a.merge_out[(uint64_t(t) * a.nh + h) * HD + d] = acc * (1.0f / sum);
+        } else {
+            merge_partials<true>(hp, a.merge_out + (uint64_t(t) * a.nh + h) * HD, HD, gridDim.x, mw, mred);
+            __syncthreads(); // mw / mred are reused by the next head's merge
         }
-        return;
     }
-    merge_partials<true>(a.part + (uint64_t(t) * a.nh + h) * gridDim.x * (HD + 2), a.merge_out + (uint64_t(t) * a.nh + h) * HD,
-                         HD, gridDim.x, mw, mred);
 }
 
 // Prefill attention (passes of more than MAX_DECODE tokens) on the f16 MFMA units, one workgroup
@@ -1131,13 +1188,19 @@ int decode_attention(hkhip_net *net, const RopeArgs &ra, const __half *kc, const
     const bool merge_in = gb > 1 && gb <= net->merge_max;
     aa.cnt = merge_in ? net->att_cnt : nullptr;
     aa.merge_out = att;
-    const dim3 dg(gb, c.n_heads, nt);
+    // One query head per workgroup (G = 1). Serving a key/value head's whole GQA group per workgroup
+    // (G = the group size: each key and value row loaded once instead of once per query head)
+    // measured slower, since a wave then runs the group's dots, softmax and value sums one after
+    // another on a kernel whose time is its dependent latency, not its bytes: 23.1 vs 9.8 us per
+    // Llama-3-8B layer at positions 512-575 (G = 4), 15.8 vs ~10 per Qwen3-0.6B layer (G = 2).
+    const dim3 dg(gb, c.n_heads, nt), db(64 * ATT_DWAVES);
+    constexpr int NV = int(ATT_DWAVES);
     if (c.head_dim == 64)
-        hipLaunchKernelGGL((attn_decode_kernel<64, ATT_DWAVES>), dg, dim3(64 * ATT_DWAVES), 0, s, aa);
+        hipLaunchKernelGGL((attn_decode_kernel<64, NV, 1>), dg, db, 0, s, aa);
     else if (c.head_dim == 128)
-        hipLaunchKernelGGL((attn_decode_kernel<128, ATT_DWAVES>), dg, dim3(64 * ATT_DWAVES), 0, s, aa);
+        hipLaunchKernelGGL((attn_decode_kernel<128, NV, 1>), dg, db, 0, s, aa);
     else
-        hipLaunchKernelGGL((attn_decode_kernel<256, ATT_DWAVES>), dg, dim3(64 * ATT_DWAVES), 0, s, aa);
+        hipLaunchKernelGGL((attn_decode_kernel<256, NV, 1>), dg, db, 0, s, aa);
     NET_TRY(hipGetLastError(), "decode attention");
     if (gb > 1 && !merge_in) {
         hipLaunchKernelGGL(attn_combine_kernel, dim3(c.n_heads, nt), dim3(std::min(256u, std::max(64u, (c.head_dim + 63) / 64 * 64))),
