@@ -327,23 +327,24 @@ hipError_t launch_mm(int t, const uint8_t *w, uint32_t rows, uint32_t cols, cons
 
 
 // Q6_K int8 operand planes. Four weights q (bytes in [0, 63]) of one 16-weight group with the
-// signed group scale sc: w = sc*(q - 32) lies in [-4096, 4096]; with x = w + 32 (16-bit lanes:
-// even and odd bytes through one packed multiply-add each, m = sc and k = 32 - 32*sc in both
-// halves), H = x >> 6 lies in [-63, 64] and L = 4*((x & 63) - 32) in [-128, 124], so that
-// 4*w = 256*H + L exactly. L's bytes are the low bytes of x << 2 with the top bit flipped.
+// signed group scale sc: w = sc*(q - 32) lies in [-4096, 4096]. In 16-bit lanes (the even and the
+// odd bytes of the word spread by one byte permute each, then one packed multiply-add each with
+// m = 4*sc and k = 128 - 128*sc in both halves) y = 4*w + 128 lies in [-16256, 16512]; its high
+// byte H = floor(y / 256) lies in [-64, 64] and its low byte minus 128, L, in [-128, 127], so that
+// 4*w = 256*H + L exactly: H is the high bytes of the four lanes and L their low bytes with the top
+// bit flipped, one byte permute each. (The same planes as x = w + 32, H = x >> 6, L = 4*((x & 63)
+// - 32), with six VALU instructions per word fewer.)
 __device__ __forceinline__ void q6k_planes(uint32_t q, uint32_t m, uint32_t k, int &H, int &L) {
     typedef unsigned short u2 __attribute__((ext_vector_type(2)));
-    typedef short s2 __attribute__((ext_vector_type(2)));
     const u2 mm = __builtin_bit_cast(u2, m), kk = __builtin_bit_cast(u2, k);
-    const u2 xe = __builtin_bit_cast(u2, q & 0x00FF00FFu) * mm + kk;
-    const u2 xo = __builtin_bit_cast(u2, (q >> 8) & 0x00FF00FFu) * mm + kk;
-    const u2 he = __builtin_bit_cast(u2, __builtin_bit_cast(s2, xe) >> s2{6, 6});
-    const u2 ho = __builtin_bit_cast(u2, __builtin_bit_cast(s2, xo) >> s2{6, 6});
-    const u2 le = xe << u2{2, 2}, lo = xo << u2{2, 2};
-    H = int(__builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, ho), __builtin_bit_cast(uint32_t, he), 0x06020400u));
-    L = int(__builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, le), 0x06020400u) ^ 0x80808080u);
+    const u2 ye = __builtin_bit_cast(u2, __builtin_amdgcn_perm(0u, q, 0x0C020C00u)) * mm + kk; // bytes 0, 2
+    const u2 yo = __builtin_bit_cast(u2, __builtin_amdgcn_perm(0u, q, 0x0C030C01u)) * mm + kk; // bytes 1, 3
+    const uint32_t e = __builtin_bit_cast(uint32_t, ye), o = __builtin_bit_cast(uint32_t, yo);
+    H = int(__builtin_amdgcn_perm(o, e, 0x07030501u));
+    L = int(__builtin_amdgcn_perm(o, e, 0x06020400u) ^ 0x80808080u);
 }
-// Both 16-bit halves of a word set to v's low 16 bits.
-__device__ __forceinline__ uint32_t half2_of(int v) { return (uint32_t(v) & 0xFFFFu) * 0x00010001u; }
+// q6k_planes' factors for the group scale sc.
+__device__ __forceinline__ uint32_t q6k_m(int sc) { return (uint32_t(4 * sc) & 0xFFFFu) * 0x00010001u; }
+__device__ __forceinline__ uint32_t q6k_k(int sc) { return (uint32_t(128 - 128 * sc) & 0xFFFFu) * 0x00010001u; }
 
 } // namespace hkhip

@@ -117,7 +117,7 @@ __device__ __forceinline__ void sk_step_q6k(const uint8_t *slot, const SkAct<NTT
         const int n = c >> 1;
         const uint32_t sidx = 8 * n + 4 * (c & 1) + 2 * (g >> 1) + (g & 1);
         const int sc = int(int8_t((scs[sidx / 4] >> (8 * (sidx % 4))) & 0xFF));
-        const uint32_t m = half2_of(sc), k = half2_of(32 - 32 * sc);
+        const uint32_t m = q6k_m(sc), k = q6k_k(sc);
         const uint32_t qs = 2 * (2 * (c & 1) + (g >> 1));
         const uint32_t lw[4] = {ql[n].x, ql[n].y, ql[n].z, ql[n].w};
         const uint32_t hw[4] = {qh[n].x, qh[n].y, qh[n].z, qh[n].w};

@@ -331,7 +331,7 @@ __global__ __launch_bounds__(NW * KS * 64, 1) void mmx_kernel(MxArgs a) {
                 const int n = c / 4, p = c % 4;
                 const uint32_t sbyte = 8 * n + 2 * p + h;
                 const int sc = int(int8_t((scs[sbyte / 4] >> (8 * (sbyte % 4))) & 0xFF));
-                const uint32_t m = half2_of(sc), k = half2_of(32 - 32 * sc);
+                const uint32_t m = q6k_m(sc), k = q6k_k(sc);
                 const uint32_t qlw[4] = {ql[n][p & 1].x, ql[n][p & 1].y, ql[n][p & 1].z, ql[n][p & 1].w};
                 const uint32_t qhw[4] = {qh[n].x, qh[n].y, qh[n].z, qh[n].w};
 #pragma unroll
