@@ -254,3 +254,29 @@ def test_separate_attention_merge(eng):
             items = seq_items(0, rng.integers(0, 256, k), p0) + seq_items(1, rng.integers(0, 256, 1), p1)
             p0, p1 = p0 + k, p1 + 1
             run_both(net, cpu, items, [k - 1, k], f"merge kernel, {k} + 1 tokens")
+
+
+def test_logits_of_many_rows(eng):
+    """logits(indices) for up to max_rows rows: 40 rows of a 48-token pass (the output product then
+    runs as a GEMM over the gathered rows), 12 rows gathered out of order (8-row decode passes), and a
+    request past max_rows refused."""
+    from hk_amd import HipError
+    from hk_amd.net import Net
+
+    cfg, fmt, out_fmt, qk_norm, bias = CFGS["qwen-q4k"]
+    model = synth.model_np(cfg, fmt, seed=5600, out_fmt=out_fmt, embd_fmt=F.Q8_0, qk_norm=qk_norm, bias=bias)
+    rng = np.random.default_rng(5601)
+    cpu = Oracle(cfg, model)
+    with Net(eng, cfg, Options(slots=2, n_batch=48)) as net:
+        net.load(model)
+        assert net.max_rows == 48
+        items = seq_items(1, rng.integers(0, cfg.vocab, 30), 0) + seq_items(2, rng.integers(0, cfg.vocab, 18), 0)
+        run_both(net, cpu, items, list(range(4, 44)), "40 rows")
+        rows = [47, 3, 29, 30, 0, 12, 40, 41, 5, 6, 33, 18]
+        got, want = net.logits_rows(rows), cpu.logits_rows(rows)
+        for r in range(len(rows)):
+            check(got[r], want[r], f"gathered row {rows[r]}")
+        with pytest.raises(HipError):
+            net.logits_rows(list(range(49)))
+        with pytest.raises(HipError):
+            net.logits_rows([48])
