@@ -280,3 +280,35 @@ def test_logits_of_many_rows(eng):
             net.logits_rows(list(range(49)))
         with pytest.raises(HipError):
             net.logits_rows([48])
+
+
+@pytest.mark.parametrize("device_layers", [1, 3])
+def test_partial_offload_then_cpu_rest(eng, device_layers):
+    """The reference's partial-offload test (tests/test_gpu.zig:350-408): a 4-layer model whose
+    leading layers run on the device and the rest on the CPU (from the handed-over hidden states,
+    each side with its own caches) gives the whole CPU forward's logits over an 18-token prompt and
+    six greedy decode steps."""
+    from hk_amd.net import Net
+
+    cfg = Config(dim=256, n_layers=4, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=512, vocab=300, max_ctx=64,
+                 rope_neox=True, rope_base=1e6)
+    model = synth.model_np(cfg, F.Q4_K, seed=5700, out_fmt=F.Q6_K, embd_fmt=F.Q8_0, qk_norm=True)
+    whole, rest = Oracle(cfg, model), Oracle(cfg, model)
+    prompt = [3, 17, 5, 5, 29, 0, 11, 8, 40, 41, 9, 12, 77, 3, 4, 90, 21, 33]
+    with Net(eng, cfg, Options(layers=device_layers)) as net:
+        net.load(model)
+        assert net.is_partial and net.layer_count == device_layers
+
+        def step(toks, pos0):
+            items = seq_items(0, toks, pos0)
+            h = net.forward_partial(items, whole.embed(toks))
+            rest.forward_items(items, hidden=h, first=device_layers)
+            whole.forward_items(items)
+            got, want = rest.logits_rows([len(toks) - 1])[0], whole.logits_rows([len(toks) - 1])[0]
+            check(got, want, f"{device_layers} device layers, pass of {len(toks)} at {pos0}")
+            return int(np.argmax(want))
+
+        tok, pos = step(prompt, 0), len(prompt)
+        for _ in range(6):
+            tok = step([tok], pos)
+            pos += 1
