@@ -312,3 +312,55 @@ def test_partial_offload_then_cpu_rest(eng, device_layers):
         for _ in range(6):
             tok = step([tok], pos)
             pos += 1
+
+
+def test_network_from_another_thread(eng):
+    """The reference's server case (tests/test_gpu.zig:446-478): a network loaded on one thread runs
+    its passes and logits from another, against the CPU forward."""
+    import threading
+
+    from hk_amd.net import Net
+
+    cfg, fmt, out_fmt, qk_norm, bias = CFGS["qwen-q4k"]
+    model = synth.model_np(cfg, fmt, seed=5800, out_fmt=out_fmt, embd_fmt=F.Q8_0, qk_norm=qk_norm, bias=bias)
+    cpu = Oracle(cfg, model)
+    out = {}
+    with Net(eng, cfg, Options(slots=1)) as net:
+        net.load(model)
+
+        def job():
+            try:
+                net.forward_items(seq_items(9, [3, 17, 5, 5, 29], 0))
+                out["first"] = net.logits_rows([4])[0]
+                net.forward_items(seq_items(9, [8], 5))
+                out["second"] = net.logits_rows([0])[0]
+            except Exception as e:  # reported on the main thread
+                out["error"] = e
+
+        th = threading.Thread(target=job)
+        th.start()
+        th.join()
+    assert "error" not in out, out.get("error")
+    cpu.forward_items(seq_items(9, [3, 17, 5, 5, 29], 0))
+    check(out["first"], cpu.logits_rows([4])[0], "prompt from another thread")
+    cpu.forward_items(seq_items(9, [8], 5))
+    check(out["second"], cpu.logits_rows([0])[0], "decode from another thread")
+
+
+def test_network_refuses_rows_not_whole_blocks(eng):
+    """The reference's odd-shape check (tests/test_gpu.zig:410-444): a layer whose rows are not a
+    whole number of 32 weights (dim 96 in Q4_K, 256-weight blocks) is refused at load with
+    UNSUPPORTED_SHAPE, not run."""
+    from hk_amd import HipError
+    from hk_amd.net import Net
+
+    cfg = Config(dim=96, n_layers=1, n_heads=1, n_kv_heads=1, head_dim=64, ffn_dim=256, vocab=64, max_ctx=16)
+    good = Config(dim=256, n_layers=1, n_heads=1, n_kv_heads=1, head_dim=64, ffn_dim=256, vocab=64, max_ctx=16)
+    model = synth.model_np(good, F.Q4_K, seed=5900)
+    layer = dict(model["layers"][0])
+    layer["attn_norm"] = np.ones(96, np.float32)
+    layer["ffn_norm"] = np.ones(96, np.float32)
+    with Net(eng, cfg) as net:
+        with pytest.raises(HipError) as e:
+            net.load_layer(0, layer)
+        assert e.value.code in (-2, -5)  # UNSUPPORTED_SHAPE (or the byte count that cannot match)
