@@ -1465,9 +1465,10 @@ uint64_t layer_dev_bytes(const hkhip_net_config &c, const hkhip_net_layer &l) {
     return total + m[0] + m[1] + m[2];
 }
 
+// A shape the network takes (max_ctx 0 too: the planner's base estimate, backend.zig:92-126).
 bool config_ok(const hkhip_net_config &c) {
     return c.dim && c.n_layers && c.n_heads && c.n_kv_heads && !(c.n_heads % c.n_kv_heads) && c.ffn_dim && c.vocab &&
-           c.max_ctx && (c.head_dim == 64 || c.head_dim == 128 || c.head_dim == 256) && !(c.rope_dim % 2) &&
+           (c.head_dim == 64 || c.head_dim == 128 || c.head_dim == 256) && !(c.rope_dim % 2) &&
            c.rope_dim <= c.head_dim;
 }
 

@@ -304,7 +304,8 @@ const float *hkhip_net_logits_dev(hkhip_net *net);
  * runtime, and the device bytes of one layer's tensors. Both count the device layouts (stacked
  * q/k/v, interleaved gate/up, split planes), the caches (keys, values and the transposed values
  * the prefill attention reads) and the pass buffers for max(n_batch, 8) tokens (64 when n_batch
- * is 0). 0 on a bad argument. hkhip_net_device_bytes: what a network holds now (bytes_needed without the margin,
+ * is 0). max_ctx may be 0 (the planner's base: bytes at n_ctx 0, then the per-position step from
+ * n_ctx 1). 0 on a bad argument. hkhip_net_device_bytes: what a network holds now (bytes_needed without the margin,
  * once every tensor is loaded and with n_batch set). */
 #define HKHIP_NET_MARGIN_BYTES (64ull << 20)
 uint64_t hkhip_net_bytes_needed(const hkhip_net_config *cfg, const hkhip_net_options *opts,

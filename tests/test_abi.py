@@ -92,3 +92,36 @@ def test_engine_init_reports_missing_device():
     h = ctypes.c_void_p()
     assert L.hkhip_init(0, ctypes.byref(h)) == -6
     assert L.hkhip_last_error()
+
+
+def test_network_bytes_needed_host_logic():
+    """hkhip_net_bytes_needed / hkhip_net_layer_bytes are host arithmetic (no device): the planner's
+    linear estimate base + n_ctx * per_ctx (backend.zig:92-126 probeCuda: bytesNeeded at n_ctx 0 and
+    1) never falls below the real figure; a second slot costs exactly its caches (keys, values and
+    the transposed values); a partial network holds only its layers (no embedding, norm or output);
+    unsupported shapes give 0."""
+    from hk_amd import formats as F, synth
+    from hk_amd.net import Config, Options, bytes_needed, layer_bytes
+
+    def cfg(ctx, **kw):
+        return Config(dim=256, n_layers=2, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=512, vocab=300, max_ctx=ctx, **kw)
+
+    model = synth.model_np(cfg(1), F.Q4_K, seed=11, out_fmt=F.Q6_K, embd_fmt=F.Q8_0, qk_norm=True, bias=True)
+    base, one = bytes_needed(cfg(0), model), bytes_needed(cfg(1), model)
+    assert base > 0 and one > base
+    for ctx in (7, 64, 100, 1000, 4096):
+        assert base + ctx * (one - base) >= bytes_needed(cfg(ctx), model), ctx
+    ctx = 1000
+    kv = 2 * 2 * 64  # layers x kv heads x head_dim
+    vt = (ctx + 31) // 32 * 32
+    assert bytes_needed(cfg(ctx), model, Options(slots=2)) - bytes_needed(cfg(ctx), model, Options(slots=1)) == \
+        kv * 2 * (2 * ctx + vt)
+    full = bytes_needed(cfg(ctx), model, Options(n_batch=64))
+    part = bytes_needed(cfg(ctx), model, Options(n_batch=64, layers=1))
+    lb = [layer_bytes(cfg(ctx), l) for l in model["layers"]]
+    assert all(b > 0 for b in lb)
+    io = F.matrix_bytes(F.Q8_0, 300, 256) + 4 * 256 + F.matrix_bytes(F.Q6_K, 300, 256)  # file bytes of the I/O tensors
+    assert full - part >= lb[1] + io  # the second layer, the I/O tensors (device layouts at least their file bytes), its caches
+    bad = cfg(ctx)
+    bad.head_dim = 96
+    assert bytes_needed(bad, model) == 0
