@@ -265,3 +265,27 @@ def test_net_many_attention_chunks(eng):
             net.forward(toks, pos)
             check(net.logits(), cpu.forward(toks, pos), f"many chunks: pass of {n} at {pos}")
             pos += n
+
+
+@pytest.mark.parametrize("fmt", [F.Q4_0, F.Q4_1, F.Q5_0, F.Q5_1, F.Q5_K, F.Q6_K, F.IQ4_XS, F.Q2_K, F.IQ2_XS, F.MXFP4,
+                                 F.NVFP4])
+def test_net_body_formats(eng, fmt):
+    """The network pass with its layers in each further format (the integer kernels' 32-weight and
+    K formats, and float-decode ones, NVFP4 on the f32 input): a prefill, then decode passes of 1, 3
+    and 8 tokens (the 8-token one on the small-batch kernel where the format has it), against the
+    CPU forward."""
+    from hk_amd.net import Net
+
+    cfg = Config(dim=256, n_layers=2, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=512, vocab=300, max_ctx=128,
+                 rope_neox=True, rope_base=1e6)
+    model = synth.model_np(cfg, fmt, seed=4900 + fmt, out_fmt=F.Q6_K, embd_fmt=F.Q8_0, qk_norm=True, bias=False)
+    rng = np.random.default_rng(4901)
+    cpu = Oracle(cfg, model)
+    with Net(eng, cfg) as net:
+        net.load(model)
+        pos = 0
+        for n in (20, 1, 3, 8, 1):
+            toks = rng.integers(0, cfg.vocab, n)
+            net.forward(toks, pos)
+            check(net.logits(), cpu.forward(toks, pos), f"{F.NAMES.get(fmt, hex(fmt))} body, pass of {n} at {pos}")
+            pos += n
