@@ -22,7 +22,9 @@ Also reported:
   extra         the decode step at batch 8 (config 4); config 5's batch-1 matvecs (IQ4_NL
                 14336x4096, Q6_K 4096x14336) rotating over at least 512 MB of matrices each; config 1 (the Q8_0
                 3072x1024 matvec, rotating over 160 copies); config 2 (a batch-1 decode step of a
-                Qwen3-0.6B-shaped decoder, tokens/s)
+                Qwen3-0.6B-shaped decoder, tokens/s); the whole-network pass on Qwen3-0.6B and
+                Llama-3-8B shapes (prefill, one-token decode, and 8 sequences decoded together in one
+                pass over their own cache slots, with and without reading their logits)
   measured_peaks  this GPU's dense int8 MFMA rate and HBM read rate from probe kernels
                 (hk_amd/csrc/peak.hip), quoted beside the published peaks the fractions use
   cpu_baseline  hk's CPU decode kernel restated with its SIMD paths (oracle/hk_cpu_simd.c, best
@@ -438,7 +440,7 @@ def network_bench(torch, eng, F, synth, which: str = "qwen3_0_6b"):
         own device copies: no layer reads another's), which keeps the host synthesis short."""
     import numpy as np
 
-    from hk_amd.net import Config, Net
+    from hk_amd.net import Config, Net, Options
     from hk_amd.rope import RopeScaling
 
     if which == "llama3_8b":
@@ -458,7 +460,7 @@ def network_bench(torch, eng, F, synth, which: str = "qwen3_0_6b"):
         model = synth.model_np(cfg, F.Q4_K, seed=synth.seed_for(2, 500), out_fmt=F.Q6_K, embd_fmt=F.Q6_K)
         n_layers_desc = "28 layers (dim 1024, GQA 16/8 with q/k norms, FFN 3072)"
     rng = np.random.default_rng(7)
-    with Net(eng, cfg) as net:
+    with Net(eng, cfg, Options(slots=9)) as net:
         net.load(model)
         del model
         prompt = rng.integers(0, cfg.vocab, 512)
@@ -474,9 +476,31 @@ def network_bench(torch, eng, F, synth, which: str = "qwen3_0_6b"):
             net.forward(toks[i:i + 1], 512 + i)
         dec_s = (time.perf_counter() - t0) / 64
         ok = bool(np.isfinite(net.logits()).all())
+        # hk's server case (kv.zig:22-29): 8 sequences, each prefilled to its own length (256 +
+        # 32 i), then decoded together, one token each per pass (forward(items)); the timed passes
+        # also read the 8 logit rows back to the host (logits(indices)).
+        lens = [256 + 32 * i for i in range(8)]
+        for i, ln in enumerate(lens):
+            net.forward_items([(1 + i, int(t), p) for p, t in enumerate(rng.integers(0, cfg.vocab, ln))])
+        step = lambda k: [(1 + i, int(rng.integers(0, cfg.vocab)), ln + k) for i, ln in enumerate(lens)]
+        for k in range(4):
+            net.forward_items(step(k))
+        t0 = time.perf_counter()
+        for k in range(4, 36):
+            net.forward_items(step(k))
+        multi_s = (time.perf_counter() - t0) / 32
+        t0 = time.perf_counter()
+        for k in range(36, 68):
+            net.forward_items(step(k))
+            rows = net.logits_rows(list(range(8)))
+        multi_lg_s = (time.perf_counter() - t0) / 32
+        ok = ok and bool(np.isfinite(rows).all())
     return {"prefill_512_ms": round(pre_s * 1e3, 2), "prefill_tokens_per_s": round(512 / pre_s, 1),
             "decode_ms_per_token": round(dec_s * 1e3, 3), "decode_tokens_per_s": round(1 / dec_s, 1),
             "context": "positions 512-575", "finite_logits": ok,
+            "sessions8_ms_per_pass": round(multi_s * 1e3, 3), "sessions8_tokens_per_s": round(8 / multi_s, 1),
+            "sessions8_with_logits_ms_per_pass": round(multi_lg_s * 1e3, 3),
+            "sessions8_context": "8 sequences at positions 260-515, one token each per pass",
             "what": f"whole network on the device: embedding, {n_layers_desc}: RMS norm fused into the products' "
                     "input quantization, rope, f16 KV cache, prefill attention on f16 MFMAs, decode attention over "
                     "context chunks; logits; host wall clock per forward call"}
