@@ -50,7 +50,7 @@ class NetTensor(ctypes.Structure):
 
 class NetOptions(ctypes.Structure):
     """hkhip_net_options (src/cuda/engine.zig:43-58 Options)."""
-    _fields_ = [(n, ctypes.c_uint32) for n in ("slots", "layers", "n_batch", "attn_merge_max")]
+    _fields_ = [(n, ctypes.c_uint32) for n in ("slots", "layers", "n_batch", "attn_merge_max", "attn_gqa")]
 
 
 class Item(ctypes.Structure):

@@ -367,6 +367,130 @@ __device__ __forceinline__ void norm_rope_row(float *h, const float (&x)[HD / 64
     wave_sync();
 }
 
+// The end of a decode attention workgroup, once its NWV waves' {max, sum, acc} of the ng (<= G)
+// query heads h0.. are in red_m / red_l / red_acc (LDS, after a barrier): merges them per head and
+// writes the normalized result (one chunk per (head, token)) or the chunk's partials, and the last
+// chunk of (token, head block) to arrive merges every chunk's partials when a.cnt is set.
+template <int HD, int NWV, int G>
+__device__ __forceinline__ void attn_decode_finish(const AttnArgs &a, uint32_t g, uint32_t t, uint32_t h0, uint32_t ng,
+                                                   const float (&red_m)[NWV][G], const float (&red_l)[NWV][G],
+                                                   const float (&red_acc)[NWV][G][HD]) {
+    // The waves' {max, sum, acc} per head (as the slice merge does, attention.zig:113-133).
+    float big[G], tot[G], wt[G][NWV];
+#pragma unroll
+    for (int gi = 0; gi < G; gi++) {
+        big[gi] = -INFINITY;
+        const bool on = uint32_t(gi) < ng; // LDS of the heads past ng is not written
+#pragma unroll
+        for (int i = 0; i < NWV; i++)
+            if (on && red_l[i][gi] != 0.0f) big[gi] = fmaxf(big[gi], red_m[i][gi]);
+        tot[gi] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NWV; i++) {
+            wt[gi][i] = on && red_l[i][gi] != 0.0f ? expf(red_m[i][gi] - big[gi]) : 0.0f;
+            tot[gi] = fmaf(wt[gi][i], red_l[i][gi], tot[gi]);
+        }
+    }
+    if (a.att) { // one chunk: the normalized result (as attn_combine_kernel writes it)
+#pragma unroll
+        for (int gi = 0; gi < G; gi++) {
+            if (uint32_t(gi) >= ng) break;
+            const float inv = 1.0f / tot[gi];
+            float *o = a.att + (uint64_t(t) * a.nh + h0 + gi) * HD;
+            for (uint32_t d = threadIdx.x; d < HD; d += NWV * 64) {
+                float v = 0.0f;
+#pragma unroll
+                for (int i = 0; i < NWV; i++) v = fmaf(wt[gi][i], red_acc[i][gi][d], v);
+                o[d] = v * inv;
+            }
+        }
+        return;
+    }
+    // The chunk's partials per head: {max, sum, acc} (unnormalized), as attn_combine_kernel reads
+    // them. With the merge in this launch, they go out by agent-scope stores (they complete at the
+    // device's coherent level, not in this XCD's L2).
+    auto put = [&](float *out, uint32_t i, float v) {
+        if (a.cnt)
+            __hip_atomic_store(out + i, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else
+            out[i] = v;
+    };
+#pragma unroll
+    for (int gi = 0; gi < G; gi++) {
+        if (uint32_t(gi) >= ng) break;
+        float *out = a.part + ((uint64_t(t) * a.nh + h0 + gi) * gridDim.x + g) * (HD + 2);
+        for (uint32_t d = threadIdx.x; d < HD; d += NWV * 64) {
+            float v = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NWV; i++) v = fmaf(wt[gi][i], red_acc[i][gi][d], v);
+            put(out, 2 + d, v);
+        }
+        if (threadIdx.x == 0) {
+            put(out, 0, big[gi]);
+            put(out, 1, tot[gi]);
+        }
+    }
+    if (!a.cnt) return; // attn_combine_kernel merges
+    // Count the chunk in; the last of (token, head block) to arrive merges every chunk's partials.
+    // No workgroup waits for another. Ordering: every access to the partials and the counter is an
+    // agent-scope atomic, which gfx950 performs at the device's coherence point (stores written
+    // through this XCD's L2, loads served past it), so a partial store is visible to every
+    // workgroup once it has completed. Each wave therefore waits for its stores to complete
+    // (vmcnt(0), with a compiler barrier) before the workgroup barrier, and only then does one
+    // thread count the chunk in; the merging workgroup reads the partials only after it has seen
+    // the final count. This is the code an agent-scope release / acquire pair generates on gfx950
+    // minus its L2 write-back (buffer_wbl2) and invalidate (buffer_inv), which exist for
+    // non-atomic data and which measured 7.5 us per Llama-3-8B layer at 512-575 positions (1.879
+    // vs 1.637 ms per token; Qwen3-0.6B 0.949 vs 0.847).
+    __shared__ uint32_t last;
+    __shared__ float mw[ATT_MERGE_MAX], mred[NWV];
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t *c = a.cnt + uint64_t(t) * a.nh + h0;
+        last = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 == gridDim.x ? 1u : 0u;
+        if (last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!last) return;
+    for (uint32_t gi = 0; gi < ng; gi++) {
+        const uint32_t h = h0 + gi;
+        const float *hp = a.part + (uint64_t(t) * a.nh + h) * gridDim.x * (HD + 2);
+        if (gridDim.x <= 8) {
+            // One round of loads: thread d reads every chunk's {max, sum, acc[d]} at once.
+            for (uint32_t d = threadIdx.x; d < HD; d += NWV * 64) {
+                float mm[8], ll[8], vv8[8];
+#pragma unroll
+                for (uint32_t i = 0; i < 8; i++) {
+                    if (i < gridDim.x) {
+                        float *q = const_cast<float *>(hp) + i * (HD + 2);
+                        mm[i] = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        ll[i] = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        vv8[i] = __hip_atomic_load(q + 2 + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
+                }
+                float mx = -INFINITY;
+#pragma unroll
+                for (uint32_t i = 0; i < 8; i++)
+                    if (i < gridDim.x && ll[i] != 0.0f) mx = fmaxf(mx, mm[i]);
+                float sum = 0.0f, av = 0.0f;
+#pragma unroll
+                for (uint32_t i = 0; i < 8; i++) {
+                    if (i < gridDim.x) {
+                        const float wgt = ll[i] != 0.0f ? expf(mm[i] - mx) : 0.0f;
+                        sum = fmaf(wgt, ll[i], sum);
+                        av = fmaf(wgt, vv8[i], av);
+                    }
+                }
+                a.merge_out[(uint64_t(t) * a.nh + h) * HD + d] = av * (1.0f / sum);
+            }
+        } else {
+            merge_partials<true>(hp, a.merge_out + (uint64_t(t) * a.nh + h) * HD, HD, gridDim.x, mw, mred);
+            __syncthreads(); // mw / mred are reused by the next head's merge
+        }
+    }
+}
+
 // G query heads h0 .. h0 + G - 1 that share one key/value head (G divides the group size: the
 // whole group, or 1) per workgroup, so each key and value row is loaded once for all of them.
 template <int HD, int NWV, int G>
@@ -571,117 +695,149 @@ __global__ __launch_bounds__(NWV * 64) void attn_decode_kernel(AttnArgs a) {
             for (int j = 0; j < 8; j++) red_acc[w][gi][8 * lane + j] = acc[gi][j];
     }
     __syncthreads();
-    // The waves' {max, sum, acc} per head (as the slice merge does, attention.zig:113-133).
-    float big[G], tot[G], wt[G][NWV];
+    attn_decode_finish<HD, NWV, G>(a, g, t, h0, G, red_m, red_l, red_acc);
+}
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// Decode attention of non-fused passes on the f16 MFMA units (v_mfma_f32_16x16x32_f16), one
+// workgroup per (chunk, block of ng <= 8 query heads sharing one key/value head, token): the key
+// and value rows of a position are loaded once for the whole block. Chunks, waves and the result
+// (partials, the in-launch merge) are as in attn_decode_kernel; wave w of chunk g takes the PB
+// blocks of 32 positions from p0 = 32 PB (g NWV + w), and being the only step of its wave, needs no
+// running rescale. Per block of 32 positions:
+//   S^T[pos][col] = K[pos] . Q[col]: A = key rows (f16, exact), B = the block's q rows split as
+//       f16 hi (columns 0..7, head = column) and lo = q - hi (columns 8..15), so that a score is
+//       column c's plus column c ^ 8's (q to ~2^-22, as attn_prefill_kernel does in two chains);
+//   O^T[dim][col] += V^T[dim][pos] . P[pos][col]: A = the transposed value cache, B = the
+//       probabilities split as f16 hi (columns 0..7) and lo (8..15).
+// The block's two score tiles take its key rows in the order that leaves lane (column c, group q)
+// holding positions 8q .. 8q + 7 of the block, exactly the k slots of the second product's B
+// operand, so the probabilities feed it without moving.
+template <int HD, int NWV, int PB>
+__global__ __launch_bounds__(NWV * 64) void attn_decode_gqa_kernel(AttnArgs a, uint32_t ng) {
+    constexpr int NS = HD / 32, NDT = HD / 16; // k steps of the scores, dimension tiles of the output
+    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const uint32_t c = lane & 15, qg = lane >> 4, hq = c & 7;
+    const uint32_t g = blockIdx.x, t = blockIdx.z;
+    const uint32_t grp = a.nh / a.nkv, h0 = blockIdx.y * ng, kvh = h0 / grp;
+    __shared__ float red_m[NWV][8], red_l[NWV][8];
+    __shared__ float red_acc[NWV][8][HD];
+    const uint64_t sl = a.slot[t];
+    const uint32_t pos = a.pos[t];
+    // q operands first (the memory counter is in order): lane (c, q) holds dimensions
+    // 32 s + 8 q .. + 8 of head hq's hi (c < 8) or lo part, zero for columns past the block.
+    v8h qb[NS];
+    {
+        const float *qrow = a.q + uint64_t(t) * a.sq + (h0 + (hq < ng ? hq : 0)) * HD + 8 * qg;
+        float4 x[NS][2];
 #pragma unroll
-    for (int gi = 0; gi < G; gi++) {
-        big[gi] = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < NWV; i++)
-            if (red_l[i][gi] != 0.0f) big[gi] = fmaxf(big[gi], red_m[i][gi]);
-        tot[gi] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < NWV; i++) {
-            wt[gi][i] = red_l[i][gi] != 0.0f ? expf(red_m[i][gi] - big[gi]) : 0.0f;
-            tot[gi] = fmaf(wt[gi][i], red_l[i][gi], tot[gi]);
+        for (int s = 0; s < NS; s++) {
+            x[s][0] = *reinterpret_cast<const float4 *>(qrow + 32 * s);
+            x[s][1] = *reinterpret_cast<const float4 *>(qrow + 32 * s + 4);
         }
-    }
-    if (a.att) { // one chunk: the normalized result (as attn_combine_kernel writes it)
 #pragma unroll
-        for (int gi = 0; gi < G; gi++) {
-            const float inv = 1.0f / tot[gi];
-            float *o = a.att + (uint64_t(t) * a.nh + h0 + gi) * HD;
-            for (uint32_t d = threadIdx.x; d < HD; d += NWV * 64) {
-                float v = 0.0f;
+        for (int s = 0; s < NS; s++) {
+            const float xs[8] = {x[s][0].x, x[s][0].y, x[s][0].z, x[s][0].w, x[s][1].x, x[s][1].y, x[s][1].z, x[s][1].w};
 #pragma unroll
-                for (int i = 0; i < NWV; i++) v = fmaf(wt[gi][i], red_acc[i][gi][d], v);
-                o[d] = v * inv;
+            for (int e = 0; e < 8; e++) {
+                const _Float16 hi = (_Float16)xs[e];
+                const _Float16 v = c < 8 ? hi : (_Float16)(xs[e] - (float)hi);
+                qb[s][e] = hq < ng ? v : (_Float16)0.0f;
             }
         }
-        return;
     }
-    // The chunk's partials per head: {max, sum, acc} (unnormalized), as attn_combine_kernel reads
-    // them. With the merge in this launch, they go out by agent-scope stores (they complete at the
-    // device's coherent level, not in this XCD's L2).
-    auto put = [&](float *out, uint32_t i, float v) {
-        if (a.cnt)
-            __hip_atomic_store(out + i, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        else
-            out[i] = v;
-    };
+    const uint32_t p0 = 32 * PB * (g * NWV + w), lastc = a.max_ctx - 1;
+    // Key rows: tile (b, u) row c is position 32 b + 8 (c / 4) + 4 u + c % 4; value rows: dimension
+    // 16 d + c, positions 32 b + 8 q .. + 8. Clamped to the caches only (rows past the token's
+    // position are masked; the caches start zeroed, so they are finite).
+    v8h ka[PB][2][NS], va[PB][NDT];
+    {
+        const __half *kb = a.kc + sl * a.kv_slot + uint64_t(kvh) * a.max_ctx * HD + 8 * qg;
+        const __half *vb = a.r.vt + sl * a.r.vt_slot + uint64_t(kvh) * HD * a.r.vt_stride + 8 * qg;
 #pragma unroll
-    for (int gi = 0; gi < G; gi++) {
-        float *out = a.part + ((uint64_t(t) * a.nh + h0 + gi) * gridDim.x + g) * (HD + 2);
-        for (uint32_t d = threadIdx.x; d < HD; d += NWV * 64) {
-            float v = 0.0f;
+        for (int b = 0; b < PB; b++) {
 #pragma unroll
-            for (int i = 0; i < NWV; i++) v = fmaf(wt[gi][i], red_acc[i][gi][d], v);
-            put(out, 2 + d, v);
-        }
-        if (threadIdx.x == 0) {
-            put(out, 0, big[gi]);
-            put(out, 1, tot[gi]);
-        }
-    }
-    if (!a.cnt) return; // attn_combine_kernel merges
-    // Count the chunk in; the last of (token, head block) to arrive merges every chunk's partials.
-    // No workgroup waits for another. Ordering: every access to the partials and the counter is an
-    // agent-scope atomic, which gfx950 performs at the device's coherence point (stores written
-    // through this XCD's L2, loads served past it), so a partial store is visible to every
-    // workgroup once it has completed. Each wave therefore waits for its stores to complete
-    // (vmcnt(0), with a compiler barrier) before the workgroup barrier, and only then does one
-    // thread count the chunk in; the merging workgroup reads the partials only after it has seen
-    // the final count. This is the code an agent-scope release / acquire pair generates on gfx950
-    // minus its L2 write-back (buffer_wbl2) and invalidate (buffer_inv), which exist for
-    // non-atomic data and which measured 7.5 us per Llama-3-8B layer at 512-575 positions (1.879
-    // vs 1.637 ms per token; Qwen3-0.6B 0.949 vs 0.847).
-    __shared__ uint32_t last;
-    __shared__ float mw[ATT_MERGE_MAX], mred[NWV];
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        uint32_t *c = a.cnt + uint64_t(t) * a.nh + h0;
-        last = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 == gridDim.x ? 1u : 0u;
-        if (last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    if (!last) return;
-    for (uint32_t gi = 0; gi < uint32_t(G); gi++) {
-        const uint32_t h = h0 + gi;
-        const float *hp = a.part + (uint64_t(t) * a.nh + h) * gridDim.x * (HD + 2);
-        if (gridDim.x <= 8) {
-            // One round of loads: thread d reads every chunk's {max, sum, acc[d]} at once.
-            for (uint32_t d = threadIdx.x; d < HD; d += NWV * 64) {
-                float mm[8], ll[8], vv8[8];
+            for (int u = 0; u < 2; u++) {
+                const uint32_t kp = p0 + 32 * b + 8 * (c >> 2) + 4 * u + (c & 3);
+                const __half *krow = kb + uint64_t(kp < lastc ? kp : lastc) * HD;
 #pragma unroll
-                for (uint32_t i = 0; i < 8; i++) {
-                    if (i < gridDim.x) {
-                        float *q = const_cast<float *>(hp) + i * (HD + 2);
-                        mm[i] = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        ll[i] = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        vv8[i] = __hip_atomic_load(q + 2 + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    }
-                }
-                float mx = -INFINITY;
-#pragma unroll
-                for (uint32_t i = 0; i < 8; i++)
-                    if (i < gridDim.x && ll[i] != 0.0f) mx = fmaxf(mx, mm[i]);
-                float sum = 0.0f, av = 0.0f;
-#pragma unroll
-                for (uint32_t i = 0; i < 8; i++) {
-                    if (i < gridDim.x) {
-                        const float wgt = ll[i] != 0.0f ? expf(mm[i] - mx) : 0.0f;
-                        sum = fmaf(wgt, ll[i], sum);
-                        av = fmaf(wgt, vv8[i], av);
-                    }
-                }
-                a.merge_out[(uint64_t(t) * a.nh + h) * HD + d] = av * (1.0f / sum);
+                for (int s = 0; s < NS; s++) ka[b][u][s] = *reinterpret_cast<const v8h *>(krow + 32 * s);
             }
-        } else {
-            merge_partials<true>(hp, a.merge_out + (uint64_t(t) * a.nh + h) * HD, HD, gridDim.x, mw, mred);
-            __syncthreads(); // mw / mred are reused by the next head's merge
+            const uint32_t vp = min(p0 + 32 * b, a.r.vt_stride - 32);
+#pragma unroll
+            for (int d = 0; d < NDT; d++)
+                va[b][d] = *reinterpret_cast<const v8h *>(vb + uint64_t(16 * d + c) * a.r.vt_stride + vp);
         }
     }
+    // Every row in flight before the first use (the compiler would otherwise sink each load next
+    // to its product).
+#pragma unroll
+    for (int b = 0; b < PB; b++) {
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+#pragma unroll
+            for (int s = 0; s < NS; s++) asm volatile("" : "+v"(ka[b][u][s]));
+#pragma unroll
+        for (int d = 0; d < NDT; d++) asm volatile("" : "+v"(va[b][d]));
+    }
+    float mx = -INFINITY, lsum = 0.0f;
+    v4f o[NDT];
+#pragma unroll
+    for (int d = 0; d < NDT; d++) o[d] = v4f{};
+    if (p0 <= pos) {
+        float sv[PB][8];
+#pragma unroll
+        for (int b = 0; b < PB; b++)
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                v4f sc = v4f{};
+#pragma unroll
+                for (int s = 0; s < NS; s++) sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[b][u][s], qb[s], sc, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float v = sc[i] + dpp_f<DPP_ROR8>(sc[i]); // hi + lo columns
+                    const uint32_t pp = p0 + 32 * b + 8 * qg + 4 * u + i;
+                    sv[b][4 * u + i] = pp <= pos ? v * a.scale : -INFINITY;
+                    mx = fmaxf(mx, sv[b][4 * u + i]);
+                }
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32)); // finite: position p0 is unmasked
+        v8h pb[PB];
+#pragma unroll
+        for (int b = 0; b < PB; b++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float p = expf(sv[b][e] - mx); // 0 where masked
+                lsum += p;
+                const _Float16 hi = (_Float16)p;
+                pb[b][e] = c < 8 ? hi : (_Float16)(p - (float)hi);
+            }
+        lsum += __shfl_xor(lsum, 16);
+        lsum += __shfl_xor(lsum, 32);
+#pragma unroll
+        for (int b = 0; b < PB; b++)
+#pragma unroll
+            for (int d = 0; d < NDT; d++) o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[b][d], pb[b], o[d], 0, 0, 0);
+    }
+    // Lane (c, q) holds dimensions 16 d + 4 q + i of column c: a head's sums are columns c and c ^ 8.
+#pragma unroll
+    for (int d = 0; d < NDT; d++) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float v = o[d][i] + dpp_f<DPP_ROR8>(o[d][i]);
+            if (c < ng) red_acc[w][c][16 * d + 4 * qg + i] = v;
+        }
+    }
+    if (qg == 0 && c < ng) {
+        red_m[w][c] = mx;
+        red_l[w][c] = lsum;
+    }
+    __syncthreads();
+    attn_decode_finish<HD, NWV, 8>(a, g, t, h0, ng, red_m, red_l, red_acc);
 }
 
 // Prefill attention (passes of more than MAX_DECODE tokens) on the f16 MFMA units, one workgroup
@@ -698,9 +854,6 @@ __global__ __launch_bounds__(NWV * 64) void attn_decode_kernel(AttnArgs a) {
 // The key rows are loaded in the order rho (bits 2 and 3 of the row swapped), which puts each
 // lane half's 16 scores exactly on the 8 + 8 positions the second product's B operand needs, so
 // the probabilities go from the first product's output to the second's input without moving.
-typedef _Float16 v8h __attribute__((ext_vector_type(8)));
-typedef float v16f __attribute__((ext_vector_type(16)));
-
 struct AttnPArgs {
     const float *q;
     const __half *kc, *vt; // this layer's key cache [nkv][max_ctx][hd], value cache transposed [nkv][hd][vt_stride], slot 0
@@ -922,7 +1075,7 @@ struct hkhip_net {
     hkhip_net_config cfg;
     uint32_t n_dev = 0;   // layers on the device
     bool partial = false; // only the leading layers (no embedding, final norm or output)
-    uint32_t n_slots = 1, n_batch = 0, max_rows = 64, merge_max = ATT_MERGE_MAX;
+    uint32_t n_slots = 1, n_batch = 0, max_rows = 64, merge_max = ATT_MERGE_MAX, gqa = 0;
     struct Layer {
         // q, k and v rows stacked (one product, one output row per token) when the three share their
         // type; else three products into three regions of the q/k/v buffer.
@@ -1172,6 +1325,28 @@ int product(hkhip_net *net, uint32_t n, const hkhip_mat *mats, uint32_t nparts, 
     return rc ? rc : gemms(net, n, mats, nparts, ys, biases, mode);
 }
 
+// Query heads per workgroup of the grouped attention kernel: the largest divisor of the GQA group
+// size up to 8 (the MFMA tile's hi / lo column halves).
+uint32_t group_block(const hkhip_net_config &c) {
+    const uint32_t grp = c.n_heads / c.n_kv_heads;
+    uint32_t ng = 8;
+    while (grp % ng) ng--;
+    return ng;
+}
+
+// Whether nt tokens' decode attention over gb chunks runs on the grouped MFMA kernel
+// (attn_decode_gqa_kernel). By size: once the per-head kernel's waves (2 gb heads nt, two per
+// chunk) pass 2048, about one round at its ~150 registers, where it was measured to fall behind:
+// per Llama-3-8B-shaped layer (32 / 8 heads), 8 tokens at 800 positions 23.3 vs 17.4 us, at 1600
+// 44.0 vs 30.5, at 3000 97.6 vs 50.3; below, the per-head kernel is as fast or up to 2 us faster
+// (8 tokens at <= 128 positions 7.2 vs 8.6, 2 tokens at 800 10.3 vs 12.6; Qwen3-0.6B-shaped,
+// 16 / 8 heads: 8 tokens at 800 14.1 vs 15.4, at 1600 27.4 vs 24.4).
+bool grouped_attention(const hkhip_net *net, uint32_t nt, uint32_t gb) {
+    const hkhip_net_config &c = net->cfg;
+    if (net->gqa == 2 || (c.head_dim != 64 && c.head_dim != 128)) return false;
+    return net->gqa == 1 || uint64_t(2) * gb * c.n_heads * nt > 2048;
+}
+
 // Decode attention over tokens [t0, t0 + nt) of the pass (nt <= MAX_DECODE), gb chunks per
 // (head, token). fused: a one-token pass whose attention kernel also does the head norms, the
 // rotation and the cache writes (ra's fields).
@@ -1188,19 +1363,27 @@ int decode_attention(hkhip_net *net, const RopeArgs &ra, const __half *kc, const
     const bool merge_in = gb > 1 && gb <= net->merge_max;
     aa.cnt = merge_in ? net->att_cnt : nullptr;
     aa.merge_out = att;
-    // One query head per workgroup (G = 1). Serving a key/value head's whole GQA group per workgroup
-    // (G = the group size: each key and value row loaded once instead of once per query head)
-    // measured slower, since a wave then runs the group's dots, softmax and value sums one after
-    // another on a kernel whose time is its dependent latency, not its bytes: 23.1 vs 9.8 us per
-    // Llama-3-8B layer at positions 512-575 (G = 4), 15.8 vs ~10 per Qwen3-0.6B layer (G = 2).
-    const dim3 dg(gb, c.n_heads, nt), db(64 * ATT_DWAVES);
+    // The per-head kernel (G = 1) or, past one round of its waves, the grouped MFMA kernel (see
+    // grouped_attention). The per-head kernel's FMA form with G = the group size measured slower
+    // (a wave runs the group's dots, softmax and value sums one after another: 23.1 vs 9.8 us per
+    // Llama-3-8B layer at positions 512-575, G = 4).
     constexpr int NV = int(ATT_DWAVES);
+    if (!fused && grouped_attention(net, nt, gb)) {
+        const uint32_t ng = group_block(c);
+        const dim3 gg(gb, c.n_heads / ng, nt);
+        if (c.head_dim == 64)
+            hipLaunchKernelGGL((attn_decode_gqa_kernel<64, NV, 2>), gg, dim3(64 * NV), 0, s, aa, ng);
+        else
+            hipLaunchKernelGGL((attn_decode_gqa_kernel<128, NV, 2>), gg, dim3(64 * NV), 0, s, aa, ng);
+    } else {
+    const dim3 dg(gb, c.n_heads, nt), db(64 * ATT_DWAVES);
     if (c.head_dim == 64)
         hipLaunchKernelGGL((attn_decode_kernel<64, NV, 1>), dg, db, 0, s, aa);
     else if (c.head_dim == 128)
         hipLaunchKernelGGL((attn_decode_kernel<128, NV, 1>), dg, db, 0, s, aa);
     else
         hipLaunchKernelGGL((attn_decode_kernel<256, NV, 1>), dg, db, 0, s, aa);
+    }
     NET_TRY(hipGetLastError(), "decode attention");
     if (gb > 1 && !merge_in) {
         hipLaunchKernelGGL(attn_combine_kernel, dim3(c.n_heads, nt), dim3(std::min(256u, std::max(64u, (c.head_dim + 63) / 64 * 64))),
@@ -1254,8 +1437,8 @@ int run_pass(hkhip_net *net, uint32_t n, uint32_t gb, bool lg) {
                     c.head_dim, c.rope_dim / 2, c.rope_neox, c.max_ctx, vt_stride(c), S, SKV, 0, c.rope_mscale,
                     c.rms_eps};
         // Prefill passes write the value heads with v_cache_block (coalesced transposed writes);
-        // one-token passes do all of it in the attention kernel.
-        const bool vsep = n > MAX_DECODE, fused = n == 1;
+        // one-token passes on the per-head kernel do all of it in the attention kernel.
+        const bool vsep = n > MAX_DECODE, fused = n == 1 && !grouped_attention(net, 1, gb);
         ra.nheads = c.n_heads + (vsep ? 1 : 2) * c.n_kv_heads;
         if (vsep) { // one launch: rope / key writes, then the value rows
             ra.ntok = n;
@@ -1497,6 +1680,11 @@ int hkhip_net_create_opts(hkhip_engine *eng, const hkhip_net_config *cfg, const 
     n->n_batch = o.n_batch;
     n->max_rows = max_rows_of(o);
     n->merge_max = o.attn_merge_max ? std::min(o.attn_merge_max, ATT_MERGE_MAX) : ATT_MERGE_MAX;
+    if (o.attn_gqa > 2) {
+        delete n;
+        return set_error(HKHIP_E_BAD_ARGUMENT, "attn_gqa %u: 0, 1 or 2", o.attn_gqa);
+    }
+    n->gqa = o.attn_gqa;
     n->layers.resize(n->n_dev);
     n->owner.assign(n->n_slots, 0);
     n->used.assign(n->n_slots, 0);

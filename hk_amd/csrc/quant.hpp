@@ -21,6 +21,7 @@ constexpr int DPP_XOR1 = 0xB1;        // quad_perm [1,0,3,2]
 constexpr int DPP_XOR2 = 0x4E;        // quad_perm [2,3,0,1]
 constexpr int DPP_HALF_MIRROR = 0x141; // lane i <-> 7-i within 8
 constexpr int DPP_MIRROR = 0x140;      // lane i <-> 15-i within 16
+constexpr int DPP_ROR8 = 0x128;        // lane i <-> i ^ 8 within 16 (rotate by 8)
 
 template <int CTRL> __device__ __forceinline__ float dpp_f(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));

@@ -65,9 +65,10 @@ class Options:
     layers: int = 0          # leading layers on the device; 0: all (fewer: a partial network)
     n_batch: int = 0         # most tokens per pass (0: buffers grown on demand)
     attn_merge_max: int = 0  # test knob: decode attention chunks merged inside the launch (0: 256)
+    attn_gqa: int = 0        # decode attention kernel: 0 by size, 1 grouped (GQA, MFMA), 2 per head
 
     def c(self) -> NetOptions:
-        return NetOptions(self.slots, self.layers, self.n_batch, self.attn_merge_max)
+        return NetOptions(self.slots, self.layers, self.n_batch, self.attn_merge_max, self.attn_gqa)
 
 
 def _items(items) -> tuple:

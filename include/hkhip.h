@@ -242,6 +242,11 @@ typedef struct hkhip_net_options {
     /* Test knob (as the CUDA engine's slice_positions, engine.zig:268): most decode attention
      * chunks merged inside the attention launch; more go through the separate merge kernel (0: 256). */
     uint32_t attn_merge_max;
+    /* Decode attention kernel (a tuning knob, results equal to rounding): 0 chooses by size (the
+     * grouped kernel, one workgroup per key/value head serving its query heads on the MFMA units,
+     * once the per-head kernel would need more waves than the GPU runs at once); 1 the grouped
+     * kernel whenever the head dim allows it (64 or 128); 2 the per-head kernel. */
+    uint32_t attn_gqa;
 } hkhip_net_options;
 /* A tensor in hk's file layout in host memory; data NULL for an absent optional tensor. */
 typedef struct hkhip_net_tensor {

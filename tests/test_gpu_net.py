@@ -11,7 +11,7 @@ import pytest
 
 from hk_amd import formats as F
 from hk_amd import synth
-from hk_amd.net import Config
+from hk_amd.net import Config, Options
 from oracle.net_oracle import Oracle
 
 pytestmark = pytest.mark.gpu
@@ -64,7 +64,8 @@ CASES = {
 
 
 @pytest.mark.parametrize("case", list(CASES))
-def test_net_passes_match_cpu(eng, case):
+@pytest.mark.parametrize("gqa", [0, 1], ids=["attn-by-size", "attn-grouped"])
+def test_net_passes_match_cpu(eng, case, gqa):
     from hk_amd.net import Net
 
     cfg, fmt, out_fmt, embd_fmt, qk_norm, bias = CASES[case]
@@ -72,7 +73,7 @@ def test_net_passes_match_cpu(eng, case):
                            bias=bias)
     rng = np.random.default_rng(4100)
     cpu = Oracle(cfg, model)
-    with Net(eng, cfg) as net:
+    with Net(eng, cfg, Options(attn_gqa=gqa)) as net:
         net.load(model)
         pos = 0
         # prefill past the first attention slice, then decode passes; repeated sizes replay graphs
@@ -94,6 +95,8 @@ def test_net_rejects(eng):
     cfg = Config(dim=256, n_layers=1, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=256, vocab=64, max_ctx=16)
     with pytest.raises(HipError):
         Net(eng, Config(dim=256, n_layers=1, n_heads=4, n_kv_heads=2, head_dim=96, ffn_dim=256, vocab=64, max_ctx=16))
+    with pytest.raises(HipError):
+        Net(eng, cfg, Options(attn_gqa=3))  # no such attention kernel choice
     model = synth.model_np(cfg, F.Q4_K, seed=4200)
     with Net(eng, cfg) as net:
         with pytest.raises(HipError):
@@ -138,7 +141,8 @@ def test_net_from_hk_file(eng, tmp_path, arch, fmt, tie, vec_type):
             net.close()
 
 
-def test_net_long_context(eng):
+@pytest.mark.parametrize("gqa", [0, 1], ids=["attn-by-size", "attn-grouped"])
+def test_net_long_context(eng, gqa):
     """Decode passes past 1030 positions, where decode attention runs over nine chunk workgroups
     of 128 positions per (head, token) and their merge (one-token passes fused with the key/value
     writes, passes of 3 and 8 tokens after the separate rope / cache kernel); a prefill of 1030
@@ -151,7 +155,7 @@ def test_net_long_context(eng):
     rng = np.random.default_rng(4501)
     cpu = Oracle(cfg, model)
     worst = 0.0
-    with Net(eng, cfg) as net:
+    with Net(eng, cfg, Options(attn_gqa=gqa)) as net:
         net.load(model)
         pos = 0
         for n in [1030, 1, 1, 3, 8, 8, 1]:
@@ -217,7 +221,8 @@ def test_net_rope_scaling(eng, kind):
             pos += n
 
 
-def test_net_attention_chunk_boundaries(eng):
+@pytest.mark.parametrize("gqa", [0, 1], ids=["attn-by-size", "attn-grouped"])
+def test_net_attention_chunk_boundaries(eng, gqa):
     """Decode passes stepping across the context sizes where the attention chunk count changes (one
     chunk of 128 positions per (head, token) up to 128, then 2, 4 and 8 by 256, 512 and 1024): each chunk count is
     its own captured graph, the one-chunk passes write the attention output directly and the
@@ -230,7 +235,7 @@ def test_net_attention_chunk_boundaries(eng):
     model = synth.model_np(cfg, F.Q4_K, seed=4800, out_fmt=F.Q8_0, embd_fmt=F.Q8_0, qk_norm=True, bias=False)
     rng = np.random.default_rng(4801)
     cpu = Oracle(cfg, model)
-    with Net(eng, cfg) as net:
+    with Net(eng, cfg, Options(attn_gqa=gqa)) as net:
         net.load(model)
         pos = 0
         # 252 by prefill, then passes of 1 and 3 tokens over 256 (chunk counts 2 -> 4), a prefill to
@@ -243,7 +248,8 @@ def test_net_attention_chunk_boundaries(eng):
             pos += n
 
 
-def test_net_many_attention_chunks(eng):
+@pytest.mark.parametrize("gqa", [0, 1], ids=["attn-by-size", "attn-grouped"])
+def test_net_many_attention_chunks(eng, gqa):
     """Decode passes past 1024 positions, where decode attention runs over more than eight chunk
     workgroups of 128 positions per (head, token): the last chunk to finish merges the others'
     partials with the general merge (two rounds of loads; up to eight chunks it takes the one-round
@@ -255,7 +261,7 @@ def test_net_many_attention_chunks(eng):
     model = synth.model_np(cfg, F.Q8_0, seed=4900, out_fmt=F.Q8_0, embd_fmt=F.Q8_0, qk_norm=True, bias=False)
     rng = np.random.default_rng(4901)
     cpu = Oracle(cfg, model)
-    with Net(eng, cfg) as net:
+    with Net(eng, cfg, Options(attn_gqa=gqa)) as net:
         net.load(model)
         pos = 0
         # 1020 by prefill, passes over 1024 (8 -> 16 chunks), a prefill to 2035, passes over 2048

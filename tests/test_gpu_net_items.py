@@ -76,7 +76,8 @@ CFGS = {
 
 
 @pytest.mark.parametrize("case", list(CFGS))
-def test_items_of_several_sequences(eng, case):
+@pytest.mark.parametrize("gqa", [0, 1], ids=["attn-by-size", "attn-grouped"])
+def test_items_of_several_sequences(eng, case, gqa):
     """Three sequences in passes that mix them: a prefill of one beside single tokens of the others
     (the GEMM path, MFMA attention over the long run, decode attention for the rest), decode passes of
     3-7 tokens over all three (graph replays with per-item slots and positions), two tokens of each of
@@ -98,7 +99,7 @@ def test_items_of_several_sequences(eng, case):
         pos[seq] += k
         return items
 
-    with Net(eng, cfg, Options(slots=3)) as net:
+    with Net(eng, cfg, Options(slots=3, attn_gqa=gqa)) as net:
         net.load(model)
         assert net.max_rows == 64 and net.layer_count == cfg.n_layers and not net.is_partial
         run_both(net, cpu, take("a", 40), [39, 0], f"{case} prefill a")
@@ -230,7 +231,8 @@ def test_bytes_needed_matches_the_allocations(eng, layers):
             net.forward_items([(1, 0, i) for i in range(97)])
 
 
-def test_separate_attention_merge(eng):
+@pytest.mark.parametrize("gqa", [0, 1], ids=["attn-by-size", "attn-grouped"])
+def test_separate_attention_merge(eng, gqa):
     """Decode passes whose attention chunk count is above the in-launch merge's limit (lowered to 2 by
     the options' test knob, as the CUDA engine's slice_positions knob does) run the separate merge
     kernel: one-token passes (keys and values written inside the attention kernel), passes of 3 and
@@ -242,7 +244,7 @@ def test_separate_attention_merge(eng):
     model = synth.model_np(cfg, F.Q8_0, seed=5500, out_fmt=F.Q8_0, embd_fmt=F.Q8_0, qk_norm=True)
     rng = np.random.default_rng(5501)
     cpu = Oracle(cfg, model)
-    with Net(eng, cfg, Options(slots=2, attn_merge_max=2)) as net:
+    with Net(eng, cfg, Options(slots=2, attn_merge_max=2, attn_gqa=gqa)) as net:
         net.load(model)
         run_both(net, cpu, seq_items(0, rng.integers(0, 256, 700), 0), [699], "prefill 700")
         run_both(net, cpu, seq_items(1, rng.integers(0, 256, 300), 0), [299], "prefill 300")
