@@ -37,10 +37,20 @@ namespace {
 constexpr uint32_t ATT_SLICE = 64;      // positions per wave step of the decode attention
 constexpr uint32_t MAX_DECODE = 8;      // tokens of a pass that runs the decode kernels (and a graph)
 constexpr uint32_t ATT_MERGE_MAX = 256; // decode attention chunks the in-launch merge takes (more: attn_combine_kernel)
+// Floats per decode attention chunk's {max, sum} pair, and 32-bit words per chunk counter: one
+// 128-byte line each, since chunk workgroups on different XCDs write them through to the coherence
+// point and writers sharing a line were measured to slow the pass (packed pairs: 1.664-1.670 vs
+// 1.624-1.632 ms per Llama-3-8B token, 0.880-0.882 vs 0.806-0.830 per Qwen3-0.6B token; padded
+// counters: 8 sequences per pass 2.839-2.870 vs 2.875-2.883 ms).
+constexpr uint32_t ATT_ML = 32, ATT_CNT = 32;
 
 // ---------------------------------------------------------------------------------------------
 // Kernels
 // ---------------------------------------------------------------------------------------------
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float block_sum(float v, float *red) {
     for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
@@ -209,7 +219,7 @@ __global__ __launch_bounds__(256) void rope_kv_v_kernel(RopeArgs a, const float 
 struct AttnArgs {
     const float *q; // stride sq floats per token
     const __half *kc, *vc; // this layer of slot 0
-    float *part;
+    float *part; // chunk partials' sums (part_ml below)
     const uint32_t *pos, *slot;
     uint64_t kv_slot; // halves between slots
     uint32_t n, nh, nkv, hd, max_ctx;
@@ -226,6 +236,9 @@ struct AttnArgs {
     // partials into merge_out itself (cnt: one counter per (token, head), zero between launches).
     uint32_t *cnt;
     float *merge_out;
+    // The chunk partials: part holds the unnormalized sums [token][head][chunk][hd], part_ml the
+    // {max, sum} pairs [token][head][chunk][2].
+    float *part_ml;
 };
 
 // A lane's DL dimensions of one value row: DL halves in one (DL = 1: the low half) or two words.
@@ -287,49 +300,107 @@ __device__ __forceinline__ float wave_max_f(float v) {
     return fmaxf(fmaxf(readlane_f(r, 0), readlane_f(r, 16)), fmaxf(readlane_f(r, 32), readlane_f(r, 48)));
 }
 
-// o[0..hd) = merge of nslice partials {max, sum, acc[hd]} at p (attention.zig:113-133 merge): every
-// thread reads one slice's {max, sum} (all loads in flight at once), the block reduces them, the
-// weights exp(m_s - max m) of the non-empty slices go to LDS (wts), then thread d sums its
-// dimension over the slices with the loads of eight slices issued together. red: one float per wave.
-// COH: the partials come from other workgroups of the same launch (agent-scope loads).
-template <bool COH = false>
-__device__ __forceinline__ void merge_partials(const float *p, float *o, uint32_t hd, uint32_t nslice, float *wts,
-                                               float *red) {
-    auto ld = [&](uint64_t i) -> float {
+// 16 bytes at p read at the device's coherence point, not from this XCD's L2 (the agent-scope
+// load's sc1 bit, as the compiler emits for __hip_atomic_load at agent scope, here on a 16-byte
+// load). The compiler does not track this load: the value may be used only after wait_loads().
+__device__ __forceinline__ v4f load_coherent4(const float *p) {
+    v4f r;
+    asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(r) : "v"(p) : "memory");
+    return r;
+}
+template <int N> __device__ __forceinline__ void wait_loads(v4f (&r)[N]) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < N; i++) asm volatile("" : "+v"(r[i])); // uses stay after the wait
+}
+
+// The merge of nslice chunk partials for each of ng query heads (attention.zig:113-133 merge):
+// acc / ml point at the first head's sums [ng][nslice][HD] and {max, sum} pairs [ng][nslice][2],
+// out at its output row [ng][HD]. The workgroup loads every (head, chunk) pair at once, one wave per
+// head turns them into the weights exp(m_s - max m) of the non-empty chunks (in LDS: wts, lsh hold
+// ng * nslice floats, tsh ng), and then each 16-byte output is summed over the chunks by tpo
+// threads, sixteen chunks' loads at a time, all heads together. COH: the partials come from other
+// workgroups of the same launch (loads at the coherence point).
+template <bool COH, int HD>
+__device__ void merge_chunks(const float *acc, const float *ml, float *out, uint32_t ng, uint32_t nslice, float *wts,
+                             float *lsh, float *tsh) {
+    auto ld = [&](const float *q) -> float {
         if constexpr (COH)
-            return __hip_atomic_load(const_cast<float *>(p) + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return __hip_atomic_load(const_cast<float *>(q), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         else
-            return p[i];
+            return *q;
     };
-    float big = -INFINITY;
-    for (uint32_t s = threadIdx.x; s < nslice; s += blockDim.x)
-        if (ld(s * (hd + 2) + 1) != 0.0f) big = fmaxf(big, ld(s * (hd + 2)));
-    for (int o = 32; o >= 1; o >>= 1) big = fmaxf(big, __shfl_xor(big, o));
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = big;
-    __syncthreads();
-    big = red[0];
-    for (uint32_t i = 1; i < (blockDim.x >> 6); i++) big = fmaxf(big, red[i]);
-    float tot = 0.0f;
-    for (uint32_t s = threadIdx.x; s < nslice; s += blockDim.x) {
-        const float l = ld(s * (hd + 2) + 1);
-        const float wgt = l != 0.0f ? expf(ld(s * (hd + 2)) - big) : 0.0f;
-        wts[s] = wgt;
-        tot = fmaf(wgt, l, tot);
-    }
-    tot = block_sum(tot, red);
-    const float inv = 1.0f / tot;
-    for (uint32_t d = threadIdx.x; d < hd; d += blockDim.x) {
-        float v = 0.0f;
-        uint32_t s = 0;
-        for (; s + 8 <= nslice; s += 8) {
-            float pv[8];
+    const uint32_t T = blockDim.x, lane = threadIdx.x & 63, NW = T >> 6, N = ng * nslice;
+    for (uint32_t i0 = 0; i0 < N; i0 += 8 * T) {
+        float m[8], l[8];
 #pragma unroll
-            for (int i = 0; i < 8; i++) pv[i] = ld((s + i) * (hd + 2) + 2 + d);
-#pragma unroll
-            for (int i = 0; i < 8; i++) v = fmaf(wts[s + i], pv[i], v);
+        for (int k = 0; k < 8; k++) {
+            const uint32_t i = i0 + threadIdx.x + k * T;
+            if (i < N) {
+                m[k] = ld(ml + ATT_ML * i);
+                l[k] = ld(ml + ATT_ML * i + 1);
+            }
         }
-        for (; s < nslice; s++) v = fmaf(wts[s], ld(s * (hd + 2) + 2 + d), v);
-        o[d] = v * inv;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t i = i0 + threadIdx.x + k * T;
+            if (i < N) {
+                wts[i] = m[k];
+                lsh[i] = l[k];
+            }
+        }
+    }
+    __syncthreads();
+    for (uint32_t h = threadIdx.x >> 6; h < ng; h += NW) {
+        float *w = wts + h * nslice;
+        const float *l = lsh + h * nslice;
+        float big = -INFINITY;
+        for (uint32_t s = lane; s < nslice; s += 64)
+            if (l[s] != 0.0f) big = fmaxf(big, w[s]);
+        for (int o = 32; o >= 1; o >>= 1) big = fmaxf(big, __shfl_xor(big, o));
+        float tot = 0.0f;
+        for (uint32_t s = lane; s < nslice; s += 64) {
+            const float wgt = l[s] != 0.0f ? expf(w[s] - big) : 0.0f;
+            w[s] = wgt;
+            tot = fmaf(wgt, l[s], tot);
+        }
+        for (int o = 32; o >= 1; o >>= 1) tot += __shfl_xor(tot, o);
+        if (lane == 0) tsh[h] = tot;
+    }
+    __syncthreads();
+    constexpr uint32_t Q = HD / 4;
+    const uint32_t O = ng * Q;
+    uint32_t tpo = 1; // threads per output: the largest power of two with tpo * O <= T
+    while (2 * tpo * O <= T && tpo < 64) tpo *= 2;
+    const uint32_t j = threadIdx.x % tpo;
+    for (uint32_t o = threadIdx.x / tpo; o < O; o += T / tpo) {
+        const uint32_t h = o / Q, d4 = o % Q;
+        const float *base = acc + uint64_t(h) * nslice * HD + 4 * d4;
+        const float *w = wts + h * nslice;
+        v4f sum = v4f{};
+        for (uint32_t s0 = j; s0 < nslice; s0 += 16 * tpo) {
+            v4f r[16];
+#pragma unroll
+            for (int k = 0; k < 16; k++) {
+                const uint32_t sk = s0 + k * tpo;
+                if (sk < nslice) {
+                    if constexpr (COH)
+                        r[k] = load_coherent4(base + uint64_t(sk) * HD);
+                    else
+                        r[k] = *reinterpret_cast<const v4f *>(base + uint64_t(sk) * HD);
+                }
+            }
+            if constexpr (COH) wait_loads(r);
+#pragma unroll
+            for (int k = 0; k < 16; k++) {
+                const uint32_t sk = s0 + k * tpo;
+                if (sk < nslice) sum += w[sk] * r[k];
+            }
+        }
+        for (uint32_t m = 1; m < tpo; m <<= 1)
+#pragma unroll
+            for (int e = 0; e < 4; e++) sum[e] += __shfl_xor(sum[e], m);
+        if (j == 0) *reinterpret_cast<v4f *>(out + h * HD + 4 * d4) = sum * (1.0f / tsh[h]);
     }
 }
 
@@ -406,7 +477,7 @@ __device__ __forceinline__ void attn_decode_finish(const AttnArgs &a, uint32_t g
         }
         return;
     }
-    // The chunk's partials per head: {max, sum, acc} (unnormalized), as attn_combine_kernel reads
+    // The chunk's partials per head: acc (unnormalized) and {max, sum}, as attn_combine_kernel reads
     // them. With the merge in this launch, they go out by agent-scope stores (they complete at the
     // device's coherent level, not in this XCD's L2).
     auto put = [&](float *out, uint32_t i, float v) {
@@ -418,16 +489,17 @@ __device__ __forceinline__ void attn_decode_finish(const AttnArgs &a, uint32_t g
 #pragma unroll
     for (int gi = 0; gi < G; gi++) {
         if (uint32_t(gi) >= ng) break;
-        float *out = a.part + ((uint64_t(t) * a.nh + h0 + gi) * gridDim.x + g) * (HD + 2);
+        const uint64_t pi = (uint64_t(t) * a.nh + h0 + gi) * gridDim.x + g;
+        float *out = a.part + pi * HD;
         for (uint32_t d = threadIdx.x; d < HD; d += NWV * 64) {
             float v = 0.0f;
 #pragma unroll
             for (int i = 0; i < NWV; i++) v = fmaf(wt[gi][i], red_acc[i][gi][d], v);
-            put(out, 2 + d, v);
+            put(out, d, v);
         }
         if (threadIdx.x == 0) {
-            put(out, 0, big[gi]);
-            put(out, 1, tot[gi]);
+            put(a.part_ml + ATT_ML * pi, 0, big[gi]);
+            put(a.part_ml + ATT_ML * pi, 1, tot[gi]);
         }
     }
     if (!a.cnt) return; // attn_combine_kernel merges
@@ -443,51 +515,49 @@ __device__ __forceinline__ void attn_decode_finish(const AttnArgs &a, uint32_t g
     // non-atomic data and which measured 7.5 us per Llama-3-8B layer at 512-575 positions (1.879
     // vs 1.637 ms per token; Qwen3-0.6B 0.949 vs 0.847).
     __shared__ uint32_t last;
-    __shared__ float mw[ATT_MERGE_MAX], mred[NWV];
+    __shared__ float mw[G * ATT_MERGE_MAX], ml_[G * ATT_MERGE_MAX], mt[G];
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (threadIdx.x == 0) {
-        uint32_t *c = a.cnt + uint64_t(t) * a.nh + h0;
+        uint32_t *c = a.cnt + (uint64_t(t) * a.nh + h0) * ATT_CNT;
         last = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 == gridDim.x ? 1u : 0u;
         if (last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     if (!last) return;
-    for (uint32_t gi = 0; gi < ng; gi++) {
-        const uint32_t h = h0 + gi;
-        const float *hp = a.part + (uint64_t(t) * a.nh + h) * gridDim.x * (HD + 2);
-        if (gridDim.x <= 8) {
-            // One round of loads: thread d reads every chunk's {max, sum, acc[d]} at once.
-            for (uint32_t d = threadIdx.x; d < HD; d += NWV * 64) {
-                float mm[8], ll[8], vv8[8];
+    const uint64_t p0 = (uint64_t(t) * a.nh + h0) * gridDim.x; // the block's first partial
+    if (gridDim.x <= 8 && ng * HD <= 2 * NWV * 64) {
+        // One round of loads per output: thread (head, d) reads every chunk's {max, sum, acc[d]} at once.
+        for (uint32_t o = threadIdx.x; o < ng * HD; o += NWV * 64) {
+            const uint32_t gi = o / HD, d = o % HD;
+            float mm[8], ll[8], vv8[8];
 #pragma unroll
-                for (uint32_t i = 0; i < 8; i++) {
-                    if (i < gridDim.x) {
-                        float *q = const_cast<float *>(hp) + i * (HD + 2);
-                        mm[i] = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        ll[i] = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        vv8[i] = __hip_atomic_load(q + 2 + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    }
+            for (uint32_t i = 0; i < 8; i++) {
+                if (i < gridDim.x) {
+                    const uint64_t pi = p0 + gi * gridDim.x + i;
+                    mm[i] = __hip_atomic_load(a.part_ml + ATT_ML * pi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    ll[i] = __hip_atomic_load(a.part_ml + ATT_ML * pi + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    vv8[i] = __hip_atomic_load(a.part + pi * HD + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
-                float mx = -INFINITY;
-#pragma unroll
-                for (uint32_t i = 0; i < 8; i++)
-                    if (i < gridDim.x && ll[i] != 0.0f) mx = fmaxf(mx, mm[i]);
-                float sum = 0.0f, av = 0.0f;
-#pragma unroll
-                for (uint32_t i = 0; i < 8; i++) {
-                    if (i < gridDim.x) {
-                        const float wgt = ll[i] != 0.0f ? expf(mm[i] - mx) : 0.0f;
-                        sum = fmaf(wgt, ll[i], sum);
-                        av = fmaf(wgt, vv8[i], av);
-                    }
-                }
-                a.merge_out[(uint64_t(t) * a.nh + h) * HD + d] = av * (1.0f / sum);
             }
-        } else {
-            merge_partials<true>(hp, a.merge_out + (uint64_t(t) * a.nh + h) * HD, HD, gridDim.x, mw, mred);
-            __syncthreads(); // mw / mred are reused by the next head's merge
+            float mx = -INFINITY;
+#pragma unroll
+            for (uint32_t i = 0; i < 8; i++)
+                if (i < gridDim.x && ll[i] != 0.0f) mx = fmaxf(mx, mm[i]);
+            float sum = 0.0f, av = 0.0f;
+#pragma unroll
+            for (uint32_t i = 0; i < 8; i++) {
+                if (i < gridDim.x) {
+                    const float wgt = ll[i] != 0.0f ? expf(mm[i] - mx) : 0.0f;
+                    sum = fmaf(wgt, ll[i], sum);
+                    av = fmaf(wgt, vv8[i], av);
+                }
+            }
+            a.merge_out[(uint64_t(t) * a.nh + h0 + gi) * HD + d] = av * (1.0f / sum);
         }
+    } else {
+        merge_chunks<true, HD>(a.part + p0 * HD, a.part_ml + ATT_ML * p0, a.merge_out + (uint64_t(t) * a.nh + h0) * HD, ng,
+                               gridDim.x, mw, ml_, mt);
     }
 }
 
@@ -698,9 +768,6 @@ __global__ __launch_bounds__(NWV * 64) void attn_decode_kernel(AttnArgs a) {
     attn_decode_finish<HD, NWV, G>(a, g, t, h0, G, red_m, red_l, red_acc);
 }
 
-typedef _Float16 v8h __attribute__((ext_vector_type(8)));
-typedef float v16f __attribute__((ext_vector_type(16)));
-typedef float v4f __attribute__((ext_vector_type(4)));
 
 // Decode attention of non-fused passes on the f16 MFMA units (v_mfma_f32_16x16x32_f16), one
 // workgroup per (chunk, block of ng <= 8 query heads sharing one key/value head, token): the key
@@ -1056,12 +1123,14 @@ template <int HD, int NWV> hipError_t launch_attn_prefill(dim3 grid, const AttnP
 }
 
 // att[t][h*hd..] = merge of the slices' partials of (head h, token t).
-__global__ __launch_bounds__(256) void attn_combine_kernel(const float *__restrict__ part, float *__restrict__ att,
-                                                           uint32_t nh, uint32_t hd, uint32_t nslice) {
-    extern __shared__ float wts[]; // [nslice]
-    __shared__ float red[4];
-    const uint32_t t = blockIdx.y, h = blockIdx.x;
-    merge_partials<false>(part + (uint64_t(t) * nh + h) * nslice * (hd + 2), att + (uint64_t(t) * nh + h) * hd, hd, nslice, wts, red);
+template <int HD>
+__global__ __launch_bounds__(256) void attn_combine_kernel(const float *__restrict__ part, const float *__restrict__ part_ml,
+                                                           float *__restrict__ att, uint32_t nh, uint32_t nslice) {
+    extern __shared__ float wts[]; // [2 * nslice]
+    __shared__ float tot[1];
+    const uint64_t th = uint64_t(blockIdx.y) * nh + blockIdx.x; // (token, head)
+    merge_chunks<false, HD>(part + th * nslice * HD, part_ml + th * nslice * ATT_ML, att + th * HD, 1, nslice, wts,
+                            wts + nslice, tot);
 }
 
 } // namespace
@@ -1091,7 +1160,7 @@ struct hkhip_net {
     // Device buffers the network allocated, with their sizes (pass buffers: [cap tokens][...]).
     std::vector<std::pair<void *, uint64_t>> owned;
     uint32_t cap = 0; // tokens the pass buffers hold
-    float *x = nullptr, *xb = nullptr, *qkv = nullptr, *att = nullptr, *h = nullptr, *part = nullptr,
+    float *x = nullptr, *xb = nullptr, *qkv = nullptr, *att = nullptr, *h = nullptr, *part = nullptr, *part_ml = nullptr,
           *logits = nullptr, *lx = nullptr, *inv_freq = nullptr;
     uint8_t *xq = nullptr;
     __half *kc = nullptr, *vc = nullptr, *vt = nullptr; // [slot][layer][...]
@@ -1155,8 +1224,8 @@ NetSizes net_sizes(const hkhip_net_config &c, uint32_t slots, uint32_t n_dev, ui
     z.vtc = sl * c.n_kv_heads * c.head_dim * vt_stride(c) * 2;
     z.logits = uint64_t(max_rows) * c.vocab * 4;
     z.inv_freq = c.rope_dim / 2 * 4 + 4;
-    z.part = uint64_t(MAX_DECODE) * c.n_heads * nslices(c) * (c.head_dim + 2) * 4;
-    z.att_cnt = uint64_t(MAX_DECODE) * c.n_heads * 4;
+    z.part = uint64_t(MAX_DECODE) * c.n_heads * nslices(c) * (c.head_dim + ATT_ML) * 4; // sums, then {max, sum}
+    z.att_cnt = uint64_t(MAX_DECODE) * c.n_heads * ATT_CNT * 4;
     z.lx = uint64_t(max_rows) * c.dim * 4;
     const uint32_t maxk = std::max(std::max(c.dim, qdim(c)), c.ffn_dim);
     z.x = T * c.dim * 4;
@@ -1336,7 +1405,8 @@ uint32_t group_block(const hkhip_net_config &c) {
 
 // Whether nt tokens' decode attention over gb chunks runs on the grouped MFMA kernel
 // (attn_decode_gqa_kernel). By size: once the per-head kernel's waves (2 gb heads nt, two per
-// chunk) pass 2048, about one round at its ~150 registers, where it was measured to fall behind:
+// chunk) pass 2048, one round at its ~180 registers (two waves per SIMD), where it was measured
+// to fall behind:
 // per Llama-3-8B-shaped layer (32 / 8 heads), 8 tokens at 800 positions 23.3 vs 17.4 us, at 1600
 // 44.0 vs 30.5, at 3000 97.6 vs 50.3; below, the per-head kernel is as fast or up to 2 us faster
 // (8 tokens at <= 128 positions 7.2 vs 8.6, 2 tokens at 800 10.3 vs 12.6; Qwen3-0.6B-shaped,
@@ -1363,6 +1433,7 @@ int decode_attention(hkhip_net *net, const RopeArgs &ra, const __half *kc, const
     const bool merge_in = gb > 1 && gb <= net->merge_max;
     aa.cnt = merge_in ? net->att_cnt : nullptr;
     aa.merge_out = att;
+    aa.part_ml = net->part_ml;
     // The per-head kernel (G = 1) or, past one round of its waves, the grouped MFMA kernel (see
     // grouped_attention). The per-head kernel's FMA form with G = the group size measured slower
     // (a wave runs the group's dots, softmax and value sums one after another: 23.1 vs 9.8 us per
@@ -1386,8 +1457,13 @@ int decode_attention(hkhip_net *net, const RopeArgs &ra, const __half *kc, const
     }
     NET_TRY(hipGetLastError(), "decode attention");
     if (gb > 1 && !merge_in) {
-        hipLaunchKernelGGL(attn_combine_kernel, dim3(c.n_heads, nt), dim3(std::min(256u, std::max(64u, (c.head_dim + 63) / 64 * 64))),
-                           gb * 4, s, net->part, att, c.n_heads, c.head_dim, gb);
+        const dim3 cg(c.n_heads, nt), cb(256);
+        if (c.head_dim == 64)
+            hipLaunchKernelGGL(attn_combine_kernel<64>, cg, cb, gb * 8, s, net->part, net->part_ml, att, c.n_heads, gb);
+        else if (c.head_dim == 128)
+            hipLaunchKernelGGL(attn_combine_kernel<128>, cg, cb, gb * 8, s, net->part, net->part_ml, att, c.n_heads, gb);
+        else
+            hipLaunchKernelGGL(attn_combine_kernel<256>, cg, cb, gb * 8, s, net->part, net->part_ml, att, c.n_heads, gb);
         NET_TRY(hipGetLastError(), "decode attention combine");
     }
     return HKHIP_OK;
@@ -1698,6 +1774,8 @@ int hkhip_net_create_opts(hkhip_engine *eng, const hkhip_net_config *cfg, const 
         hkhip_net_destroy(n);
         return rc;
     }
+    // The chunk partials' {max, sum} pairs follow their sums: [8][heads][chunks][hd], then [..][2].
+    n->part_ml = n->part + uint64_t(MAX_DECODE) * c.n_heads * nslices(c) * c.head_dim;
     // Positions a pass has not written yet are read (and weighted by 0) by the attention kernels:
     // they must hold finite values. The chunk counters start at zero.
     if (hipMemset(n->kc, 0, z.cache) != hipSuccess || hipMemset(n->vc, 0, z.cache) != hipSuccess ||
