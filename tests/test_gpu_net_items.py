@@ -258,6 +258,32 @@ def test_separate_attention_merge(eng, gqa):
             run_both(net, cpu, items, [k - 1, k], f"merge kernel, {k} + 1 tokens")
 
 
+@pytest.mark.parametrize("heads,kv_heads,hd", [(8, 1, 64), (6, 2, 128), (12, 2, 64), (16, 1, 64)],
+                         ids=["group8", "group3-hd128", "group6", "group16"])
+def test_grouped_attention_group_sizes(eng, heads, kv_heads, hd):
+    """The grouped decode attention kernel (forced by the options' knob) at GQA group sizes whose
+    workgroups hold 8, 3 and 6 query heads and, for a group of 16, two head blocks per key/value
+    head: two sequences past 1024 positions (16 chunks: the workgroup merging all its heads at once
+    with the many-chunk merge), passes of 1, 2 and 1 + 3 tokens and a one-token pass of the short
+    sequence (4 chunks: the one-round merge)."""
+    from hk_amd.net import Net
+
+    cfg = Config(dim=256, n_layers=1, n_heads=heads, n_kv_heads=kv_heads, head_dim=hd, ffn_dim=256, vocab=256,
+                 max_ctx=1200, rope_neox=True, rope_base=1e4)
+    model = synth.model_np(cfg, F.Q8_0, seed=5600 + heads, out_fmt=F.Q8_0, embd_fmt=F.Q8_0, qk_norm=True)
+    rng = np.random.default_rng(5601)
+    cpu = Oracle(cfg, model)
+    with Net(eng, cfg, Options(slots=2, attn_gqa=1)) as net:
+        net.load(model)
+        run_both(net, cpu, seq_items(0, rng.integers(0, 256, 1030), 0), [1029], "prefill 1030")
+        run_both(net, cpu, seq_items(1, rng.integers(0, 256, 400), 0), [399], "prefill 400")
+        p0, p1 = 1030, 400
+        for k0, k1 in ((1, 0), (1, 1), (3, 1), (0, 1)):
+            items = seq_items(0, rng.integers(0, 256, k0), p0) + seq_items(1, rng.integers(0, 256, k1), p1)
+            p0, p1 = p0 + k0, p1 + k1
+            run_both(net, cpu, items, list(range(k0 + k1)), f"{heads}/{kv_heads} heads: {k0} + {k1} tokens")
+
+
 def test_logits_of_many_rows(eng):
     """logits(indices) for up to max_rows rows: 40 rows of a 48-token pass (the output product then
     runs as a GEMM over the gathered rows), 12 rows gathered out of order (8-row decode passes), and a
