@@ -223,9 +223,10 @@ def test_net_rope_scaling(eng, kind):
 
 @pytest.mark.parametrize("gqa", [0, 1], ids=["attn-by-size", "attn-grouped"])
 def test_net_attention_chunk_boundaries(eng, gqa):
-    """Decode passes stepping across the context sizes where the attention chunk count changes (one
-    chunk of 128 positions per (head, token) up to 128, then 2, 4 and 8 by 256, 512 and 1024): each chunk count is
-    its own captured graph, the one-chunk passes write the attention output directly and the
+    """Decode passes stepping across context sizes where the attention chunk count changes (one
+    chunk of 128 positions per (head, token) up to position 127, one more per further 128: the passes
+    cross 256, 512 and 1024, the last up to the network's 9 chunks): each chunk count is its own
+    captured graph, the one-chunk passes write the attention output directly and the
     one-token passes do the key/value writes inside the attention kernel. Every pass is checked
     against the CPU forward, so each reads the cache rows all earlier passes wrote."""
     from hk_amd.net import Net
@@ -238,8 +239,8 @@ def test_net_attention_chunk_boundaries(eng, gqa):
     with Net(eng, cfg, Options(attn_gqa=gqa)) as net:
         net.load(model)
         pos = 0
-        # 252 by prefill, then passes of 1 and 3 tokens over 256 (chunk counts 2 -> 4), a prefill to
-        # 509, passes over 512 (4 -> 8), a prefill to 1020 and passes over 1024 (8 -> the cap of 9)
+        # 252 by prefill, then passes of 1 and 3 tokens over 256 (chunk counts 2 -> 3), a prefill to
+        # 509, passes over 512 (4 -> 5), a prefill to 1020 and passes over 1024 (8 -> 9)
         plan = [252, 1, 1, 1, 1, 1, 3, 1, 248, 1, 1, 1, 3, 1, 505, 1, 1, 1, 3, 1, 8]
         for n in plan:
             toks = rng.integers(0, cfg.vocab, n)
@@ -253,7 +254,7 @@ def test_net_many_attention_chunks(eng, gqa):
     """Decode passes past 1024 positions, where decode attention runs over more than eight chunk
     workgroups of 128 positions per (head, token): the last chunk to finish merges the others'
     partials with the general merge (two rounds of loads; up to eight chunks it takes the one-round
-    merge), past 2048 positions over the capped chunk count of 18."""
+    merge), past 2048 positions over 17 chunks."""
     from hk_amd.net import Net
 
     cfg = Config(dim=128, n_layers=1, n_heads=2, n_kv_heads=1, head_dim=64, ffn_dim=256, vocab=256, max_ctx=2200,
@@ -264,8 +265,8 @@ def test_net_many_attention_chunks(eng, gqa):
     with Net(eng, cfg, Options(attn_gqa=gqa)) as net:
         net.load(model)
         pos = 0
-        # 1020 by prefill, passes over 1024 (8 -> 16 chunks), a prefill to 2035, passes over 2048
-        # (16 -> the cap of 18)
+        # 1020 by prefill, passes over 1024 (8 -> 9 chunks), a prefill to 2035, passes over 2048
+        # (16 -> 17)
         for n in [1020, 1, 3, 1, 1010, 1, 3, 8, 1, 1, 1]:
             toks = rng.integers(0, cfg.vocab, n)
             net.forward(toks, pos)
