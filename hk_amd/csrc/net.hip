@@ -28,6 +28,7 @@
 #include <vector>
 
 #include "common.hpp"
+#include "qact.hpp"
 #include "quant.hpp"
 
 using namespace hkhip;
@@ -237,8 +238,13 @@ struct AttnArgs {
     uint32_t *cnt;
     float *merge_out;
     // The chunk partials: part holds the unnormalized sums [token][head][chunk][hd], part_ml the
-    // {max, sum} pairs [token][head][chunk][2].
+    // {max, sum} pairs [token][head][chunk][ATT_ML].
     float *part_ml;
+    // q8_on (grouped kernel, head blocks of whole 256-value blocks): the workgroup that writes a head
+    // block's results also quantizes them into q8 (qact_q8k_kernel's planes for the pass's output
+    // rows), for the o product's prepared input.
+    int q8_on;
+    Q8KOut q8;
 };
 
 // A lane's DL dimensions of one value row: DL halves in one (DL = 1: the low half) or two words.
@@ -438,6 +444,19 @@ __device__ __forceinline__ void norm_rope_row(float *h, const float (&x)[HD / 64
     wave_sync();
 }
 
+// The ng * HD results of token t's head block h0.. (written to att by this workgroup, visible to it
+// after the barrier) quantized as whole Q8K blocks, one wave per block (qact_q8k_kernel's steps).
+template <int HD, int NWV>
+__device__ __forceinline__ void attn_quantize_block(const AttnArgs &a, uint32_t t, uint32_t h0, uint32_t ng) {
+    __syncthreads();
+    const uint32_t lane = threadIdx.x & 63, nb = ng * HD / QK_K, nsb = a.nh * HD / QK_K;
+    const float *row = a.merge_out + (uint64_t(t) * a.nh + h0) * HD;
+    for (uint32_t j = threadIdx.x >> 6; j < nb; j += NWV) {
+        const float4 v = reinterpret_cast<const float4 *>(row + QK_K * j)[lane];
+        q8k_out(a.q8, uint64_t(t) * nsb + h0 * HD / QK_K + j, lane, quant_q8k_wave(v, lane));
+    }
+}
+
 // The end of a decode attention workgroup, once its NWV waves' {max, sum, acc} of the ng (<= G)
 // query heads h0.. are in red_m / red_l / red_acc (LDS, after a barrier): merges them per head and
 // writes the normalized result (one chunk per (head, token)) or the chunk's partials, and the last
@@ -475,6 +494,7 @@ __device__ __forceinline__ void attn_decode_finish(const AttnArgs &a, uint32_t g
                 o[d] = v * inv;
             }
         }
+        if (a.q8_on) attn_quantize_block<HD, NWV>(a, t, h0, ng);
         return;
     }
     // The chunk's partials per head: acc (unnormalized) and {max, sum}, as attn_combine_kernel reads
@@ -559,6 +579,7 @@ __device__ __forceinline__ void attn_decode_finish(const AttnArgs &a, uint32_t g
         merge_chunks<true, HD>(a.part + p0 * HD, a.part_ml + ATT_ML * p0, a.merge_out + (uint64_t(t) * a.nh + h0) * HD, ng,
                                gridDim.x, mw, ml_, mt);
     }
+    if (a.q8_on) attn_quantize_block<HD, NWV>(a, t, h0, ng);
 }
 
 // G query heads h0 .. h0 + G - 1 that share one key/value head (G divides the group size: the
@@ -1348,8 +1369,9 @@ bool gemm_path(uint32_t n, int t) {
     return n > MAX_DECODE || (n >= NET_SK_MIN && (t == HKHIP_Q4_K || t == HKHIP_Q6_K));
 }
 
+// prepared: the products' Q8K input is already in net->xq (written by the attention kernel).
 int product(hkhip_net *net, uint32_t n, const hkhip_mat *mats, uint32_t nparts, const float *xin, const float *norm,
-            float *const *ys, const float *const *biases, int mode) {
+            float *const *ys, const float *const *biases, int mode, bool prepared = false) {
     hkhip_engine *eng = net->eng;
     const uint32_t cols = mats[0].cols;
     if (!gemm_path(n, mats[0].t)) {
@@ -1390,7 +1412,7 @@ int product(hkhip_net *net, uint32_t n, const hkhip_mat *mats, uint32_t nparts, 
         }
         return rc;
     }
-    const int rc = hkhip_qact(eng, xin, n, cols, act_kind(mats[0].t), net->xq);
+    const int rc = prepared ? HKHIP_OK : hkhip_qact(eng, xin, n, cols, act_kind(mats[0].t), net->xq);
     return rc ? rc : gemms(net, n, mats, nparts, ys, biases, mode);
 }
 
@@ -1411,17 +1433,24 @@ uint32_t group_block(const hkhip_net_config &c) {
 // 44.0 vs 30.5, at 3000 97.6 vs 50.3; below, the per-head kernel is as fast or up to 2 us faster
 // (8 tokens at <= 128 positions 7.2 vs 8.6, 2 tokens at 800 10.3 vs 12.6; Qwen3-0.6B-shaped,
 // 16 / 8 heads: 8 tokens at 800 14.1 vs 15.4, at 1600 27.4 vs 24.4).
-bool grouped_attention(const hkhip_net *net, uint32_t nt, uint32_t gb) {
+// q8: the o product would take the results as a Q8K input (attn_quantize_block); when a head block
+// is whole Q8K blocks the grouped kernel then also saves the quantizer launch (4.6-4.8 us), which
+// outweighs what the per-head kernel is faster by at any size measured above.
+bool q8_in_attention(const hkhip_net *net, uint32_t gb) {
+    const hkhip_net_config &c = net->cfg;
+    return group_block(c) * c.head_dim % QK_K == 0 && (gb == 1 || gb <= net->merge_max);
+}
+bool grouped_attention(const hkhip_net *net, uint32_t nt, uint32_t gb, bool q8 = false) {
     const hkhip_net_config &c = net->cfg;
     if (net->gqa == 2 || (c.head_dim != 64 && c.head_dim != 128)) return false;
-    return net->gqa == 1 || uint64_t(2) * gb * c.n_heads * nt > 2048;
+    return net->gqa == 1 || uint64_t(2) * gb * c.n_heads * nt > 2048 || (q8 && q8_in_attention(net, gb));
 }
 
 // Decode attention over tokens [t0, t0 + nt) of the pass (nt <= MAX_DECODE), gb chunks per
 // (head, token). fused: a one-token pass whose attention kernel also does the head norms, the
 // rotation and the cache writes (ra's fields).
 int decode_attention(hkhip_net *net, const RopeArgs &ra, const __half *kc, const __half *vc, uint32_t t0, uint32_t nt,
-                     uint32_t gb, bool fused) {
+                     uint32_t gb, bool fused, bool *q8_done = nullptr) {
     const hkhip_net_config &c = net->cfg;
     hipStream_t s = net->eng->cur;
     AttnArgs aa{ra.q + uint64_t(t0) * ra.sq, kc, vc, net->part, net->pos + t0, net->slot + t0, ra.kv_slot, nt,
@@ -1439,9 +1468,17 @@ int decode_attention(hkhip_net *net, const RopeArgs &ra, const __half *kc, const
     // (a wave runs the group's dots, softmax and value sums one after another: 23.1 vs 9.8 us per
     // Llama-3-8B layer at positions 512-575, G = 4).
     constexpr int NV = int(ATT_DWAVES);
-    if (!fused && grouped_attention(net, nt, gb)) {
+    if (!fused && grouped_attention(net, nt, gb, q8_done && t0 == 0)) {
         const uint32_t ng = group_block(c);
         const dim3 gg(gb, c.n_heads / ng, nt);
+        // q8_done (a pass's only attention launch, the o product on a Q8K input): the workgroups
+        // that write the results also quantize them, when a head block is whole Q8K blocks and no
+        // separate merge kernel follows; the caller then skips the o product's quantizer launch.
+        if (q8_done && t0 == 0 && q8_in_attention(net, gb)) {
+            aa.q8_on = 1;
+            aa.q8 = q8k_planes(reinterpret_cast<uint8_t *>(net->xq), act_layout(nt, qdim(c)), nt, qdim(c));
+            *q8_done = true;
+        }
         if (c.head_dim == 64)
             hipLaunchKernelGGL((attn_decode_gqa_kernel<64, NV, 2>), gg, dim3(64 * NV), 0, s, aa, ng);
         else
@@ -1525,8 +1562,10 @@ int run_pass(hkhip_net *net, uint32_t n, uint32_t gb, bool lg) {
             hipLaunchKernelGGL(rope_kv_kernel, dim3((ra.nheads + 3) / 4, n), dim3(256), 0, s, ra);
             NET_TRY(hipGetLastError(), "rope / kv write");
         }
+        bool att_q8 = false;
         if (n <= MAX_DECODE) {
-            if ((rc = decode_attention(net, ra, kc, vc, 0, n, gb, fused))) return rc;
+            const bool want_q8 = gemm_path(n, L.wo.t) && act_kind(L.wo.t) == HKHIP_ACT_Q8K;
+            if ((rc = decode_attention(net, ra, kc, vc, 0, n, gb, fused, want_q8 ? &att_q8 : nullptr))) return rc;
         } else {
             // Each sequence's run of consecutive positions: longer than a decode pass on the MFMA
             // prefill kernel, else (and for head dims it does not take) on the decode kernel, up to
@@ -1552,7 +1591,7 @@ int run_pass(hkhip_net *net, uint32_t n, uint32_t gb, bool lg) {
         }
         {
             float *const ys[1] = {net->x};
-            if ((rc = product(net, n, &L.wo, 1, net->att, nullptr, ys, nullptr, HKHIP_ACCUMULATE))) return rc;
+            if ((rc = product(net, n, &L.wo, 1, net->att, nullptr, ys, nullptr, HKHIP_ACCUMULATE, att_q8))) return rc;
         }
         { // gate/up with silu(gate) * up in the products' epilogue (decode kernels and GEMMs alike)
             float *const ys[1] = {net->h};

@@ -1,6 +1,6 @@
 // Activation quantizer kernels (qact): f32 [n][k] -> the engine's activation buffer, with the
 // block quantizers of quant.hpp (hk's quantizeA8 / quantizeQ8K, src/quant/vecdot.zig:134-180).
-#include "quant.hpp"
+#include "qact.hpp"
 
 namespace hkhip {
 
@@ -45,68 +45,7 @@ __global__ void qact_a8_kernel(const float *__restrict__ x, uint64_t total, A8Ou
     if (i < total) a8_out(o, i, r);
 }
 
-// Q8K: one wave per 256-value block, four consecutive values per lane.
-// fp32 -> bf16 bits, round to nearest even (finite inputs).
-__device__ __forceinline__ uint32_t bf16_bits_rne(float x) {
-    const uint32_t u = __builtin_bit_cast(uint32_t, x);
-    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
-}
-
-// Token-interleaved copies for the small-batch kernel (tiles > 0; layout in common.hpp): token
-// t's entries. The padding positions of the last tile are not written: the reader takes the last
-// token's entries for them.
-struct QactIl {
-    uint8_t *qs;
-    uint16_t *mb;
-    float *d;
-    uint32_t tiles, n, nsb;
-};
-
-struct Q8KOut {
-    int8_t *qs;
-    float *d;
-    int16_t *bs;
-    uint16_t *mb;
-    float *db;
-    QactIl il;
-};
-// Block b of the input, quantized by one wave (r: this lane's part).
-__device__ __forceinline__ void q8k_out(const Q8KOut &o, uint64_t b, uint32_t lane, const Q8KQ &r) {
-    int8_t *qs = o.qs;
-    float *dout = o.d, *dbout = o.db;
-    int16_t *bsout = o.bs;
-    uint16_t *mbout = o.mb;
-    const QactIl &il = o.il;
-    reinterpret_cast<uint32_t *>(qs + b * QK_K)[lane] = r.packed;
-    if ((lane & 3) == 0) bsout[b * 16 + lane / 4] = (int16_t)r.bsum;
-    if (lane == 0) dout[b] = r.d;
-    // GEMM min-term operand: the sum over the 32 values of sub-block s, bsum32 = 64*u + v
-    // (v in [0, 63], u in [-64, 63]), as the exact bf16 integers 64*u and v. The 16-value sums
-    // sit in lanes 4g; sub-block s = groups 2s and 2s+1 (lanes 8s and 8s+4).
-    const int b32 = r.bsum + __shfl_down(r.bsum, 4);
-    const int bv = b32 & 63;
-    const uint16_t mu = uint16_t(bf16_bits_rne((float)(b32 - bv))), mv = uint16_t(bf16_bits_rne((float)bv));
-    if ((lane & 7) == 0) {
-        mbout[b * 16 + lane / 8] = mu;
-        mbout[b * 16 + 8 + lane / 8] = mv;
-        dbout[b * 8 + lane / 8] = r.d * (float)b32;
-    }
-    if (il.tiles) {
-        const uint32_t b32i = uint32_t(b); // tokens <= SK_MAX_TOKENS: a small index
-        const uint32_t t = b32i / il.nsb, sb = b32i - t * il.nsb;
-        const uint32_t tile = t / 16, p = t % 16;
-        const uint32_t c64 = 4 * sb + lane / 16, g = (lane % 16) / 4;
-        uint8_t *e = il.qs + ((uint64_t(c64) * il.tiles + tile) * 64 + 16 * g + p) * 16 + 4 * (lane % 4);
-        *reinterpret_cast<uint32_t *>(e) = r.packed;
-        const uint64_t mbase = (uint64_t(sb) * il.tiles + tile) * 256; // in uint16: 2 halves x 16 x 8
-        if ((lane & 7) == 0) {
-            il.mb[mbase + p * 8 + lane / 8] = mu;
-            il.mb[mbase + 128 + p * 8 + lane / 8] = mv;
-        }
-        if (lane == 0) il.d[(uint64_t(sb) * il.tiles + tile) * 16 + p] = r.d;
-    }
-}
-
+// Q8K: one wave per 256-value block, four consecutive values per lane (q8k_out: qact.hpp).
 __global__ void qact_q8k_kernel(const float *__restrict__ x, uint64_t nblocks, Q8KOut o) {
     const uint32_t lane = threadIdx.x & 63;
     const uint64_t b = (uint64_t(blockIdx.x) * blockDim.x + threadIdx.x) / 64;
@@ -229,14 +168,6 @@ static A8Out a8_planes(uint8_t *xq, const ActLayout &L, uint32_t n, uint32_t k) 
                  reinterpret_cast<int32_t *>(xq + L.a8_s), reinterpret_cast<float *>(xq + L.a8_ds),
                  k % QK_K == 0 ? reinterpret_cast<uint16_t *>(xq + L.a8_dsb) : nullptr, n, k / 32};
 }
-static Q8KOut q8k_planes(uint8_t *xq, const ActLayout &L, uint32_t n, uint32_t k) {
-    return Q8KOut{reinterpret_cast<int8_t *>(xq + L.k_qs), reinterpret_cast<float *>(xq + L.k_d),
-                  reinterpret_cast<int16_t *>(xq + L.k_bs), reinterpret_cast<uint16_t *>(xq + L.k_mb),
-                  reinterpret_cast<float *>(xq + L.k_db),
-                  QactIl{xq + L.k_il, reinterpret_cast<uint16_t *>(xq + L.k_ilmb), reinterpret_cast<float *>(xq + L.k_ild),
-                         L.tiles, n, k / QK_K}};
-}
-
 hipError_t launch_qact(const float *x, uint32_t n, uint32_t k, int kind, uint8_t *xq, hipStream_t s) {
     ActLayout L = act_layout(n, k);
     uint64_t total = uint64_t(n) * k;

@@ -284,6 +284,40 @@ def test_grouped_attention_group_sizes(eng, heads, kv_heads, hd):
             run_both(net, cpu, items, list(range(k0 + k1)), f"{heads}/{kv_heads} heads: {k0} + {k1} tokens")
 
 
+@pytest.mark.parametrize("heads,kv_heads,hd", [(8, 2, 64), (4, 2, 128)], ids=["hd64-group4", "hd128-group2"])
+def test_attention_output_quantized_in_kernel(eng, heads, kv_heads, hd):
+    """Passes of 5-8 tokens whose o product (Q4_K) takes a prepared Q8K input: the grouped attention
+    kernel's workgroups quantize their head block's results themselves (a head block is whole
+    256-value blocks here) and the pass skips the o product's quantizer launch — with one chunk per
+    (head block, token) (short contexts) and with the chunks merged in the launch (past 128
+    positions), one token per sequence and two tokens of one sequence in a pass."""
+    from hk_amd.net import Net
+
+    cfg = Config(dim=256, n_layers=2, n_heads=heads, n_kv_heads=kv_heads, head_dim=hd, ffn_dim=512, vocab=300,
+                 max_ctx=400, rope_neox=True, rope_base=1e4)
+    model = synth.model_np(cfg, F.Q4_K, seed=5700 + hd, out_fmt=F.Q6_K, embd_fmt=F.Q8_0, qk_norm=True)
+    rng = np.random.default_rng(5701)
+    cpu = Oracle(cfg, model)
+    lens = [20, 60, 100, 140, 200, 300]
+    with Net(eng, cfg, Options(slots=6, attn_gqa=1)) as net:
+        net.load(model)
+        for i, ln in enumerate(lens):
+            run_both(net, cpu, seq_items(i, rng.integers(0, cfg.vocab, ln), 0), [ln - 1], f"prefill {ln}")
+        pos = list(lens)
+
+        def step(seqs, what):
+            items = []
+            for i in seqs:
+                items += seq_items(i, rng.integers(0, cfg.vocab, 1), pos[i])
+                pos[i] += 1
+            run_both(net, cpu, items, list(range(len(items))), what)
+
+        step([0, 1, 2, 3, 4], "5 sequences, contexts <= 128")  # one chunk: no merge
+        step([0, 1, 2, 3, 4, 5], "6 sequences")
+        step([0, 1, 2, 3, 4, 5, 0, 1], "8 tokens, two of sequences 0 and 1")
+        step([3, 4, 5, 3, 4, 5], "6 tokens of 3 sequences past 128")
+
+
 def test_logits_of_many_rows(eng):
     """logits(indices) for up to max_rows rows: 40 rows of a 48-token pass (the output product then
     runs as a GEMM over the gathered rows), 12 rows gathered out of order (8-row decode passes), and a
