@@ -412,13 +412,31 @@ __device__ void merge_chunks(const float *acc, const float *ml, float *out, uint
 
 // Registers of a lane's share of the rope_dim / 2 rotation frequencies.
 template <int HD> constexpr int rope_regs() { return (HD / 2 + 63) / 64; }
-// One row of HD values held by a wave (lane l: elements l + 64 j in x): headNorm (ops.zig:31-38,
-// when nw_on) into the LDS row h, then the rotation of ropeAngles / ropeApply (ops.zig:154-185)
-// in place -- the steps head_norm_rope takes, from registers.
+// cos and sin (times ropeMscale) of the lane's rotation angles pos * fr (ropeAngles, ops.zig:154-170).
 template <int HD>
-__device__ __forceinline__ void norm_rope_row(float *h, const float (&x)[HD / 64], const float (&nw)[HD / 64], bool nw_on,
-                                              const float (&fr)[rope_regs<HD>()], uint32_t pos, const RopeArgs &a,
-                                              uint32_t lane) {
+__device__ __forceinline__ void rope_cs(float (&cs)[rope_regs<HD>()], float (&sn)[rope_regs<HD>()],
+                                        const float (&fr)[rope_regs<HD>()], uint32_t pos, const RopeArgs &a,
+                                        uint32_t lane) {
+    const float p = float(pos);
+#pragma unroll
+    for (int f = 0; f < rope_regs<HD>(); f++) {
+        cs[f] = 0.0f;
+        sn[f] = 0.0f;
+        if (lane + 64 * f < a.rope_half) {
+            float s_, c_;
+            sincosf(p * fr[f], &s_, &c_);
+            cs[f] = c_ * a.mscale;
+            sn[f] = s_ * a.mscale;
+        }
+    }
+}
+// One row of HD values held by a wave (lane l: elements l + 64 j in x): headNorm (ops.zig:31-38,
+// when nw_on) into the LDS row h, then the rotation of ropeApply (ops.zig:171-185) by the angles
+// rope_cs gave, in place -- the steps head_norm_rope takes, from registers.
+template <int HD>
+__device__ __forceinline__ void norm_rope_row_cs(float *h, const float (&x)[HD / 64], const float (&nw)[HD / 64],
+                                                 bool nw_on, const float (&cs)[rope_regs<HD>()],
+                                                 const float (&sn)[rope_regs<HD>()], const RopeArgs &a, uint32_t lane) {
     float ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < HD / 64; j++) ss = fmaf(x[j], x[j], ss);
@@ -427,14 +445,11 @@ __device__ __forceinline__ void norm_rope_row(float *h, const float (&x)[HD / 64
 #pragma unroll
     for (int j = 0; j < HD / 64; j++) h[lane + 64 * j] = nw_on ? (x[j] * inv) * nw[j] : x[j];
     wave_sync();
-    const float p = float(pos);
 #pragma unroll
     for (int f = 0; f < rope_regs<HD>(); f++) {
         const uint32_t i = lane + 64 * f;
         if (i < a.rope_half) {
-            float sn, cs;
-            sincosf(p * fr[f], &sn, &cs);
-            const float c = cs * a.mscale, s = sn * a.mscale;
+            const float c = cs[f], s = sn[f];
             const uint32_t i0 = a.neox ? i : 2 * i, i1 = a.neox ? i + a.rope_half : 2 * i + 1;
             const float x0 = h[i0], x1 = h[i1];
             h[i0] = x0 * c - x1 * s;
@@ -442,6 +457,14 @@ __device__ __forceinline__ void norm_rope_row(float *h, const float (&x)[HD / 64
         }
     }
     wave_sync();
+}
+template <int HD>
+__device__ __forceinline__ void norm_rope_row(float *h, const float (&x)[HD / 64], const float (&nw)[HD / 64], bool nw_on,
+                                              const float (&fr)[rope_regs<HD>()], uint32_t pos, const RopeArgs &a,
+                                              uint32_t lane) {
+    float cs[rope_regs<HD>()], sn[rope_regs<HD>()];
+    rope_cs<HD>(cs, sn, fr, pos, a, lane);
+    norm_rope_row_cs<HD>(h, x, nw, nw_on, cs, sn, a, lane);
 }
 
 // The ng * HD results of token t's head block h0.. (written to att by this workgroup, visible to it
@@ -804,7 +827,7 @@ __global__ __launch_bounds__(NWV * 64) void attn_decode_kernel(AttnArgs a) {
 // The block's two score tiles take its key rows in the order that leaves lane (column c, group q)
 // holding positions 8q .. 8q + 7 of the block, exactly the k slots of the second product's B
 // operand, so the probabilities feed it without moving.
-template <int HD, int NWV, int PB>
+template <int HD, int NWV, int PB, bool FUSED>
 __global__ __launch_bounds__(NWV * 64) void attn_decode_gqa_kernel(AttnArgs a, uint32_t ng) {
     constexpr int NS = HD / 32, NDT = HD / 16; // k steps of the scores, dimension tiles of the output
     const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -817,8 +840,30 @@ __global__ __launch_bounds__(NWV * 64) void attn_decode_gqa_kernel(AttnArgs a, u
     const uint32_t pos = a.pos[t];
     // q operands first (the memory counter is in order): lane (c, q) holds dimensions
     // 32 s + 8 q .. + 8 of head hq's hi (c < 8) or lo part, zero for columns past the block.
+    // Fused (every token of the pass in its own slot): the raw q rows of this wave's heads, the norm
+    // weights, the inverse frequencies and the token's raw new key and value rows instead, ahead of
+    // the cache rows; the operands are built from the normalized, rotated rows below.
     v8h qb[NS];
-    {
+    float4 xq[NS][2];                                                          // fused: raw q
+    float qnw[HD / 64], knw[HD / 64], kx[HD / 64], vx[HD / 64], fr[rope_regs<HD>()]; // norms, new key / value
+    if constexpr (FUSED) {
+        const float *qrow = a.q + uint64_t(t) * a.sq + (h0 + (hq < ng ? hq : 0)) * HD + 8 * qg;
+#pragma unroll
+        for (int s = 0; s < NS; s++) {
+            xq[s][0] = *reinterpret_cast<const float4 *>(qrow + 32 * s);
+            xq[s][1] = *reinterpret_cast<const float4 *>(qrow + 32 * s + 4);
+        }
+        const float *ksrc = a.r.k + uint64_t(t) * a.r.skv + kvh * HD, *vsrc = a.r.v + uint64_t(t) * a.r.skv + kvh * HD;
+#pragma unroll
+        for (int j = 0; j < HD / 64; j++) {
+            qnw[j] = a.r.q_norm ? a.r.q_norm[lane + 64 * j] : 1.0f;
+            knw[j] = a.r.k_norm ? a.r.k_norm[lane + 64 * j] : 1.0f;
+            kx[j] = ksrc[lane + 64 * j];
+            vx[j] = vsrc[lane + 64 * j];
+        }
+#pragma unroll
+        for (int f = 0; f < rope_regs<HD>(); f++) fr[f] = lane + 64 * f < a.r.rope_half ? a.r.inv_freq[lane + 64 * f] : 0.0f;
+    } else {
         const float *qrow = a.q + uint64_t(t) * a.sq + (h0 + (hq < ng ? hq : 0)) * HD + 8 * qg;
         float4 x[NS][2];
 #pragma unroll
@@ -870,6 +915,130 @@ __global__ __launch_bounds__(NWV * 64) void attn_decode_gqa_kernel(AttnArgs a, u
             for (int s = 0; s < NS; s++) asm volatile("" : "+v"(ka[b][u][s]));
 #pragma unroll
         for (int d = 0; d < NDT; d++) asm volatile("" : "+v"(va[b][d]));
+    }
+    if constexpr (FUSED) {
+        // q in the operand layout, in registers: a head's sum of squares is its lanes' partials over
+        // the four lane groups (headNorm, ops.zig:31-38), and every rotation pair (ropeApply,
+        // ops.zig:171-185) lies in one lane -- (i, i + rope_half) two or one k steps apart (neox,
+        // rope_half a multiple of 32: the host's condition), (2i, 2i + 1) neighbours (pairwise) --
+        // with the angles' cos / sin from a table each wave writes (identical values) to LDS. In the
+        // chunk holding the token's position one wave builds the new key row as rope_kv_kernel
+        // does, and both new rows go to f16.
+        __shared__ float cst[2][HD / 2], qwt[HD], knf[HD];
+        __shared__ __attribute__((aligned(16))) _Float16 kv16[2][HD];
+        float cs[rope_regs<HD>()], sn[rope_regs<HD>()];
+        rope_cs<HD>(cs, sn, fr, pos, a.r, lane);
+#pragma unroll
+        for (int j = 0; j < HD / 64; j++) qwt[lane + 64 * j] = qnw[j]; // identical in every wave
+#pragma unroll
+        for (int f = 0; f < rope_regs<HD>(); f++)
+            if (lane + 64 * f < a.r.rope_half) {
+                cst[0][lane + 64 * f] = cs[f];
+                cst[1][lane + 64 * f] = sn[f];
+            }
+        float y[NS][8];
+#pragma unroll
+        for (int s = 0; s < NS; s++) {
+            const float v[8] = {xq[s][0].x, xq[s][0].y, xq[s][0].z, xq[s][0].w, xq[s][1].x, xq[s][1].y, xq[s][1].z, xq[s][1].w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) y[s][e] = v[e];
+        }
+        wave_sync(); // the norm weights and the angle table
+        if (a.r.q_norm) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int s = 0; s < NS; s++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) ss = fmaf(y[s][e], y[s][e], ss);
+            ss += __shfl_xor(ss, 16);
+            ss += __shfl_xor(ss, 32);
+            const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, float(HD)) + a.r.eps));
+#pragma unroll
+            for (int s = 0; s < NS; s++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) y[s][e] = (y[s][e] * inv) * qwt[32 * s + 8 * qg + e];
+        }
+        const uint32_t rh = a.r.rope_half;
+        if (a.r.neox) {
+#pragma unroll
+            for (int s = 0; s < NS; s++)
+#pragma unroll
+                for (int s2 = s + 1; s2 < NS; s2++)
+                    if (uint32_t(32 * (s2 - s)) == rh && uint32_t(32 * s) < rh)
+#pragma unroll
+                        for (int e = 0; e < 8; e++) {
+                            const uint32_t i = 32 * s + 8 * qg + e;
+                            const float cc = cst[0][i], sc = cst[1][i], x0 = y[s][e], x1 = y[s2][e];
+                            y[s][e] = x0 * cc - x1 * sc;
+                            y[s2][e] = x0 * sc + x1 * cc;
+                        }
+        } else {
+#pragma unroll
+            for (int s = 0; s < NS; s++)
+#pragma unroll
+                for (int e = 0; e < 8; e += 2) {
+                    const uint32_t i = (32 * s + 8 * qg + e) / 2;
+                    if (i < rh) {
+                        const float cc = cst[0][i], sc = cst[1][i], x0 = y[s][e], x1 = y[s][e + 1];
+                        y[s][e] = x0 * cc - x1 * sc;
+                        y[s][e + 1] = x0 * sc + x1 * cc;
+                    }
+                }
+        }
+#pragma unroll
+        for (int s = 0; s < NS; s++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float xv = hq < ng ? y[s][e] : 0.0f;
+                const _Float16 hi = (_Float16)xv;
+                qb[s][e] = c < 8 ? hi : (_Float16)(xv - (float)hi);
+            }
+        const bool own = pos / (32 * PB * NWV) == g; // uniform over the workgroup
+        if (own) {
+            if (w == NWV - 1) {
+                norm_rope_row_cs<HD>(knf, kx, knw, a.r.k_norm != nullptr, cs, sn, a.r, lane);
+#pragma unroll
+                for (int j = 0; j < HD / 64; j++) {
+                    kv16[0][lane + 64 * j] = (_Float16)knf[lane + 64 * j];
+                    kv16[1][lane + 64 * j] = (_Float16)vx[j];
+                }
+            }
+            __syncthreads();
+        }
+        if (own) {
+            // The loads brought the cache's old rows for the token's position: the new ones replace
+            // them, and the first head block of the key/value head writes them to the caches (no
+            // other workgroup of the launch reads this position of this slot).
+#pragma unroll
+            for (int b = 0; b < PB; b++) {
+#pragma unroll
+                for (int u = 0; u < 2; u++)
+                    if (p0 + 32 * b + 8 * (c >> 2) + 4 * u + (c & 3) == pos)
+#pragma unroll
+                        for (int s = 0; s < NS; s++) ka[b][u][s] = *reinterpret_cast<const v8h *>(&kv16[0][32 * s + 8 * qg]);
+                const uint32_t base = p0 + 32 * b + 8 * qg;
+                if (pos >= base && pos < base + 8) {
+#pragma unroll
+                    for (int d = 0; d < NDT; d++) {
+                        const _Float16 nv = kv16[1][16 * d + c];
+#pragma unroll
+                        for (int e = 0; e < 8; e++)
+                            if (base + e == pos) va[b][d][e] = nv;
+                    }
+                }
+            }
+            if (h0 % grp == 0) {
+                const __half *k16 = reinterpret_cast<const __half *>(kv16[0]), *v16 = reinterpret_cast<const __half *>(kv16[1]);
+                __half *kd = a.r.kc + sl * a.r.kv_slot + (uint64_t(kvh) * a.max_ctx + pos) * HD;
+                __half *vd = a.r.vc + sl * a.r.kv_slot + (uint64_t(kvh) * a.max_ctx + pos) * HD;
+                __half *vtd = a.r.vt + sl * a.r.vt_slot + uint64_t(kvh) * HD * a.r.vt_stride + pos;
+                for (uint32_t d = threadIdx.x; d < HD; d += NWV * 64) {
+                    kd[d] = k16[d];
+                    vd[d] = v16[d];
+                    vtd[uint64_t(d) * a.r.vt_stride] = v16[d];
+                }
+            }
+        }
     }
     float mx = -INFINITY, lsum = 0.0f;
     v4f o[NDT];
@@ -1166,6 +1335,7 @@ struct hkhip_net {
     uint32_t n_dev = 0;   // layers on the device
     bool partial = false; // only the leading layers (no embedding, final norm or output)
     uint32_t n_slots = 1, n_batch = 0, max_rows = 64, merge_max = ATT_MERGE_MAX, gqa = 0;
+    bool distinct = false; // the staged pass's items each in a slot of their own
     struct Layer {
         // q, k and v rows stacked (one product, one output row per token) when the three share their
         // type; else three products into three regions of the q/k/v buffer.
@@ -1468,7 +1638,7 @@ int decode_attention(hkhip_net *net, const RopeArgs &ra, const __half *kc, const
     // (a wave runs the group's dots, softmax and value sums one after another: 23.1 vs 9.8 us per
     // Llama-3-8B layer at positions 512-575, G = 4).
     constexpr int NV = int(ATT_DWAVES);
-    if (!fused && grouped_attention(net, nt, gb, q8_done && t0 == 0)) {
+    if (grouped_attention(net, nt, gb, q8_done && t0 == 0)) { // fused: every token in its own slot
         const uint32_t ng = group_block(c);
         const dim3 gg(gb, c.n_heads / ng, nt);
         // q8_done (a pass's only attention launch, the o product on a Q8K input): the workgroups
@@ -1479,10 +1649,16 @@ int decode_attention(hkhip_net *net, const RopeArgs &ra, const __half *kc, const
             aa.q8 = q8k_planes(reinterpret_cast<uint8_t *>(net->xq), act_layout(nt, qdim(c)), nt, qdim(c));
             *q8_done = true;
         }
-        if (c.head_dim == 64)
-            hipLaunchKernelGGL((attn_decode_gqa_kernel<64, NV, 2>), gg, dim3(64 * NV), 0, s, aa, ng);
+        // The fused form runs four waves of 32 positions per chunk: with two of 64 the q rows'
+        // registers next to the rows in flight left one wave per SIMD (233 VGPRs + 32 AGPRs).
+        if (c.head_dim == 64 && fused)
+            hipLaunchKernelGGL((attn_decode_gqa_kernel<64, 2 * NV, 1, true>), gg, dim3(128 * NV), 0, s, aa, ng);
+        else if (c.head_dim == 64)
+            hipLaunchKernelGGL((attn_decode_gqa_kernel<64, NV, 2, false>), gg, dim3(64 * NV), 0, s, aa, ng);
+        else if (fused)
+            hipLaunchKernelGGL((attn_decode_gqa_kernel<128, 2 * NV, 1, true>), gg, dim3(128 * NV), 0, s, aa, ng);
         else
-            hipLaunchKernelGGL((attn_decode_gqa_kernel<128, NV, 2>), gg, dim3(64 * NV), 0, s, aa, ng);
+            hipLaunchKernelGGL((attn_decode_gqa_kernel<128, NV, 2, false>), gg, dim3(64 * NV), 0, s, aa, ng);
     } else {
     const dim3 dg(gb, c.n_heads, nt), db(64 * ATT_DWAVES);
     if (c.head_dim == 64)
@@ -1551,7 +1727,15 @@ int run_pass(hkhip_net *net, uint32_t n, uint32_t gb, bool lg) {
                     c.rms_eps};
         // Prefill passes write the value heads with v_cache_block (coalesced transposed writes);
         // one-token passes on the per-head kernel do all of it in the attention kernel.
-        const bool vsep = n > MAX_DECODE, fused = n == 1 && !grouped_attention(net, 1, gb);
+        // Decode passes: the o product may take its Q8K input from the attention kernel; the
+        // grouped kernel does the rope / cache work itself when every token has a slot of its own,
+        // the per-head kernel in one-token passes.
+        const bool vsep = n > MAX_DECODE;
+        const bool want_q8 = !vsep && gemm_path(n, L.wo.t) && act_kind(L.wo.t) == HKHIP_ACT_Q8K;
+        // (The grouped kernel rotates q in its operand registers: neox pairs must lie 32 dimensions
+        // apart or a multiple of it.)
+        const bool rope_in_lanes = !c.rope_neox || c.rope_dim / 2 % 32 == 0;
+        const bool fused = !vsep && (grouped_attention(net, n, gb, want_q8) ? net->distinct && rope_in_lanes : n == 1);
         ra.nheads = c.n_heads + (vsep ? 1 : 2) * c.n_kv_heads;
         if (vsep) { // one launch: rope / key writes, then the value rows
             ra.ntok = n;
@@ -1564,7 +1748,6 @@ int run_pass(hkhip_net *net, uint32_t n, uint32_t gb, bool lg) {
         }
         bool att_q8 = false;
         if (n <= MAX_DECODE) {
-            const bool want_q8 = gemm_path(n, L.wo.t) && act_kind(L.wo.t) == HKHIP_ACT_Q8K;
             if ((rc = decode_attention(net, ra, kc, vc, 0, n, gb, fused, want_q8 ? &att_q8 : nullptr))) return rc;
         } else {
             // Each sequence's run of consecutive positions: longer than a decode pass on the MFMA
@@ -1659,6 +1842,10 @@ int stage_items(hkhip_net *net, const hkhip_item *items, uint32_t n, uint32_t *m
             net->runs.push_back({i, i + 1});
     }
     *max_pos = mp;
+    net->distinct = true; // every item in a slot of its own
+    for (uint32_t i = 0; i < n; i++)
+        for (uint32_t j = 0; j < i; j++)
+            if (sl[i] == sl[j]) net->distinct = false;
     NET_TRY(hipMemcpyAsync(net->io, net->stage, uint64_t(3) * net->cap * 4, hipMemcpyHostToDevice, net->eng->cur),
             "items");
     return HKHIP_OK;
@@ -1679,7 +1866,8 @@ int forward_staged(hkhip_net *net, uint32_t n, uint32_t max_pos, bool lg) {
     hipStream_t s = net->eng->cur;
     int rc;
     // Decode attention chunks: as many as cover positions 0..max_pos (ATT_DWAVES waves of 64
-    // positions each), so that short contexts skip the merge; one graph per (size, chunks), so a
+    // positions each), so that short contexts skip the merge; one graph per (size, chunks, whether
+    // every item has a slot of its own: the fused attention), so a
     // growing context captures a new graph every 128 positions. (Rounding the count up to a power of
     // two, for fewer graphs, launched up to 3 empty chunks per (head, token) at 512-575 positions:
     // 1.632 vs 1.626 ms per Llama-3-8B token, 0.838 vs 0.823 ms per Qwen3-0.6B token, 3.18 vs 3.12 ms
@@ -1691,7 +1879,7 @@ int forward_staged(hkhip_net *net, uint32_t n, uint32_t max_pos, bool lg) {
         NET_TRY(hipStreamSynchronize(s), "prefill pass");
         return HKHIP_OK;
     }
-    const uint32_t key = n | (gb << 8) | (lg ? 1u << 31 : 0u);
+    const uint32_t key = n | (gb << 8) | (net->distinct ? 1u << 30 : 0u) | (lg ? 1u << 31 : 0u);
     auto it = net->graphs.find(key);
     if (it != net->graphs.end()) {
         NET_TRY(hipGraphLaunch(it->second, s), "graph launch");
