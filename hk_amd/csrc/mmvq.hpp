@@ -918,9 +918,21 @@ __global__ __launch_bounds__(NW * 64) void mmvr_kernel(MvArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; i++) dst[i] = src[i];
     };
+    // The fused norm's weights of those chunks too, before any weight row: loaded after them, the
+    // staging would wait for the first step's rows (the memory counter is in order).
+    float4 nv[NORM ? PB : 1][4];
     if (a.x) {
 #pragma unroll
         for (int j = 0; j < PB; j++) xload(wave + NW * j, xv[j]);
+        if (NORM && a.norm) {
+#pragma unroll
+            for (int j = 0; j < PB; j++) {
+                const uint32_t cidx = wave + NW * j, e = 1024 * (cidx < nchunk ? cidx : nchunk - 1) + 16 * lane;
+                const float4 *wv = reinterpret_cast<const float4 *>(a.norm + (e < nflat ? e % K : 0));
+#pragma unroll
+                for (int i = 0; i < 4; i++) nv[NORM ? j : 0][i] = wv[i];
+            }
+        }
     } else {
 #pragma unroll
         for (int t = 0; t < NT; t++) {
@@ -946,12 +958,12 @@ __global__ __launch_bounds__(NW * 64) void mmvr_kernel(MvArgs a) {
         // The tokens' factors go to LDS (after the partial sums), not registers: NT of them live
         // through the staging pushed the 8-token kernels into spills.
         float *sinv = reinterpret_cast<float *>(smem + mvr_norm_offset(ntok, K, F::kq, KS > 1 ? NW * 64 * NT * 4 : 0)) + nflat / 16;
-        auto norm_chunk = [&](float4 *v, uint32_t e) {
+        auto norm_chunk = [&](float4 *v, uint32_t e, const float4 *w) { // w: the weights, or null (loaded here)
             const float inv = sinv[e < nflat ? e / K : 0];
             const float4 *wv = reinterpret_cast<const float4 *>(a.norm + (e < nflat ? e % K : 0));
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const float4 w4 = wv[i];
+                const float4 w4 = w ? w[i] : wv[i];
                 v[i].x = (v[i].x * inv) * w4.x;
                 v[i].y = (v[i].y * inv) * w4.y;
                 v[i].z = (v[i].z * inv) * w4.z;
@@ -994,7 +1006,7 @@ __global__ __launch_bounds__(NW * 64) void mmvr_kernel(MvArgs a) {
             __syncthreads();
 #pragma unroll
             for (int j = 0; j < PB; j++) {
-                norm_chunk(xv[j], 1024 * (wave + NW * j) + 16 * lane);
+                norm_chunk(xv[j], 1024 * (wave + NW * j) + 16 * lane, nv[NORM ? j : 0]);
                 asm volatile("" ::: "memory");
             }
         }
@@ -1009,7 +1021,7 @@ __global__ __launch_bounds__(NW * 64) void mmvr_kernel(MvArgs a) {
             for (int j = 0; j < PB; j++) xload(c0 + NW * j, xv[j]);
             if (NORM && a.norm) {
 #pragma unroll
-                for (int j = 0; j < PB; j++) norm_chunk(xv[j], 1024 * (c0 + NW * j) + 16 * lane);
+                for (int j = 0; j < PB; j++) norm_chunk(xv[j], 1024 * (c0 + NW * j) + 16 * lane, nullptr);
             }
 #pragma unroll
             for (int j = 0; j < PB; j++) {
