@@ -24,7 +24,8 @@ Also reported:
                 3072x1024 matvec, rotating over 160 copies); config 2 (a batch-1 decode step of a
                 Qwen3-0.6B-shaped decoder, tokens/s); the whole-network pass on Qwen3-0.6B and
                 Llama-3-8B shapes (prefill, one-token decode, and 8 sequences decoded together in one
-                pass over their own cache slots, with and without reading their logits)
+                pass over their own cache slots, with and without reading their logits); decode
+                attention at ~6000 positions (one layer of Llama-3-8B's attention shapes)
   measured_peaks  this GPU's dense int8 MFMA rate and HBM read rate from probe kernels
                 (hk_amd/csrc/peak.hip), quoted beside the published peaks the fractions use
   cpu_baseline  hk's CPU decode kernel restated with its SIMD paths (oracle/hk_cpu_simd.c, best
@@ -377,6 +378,7 @@ def main():
         eng.free(qhead)
         extra["network_qwen3_0_6b"] = network_bench(torch, eng, F, synth)
         extra["network_llama3_8b"] = network_bench(torch, eng, F, synth, "llama3_8b")
+        extra["long_context_attention"] = long_context_bench(torch, eng, F, synth)
         result["extra"] = extra
         phase("extra")
 
@@ -426,6 +428,48 @@ def main():
     }
     print(json.dumps(line), flush=True)
     eng.close()
+
+
+def long_context_bench(torch, eng, F, synth):
+    """Decode attention at long context: a one-layer network with Llama-3-8B's attention shapes
+    (dim 4096, 32 query / 8 key-value heads of 128, pairwise RoPE; FFN 256 and a 256-token
+    vocabulary, so the products stay small beside the attention), max_ctx 8192; 8 sequences
+    prefilled to 5800-6150 positions and then decoded together (one token each per pass), and one
+    sequence at 6000 positions decoded alone; with the kernel each pass chooses (attn_gqa 0) and
+    with the per-head kernel forced (2). Host clock per pass (graph replays)."""
+    import numpy as np
+
+    from hk_amd.net import Config, Net, Options
+
+    cfg = Config(dim=4096, n_layers=1, n_heads=32, n_kv_heads=8, head_dim=128, ffn_dim=256, vocab=256,
+                 max_ctx=8192, rope_neox=False, rope_base=500000.0, rms_eps=1e-5)
+    model = synth.model_np(cfg, F.Q4_K, seed=synth.seed_for(4, 600), out_fmt=F.Q6_K, embd_fmt=F.Q8_0, qk_norm=False)
+    lens = [5800 + 50 * i for i in range(8)]
+    out = {"context": "8 sequences at positions 5800-6170 (one token each per pass); one at 6000-6019"}
+    for mode, name in ((0, "chosen"), (2, "per_head")):
+        rng = np.random.default_rng(11)
+        with Net(eng, cfg, Options(slots=9, attn_gqa=mode)) as net:
+            net.load(model)
+            for i, ln in enumerate(lens):
+                net.forward_items([(1 + i, int(t), p) for p, t in enumerate(rng.integers(0, cfg.vocab, ln))])
+            step = lambda k: [(1 + i, int(rng.integers(0, cfg.vocab)), ln + k) for i, ln in enumerate(lens)]
+            for k in range(4):
+                net.forward_items(step(k))
+            t0 = time.perf_counter()
+            for k in range(4, 20):
+                net.forward_items(step(k))
+            multi_s = (time.perf_counter() - t0) / 16
+            net.forward_items([(99, int(t), p) for p, t in enumerate(rng.integers(0, cfg.vocab, 6000))])
+            for k in range(4):
+                net.forward_items([(99, 5, 6000 + k)])
+            t0 = time.perf_counter()
+            for k in range(4, 20):
+                net.forward_items([(99, 5, 6000 + k)])
+            one_s = (time.perf_counter() - t0) / 16
+            ok = bool(np.isfinite(net.logits_rows([0])).all())
+        out[name] = {"sessions8_ms_per_pass": round(multi_s * 1e3, 3), "one_token_ms_per_pass": round(one_s * 1e3, 3),
+                     "finite_logits": ok}
+    return out
 
 
 def network_bench(torch, eng, F, synth, which: str = "qwen3_0_6b"):
