@@ -195,8 +195,9 @@ def test_net_mixed_types(eng):
             pos += n
 
 
+@pytest.mark.parametrize("gqa", [0, 1], ids=["attn-by-size", "attn-grouped"])
 @pytest.mark.parametrize("kind", ["llama3", "yarn", "linear"])
-def test_net_rope_scaling(eng, kind):
+def test_net_rope_scaling(eng, kind, gqa):
     """Scaled RoPE: the host computes the inverse frequencies (and yarn's cos/sin magnitude) as hk's
     model setup does and hands them to the pass (hkhip_net_config.inv_freq / rope_mscale); llama3
     with per-frequency factors (a file's rope_freqs.weight)."""
@@ -211,7 +212,7 @@ def test_net_rope_scaling(eng, kind):
     model = synth.model_np(cfg, F.Q8_0, seed=4700, qk_norm=kind == "yarn")
     rng = np.random.default_rng(4701)
     cpu = Oracle(cfg, model)
-    with Net(eng, cfg) as net:
+    with Net(eng, cfg, Options(attn_gqa=gqa)) as net:
         net.load(model)
         pos = 0
         for n in [30, 1, 4, 1]:

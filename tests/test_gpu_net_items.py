@@ -258,18 +258,24 @@ def test_separate_attention_merge(eng, gqa):
             run_both(net, cpu, items, [k - 1, k], f"merge kernel, {k} + 1 tokens")
 
 
-@pytest.mark.parametrize("heads,kv_heads,hd", [(8, 1, 64), (6, 2, 128), (12, 2, 64), (16, 1, 64)],
-                         ids=["group8", "group3-hd128", "group6", "group16"])
-def test_grouped_attention_group_sizes(eng, heads, kv_heads, hd):
+@pytest.mark.parametrize("heads,kv_heads,hd,rope_dim,neox", [(8, 1, 64, 0, True), (6, 2, 128, 0, True), (12, 2, 64, 0, True),
+                                                          (16, 1, 64, 0, True), (8, 2, 128, 64, True),
+                                                          (8, 2, 128, 64, False), (8, 2, 128, 32, True)],
+                         ids=["group8", "group3-hd128", "group6", "group16", "rope64-neox", "rope64-pairwise",
+                              "rope32-neox-separate"])
+def test_grouped_attention_group_sizes(eng, heads, kv_heads, hd, rope_dim, neox):
     """The grouped decode attention kernel (forced by the options' knob) at GQA group sizes whose
     workgroups hold 8, 3 and 6 query heads and, for a group of 16, two head blocks per key/value
     head: two sequences past 1024 positions (16 chunks: the workgroup merging all its heads at once
     with the many-chunk merge), passes of 1, 2 and 1 + 3 tokens and a one-token pass of the short
-    sequence (4 chunks: the one-round merge)."""
+    sequence (4 chunks: the one-round merge). Passes whose tokens each have their own sequence do
+    the rope / cache work inside the kernel, q rotated in its operand registers: full and partial
+    rotary, neox and pairwise; neox partial rotary over 32 dimensions (pairs 16 apart) takes the
+    separate rope kernel."""
     from hk_amd.net import Net
 
     cfg = Config(dim=256, n_layers=1, n_heads=heads, n_kv_heads=kv_heads, head_dim=hd, ffn_dim=256, vocab=256,
-                 max_ctx=1200, rope_neox=True, rope_base=1e4)
+                 max_ctx=1200, rope_dim=rope_dim, rope_neox=neox, rope_base=1e4)
     model = synth.model_np(cfg, F.Q8_0, seed=5600 + heads, out_fmt=F.Q8_0, embd_fmt=F.Q8_0, qk_norm=True)
     rng = np.random.default_rng(5601)
     cpu = Oracle(cfg, model)
