@@ -536,7 +536,7 @@ def network_bench(torch, eng, F, synth, which: str = "qwen3_0_6b"):
         t0 = time.perf_counter()
         for k in range(36, 68):
             net.forward_items(step(k))
-            rows = net.logits_rows(list(range(8)))
+            rows = net.logits_view(list(range(8)))  # the engine's own rows, as hk's Device.logits
         multi_lg_s = (time.perf_counter() - t0) / 32
         ok = ok and bool(np.isfinite(rows).all())
     return {"prefill_512_ms": round(pre_s * 1e3, 2), "prefill_tokens_per_s": round(512 / pre_s, 1),

@@ -106,6 +106,7 @@ SIGNATURES = {
     "hkhip_net_forward_items": (_I, [_P, ctypes.POINTER(Item), _U32]),
     "hkhip_net_forward_partial": (_I, [_P, ctypes.POINTER(Item), _U32, _P]),
     "hkhip_net_logits_rows": (_I, [_P, _P, _U32, _P]),
+    "hkhip_net_logits_view": (_I, [_P, _P, _U32, _P]),
     "hkhip_net_release": (None, [_P, _U64]),
     "hkhip_net_max_rows": (_U32, [_P]),
     "hkhip_net_layer_count": (_U32, [_P]),

@@ -1358,6 +1358,7 @@ struct hkhip_net {
     uint32_t *io = nullptr, *tok = nullptr, *pos = nullptr, *slot = nullptr; // device [tok | pos | slot][cap]
     uint32_t *att_cnt = nullptr; // [MAX_DECODE][n_heads] decode attention chunk counters (zero between launches)
     uint32_t *stage = nullptr;   // pinned host copy of io
+    float *logits_h = nullptr;   // pinned host rows of hkhip_net_logits_view ([max_rows][vocab], on first use)
     // The current pass on the host: runs of consecutive positions of one sequence [begin, end).
     std::vector<std::pair<uint32_t, uint32_t>> runs;
     std::vector<uint64_t> owner; // sequence of each slot
@@ -2051,6 +2052,7 @@ void hkhip_net_destroy(hkhip_net *net) {
     for (auto &p : net->owned)
         if (p.first) (void)hipFree(p.first);
     if (net->stage) (void)hipHostFree(net->stage);
+    if (net->logits_h) (void)hipHostFree(net->logits_h);
     delete net;
 }
 
@@ -2151,8 +2153,41 @@ int hkhip_net_forward_partial(hkhip_net *net, const hkhip_item *items, uint32_t 
     return HKHIP_OK;
 }
 
+namespace {
+// The logits of rows idx[0..n) of the last pass into net->logits (device), on the engine's stream.
+int logits_compute(hkhip_net *net, const uint32_t *idx, uint32_t n);
+} // namespace
+
 int hkhip_net_logits_rows(hkhip_net *net, const uint32_t *idx, uint32_t n, float *host_out) {
     if (!net || !idx || !host_out) return set_error(HKHIP_E_BAD_ARGUMENT, "null argument");
+    const int rc = logits_compute(net, idx, n);
+    if (rc) return rc;
+    hipStream_t s = net->eng->cur;
+    NET_TRY(hipMemcpyAsync(host_out, net->logits, uint64_t(n) * net->cfg.vocab * 4, hipMemcpyDeviceToHost, s), "logits");
+    NET_TRY(hipStreamSynchronize(s), "logits");
+    return HKHIP_OK;
+}
+
+int hkhip_net_logits_view(hkhip_net *net, const uint32_t *idx, uint32_t n, const float **rows) {
+    if (!net || !idx || !rows) return set_error(HKHIP_E_BAD_ARGUMENT, "null argument");
+    *rows = nullptr;
+    const int rc = logits_compute(net, idx, n);
+    if (rc) return rc;
+    if (!net->logits_h && hipHostMalloc(reinterpret_cast<void **>(&net->logits_h), uint64_t(net->max_rows) * net->cfg.vocab * 4,
+                                        hipHostMallocDefault) != hipSuccess) {
+        net->logits_h = nullptr;
+        return set_error(HKHIP_E_DEVICE_FAILED, "hipHostMalloc of the pinned logits rows (%u x %u floats)", net->max_rows,
+                         net->cfg.vocab);
+    }
+    hipStream_t s = net->eng->cur;
+    NET_TRY(hipMemcpyAsync(net->logits_h, net->logits, uint64_t(n) * net->cfg.vocab * 4, hipMemcpyDeviceToHost, s), "logits");
+    NET_TRY(hipStreamSynchronize(s), "logits");
+    *rows = net->logits_h;
+    return HKHIP_OK;
+}
+
+namespace {
+int logits_compute(hkhip_net *net, const uint32_t *idx, uint32_t n) {
     if (!net->last_hidden) return set_error(HKHIP_E_BAD_ARGUMENT, "no full forward pass to read logits of");
     if (n < 1 || n > net->max_rows) return set_error(HKHIP_E_BAD_ARGUMENT, "%u rows: 1..%u", n, net->max_rows);
     const hkhip_net_config &c = net->cfg;
@@ -2172,12 +2207,9 @@ int hkhip_net_logits_rows(hkhip_net *net, const uint32_t *idx, uint32_t n, float
     }
     // One pass over the output matrix for every requested row (engine.zig:799-817).
     float *const ys[1] = {net->logits};
-    int rc = product(net, n, &net->output, 1, src, net->out_norm, ys, nullptr, HKHIP_STORE);
-    if (rc) return rc;
-    NET_TRY(hipMemcpyAsync(host_out, net->logits, uint64_t(n) * c.vocab * 4, hipMemcpyDeviceToHost, s), "logits");
-    NET_TRY(hipStreamSynchronize(s), "logits");
-    return HKHIP_OK;
+    return product(net, n, &net->output, 1, src, net->out_norm, ys, nullptr, HKHIP_STORE);
 }
+} // namespace
 
 void hkhip_net_release(hkhip_net *net, uint64_t seq) {
     if (!net) return;

@@ -152,6 +152,15 @@ class Net:
         check(lib().hkhip_net_logits_rows(self._h, idx.ctypes.data, idx.size, out.ctypes.data))
         return out
 
+    def logits_view(self, indices) -> np.ndarray:
+        """The same rows as logits_rows, as the reference's Device.logits returns them
+        (engine.zig:799-816): a view of the network's own (pinned) host buffer, valid until the
+        next call on this network, no copy."""
+        idx = np.ascontiguousarray(indices, dtype=np.uint32)
+        p = ctypes.c_void_p()
+        check(lib().hkhip_net_logits_view(self._h, idx.ctypes.data, idx.size, ctypes.byref(p)))
+        return np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_float)), shape=(idx.size, self.cfg.vocab))
+
     def release(self, seq: int) -> None:
         lib().hkhip_net_release(self._h, seq)
 

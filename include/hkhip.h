@@ -289,6 +289,11 @@ int hkhip_net_forward_partial(hkhip_net *net, const hkhip_item *items, uint32_t 
  * in the order of idx, to host_out [n][vocab]; 1 <= n <= hkhip_net_max_rows. One pass over the
  * output matrix for all rows. */
 int hkhip_net_logits_rows(hkhip_net *net, const uint32_t *idx, uint32_t n, float *host_out);
+/* Device.logits as the reference returns it (engine.zig:799-816: a slice of the engine's own host
+ * buffer, valid until the next call): the same rows, in pinned host memory the network owns
+ * ([max_rows][vocab] floats, allocated on the first call); *rows points at them until the next
+ * call on net. No copy into the caller's memory. */
+int hkhip_net_logits_view(hkhip_net *net, const uint32_t *idx, uint32_t n, const float **rows);
 /* Device.release (engine.zig:570-575): frees the slot of sequence seq (nothing if it holds none). */
 void hkhip_net_release(hkhip_net *net, uint64_t seq);
 /* Device.maxRows / layerCount / isPartial (backend.zig:147-185). */

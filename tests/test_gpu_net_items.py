@@ -326,8 +326,8 @@ def test_attention_output_quantized_in_kernel(eng, heads, kv_heads, hd):
 
 def test_logits_of_many_rows(eng):
     """logits(indices) for up to max_rows rows: 40 rows of a 48-token pass (the output product then
-    runs as a GEMM over the gathered rows), 12 rows gathered out of order (8-row decode passes), and a
-    request past max_rows refused."""
+    runs as a GEMM over the gathered rows), 12 rows gathered out of order (8-row decode passes), a
+    request past max_rows refused, and the same rows read as a view of the network's host rows."""
     from hk_amd import HipError
     from hk_amd.net import Net
 
@@ -348,6 +348,16 @@ def test_logits_of_many_rows(eng):
             net.logits_rows(list(range(49)))
         with pytest.raises(HipError):
             net.logits_rows([48])
+        # The reference's form of logits(indices): the network's own host rows, valid until the next
+        # call (engine.zig:799-816); the same values as the copying form, bit for bit.
+        view = net.logits_view(rows)
+        assert np.array_equal(view, got)
+        two = net.logits_rows([12, 47])  # (2 rows run the decode kernels: their own rounding)
+        view2 = net.logits_view([12, 47])
+        assert np.array_equal(view2, two)
+        assert view2.ctypes.data == view.ctypes.data  # one buffer, overwritten by the next call
+        with pytest.raises(HipError):
+            net.logits_view(list(range(49)))
 
 
 @pytest.mark.parametrize("device_layers", [1, 3])
