@@ -115,13 +115,15 @@ __global__ __launch_bounds__(256) void qact_q8k_row_kernel(RowIn in, Q8KOut o) {
         q8k_out(o, uint64_t(t) * nsb + sb, lane, quant_q8k_wave(row_values4(in, xr, inv, sb * QK_K + 4 * lane), lane));
 }
 
-// The norm case for rows of up to QACT_NORM_LDS values, one workgroup per row: the 16-byte load
+// The norm case for rows of up to QACT_NORM_LDS values, workgroups of (row, piece of 1024 values): the 16-byte load
 // f = 256 i + thread of the row is value 4 f.. of block 4 i + wave, lanes in value order, which is
 // exactly what the wave quantizing that block wants, so every value and its norm weight are loaded
 // once, up front, into registers (all loads in flight together), the sum of squares is reduced with
-// one barrier, and each wave quantizes its blocks from its registers. (Norm weights loaded inside
-// the block loop, and the row staged through LDS, put a dependent global round trip per block
-// behind two barriers: 6.2-7.6 us per launch at 8-512 rows.)
+// one barrier, and each wave quantizes the block of its workgroup's piece from its registers. (Norm
+// weights loaded inside the block loop, and the row staged through LDS, put a dependent global
+// round trip per block behind two barriers: 6.2-7.6 us per launch at 8-512 rows; one workgroup per
+// row, each wave quantizing its four blocks in turn: 8 sequences per Llama-3-8B pass 2.668 vs 2.529
+// ms with the row split four ways.)
 constexpr uint32_t QACT_NORM_LDS = 8192;
 __global__ __launch_bounds__(256) void qact_q8k_norm_row_kernel(RowIn in, Q8KOut o) {
     constexpr int IT = QACT_NORM_LDS / QK_K / 4; // blocks per wave at most
@@ -136,7 +138,7 @@ __global__ __launch_bounds__(256) void qact_q8k_norm_row_kernel(RowIn in, Q8KOut
         if (w + 4 * it < nsb) x[it] = xr4[(w + 4 * it) * 64 + lane];
 #pragma unroll
     for (int it = 0; it < IT; it++)
-        if (w + 4 * it < nsb) g[it] = g4[(w + 4 * it) * 64 + lane];
+        if (uint32_t(it) == blockIdx.y && w + 4 * it < nsb) g[it] = g4[(w + 4 * it) * 64 + lane];
     float ss = 0.0f;
 #pragma unroll
     for (int it = 0; it < IT; it++) {
@@ -152,10 +154,12 @@ __global__ __launch_bounds__(256) void qact_q8k_norm_row_kernel(RowIn in, Q8KOut
     __syncthreads();
     ss = (red[0] + red[1]) + (red[2] + red[3]);
     const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, float(in.k)) + in.eps));
+    // Workgroup (row, piece) quantizes blocks 4 piece .. 4 piece + 3 (one per wave; its loads hold
+    // them), every workgroup of the row summing the squares of the whole row in the same order.
 #pragma unroll
     for (int it = 0; it < IT; it++) {
         const uint32_t sb = w + 4 * it;
-        if (sb < nsb) {
+        if (uint32_t(it) == blockIdx.y && sb < nsb) {
             const float4 v = make_float4((x[it].x * inv) * g[it].x, (x[it].y * inv) * g[it].y,
                                          (x[it].z * inv) * g[it].z, (x[it].w * inv) * g[it].w);
             q8k_out(o, uint64_t(t) * nsb + sb, lane, quant_q8k_wave(v, lane));
@@ -193,7 +197,7 @@ hipError_t launch_qact_row(const float *x, uint32_t n, uint32_t k, int kind, uin
     if (kind == HKHIP_ACT_A8)
         qact_a8_row_kernel<<<grid, 256, 0, s>>>(in, a8_planes(xq, L, n, k));
     else if (norm && k <= QACT_NORM_LDS)
-        qact_q8k_norm_row_kernel<<<n, 256, 0, s>>>(in, q8k_planes(xq, L, n, k));
+        qact_q8k_norm_row_kernel<<<dim3(n, (k / QK_K + 3) / 4), 256, 0, s>>>(in, q8k_planes(xq, L, n, k));
     else
         qact_q8k_row_kernel<<<grid, 256, 0, s>>>(in, q8k_planes(xq, L, n, k));
     return hipGetLastError();
