@@ -329,7 +329,7 @@ template <int N> __device__ __forceinline__ void wait_loads(v4f (&r)[N]) {
 // workgroups of the same launch (loads at the coherence point).
 template <bool COH, int HD>
 __device__ void merge_chunks(const float *acc, const float *ml, float *out, uint32_t ng, uint32_t nslice, float *wts,
-                             float *lsh, float *tsh) {
+                             float *lsh, float *tsh, float *out_lds = nullptr) {
     auto ld = [&](const float *q) -> float {
         if constexpr (COH)
             return __hip_atomic_load(const_cast<float *>(q), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -406,7 +406,11 @@ __device__ void merge_chunks(const float *acc, const float *ml, float *out, uint
         for (uint32_t m = 1; m < tpo; m <<= 1)
 #pragma unroll
             for (int e = 0; e < 4; e++) sum[e] += __shfl_xor(sum[e], m);
-        if (j == 0) *reinterpret_cast<v4f *>(out + h * HD + 4 * d4) = sum * (1.0f / tsh[h]);
+        if (j == 0) {
+            const v4f r = sum * (1.0f / tsh[h]);
+            *reinterpret_cast<v4f *>(out + h * HD + 4 * d4) = r;
+            if (out_lds) *reinterpret_cast<v4f *>(out_lds + h * HD + 4 * d4) = r; // the same values, for this workgroup
+        }
     }
 }
 
@@ -467,15 +471,15 @@ __device__ __forceinline__ void norm_rope_row(float *h, const float (&x)[HD / 64
     norm_rope_row_cs<HD>(h, x, nw, nw_on, cs, sn, a, lane);
 }
 
-// The ng * HD results of token t's head block h0.. (written to att by this workgroup, visible to it
-// after the barrier) quantized as whole Q8K blocks, one wave per block (qact_q8k_kernel's steps).
+// The ng * HD results of token t's head block h0.. (the values this workgroup wrote to att, kept in
+// its LDS row qo) quantized as whole Q8K blocks, one wave per block (qact_q8k_kernel's steps).
 template <int HD, int NWV>
-__device__ __forceinline__ void attn_quantize_block(const AttnArgs &a, uint32_t t, uint32_t h0, uint32_t ng) {
+__device__ __forceinline__ void attn_quantize_block(const AttnArgs &a, uint32_t t, uint32_t h0, uint32_t ng,
+                                                    const float *qo) {
     __syncthreads();
     const uint32_t lane = threadIdx.x & 63, nb = ng * HD / QK_K, nsb = a.nh * HD / QK_K;
-    const float *row = a.merge_out + (uint64_t(t) * a.nh + h0) * HD;
     for (uint32_t j = threadIdx.x >> 6; j < nb; j += NWV) {
-        const float4 v = reinterpret_cast<const float4 *>(row + QK_K * j)[lane];
+        const float4 v = reinterpret_cast<const float4 *>(qo + QK_K * j)[lane];
         q8k_out(a.q8, uint64_t(t) * nsb + h0 * HD / QK_K + j, lane, quant_q8k_wave(v, lane));
     }
 }
@@ -504,6 +508,7 @@ __device__ __forceinline__ void attn_decode_finish(const AttnArgs &a, uint32_t g
             tot[gi] = fmaf(wt[gi][i], red_l[i][gi], tot[gi]);
         }
     }
+    __shared__ float qo[G * HD]; // with q8_on: this workgroup's results, for attn_quantize_block
     if (a.att) { // one chunk: the normalized result (as attn_combine_kernel writes it)
 #pragma unroll
         for (int gi = 0; gi < G; gi++) {
@@ -515,9 +520,10 @@ __device__ __forceinline__ void attn_decode_finish(const AttnArgs &a, uint32_t g
 #pragma unroll
                 for (int i = 0; i < NWV; i++) v = fmaf(wt[gi][i], red_acc[i][gi][d], v);
                 o[d] = v * inv;
+                if (a.q8_on) qo[gi * HD + d] = v * inv;
             }
         }
-        if (a.q8_on) attn_quantize_block<HD, NWV>(a, t, h0, ng);
+        if (a.q8_on) attn_quantize_block<HD, NWV>(a, t, h0, ng, qo);
         return;
     }
     // The chunk's partials per head: acc (unnormalized) and {max, sum}, as attn_combine_kernel reads
@@ -597,12 +603,13 @@ __device__ __forceinline__ void attn_decode_finish(const AttnArgs &a, uint32_t g
                 }
             }
             a.merge_out[(uint64_t(t) * a.nh + h0 + gi) * HD + d] = av * (1.0f / sum);
+            if (a.q8_on) qo[gi * HD + d] = av * (1.0f / sum);
         }
     } else {
         merge_chunks<true, HD>(a.part + p0 * HD, a.part_ml + ATT_ML * p0, a.merge_out + (uint64_t(t) * a.nh + h0) * HD, ng,
-                               gridDim.x, mw, ml_, mt);
+                               gridDim.x, mw, ml_, mt, a.q8_on ? qo : nullptr);
     }
-    if (a.q8_on) attn_quantize_block<HD, NWV>(a, t, h0, ng);
+    if (a.q8_on) attn_quantize_block<HD, NWV>(a, t, h0, ng, qo);
 }
 
 // G query heads h0 .. h0 + G - 1 that share one key/value head (G divides the group size: the
