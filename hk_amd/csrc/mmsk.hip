@@ -446,11 +446,13 @@ hipError_t launch_mmsk_parts(int t, const MvPartDesc *parts, int nparts, uint32_
     a.ilmb = xq + A.k_ilmb;
     a.ild = reinterpret_cast<const float *>(xq + A.k_ild);
     a.mode = mode;
-    // K slices: enough waves for ~2048 in the launch, each with at least 4 super-blocks when
-    // the matrix has them.
+    // K slices: enough waves for ~2048 in the launch, each with at least 2 super-blocks when the
+    // matrix has them. (At least 4, as first set, left Qwen3-0.6B's products at 8 tokens on 64-384
+    // workgroups of one or two waves: 8 sequences per pass 1.49-1.51 vs 1.34-1.36 ms; the Llama-3-8B
+    // pass and batch-8 step measured the same either way, 2.51-2.53 and 2.03-2.13 ms.)
     const uint32_t nsb = cols / 256;
     uint32_t ks = 1;
-    while (ks < sk_max_ks<RT>() && tiles * ks * 2 <= 2048 && nsb / (2 * ks) >= 4) ks *= 2;
+    while (ks < sk_max_ks<RT>() && tiles * ks * 2 <= 2048 && nsb / (2 * ks) >= 2) ks *= 2;
     // A ring of two slots: one super-block in flight while the other is computed. Deeper rings keep
     // more bytes in flight per wave but need more registers for the activations, which halves
     // the waves per SIMD (Q4_K, 16 tokens: 116 VGPRs and four waves at two slots, 192 and two at
