@@ -452,6 +452,8 @@ hipError_t launch_mmsk_parts(int t, const MvPartDesc *parts, int nparts, uint32_
     // pass and batch-8 step measured the same either way, 2.51-2.53 and 2.03-2.13 ms.)
     const uint32_t nsb = cols / 256;
     uint32_t ks = 1;
+    // (More waves, K slices up to 4096 or 8192 in the launch: the Llama-3-8B 8-sequence pass 2.57-2.62
+    // vs 2.52 ms.)
     while (ks < sk_max_ks<RT>() && tiles * ks * 2 <= 2048 && nsb / (2 * ks) >= 2) ks *= 2;
     // A ring of two slots: one super-block in flight while the other is computed. Deeper rings keep
     // more bytes in flight per wave but need more registers for the activations, which halves
