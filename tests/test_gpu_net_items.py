@@ -195,6 +195,37 @@ def test_partial_offload(eng):
         assert e.value.code == E_PARTIAL
 
 
+@pytest.mark.parametrize("gqa,merge_max", [(0, 0), (1, 0), (0, 2), (1, 2)],
+                         ids=["per-head", "grouped", "per-head-merge-kernel", "grouped-merge-kernel"])
+def test_attention_merges_at_the_hidden_state_bar(eng, gqa, merge_max):
+    """The decode attention merges held to the products' 1e-3 on hidden states (a partial network
+    hands them back before any requantizing product of later layers): two sequences past 1024 and
+    2048 positions, so the chunk counts run through the one-round merge (up to 8 chunks), the
+    many-chunk merge (9-17) and, with the merge limit lowered to 2, the separate merge kernel; passes
+    of 1, 2, 3 and 8 tokens (the 8-token passes on the small-batch products, the grouped kernel
+    quantizing their o input)."""
+    from hk_amd.net import Net
+
+    cfg = Config(dim=256, n_layers=2, n_heads=8, n_kv_heads=2, head_dim=64, ffn_dim=512, vocab=300, max_ctx=2300,
+                 rope_neox=True, rope_base=1e4)
+    model = synth.model_np(cfg, F.Q4_K, seed=5800, out_fmt=F.Q6_K, embd_fmt=F.Q8_0, qk_norm=True)
+    rng = np.random.default_rng(5801)
+    cpu = Oracle(cfg, model)
+    with Net(eng, cfg, Options(slots=2, layers=1, attn_gqa=gqa, attn_merge_max=merge_max)) as net:
+        net.load(model)
+        pos = {0: 0, 1: 0}
+        for plan in ([(0, 1000)], [(1, 300)], [(0, 1)], [(0, 1), (1, 1)], [(0, 3)], [(0, 8)], [(0, 30)],
+                     [(0, 1)], [(0, 1), (1, 1)], [(0, 1010)], [(0, 1), (1, 1)], [(0, 8)], [(0, 1)]):
+            items = []
+            for seq, k in plan:
+                items += seq_items(seq, rng.integers(0, cfg.vocab, k), pos[seq])
+                pos[seq] += k
+            h_in = cpu.embed([t for _, t, _ in items])
+            got = net.forward_partial(items, h_in)
+            want = cpu.forward_items(items, hidden=h_in, layers=1)
+            check(got, want, f"{plan} (positions {pos})", HIDDEN_REL)
+
+
 @pytest.mark.parametrize("layers", [0, 1])
 def test_bytes_needed_matches_the_allocations(eng, layers):
     """bytesNeeded's estimate is what the network allocates (its own buffers and the uploaded
