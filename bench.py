@@ -547,7 +547,8 @@ def network_bench(torch, eng, F, synth, which: str = "qwen3_0_6b"):
             "sessions8_context": "8 sequences at positions 260-515, one token each per pass",
             "what": f"whole network on the device: embedding, {n_layers_desc}: RMS norm fused into the products' "
                     "input quantization, rope, f16 KV cache, prefill attention on f16 MFMAs, decode attention over "
-                    "context chunks; logits; host wall clock per forward call"}
+                    "context chunks (per query head, or per GQA group on f16 MFMAs for large passes); logits; "
+                    "host wall clock per forward call"}
 
 
 def measured_peaks():
