@@ -1151,6 +1151,7 @@ __global__ __launch_bounds__(NWV * 64, 2) void attn_prefill_kernel(AttnPArgs a) 
     const uint64_t sl = a.slot[0];
     const uint32_t t = tile * 32 + j, tc = t < a.n ? t : a.n - 1; // this lane's token (clamped)
     const uint32_t tpos = pos0 + tc;
+    const uint32_t tfirst = pos0 + tile * 32; // the tile's first token position (lane 0's)
     const uint32_t pend = pos0 + min(tile * 32 + 32, a.n); // positions [0, pend) are needed
 
     // The tile's q operands (the same 32 tokens for the four waves) live in LDS, split over the
@@ -1214,13 +1215,22 @@ __global__ __launch_bounds__(NWV * 64, 2) void attn_prefill_kernel(AttnPArgs a) 
         }
         if (pn < pend) load_k(pn);
         // Score v of this lane: position p0 + 16(g >> 1) + 8h + 4(g & 1) + e, g = v / 4, e = v % 4.
+        // Only the tiles reaching past the tile's first token position are masked.
         float sv[16], mx = -INFINITY;
+        if (p0 + 31 > tfirst) {
 #pragma unroll
-        for (int v = 0; v < 16; v++) {
-            const int g = v / 4, e = v % 4;
-            const uint32_t pp = p0 + 16 * (g >> 1) + 8 * h + 4 * (g & 1) + e;
-            sv[v] = pp <= tpos ? s[v] * a.scale : -INFINITY;
-            mx = fmaxf(mx, sv[v]);
+            for (int v = 0; v < 16; v++) {
+                const int g = v / 4, e = v % 4;
+                const uint32_t pp = p0 + 16 * (g >> 1) + 8 * h + 4 * (g & 1) + e;
+                sv[v] = pp <= tpos ? s[v] * a.scale : -INFINITY;
+                mx = fmaxf(mx, sv[v]);
+            }
+        } else {
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                sv[v] = s[v] * a.scale;
+                mx = fmaxf(mx, sv[v]);
+            }
         }
         mx = fmaxf(mx, __shfl_xor(mx, 32));
         const float mn = fmaxf(m, mx);
@@ -1236,10 +1246,13 @@ __global__ __launch_bounds__(NWV * 64, 2) void attn_prefill_kernel(AttnPArgs a) 
         ps += __shfl_xor(ps, 32);
         l = l * corr + ps;
         m = mn;
+        // The running sums need rescaling only where some lane's maximum moved.
+        if (__any(corr != 1.0f)) {
 #pragma unroll
-        for (int d = 0; d < NDT; d++)
+            for (int d = 0; d < NDT; d++)
 #pragma unroll
-            for (int v = 0; v < 16; v++) acc[d][v] *= corr;
+                for (int v = 0; v < 16; v++) acc[d][v] *= corr;
+        }
 #pragma unroll
         for (int cc = 0; cc < 2; cc++) {
             v8h ph, pl;
