@@ -1,7 +1,7 @@
 """Synthetic weights and activations of the shapes the benchmarks and tests use.
 
 Blocks are random but valid: quant bytes are uniform; scale fields are finite f16 drawn as
-SURVEY-style |N(0, 0.02)| magnitudes (per format below); activations are N(0, 1) f32, with an
+|N(0, 0.02)| magnitudes (the spread of trained weights' block scales) (per format below); activations are N(0, 1) f32, with an
 optional fraction of outliers at +-20. The same generator runs on NumPy (host, tests and the
 CPU baseline) or torch (device, for multi-GB benchmark matrices).
 
