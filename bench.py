@@ -436,7 +436,8 @@ def long_context_bench(torch, eng, F, synth):
     vocabulary, so the products stay small beside the attention), max_ctx 8192; 8 sequences
     prefilled to 5800-6150 positions and then decoded together (one token each per pass), and one
     sequence at 6000 positions decoded alone; with the kernel each pass chooses (attn_gqa 0) and
-    with the per-head kernel forced (2). Host clock per pass (graph replays)."""
+    with the per-head kernel forced (2). Host clock per pass (graph replays); also the 6000-token
+    prompt's prefill pass (one layer: its GEMMs and the MFMA prefill attention)."""
     import numpy as np
 
     from hk_amd.net import Config, Net, Options
@@ -459,7 +460,12 @@ def long_context_bench(torch, eng, F, synth):
             for k in range(4, 20):
                 net.forward_items(step(k))
             multi_s = (time.perf_counter() - t0) / 16
-            net.forward_items([(99, int(t), p) for p, t in enumerate(rng.integers(0, cfg.vocab, 6000))])
+            torch.cuda.synchronize()
+            prompt = [(99, int(t), p) for p, t in enumerate(rng.integers(0, cfg.vocab, 6000))]
+            t0 = time.perf_counter()
+            net.forward_items(prompt)
+            torch.cuda.synchronize()
+            prefill_s = time.perf_counter() - t0
             for k in range(4):
                 net.forward_items([(99, 5, 6000 + k)])
             t0 = time.perf_counter()
@@ -469,6 +475,8 @@ def long_context_bench(torch, eng, F, synth):
             ok = bool(np.isfinite(net.logits_rows([0])).all())
         out[name] = {"sessions8_ms_per_pass": round(multi_s * 1e3, 3), "one_token_ms_per_pass": round(one_s * 1e3, 3),
                      "finite_logits": ok}
+        if mode == 0:  # the prefill kernels do not depend on the decode attention choice
+            out["prefill_6000_ms"] = round(prefill_s * 1e3, 2)
     return out
 
 

@@ -103,8 +103,8 @@ SIGNATURES = {
     "hkhip_gemm_host": (_I, [_U8, _P, _P, _P, _P, _U64, _U64, _U64]),
     "hkhip_net_create": (_I, [_P, ctypes.POINTER(NetConfig), ctypes.POINTER(_P)]),
     "hkhip_net_create_opts": (_I, [_P, ctypes.POINTER(NetConfig), ctypes.POINTER(NetOptions), ctypes.POINTER(_P)]),
-    "hkhip_net_forward_items": (_I, [_P, ctypes.POINTER(Item), _U32]),
-    "hkhip_net_forward_partial": (_I, [_P, ctypes.POINTER(Item), _U32, _P]),
+    "hkhip_net_forward_items": (_I, [_P, _P, _U32]),
+    "hkhip_net_forward_partial": (_I, [_P, _P, _U32, _P]),
     "hkhip_net_logits_rows": (_I, [_P, _P, _U32, _P]),
     "hkhip_net_logits_view": (_I, [_P, _P, _U32, _P]),
     "hkhip_net_release": (None, [_P, _U64]),

@@ -1883,9 +1883,11 @@ int stage_items(hkhip_net *net, const hkhip_item *items, uint32_t n, uint32_t *m
     }
     *max_pos = mp;
     net->distinct = true; // every item in a slot of its own
-    for (uint32_t i = 0; i < n; i++)
-        for (uint32_t j = 0; j < i; j++)
-            if (sl[i] == sl[j]) net->distinct = false;
+    std::vector<uint8_t> seen(net->n_slots, 0);
+    for (uint32_t i = 0; i < n && net->distinct; i++) {
+        if (seen[sl[i]]) net->distinct = false;
+        seen[sl[i]] = 1;
+    }
     NET_TRY(hipMemcpyAsync(net->io, net->stage, uint64_t(3) * net->cap * 4, hipMemcpyHostToDevice, net->eng->cur),
             "items");
     return HKHIP_OK;

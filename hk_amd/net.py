@@ -71,10 +71,25 @@ class Options:
         return NetOptions(self.slots, self.layers, self.n_batch, self.attn_merge_max, self.attn_gqa)
 
 
+# hkhip_item's layout (include/hkhip.h): u64 seq, u32 token, u32 pos -- 16 bytes, no padding.
+_ITEM_DTYPE = np.dtype([("seq", "<u8"), ("token", "<u4"), ("pos", "<u4")])
+assert _ITEM_DTYPE.itemsize == ctypes.sizeof(Item)
+
+
 def _items(items) -> tuple:
-    """(ctypes array, count) of hkhip_item from (seq, token, pos) triples."""
-    arr = (Item * max(len(items), 1))(*[Item(int(s), int(t), int(p)) for s, t, p in items])
-    return arr, len(items)
+    """(pointer, count, keep-alive array) of hkhip_item from (seq, token, pos) triples, built in
+    bulk (a prompt's thousands of items)."""
+    n = len(items)
+    if n == 0:
+        arr = np.zeros(1, _ITEM_DTYPE)
+    elif isinstance(items, np.ndarray):  # an [n][3] array
+        a = items.reshape(n, 3).astype(np.uint64)
+        arr = np.empty(n, _ITEM_DTYPE)
+        arr["seq"], arr["token"], arr["pos"] = a[:, 0], a[:, 1], a[:, 2]
+    else:
+        arr = np.fromiter((tuple(it) for it in items) if not isinstance(items[0], tuple) else items,
+                          _ITEM_DTYPE, n)
+    return arr.ctypes.data, n, arr
 
 
 def _layer(tensors: dict, keep: list) -> NetLayer:
@@ -135,15 +150,15 @@ class Net:
     # Device.forward / forwardPartial / logits / release / maxRows / layerCount / isPartial
     def forward_items(self, items) -> None:
         """One pass over (seq, token, pos) items of one or more sequences."""
-        arr, n = _items(items)
-        check(lib().hkhip_net_forward_items(self._h, arr, n))
+        p, n, _keep = _items(items)
+        check(lib().hkhip_net_forward_items(self._h, p, n))
 
     def forward_partial(self, items, hidden: np.ndarray) -> np.ndarray:
         """A partial network's pass: hidden [n][dim] in, the state after its last layer out."""
-        arr, n = _items(items)
+        p, n, _keep = _items(items)
         h = np.ascontiguousarray(hidden, dtype=np.float32).copy()
         assert h.shape == (n, self.cfg.dim)
-        check(lib().hkhip_net_forward_partial(self._h, arr, n, h.ctypes.data))
+        check(lib().hkhip_net_forward_partial(self._h, p, n, h.ctypes.data))
         return h
 
     def logits_rows(self, indices) -> np.ndarray:
