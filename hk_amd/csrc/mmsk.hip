@@ -33,6 +33,8 @@
 // the activation loads are ordinary, and the compiler's waits for them, which do not count the
 // direct loads, keep about one super-block less in flight. The launches use PF = 2: fewer bytes
 // in flight per wave, but twice the waves per SIMD of a deeper ring (see launch_mmsk_parts).
+// Launches of up to 8 tokens and 256 or more four-tile workgroups take mmsa_kernel instead, whose
+// workgroups stage the tokens' activations in LDS once rather than every wave re-reading them.
 
 #include "common.hpp"
 
@@ -64,6 +66,7 @@ struct SkPart {
 struct SkArgs {
     SkPart p[SK_PARTS];
     uint32_t nparts, K, n, tiles; // tiles: 16-token tiles of the interleaved planes
+    uint32_t rtiles;              // 16-row tiles of the launch (the shared-activation kernel)
     const uint8_t *il;
     const uint8_t *ilmb;
     const float *ild;
@@ -310,7 +313,9 @@ __global__ __launch_bounds__(KS * 64) void mmsk_kernel(SkArgs a) {
     const uint32_t sb0 = nsb * wave / KS, sb1 = nsb * (wave + 1) / KS;
 
     // Weight piece P = 64i + lane (16 bytes) of a super-block: byte 16*(P % PPR) of row P / PPR's
-    // block; pieces past the last repeat it (they land in the slot's padding).
+    // block; pieces past the last repeat it (they land in the slot's padding). Q6_K's scale words
+    // sit right after the rows, where the last load's padding lanes would write: those lanes are
+    // switched off (two direct loads into the same LDS bytes land in no defined order).
     constexpr uint32_t PPR = RB / 16, NP = PPR * 16 * RT;
     uint32_t woff[NDMA];
 #pragma unroll
@@ -332,7 +337,8 @@ __global__ __launch_bounds__(KS * 64) void mmsk_kernel(SkArgs a) {
     auto issue = [&](uint32_t sb, uint8_t *slot, SkAct<NTT> &x) {
         const uint8_t *gw = W + uint64_t(sb) * RB;
 #pragma unroll
-        for (uint32_t i = 0; i < NDMA; i++) load_lds16(gw + woff[i], slot + 1024 * i);
+        for (uint32_t i = 0; i < NDMA; i++)
+            if (!q6 || 64 * i + lane < NP) load_lds16(gw + woff[i], slot + 1024 * i);
         if constexpr (q6) load_lds4(WS + (((sbase + sb) >> 1) << 2), slot + 16 * RB);
 #pragma unroll
         for (int tt = 0; tt < NTT; tt++) {
@@ -391,6 +397,156 @@ __global__ __launch_bounds__(KS * 64) void mmsk_kernel(SkArgs a) {
                 for (int w = 0; w < KS - 1; w++) acc[rt][tt] += part[w][rt][tt][lane];
         sk_store<NTT, RT>(acc, a.n, a.mode, r0, rows, Y, B, g, p);
     }
+}
+
+
+// ---- Shared-activation variant (at most SA_TOK tokens, one token tile) ----
+//
+// Each wave above re-reads a super-block's activation operands from L2 for every 16-row tile
+// (5.3 KB against the tile's 2.3 KB of weights), and those reads, not the weights, set its rate
+// (a loads-only probe of that structure: 20.1 us for 66 MB, against 13.1 us for the weights
+// alone). Here a workgroup of SA_NR waves, each with its own 16-row tile over the whole K, first
+// copies the live tokens' interleaved entries (k_il / k_ilmb / k_ild, tokens 0..SA_TOK-1 of tile
+// 0) into LDS by direct loads, behind one barrier; afterwards a wave's only global loads are its
+// weights, through the same two-slot ring, and the activation operands come from LDS (the probe
+// of this structure: 14.7 us). Measured at 8 tokens on Llama-3-8B shapes, alternating runs against
+// the kernel above: the batch-8 decode step 1.97-2.04 vs 2.09-2.10 ms, gate/up 21.4-22.4 vs
+// 21.6-23.9 us; a ring of three or four slots (no register cost here) was slower, 23.4-23.9 us.
+constexpr uint32_t SA_NR = 4, SA_TOK = 8, SA_PF = 2;
+
+// LDS geometry: A [nsb*4 chunks][4 g][SA_TOK] x 16 B, MB [nsb][2][SA_TOK] x 16 B (Q4_K),
+// D [nsb][SA_TOK] f32, then the waves' rings; each staged region padded to whole direct loads.
+struct SaGeom {
+    uint32_t la, lm, ld; // direct loads of each region (1 KB, 1 KB, 256 B)
+    uint32_t mb, d, ring, total;
+};
+template <int T> __host__ __device__ inline SaGeom sa_geom(uint32_t nsb) {
+    SaGeom G{};
+    G.la = nsb * 16 * SA_TOK / 64;
+    G.lm = T == HKHIP_Q6_K ? 0 : (nsb * 2 * SA_TOK + 63) / 64;
+    G.ld = (nsb * SA_TOK + 63) / 64;
+    G.mb = 1024 * G.la;
+    G.d = G.mb + 1024 * G.lm;
+    G.ring = G.d + 256 * G.ld;
+    G.total = G.ring + SA_NR * SA_PF * 1024 * sk_dma<T, 1>();
+    return G;
+}
+
+template <int T>
+__global__ __launch_bounds__(SA_NR * 64) void mmsa_kernel(SkArgs a) {
+    constexpr bool q6 = T == HKHIP_Q6_K;
+    constexpr uint32_t RB = sk_rb<T>(), NDMA = sk_dma<T, 1>(), SLOT = 1024 * NDMA;
+    constexpr int OPS = NDMA + (q6 ? 1 : 0); // loads per super-block and wave
+    extern __shared__ __attribute__((aligned(16))) uint8_t sa_smem[];
+
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t g = lane >> 4, p = lane & 15;
+    const uint32_t nsb = a.K / 256, last = nsb - 1;
+    const SaGeom G = sa_geom<T>(nsb);
+    uint8_t *const A = sa_smem;
+    uint8_t *const MB = sa_smem + G.mb;
+    uint8_t *const D = sa_smem + G.d;
+    uint8_t *const ring = sa_smem + G.ring + wave * SA_PF * SLOT;
+
+    // This wave's row tile and its part (wave-uniform); waves past the last tile stage and wait
+    // with the others, then stream the last tile again and store nothing.
+    const uint32_t tile_raw = blockIdx.x * SA_NR + wave;
+    const bool real = tile_raw < a.rtiles;
+    const uint32_t tile = real ? tile_raw : a.rtiles - 1;
+    uint32_t pi = 0;
+#pragma unroll
+    for (int i = 1; i < SK_PARTS; i++)
+        if (i < int(a.nparts) && tile >= a.p[i].tile0) pi = i;
+    const uint8_t *W = a.p[0].w;
+    const uint8_t *WS = a.p[0].ws;
+    float *Y = a.p[0].y;
+    const float *B = a.p[0].bias;
+    uint32_t rows = a.p[0].rows, tile0 = a.p[0].tile0;
+#pragma unroll
+    for (int i = 1; i < SK_PARTS; i++) {
+        if (pi == uint32_t(i)) {
+            W = a.p[i].w;
+            WS = a.p[i].ws;
+            Y = a.p[i].y;
+            B = a.p[i].bias;
+            rows = a.p[i].rows;
+            tile0 = a.p[i].tile0;
+        }
+    }
+    const uint32_t r0 = (tile - tile0) * 16;
+
+    constexpr uint32_t PPR = RB / 16, NP = PPR * 16;
+    uint32_t woff[NDMA];
+#pragma unroll
+    for (uint32_t i = 0; i < NDMA; i++) {
+        const uint32_t P = 64 * i + lane < NP ? 64 * i + lane : NP - 1;
+        const uint32_t row = r0 + P / PPR < rows ? r0 + P / PPR : rows - 1;
+        woff[i] = row * nsb * RB + 16 * (P % PPR);
+    }
+    const uint32_t srow = r0 + (lane & 15) < rows ? r0 + (lane & 15) : rows - 1;
+    const uint32_t sbase = srow * nsb;
+    auto issue = [&](uint32_t sb, uint8_t *slot) {
+        const uint8_t *gw = W + uint64_t(sb) * RB;
+#pragma unroll
+        for (uint32_t i = 0; i < NDMA; i++)
+            if (!q6 || 64 * i + lane < NP) load_lds16(gw + woff[i], slot + 1024 * i);
+        if constexpr (q6) load_lds4(WS + (((sbase + sb) >> 1) << 2), slot + 16 * RB);
+    };
+#pragma unroll
+    for (uint32_t i = 0; i + 1 < SA_PF; i++) issue(i < last ? i : last, ring + SLOT * i);
+
+    // Staging: direct load i of a region goes to wave i % SA_NR; entry q = 64*i + lane. Tokens
+    // past n take the last token's entries (never read: padding lanes read that token's own).
+    const uint32_t nt = a.n;
+    auto tok = [&](uint32_t q) { const uint32_t t = q % SA_TOK; return t < nt ? t : nt - 1; };
+    for (uint32_t i = wave; i < G.la; i += SA_NR) {
+        const uint32_t q = 64 * i + lane, gq = (q / SA_TOK) % 4, ch = q / (4 * SA_TOK);
+        load_lds16(a.il + (uint64_t(ch) * a.tiles * 64 + 16 * gq + tok(q)) * 16, A + 1024 * i);
+    }
+    if constexpr (!q6) {
+        for (uint32_t i = wave; i < G.lm; i += SA_NR) {
+            const uint32_t q = 64 * i + lane, h1 = (q / SA_TOK) % 2;
+            const uint32_t sb = q / (2 * SA_TOK) < nsb ? q / (2 * SA_TOK) : last;
+            load_lds16(a.ilmb + ((uint64_t(sb) * a.tiles) * 2 + h1) * 256 + 16 * tok(q), MB + 1024 * i);
+        }
+    }
+    for (uint32_t i = wave; i < G.ld; i += SA_NR) {
+        const uint32_t q = 64 * i + lane;
+        const uint32_t sb = q / SA_TOK < nsb ? q / SA_TOK : last;
+        load_lds4(a.ild + (uint64_t(sb) * a.tiles) * 16 + tok(q), D + 256 * i);
+    }
+    wait_vm<0>();
+    __syncthreads();
+
+    const uint32_t tpc = p < nt ? p : nt - 1;
+    auto fetch = [&](uint32_t sb, SkAct<1> &x) {
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            x.a[0][c] = *reinterpret_cast<const v4i *>(A + (((4 * sb + c) * 4 + g) * SA_TOK + tpc) * 16);
+        if constexpr (!q6) x.mb[0] = *reinterpret_cast<const v4i *>(MB + ((sb * 2 + (g & 1)) * SA_TOK + tpc) * 16);
+        x.da[0] = *reinterpret_cast<const float *>(D + (sb * SA_TOK + tpc) * 4);
+    };
+
+    v4f acc[1][1] = {{v4f{0.0f, 0.0f, 0.0f, 0.0f}}};
+    for (uint32_t sb = 0; sb <= last; sb += SA_PF) {
+#pragma unroll
+        for (uint32_t i = 0; i < SA_PF; i++) {
+            const uint32_t nx = sb + i + SA_PF - 1;
+            issue(nx < last ? nx : last, ring + SLOT * ((i + SA_PF - 1) % SA_PF));
+            wait_vm<OPS * (SA_PF - 1)>();
+            const uint32_t cur = sb + i <= last ? sb + i : last;
+            SkAct<1> x;
+            fetch(cur, x);
+            const float keep = sb + i <= last ? 1.0f : 0.0f;
+            if constexpr (q6)
+                sk_step_q6k<1>(ring + SLOT * i, x, keep, g, p, (sbase + cur) & 1, acc);
+            else
+                sk_step_q4k<1, 1>(ring + SLOT * i, x, keep, g, p, acc);
+        }
+    }
+    wait_vm<0>();
+    if (real) sk_store<1, 1>(acc, a.n, a.mode, r0, rows, Y, B, g, p);
 }
 
 typedef void (*sk_kernel_t)(SkArgs);
@@ -455,6 +611,23 @@ hipError_t launch_mmsk_parts(int t, const MvPartDesc *parts, int nparts, uint32_
     // (More waves, K slices up to 4096 or 8192 in the launch: the Llama-3-8B 8-sequence pass 2.57-2.62
     // vs 2.52 ms.)
     while (ks < sk_max_ks<RT>() && tiles * ks * 2 <= 2048 && nsb / (2 * ks) >= 2) ks *= 2;
+    // Up to SA_TOK tokens, a launch of at least 256 shared-activation workgroups whose staged
+    // activations leave room for two workgroups per CU: that kernel.
+    if (n <= sk::SA_TOK && (tiles + sk::SA_NR - 1) / sk::SA_NR >= 256) {
+        const uint32_t lds = t == HKHIP_Q6_K ? sk::sa_geom<HKHIP_Q6_K>(nsb).total : sk::sa_geom<HKHIP_Q4_K>(nsb).total;
+        if (lds <= 80u * 1024) {
+            const sk_kernel_t k = t == HKHIP_Q6_K ? sk::mmsa_kernel<HKHIP_Q6_K> : sk::mmsa_kernel<HKHIP_Q4_K>;
+            static bool attr[2] = {false, false};
+            if (!attr[t == HKHIP_Q6_K]) {
+                (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                          int(80u * 1024));
+                attr[t == HKHIP_Q6_K] = true;
+            }
+            a.rtiles = tiles;
+            hipLaunchKernelGGL(k, dim3((tiles + sk::SA_NR - 1) / sk::SA_NR), dim3(sk::SA_NR * 64), lds, s, a);
+            return hipGetLastError();
+        }
+    }
     // A ring of two slots: one super-block in flight while the other is computed. Deeper rings keep
     // more bytes in flight per wave but need more registers for the activations, which halves
     // the waves per SIMD (Q4_K, 16 tokens: 116 VGPRs and four waves at two slots, 192 and two at

@@ -691,6 +691,29 @@ def test_small_batch_many_tiles(eng, torch_cuda, t, n, mode):
         eng.free(w)
 
 
+@pytest.mark.parametrize("t", [F.Q4_K, F.Q6_K])
+@pytest.mark.parametrize("n,m,k", [(7, 16400, 768), (4, 16385, 256), (8, 24576, 1280)])
+def test_small_batch_shared_activations(eng, torch_cuda, t, n, m, k):
+    """The small-batch products whose launch is large enough for workgroups that stage the tokens'
+    activations in LDS once (at most 8 tokens, 256 or more workgroups of four 16-row tiles): odd
+    super-block counts (ring steps past the end), a single super-block, and a last workgroup
+    whose waves are mostly past the last row tile (16400 and 16385 rows); every row against the
+    oracle, with a bias."""
+    torch = torch_cuda
+    raw = synth.weights_np(t, m, k, seed=1750 + t + n)
+    x = synth.activations_np(n, k, seed=1751 + n, outliers=0.01)
+    w = eng.upload(raw, t, m, k)
+    xq = torch.empty(eng.act_bytes(n, k), dtype=torch.uint8, device="cuda")
+    eng.qact(torch.from_numpy(x).cuda(), n, k, F.ACT_KIND[t], xq)
+    bias = np.linspace(-2, 2, m).astype(np.float32)
+    y = torch.full((n, m), float("nan"), device="cuda")
+    eng.matvec_parts([w], [y], n, xq=xq, biases=[torch.from_numpy(bias).cuda()])
+    torch.cuda.synchronize()
+    want = O.matmul(t, raw, m, k, x, n, bias=bias, threads=16)
+    assert parity_err(y.cpu().numpy(), want) <= PARITY_TOL
+    eng.free(w)
+
+
 @pytest.mark.parametrize("t", FMTS)
 def test_gemm_unaligned_output(eng, torch_cuda, t):
     """Outputs that are not 16-byte aligned (here one float past an aligned buffer) take the
