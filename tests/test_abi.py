@@ -125,3 +125,22 @@ def test_network_bytes_needed_host_logic():
     bad = cfg(ctx)
     bad.head_dim = 96
     assert bytes_needed(bad, model) == 0
+
+
+def test_items_pack_as_the_c_struct():
+    """hk_amd.net packs (seq, token, pos) items in bulk into hkhip_item's 16-byte layout (u64 seq,
+    u32 token, u32 pos): the bytes match ctypes' own Item structures, for tuples, lists and an
+    [n][3] array, with seq ids over the whole u64 range; a value out of its field's range raises."""
+    from hk_amd.net import _items
+
+    items = [(2**64 - 1, 5, 7), (0, 2**32 - 1, 0), (3, np.uint32(9), 10)]
+    want = (_lib.Item * 3)(*[_lib.Item(*it) for it in items])
+    for form in (items, [list(it) for it in items]):
+        p, n, keep = _items(form)
+        assert n == 3 and ctypes.string_at(p, 48) == bytes(want)
+    arr = np.array([[1, 2, 3], [4, 5, 6]], dtype=np.int64)
+    p, n, keep = _items(arr)
+    assert n == 2 and ctypes.string_at(p, 32) == bytes((_lib.Item * 2)(_lib.Item(1, 2, 3), _lib.Item(4, 5, 6)))
+    assert _items([])[1] == 0
+    with pytest.raises((OverflowError, ValueError)):
+        _items([(-1, 0, 0)])
