@@ -714,6 +714,36 @@ def test_small_batch_shared_activations(eng, torch_cuda, t, n, m, k):
     eng.free(w)
 
 
+@pytest.mark.parametrize("t", [F.Q4_K, F.Q6_K])
+@pytest.mark.parametrize("n,mode", [(5, 1), (8, 1), (6, 2)])
+def test_small_batch_shared_activations_modes(eng, torch_cuda, t, n, mode):
+    """The shared-activation workgroups with two fused parts of ragged heights (1027 row tiles, a
+    part boundary inside a workgroup), in accumulate mode with biases and in silu(gate)*up mode;
+    every row against the oracle."""
+    torch = torch_cuda
+    k = 1024
+    heights = [8210, 8222] if mode == 2 else [8209, 8223]
+    raws = [synth.weights_np(t, m, k, seed=1760 + i + t + n) for i, m in enumerate(heights)]
+    x = synth.activations_np(n, k, seed=1761 + n, outliers=0.01)
+    mats = [eng.upload(r, t, m, k) for r, m in zip(raws, heights)]
+    cols = [m // 2 if mode == 2 else m for m in heights]
+    y0s = [synth.activations_np(n, c, seed=1762 + c) for c in cols]
+    ys = [torch.from_numpy(y0.copy()).cuda() if mode == 1 else torch.full((n, c), float("nan"), device="cuda")
+          for y0, c in zip(y0s, cols)]
+    biases = [np.linspace(-1, 1, m).astype(np.float32) for m in heights] if mode == 1 else None
+    xq = torch.empty(eng.act_bytes(n, k), dtype=torch.uint8, device="cuda")
+    eng.qact(torch.from_numpy(x).cuda(), n, k, F.ACT_KIND[t], xq)
+    eng.matvec_parts(mats, ys, n, xq=xq, mode=mode,
+                     biases=[torch.from_numpy(b).cuda() for b in biases] if biases else None)
+    torch.cuda.synchronize()
+    for i, (r, m) in enumerate(zip(raws, heights)):
+        want = O.matmul(t, r, m, k, x, n, bias=biases[i] if biases else None, threads=16)
+        want = want + y0s[i] if mode == 1 else silu_mul_ref(want)
+        assert parity_err(ys[i].cpu().numpy(), want) <= PARITY_TOL
+    for w in mats:
+        eng.free(w)
+
+
 @pytest.mark.parametrize("t", FMTS)
 def test_gemm_unaligned_output(eng, torch_cuda, t):
     """Outputs that are not 16-byte aligned (here one float past an aligned buffer) take the
