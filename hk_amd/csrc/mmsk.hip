@@ -412,6 +412,9 @@ __global__ __launch_bounds__(KS * 64) void mmsk_kernel(SkArgs a) {
 // of this structure: 14.7 us). Measured at 8 tokens on Llama-3-8B shapes, alternating runs against
 // the kernel above: the batch-8 decode step 1.97-2.04 vs 2.09-2.10 ms, gate/up 21.4-22.4 vs
 // 21.6-23.9 us; a ring of three or four slots (no register cost here) was slower, 23.4-23.9 us.
+// Four tiles per workgroup: two (twice the staging, three workgroups per CU) took gate/up to 28.4
+// us and the Q6_K lm_head to 121 us (vs 21.3 / 101.7); eight, 23.4 (the old kernel: too few
+// workgroups) / 106.9.
 constexpr uint32_t SA_NR = 4, SA_TOK = 8, SA_PF = 2;
 
 // LDS geometry: A [nsb*4 chunks][4 g][SA_TOK] x 16 B, MB [nsb][2][SA_TOK] x 16 B (Q4_K),
